@@ -1,0 +1,157 @@
+/* d8s_hip.h -- C ABI of libd8s_hip.so, the gfx950 kernels of the INT8 DenseNet encoder.
+ *
+ * The reference binds its CUDA kernels by name through ctypes (src/knee/cudart.py:87-152:
+ * `Module.function`, `Function.launch` with by-value argument structs) and launches them from the
+ * runner `Dense8SEncoder` (src/knee/dense8s.py:944-1488).  This library replaces that native
+ * surface: every entry point below stands for one kernel family of the reference's final launch
+ * sequence (src/knee/dense8s.py:1354-1385) and is called from Python through ctypes.
+ *
+ * Conventions (all entry points):
+ *   - pointers are device pointers owned by the caller; nothing is allocated or freed here;
+ *   - `stream` is a hipStream_t (PyTorch's `torch.cuda.Stream.cuda_stream`); every call is
+ *     asynchronous on it and may be recorded into a HIP graph;
+ *   - the return value is 0 on success, otherwise a hipError_t (invalid arguments give
+ *     hipErrorInvalidValue = 1); the message of the last failure on the calling thread is
+ *     d8s_last_error().
+ *
+ * Data layout (the reference's block "store", src/knee/dense8s_kernels.cu:10-14):
+ *   in0  [N][G0][HW][32] int8   block input, 32 channels per group, channel c = 32 g + i;
+ *   seg  [L][N][HW][32]  int8   layer outputs: layer l owns group G0 + l;
+ *   bott [4][N*HW][32]   uint8  planar bottleneck: plane b holds channels 32 b .. 32 b + 31.
+ * Channel c of pixel p holds x = sigma_c * q with q int8 (per-channel scale sigma).
+ */
+#ifndef D8S_HIP_H
+#define D8S_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define D8S_ABI_VERSION 1
+
+/* Arguments of the 1x1 GEMMs (conv1 and the transition).  Same fields and meaning as the
+ * reference's `struct KArg` (src/knee/dense8s_kernels.cu:146-158, src/knee/dense8s.py:76-82),
+ * plus `wsum`: gfx950's int8 MFMA multiplies signed bytes, so the unsigned prologue output u is fed
+ * as u - 128 and the GEMM adds 128 * sum_k w[o][k] back (exact in int32).
+ *   in0, seg  the block store (see above);  G0 groups in in0, G groups read (G0 + layers so far);
+ *   w         weights [G][cout][32] int8 (the reference's `_chunked`, dense8s.py:436-440);
+ *   abh       fp16 prologue table [G*16][4] = (A_2p, A_2p+1, B_2p, B_2p+1) (dense8s.py:443-449);
+ *   gd        epilogue table [cout][2] float: conv1 (g, d) of `L*_gdu`; transition (k', 0) of
+ *             `T*_gdf` (dense8s.py:485-486,500-501);
+ *   wsum      [cout] int32, sum over k of w[o][k];
+ *   out       conv1: planar u8 bottleneck [4][rows][32]; transition: next block's in0
+ *             [N][G0n][HW/4][32];
+ *   N, HW, W  images, pixels per image, image width;  rows = N*HW;  cout output channels. */
+typedef struct D8sGemmArgs {
+    const int8_t* in0;
+    const int8_t* seg;
+    const int8_t* w;
+    const uint16_t* abh;
+    const float* gd;
+    const int32_t* wsum;
+    void* out;
+    int32_t G0, G, N, HW, W, rows, cout, G0n;
+} D8sGemmArgs;
+
+/* Arguments of the 3x3 conv (pad 1, 128 -> 32).  Same meaning as the reference's `struct C2Arg`
+ * (src/knee/dense8s_kernels.cu:1936-1942, src/knee/dense8s.py:131-137) without the rectangle fields,
+ * which this library chooses itself, plus `wsum` (see D8sGemmArgs).
+ *   x     planar u8 bottleneck [4][N*H*W][32];
+ *   w     weights [4][9][32][32] int8 = [input block][tap][output][input] (`L*_w2k`, dense8s.py:487-488);
+ *   sc    [32] float requantisation scale c2u (dense8s.py:489);
+ *   wsum  [32] int32, sum over (input channel, tap) of w;
+ *   out   the layer's store slot [N][H*W][32] int8. */
+typedef struct D8sConv2Args {
+    const uint8_t* x;
+    const int8_t* w;
+    const float* sc;
+    const int32_t* wsum;
+    int8_t* out;
+    int32_t N, H, W, pad_;
+} D8sConv2Args;
+
+/* Arguments of the stem: 7x7/2 conv (pad 3) with norm0 folded in, bias, ReLU, 3x3/2 max-pool (pad 1)
+ * and per-channel int8 quantisation into the first block's in0.  Replaces the reference's TensorRT
+ * fp16 stem engine + `quant_seg` (src/knee/dense8s.py:684-716,1330-1352;
+ * src/knee/dense8s_kernels.cu:2365-2412), with the uint8 normalisation and flip of the input fused
+ * into the load (the role of `gather_u8_to_f16`, src/knee/data/fused_uint8.py:480-506).
+ *   x      input [N][3][H][W]: uint8 when kind = D8S_IN_U8 (x16 = lut[c][u]), fp16 when
+ *          kind = D8S_IN_F16 (used as is);
+ *   lut    [3][256] fp16 (kind = D8S_IN_U8 only);
+ *   w16    [64][168] fp16, norm0 folded in, k = (channel * 7 + ky) * 8 + kx + 1 and k % 8 = 0
+ *          zero: the reference's `S_w16` table (src/knee/dense8s.py:522-530);
+ *   bias   [64] float;  inv [64] float = 1 / sigma0;
+ *   out    in0 of block 0 [N][2][(H/4)*(W/4)][32];
+ *   flip   1: the image is mirrored horizontally (x[..., W-1-j]). */
+#define D8S_IN_F16 0
+#define D8S_IN_U8 1
+typedef struct D8sStemArgs {
+    const void* x;
+    const uint16_t* lut;
+    const uint16_t* w16;
+    const float* bias;
+    const float* inv;
+    int8_t* out;
+    int32_t N, H, W, kind, flip, pad_;
+} D8sStemArgs;
+
+/* conv1 of a dense layer: u = RNE(255 sat(fp16(A q + B))) per input channel (prologue), acc = sum_k
+ * w[o][k] u[k] (int32, i8 MFMA), v = low byte of fma(sat(fma(g, acc, d)), 255, 2^23) into the planar
+ * bottleneck.  cout must be 128.  Replaces `conv1_w64_pl` (src/knee/dense8s_kernels.cu:479-627,
+ * launch src/knee/dense8s.py:1205-1240). */
+int d8s_conv1(const D8sGemmArgs* a, void* stream);
+
+/* The same GEMM writing the int32 accumulators acc[rows][cout] (and the bottleneck too when
+ * a->out is not NULL).  The reference has no such kernel: its checks recompute the accumulators
+ * (kaggle/int8_pack/pack_dense8s.py:246-283); here they are compared bit for bit. */
+int d8s_conv1_acc32(const D8sGemmArgs* a, int32_t* acc, void* stream);
+
+/* conv2 of a dense layer: acc = sum over taps and input channels (zero padding) of w u (int32,
+ * i8 MFMA), q = RNE(clamp(float(acc) * sc[o], -127, 127)) into the store slot.  Replaces
+ * `conv2_t8x32_pl` / `conv2_t16x16_pl` (src/knee/dense8s_kernels.cu:2679-2832, launch
+ * src/knee/dense8s.py:1274-1290). */
+int d8s_conv2(const D8sConv2Args* a, void* stream);
+
+/* Transition: prologue on the 4 pixels of every 2x2 square, s = sum of the four u, S = sum_k w[o][k]
+ * s[k] (exact int32), q = RNE(clamp(k'_o * (float(S) / 4), -127, 127)) into the next block's in0.
+ * H and W even, cout a multiple of 32.  Replaces `trans_w0` / `trans_w1`
+ * (src/knee/dense8s_kernels.cu:3041-3262, launch src/knee/dense8s.py:1242-1272). */
+int d8s_transition(const D8sGemmArgs* a, void* stream);
+
+/* Final features: out[n][c] = (sum over the four strided partials of sum_p relu(fma(a_c, q, b_c))) / HW,
+ * norm5 with sigma folded in (ab = `F_ab` [ctot][2]).  Replaces `final_q`
+ * (src/knee/dense8s_kernels.cu:2304-2323, launch src/knee/dense8s.py:1380-1384); same arguments. */
+int d8s_final(const int8_t* in0, int32_t G0, const int8_t* seg, int32_t N, int32_t HW,
+              const float* ab, float* out, int32_t ctot, void* stream);
+
+/* Stem (see D8sStemArgs).  H and W multiples of 4. */
+int d8s_stem(const D8sStemArgs* a, void* stream);
+
+/* Library identification: "d8s-hip <abi> <source hash> gfx950". */
+const char* d8s_version(void);
+
+/* Message of the last failed call on the calling thread ("" if none). */
+const char* d8s_last_error(void);
+
+/* Diagnostics (the reference's micro-benchmarks, src/knee/dense8s_kernels.cu:4232-4417).
+ * d8s_micro_copy: dst[i] = src[i] over `bytes` (a multiple of 16): the HBM bandwidth floor.
+ * d8s_micro_mfma: `blocks` workgroups each running `iters` rounds of independent
+ *   v_mfma_i32_32x32x32_i8 on 4 waves; sink receives one value per block (keeps the work alive).
+ * d8s_probe_mfma_i8: D = A B for one 32x32x32 int8 MFMA tile, A [32][32] and B [32][32]
+ *   row-major (B indexed [k][j]), D [32][32] int32 row-major: checks this library's operand and
+ *   result lane layout.
+ * d8s_probe_mfma_f16: the same for one 32x32x16 fp16 MFMA tile, A [32][16], B [16][32] fp16 bits,
+ *   D [32][32] float. */
+int d8s_micro_copy(const void* src, void* dst, size_t bytes, void* stream);
+int d8s_micro_mfma(int32_t blocks, int32_t iters, int32_t* sink, void* stream);
+int d8s_probe_mfma_i8(const int8_t* A, const int8_t* B, int32_t* D, void* stream);
+int d8s_probe_mfma_f16(const uint16_t* A, const uint16_t* B, float* D, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* D8S_HIP_H */

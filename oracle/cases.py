@@ -1,0 +1,145 @@
+"""Seeded synthetic cases of the isolated kernels (configurations 2 and 3 of the benchmark).
+
+TEST INFRASTRUCTURE ONLY (see oracle/__init__.py).
+
+Config 2 (1x1 GEMM with the BN + ReLU + quantise prologue): activations x ~ N(0, 1) quantised per
+tensor (q = RNE(clamp(x / s, +-127)), s = max|x| / 127), weights ~ N(0, 2 / C_in) quantised per output
+channel.  The store is laid out as in the encoder: the block's c0 input channels in in0, the rest in
+layer slots of seg.  The prologue BatchNorm has gamma ~ U(0.8, 1.2), beta ~ N(0, 0.1), mean ~ N(0, 0.1),
+var ~ U(0.5, 1.5); its u8 scale is the maximum of relu(bn(x)) over the data.
+Config 3 (3x3 conv, 128 -> 32): bottleneck u8 ~ U{0..79} (the range of the reference's `unit_conv2`,
+kaggle/int8_pack/pack_dense8s.py:286-320), weights ~ N(0, 2 / 1152) quantised per output channel.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import numpy as np
+
+# (side, C_in) of config 2 and the block input width c0 at that side (DenseNet169 at 512 px)
+GEMM_CASES = [(128, 64), (128, 160), (128, 224), (64, 128), (64, 320), (64, 480),
+              (32, 256), (32, 768), (32, 1248), (16, 640), (16, 1152), (16, 1632)]
+C0_AT = {128: 64, 64: 128, 32: 256, 16: 640}
+CONV2_SIDES = (128, 64, 32, 16)
+
+
+def quant_weight_np(w: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
+    """int8 per output channel in float32 arithmetic (`src/knee/dense8.py:182-188`)."""
+    w = w.astype(np.float32)
+    scale = np.maximum(np.abs(w.reshape(w.shape[0], -1)).max(1), np.float32(1e-12)) / np.float32(127)
+    inv = (np.float32(1.0) / scale).astype(np.float32)
+    q = np.clip(np.rint(w * inv.reshape(-1, *[1] * (w.ndim - 1))), -128, 127)
+    return q.astype(np.int8), scale.astype(np.float32)
+
+
+def abh_table(ab: np.ndarray) -> np.ndarray:
+    h = ab.astype(np.float16)
+    return np.ascontiguousarray(
+        np.stack([h[0::2, 0], h[1::2, 0], h[0::2, 1], h[1::2, 1]], 1)).view(np.int16)
+
+
+def chunked(w: np.ndarray) -> np.ndarray:
+    cout, cin = w.shape
+    return np.ascontiguousarray(w.reshape(cout, cin // 32, 32).transpose(1, 0, 2))
+
+
+def bn_random(rng, c: int) -> tuple[np.ndarray, np.ndarray]:
+    gamma = rng.uniform(0.8, 1.2, c)
+    beta = rng.normal(0, 0.1, c)
+    mean = rng.normal(0, 0.1, c)
+    var = rng.uniform(0.5, 1.5, c)
+    a = gamma / np.sqrt(var + 1e-5)
+    return a, beta - mean * a
+
+
+@dataclass
+class GemmCase:
+    S: int
+    N: int
+    G0: int
+    G: int
+    in0: np.ndarray         # [N][G0][HW][32] int8
+    seg: np.ndarray         # [G - G0][N][HW][32] int8 (at least one slot)
+    q: np.ndarray           # [N][C][HW] int8 (channel-major view of the whole store)
+    abh: np.ndarray         # [C/2][4] int16
+    ab: np.ndarray          # [C][2] float32
+    w: np.ndarray           # [128][C] int8
+    w1: np.ndarray          # [G][128][32] int8
+    gd: np.ndarray          # [128][2] float32
+
+
+def store_from_q(q: np.ndarray, G0: int) -> tuple[np.ndarray, np.ndarray]:
+    """q [N][C][HW] -> (in0 [N][G0][HW][32], seg [L][N][HW][32]) (at least one seg slot)."""
+    N, C, HW = q.shape
+    G = C // 32
+    g = q.reshape(N, G, 32, HW).transpose(0, 1, 3, 2)           # [N][G][HW][32]
+    in0 = np.ascontiguousarray(g[:, :G0])
+    seg = np.ascontiguousarray(g[:, G0:].transpose(1, 0, 2, 3)) if G > G0 \
+        else np.zeros((1, N, HW, 32), np.int8)
+    return in0, seg
+
+
+def gemm_case(S: int, C: int, N: int = 24, seed: int = 11, cout: int = 128) -> GemmCase:
+    rng = np.random.default_rng([seed, S, C])
+    HW = S * S
+    x = rng.standard_normal((N, C, HW), dtype=np.float32)
+    s = float(np.abs(x).max()) / 127
+    q = np.clip(np.rint(x / s), -127, 127).astype(np.int8)
+    a, b = bn_random(rng, C)
+    # u8 scale of the conv input: max of relu(a x + b) over a sample of the data
+    xs = q[:, :, :: max(1, HW // 1024)].astype(np.float64) * s
+    s1 = max(float(np.maximum(a[None, :, None] * xs + b[None, :, None], 0).max()), 1e-12) / 255
+    sig = np.full(C, s)
+    ab = np.stack([a * sig / (255 * s1), b / (255 * s1)], 1).astype(np.float32)
+    w, _ = quant_weight_np(rng.normal(0, np.sqrt(2.0 / C), (cout, C)).astype(np.float32))
+    # epilogue: v = sat(g acc + d) spans [0, 1] over a typical accumulator range
+    acc_scale = 255.0 * 127 * np.sqrt(C) * 0.5
+    g = (rng.uniform(0.5, 1.5, cout) / acc_scale).astype(np.float32)
+    d = rng.normal(0.3, 0.2, cout).astype(np.float32)
+    G0 = C0_AT.get(S, C) // 32 if C >= C0_AT.get(S, C) else C // 32
+    in0, seg = store_from_q(q, G0)
+    return GemmCase(S, N, G0, C // 32, in0, seg, q, abh_table(ab), ab, w, chunked(w),
+                    np.stack([g, d], 1).astype(np.float32))
+
+
+@dataclass
+class Conv2Case:
+    S: int
+    N: int
+    v: np.ndarray           # [N][128][H][W] uint8
+    bott: np.ndarray        # planar [4][N*H*W][32] uint8
+    w2: np.ndarray          # [32][128][3][3] int8
+    w2k: np.ndarray         # [4][9][32][32] int8
+    sc: np.ndarray          # [32] float32
+
+
+def conv2_case(S: int, N: int = 24, seed: int = 21) -> Conv2Case:
+    rng = np.random.default_rng([seed, S])
+    v = rng.integers(0, 80, (N, 128, S, S), dtype=np.uint8)
+    bott = np.ascontiguousarray(v.reshape(N, 4, 32, S * S).transpose(1, 0, 3, 2)).reshape(4, -1, 32)
+    w2, _ = quant_weight_np(rng.normal(0, np.sqrt(2.0 / 1152), (32, 128, 3, 3)).astype(np.float32))
+    w2k = np.ascontiguousarray(w2.reshape(32, 4, 32, 9).transpose(1, 3, 0, 2))
+    # q = acc sc spans about [-127, 127] with a few saturated values
+    sc = (rng.uniform(0.5, 1.5, 32) * 127 / (40.0 * 127 * np.sqrt(1152) * 0.5)).astype(np.float32)
+    return Conv2Case(S, N, v, bott, w2, w2k, sc)
+
+
+def trans_case(S: int, C: int, N: int = 4, seed: int = 31, c0: int | None = None):
+    """A transition case: the store of a block (C channels at side S, c0 in in0) and the tables."""
+    rng = np.random.default_rng([seed, S, C])
+    HW = S * S
+    q = rng.integers(-127, 128, (N, C, HW), dtype=np.int16).astype(np.int8)
+    a, b = bn_random(rng, C)
+    sig = rng.uniform(0.5, 1.5, C) / 127
+    xs = q.astype(np.float64) * sig[None, :, None]
+    s1 = max(float(np.maximum(a[None, :, None] * xs + b[None, :, None], 0).max()), 1e-12) / 255
+    ab = np.stack([a * sig / (255 * s1), b / (255 * s1)], 1).astype(np.float32)
+    cout = C // 2
+    tw, _ = quant_weight_np(rng.normal(0, np.sqrt(2.0 / C), (cout, C)).astype(np.float32))
+    # |sum_k w u| ~ 3200 sqrt(C) for these weights and bytes: k' maps that to about +-64
+    kq = (rng.uniform(0.5, 1.5, cout) * 127 / (2 * 3200 * np.sqrt(C))).astype(np.float32)
+    gdf = np.stack([kq, np.zeros_like(kq)], 1).astype(np.float32)
+    G0 = (c0 if c0 is not None else C) // 32
+    in0, seg = store_from_q(q, G0)
+    return {"S": S, "N": N, "C": C, "G0": G0, "G": C // 32, "q": q, "in0": in0, "seg": seg,
+            "abh": abh_table(ab), "ab": ab, "tw": tw, "w": chunked(tw), "gdf": gdf, "cout": cout}

@@ -1,0 +1,843 @@
+// gfx950 kernels of the INT8 DenseNet encoder and their C ABI (include/d8s_hip.h).
+//
+// Matrix products run on the CDNA4 int8 MFMA v_mfma_i32_32x32x32_i8 (wave64, 32 x 32 int32 tile,
+// K = 32 = one store group per instruction) and, in the stem, on v_mfma_f32_32x32x16_f16.  The
+// weights are the MFMA's A operand (rows = output channels) and the activations its B operand
+// (columns = pixels): after the MFMA every lane holds 16 output channels of ONE pixel, so one lane
+// exchange (lanes l <-> l ^ 32) gives each lane 16 consecutive channel bytes and the epilogues store
+// whole 16-byte chunks of the [pixel][32] rows.
+//
+// Lane layouts relied on (checked by d8s_probe_mfma_i8 / d8s_probe_mfma_f16 on the GPU):
+//   operands: lane l holds row (A) / column (B) l & 31 and the K-chunk (l >> 5) of the instruction's K;
+//   result:   lane l, element v: column j = l & 31, row i = 8 (v >> 2) + 4 (l >> 5) + (v & 3).
+//
+// Unsigned activations: the MFMA multiplies signed bytes.  The u8 values u are fed as u - 128
+// (= u ^ 0x80 read as int8) and every accumulator starts at 128 * sum_k w[o][k], so it ends at
+// sum_k w[o][k] u[k] exactly (int32).  Zero padding of the 3x3 conv is u = 0, i.e. byte 0x80.
+#include <hip/hip_runtime.h>
+
+#include <stdint.h>
+#include <string.h>
+
+#include <string>
+
+#include "d8s_hip.h"
+
+#ifndef D8S_SRC_HASH
+#define D8S_SRC_HASH "unknown"
+#endif
+
+#define DEV __device__ __forceinline__
+
+typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
+typedef int32_t i32x16 __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef int16_t i16x2 __attribute__((ext_vector_type(2)));
+
+static constexpr uint32_t SIGN4 = 0x80808080u;
+
+DEV f16x2 as_h2(uint32_t x) { return __builtin_bit_cast(f16x2, x); }
+DEV uint32_t h2_bits(f16x2 x) { return __builtin_bit_cast(uint32_t, x); }
+
+DEV i32x16 mfma_i8(u32x4 a, u32x4 b, i32x16 c) {
+    return __builtin_amdgcn_mfma_i32_32x32x32_i8(__builtin_bit_cast(i32x4, a),
+                                                 __builtin_bit_cast(i32x4, b), c, 0, 0, 0);
+}
+
+// The four low bytes of the 16-bit halves of (lo, hi) as one dword: byte order lo.0, lo.1, hi.0, hi.1.
+DEV uint32_t pack_low_bytes(uint32_t lo, uint32_t hi) {
+    return (lo & 0xffu) | ((lo >> 8) & 0xff00u) | ((hi & 0xffu) << 16) | ((hi << 8) & 0xff000000u);
+}
+
+// fp16 prologue of 4 store bytes (4 consecutive channels): q -> u = RNE(255 sat(fp16(A q + B))).
+// The byte q + 128 goes into the mantissa of fp16 1024 (exact 1024 + 128 + q), -1152 leaves q exactly,
+// one fused fp16 fma with saturation gives v, and fma(v, 255, 1024) = 1024 + RNE(255 v) (ulp 1 in
+// [1024, 2048)): u is the low byte of each half.  (a01, b01) are the fp16 pairs (A, B) of channels
+// 0-1, (a23, b23) of channels 2-3.  Returns the halves 1024 + u for channels (0, 1) and (2, 3).
+// Same roundings as the reference's `pro4h` (src/knee/dense8s_kernels.cu:122-139) and its emulation
+// `emulate(f16_layers)` (src/knee/dense8s.py:584-587).
+DEV void pro4_halves(uint32_t x, uint32_t a01, uint32_t b01, uint32_t a23, uint32_t b23,
+                     uint32_t& rl, uint32_t& rh) {
+    const uint32_t w = x ^ SIGN4;
+    const uint32_t lo = 0x64006400u | (w & 0xffu) | ((w << 8) & 0xff0000u);
+    const uint32_t hi = 0x64006400u | ((w >> 16) & 0xffu) | ((w >> 8) & 0xff0000u);
+    const f16x2 m1152 = {(_Float16)-1152.0f, (_Float16)-1152.0f};
+    const f16x2 zero = {(_Float16)0.0f, (_Float16)0.0f};
+    const f16x2 one = {(_Float16)1.0f, (_Float16)1.0f};
+    const f16x2 k255 = {(_Float16)255.0f, (_Float16)255.0f};
+    const f16x2 k1024 = {(_Float16)1024.0f, (_Float16)1024.0f};
+    f16x2 vl = __builtin_elementwise_fma(as_h2(lo) + m1152, as_h2(a01), as_h2(b01));
+    f16x2 vh = __builtin_elementwise_fma(as_h2(hi) + m1152, as_h2(a23), as_h2(b23));
+    vl = __builtin_elementwise_min(__builtin_elementwise_max(vl, zero), one);
+    vh = __builtin_elementwise_min(__builtin_elementwise_max(vh, zero), one);
+    rl = h2_bits(__builtin_elementwise_fma(vl, k255, k1024));
+    rh = h2_bits(__builtin_elementwise_fma(vh, k255, k1024));
+}
+
+// The prologue of 4 store bytes as the MFMA operand: 4 bytes u - 128.
+DEV uint32_t pro4(uint32_t x, uint32_t a01, uint32_t b01, uint32_t a23, uint32_t b23) {
+    uint32_t rl, rh;
+    pro4_halves(x, a01, b01, a23, b23, rl, rh);
+    return pack_low_bytes(rl, rh) ^ SIGN4;
+}
+
+// 16 channels: x = 4 store dwords, p = 16 parameter dwords (A01, B01, A23, B23 per store dword).
+DEV u32x4 pro16(u32x4 x, u32x4 p0, u32x4 p1, u32x4 p2, u32x4 p3) {
+    return u32x4{pro4(x.x, p0.x, p0.y, p0.z, p0.w), pro4(x.y, p1.x, p1.y, p1.z, p1.w),
+                 pro4(x.z, p2.x, p2.y, p2.z, p2.w), pro4(x.w, p3.x, p3.y, p3.z, p3.w)};
+}
+
+// Lanes l and l ^ 32 hold the same pixel: lane half h = l >> 5 has channel dwords 2k + h (channels
+// 8k + 4h .. 8k + 4h + 3, k = 0..3) of a 32-channel row.  After the exchange lane half h holds the row's
+// bytes 16h .. 16h + 15 (dwords 4h .. 4h + 3).
+DEV u32x4 xchg_rows(uint32_t e0, uint32_t e1, uint32_t e2, uint32_t e3, int h) {
+    const uint32_t r1 = (uint32_t)__shfl_xor((int)(h ? e0 : e2), 32);
+    const uint32_t r2 = (uint32_t)__shfl_xor((int)(h ? e1 : e3), 32);
+    return h ? u32x4{r1, e2, r2, e3} : u32x4{e0, r1, e1, r2};
+}
+
+// Row i (output channel) of element v of a 32x32 MFMA result, for lane half h.
+DEV int res_row(int v, int h) { return 8 * (v >> 2) + 4 * h + (v & 3); }
+
+// Swizzled 16-byte half `half` of 32-byte row r in LDS (halves swapped on every other group of 4
+// rows: the 16-byte reads of 8 consecutive rows hit distinct banks).
+DEV int swz(int r, int half) { return r * 2 + (half ^ ((r >> 2) & 1)); }
+
+// ------------------------------------------------------------------------------------------------
+// conv1: 1x1 GEMM, M = N*HW pixels, K = G*32 store channels, 128 outputs.
+// Workgroup = 256 pixels, 4 waves x 64 pixels x 128 outputs (2 x 4 MFMA tiles per K group).
+// The store bytes go global -> registers -> prologue -> MFMA operand (no LDS); the weights of a
+// group (4 KB) are staged in LDS, double-buffered; the fp16 prologue table of the layer sits in LDS.
+// ------------------------------------------------------------------------------------------------
+static constexpr int C1_BM = 256;
+
+template <bool ACC32>
+__global__ __launch_bounds__(256) void k_conv1(D8sGemmArgs a, int32_t* __restrict__ acc_out) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    const int G = a.G, G0 = a.G0;
+    u32x4* s_w = (u32x4*)smem;                          // [2][256] 16-byte chunks
+    uint32_t* s_abh = (uint32_t*)(smem + 2 * 4096);      // [G * 32] dwords
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int h = lane >> 5, j = lane & 31;
+
+    const uint32_t* abh32 = (const uint32_t*)a.abh;
+    for (int i = tid; i < G * 32; i += 256) s_abh[i] = abh32[i];
+
+    // the lane's two pixels (columns of the two MFMA tiles) and their store rows
+    const int64_t rows = a.rows, HW = a.HW;
+    const int64_t in_gs = HW * 32, seg_gs = (int64_t)a.N * HW * 32;
+    const int64_t mbase = (int64_t)blockIdx.x * C1_BM + wave * 64 + j;
+    const int8_t* pin[2];
+    const int8_t* pseg[2];
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+        int64_t m = mbase + 32 * t;
+        if (m >= rows) m = rows - 1;
+        const int64_t n = m / HW, p = m - n * HW;
+        pin[t] = a.in0 + (n * G0 * HW + p) * 32 + 16 * h;
+        pseg[t] = a.seg + (n * HW + p) * 32 + 16 * h;
+    }
+    auto src = [&](int t, int g) -> const u32x4* {
+        return (const u32x4*)(g < G0 ? pin[t] + g * in_gs : pseg[t] + (g - G0) * seg_gs);
+    };
+    const u32x4* wg = (const u32x4*)a.w;                 // group g: wg[g * 256 + i]
+    const int wo = tid >> 1, whf = tid & 1;
+    const int wdst = swz(wo, whf);
+
+    i32x16 acc[2][4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        i32x16 init;
+#pragma unroll
+        for (int v = 0; v < 16; ++v) init[v] = 128 * a.wsum[32 * c + res_row(v, h)];
+        acc[0][c] = init;
+        acc[1][c] = init;
+    }
+
+    u32x4 ra[2][2];
+    u32x4 rw;
+    ra[0][0] = *src(0, 0);
+    ra[0][1] = *src(1, 0);
+    rw = wg[tid];
+    if (G > 1) {
+        ra[1][0] = *src(0, 1);
+        ra[1][1] = *src(1, 1);
+    }
+    __syncthreads();                                    // s_abh
+    s_w[wdst] = rw;
+    if (G > 1) rw = wg[256 + tid];
+    __syncthreads();
+
+    auto step = [&](const int slot, const int g) {
+        const u32x4* pp = (const u32x4*)(s_abh + g * 32 + h * 16);
+        const u32x4 p0 = pp[0], p1 = pp[1], p2 = pp[2], p3 = pp[3];
+        const u32x4 b0 = pro16(ra[slot][0], p0, p1, p2, p3);
+        const u32x4 b1 = pro16(ra[slot][1], p0, p1, p2, p3);
+        if (g + 2 < G) {
+            ra[slot][0] = *src(0, g + 2);
+            ra[slot][1] = *src(1, g + 2);
+        }
+        const u32x4* sw = s_w + (g & 1) * 256;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const u32x4 aw = sw[swz(32 * c + j, h)];
+            acc[0][c] = mfma_i8(aw, b0, acc[0][c]);
+            acc[1][c] = mfma_i8(aw, b1, acc[1][c]);
+        }
+        if (g + 1 < G) s_w[((g + 1) & 1) * 256 + wdst] = rw;
+        if (g + 2 < G) rw = wg[(int64_t)(g + 2) * 256 + tid];
+        __syncthreads();
+    };
+    for (int g = 0; g < G; g += 2) {
+        step(0, g);
+        if (g + 1 < G) step(1, g + 1);
+    }
+
+    // epilogue: v = low byte of fma(sat(fma(g, acc, d)), 255, 2^23) (conv1w_body epilogue,
+    // src/knee/dense8s_kernels.cu:595-611), planar bottleneck [4][rows][32]
+    const float2* gd = (const float2*)a.gd;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        float2 prm[16];
+#pragma unroll
+        for (int v = 0; v < 16; ++v) prm[v] = gd[32 * c + res_row(v, h)];
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            const int64_t m = mbase + 32 * t;
+            if (ACC32) {
+                if (m < rows) {
+#pragma unroll
+                    for (int k = 0; k < 4; ++k) {
+                        const i32x4 q = {acc[t][c][4 * k], acc[t][c][4 * k + 1],
+                                         acc[t][c][4 * k + 2], acc[t][c][4 * k + 3]};
+                        *(i32x4*)(acc_out + m * 128 + 32 * c + 8 * k + 4 * h) = q;
+                    }
+                }
+                if (a.out == nullptr) continue;
+            }
+            uint32_t e[4];
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                uint32_t d = 0;
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int v = 4 * k + r;
+                    float y = __builtin_fmaf(prm[v].x, (float)acc[t][c][v], prm[v].y);
+                    y = __builtin_fminf(__builtin_fmaxf(y, 0.0f), 1.0f);
+                    const uint32_t b = __float_as_uint(__builtin_fmaf(y, 255.0f, 8388608.0f)) & 0xffu;
+                    d |= b << (8 * r);
+                }
+                e[k] = d;
+            }
+            const u32x4 row = xchg_rows(e[0], e[1], e[2], e[3], h);
+            if (m < rows) *(u32x4*)((uint8_t*)a.out + ((int64_t)c * rows + m) * 32 + 16 * h) = row;
+        }
+    }
+}
+
+// ------------------------------------------------------------------------------------------------
+// conv2: 3x3 pad 1, 128 -> 32.  Persistent workgroups with the 36 KB of weights resident in LDS; one
+// spatial tile of TH x TW = 256 output pixels at a time (TW = 32 for W >= 32), its halo of all 4
+// bottleneck planes in LDS.  4 waves x 64 pixels (2 MFMA tiles) x 32 outputs, 36 MFMAs per tile.
+// ------------------------------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void k_conv2(D8sConv2Args a, int TW, int TH, int tiles_x,
+                                               int tiles_y) {
+    __shared__ __attribute__((aligned(16))) u32x4 s_w[4 * 9 * 32 * 2];
+    extern __shared__ __attribute__((aligned(16))) u32x4 s_x[];       // [4][HP][2]
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int h = lane >> 5, j = lane & 31;
+    const int HWd = TW + 2, HP = (TH + 2) * HWd;
+    const int H = a.H, W = a.W;
+    const int64_t M = (int64_t)a.N * H * W;
+
+    for (int i = tid; i < 4 * 9 * 32 * 2; i += 256) s_w[swz(i >> 1, i & 1)] = ((const u32x4*)a.w)[i];
+
+    i32x16 init;
+    float sc[16];
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+        init[v] = 128 * a.wsum[res_row(v, h)];
+        sc[v] = a.sc[res_row(v, h)];
+    }
+    int q0[2], ty[2], tx[2];
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+        const int p = wave * 64 + 32 * t + j;
+        ty[t] = p / TW;
+        tx[t] = p - ty[t] * TW;
+        q0[t] = ty[t] * HWd + tx[t];
+    }
+    const int per_img = tiles_x * tiles_y;
+    const int total = a.N * per_img;
+    for (int tile = blockIdx.x; tile < total; tile += gridDim.x) {
+        const int n = tile / per_img, r = tile - n * per_img;
+        const int y0 = (r / tiles_x) * TH, x0 = (r % tiles_x) * TW;
+        __syncthreads();                                  // weights / previous tile's reads
+        for (int i = tid; i < 8 * HP; i += 256) {
+            const int c = i / (2 * HP), rr = i - c * 2 * HP;
+            const int hp = rr >> 1, hh = rr & 1;
+            const int hy = hp / HWd, hx = hp - hy * HWd;
+            const int y = y0 - 1 + hy, x = x0 - 1 + hx;
+            u32x4 v = {SIGN4, SIGN4, SIGN4, SIGN4};
+            if ((unsigned)y < (unsigned)H && (unsigned)x < (unsigned)W)
+                v = *(const u32x4*)(a.x + (c * M + ((int64_t)n * H + y) * W + x) * 32 + 16 * hh) ^ SIGN4;
+            s_x[c * HP * 2 + swz(hp, hh)] = v;
+        }
+        __syncthreads();
+        i32x16 acc0 = init, acc1 = init;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const u32x4* sx = s_x + c * HP * 2;
+#pragma unroll
+            for (int tap = 0; tap < 9; ++tap) {
+                const int off = (tap / 3) * HWd + (tap % 3);
+                const u32x4 aw = s_w[swz((c * 9 + tap) * 32 + j, h)];
+                const u32x4 b0 = sx[swz(q0[0] + off, h)];
+                const u32x4 b1 = sx[swz(q0[1] + off, h)];
+                acc0 = mfma_i8(aw, b0, acc0);
+                acc1 = mfma_i8(aw, b1, acc1);
+            }
+        }
+        // epilogue: q = RNE(clamp(float(acc) * sc, -127, 127)) (conv2t_body,
+        // src/knee/dense8s_kernels.cu:2797-2809)
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            const i32x16 ac = t ? acc1 : acc0;
+            uint32_t e[4];
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                uint32_t d = 0;
+#pragma unroll
+                for (int rr = 0; rr < 4; ++rr) {
+                    const int v = 4 * k + rr;
+                    const float q = __builtin_rintf(
+                        __builtin_fminf(__builtin_fmaxf((float)ac[v] * sc[v], -127.0f), 127.0f));
+                    d |= ((uint32_t)(int)q & 0xffu) << (8 * rr);
+                }
+                e[k] = d;
+            }
+            const u32x4 row = xchg_rows(e[0], e[1], e[2], e[3], h);
+            const int y = y0 + ty[t], x = x0 + tx[t];
+            if (ty[t] < TH && y < H && x < W)
+                *(u32x4*)(a.out + (((int64_t)n * H + y) * W + x) * 32 + 16 * h) = row;
+        }
+    }
+}
+
+// ------------------------------------------------------------------------------------------------
+// Transition: the mean of every 2x2 square comes before the 1x1 conv (they commute).  With
+// s = sum of the four u (0..1020), s - 512 = 4 hq + lq, hq in [-128, 127], lq in [0, 3], and
+// S = sum_k w s = 4 (sum_k w hq + 128 sum_k w) + sum_k w lq: two int8 MFMAs per K group at quarter
+// resolution, exact.  Workgroup = 64 output pixels x 128 outputs (4 waves x 32 outputs); the pooled
+// operands (hq and lq bytes) of a group are built by the whole workgroup into LDS, double-buffered.
+// ------------------------------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void k_trans(D8sGemmArgs a) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    const int G = a.G, G0 = a.G0;
+    u32x4* s_b = (u32x4*)smem;                            // [2 buf][2 (hq, lq)][64 px][2]
+    uint32_t* s_abh = (uint32_t*)(smem + 8192);           // [G * 32]
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int h = lane >> 5, j = lane & 31;
+    const uint32_t* abh32 = (const uint32_t*)a.abh;
+    for (int i = tid; i < G * 32; i += 256) s_abh[i] = abh32[i];
+
+    const int64_t HW = a.HW, W = a.W;
+    const int W2 = a.W >> 1, HW4 = a.HW >> 2;
+    const int64_t NO = (int64_t)a.N * HW4;
+    const int64_t op0 = (int64_t)blockIdx.y * 64;
+    const int co = blockIdx.x * 4 + wave;                 // output tile of 32 channels
+    const bool co_ok = co * 32 < a.cout;
+
+    // staging role: output pixel pp, 8 channels 8 qq .. 8 qq + 7
+    const int pp = tid >> 2, qq = tid & 3;
+    const int8_t* base_in0;
+    const int8_t* base_seg;
+    int64_t off[4];
+    {
+        int64_t op = op0 + pp;
+        if (op >= NO) op = NO - 1;
+        const int64_t n = op / HW4, p4 = op - n * HW4;
+        const int64_t oy = p4 / W2, ox = p4 - oy * W2;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) off[k] = ((2 * oy + (k >> 1)) * W + 2 * ox + (k & 1)) * 32 + 8 * qq;
+        base_in0 = a.in0 + n * G0 * HW * 32;
+        base_seg = a.seg + n * HW * 32;
+    }
+    const int64_t seg_gs = (int64_t)a.N * HW * 32;
+    auto load_raw = [&](int g, u32x2* rx) {
+        const int8_t* s = g < G0 ? base_in0 + g * HW * 32 : base_seg + (g - G0) * seg_gs;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) rx[k] = *(const u32x2*)(s + off[k]);
+    };
+    auto stage = [&](int g, const u32x2* rx, int buf) {
+        const u32x4* pr = (const u32x4*)(s_abh + g * 32 + qq * 8);
+        const u32x4 pa = pr[0], pb = pr[1];
+        uint32_t s[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            uint32_t rl, rh;
+            pro4_halves(rx[k].x, pa.x, pa.y, pa.z, pa.w, rl, rh);
+            s[0] += rl & 0x00ff00ffu;
+            s[1] += rh & 0x00ff00ffu;
+            pro4_halves(rx[k].y, pb.x, pb.y, pb.z, pb.w, rl, rh);
+            s[2] += rl & 0x00ff00ffu;
+            s[3] += rh & 0x00ff00ffu;
+        }
+        uint32_t hq[4], lq[4];
+        const i16x2 k512 = {512, 512};
+        const i16x2 k3 = {3, 3};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const i16x2 sv = __builtin_bit_cast(i16x2, s[i]) - k512;
+            hq[i] = __builtin_bit_cast(uint32_t, (i16x2)(sv >> (i16x2){2, 2}));
+            lq[i] = __builtin_bit_cast(uint32_t, (i16x2)(sv & k3));
+        }
+        const u32x2 hb = {pack_low_bytes(hq[0], hq[1]), pack_low_bytes(hq[2], hq[3])};
+        const u32x2 lb = {pack_low_bytes(lq[0], lq[1]), pack_low_bytes(lq[2], lq[3])};
+        uint8_t* row_h = (uint8_t*)(s_b + (buf * 2 + 0) * 128);
+        uint8_t* row_l = (uint8_t*)(s_b + (buf * 2 + 1) * 128);
+        const int o16 = swz(pp, qq >> 1) * 16 + 8 * (qq & 1);
+        *(u32x2*)(row_h + o16) = hb;
+        *(u32x2*)(row_l + o16) = lb;
+    };
+
+    i32x16 acch[2], accl[2];
+    {
+        i32x16 init;
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+            const int o = co * 32 + res_row(v, h);
+            init[v] = co_ok ? 128 * a.wsum[o] : 0;
+        }
+        acch[0] = acch[1] = init;
+        accl[0] = accl[1] = i32x16{};
+    }
+    const u32x4* wrow = (const u32x4*)(a.w + ((int64_t)(co_ok ? co : 0) * 32 + j) * 32 + 16 * h);
+    const int64_t wg = (int64_t)a.cout * 2;               // 16-byte chunks per weight group
+
+    u32x2 rx[4];
+    load_raw(0, rx);
+    __syncthreads();                                      // s_abh
+    for (int g = 0; g < G; ++g) {
+        const int buf = g & 1;
+        stage(g, rx, buf);
+        if (g + 1 < G) load_raw(g + 1, rx);
+        u32x4 aw = {0u, 0u, 0u, 0u};
+        if (co_ok) aw = wrow[g * wg];
+        __syncthreads();
+        if (co_ok) {
+            const u32x4* bh = s_b + (buf * 2 + 0) * 128;
+            const u32x4* bl = s_b + (buf * 2 + 1) * 128;
+#pragma unroll
+            for (int t = 0; t < 2; ++t) {
+                const int px = 32 * t + j;
+                acch[t] = mfma_i8(aw, bh[swz(px, h)], acch[t]);
+                accl[t] = mfma_i8(aw, bl[swz(px, h)], accl[t]);
+            }
+        }
+    }
+    if (!co_ok) return;
+    // epilogue: q = RNE(clamp(k' * (float(S) / 4), -127, 127)) (trans_w_body with the exact mean,
+    // src/knee/dense8s_kernels.cu:3226-3245)
+    float kq[16];
+#pragma unroll
+    for (int v = 0; v < 16; ++v) kq[v] = a.gd[2 * (co * 32 + res_row(v, h))];
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+        uint32_t e[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            uint32_t d = 0;
+#pragma unroll
+            for (int rr = 0; rr < 4; ++rr) {
+                const int v = 4 * k + rr;
+                const int32_t S = 4 * acch[t][v] + accl[t][v];
+                const float x = kq[v] * ((float)S * 0.25f);
+                const float q = __builtin_rintf(__builtin_fminf(__builtin_fmaxf(x, -127.0f), 127.0f));
+                d |= ((uint32_t)(int)q & 0xffu) << (8 * rr);
+            }
+            e[k] = d;
+        }
+        const u32x4 row = xchg_rows(e[0], e[1], e[2], e[3], h);
+        const int64_t op = op0 + 32 * t + j;
+        if (op < NO) {
+            const int64_t n = op / HW4, p4 = op - n * HW4;
+            *(u32x4*)((int8_t*)a.out + ((n * a.G0n + co) * HW4 + p4) * 32 + 16 * h) = row;
+        }
+    }
+}
+
+// ------------------------------------------------------------------------------------------------
+// Final features: out[n][c] = (((P0 + P1) + P2) + P3) / HW with P_q = sum over pixels s = q, q + 4, ...
+// (in order) of relu(fma(a_c, q_s, b_c)): the summation order of the reference's `final_q`
+// (src/knee/dense8s_kernels.cu:2304-2323), so the fp32 result is the same.  Workgroup = one image x 2
+// groups: 64 channels x 4 partials.
+// ------------------------------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void k_final(const int8_t* __restrict__ in0, int G0,
+                                               const int8_t* __restrict__ seg, int N, int HW, int G,
+                                               const float* __restrict__ ab, float* __restrict__ out,
+                                               int ctot) {
+    __shared__ float part[4][64];
+    const int n = blockIdx.x;
+    const int c64 = threadIdx.x & 63, qp = threadIdx.x >> 6;
+    const int g = blockIdx.y * 2 + (c64 >> 5), cc = c64 & 31;
+    float acc = 0.0f;
+    if (g < G) {
+        const int8_t* base = g < G0 ? in0 + ((int64_t)n * G0 + g) * HW * 32
+                                    : seg + ((int64_t)(g - G0) * N + n) * HW * 32;
+        const float2 p = ((const float2*)ab)[g * 32 + cc];
+        for (int s = qp; s < HW; s += 4)
+            acc += __builtin_fmaxf(__builtin_fmaf(p.x, (float)base[(int64_t)s * 32 + cc], p.y), 0.0f);
+    }
+    part[qp][c64] = acc;
+    __syncthreads();
+    if (qp == 0 && g < G)
+        out[(int64_t)n * ctot + g * 32 + cc] =
+            (((part[0][c64] + part[1][c64]) + part[2][c64]) + part[3][c64]) / (float)HW;
+}
+
+// ------------------------------------------------------------------------------------------------
+// Stem: 7x7/2 conv (pad 3) on fp16 MFMA 32x32x16 (fp32 accumulation, bias as the initial value),
+// ReLU, int8 quantisation q = RNE(min(relu(y) / sigma0, 127)), 3x3/2 max-pool (pad 1) on the bytes
+// (quantisation is monotonic, so pooling after it gives the same bytes), into in0 of block 0.
+// Workgroup = 8 x 16 pooled pixels = 17 x 33 conv pixels (18 MFMA pixel tiles) x 64 channels.
+// K = (channel, ky, kx') with kx' = kx + 1 in 1..7 and kx' = 0 a zero weight (the reference's `S_w16`
+// layout, src/knee/dense8s.py:522-530): 168 -> 11 steps of 16.  A lane's 8 K values are 8 consecutive
+// input columns 2 cx - 4 .. 2 cx + 3, whose start is even: 4-byte aligned fp16 pairs in LDS.
+// The input tile (39 x 72 per channel) is built in LDS as fp16: x16 = lut[c][u] (uint8 input) or the
+// fp16 input itself, mirrored when flip = 1, zero outside the image.
+// ------------------------------------------------------------------------------------------------
+static constexpr int ST_PY = 8, ST_PX = 16;
+static constexpr int ST_CY = 2 * ST_PY + 1, ST_CX = 2 * ST_PX + 1, ST_NCP = ST_CY * ST_CX;   // 17 x 33
+static constexpr int ST_IY = 4 * ST_PY + 7, ST_IX = 4 * ST_PX + 8;                        // 39 x 72
+static constexpr int ST_WROW = 184;                      // fp16 per weight row in LDS (168 + pad)
+static constexpr int ST_PT = (ST_NCP + 31) / 32;         // 18 pixel tiles
+
+__global__ __launch_bounds__(256) void k_stem(D8sStemArgs a, int tiles_x, int tiles_y) {
+    __shared__ __attribute__((aligned(16))) _Float16 s_in[3 * ST_IY * ST_IX];
+    __shared__ __attribute__((aligned(16))) _Float16 s_wt[64 * ST_WROW];
+    __shared__ __attribute__((aligned(16))) uint8_t s_c[ST_PT * 32 * 64];
+    __shared__ _Float16 s_lut[3 * 256];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int h = lane >> 5, j = lane & 31;
+    const int H = a.H, W = a.W, Hc = H / 2, Wc = W / 2, Hp = H / 4, Wp = W / 4;
+    const int per_img = tiles_x * tiles_y;
+    const int n = blockIdx.x / per_img, r = blockIdx.x - n * per_img;
+    const int py0 = (r / tiles_x) * ST_PY, px0 = (r % tiles_x) * ST_PX;
+    const int cy0 = 2 * py0 - 1, cx0 = 2 * px0 - 1;
+    const int iy0 = 2 * cy0 - 3, ix0 = 2 * cx0 - 4;
+
+    // weights [64][168] -> [64][184], zero tail (K steps past 168)
+    const uint16_t* wsrc = a.w16;
+    for (int i = tid; i < 64 * ST_WROW; i += 256) {
+        const int o = i / ST_WROW, k = i - o * ST_WROW;
+        s_wt[i] = k < 168 ? __builtin_bit_cast(_Float16, wsrc[o * 168 + k]) : (_Float16)0.0f;
+    }
+    if (a.kind == D8S_IN_U8)
+        for (int i = tid; i < 3 * 256; i += 256) s_lut[i] = __builtin_bit_cast(_Float16, a.lut[i]);
+    __syncthreads();
+    for (int i = tid; i < 3 * ST_IY * ST_IX; i += 256) {
+        const int c = i / (ST_IY * ST_IX), rr = i - c * ST_IY * ST_IX;
+        const int ly = rr / ST_IX, lx = rr - ly * ST_IX;
+        const int y = iy0 + ly, x = ix0 + lx;
+        _Float16 v = (_Float16)0.0f;
+        if ((unsigned)y < (unsigned)H && (unsigned)x < (unsigned)W) {
+            const int xs = a.flip ? W - 1 - x : x;
+            const int64_t idx = (((int64_t)n * 3 + c) * H + y) * W + xs;
+            if (a.kind == D8S_IN_U8)
+                v = s_lut[c * 256 + ((const uint8_t*)a.x)[idx]];
+            else
+                v = __builtin_bit_cast(_Float16, ((const uint16_t*)a.x)[idx]);
+        }
+        s_in[i] = v;
+    }
+    __syncthreads();
+
+    float bias[2][16], inv[2][16];
+#pragma unroll
+    for (int ot = 0; ot < 2; ++ot)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+            bias[ot][v] = a.bias[32 * ot + res_row(v, h)];
+            inv[ot][v] = a.inv[32 * ot + res_row(v, h)];
+        }
+    for (int pt = wave; pt < ST_PT; pt += 4) {
+        int cp = pt * 32 + j;
+        const bool cp_ok = cp < ST_NCP;
+        if (!cp_ok) cp = ST_NCP - 1;
+        const int ly = cp / ST_CX, lx = cp - ly * ST_CX;
+        f32x16 acc[2];
+#pragma unroll
+        for (int ot = 0; ot < 2; ++ot)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) acc[ot][v] = bias[ot][v];
+#pragma unroll
+        for (int s = 0; s < 11; ++s) {
+            int rk = 2 * s + h;                           // (channel, ky) row of K
+            if (rk > 20) rk = 20;                         // its weights are zero
+            const int c = rk / 7, ky = rk - 7 * (rk / 7);
+            const uint32_t* pin = (const uint32_t*)(s_in + (c * ST_IY + 2 * ly + ky) * ST_IX + 2 * lx);
+            const u32x4 bx = {pin[0], pin[1], pin[2], pin[3]};
+            const f16x8 b = __builtin_bit_cast(f16x8, bx);
+#pragma unroll
+            for (int ot = 0; ot < 2; ++ot) {
+                const f16x8 w = *(const f16x8*)(s_wt + (32 * ot + j) * ST_WROW + 16 * s + 8 * h);
+                acc[ot] = __builtin_amdgcn_mfma_f32_32x32x16_f16(w, b, acc[ot], 0, 0, 0);
+            }
+        }
+        const int cy = cy0 + ly, cx = cx0 + lx;
+        const bool in_img = cp_ok && (unsigned)cy < (unsigned)Hc && (unsigned)cx < (unsigned)Wc;
+#pragma unroll
+        for (int ot = 0; ot < 2; ++ot) {
+            uint32_t e[4];
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                uint32_t d = 0;
+#pragma unroll
+                for (int rr = 0; rr < 4; ++rr) {
+                    const int v = 4 * k + rr;
+                    const float t = __builtin_fmaxf(acc[ot][v], 0.0f) * inv[ot][v];
+                    const float q = __builtin_rintf(__builtin_fminf(t, 127.0f));
+                    d |= ((uint32_t)(int)q & 0xffu) << (8 * rr);
+                }
+                e[k] = in_img ? d : 0u;
+            }
+            const u32x4 row = xchg_rows(e[0], e[1], e[2], e[3], h);
+            if (cp_ok) *(u32x4*)(s_c + cp * 64 + 32 * ot + 16 * h) = row;
+        }
+    }
+    __syncthreads();
+    // 3x3/2 max-pool of the bytes (all in [0, 127]: byte-wise max by the borrow-free difference)
+    for (int i = tid; i < ST_PY * ST_PX * 4; i += 256) {
+        const int k = i & 3, pix = i >> 2;
+        const int py = pix / ST_PX, px = pix - py * ST_PX;
+        u32x4 m = {0u, 0u, 0u, 0u};
+#pragma unroll
+        for (int dy = 0; dy < 3; ++dy)
+#pragma unroll
+            for (int dx = 0; dx < 3; ++dx) {
+                const u32x4 v = *(const u32x4*)(s_c + ((2 * py + dy) * ST_CX + 2 * px + dx) * 64 + 16 * k);
+                const u32x4 ge = (((m | SIGN4) - v) & SIGN4) >> 7;     // 1 per byte where m >= v
+                const u32x4 mask = ge * 255u;
+                m = (m & mask) | (v & ~mask);
+            }
+        const int gy = py0 + py, gx = px0 + px;
+        if (gy < Hp && gx < Wp)
+            *(u32x4*)(a.out + ((((int64_t)n * 2 + (k >> 1)) * Hp + gy) * Wp + gx) * 32 + 16 * (k & 1)) = m;
+    }
+}
+
+// ------------------------------------------------------------------------------------------------
+// Diagnostics
+// ------------------------------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void k_copy(const u32x4* __restrict__ src, u32x4* __restrict__ dst,
+                                              int64_t n) {
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256)
+        dst[i] = src[i];
+}
+
+__global__ __launch_bounds__(256) void k_mfma_loop(int iters, int32_t* sink) {
+    const int lane = threadIdx.x & 63;
+    u32x4 a = {(uint32_t)lane, 1u, 2u, 3u}, b = {3u, (uint32_t)lane, 1u, 2u};
+    i32x16 c0 = {}, c1 = {}, c2 = {}, c3 = {};
+    for (int i = 0; i < iters; ++i) {
+        c0 = mfma_i8(a, b, c0);
+        c1 = mfma_i8(a, b, c1);
+        c2 = mfma_i8(a, b, c2);
+        c3 = mfma_i8(a, b, c3);
+    }
+    int32_t s = 0;
+#pragma unroll
+    for (int v = 0; v < 16; ++v) s += c0[v] ^ c1[v] ^ c2[v] ^ c3[v];
+    if (threadIdx.x == 0) sink[blockIdx.x] = s;
+}
+
+__global__ void k_probe_i8(const int8_t* A, const int8_t* B, int32_t* D) {
+    const int l = threadIdx.x, h = l >> 5, j = l & 31;
+    u32x4 av, bv;
+    uint8_t* pa = (uint8_t*)&av;
+    uint8_t* pb = (uint8_t*)&bv;
+    for (int k = 0; k < 16; ++k) {
+        pa[k] = (uint8_t)A[j * 32 + 16 * h + k];          // A[i = j][k]
+        pb[k] = (uint8_t)B[(16 * h + k) * 32 + j];        // B[k][j]
+    }
+    const i32x16 d = mfma_i8(av, bv, i32x16{});
+    for (int v = 0; v < 16; ++v) D[res_row(v, h) * 32 + j] = d[v];
+}
+
+__global__ void k_probe_f16(const uint16_t* A, const uint16_t* B, float* D) {
+    const int l = threadIdx.x, h = l >> 5, j = l & 31;
+    f16x8 av, bv;
+    for (int k = 0; k < 8; ++k) {
+        av[k] = __builtin_bit_cast(_Float16, A[j * 16 + 8 * h + k]);
+        bv[k] = __builtin_bit_cast(_Float16, B[(8 * h + k) * 32 + j]);
+    }
+    const f32x16 d = __builtin_amdgcn_mfma_f32_32x32x16_f16(av, bv, f32x16{}, 0, 0, 0);
+    for (int v = 0; v < 16; ++v) D[res_row(v, h) * 32 + j] = d[v];
+}
+
+// ------------------------------------------------------------------------------------------------
+// C ABI
+// ------------------------------------------------------------------------------------------------
+static thread_local std::string g_err;
+
+static int fail(int code, const std::string& msg) {
+    g_err = msg;
+    return code;
+}
+
+static int launched(const char* what) {
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return fail((int)e, std::string(what) + ": " + hipGetErrorString(e));
+    return 0;
+}
+
+static int cu_count() {
+    static int cached[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (!cached[dev]) {
+        int v = 0;
+        if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0)
+            v = 256;
+        cached[dev] = v;
+    }
+    return cached[dev];
+}
+
+#define REQUIRE(cond, msg) \
+    do { if (!(cond)) return fail((int)hipErrorInvalidValue, msg); } while (0)
+
+static int check_gemm(const D8sGemmArgs* a, const char* what) {
+    REQUIRE(a != nullptr, std::string(what) + ": null arguments");
+    REQUIRE(a->in0 && a->w && a->abh && a->gd && a->wsum, std::string(what) + ": null pointer");
+    REQUIRE(a->G0 >= 1 && a->G >= 1 && a->N >= 1 && a->HW >= 1 && a->W >= 1,
+            std::string(what) + ": G0, G, N, HW, W must be >= 1");
+    REQUIRE(a->G <= a->G0 || a->seg != nullptr, std::string(what) + ": seg is null with G > G0");
+    REQUIRE(a->HW % a->W == 0, std::string(what) + ": HW is not a multiple of W");
+    REQUIRE((int64_t)a->rows == (int64_t)a->N * a->HW, std::string(what) + ": rows != N * HW");
+    REQUIRE(a->G <= 1200, std::string(what) + ": more than 1200 groups");
+    return 0;
+}
+
+static int conv1_launch(const D8sGemmArgs* a, int32_t* acc, hipStream_t st) {
+    if (int rc = check_gemm(a, "d8s_conv1")) return rc;
+    REQUIRE(a->cout == 128, "d8s_conv1: cout must be 128");
+    REQUIRE(acc != nullptr || a->out != nullptr, "d8s_conv1: null output");
+    const unsigned blocks = (unsigned)((a->rows + C1_BM - 1) / C1_BM);
+    const size_t shm = 2 * 4096 + (size_t)a->G * 128;
+    if (acc)
+        hipLaunchKernelGGL(k_conv1<true>, dim3(blocks), dim3(256), shm, st, *a, acc);
+    else
+        hipLaunchKernelGGL(k_conv1<false>, dim3(blocks), dim3(256), shm, st, *a, nullptr);
+    return launched("d8s_conv1");
+}
+
+extern "C" int d8s_conv1(const D8sGemmArgs* a, void* stream) {
+    if (a != nullptr && a->out == nullptr) return fail((int)hipErrorInvalidValue, "d8s_conv1: null output");
+    return conv1_launch(a, nullptr, (hipStream_t)stream);
+}
+
+extern "C" int d8s_conv1_acc32(const D8sGemmArgs* a, int32_t* acc, void* stream) {
+    REQUIRE(acc != nullptr, "d8s_conv1_acc32: null accumulator buffer");
+    return conv1_launch(a, acc, (hipStream_t)stream);
+}
+
+extern "C" int d8s_conv2(const D8sConv2Args* a, void* stream) {
+    REQUIRE(a != nullptr, "d8s_conv2: null arguments");
+    REQUIRE(a->x && a->w && a->sc && a->wsum && a->out, "d8s_conv2: null pointer");
+    REQUIRE(a->N >= 1 && a->H >= 1 && a->W >= 1, "d8s_conv2: N, H, W must be >= 1");
+    int TW = 32;
+    while (TW > 1 && TW / 2 >= a->W) TW /= 2;
+    const int TH = 256 / TW;
+    const int tiles_x = (a->W + TW - 1) / TW, tiles_y = (a->H + TH - 1) / TH;
+    const int64_t total = (int64_t)a->N * tiles_x * tiles_y;
+    REQUIRE(total < (1ll << 31), "d8s_conv2: too many tiles");
+    const size_t shm = (size_t)4 * (TH + 2) * (TW + 2) * 32;
+    const unsigned grid = (unsigned)(total < 2 * cu_count() ? total : 2 * cu_count());
+    hipLaunchKernelGGL(k_conv2, dim3(grid), dim3(256), shm, (hipStream_t)stream, *a, TW, TH,
+                       tiles_x, tiles_y);
+    return launched("d8s_conv2");
+}
+
+extern "C" int d8s_transition(const D8sGemmArgs* a, void* stream) {
+    if (int rc = check_gemm(a, "d8s_transition")) return rc;
+    REQUIRE(a->out != nullptr, "d8s_transition: null output");
+    REQUIRE(a->cout >= 32 && a->cout % 32 == 0, "d8s_transition: cout must be a positive multiple of 32");
+    REQUIRE(a->G0n == a->cout / 32, "d8s_transition: G0n != cout / 32");
+    REQUIRE(a->W % 2 == 0 && (a->HW / a->W) % 2 == 0, "d8s_transition: H and W must be even");
+    const int64_t NO = (int64_t)a->N * (a->HW / 4);
+    const dim3 grid((unsigned)((a->cout + 127) / 128), (unsigned)((NO + 63) / 64));
+    const size_t shm = 8192 + (size_t)a->G * 128;
+    hipLaunchKernelGGL(k_trans, grid, dim3(256), shm, (hipStream_t)stream, *a);
+    return launched("d8s_transition");
+}
+
+extern "C" int d8s_final(const int8_t* in0, int32_t G0, const int8_t* seg, int32_t N, int32_t HW,
+                         const float* ab, float* out, int32_t ctot, void* stream) {
+    REQUIRE(in0 && ab && out, "d8s_final: null pointer");
+    REQUIRE(G0 >= 1 && N >= 1 && HW >= 1 && ctot >= 32 * G0 && ctot % 32 == 0,
+            "d8s_final: bad sizes (G0, N, HW >= 1, ctot a multiple of 32 and >= 32 G0)");
+    REQUIRE(ctot == 32 * G0 || seg != nullptr, "d8s_final: seg is null with ctot > 32 G0");
+    const int G = ctot / 32;
+    hipLaunchKernelGGL(k_final, dim3((unsigned)N, (unsigned)((G + 1) / 2)), dim3(256), 0,
+                       (hipStream_t)stream, in0, G0, seg, N, HW, G, ab, out, ctot);
+    return launched("d8s_final");
+}
+
+extern "C" int d8s_stem(const D8sStemArgs* a, void* stream) {
+    REQUIRE(a != nullptr, "d8s_stem: null arguments");
+    REQUIRE(a->x && a->w16 && a->bias && a->inv && a->out, "d8s_stem: null pointer");
+    REQUIRE(a->kind == D8S_IN_F16 || (a->kind == D8S_IN_U8 && a->lut != nullptr),
+            "d8s_stem: kind must be D8S_IN_F16, or D8S_IN_U8 with a lut");
+    REQUIRE(a->N >= 1 && a->H >= 4 && a->W >= 4 && a->H % 4 == 0 && a->W % 4 == 0,
+            "d8s_stem: H and W must be positive multiples of 4");
+    const int Hp = a->H / 4, Wp = a->W / 4;
+    const int tiles_x = (Wp + ST_PX - 1) / ST_PX, tiles_y = (Hp + ST_PY - 1) / ST_PY;
+    const int64_t blocks = (int64_t)a->N * tiles_x * tiles_y;
+    REQUIRE(blocks < (1ll << 31), "d8s_stem: too many tiles");
+    hipLaunchKernelGGL(k_stem, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream, *a, tiles_x,
+                       tiles_y);
+    return launched("d8s_stem");
+}
+
+extern "C" const char* d8s_version(void) {
+    static const std::string v = std::string("d8s-hip ") + std::to_string(D8S_ABI_VERSION) + " " +
+                                 D8S_SRC_HASH + " gfx950";
+    return v.c_str();
+}
+
+extern "C" const char* d8s_last_error(void) { return g_err.c_str(); }
+
+extern "C" int d8s_micro_copy(const void* src, void* dst, size_t bytes, void* stream) {
+    REQUIRE(src && dst && bytes % 16 == 0, "d8s_micro_copy: null pointer or size not a multiple of 16");
+    const int64_t n = (int64_t)(bytes / 16);
+    const int64_t want = (n + 255) / 256;
+    const unsigned grid = (unsigned)(want < 16 * cu_count() ? (want > 0 ? want : 1) : 16 * cu_count());
+    hipLaunchKernelGGL(k_copy, dim3(grid), dim3(256), 0, (hipStream_t)stream, (const u32x4*)src,
+                       (u32x4*)dst, n);
+    return launched("d8s_micro_copy");
+}
+
+extern "C" int d8s_micro_mfma(int32_t blocks, int32_t iters, int32_t* sink, void* stream) {
+    REQUIRE(sink && blocks >= 1 && iters >= 1, "d8s_micro_mfma: bad arguments");
+    hipLaunchKernelGGL(k_mfma_loop, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream, iters,
+                       sink);
+    return launched("d8s_micro_mfma");
+}
+
+extern "C" int d8s_probe_mfma_i8(const int8_t* A, const int8_t* B, int32_t* D, void* stream) {
+    REQUIRE(A && B && D, "d8s_probe_mfma_i8: null pointer");
+    hipLaunchKernelGGL(k_probe_i8, dim3(1), dim3(64), 0, (hipStream_t)stream, A, B, D);
+    return launched("d8s_probe_mfma_i8");
+}
+
+extern "C" int d8s_probe_mfma_f16(const uint16_t* A, const uint16_t* B, float* D, void* stream) {
+    REQUIRE(A && B && D, "d8s_probe_mfma_f16: null pointer");
+    hipLaunchKernelGGL(k_probe_f16, dim3(1), dim3(64), 0, (hipStream_t)stream, A, B, D);
+    return launched("d8s_probe_mfma_f16");
+}

@@ -1,0 +1,797 @@
+"""The INT8 DenseNet encoder on gfx950: plan, tables, package format and the runner.
+
+Host side of the reference's `src/knee/dense8s.py` (interface `Dense8SEncoder`, `:944-1651`), with the
+arithmetic on the HIP kernels of `libd8s_hip.so` (`hip.py`, C ABI `include/d8s_hip.h`):
+
+- `calibrate(encoder, batches)`: per-channel maxima of every store segment and per-tensor maxima of
+  every conv input, by forward hooks (`dense8s.py:272-318`);
+- `make_plan(encoder, cal, img)`: BatchNorm as affines, int8 weights per output channel with the sign
+  of norm2 folded into conv1, scales (`dense8s.py:374-433`, `dense8.py:176-188`);
+- `kernel_params(plan)`: the kernel tables, float64 expressions cast once to float32 / fp16
+  (`dense8s.py:436-519`); `derived_params` adds the tables only this build's kernels use;
+- `pack_meta` / `save_pack` / `load_pack`: the `.npz` package (format 1, kind "dense8s",
+  `dense8s.py:810-863`, `dense8.py:597-603`);
+- `Dense8SEncoder(pack, dev, n_total, max_inflight)`: the runner, same constructor, attributes and
+  methods as the reference's (`__call__`, `capture`, `graph_in_buf`, `store`, `trace`, `profile`,
+  `time_layers`).
+
+Quantisation (as the reference's final path: fp16 prologues everywhere, u8 bottleneck, our conv2):
+  store      q = RNE(x / sigma_c), sigma_c = max|x_c| / 127 per channel (calibration);
+  conv input u = RNE(255 sat(fp16(A q + B))), A = a sigma / (255 s), B = b / (255 s), s = amax / 255;
+  bottleneck v = RNE(255 sat(g acc + d)) (u8, scale s2u = amax / 255);
+  conv2      q = RNE(clamp(acc c2u, +-127)), c2u = s2u w2s / sigma;
+  transition q' = RNE(clamp(k' acc_mean, +-127)), k' = ts tws / sigma' (mean of the 2x2 square first);
+  final      f = mean relu(a5 sigma q + b5).
+"""
+from __future__ import annotations
+
+import collections
+import ctypes
+import itertools
+import json
+import time
+from dataclasses import dataclass, field
+from pathlib import Path
+
+import numpy as np
+import torch
+
+from . import hip
+
+QU = 255                        # u8 inputs of the kernels
+QS = 127                        # the store
+GROUP = 32                      # channels per store group = growth rate
+GROWTH = 32
+BOTTLENECK = 128
+PACK_FORMAT = 1
+KIND = "dense8s"
+STEM_C = 64
+
+
+# --- calibration ----------------------------------------------------------------------------
+@torch.no_grad()
+def calibrate(encoder, batches) -> dict:
+    """Maxima over `batches` (tensors (N, in, H, W) on the device of the float encoder): per channel |x|
+    of every store segment (block inputs = pool0 / transition outputs, every conv2 output) and per
+    tensor the conv inputs.  Keys `seg0.{b}`, `conv2.{b}.{l}` (lists) and `in1.{b}.{l}`, `in2.{b}.{l}`,
+    `tin.{b}` (numbers), as `src/knee/dense8s.py:272-318`.
+    """
+    f = encoder.features
+    chan: dict[str, torch.Tensor] = {}
+    tens: dict[str, float] = {}
+    hooks = []
+
+    def per_channel(key):
+        def hook(_m, _inp, y):
+            v = y.detach().float().abs().amax(dim=(0, 2, 3))
+            chan[key] = v if key not in chan else torch.maximum(chan[key], v)
+        return hook
+
+    def per_tensor(key):
+        def hook(_m, inp):
+            tens[key] = max(tens.get(key, 0.0), float(inp[0].detach().float().abs().max()))
+        return hook
+
+    hooks.append(f.pool0.register_forward_hook(per_channel("seg0.0")))
+    b = 0
+    while hasattr(f, f"denseblock{b + 1}"):
+        for li, layer in enumerate(getattr(f, f"denseblock{b + 1}").values()):
+            hooks.append(layer.conv2.register_forward_hook(per_channel(f"conv2.{b}.{li}")))
+            hooks.append(layer.conv1.register_forward_pre_hook(per_tensor(f"in1.{b}.{li}")))
+            hooks.append(layer.conv2.register_forward_pre_hook(per_tensor(f"in2.{b}.{li}")))
+        if hasattr(f, f"transition{b + 1}"):
+            tr = getattr(f, f"transition{b + 1}")
+            hooks.append(tr.conv.register_forward_pre_hook(per_tensor(f"tin.{b}")))
+            hooks.append(tr.pool.register_forward_hook(per_channel(f"seg0.{b + 1}")))
+        b += 1
+    try:
+        for x in batches:
+            encoder(x)
+    finally:
+        for hk in hooks:
+            hk.remove()
+    out: dict = {k: v.cpu().numpy().astype(np.float64).tolist() for k, v in chan.items()}
+    out.update(tens)
+    return out
+
+
+# --- plan -----------------------------------------------------------------------------------
+@dataclass
+class SLayer:
+    c_in: int
+    a1: np.ndarray              # norm1 as an affine [c_in] (float64)
+    b1: np.ndarray
+    s1: float                   # u8 scale of the conv1 input
+    w1: np.ndarray              # int8 [128, c_in], sign of norm2 inside
+    w1s: np.ndarray             # [128] > 0: weight scale times |a2|
+    bias1: np.ndarray           # [128] = b2 of norm2
+    s2: float                   # int8 scale of the conv2 input (amax / 127)
+    w2: np.ndarray              # int8 [32, 128, 3, 3]
+    w2s: np.ndarray             # [32]
+    sig: np.ndarray             # [32] per-channel scale of the output in the store
+
+
+@dataclass
+class SBlock:
+    c0: int
+    h: int
+    w: int
+    sig0: np.ndarray            # [c0] per-channel scale of the block input
+    layers: list[SLayer]
+    ta: np.ndarray | None = None        # transition: norm as an affine [c_tot]
+    tb: np.ndarray | None = None
+    ts: float | None = None             # u8 scale of the transition conv input
+    tw: np.ndarray | None = None        # int8 [c_tot // 2, c_tot]
+    tws: np.ndarray | None = None       # [c_tot // 2]
+
+    @property
+    def c_tot(self) -> int:
+        return self.c0 + GROWTH * len(self.layers)
+
+    @property
+    def sig_all(self) -> np.ndarray:
+        return np.concatenate([self.sig0] + [L.sig for L in self.layers])
+
+
+@dataclass
+class SPlan:
+    img: int
+    in_ch: int
+    w0: np.ndarray              # stem with norm0 folded in, float32 [64, in_ch, 7, 7]
+    b0: np.ndarray
+    blocks: list[SBlock] = field(default_factory=list)
+    a5: np.ndarray | None = None
+    b5: np.ndarray | None = None
+
+    @property
+    def n_features(self) -> int:
+        return self.blocks[-1].c_tot
+
+
+def bn_affine(bn) -> tuple[np.ndarray, np.ndarray]:
+    """BatchNorm in eval as y = s x + t (float64), `src/knee/dense8.py:176-179`."""
+    s = bn.weight.detach().double() / torch.sqrt(bn.running_var.detach().double() + bn.eps)
+    t = bn.bias.detach().double() - bn.running_mean.detach().double() * s
+    return s.cpu().numpy(), t.cpu().numpy()
+
+
+def quant_weight(w: torch.Tensor) -> tuple[np.ndarray, np.ndarray]:
+    """int8 per output channel, scale = max|w| / 127, q = RNE(w / scale) in float32
+    (`src/knee/dense8.py:182-188`)."""
+    w = w.detach().float().cpu()
+    scale = w.abs().flatten(1).amax(1).clamp_min(1e-12) / QS
+    inv = (1.0 / scale).view(-1, *[1] * (w.dim() - 1))
+    q = torch.round(w * inv).clamp(-128, 127)
+    return q.to(torch.int8).numpy(), scale.numpy().astype(np.float32)
+
+
+def store_scale(v, floor: float = 1e-6) -> np.ndarray:
+    """sigma = max(amax, floor) / 127 per channel (`src/knee/dense8s.py:374-375`)."""
+    return np.maximum(np.asarray(v, dtype=np.float64), floor) / QS
+
+
+def make_plan(encoder, cal: dict, img: int) -> SPlan:
+    """The plan of `encoder` (a `densenet.DenseNet` in eval, BatchNorms not folded) with the maxima `cal`
+    of `calibrate` (`src/knee/dense8s.py:378-433`)."""
+    f = encoder.features
+    a0, b0 = bn_affine(f.norm0)
+    w0 = f.conv0.weight.detach().double().cpu().numpy() * a0[:, None, None, None]
+    plan = SPlan(img=img, in_ch=int(f.conv0.weight.shape[1]), w0=w0.astype(np.float32),
+                 b0=b0.astype(np.float32))
+    h = w = img // 4
+    c = int(f.conv0.weight.shape[0])
+    sig0 = store_scale(cal["seg0.0"])
+    k = 1
+    while hasattr(f, f"denseblock{k}"):
+        bi = k - 1
+        layers = []
+        for li, layer in enumerate(getattr(f, f"denseblock{k}").values()):
+            if not hasattr(layer.norm2, "running_var"):
+                raise ValueError(f"denseblock{k}.denselayer{li + 1}: norm2 folded, the whole model "
+                                 f"is needed")
+            a1, b1 = bn_affine(layer.norm1)
+            a2, b2 = bn_affine(layer.norm2)
+            q1, s1w = quant_weight(layer.conv1.weight)
+            sign = np.where(a2 < 0, -1, 1).astype(np.int8)
+            mag = np.abs(a2)
+            dead = mag < 1e-30
+            q1 = (q1 * sign[:, None, None, None]).astype(np.int8)
+            q1[dead] = 0
+            w1s = np.where(dead, s1w, s1w * mag)
+            q2, s2w = quant_weight(layer.conv2.weight)
+            layers.append(SLayer(
+                c_in=c + GROWTH * li, a1=a1, b1=b1,
+                s1=max(float(cal[f"in1.{bi}.{li}"]), 1e-12) / QU,
+                w1=q1.reshape(BOTTLENECK, -1), w1s=w1s.astype(np.float64),
+                bias1=b2.astype(np.float64),
+                s2=max(float(cal[f"in2.{bi}.{li}"]), 1e-12) / QS, w2=q2,
+                w2s=s2w.astype(np.float64), sig=store_scale(cal[f"conv2.{bi}.{li}"])))
+        blk = SBlock(c0=c, h=h, w=w, sig0=sig0, layers=layers)
+        c = blk.c_tot
+        if hasattr(f, f"transition{k}"):
+            tr = getattr(f, f"transition{k}")
+            blk.ta, blk.tb = bn_affine(tr.norm)
+            tq, tsw = quant_weight(tr.conv.weight)
+            blk.ts = max(float(cal[f"tin.{bi}"]), 1e-12) / QU
+            blk.tw, blk.tws = tq.reshape(tq.shape[0], -1), tsw.astype(np.float64)
+            sig0 = store_scale(cal[f"seg0.{bi + 1}"])
+            c //= 2
+            h //= 2
+            w //= 2
+        plan.blocks.append(blk)
+        k += 1
+    plan.a5, plan.b5 = bn_affine(f.norm5)
+    return plan
+
+
+def chunked(w: np.ndarray) -> np.ndarray:
+    """[cout, cin] -> [cin // 32, cout, 32]: the weights of one store group contiguous."""
+    cout, cin = w.shape
+    return np.ascontiguousarray(w.reshape(cout, cin // GROUP, GROUP).transpose(1, 0, 2))
+
+
+def abh_table(ab: np.ndarray) -> np.ndarray:
+    """The prologue [c, 2] (A, B) as fp16 pairs: [c // 2, 4] int16 = (A_2p, A_2p+1, B_2p, B_2p+1)."""
+    h = ab.astype(np.float16)
+    return np.ascontiguousarray(
+        np.stack([h[0::2, 0], h[1::2, 0], h[0::2, 1], h[1::2, 1]], 1)).view(np.int16)
+
+
+def abh_values(abh: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
+    """(A, B) per channel as float64 from an `abh_table`."""
+    h = np.ascontiguousarray(abh).view(np.float16).astype(np.float64)
+    return h[:, :2].reshape(-1), h[:, 2:].reshape(-1)
+
+
+def stem_weights16(w: np.ndarray) -> np.ndarray:
+    """Stem weights [64, 3, 7, 7] -> [64, 168] fp16, k = (channel * 7 + ky) * 8 + kx + 1, k % 8 = 0 zero
+    (`src/knee/dense8s.py:522-530`)."""
+    cout, cin, kh, kw = w.shape
+    out = np.zeros((cout, cin, kh, kw + 1), np.float32)
+    out[..., 1:] = w
+    return np.ascontiguousarray(out.reshape(cout, -1).astype(np.float16))
+
+
+def kernel_params(plan: SPlan) -> dict[str, np.ndarray]:
+    """The tables of the final path (`src/knee/dense8s.py:457-519`), same names and expressions:
+    - `L{b}_{l}_ab` [c_in, 2], `L{b}_{l}_abh` [c_in/2, 4]: conv1 prologue a sigma / (255 s1), b / (255 s1);
+    - `L{b}_{l}_gdu` [128, 2]: conv1 epilogue into the u8 bottleneck (scale s2u = s2 127 / 255);
+    - `L{b}_{l}_w1` [G, 128, 32] int8; `L{b}_{l}_w2k` [4, 9, 32, 32] int8 (input block, tap, output,
+      input); `L{b}_{l}_c2u` [32] = s2u w2s / sigma;
+    - `T{b}_ab`, `T{b}_abh`, `T{b}_w` [G, cout, 32] int8, `T{b}_gdf` [cout, 2] = (ts tws / sigma', 0);
+    - `F_ab` [n_features, 2] = (a5 sigma, b5);
+    - `S_w16` [64, 168] fp16, `S_bias` [64] = b0, `S_inv` [64] = 1 / sigma0.
+    """
+    out: dict[str, np.ndarray] = {}
+    for bi, blk in enumerate(plan.blocks):
+        sig = blk.sig_all
+        for li, L in enumerate(blk.layers):
+            s = sig[:L.c_in]
+            out[f"L{bi}_{li}_ab"] = np.stack([L.a1 * s / (QU * L.s1),
+                                              L.b1 / (QU * L.s1)], 1).astype(np.float32)
+            out[f"L{bi}_{li}_abh"] = abh_table(out[f"L{bi}_{li}_ab"])
+            out[f"L{bi}_{li}_w1"] = chunked(L.w1)
+            s2u = L.s2 * QS / QU
+            out[f"L{bi}_{li}_gdu"] = np.stack([L.w1s * L.s1 / (QU * s2u),
+                                               L.bias1 / (QU * s2u)], 1).astype(np.float32)
+            w2 = L.w2.reshape(GROWTH, 4, GROUP, 9)                 # [o, block, i, tap]
+            out[f"L{bi}_{li}_w2k"] = np.ascontiguousarray(w2.transpose(1, 3, 0, 2))
+            out[f"L{bi}_{li}_c2u"] = (s2u * L.w2s / L.sig).astype(np.float32)
+        if blk.ta is not None:
+            nxt = plan.blocks[bi + 1].sig0
+            out[f"T{bi}_ab"] = np.stack([blk.ta * sig / (QU * blk.ts),
+                                         blk.tb / (QU * blk.ts)], 1).astype(np.float32)
+            out[f"T{bi}_abh"] = abh_table(out[f"T{bi}_ab"])
+            out[f"T{bi}_w"] = chunked(blk.tw)
+            out[f"T{bi}_gd"] = np.stack([0.25 * blk.ts * blk.tws / nxt,
+                                         np.zeros_like(nxt)], 1).astype(np.float32)
+            out[f"T{bi}_gdf"] = np.stack([blk.ts * blk.tws / nxt, np.zeros_like(nxt)],
+                                         1).astype(np.float32)
+    last = plan.blocks[-1]
+    out["F_ab"] = np.stack([plan.a5 * last.sig_all, plan.b5], 1).astype(np.float32)
+    s0 = plan.blocks[0].sig0
+    out["S_w0"] = (plan.w0.astype(np.float64) / s0[:, None, None, None]).astype(np.float32)
+    out["S_b0"] = (plan.b0.astype(np.float64) / s0).astype(np.float32)
+    out["S_w16"] = stem_weights16(plan.w0)
+    out["S_bias"] = plan.b0.astype(np.float32)
+    out["S_inv"] = (1.0 / s0).astype(np.float32)
+    return out
+
+
+def input_lut(mean, std) -> np.ndarray:
+    """[3, 256] fp16 bits of x = (u / 255 - mean_c) / std_c: the fused uint8 normalisation of the stem
+    (with mean 0, std 1 it is the reference's u / 255 table, `src/knee/data/fused_uint8.py:735`)."""
+    u = np.arange(256, dtype=np.float64) / 255.0
+    m = np.asarray(mean, dtype=np.float64).reshape(-1, 1)
+    s = np.asarray(std, dtype=np.float64).reshape(-1, 1)
+    return np.ascontiguousarray(((u[None, :] - m) / s).astype(np.float16)).view(np.int16)
+
+
+def derived_params(meta: dict, par: dict) -> dict[str, np.ndarray]:
+    """Tables this build's kernels need beyond the reference's, derived from the package tables (so a
+    package with only the reference's tables loads too): per-output weight sums for the offset of the
+    unsigned activations (`L*_w1sum`, `L*_w2sum`, `T*_wsum`, int32) and the input table `S_lut`.
+    """
+    out: dict[str, np.ndarray] = {}
+    for bi, b in enumerate(meta["blocks"]):
+        for li in range(b["L"]):
+            w1 = par[f"L{bi}_{li}_w1"].astype(np.int64)           # [G, 128, 32]
+            out[f"L{bi}_{li}_w1sum"] = w1.sum(axis=(0, 2)).astype(np.int32)
+            w2 = par[f"L{bi}_{li}_w2k"].astype(np.int64)          # [4, 9, 32, 32]
+            out[f"L{bi}_{li}_w2sum"] = w2.sum(axis=(0, 1, 3)).astype(np.int32)
+        if b["trans"]:
+            tw = par[f"T{bi}_w"].astype(np.int64)                 # [G, cout, 32]
+            out[f"T{bi}_wsum"] = tw.sum(axis=(0, 2)).astype(np.int32)
+    inp = meta.get("input", {})
+    out["S_lut"] = input_lut(inp.get("mean", [0.0] * 3), inp.get("std", [1.0] * 3))
+    return out
+
+
+# --- package -------------------------------------------------------------------------------
+RUNTIME_TABLES = ("_abh", "_w1", "_gdu", "_w2k", "_c2u", "_w", "_gdf")
+
+
+def pack_meta(plan: SPlan, n: int, input_kind: str = "u8", mean=(0.5, 0.5, 0.5),
+              std=(0.25, 0.25, 0.25)) -> dict:
+    """Package metadata: format 1, kind "dense8s" (`src/knee/dense8s.py:810-830`).  `n` = images per
+    pass (graph block); `input`: "u8" (raw slices, normalised in the stem with mean / std) or "f16"
+    (already normalised fp16, the reference's input)."""
+    if input_kind not in ("u8", "f16"):
+        raise ValueError(f"input kind {input_kind!r}: expected 'u8' or 'f16'")
+    blocks = [{"c0": b.c0, "h": b.h, "w": b.w, "L": len(b.layers), "trans": b.ta is not None}
+              for b in plan.blocks]
+    return {"format": PACK_FORMAT, "kind": KIND, "n": int(n), "img": plan.img,
+            "in_ch": plan.in_ch, "kernels_sha": hip.source_sha(), "n_features": plan.n_features,
+            "stem_c": int(plan.w0.shape[0]), "conv2": "ours", "stem": "hip", "conv2_int8": True,
+            "stem_int8": False, "engines": [],
+            "input": {"kind": input_kind, "mean": [float(v) for v in mean],
+                      "std": [float(v) for v in std]},
+            "blocks": blocks}
+
+
+def pack_params(plan: SPlan) -> dict[str, np.ndarray]:
+    par = kernel_params(plan)
+    keep = ("F_ab", "S_w16", "S_bias", "S_inv")
+    return {k: v for k, v in par.items() if k in keep or k.endswith(RUNTIME_TABLES)}
+
+
+def make_pack(plan: SPlan, n: int, **kw) -> dict:
+    """The package in memory, as `load_pack` returns it."""
+    return {"meta": pack_meta(plan, n, **kw), "engines": {}, "par": pack_params(plan), "cubin": None}
+
+
+def save_pack(path: Path, plan: SPlan, n: int, **kw) -> None:
+    meta = pack_meta(plan, n, **kw)
+    arrays = {"meta": np.frombuffer(json.dumps(meta).encode(), np.uint8)}
+    arrays |= {f"par_{k}": v for k, v in pack_params(plan).items()}
+    with open(path, "wb") as fh:
+        np.savez(fh, **arrays)
+
+
+def load_pack(path: Path) -> dict:
+    """{"meta", "engines", "par", "cubin"} as `src/knee/dense8.py:597-603` (no pickles: numpy arrays
+    and a JSON byte vector)."""
+    with np.load(path, allow_pickle=False) as z:
+        meta = json.loads(bytes(z["meta"]).decode())
+        engines = {k[4:]: z[k].tobytes() for k in z.files if k.startswith("eng_")}
+        par = {k[4:]: np.array(z[k]) for k in z.files if k.startswith("par_")}
+        cubin = z["cubin"].tobytes() if "cubin" in z.files else None
+    return {"meta": meta, "engines": engines, "par": par, "cubin": cubin}
+
+
+def is_pack(pack: dict) -> bool:
+    return isinstance(pack, dict) and pack.get("meta", {}).get("kind") == KIND
+
+
+def validate_meta(meta: dict) -> None:
+    """ValueError for a package this runner cannot run (`src/knee/dense8s.py:954-956,1121-1124`)."""
+    if meta.get("kind") != KIND or meta.get("format") != PACK_FORMAT:
+        raise ValueError(f"package {meta.get('kind')} format {meta.get('format')}, "
+                         f"expected {KIND} {PACK_FORMAT}")
+    if meta.get("conv2", "trt") != "ours":
+        raise ValueError("package with TensorRT conv2 engines: only conv2 'ours' runs here")
+    if int(meta.get("stem_c", STEM_C)) != STEM_C or int(meta.get("in_ch", 3)) != 3:
+        raise ValueError(f"stem {meta.get('stem_c')} x {meta.get('in_ch')}: 64 channels of 3 "
+                         f"inputs expected")
+    img = int(meta["img"])
+    if img % 4 or img < 8:
+        raise ValueError(f"image side {img}: a multiple of 4 (>= 8) expected")
+    if int(meta["n"]) < 1:
+        raise ValueError(f"package batch {meta['n']} < 1")
+    blocks = meta["blocks"]
+    if not blocks or blocks[-1]["trans"] or any(not b["trans"] for b in blocks[:-1]):
+        raise ValueError("blocks: every block but the last needs a transition")
+    for bi, b in enumerate(blocks):
+        if b["c0"] % GROUP:
+            raise ValueError(f"block {bi}: c0 {b['c0']} not a multiple of {GROUP}")
+        if b["trans"] and (b["h"] % 2 or b["w"] % 2):
+            raise ValueError(f"block {bi}: odd side {b['h']} x {b['w']} before a transition")
+    inp = meta.get("input", {"kind": "f16"})
+    if inp.get("kind", "f16") not in ("u8", "f16"):
+        raise ValueError(f"input kind {inp.get('kind')!r}")
+
+
+# --- runner ----------------------------------------------------------------------------------
+# Graph inputs shared among the encoders of one GPU (the seeds of an ensemble read the same windows):
+# {(gpu, shape, dtype): {"buf", "src", "root"}} (`src/knee/dense8s.py:911-941`).
+_SHARED_IN: dict = {}
+_NOVER = itertools.count()
+
+
+def _shared_in(dev: int, shape: tuple, dtype) -> dict:
+    key = (dev, tuple(shape), dtype)
+    s = _SHARED_IN.get(key)
+    if s is None:
+        s = {"buf": torch.zeros(shape, dtype=dtype, device=f"cuda:{dev}"), "src": None, "root": None}
+        _SHARED_IN[key] = s
+    return s
+
+
+def _src_key(x: torch.Tensor) -> tuple:
+    """(root tensor, key of the source): a copy into the graph input is skipped when the key repeats.
+    Inference tensors have no version counter, so their key is always new."""
+    root = x
+    while root._base is not None:
+        root = root._base
+    ver = ("inf", next(_NOVER)) if x.is_inference() else x._version
+    return root, (id(root), x.data_ptr(), ver, tuple(x.shape), tuple(x.stride()))
+
+
+def _ptr(t: torch.Tensor | None) -> int:
+    return 0 if t is None else int(t.data_ptr())
+
+
+class Dense8SEncoder:
+    """The INT8 encoder on GPU `dev`: `enc(x)` with x (N, 3, img, img) on that GPU, uint8 (package input
+    "u8") or fp16 ("f16"); returns (N, n_features) float32 in its own buffer (valid until the next
+    call).  Blocks of `nb` images per pass; N is padded up to a multiple of `nb`.  Interface of the
+    reference's runner (`src/knee/dense8s.py:944-1488`): own stream, `max_inflight`, `capture(n)`,
+    `graph_in_buf(n)`, `nb`, `graphs`, `calls`, `load_s`, `in_dtype`, `in_shape`, `stream`, `out`.
+    `flip=True` in `__call__` encodes the horizontally mirrored images (flip TTA, fused in the stem).
+    """
+
+    def __init__(self, pack: dict, dev: int, n_total: int, max_inflight: int | None = None) -> None:
+        t0 = time.perf_counter()
+        meta = pack["meta"]
+        validate_meta(meta)
+        self.meta, self.dev = meta, int(dev)
+        self.nb = int(meta["n"])
+        self.n_out = -(-int(n_total) // self.nb) * self.nb
+        self.max_inflight = max_inflight
+        self.inflight: collections.deque = collections.deque()
+        self.graphs: dict = {}
+        self.calls = {"graph": 0, "plain": 0}
+        self._pad: torch.Tensor | None = None
+        self.lib = hip.library()
+        self.library_version = hip.version()
+        self.pack_sha = meta.get("kernels_sha")
+        inp = meta.get("input", {"kind": "f16"})
+        self.in_kind = hip.IN_U8 if inp.get("kind", "f16") == "u8" else hip.IN_F16
+        self.in_dtype = torch.uint8 if self.in_kind == hip.IN_U8 else torch.float16
+        self.in_shape = (self.nb, int(meta["in_ch"]), int(meta["img"]), int(meta["img"]))
+        d = f"cuda:{self.dev}"
+        with torch.cuda.device(self.dev):
+            self.stream = torch.cuda.Stream(self.dev)
+            self._buffers(pack, d)
+            self.out = torch.empty((self.n_out, meta["n_features"]), dtype=torch.float32, device=d)
+        self.load_s = time.perf_counter() - t0
+
+    # -- initialisation --
+    def _buffers(self, pack: dict, d: str) -> None:
+        meta, n = self.meta, self.nb
+        blocks = meta["blocks"]
+        par = dict(pack["par"])
+        missing = [k for k in self._needed_tables() if k not in par]
+        if missing:
+            raise ValueError(f"package tables missing: {missing[:4]}{'...' if len(missing) > 4 else ''}")
+        par.update(derived_params(meta, par))
+        # two alternating arenas: block b reads arena b % 2, its transition writes the other one
+        sizes, lay = [0, 0], []
+        for bi, b in enumerate(blocks):
+            hw = b["h"] * b["w"]
+            in0 = n * (b["c0"] // GROUP) * hw * GROUP
+            seg = b["L"] * n * hw * GROUP
+            lay.append((bi % 2, in0))
+            sizes[bi % 2] = max(sizes[bi % 2], in0 + seg)
+        self.arenas = [torch.empty(max(s, 16), dtype=torch.int8, device=d) for s in sizes]
+        self.arena_mb = round(sum(sizes) / 2**20, 1)
+        self.in0 = [self.arenas[a].data_ptr() for a, _ in lay]
+        self.seg = [self.arenas[a].data_ptr() + in0 for a, in0 in lay]
+        hw_max = max(b["h"] * b["w"] for b in blocks)
+        self.bott = torch.empty(n * BOTTLENECK * hw_max, dtype=torch.uint8, device=d)
+        dev = torch.device(d)
+        self.par = {k: torch.from_numpy(np.ascontiguousarray(v)).to(dev)
+                    for k, v in par.items() if k not in ("S_w0", "S_b0", "S_w8f")}
+        self._build_launches()
+
+    def _needed_tables(self) -> list[str]:
+        names = ["F_ab", "S_w16", "S_bias", "S_inv"]
+        for bi, b in enumerate(self.meta["blocks"]):
+            for li in range(b["L"]):
+                names += [f"L{bi}_{li}_{k}" for k in ("abh", "w1", "gdu", "w2k", "c2u")]
+            if b["trans"]:
+                names += [f"T{bi}_{k}" for k in ("abh", "w", "gdf")]
+        return names
+
+    def _build_launches(self) -> None:
+        """Argument structs of every launch of a pass (`src/knee/dense8s.py:1103-1152`)."""
+        n, P = self.nb, lambda k: _ptr(self.par[k])  # noqa: E731
+        meta = self.meta
+        self.plan_l: list = []
+        for bi, b in enumerate(meta["blocks"]):
+            hw, g0 = b["h"] * b["w"], b["c0"] // GROUP
+            layers = []
+            for li in range(b["L"]):
+                c1 = hip.GemmArgs(self.in0[bi], self.seg[bi], P(f"L{bi}_{li}_w1"),
+                                  P(f"L{bi}_{li}_abh"), P(f"L{bi}_{li}_gdu"), P(f"L{bi}_{li}_w1sum"),
+                                  _ptr(self.bott), g0, g0 + li, n, hw, b["w"], n * hw, BOTTLENECK, 0)
+                c2 = hip.Conv2Args(_ptr(self.bott), P(f"L{bi}_{li}_w2k"), P(f"L{bi}_{li}_c2u"),
+                                   P(f"L{bi}_{li}_w2sum"), self.seg[bi] + li * n * hw * GROUP,
+                                   n, b["h"], b["w"], 0)
+                layers.append((c1, c2))
+            trans = None
+            if b["trans"]:
+                cout = (b["c0"] + GROWTH * b["L"]) // 2
+                trans = hip.GemmArgs(self.in0[bi], self.seg[bi], P(f"T{bi}_w"), P(f"T{bi}_abh"),
+                                     P(f"T{bi}_gdf"), P(f"T{bi}_wsum"), self.in0[bi + 1], g0,
+                                     g0 + b["L"], n, hw, b["w"], n * hw, cout, cout // GROUP)
+            self.plan_l.append((layers, trans))
+        img = int(meta["img"])
+        self.stem_args = hip.StemArgs(0, P("S_lut"), P("S_w16"), P("S_bias"), P("S_inv"),
+                                      self.in0[0], n, img, img, self.in_kind, 0, 0)
+
+    # -- one pass --
+    def _stem(self, x_ptr: int, flip: bool, st: int) -> None:
+        self.stem_args.x = x_ptr
+        self.stem_args.flip = 1 if flip else 0
+        hip.check(self.lib.d8s_stem(ctypes.byref(self.stem_args), st), "d8s_stem")
+
+    def _final(self, bi: int, f_ptr: int, st: int, n: int | None = None) -> None:
+        b = self.meta["blocks"][bi]
+        n = self.nb if n is None else n
+        hip.check(self.lib.d8s_final(self.in0[bi], b["c0"] // GROUP, self.seg[bi], n,
+                                     b["h"] * b["w"], _ptr(self.par["F_ab"]), f_ptr,
+                                     self.meta["n_features"], st), "d8s_final")
+
+    def _conv1(self, c1, st: int) -> None:
+        hip.check(self.lib.d8s_conv1(ctypes.byref(c1), st), "d8s_conv1")
+
+    def _conv2(self, c2, st: int) -> None:
+        hip.check(self.lib.d8s_conv2(ctypes.byref(c2), st), "d8s_conv2")
+
+    def _trans(self, t, st: int) -> None:
+        hip.check(self.lib.d8s_transition(ctypes.byref(t), st), "d8s_transition")
+
+    def _pass(self, x_ptr: int, f_ptr: int, flip: bool = False, events: list | None = None) -> None:
+        st = self.stream.cuda_stream
+        mark = ((lambda tag: events.append((tag, _record(self.stream)))) if events is not None
+                else (lambda tag: None))
+        mark("start")
+        self._stem(x_ptr, flip, st)
+        mark("stem")
+        for bi, (layers, trans) in enumerate(self.plan_l):
+            for c1, c2 in layers:
+                self._conv1(c1, st)
+                mark(f"conv1_{bi}")
+                self._conv2(c2, st)
+                mark(f"conv2_{bi}")
+            if trans is not None:
+                self._trans(trans, st)
+                mark(f"trans{bi}")
+            else:
+                self._final(bi, f_ptr, st)
+                mark("final")
+
+    def _padded(self, chunk: torch.Tensor) -> torch.Tensor:
+        if chunk.shape[0] == self.nb:
+            return chunk
+        if self._pad is None:
+            self._pad = torch.zeros((self.nb, *chunk.shape[1:]), dtype=self.in_dtype,
+                                    device=f"cuda:{self.dev}")
+        self._pad[:chunk.shape[0]].copy_(chunk)
+        return self._pad
+
+    def _enqueue(self, xf: torch.Tensor, flip: bool, out_off: int = 0) -> None:
+        for i, chunk in enumerate(xf.split(self.nb)):
+            if self.max_inflight:
+                while len(self.inflight) >= self.max_inflight:
+                    self.inflight.popleft().synchronize()
+            self._pass(self._padded(chunk).data_ptr(), self.out[out_off + i * self.nb].data_ptr(),
+                       flip)
+            if self.max_inflight:
+                ev = torch.cuda.Event(blocking=True)
+                ev.record(self.stream)
+                self.inflight.append(ev)
+
+    def _check_input(self, x: torch.Tensor) -> None:
+        if x.dtype != self.in_dtype:
+            raise ValueError(f"input {x.dtype}: this package takes {self.in_dtype}")
+        if tuple(x.shape[1:]) != self.in_shape[1:]:
+            raise ValueError(f"input {tuple(x.shape)}: expected (N, {', '.join(map(str, self.in_shape[1:]))})")
+        if x.device != torch.device(f"cuda:{self.dev}"):
+            raise ValueError(f"input on {x.device}, encoder on cuda:{self.dev}")
+        if x.shape[0] > self.n_out:
+            raise ValueError(f"{x.shape[0]} images: the output holds {self.n_out}")
+
+    def capture(self, n: int, flip: bool = False) -> float:
+        """One HIP graph per block of `nb` images of a batch of `n` (`src/knee/dense8s.py:1410-1433`);
+        returns the seconds spent."""
+        n = -(-n // self.nb) * self.nb
+        if n > self.out.shape[0]:
+            raise ValueError(f"graph for {n} images: the encoder does {self.nb} per block, "
+                             f"the output holds {self.out.shape[0]}")
+        t = time.perf_counter()
+        with torch.cuda.device(self.dev):
+            shared = _shared_in(self.dev, (n, *self.in_shape[1:]), self.in_dtype)
+            static_in = shared["buf"]
+            shared["src"] = shared["root"] = None
+            with torch.cuda.stream(self.stream):
+                self._enqueue(static_in[:self.nb], flip)
+            self.stream.synchronize()
+            self.inflight.clear()
+            graphs = []
+            for i, chunk in enumerate(static_in.split(self.nb)):
+                g = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(g, stream=self.stream, capture_error_mode="thread_local"):
+                    self._pass(chunk.data_ptr(), self.out[i * self.nb].data_ptr(), flip)
+                graphs.append(g)
+            self.stream.synchronize()
+        self.graphs[(n, bool(flip))] = (graphs, shared)
+        return time.perf_counter() - t
+
+    def _graphs_for(self, n: int, flip: bool):
+        gs = self.graphs.get((n, bool(flip)))
+        if gs is None:
+            k = -(-n // self.nb)
+            for (m_, f_), (g_, s_) in sorted(self.graphs.items()):
+                if f_ == bool(flip) and m_ >= k * self.nb:
+                    return g_[:k], s_
+        return gs
+
+    def graph_in_buf(self, n: int, flip: bool = False) -> torch.Tensor | None:
+        """The static input buffer `[:n]` of the graphs captured for `n` images, or None."""
+        gs = self._graphs_for(n, flip)
+        return None if gs is None else gs[1]["buf"][:n]
+
+    def __call__(self, x: torch.Tensor, flip: bool = False) -> torch.Tensor:
+        self._check_input(x)
+        cur = torch.cuda.current_stream(self.dev)
+        self.stream.wait_stream(cur)
+        n = x.shape[0]
+        with torch.cuda.device(self.dev), torch.cuda.stream(self.stream):
+            gs = self._graphs_for(n, flip)
+            if gs is not None:
+                graphs, shared = gs
+                buf = shared["buf"][:n]
+                if (x.data_ptr() == buf.data_ptr() and x.shape == buf.shape
+                        and x.stride() == buf.stride()):
+                    shared["src"] = shared["root"] = None
+                else:
+                    root, key = _src_key(x)
+                    key = key + (n,)
+                    if shared["src"] != key:
+                        buf.copy_(x)
+                        shared["src"], shared["root"] = key, root
+                        self.calls["copy"] = self.calls.get("copy", 0) + 1
+                for g in graphs:
+                    if self.max_inflight:
+                        while len(self.inflight) >= self.max_inflight:
+                            self.inflight.popleft().synchronize()
+                    g.replay()
+                    if self.max_inflight:
+                        ev = torch.cuda.Event(blocking=True)
+                        ev.record(self.stream)
+                        self.inflight.append(ev)
+                self.calls["graph"] += 1
+            else:
+                self._enqueue(x.contiguous(), flip)
+                self.calls["plain"] += 1
+        cur.wait_stream(self.stream)
+        return self.out[:n]
+
+    # -- diagnostics --
+    def store(self, bi: int, j: int) -> torch.Tensor:
+        """Store segment (bi, j) as a float tensor (nb, c, h, w) of integers (j = 0 block input, j >= 1
+        output of layer j - 1), `src/knee/dense8s.py:1491-1508`."""
+        b = self.meta["blocks"][bi]
+        n, h, w = self.nb, b["h"], b["w"]
+        hw, g0 = h * w, b["c0"] // GROUP
+        a = self.arenas[bi % 2]
+        if j == 0:
+            off = self.in0[bi] - a.data_ptr()
+            t = a[off:off + n * g0 * hw * GROUP].view(n, g0, hw, GROUP)
+            return t.permute(0, 1, 3, 2).reshape(n, g0 * GROUP, h, w).float()
+        off = self.seg[bi] - a.data_ptr() + (j - 1) * n * hw * GROUP
+        t = a[off:off + n * hw * GROUP].view(n, hw, GROUP)
+        return t.permute(0, 2, 1).reshape(n, GROUP, h, w).float()
+
+    def bottleneck(self, bi: int) -> torch.Tensor:
+        """The planar bottleneck of the last conv1 run in block bi as uint8 (nb, 128, h, w)."""
+        b = self.meta["blocks"][bi]
+        n, h, w = self.nb, b["h"], b["w"]
+        hw = h * w
+        t = self.bott[:4 * n * hw * GROUP].view(4, n, hw, GROUP)
+        return t.permute(1, 0, 3, 2).reshape(n, 4 * GROUP, h, w)
+
+    @torch.no_grad()
+    def trace(self, x: torch.Tensor, flip: bool = False) -> tuple[dict, torch.Tensor]:
+        """One pass over the first `nb` images stopping after every launch: the store {(block, j):
+        tensor} and the features (`src/knee/dense8s.py:1510-1546`)."""
+        self._check_input(x)
+        xf = self._padded(x[:self.nb].contiguous())
+        out: dict = {}
+        st = self.stream.cuda_stream
+        with torch.cuda.device(self.dev), torch.cuda.stream(self.stream):
+            self.stream.wait_stream(torch.cuda.current_stream(self.dev))
+            f = torch.zeros((self.nb, self.meta["n_features"]), dtype=torch.float32,
+                            device=f"cuda:{self.dev}")
+            self._stem(xf.data_ptr(), flip, st)
+            for bi, (layers, trans) in enumerate(self.plan_l):
+                self.stream.synchronize()
+                out[(bi, 0)] = self.store(bi, 0).clone()
+                for li, (c1, c2) in enumerate(layers):
+                    self._conv1(c1, st)
+                    self.stream.synchronize()
+                    out[("bott", bi, li)] = self.bottleneck(bi).clone()
+                    self._conv2(c2, st)
+                    self.stream.synchronize()
+                    out[(bi, li + 1)] = self.store(bi, li + 1).clone()
+                if trans is not None:
+                    self._trans(trans, st)
+                else:
+                    self._final(bi, f.data_ptr(), st)
+            self.stream.synchronize()
+        return out, f
+
+    def profile(self, x: torch.Tensor, reps: int = 3, flip: bool = False) -> dict:
+        """GPU milliseconds per item (stem, conv1 / conv2 per block, transitions, final) of a pass of
+        `nb` images, from HIP events between launches (`src/knee/dense8s.py:1548-1563`)."""
+        self._check_input(x)
+        xf = self._padded(x[:self.nb].contiguous())
+        tot: dict[str, float] = collections.defaultdict(float)
+        with torch.cuda.device(self.dev), torch.cuda.stream(self.stream):
+            self.stream.wait_stream(torch.cuda.current_stream(self.dev))
+            for r in range(reps + 1):
+                ev: list = []
+                self._pass(xf.data_ptr(), self.out.data_ptr(), flip, ev)
+                self.stream.synchronize()
+                if r == 0:
+                    continue
+                for (_, a), (tag, b) in zip(ev, ev[1:]):
+                    tot[tag] += a.elapsed_time(b)
+        return {k: round(v / reps, 4) for k, v in sorted(tot.items())}
+
+    def _time(self, fn, reps: int = 20) -> float:
+        """ms per call of `fn` (launching on the runner's stream): a HIP graph of `reps` calls replayed
+        once as warm-up and once under events (`src/knee/dense8s.py:1565-1581`)."""
+        with torch.cuda.device(self.dev), torch.cuda.stream(self.stream):
+            fn()
+            self.stream.synchronize()
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, stream=self.stream, capture_error_mode="thread_local"):
+                for _ in range(reps):
+                    fn()
+            g.replay()
+            e0 = _record(self.stream)
+            g.replay()
+            e1 = _record(self.stream)
+            self.stream.synchronize()
+        return e0.elapsed_time(e1) / reps
+
+    def time_layers(self, reps: int = 20) -> dict:
+        """ms of every conv1, conv2 and transition on the current store."""
+        st = self.stream.cuda_stream
+        out: dict = {}
+        for bi, (layers, trans) in enumerate(self.plan_l):
+            for li, (c1, c2) in enumerate(layers):
+                out[f"c1 b{bi}l{li}"] = round(self._time(lambda c=c1: self._conv1(c, st), reps), 4)
+                out[f"c2 b{bi}l{li}"] = round(self._time(lambda c=c2: self._conv2(c, st), reps), 4)
+            if trans is not None:
+                out[f"t{bi}"] = round(self._time(lambda t=trans: self._trans(t, st), reps), 4)
+        return out
+
+
+def _record(stream) -> torch.cuda.Event:
+    e = torch.cuda.Event(enable_timing=True)
+    e.record(stream)
+    return e

@@ -1,0 +1,128 @@
+"""ctypes binding of `libd8s_hip.so`, the gfx950 kernel library (C ABI: `include/d8s_hip.h`).
+
+The reference compiles its CUDA source with NVRTC and launches kernels through the driver API from
+ctypes (`src/knee/cudart.py:1-15,87-152`).  Here the kernels are compiled ahead of time by hipcc into
+one shared library whose `extern "C"` entry points take the same by-value argument structs the
+reference's kernels take (`KArg` -> `D8sGemmArgs`, `C2Arg` -> `D8sConv2Args`) and a `hipStream_t`
+(a torch stream's `cuda_stream`).  Launches are asynchronous and are recorded into HIP graphs when
+the stream is capturing.  A failing call raises `D8sError` carrying the HIP error code and message,
+as `cudart.CudaError` carries the CUresult (`src/knee/cudart.py:29-31,57-65`).
+
+There is no fallback: if the library is missing, `library()` raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import hashlib
+import threading
+from pathlib import Path
+
+PKG = Path(__file__).resolve().parent
+CSRC = PKG / "csrc"
+SOURCE = CSRC / "d8s_kernels.hip"
+HEADER = PKG.parent / "include" / "d8s_hip.h"
+LIB_PATH = PKG / "libd8s_hip.so"
+ABI_VERSION = 1
+
+_LOCK = threading.Lock()
+_STATE: dict = {}
+
+
+class D8sError(RuntimeError):
+    """A failed library call: `code` is the hipError_t, the message comes from d8s_last_error()."""
+
+    def __init__(self, what: str, code: int, msg: str) -> None:
+        super().__init__(f"{what}: hipError {code}: {msg}")
+        self.code = code
+
+
+i32, u64, vp = ctypes.c_int32, ctypes.c_uint64, ctypes.c_void_p
+
+
+class GemmArgs(ctypes.Structure):
+    """`D8sGemmArgs` (the reference's `KArg`, `src/knee/dense8s.py:76-82`, plus `wsum`)."""
+    _fields_ = [("in0", u64), ("seg", u64), ("w", u64), ("abh", u64), ("gd", u64), ("wsum", u64),
+                ("out", u64), ("G0", i32), ("G", i32), ("N", i32), ("HW", i32), ("W", i32),
+                ("rows", i32), ("cout", i32), ("G0n", i32)]
+
+
+class Conv2Args(ctypes.Structure):
+    """`D8sConv2Args` (the reference's `C2Arg`, `src/knee/dense8s.py:131-137`, plus `wsum`)."""
+    _fields_ = [("x", u64), ("w", u64), ("sc", u64), ("wsum", u64), ("out", u64), ("N", i32),
+                ("H", i32), ("W", i32), ("pad_", i32)]
+
+
+class StemArgs(ctypes.Structure):
+    """`D8sStemArgs`: the stem with the fused uint8 normalisation / flip of the input."""
+    _fields_ = [("x", u64), ("lut", u64), ("w16", u64), ("bias", u64), ("inv", u64), ("out", u64),
+                ("N", i32), ("H", i32), ("W", i32), ("kind", i32), ("flip", i32), ("pad_", i32)]
+
+
+IN_F16, IN_U8 = 0, 1
+
+# entry point -> argument types (all return int32 status)
+SIGNATURES = {
+    "d8s_conv1": [ctypes.POINTER(GemmArgs), vp],
+    "d8s_conv1_acc32": [ctypes.POINTER(GemmArgs), vp, vp],
+    "d8s_conv2": [ctypes.POINTER(Conv2Args), vp],
+    "d8s_transition": [ctypes.POINTER(GemmArgs), vp],
+    "d8s_final": [vp, i32, vp, i32, i32, vp, vp, i32, vp],
+    "d8s_stem": [ctypes.POINTER(StemArgs), vp],
+    "d8s_micro_copy": [vp, vp, ctypes.c_size_t, vp],
+    "d8s_micro_mfma": [i32, i32, vp, vp],
+    "d8s_probe_mfma_i8": [vp, vp, vp, vp],
+    "d8s_probe_mfma_f16": [vp, vp, vp, vp],
+}
+STRING_FUNCS = ("d8s_version", "d8s_last_error")
+
+
+def source_sha() -> str:
+    """Hash of the kernel source and header: the build's `kernels_sha` (`src/knee/dense8s.py:781-783`)."""
+    h = hashlib.sha1(SOURCE.read_bytes())
+    h.update(HEADER.read_bytes())
+    return h.hexdigest()[:12]
+
+
+def library(path: Path | None = None) -> ctypes.CDLL:
+    """The loaded library (once per process).  Raises FileNotFoundError / OSError if it is missing:
+    the encoder has no other implementation.
+    """
+    with _LOCK:
+        lib = _STATE.get("lib")
+        if lib is not None:
+            return lib
+        p = Path(path or LIB_PATH)
+        if not p.is_file():
+            raise FileNotFoundError(f"{p}: the HIP kernel library is not built "
+                                    f"(run __graft_entry__.build())")
+        lib = ctypes.CDLL(str(p))
+        for name, argtypes in SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.argtypes = argtypes
+            fn.restype = ctypes.c_int32
+        for name in STRING_FUNCS:
+            fn = getattr(lib, name)
+            fn.argtypes = []
+            fn.restype = ctypes.c_char_p
+        _STATE["lib"] = lib
+        return lib
+
+
+def version() -> str:
+    return library().d8s_version().decode()
+
+
+def built_sha() -> str:
+    """The source hash compiled into the loaded library."""
+    parts = version().split()
+    return parts[2] if len(parts) >= 3 else ""
+
+
+def check(rc: int, what: str) -> None:
+    if rc != 0:
+        raise D8sError(what, int(rc), library().d8s_last_error().decode())
+
+
+def call(name: str, *args) -> None:
+    """Calls entry point `name` and raises D8sError on a non-zero status."""
+    check(getattr(library(), name)(*args), name)

@@ -1,0 +1,110 @@
+"""The whole INT8 encoder on the GPU (`Dense8SEncoder`): every launch bit-exact against the C oracle on
+the kernels' own inputs, the features against the float64 emulation and the fp32 DenseNet169.
+
+Tolerances (stated here, reported in every assertion message):
+- stem bytes: max_diff <= 1 and mismatch fraction < 1e-3 (the fp32 sums run in the MFMA's order);
+- every conv1 / conv2 / transition byte and the final features: equal to the C oracle;
+- features vs the float64 emulation: rel_l2 < 1e-2 (epilogue roundings in fp32 vs float64);
+- features vs the fp32 DenseNet169 (config 4): rel_l2 <= 0.0704 = 1.05 x 0.067, the reference's gate
+  (kaggle/int8_pack/pack_dense8s.py:1151,839-842), and cosine >= 0.99.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import checks, emulate as emu, fp32
+from rsna_knee_efficiency_amd import dense8s, densenet, synthetic
+
+pytestmark = pytest.mark.gpu
+
+
+def test_smoke_small(dev):
+    res = checks.smoke_check(str(dev))
+    print(res)
+
+
+@pytest.fixture(scope="module")
+def study512(dev):
+    """Config 4: seeded DenseNet169 (seed 0), calibration over 64 seeded slices (seed 7), one study of 24
+    uint8 slices (seed 1234) at 512 px, normalised with mean 0.5 / std 0.25 in the stem."""
+    torch.backends.cudnn.allow_tf32 = False
+    torch.backends.cuda.matmul.allow_tf32 = False
+    model = densenet.seeded_densenet169(0).to(dev)
+    cal_x = synthetic.study_u8(64, 512, seed=7)
+    cal = dense8s.calibrate(model, [synthetic.normalise(torch.from_numpy(c).to(dev))
+                                    for c in np.split(cal_x, 8)])
+    plan = dense8s.make_plan(model.cpu(), cal, 512)
+    pack = dense8s.make_pack(plan, 24, input_kind="u8")
+    enc = dense8s.Dense8SEncoder(pack, dev.index or 0, 24)
+    x = synthetic.study_u8(24, 512, seed=1234)
+    return {"model": model, "plan": plan, "pack": pack, "enc": enc, "x": x,
+            "xd": torch.from_numpy(x).to(dev)}
+
+
+def test_encoder512_layers_exact(dev, study512):
+    enc, x = study512["enc"], study512["xd"]
+    trace, f = enc.trace(x)
+    feats = f.cpu().numpy()
+    par = dense8s.kernel_params(study512["plan"])
+    res = checks.summarize(checks.check_trace(enc, trace, feats, par, max_rows=1024))
+    print(res)
+    assert res["conv1"]["mismatch"] == 0 and res["conv1"]["launches"] == 82, res
+    assert res["conv2"]["mismatch"] == 0 and res["conv2"]["launches"] == 82, res
+    assert res["trans"]["mismatch"] == 0 and res["trans"]["launches"] == 3, res
+    assert res["final"]["equal"], res
+    lut = dense8s.input_lut([0.5] * 3, [0.25] * 3)
+    got0 = trace[(0, 0)].cpu().numpy().astype(np.int8)
+    want0 = checks.stem_reference(study512["x"][:4], 1, lut, False, par["S_w16"], par["S_bias"],
+                                  par["S_inv"])
+    st = checks.bytes_cmp(got0[:4], want0)
+    assert st["max_diff"] <= 1 and st["mismatch_frac"] < 1e-3, st
+    full = enc(x).cpu().numpy()
+    assert np.array_equal(full, feats)
+
+
+def test_encoder512_vs_fp32(dev, study512):
+    """Features and the 1664 -> 8 head logits against the fp32 DenseNet169 forward."""
+    enc, x = study512["enc"], study512["xd"]
+    feats = enc(x).cpu().numpy().astype(np.float64)
+    sd = {k: v.to(dev) for k, v in study512["model"].state_dict().items()}
+    ref = fp32.forward(sd, synthetic.normalise(x)).cpu().numpy().astype(np.float64)
+    c = checks.feat_cmp(feats, ref)
+    head_w, head_b = synthetic.linear_head(1664, 8, seed=99)
+    lg = checks.feat_cmp(feats @ head_w.T + head_b, ref @ head_w.T + head_b)
+    print({"features": c, "logits": lg})
+    assert c["rel_l2"] <= 1.05 * 0.067 and c["cos_min"] >= 0.99, c
+    assert lg["cos_min"] >= 0.99, lg
+
+
+def test_encoder512_vs_emulate(dev, study512):
+    """Two images against the reference's own CPU path (float64 emulation, fp16 stem formula)."""
+    enc = study512["enc"]
+    feats = enc(study512["xd"]).cpu().numpy()[:2]
+    lut = dense8s.input_lut([0.5] * 3, [0.25] * 3)
+    x16 = np.asarray(lut).view(np.float16).astype(np.float64)[np.arange(3)[None, :, None, None],
+                                                               study512["x"][:2]]
+    par = dense8s.kernel_params(study512["plan"])
+    ref = emu.emulate(study512["plan"], torch.from_numpy(x16), par, stem_kind="f16").numpy()
+    c = checks.feat_cmp(feats, ref)
+    print(c)
+    assert c["rel_l2"] < 1e-2, c
+
+
+def test_encoder512_graph_and_flip(dev, study512):
+    enc, x = study512["enc"], study512["xd"]
+    plain = enc(x).clone()
+    enc.capture(24)
+    for _ in range(3):
+        got = enc(x).clone()
+        torch.cuda.synchronize(dev)
+        assert torch.equal(got, plain)
+        _ = (x.float() * 2).sum()                       # eager work between replays
+    assert enc.calls["graph"] >= 3
+    fl = enc(x, flip=True).clone()
+    mirrored = enc(torch.flip(x, dims=[-1]).contiguous()).clone()
+    assert torch.equal(fl, mirrored)
+    assert not torch.equal(fl, plain)
+    short = enc(x[:5]).clone()                          # fewer images than the block: padded
+    assert torch.equal(short, plain[:5])

@@ -1,0 +1,167 @@
+"""Parity of every HIP kernel with the oracle, through the C ABI, at the configurations' sizes.
+
+Integer accumulators and all bytes must be EQUAL to the oracle's (exact float64 sums + the C oracle's
+fp32 epilogues); the stem (fp32 sums in the MFMA's order) within 1 LSB with < 1e-3 of the bytes off.
+"""
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import cases, checks, lib
+from rsna_knee_efficiency_amd import dense8s, hip
+
+pytestmark = pytest.mark.gpu
+
+
+def _t(a, dev):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+
+
+def test_mfma_layout_i8(dev):
+    rng = np.random.default_rng(0)
+    A = rng.integers(-128, 128, (32, 32)).astype(np.int8)
+    B = rng.integers(-128, 128, (32, 32)).astype(np.int8)
+    D = torch.zeros(32 * 32, dtype=torch.int32, device=dev)
+    a, b = _t(A, dev), _t(B, dev)
+    hip.call("d8s_probe_mfma_i8", a.data_ptr(), b.data_ptr(), D.data_ptr(),
+             torch.cuda.current_stream(dev).cuda_stream)
+    torch.cuda.synchronize(dev)
+    assert np.array_equal(D.cpu().numpy().reshape(32, 32), A.astype(np.int64) @ B.astype(np.int64))
+
+
+def test_mfma_layout_f16(dev):
+    rng = np.random.default_rng(1)
+    A = rng.integers(-8, 9, (32, 16)).astype(np.float16)
+    B = rng.integers(-8, 9, (16, 32)).astype(np.float16)
+    D = torch.zeros(32 * 32, dtype=torch.float32, device=dev)
+    a, b = _t(A.view(np.int16), dev), _t(B.view(np.int16), dev)
+    hip.call("d8s_probe_mfma_f16", a.data_ptr(), b.data_ptr(), D.data_ptr(),
+             torch.cuda.current_stream(dev).cuda_stream)
+    torch.cuda.synchronize(dev)
+    assert np.array_equal(D.cpu().numpy().reshape(32, 32),
+                          (A.astype(np.float64) @ B.astype(np.float64)).astype(np.float32))
+
+
+@pytest.mark.parametrize("S,C", cases.GEMM_CASES)
+def test_conv1_config2(dev, S, C):
+    """Config 2: the fused prologue 1x1 GEMM, batch 24; int32 accumulators and u8 bottleneck exact."""
+    c = cases.gemm_case(S, C)
+    print(f"conv1 S={S} C_in={C} G0={c.G0} G={c.G}", flush=True)
+    acc, byt = checks.run_conv1(c, dev)
+    acc_x, byt_x = checks.exact_conv1(c)
+    assert np.array_equal(acc, acc_x), f"accumulators: {checks.bytes_cmp(acc, acc_x)}"
+    assert np.array_equal(byt, byt_x), f"bottleneck: {checks.bytes_cmp(byt, byt_x)}"
+    # the C oracle's own GEMM on sampled rows (independent of the float64 matmul)
+    rng = np.random.default_rng(S + C)
+    M = c.N * S * S
+    sel = np.unique(np.concatenate([rng.choice(M, 256, replace=False), [0, M - 1, S * S - 1, S * S]]))
+    acc_o, byt_o = lib.conv1(c.in0, c.seg, c.G0, c.G, c.N, S * S, c.abh, c.w1, c.gd, sel)
+    assert np.array_equal(acc[sel], acc_o) and np.array_equal(byt[sel], byt_o)
+    # the plain entry point writes the same bytes
+    _, byt2 = checks.run_conv1(c, dev, acc32=False)
+    assert np.array_equal(byt2, byt)
+    sat = float((byt_x == 255).mean())
+    zero = float((byt_x == 0).mean())
+    assert 0.0 < zero < 0.9 and sat < 0.5, (zero, sat)
+
+
+@pytest.mark.parametrize("S", cases.CONV2_SIDES)
+def test_conv2_config3(dev, S):
+    """Config 3: 3x3 pad-1 conv 128 -> 32, batch 24, written into its slot of a store (the other slots
+    untouched)."""
+    c = cases.conv2_case(S)
+    print(f"conv2 S={S}", flush=True)
+    got, others = checks.run_conv2(c, dev)
+    acc_x, q_x = checks.exact_conv2(c)
+    assert np.array_equal(got, q_x), checks.bytes_cmp(got, q_x)
+    assert np.all(others == 0x5A)
+    rng = np.random.default_rng(S)
+    M = c.N * S * S
+    sel = np.unique(np.concatenate([rng.choice(M, 256, replace=False), [0, S - 1, M - 1]]))
+    acc_o, q_o = lib.conv2(c.bott, c.N, S, S, c.w2k, c.sc, sel)
+    assert np.array_equal(acc_o, acc_x[sel]) and np.array_equal(q_o, got[sel])
+    assert 0.001 < float((np.abs(q_x) == 127).mean()) < 0.2
+
+
+@pytest.mark.parametrize("S,C,c0", [(128, 256, 64), (64, 512, 128), (32, 1280, 256), (16, 128, 64)])
+def test_transition(dev, S, C, c0):
+    t = cases.trans_case(S, C, N=4, c0=c0)
+    print(f"transition S={S} C={C}", flush=True)
+    got = checks.run_trans(t, dev)
+    S_x, q_x = checks.exact_trans(t)
+    assert np.array_equal(got, q_x), checks.bytes_cmp(got, q_x)
+    rng = np.random.default_rng(C)
+    n_out = t["N"] * S * S // 4
+    sel = np.unique(np.concatenate([rng.choice(n_out, 128, replace=False), [0, n_out - 1]]))
+    S_o, q_o = lib.trans(t["in0"], t["seg"], t["G0"], t["G"], t["N"], S * S, S, t["abh"], t["w"],
+                         t["gdf"], t["cout"], sel)
+    assert np.array_equal(S_o, S_x[sel]) and np.array_equal(q_o, got[sel])
+    assert float((np.abs(q_x) == 127).mean()) < 0.2 and float((q_x == 0).mean()) < 0.5
+
+
+@pytest.mark.parametrize("N,HW,C,c0", [(24, 256, 1664, 640), (3, 4, 128, 64), (2, 9, 96, 32)])
+def test_final(dev, N, HW, C, c0):
+    rng = np.random.default_rng(HW)
+    q = rng.integers(-127, 128, (N, C, HW)).astype(np.int8)
+    in0, seg = cases.store_from_q(q, c0 // 32)
+    ab = np.stack([rng.uniform(0.001, 0.02, C), rng.normal(0, 0.2, C)], 1).astype(np.float32)
+    got = checks.run_final(in0, c0 // 32, seg, N, HW, ab, C, dev)
+    want = lib.final(in0, c0 // 32, seg, N, HW, ab, C)
+    assert np.array_equal(got, want)
+    ref = np.maximum(ab[:, 0][None, :, None] * q.astype(np.float64) + ab[:, 1][None, :, None], 0).mean(2)
+    assert np.abs(got - ref).max() / np.abs(ref).max() < 1e-5
+
+
+def _stem_tables(seed: int = 3):
+    rng = np.random.default_rng(seed)
+    w = rng.normal(0, np.sqrt(2 / 147), (64, 3, 7, 7)).astype(np.float32)
+    w16 = dense8s.stem_weights16(w)
+    bias = rng.normal(0, 0.1, 64).astype(np.float32)
+    inv = (1.0 / rng.uniform(0.02, 0.05, 64)).astype(np.float32)
+    lut = dense8s.input_lut([0.5] * 3, [0.25] * 3)
+    return w16, bias, inv, lut
+
+
+@pytest.mark.parametrize("H,W,N", [(512, 512, 2), (64, 96, 3), (20, 12, 1)])
+def test_stem(dev, H, W, N):
+    w16, bias, inv, lut = _stem_tables()
+    rng = np.random.default_rng(H + W)
+    x = rng.integers(0, 256, (N, 3, H, W)).astype(np.uint8)
+    print(f"stem {N}x3x{H}x{W}", flush=True)
+    got = checks.run_stem(x, hip.IN_U8, lut, False, w16, bias, inv, dev)
+    want = checks.stem_reference(x, hip.IN_U8, lut, False, w16, bias, inv)
+    cmp_ = checks.bytes_cmp(got, want)
+    assert cmp_["max_diff"] <= 1 and cmp_["mismatch_frac"] < 1e-3, cmp_
+    # flip = the kernel on the mirrored image; fp16 input = the same values as the uint8 table
+    got_f = checks.run_stem(x, hip.IN_U8, lut, True, w16, bias, inv, dev)
+    got_m = checks.run_stem(np.ascontiguousarray(x[..., ::-1]), hip.IN_U8, lut, False, w16, bias,
+                            inv, dev)
+    assert np.array_equal(got_f, got_m)
+    x16 = np.asarray(lut).view(np.float16)[np.arange(3)[None, :, None, None], x]
+    got_h = checks.run_stem(x16, hip.IN_F16, None, False, w16, bias, inv, dev)
+    assert np.array_equal(got_h, got)
+    Hp, Wp = H // 4, W // 4
+    sel = np.unique(np.concatenate([rng.choice(N * Hp * Wp, min(64, N * Hp * Wp), replace=False),
+                                    [0, N * Hp * Wp - 1]]))
+    want_o = lib.stem(x, 1, lut, False, w16, bias, inv, sel)
+    flat = got.transpose(0, 2, 3, 1).reshape(-1, 64)[sel]
+    cmp_o = checks.bytes_cmp(flat, want_o)
+    assert cmp_o["max_diff"] <= 1 and cmp_o["mismatch_frac"] < 1e-2, cmp_o
+
+
+def test_entry_point_errors(dev):
+    """Invalid arguments are rejected on the host with hipErrorInvalidValue and a message."""
+    lib_ = hip.library()
+    args = hip.GemmArgs()
+    rc = lib_.d8s_conv1(ctypes.byref(args), None)
+    assert rc == 1 and b"null" in lib_.d8s_last_error()
+    c2 = hip.Conv2Args(1, 1, 1, 1, 1, 0, 4, 4, 0)
+    assert lib_.d8s_conv2(ctypes.byref(c2), None) == 1
+    st = hip.StemArgs(1, 0, 1, 1, 1, 1, 1, 10, 10, hip.IN_U8, 0, 0)
+    assert lib_.d8s_stem(ctypes.byref(st), None) == 1
+    with pytest.raises(hip.D8sError):
+        hip.call("d8s_transition", ctypes.byref(args), None)
