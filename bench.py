@@ -1,0 +1,240 @@
+"""Benchmark of the INT8 DenseNet169 encoder on one MI355X (BASELINE.json metric: 512 px DenseNet169 INT8
+slices/s on 1 MI355X; 24-slice study latency in ms).
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+
+Workload (`value`): configuration 5, sustained throughput.  A step = one synthetic study: 2 seeded
+DenseNet169 weight sets x 2 crops x 24 slices of 3 x 512 x 512 uint8 with flip TTA = one pass of 96
+encoded images per seed (48 slices + their mirrors, the flip fused in the stem), i.e. 192 encoded
+slices per step.  Inputs are resident in HBM (4 distinct studies, cycled); each encoder call replays
+its HIP graph.  value = 192 K / T slices/s.
+`study_latency_ms`: configuration 4, one 24-slice study through one encoder (batch 24, one pass).
+`roofline`: the dominant kernel family, from HIP events between launches on the encoder's stream over
+R eager passes of configuration 5 (algorithmic bytes of every launch / its measured time).
+`cpu_baseline`: the float32 DenseNet169 forward (`oracle/fp32.py`) at batch 1 on the host cores.
+One JSON line on stdout.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+import torch
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+import __graft_entry__  # noqa: E402
+
+__graft_entry__.load_package()
+from rsna_knee_efficiency_amd import dense8s, densenet, synthetic  # noqa: E402
+
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, published
+I8_PEAK_TOPS = 5000.0          # MI355X dense int8 MFMA, published
+IMG = 512
+SLICES = 24
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+def build_encoder(seed: int, nb: int, dev: torch.device) -> tuple[dense8s.Dense8SEncoder, dense8s.SPlan]:
+    model = densenet.seeded_densenet169(seed).to(dev)
+    cal_x = synthetic.study_u8(64, IMG, seed=7)
+    with torch.no_grad():
+        cal = dense8s.calibrate(model, [synthetic.normalise(torch.from_numpy(c).to(dev))
+                                        for c in np.split(cal_x, 8)])
+    plan = dense8s.make_plan(model.cpu(), cal, IMG)
+    enc = dense8s.Dense8SEncoder(dense8s.make_pack(plan, nb, input_kind="u8"), dev.index or 0, nb)
+    return enc, plan
+
+
+def kernel_bytes(meta: dict, n: int) -> dict[str, list[float]]:
+    """Algorithmic HBM bytes of every launch of a pass of n images, per kernel family: compulsory reads
+    of the activations and writes of the outputs, plus the weights and tables (read once)."""
+    out: dict[str, list[float]] = {"stem": [], "conv1": [], "conv2": [], "trans": [], "final": []}
+    img = meta["img"]
+    out["stem"].append(n * 3 * img * img + n * 64 * (img // 4) ** 2 + 64 * 168 * 2 + 3 * 256 * 2)
+    for b in meta["blocks"]:
+        hw = b["h"] * b["w"]
+        M = n * hw
+        for li in range(b["L"]):
+            cin = b["c0"] + 32 * li
+            out["conv1"].append(M * cin + M * 128 + 128 * cin + cin * 4 + 128 * 12)
+            out["conv2"].append(M * 128 + M * 32 + 36864 + 32 * 8)
+        ctot = b["c0"] + 32 * b["L"]
+        if b["trans"]:
+            cout = ctot // 2
+            out["trans"].append(M * ctot + (M // 4) * cout + cout * ctot + ctot * 4 + cout * 12)
+        else:
+            out["final"].append(M * ctot + n * ctot * 4 + ctot * 8)
+    return out
+
+
+def kernel_ops(meta: dict, n: int) -> dict[str, float]:
+    """int8 MFMA operations (2 per MAC) of a pass, per family (the transition at quarter resolution)."""
+    img = meta["img"]
+    ops = {"stem": 2.0 * n * 64 * 147 * (img // 2) ** 2, "conv1": 0.0, "conv2": 0.0, "trans": 0.0}
+    for b in meta["blocks"]:
+        M = n * b["h"] * b["w"]
+        for li in range(b["L"]):
+            ops["conv1"] += 2.0 * M * (b["c0"] + 32 * li) * 128
+            ops["conv2"] += 2.0 * M * 1152 * 32
+        if b["trans"]:
+            ctot = b["c0"] + 32 * b["L"]
+            ops["trans"] += 2.0 * (M // 4) * ctot * (ctot // 2)
+    return ops
+
+
+def family_times(enc: dense8s.Dense8SEncoder, x: torch.Tensor, reps: int, mode) -> dict[str, float]:
+    """Summed ms per kernel family of one pass (mean over reps), from HIP events between launches."""
+    prof = enc.profile(x, reps=reps, flip=mode)
+    fam: dict[str, float] = {}
+    for tag, ms in prof.items():
+        key = tag.rstrip("0123456789").rstrip("_")
+        key = {"trans": "trans", "conv1": "conv1", "conv2": "conv2", "stem": "stem",
+               "final": "final"}.get(key, key)
+        fam[key] = fam.get(key, 0.0) + ms
+    return fam
+
+
+def cpu_baseline(reps: int = 5, warmup: int = 2) -> dict:
+    from oracle import fp32
+    cores = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
+    cores = min(cores or 1, int(os.environ.get("OMP_NUM_THREADS", cores or 1)))
+    torch.set_num_threads(cores)
+    model = densenet.seeded_densenet169(0)
+    sd = model.state_dict()
+    x = synthetic.normalise(torch.from_numpy(synthetic.study_u8(1, IMG, seed=1234)))
+    for _ in range(warmup):
+        fp32.forward(sd, x)
+    ts = []
+    for _ in range(reps):
+        t = time.perf_counter()
+        fp32.forward(sd, x)
+        ts.append(time.perf_counter() - t)
+    med = float(np.median(ts))
+    cpu = platform.processor() or ""
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                cpu = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {"value": round(1.0 / med, 4), "unit": "slices/s", "cores": cores, "kind": "port",
+            "sample": f"fp32 DenseNet169 forward (oracle/fp32.py), batch 1, 512 px, {warmup} warm-up + "
+                      f"{reps} timed, median {med * 1e3:.0f} ms; CPU {cpu}"}
+
+
+def main() -> None:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--prof-reps", type=int, default=3)
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print(f"bench.py: this build runs on one GPU (the encoder is per-GPU, replicas need no "
+              f"communication); --gpus {args.gpus} is not supported", file=sys.stderr)
+        sys.exit(2)
+    if not torch.cuda.is_available():
+        print("bench.py: no GPU", file=sys.stderr)
+        sys.exit(2)
+    torch.backends.cudnn.allow_tf32 = False
+    torch.backends.cuda.matmul.allow_tf32 = False
+    dev = torch.device("cuda:0")
+    t0 = time.perf_counter()
+    nb = 4 * SLICES                                     # 2 crops x 24 slices x flip
+    encs = [build_encoder(seed, nb, dev)[0] for seed in (0, 1)]
+    log(f"encoders built in {time.perf_counter() - t0:.1f} s")
+    # 4 distinct studies resident in HBM: each 2 crops x 24 slices (uint8)
+    studies = []
+    for s in range(4):
+        crops = [synthetic.study_u8(SLICES, IMG, seed=1234 + 2 * s + c) for c in range(2)]
+        studies.append(torch.from_numpy(np.concatenate(crops)).to(dev))
+    for e in encs:
+        e.capture(2 * SLICES, flip="tta")
+    torch.cuda.synchronize()
+
+    def step(k: int) -> None:
+        for e in encs:
+            e(studies[k % len(studies)], flip="tta")
+
+    for k in range(args.warmup):
+        step(k)
+    torch.cuda.synchronize()
+    t = time.perf_counter()
+    for k in range(args.steps):
+        step(k)
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t
+    per_step = 2 * nb
+    value = per_step * args.steps / dt
+    log(f"config 5: {args.steps} studies in {dt:.3f} s: {value:.1f} slices/s")
+
+    # configuration 4: one 24-slice study, batch 24, one encoder
+    enc4, _ = build_encoder(0, SLICES, dev)
+    x4 = studies[0][:SLICES].contiguous()
+    enc4.capture(SLICES)
+    for _ in range(args.warmup):
+        enc4(x4)
+    torch.cuda.synchronize()
+    lat = []
+    for _ in range(max(args.steps, 5)):
+        ta = time.perf_counter()
+        enc4(x4)
+        torch.cuda.synchronize()
+        lat.append(time.perf_counter() - ta)
+    study_ms = float(np.median(lat)) * 1e3
+    log(f"config 4: study latency {study_ms:.3f} ms (median of {len(lat)})")
+
+    # per-family kernel times (eager passes, HIP events on the encoder's stream)
+    fam = family_times(encs[0], studies[0], args.prof_reps, "tta")
+    byts = kernel_bytes(encs[0].meta, nb)
+    ops = kernel_ops(encs[0].meta, nb)
+    pass_ms = sum(fam.values())
+    dom = max(("conv1", "conv2", "trans", "stem"), key=lambda k: fam.get(k, 0.0))
+    dom_bytes = sum(byts[dom])
+    launches = len(byts[dom])
+    avg_ms = fam[dom] / launches
+    achieved = dom_bytes / launches / (avg_ms * 1e-3) / 1e9
+    fam_gbs = {k: round(sum(byts[k]) / (fam[k] * 1e-3) / 1e9, 1) for k in byts if fam.get(k)}
+    fam_tops = {k: round(ops[k] / (fam[k] * 1e-3) / 1e12, 1) for k in ops if fam.get(k)}
+    log(f"pass of {nb}: {pass_ms:.3f} ms; families ms {json.dumps({k: round(v, 3) for k, v in fam.items()})}")
+    log(f"families GB/s {fam_gbs}; int8 TOP/s {fam_tops}")
+    total_bytes = sum(sum(v) for v in byts.values())
+    out = {
+        "metric": "512px DenseNet169 INT8 slices/sec on 1 MI355X; 24-slice study latency ms",
+        "value": round(value, 2), "unit": "slices/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(dt / args.steps * 1e3, 3),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "i8",
+        "data": "synthetic (seeded uint8 slice stacks, seeded DenseNet169 weights)",
+        "config": {"workload": "C5 sustained: per step one study = 2 seeds x (2 crops x 24 slices "
+                               "+ flip TTA) = 2 passes of 96 encoded 512px slices",
+                   "global_batch": nb, "seeds": 2, "image": IMG, "parallelism": "none (1 GPU)"},
+        "study_latency_ms": round(study_ms, 3),
+        "study_latency_config": "C4: one 24-slice study, batch 24, one encoder, HIP graph replay",
+        "pass_ms_eager": round(pass_ms, 3),
+        "pass_hbm_frac": round(total_bytes / (pass_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+        "family_ms": {k: round(v, 3) for k, v in fam.items()},
+        "family_gbs": fam_gbs, "family_int8_tops": fam_tops,
+        "roofline": {"bound": "hbm", "kernel": f"d8s_{dom} (all {launches} launches of a pass)",
+                     "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None},
+    }
+    if not args.no_cpu:
+        log("cpu baseline ...")
+        out["cpu_baseline"] = cpu_baseline()
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -85,7 +85,9 @@ typedef struct D8sConv2Args {
  *          zero: the reference's `S_w16` table (src/knee/dense8s.py:522-530);
  *   bias   [64] float;  inv [64] float = 1 / sigma0;
  *   out    in0 of block 0 [N][2][(H/4)*(W/4)][32];
- *   flip   1: the image is mirrored horizontally (x[..., W-1-j]). */
+ *   flip   0: as is; 1: every image mirrored horizontally (x[..., W-1-j]); 2: flip-TTA pairs, N even:
+ *          x holds N/2 images, output image n < N/2 is image n, output image n >= N/2 is image
+ *          n - N/2 mirrored. */
 #define D8S_IN_F16 0
 #define D8S_IN_U8 1
 typedef struct D8sStemArgs {

@@ -509,7 +509,9 @@ __global__ __launch_bounds__(256) void k_final(const int8_t* __restrict__ in0, i
 // layout, src/knee/dense8s.py:522-530): 168 -> 11 steps of 16.  A lane's 8 K values are 8 consecutive
 // input columns 2 cx - 4 .. 2 cx + 3, whose start is even: 4-byte aligned fp16 pairs in LDS.
 // The input tile (39 x 72 per channel) is built in LDS as fp16: x16 = lut[c][u] (uint8 input) or the
-// fp16 input itself, mirrored when flip = 1, zero outside the image.
+// fp16 input itself, zero outside the image, mirrored when flip = 1 (every image) or, with flip = 2
+// (flip-TTA pairs), for the second half of the batch: output image n >= N/2 is source image n - N/2
+// mirrored, so N/2 input images give N encoded images without a mirrored copy in memory.
 // ------------------------------------------------------------------------------------------------
 static constexpr int ST_PY = 8, ST_PX = 16;
 static constexpr int ST_CY = 2 * ST_PY + 1, ST_CX = 2 * ST_PX + 1, ST_NCP = ST_CY * ST_CX;   // 17 x 33
@@ -530,6 +532,9 @@ __global__ __launch_bounds__(256) void k_stem(D8sStemArgs a, int tiles_x, int ti
     const int py0 = (r / tiles_x) * ST_PY, px0 = (r % tiles_x) * ST_PX;
     const int cy0 = 2 * py0 - 1, cx0 = 2 * px0 - 1;
     const int iy0 = 2 * cy0 - 3, ix0 = 2 * cx0 - 4;
+    const int half = a.N >> 1;
+    const int ns = (a.flip == 2 && n >= half) ? n - half : n;          // source image
+    const bool mirror = a.flip == 1 || (a.flip == 2 && n >= half);
 
     // weights [64][168] -> [64][184], zero tail (K steps past 168)
     const uint16_t* wsrc = a.w16;
@@ -546,8 +551,8 @@ __global__ __launch_bounds__(256) void k_stem(D8sStemArgs a, int tiles_x, int ti
         const int y = iy0 + ly, x = ix0 + lx;
         _Float16 v = (_Float16)0.0f;
         if ((unsigned)y < (unsigned)H && (unsigned)x < (unsigned)W) {
-            const int xs = a.flip ? W - 1 - x : x;
-            const int64_t idx = (((int64_t)n * 3 + c) * H + y) * W + xs;
+            const int xs = mirror ? W - 1 - x : x;
+            const int64_t idx = (((int64_t)ns * 3 + c) * H + y) * W + xs;
             if (a.kind == D8S_IN_U8)
                 v = s_lut[c * 256 + ((const uint8_t*)a.x)[idx]];
             else
@@ -796,6 +801,8 @@ extern "C" int d8s_stem(const D8sStemArgs* a, void* stream) {
             "d8s_stem: kind must be D8S_IN_F16, or D8S_IN_U8 with a lut");
     REQUIRE(a->N >= 1 && a->H >= 4 && a->W >= 4 && a->H % 4 == 0 && a->W % 4 == 0,
             "d8s_stem: H and W must be positive multiples of 4");
+    REQUIRE(a->flip >= 0 && a->flip <= 2 && (a->flip != 2 || a->N % 2 == 0),
+            "d8s_stem: flip must be 0, 1, or 2 (TTA pairs, N even)");
     const int Hp = a->H / 4, Wp = a->W / 4;
     const int tiles_x = (Wp + ST_PX - 1) / ST_PX, tiles_y = (Hp + ST_PY - 1) / ST_PY;
     const int64_t blocks = (int64_t)a->N * tiles_x * tiles_y;

@@ -447,7 +447,8 @@ class Dense8SEncoder:
     call).  Blocks of `nb` images per pass; N is padded up to a multiple of `nb`.  Interface of the
     reference's runner (`src/knee/dense8s.py:944-1488`): own stream, `max_inflight`, `capture(n)`,
     `graph_in_buf(n)`, `nb`, `graphs`, `calls`, `load_s`, `in_dtype`, `in_shape`, `stream`, `out`.
-    `flip=True` in `__call__` encodes the horizontally mirrored images (flip TTA, fused in the stem).
+    `__call__(x, flip=True)` encodes the horizontally mirrored images; `flip="tta"` returns (2N, C): the N
+    images, then the same images mirrored (flip TTA fused in the stem: no mirrored copy in memory).
     """
 
     def __init__(self, pack: dict, dev: int, n_total: int, max_inflight: int | None = None) -> None:
@@ -541,9 +542,23 @@ class Dense8SEncoder:
                                       self.in0[0], n, img, img, self.in_kind, 0, 0)
 
     # -- one pass --
-    def _stem(self, x_ptr: int, flip: bool, st: int) -> None:
+    @staticmethod
+    def _mode(flip) -> int:
+        """flip -> stem mode: False 0 (as is), True 1 (every image mirrored), "tta" 2 (flip-TTA pairs: a
+        pass encodes nb/2 input images, then the same images mirrored)."""
+        if isinstance(flip, str):
+            if flip != "tta":
+                raise ValueError(f"flip {flip!r}: expected False, True or 'tta'")
+            return 2
+        return 1 if flip else 0
+
+    def _per_pass(self, mode: int) -> int:
+        """Input images one pass of `nb` encoded images consumes."""
+        return self.nb // 2 if mode == 2 else self.nb
+
+    def _stem(self, x_ptr: int, mode: int, st: int) -> None:
         self.stem_args.x = x_ptr
-        self.stem_args.flip = 1 if flip else 0
+        self.stem_args.flip = mode
         hip.check(self.lib.d8s_stem(ctypes.byref(self.stem_args), st), "d8s_stem")
 
     def _final(self, bi: int, f_ptr: int, st: int, n: int | None = None) -> None:
@@ -562,12 +577,14 @@ class Dense8SEncoder:
     def _trans(self, t, st: int) -> None:
         hip.check(self.lib.d8s_transition(ctypes.byref(t), st), "d8s_transition")
 
-    def _pass(self, x_ptr: int, f_ptr: int, flip: bool = False, events: list | None = None) -> None:
+    def _pass(self, x_ptr: int, f_ptr: int, mode: int = 0, events: list | None = None) -> None:
+        """The launch sequence of one pass (`src/knee/dense8s.py:1354-1385`): stem, then per block
+        conv1 / conv2 of every layer, the transition or the final features."""
         st = self.stream.cuda_stream
         mark = ((lambda tag: events.append((tag, _record(self.stream)))) if events is not None
                 else (lambda tag: None))
         mark("start")
-        self._stem(x_ptr, flip, st)
+        self._stem(x_ptr, mode, st)
         mark("stem")
         for bi, (layers, trans) in enumerate(self.plan_l):
             for c1, c2 in layers:
@@ -582,8 +599,10 @@ class Dense8SEncoder:
                 self._final(bi, f_ptr, st)
                 mark("final")
 
-    def _padded(self, chunk: torch.Tensor) -> torch.Tensor:
-        if chunk.shape[0] == self.nb:
+    def _padded(self, chunk: torch.Tensor, mode: int) -> torch.Tensor:
+        """One pass worth of input images: `chunk` itself if full, else copied to the head of a buffer (the
+        rest holds old images, whose outputs are computed and discarded)."""
+        if chunk.shape[0] == self._per_pass(mode):
             return chunk
         if self._pad is None:
             self._pad = torch.zeros((self.nb, *chunk.shape[1:]), dtype=self.in_dtype,
@@ -591,34 +610,51 @@ class Dense8SEncoder:
         self._pad[:chunk.shape[0]].copy_(chunk)
         return self._pad
 
-    def _enqueue(self, xf: torch.Tensor, flip: bool, out_off: int = 0) -> None:
-        for i, chunk in enumerate(xf.split(self.nb)):
+    def _enqueue(self, xf: torch.Tensor, mode: int) -> None:
+        for i, chunk in enumerate(xf.split(self._per_pass(mode))):
             if self.max_inflight:
                 while len(self.inflight) >= self.max_inflight:
                     self.inflight.popleft().synchronize()
-            self._pass(self._padded(chunk).data_ptr(), self.out[out_off + i * self.nb].data_ptr(),
-                       flip)
+            self._pass(self._padded(chunk, mode).data_ptr(), self.out[i * self.nb].data_ptr(), mode)
             if self.max_inflight:
                 ev = torch.cuda.Event(blocking=True)
                 ev.record(self.stream)
                 self.inflight.append(ev)
 
-    def _check_input(self, x: torch.Tensor) -> None:
+    def _check_input(self, x: torch.Tensor, mode: int = 0) -> None:
         if x.dtype != self.in_dtype:
             raise ValueError(f"input {x.dtype}: this package takes {self.in_dtype}")
         if tuple(x.shape[1:]) != self.in_shape[1:]:
-            raise ValueError(f"input {tuple(x.shape)}: expected (N, {', '.join(map(str, self.in_shape[1:]))})")
+            raise ValueError(f"input {tuple(x.shape)}: expected (N, "
+                             f"{', '.join(map(str, self.in_shape[1:]))})")
         if x.device != torch.device(f"cuda:{self.dev}"):
             raise ValueError(f"input on {x.device}, encoder on cuda:{self.dev}")
-        if x.shape[0] > self.n_out:
-            raise ValueError(f"{x.shape[0]} images: the output holds {self.n_out}")
+        if mode == 2 and self.nb % 2:
+            raise ValueError(f"flip-TTA pairs need an even images-per-pass, the package has {self.nb}")
+        k = self._per_pass(mode)
+        if -(-x.shape[0] // k) * self.nb > self.n_out:
+            raise ValueError(f"{x.shape[0]} images: the output holds {self.n_out} encoded images")
 
-    def capture(self, n: int, flip: bool = False) -> float:
-        """One HIP graph per block of `nb` images of a batch of `n` (`src/knee/dense8s.py:1410-1433`);
+    def _result(self, n: int, mode: int) -> torch.Tensor:
+        """The features of `n` input images: (n, C) views of `out`, or for flip-TTA (2n, C) with the n
+        plain images first, then the n mirrored ones."""
+        if mode != 2:
+            return self.out[:n]
+        k = self.nb // 2
+        if n == k:
+            return self.out[:self.nb]
+        idx = torch.arange(n, device=self.out.device)
+        rows = (idx // k) * self.nb + idx % k
+        return self.out.index_select(0, torch.cat([rows, rows + k]))
+
+    def capture(self, n: int, flip=False) -> float:
+        """One HIP graph per pass over a batch of `n` input images (`src/knee/dense8s.py:1410-1433`);
         returns the seconds spent."""
-        n = -(-n // self.nb) * self.nb
-        if n > self.out.shape[0]:
-            raise ValueError(f"graph for {n} images: the encoder does {self.nb} per block, "
+        mode = self._mode(flip)
+        k = self._per_pass(mode)
+        n = -(-n // k) * k
+        if n // k * self.nb > self.out.shape[0]:
+            raise ValueError(f"graph for {n} images: the encoder does {self.nb} per pass, "
                              f"the output holds {self.out.shape[0]}")
         t = time.perf_counter()
         with torch.cuda.device(self.dev):
@@ -626,40 +662,42 @@ class Dense8SEncoder:
             static_in = shared["buf"]
             shared["src"] = shared["root"] = None
             with torch.cuda.stream(self.stream):
-                self._enqueue(static_in[:self.nb], flip)
+                self.stream.wait_stream(torch.cuda.current_stream(self.dev))
+                self._enqueue(static_in[:k], mode)
             self.stream.synchronize()
             self.inflight.clear()
             graphs = []
-            for i, chunk in enumerate(static_in.split(self.nb)):
+            for i, chunk in enumerate(static_in.split(k)):
                 g = torch.cuda.CUDAGraph()
                 with torch.cuda.graph(g, stream=self.stream, capture_error_mode="thread_local"):
-                    self._pass(chunk.data_ptr(), self.out[i * self.nb].data_ptr(), flip)
+                    self._pass(chunk.data_ptr(), self.out[i * self.nb].data_ptr(), mode)
                 graphs.append(g)
             self.stream.synchronize()
-        self.graphs[(n, bool(flip))] = (graphs, shared)
+        self.graphs[(n, mode)] = (graphs, shared)
         return time.perf_counter() - t
 
-    def _graphs_for(self, n: int, flip: bool):
-        gs = self.graphs.get((n, bool(flip)))
+    def _graphs_for(self, n: int, mode: int):
+        gs = self.graphs.get((n, mode))
         if gs is None:
-            k = -(-n // self.nb)
-            for (m_, f_), (g_, s_) in sorted(self.graphs.items()):
-                if f_ == bool(flip) and m_ >= k * self.nb:
+            k = -(-n // self._per_pass(mode))
+            for (m_, md), (g_, s_) in sorted(self.graphs.items()):
+                if md == mode and m_ >= k * self._per_pass(mode):
                     return g_[:k], s_
         return gs
 
-    def graph_in_buf(self, n: int, flip: bool = False) -> torch.Tensor | None:
+    def graph_in_buf(self, n: int, flip=False) -> torch.Tensor | None:
         """The static input buffer `[:n]` of the graphs captured for `n` images, or None."""
-        gs = self._graphs_for(n, flip)
+        gs = self._graphs_for(n, self._mode(flip))
         return None if gs is None else gs[1]["buf"][:n]
 
-    def __call__(self, x: torch.Tensor, flip: bool = False) -> torch.Tensor:
-        self._check_input(x)
+    def __call__(self, x: torch.Tensor, flip=False) -> torch.Tensor:
+        mode = self._mode(flip)
+        self._check_input(x, mode)
         cur = torch.cuda.current_stream(self.dev)
         self.stream.wait_stream(cur)
         n = x.shape[0]
         with torch.cuda.device(self.dev), torch.cuda.stream(self.stream):
-            gs = self._graphs_for(n, flip)
+            gs = self._graphs_for(n, mode)
             if gs is not None:
                 graphs, shared = gs
                 buf = shared["buf"][:n]
@@ -684,10 +722,11 @@ class Dense8SEncoder:
                         self.inflight.append(ev)
                 self.calls["graph"] += 1
             else:
-                self._enqueue(x.contiguous(), flip)
+                self._enqueue(x.contiguous(), mode)
                 self.calls["plain"] += 1
+            res = self._result(n, mode)
         cur.wait_stream(self.stream)
-        return self.out[:n]
+        return res
 
     # -- diagnostics --
     def store(self, bi: int, j: int) -> torch.Tensor:
@@ -714,18 +753,19 @@ class Dense8SEncoder:
         return t.permute(1, 0, 3, 2).reshape(n, 4 * GROUP, h, w)
 
     @torch.no_grad()
-    def trace(self, x: torch.Tensor, flip: bool = False) -> tuple[dict, torch.Tensor]:
-        """One pass over the first `nb` images stopping after every launch: the store {(block, j):
-        tensor} and the features (`src/knee/dense8s.py:1510-1546`)."""
-        self._check_input(x)
-        xf = self._padded(x[:self.nb].contiguous())
+    def trace(self, x: torch.Tensor, flip=False) -> tuple[dict, torch.Tensor]:
+        """One pass over the first images stopping after every launch: the store {(block, j): tensor},
+        the bottleneck {("bott", block, layer): tensor} and the features (`src/knee/dense8s.py:1510-1546`)."""
+        mode = self._mode(flip)
+        self._check_input(x, mode)
+        xf = self._padded(x[:self._per_pass(mode)].contiguous(), mode)
         out: dict = {}
         st = self.stream.cuda_stream
         with torch.cuda.device(self.dev), torch.cuda.stream(self.stream):
             self.stream.wait_stream(torch.cuda.current_stream(self.dev))
             f = torch.zeros((self.nb, self.meta["n_features"]), dtype=torch.float32,
                             device=f"cuda:{self.dev}")
-            self._stem(xf.data_ptr(), flip, st)
+            self._stem(xf.data_ptr(), mode, st)
             for bi, (layers, trans) in enumerate(self.plan_l):
                 self.stream.synchronize()
                 out[(bi, 0)] = self.store(bi, 0).clone()
@@ -743,17 +783,18 @@ class Dense8SEncoder:
             self.stream.synchronize()
         return out, f
 
-    def profile(self, x: torch.Tensor, reps: int = 3, flip: bool = False) -> dict:
+    def profile(self, x: torch.Tensor, reps: int = 3, flip=False) -> dict:
         """GPU milliseconds per item (stem, conv1 / conv2 per block, transitions, final) of a pass of
         `nb` images, from HIP events between launches (`src/knee/dense8s.py:1548-1563`)."""
-        self._check_input(x)
-        xf = self._padded(x[:self.nb].contiguous())
+        mode = self._mode(flip)
+        self._check_input(x, mode)
+        xf = self._padded(x[:self._per_pass(mode)].contiguous(), mode)
         tot: dict[str, float] = collections.defaultdict(float)
         with torch.cuda.device(self.dev), torch.cuda.stream(self.stream):
             self.stream.wait_stream(torch.cuda.current_stream(self.dev))
             for r in range(reps + 1):
                 ev: list = []
-                self._pass(xf.data_ptr(), self.out.data_ptr(), flip, ev)
+                self._pass(xf.data_ptr(), self.out.data_ptr(), mode, ev)
                 self.stream.synchronize()
                 if r == 0:
                     continue

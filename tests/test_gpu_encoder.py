@@ -37,7 +37,7 @@ def study512(dev):
                                     for c in np.split(cal_x, 8)])
     plan = dense8s.make_plan(model.cpu(), cal, 512)
     pack = dense8s.make_pack(plan, 24, input_kind="u8")
-    enc = dense8s.Dense8SEncoder(pack, dev.index or 0, 24)
+    enc = dense8s.Dense8SEncoder(pack, dev.index or 0, 48)       # room for 2 passes (flip TTA)
     x = synthetic.study_u8(24, 512, seed=1234)
     return {"model": model, "plan": plan, "pack": pack, "enc": enc, "x": x,
             "xd": torch.from_numpy(x).to(dev)}
@@ -108,3 +108,18 @@ def test_encoder512_graph_and_flip(dev, study512):
     assert not torch.equal(fl, plain)
     short = enc(x[:5]).clone()                          # fewer images than the block: padded
     assert torch.equal(short, plain[:5])
+
+
+def test_encoder512_flip_tta(dev, study512):
+    """flip="tta": N images in, 2N features out (the N images, then the N mirrored), one pass per 12
+    input images (24 encoded), equal to separate plain and mirrored calls."""
+    enc, x = study512["enc"], study512["xd"]
+    plain = enc(x).clone()
+    mirrored = enc(x, flip=True).clone()
+    for n in (12, 20, 5):
+        got = enc(x[:n], flip="tta").clone()
+        assert got.shape[0] == 2 * n
+        assert torch.equal(got[:n], plain[:n]) and torch.equal(got[n:], mirrored[:n])
+    enc.capture(12, flip="tta")
+    got = enc(x[:12], flip="tta").clone()
+    assert torch.equal(got[:12], plain[:12]) and torch.equal(got[12:], mirrored[:12])
