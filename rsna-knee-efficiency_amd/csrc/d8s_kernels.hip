@@ -48,10 +48,11 @@ DEV i32x16 mfma_i8(u32x4 a, u32x4 b, i32x16 c) {
                                                  __builtin_bit_cast(i32x4, b), c, 0, 0, 0);
 }
 
+// v_perm_b32: byte i of the result is byte sel.i of the pair (s0:s1), bytes 0-3 from s1, 4-7 from s0.
+DEV uint32_t perm(uint32_t s0, uint32_t s1, uint32_t sel) { return __builtin_amdgcn_perm(s0, s1, sel); }
+
 // The four low bytes of the 16-bit halves of (lo, hi) as one dword: byte order lo.0, lo.1, hi.0, hi.1.
-DEV uint32_t pack_low_bytes(uint32_t lo, uint32_t hi) {
-    return (lo & 0xffu) | ((lo >> 8) & 0xff00u) | ((hi & 0xffu) << 16) | ((hi << 8) & 0xff000000u);
-}
+DEV uint32_t pack_low_bytes(uint32_t lo, uint32_t hi) { return perm(hi, lo, 0x06040200u); }
 
 // fp16 prologue of 4 store bytes (4 consecutive channels): q -> u = RNE(255 sat(fp16(A q + B))).
 // The byte q + 128 goes into the mantissa of fp16 1024 (exact 1024 + 128 + q), -1152 leaves q exactly,
@@ -63,8 +64,8 @@ DEV uint32_t pack_low_bytes(uint32_t lo, uint32_t hi) {
 DEV void pro4_halves(uint32_t x, uint32_t a01, uint32_t b01, uint32_t a23, uint32_t b23,
                      uint32_t& rl, uint32_t& rh) {
     const uint32_t w = x ^ SIGN4;
-    const uint32_t lo = 0x64006400u | (w & 0xffu) | ((w << 8) & 0xff0000u);
-    const uint32_t hi = 0x64006400u | ((w >> 16) & 0xffu) | ((w >> 8) & 0xff0000u);
+    const uint32_t lo = perm(0x64646464u, w, 0x04010400u);    // halves 0x64 b0, 0x64 b1
+    const uint32_t hi = perm(0x64646464u, w, 0x04030402u);    // halves 0x64 b2, 0x64 b3
     const f16x2 m1152 = {(_Float16)-1152.0f, (_Float16)-1152.0f};
     const f16x2 zero = {(_Float16)0.0f, (_Float16)0.0f};
     const f16x2 one = {(_Float16)1.0f, (_Float16)1.0f};
@@ -109,20 +110,27 @@ DEV int swz(int r, int half) { return r * 2 + (half ^ ((r >> 2) & 1)); }
 
 // ------------------------------------------------------------------------------------------------
 // conv1: 1x1 GEMM, M = N*HW pixels, K = G*32 store channels, 128 outputs.
-// Workgroup = 256 pixels, 4 waves x 64 pixels x 128 outputs (2 x 4 MFMA tiles per K group).
-// The store bytes go global -> registers -> prologue -> MFMA operand (no LDS); the weights of a
-// group (4 KB) are staged in LDS, double-buffered; the fp16 prologue table of the layer sits in LDS.
+// A wave computes 64 pixels x 128 outputs (2 x 4 MFMA tiles per K group) over the K groups of its
+// k-slice: with KS slices a workgroup of 4 waves covers 64 * 4 / KS pixels, slice s taking groups
+// s, s + KS, ... and the partial sums are added through LDS at the end (KS > 1 fills the chip when
+// there are few pixels: the 16 x 16 and 32 x 32 blocks).  The main loop has no barrier: the store
+// bytes go global -> registers (4 groups ahead) -> prologue -> MFMA operand, the weights global ->
+// registers (2 groups ahead, L1/L2 hits: every wave reads the same layer); only the fp16 prologue
+// table of the layer sits in LDS.
 // ------------------------------------------------------------------------------------------------
-static constexpr int C1_BM = 256;
+static constexpr int C1_RED = 20;                        // dwords per lane row of the k-slice sums
+static constexpr size_t C1_RED_BYTES = 2 * 8 * 64 * C1_RED * 4;   // two regions: 80 KB
 
-template <bool ACC32>
-__global__ __launch_bounds__(256) void k_conv1(D8sGemmArgs a, int32_t* __restrict__ acc_out) {
+template <int KS, bool ACC32>
+__global__ __launch_bounds__(256, 2) void k_conv1(D8sGemmArgs a, int32_t* __restrict__ acc_out) {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    constexpr int PX = 64 * 4 / KS;                       // pixels per workgroup
     const int G = a.G, G0 = a.G0;
-    u32x4* s_w = (u32x4*)smem;                          // [2][256] 16-byte chunks
-    uint32_t* s_abh = (uint32_t*)(smem + 2 * 4096);      // [G * 32] dwords
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    uint32_t* s_abh = (uint32_t*)smem;                    // [G * 32] dwords
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);    // uniform: scalar branches
     const int h = lane >> 5, j = lane & 31;
+    const int slice = wave % KS, pg = wave / KS;
 
     const uint32_t* abh32 = (const uint32_t*)a.abh;
     for (int i = tid; i < G * 32; i += 256) s_abh[i] = abh32[i];
@@ -130,7 +138,7 @@ __global__ __launch_bounds__(256) void k_conv1(D8sGemmArgs a, int32_t* __restric
     // the lane's two pixels (columns of the two MFMA tiles) and their store rows
     const int64_t rows = a.rows, HW = a.HW;
     const int64_t in_gs = HW * 32, seg_gs = (int64_t)a.N * HW * 32;
-    const int64_t mbase = (int64_t)blockIdx.x * C1_BM + wave * 64 + j;
+    const int64_t mbase = (int64_t)blockIdx.x * PX + pg * 64 + j;
     const int8_t* pin[2];
     const int8_t* pseg[2];
 #pragma unroll
@@ -144,57 +152,96 @@ __global__ __launch_bounds__(256) void k_conv1(D8sGemmArgs a, int32_t* __restric
     auto src = [&](int t, int g) -> const u32x4* {
         return (const u32x4*)(g < G0 ? pin[t] + g * in_gs : pseg[t] + (g - G0) * seg_gs);
     };
-    const u32x4* wg = (const u32x4*)a.w;                 // group g: wg[g * 256 + i]
-    const int wo = tid >> 1, whf = tid & 1;
-    const int wdst = swz(wo, whf);
+    // weights: output tile c, row 32 c + j, half h of group g at wl + g * 256 + 64 c
+    const u32x4* wl = (const u32x4*)a.w + j * 2 + h;
 
     i32x16 acc[2][4];
+    const int32_t wmul = slice == 0 ? 128 : 0;            // the offset is added by slice 0 only
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
         i32x16 init;
 #pragma unroll
-        for (int v = 0; v < 16; ++v) init[v] = 128 * a.wsum[32 * c + res_row(v, h)];
+        for (int v = 0; v < 16; ++v) init[v] = wmul * a.wsum[32 * c + res_row(v, h)];
         acc[0][c] = init;
         acc[1][c] = init;
     }
 
-    u32x4 ra[2][2];
-    u32x4 rw;
-    ra[0][0] = *src(0, 0);
-    ra[0][1] = *src(1, 0);
-    rw = wg[tid];
-    if (G > 1) {
-        ra[1][0] = *src(0, 1);
-        ra[1][1] = *src(1, 1);
-    }
-    __syncthreads();                                    // s_abh
-    s_w[wdst] = rw;
-    if (G > 1) rw = wg[256 + tid];
-    __syncthreads();
+    // this slice's groups: g_k = slice + k KS, k < nk
+    const int nk = (G - slice + KS - 1) / KS;
+    u32x4 ra[4][2];
+    u32x4 rb[4];
+    auto load_a = [&](int slot, int k) {
+        const int g = slice + k * KS;
+        ra[slot][0] = *src(0, g);
+        ra[slot][1] = *src(1, g);
+    };
+    auto load_b = [&](int k) {
+        const u32x4* p = wl + (int64_t)(slice + k * KS) * 256;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) rb[c] = p[64 * c];
+    };
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+        if (k < nk) load_a(k, k);
+    if (nk > 0) load_b(0);
+    __syncthreads();                                      // s_abh
 
-    auto step = [&](const int slot, const int g) {
+    auto step = [&](const int slot, const int k) {
+        const int g = slice + k * KS;
         const u32x4* pp = (const u32x4*)(s_abh + g * 32 + h * 16);
         const u32x4 p0 = pp[0], p1 = pp[1], p2 = pp[2], p3 = pp[3];
         const u32x4 b0 = pro16(ra[slot][0], p0, p1, p2, p3);
         const u32x4 b1 = pro16(ra[slot][1], p0, p1, p2, p3);
-        if (g + 2 < G) {
-            ra[slot][0] = *src(0, g + 2);
-            ra[slot][1] = *src(1, g + 2);
-        }
-        const u32x4* sw = s_w + (g & 1) * 256;
+        if (k + 4 < nk) load_a(slot, k + 4);
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
-            const u32x4 aw = sw[swz(32 * c + j, h)];
-            acc[0][c] = mfma_i8(aw, b0, acc[0][c]);
-            acc[1][c] = mfma_i8(aw, b1, acc[1][c]);
+            acc[0][c] = mfma_i8(rb[c], b0, acc[0][c]);
+            acc[1][c] = mfma_i8(rb[c], b1, acc[1][c]);
         }
-        if (g + 1 < G) s_w[((g + 1) & 1) * 256 + wdst] = rw;
-        if (g + 2 < G) rw = wg[(int64_t)(g + 2) * 256 + tid];
-        __syncthreads();
+        if (k + 1 < nk) load_b(k + 1);
     };
-    for (int g = 0; g < G; g += 2) {
-        step(0, g);
-        if (g + 1 < G) step(1, g + 1);
+    for (int k = 0; k < nk; k += 4) {
+        step(0, k);
+        if (k + 1 < nk) step(1, k + 1);
+        if (k + 2 < nk) step(2, k + 2);
+        if (k + 3 < nk) step(3, k + 3);
+    }
+
+    if (KS > 1) {
+        // partial sums of the slices into slice 0 through LDS: [region][t][c][lane] rows of 16 int32,
+        // rows C1_RED dwords apart (the padding spreads 8 consecutive lanes over distinct banks)
+        auto row = [&](int region, int t, int c) {
+            return (i32x16*)((int32_t*)smem + ((region * 8 + t * 4 + c) * 64 + lane) * C1_RED);
+        };
+        auto put = [&](int region) {
+            __syncthreads();
+#pragma unroll
+            for (int t = 0; t < 2; ++t)
+#pragma unroll
+                for (int c = 0; c < 4; ++c) *row(region, t, c) = acc[t][c];
+        };
+        auto take = [&](int region) {
+#pragma unroll
+            for (int t = 0; t < 2; ++t)
+#pragma unroll
+                for (int c = 0; c < 4; ++c) acc[t][c] += *row(region, t, c);
+        };
+        if (KS == 2) {
+            if (slice == 1) put(pg);
+            else __syncthreads();
+            __syncthreads();
+            if (slice == 0) take(pg);
+        } else {
+            if (slice >= 2) put(slice - 2);
+            else __syncthreads();
+            __syncthreads();
+            if (slice < 2) take(slice);
+            if (slice == 1) put(0);
+            else __syncthreads();
+            __syncthreads();
+            if (slice == 0) take(0);
+        }
+        if (slice != 0) return;
     }
 
     // epilogue: v = low byte of fma(sat(fma(g, acc, d)), 255, 2^23) (conv1w_body epilogue,
@@ -236,6 +283,7 @@ __global__ __launch_bounds__(256) void k_conv1(D8sGemmArgs a, int32_t* __restric
             const u32x4 row = xchg_rows(e[0], e[1], e[2], e[3], h);
             if (m < rows) *(u32x4*)((uint8_t*)a.out + ((int64_t)c * rows + m) * 32 + 16 * h) = row;
         }
+        asm volatile("" ::: "memory");                  // one output tile's parameters live at a time
     }
 }
 
@@ -733,12 +781,26 @@ static int conv1_launch(const D8sGemmArgs* a, int32_t* acc, hipStream_t st) {
     if (int rc = check_gemm(a, "d8s_conv1")) return rc;
     REQUIRE(a->cout == 128, "d8s_conv1: cout must be 128");
     REQUIRE(acc != nullptr || a->out != nullptr, "d8s_conv1: null output");
-    const unsigned blocks = (unsigned)((a->rows + C1_BM - 1) / C1_BM);
-    const size_t shm = 2 * 4096 + (size_t)a->G * 128;
-    if (acc)
-        hipLaunchKernelGGL(k_conv1<true>, dim3(blocks), dim3(256), shm, st, *a, acc);
-    else
-        hipLaunchKernelGGL(k_conv1<false>, dim3(blocks), dim3(256), shm, st, *a, nullptr);
+    // k-slices: the fewest that give at least 1.5 workgroups per CU
+    const int64_t want = 3 * (int64_t)cu_count() / 2;
+    int ks = 1;
+    while (ks < 4 && (a->rows + 64 * 4 / ks - 1) / (64 * 4 / ks) < want) ks *= 2;
+    const int px = 64 * 4 / ks;
+    const unsigned blocks = (unsigned)((a->rows + px - 1) / px);
+    size_t shm = (size_t)a->G * 128;
+    if (ks > 1 && shm < C1_RED_BYTES) shm = C1_RED_BYTES;
+#define C1_LAUNCH(KS_)                                                                        \
+    do {                                                                                      \
+        if (acc)                                                                              \
+            hipLaunchKernelGGL((k_conv1<KS_, true>), dim3(blocks), dim3(256), shm, st, *a, acc); \
+        else                                                                                  \
+            hipLaunchKernelGGL((k_conv1<KS_, false>), dim3(blocks), dim3(256), shm, st, *a,     \
+                               nullptr);                                                      \
+    } while (0)
+    if (ks == 1) C1_LAUNCH(1);
+    else if (ks == 2) C1_LAUNCH(2);
+    else C1_LAUNCH(4);
+#undef C1_LAUNCH
     return launched("d8s_conv1");
 }
 

@@ -470,6 +470,9 @@ class Dense8SEncoder:
         self.in_kind = hip.IN_U8 if inp.get("kind", "f16") == "u8" else hip.IN_F16
         self.in_dtype = torch.uint8 if self.in_kind == hip.IN_U8 else torch.float16
         self.in_shape = (self.nb, int(meta["in_ch"]), int(meta["img"]), int(meta["img"]))
+        missing = [k for k in self._needed_tables() if k not in pack["par"]]
+        if missing:
+            raise ValueError(f"package tables missing: {missing[:4]}{'...' if len(missing) > 4 else ''}")
         d = f"cuda:{self.dev}"
         with torch.cuda.device(self.dev):
             self.stream = torch.cuda.Stream(self.dev)
@@ -482,9 +485,6 @@ class Dense8SEncoder:
         meta, n = self.meta, self.nb
         blocks = meta["blocks"]
         par = dict(pack["par"])
-        missing = [k for k in self._needed_tables() if k not in par]
-        if missing:
-            raise ValueError(f"package tables missing: {missing[:4]}{'...' if len(missing) > 4 else ''}")
         par.update(derived_params(meta, par))
         # two alternating arenas: block b reads arena b % 2, its transition writes the other one
         sizes, lay = [0, 0], []

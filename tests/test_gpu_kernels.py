@@ -69,6 +69,15 @@ def test_conv1_config2(dev, S, C):
     assert 0.0 < zero < 0.9 and sat < 0.5, (zero, sat)
 
 
+@pytest.mark.parametrize("S,C,N", [(64, 320, 12), (8, 96, 3), (2, 64, 1)])
+def test_conv1_ks_variants(dev, S, C, N):
+    """Pixel counts that select the 2-slice and 4-slice k-split and ragged last workgroups."""
+    c = cases.gemm_case(S, C, N=N, seed=17)
+    acc, byt = checks.run_conv1(c, dev)
+    acc_x, byt_x = checks.exact_conv1(c)
+    assert np.array_equal(acc, acc_x) and np.array_equal(byt, byt_x)
+
+
 @pytest.mark.parametrize("S", cases.CONV2_SIDES)
 def test_conv2_config3(dev, S):
     """Config 3: 3x3 pad-1 conv 128 -> 32, batch 24, written into its slot of a store (the other slots
