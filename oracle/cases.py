@@ -113,10 +113,12 @@ class Conv2Case:
     sc: np.ndarray          # [32] float32
 
 
-def conv2_case(S: int, N: int = 24, seed: int = 21) -> Conv2Case:
-    rng = np.random.default_rng([seed, S])
-    v = rng.integers(0, 80, (N, 128, S, S), dtype=np.uint8)
-    bott = np.ascontiguousarray(v.reshape(N, 4, 32, S * S).transpose(1, 0, 3, 2)).reshape(4, -1, 32)
+def conv2_case(S: int, N: int = 24, seed: int = 21, W: int | None = None) -> Conv2Case:
+    """An H x W = S x (W or S) map of N images."""
+    W = S if W is None else W
+    rng = np.random.default_rng([seed, S, W])
+    v = rng.integers(0, 80, (N, 128, S, W), dtype=np.uint8)
+    bott = np.ascontiguousarray(v.reshape(N, 4, 32, S * W).transpose(1, 0, 3, 2)).reshape(4, -1, 32)
     w2, _ = quant_weight_np(rng.normal(0, np.sqrt(2.0 / 1152), (32, 128, 3, 3)).astype(np.float32))
     w2k = np.ascontiguousarray(w2.reshape(32, 4, 32, 9).transpose(1, 3, 0, 2))
     # q = acc sc spans about [-127, 127] with a few saturated values

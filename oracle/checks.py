@@ -85,13 +85,13 @@ def exact_conv1(c: cases.GemmCase) -> tuple[np.ndarray, np.ndarray]:
 def run_conv2(c: cases.Conv2Case, device, slots: int = 3, slot: int = 1) -> tuple[np.ndarray, np.ndarray]:
     """Runs d8s_conv2 into slot `slot` of a `slots`-slot store filled with a sentinel; returns (the slot
     [M, 32] int8, the other slots' bytes) so a write outside the slot shows."""
-    S, N = c.S, c.N
-    M = N * S * S
+    N, _, H, W = c.v.shape
+    M = N * H * W
     bott, w2k, sc = (_dev(a, device) for a in (c.bott, c.w2k, c.sc))
     wsum = _dev(c.w2k.astype(np.int64).sum(axis=(0, 1, 3)).astype(np.int32), device)
     store = torch.full((slots * M * 32,), 0x5A, dtype=torch.int8, device=device)
     args = hip.Conv2Args(_ptr(bott), _ptr(w2k), _ptr(sc), _ptr(wsum), _ptr(store) + slot * M * 32,
-                         N, S, S, 0)
+                         N, H, W, 0)
     hip.call("d8s_conv2", ctypes.byref(args), _stream(device))
     torch.cuda.synchronize(device)
     s = store.cpu().numpy().reshape(slots, M, 32)
@@ -106,7 +106,7 @@ def exact_conv2(c: cases.Conv2Case) -> tuple[np.ndarray, np.ndarray]:
     accs = []
     for n0 in range(0, c.N, 4):
         v = torch.from_numpy(c.v[n0:n0 + 4].astype(np.float64))
-        a = F.conv2d(v, w, padding=1)                          # [n, 32, S, S]
+        a = F.conv2d(v, w, padding=1)                          # [n, 32, H, W]
         accs.append(a.permute(0, 2, 3, 1).reshape(-1, 32).numpy())
     acc = np.concatenate(accs).astype(np.int32)
     return acc, lib.conv2_epilogue(acc, c.sc)

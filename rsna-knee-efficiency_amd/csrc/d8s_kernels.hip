@@ -288,90 +288,177 @@ __global__ __launch_bounds__(256, 2) void k_conv1(D8sGemmArgs a, int32_t* __rest
 }
 
 // ------------------------------------------------------------------------------------------------
-// conv2: 3x3 pad 1, 128 -> 32.  Persistent workgroups with the 36 KB of weights resident in LDS; one
-// spatial tile of TH x TW = 256 output pixels at a time (TW = 32 for W >= 32), its halo of all 4
-// bottleneck planes in LDS.  4 waves x 64 pixels (2 MFMA tiles) x 32 outputs, 36 MFMAs per tile.
+// conv2: 3x3 pad 1, 128 -> 32.  Persistent workgroups with the 36 KB of weights resident in LDS, one
+// spatial tile of TH x TW output pixels at a time with the halo of its 4 bottleneck planes in LDS.
+// The next tile's halo is loaded into registers while the current one is computed.
+//   KSPL = 1: the 4 waves take PT MFMA pixel tiles (32 pixels) each over all 4 planes (36 MFMA
+//             K-steps of 32), TH x TW = 4 * 32 * PT;
+//   KSPL = 4: wave w takes plane w (9 K-steps) of the same PT pixel tiles, TH x TW = 32 * PT, and the
+//             four partial sums are added through LDS (narrow maps: 4x the tiles).
+// Tile shapes are compile-time so the halo's 16-byte chunks decompose without runtime divisions.
 // ------------------------------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void k_conv2(D8sConv2Args a, int TW, int TH, int tiles_x,
-                                               int tiles_y) {
+static constexpr int C2_RED = 20;                         // dwords per lane row of the partial sums
+
+template <int TW, int TH, int KSPL, int PT>
+struct C2Shape {
+    static constexpr int HWd = TW + 2, HP = (TH + 2) * HWd;
+    static constexpr int NCHUNK = 8 * HP;                 // 16-byte halo chunks (4 planes x 2 halves)
+    static constexpr int NCH = (NCHUNK + 255) / 256;      // per thread
+    static constexpr size_t HALO_BYTES = (size_t)NCHUNK * 16;
+    static constexpr size_t RED_BYTES = KSPL > 1 ? (size_t)3 * PT * 64 * C2_RED * 4 : 0;
+    static_assert(TW * TH == (KSPL == 1 ? 4 : 1) * 32 * PT, "tile = the waves' pixel tiles");
+};
+
+template <int TW, int TH, int KSPL, int PT>
+__global__ __launch_bounds__(256, 2) void k_conv2(D8sConv2Args a, int tiles_x, int tiles_y) {
+    using S = C2Shape<TW, TH, KSPL, PT>;
+    constexpr int HWd = S::HWd, HP = S::HP, NCH = S::NCH;
     __shared__ __attribute__((aligned(16))) u32x4 s_w[4 * 9 * 32 * 2];
-    extern __shared__ __attribute__((aligned(16))) u32x4 s_x[];       // [4][HP][2]
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    extern __shared__ __attribute__((aligned(16))) u32x4 s_x[];       // [4][HP][2], then partial sums
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int h = lane >> 5, j = lane & 31;
-    const int HWd = TW + 2, HP = (TH + 2) * HWd;
     const int H = a.H, W = a.W;
     const int64_t M = (int64_t)a.N * H * W;
 
-    for (int i = tid; i < 4 * 9 * 32 * 2; i += 256) s_w[swz(i >> 1, i & 1)] = ((const u32x4*)a.w)[i];
+    {
+        u32x4 wv[9];                                      // 2304 chunks = 9 per thread, all in flight
+#pragma unroll
+        for (int k = 0; k < 9; ++k) wv[k] = ((const u32x4*)a.w)[tid + 256 * k];
+#pragma unroll
+        for (int k = 0; k < 9; ++k) s_w[swz((tid + 256 * k) >> 1, tid & 1)] = wv[k];
+    }
 
+    const int32_t wmul = (KSPL == 1 || wave == 0) ? 128 : 0;
     i32x16 init;
     float sc[16];
 #pragma unroll
     for (int v = 0; v < 16; ++v) {
-        init[v] = 128 * a.wsum[res_row(v, h)];
+        init[v] = wmul * a.wsum[res_row(v, h)];
         sc[v] = a.sc[res_row(v, h)];
     }
-    int q0[2], ty[2], tx[2];
+    int q0[PT], ty[PT], tx[PT];
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
-        const int p = wave * 64 + 32 * t + j;
+    for (int t = 0; t < PT; ++t) {
+        const int p = (KSPL == 1 ? wave * PT * 32 : 0) + 32 * t + j;
         ty[t] = p / TW;
         tx[t] = p - ty[t] * TW;
         q0[t] = ty[t] * HWd + tx[t];
     }
-    const int per_img = tiles_x * tiles_y;
-    const int total = a.N * per_img;
-    for (int tile = blockIdx.x; tile < total; tile += gridDim.x) {
+
+    // halo chunks of this thread: chunk i = tid + 256 k -> plane c, halo pixel hp, half hh.  Every
+    // chunk is loaded (chunks outside the image from the tile's first pixel) with no use of the data
+    // until the LDS store, so all NCH loads are in flight together; the store applies the padding
+    // (u = 0, i.e. byte 0x80) and the u - 128 offset.
+    u32x4 hreg[NCH];
+    uint32_t hvalid = 0;
+    auto hload = [&](int tile) {
+        const int per_img = tiles_x * tiles_y;
         const int n = tile / per_img, r = tile - n * per_img;
         const int y0 = (r / tiles_x) * TH, x0 = (r % tiles_x) * TW;
-        __syncthreads();                                  // weights / previous tile's reads
-        for (int i = tid; i < 8 * HP; i += 256) {
-            const int c = i / (2 * HP), rr = i - c * 2 * HP;
+        const uint8_t* base = a.x + (((int64_t)n * H + y0) * W + x0) * 32;
+        hvalid = 0;
+#pragma unroll
+        for (int k = 0; k < NCH; ++k) {
+            const int i = tid + 256 * k;
+            const int c = i / (2 * HP), rr = i - c * (2 * HP);
             const int hp = rr >> 1, hh = rr & 1;
             const int hy = hp / HWd, hx = hp - hy * HWd;
             const int y = y0 - 1 + hy, x = x0 - 1 + hx;
-            u32x4 v = {SIGN4, SIGN4, SIGN4, SIGN4};
-            if ((unsigned)y < (unsigned)H && (unsigned)x < (unsigned)W)
-                v = *(const u32x4*)(a.x + (c * M + ((int64_t)n * H + y) * W + x) * 32 + 16 * hh) ^ SIGN4;
-            s_x[c * HP * 2 + swz(hp, hh)] = v;
+            const bool ok = i < S::NCHUNK && (unsigned)y < (unsigned)H && (unsigned)x < (unsigned)W;
+            const int64_t off = ok ? (c * M + (int64_t)(hy - 1) * W + (hx - 1)) * 32 + 16 * hh : 0;
+            hreg[k] = *(const u32x4*)(base + off);
+            hvalid |= (uint32_t)ok << k;
         }
-        __syncthreads();
-        i32x16 acc0 = init, acc1 = init;
+    };
+    auto hstore = [&]() {
 #pragma unroll
-        for (int c = 0; c < 4; ++c) {
-            const u32x4* sx = s_x + c * HP * 2;
+        for (int k = 0; k < NCH; ++k) {
+            const int i = tid + 256 * k;
+            const int c = i / (2 * HP), rr = i - c * (2 * HP);
+            const u32x4 pad = {SIGN4, SIGN4, SIGN4, SIGN4};
+            if (i < S::NCHUNK) s_x[c * HP * 2 + swz(rr >> 1, rr & 1)] = ((hvalid >> k) & 1) ? hreg[k] ^ SIGN4 : pad;
+        }
+    };
+
+    const int total = a.N * tiles_x * tiles_y;
+    int tile = blockIdx.x;
+    if (tile >= total) return;
+    hload(tile);
+    __syncthreads();                                      // weights
+    hstore();
+    __syncthreads();
+    for (; tile < total; tile += gridDim.x) {
+        const int next = tile + gridDim.x;
+        if (next < total) hload(next);                    // in flight during this tile's MFMAs
+        i32x16 acc[PT];
 #pragma unroll
-            for (int tap = 0; tap < 9; ++tap) {
-                const int off = (tap / 3) * HWd + (tap % 3);
-                const u32x4 aw = s_w[swz((c * 9 + tap) * 32 + j, h)];
-                const u32x4 b0 = sx[swz(q0[0] + off, h)];
-                const u32x4 b1 = sx[swz(q0[1] + off, h)];
-                acc0 = mfma_i8(aw, b0, acc0);
-                acc1 = mfma_i8(aw, b1, acc1);
+        for (int t = 0; t < PT; ++t) acc[t] = init;
+        // K steps (plane, tap); the operands of step s + 1 are read from LDS before step s's MFMAs
+        constexpr int NS = KSPL == 1 ? 36 : 9;
+        u32x4 aw[2], bx[2][PT];
+        auto fetch = [&](int s, int slot) {
+            const int c = KSPL == 1 ? s / 9 : wave, tap = s % 9;
+            const int off = (tap / 3) * HWd + (tap % 3);
+            aw[slot] = s_w[swz((c * 9 + tap) * 32 + j, h)];
+#pragma unroll
+            for (int t = 0; t < PT; ++t) bx[slot][t] = s_x[c * HP * 2 + swz(q0[t] + off, h)];
+        };
+        fetch(0, 0);
+#pragma unroll
+        for (int s = 0; s < NS; ++s) {
+            if (s + 1 < NS) fetch(s + 1, (s + 1) & 1);
+#pragma unroll
+            for (int t = 0; t < PT; ++t) acc[t] = mfma_i8(aw[s & 1], bx[s & 1][t], acc[t]);
+        }
+        if (KSPL > 1) {
+            // waves 1..3 hand their partial sums to wave 0 (rows of 16 int32 per lane, padded)
+            int32_t* red = (int32_t*)((uint8_t*)s_x + S::HALO_BYTES);
+            if (wave > 0) {
+#pragma unroll
+                for (int t = 0; t < PT; ++t)
+                    *(i32x16*)(red + (((wave - 1) * PT + t) * 64 + lane) * C2_RED) = acc[t];
+            }
+            __syncthreads();
+            if (wave == 0) {
+#pragma unroll
+                for (int w = 0; w < 3; ++w)
+#pragma unroll
+                    for (int t = 0; t < PT; ++t)
+                        acc[t] += *(const i32x16*)(red + ((w * PT + t) * 64 + lane) * C2_RED);
             }
         }
         // epilogue: q = RNE(clamp(float(acc) * sc, -127, 127)) (conv2t_body,
         // src/knee/dense8s_kernels.cu:2797-2809)
+        if (KSPL == 1 || wave == 0) {
+            const int per_img = tiles_x * tiles_y;
+            const int n = tile / per_img, r = tile - n * per_img;
+            const int y0 = (r / tiles_x) * TH, x0 = (r % tiles_x) * TW;
 #pragma unroll
-        for (int t = 0; t < 2; ++t) {
-            const i32x16 ac = t ? acc1 : acc0;
-            uint32_t e[4];
+            for (int t = 0; t < PT; ++t) {
+                uint32_t e[4];
 #pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                uint32_t d = 0;
+                for (int k = 0; k < 4; ++k) {
+                    uint32_t d = 0;
 #pragma unroll
-                for (int rr = 0; rr < 4; ++rr) {
-                    const int v = 4 * k + rr;
-                    const float q = __builtin_rintf(
-                        __builtin_fminf(__builtin_fmaxf((float)ac[v] * sc[v], -127.0f), 127.0f));
-                    d |= ((uint32_t)(int)q & 0xffu) << (8 * rr);
+                    for (int rr = 0; rr < 4; ++rr) {
+                        const int v = 4 * k + rr;
+                        const float q = __builtin_rintf(
+                            __builtin_fminf(__builtin_fmaxf((float)acc[t][v] * sc[v], -127.0f), 127.0f));
+                        d |= ((uint32_t)(int)q & 0xffu) << (8 * rr);
+                    }
+                    e[k] = d;
                 }
-                e[k] = d;
+                const u32x4 row = xchg_rows(e[0], e[1], e[2], e[3], h);
+                const int y = y0 + ty[t], x = x0 + tx[t];
+                if (y < H && x < W)
+                    *(u32x4*)(a.out + (((int64_t)n * H + y) * W + x) * 32 + 16 * h) = row;
             }
-            const u32x4 row = xchg_rows(e[0], e[1], e[2], e[3], h);
-            const int y = y0 + ty[t], x = x0 + tx[t];
-            if (ty[t] < TH && y < H && x < W)
-                *(u32x4*)(a.out + (((int64_t)n * H + y) * W + x) * 32 + 16 * h) = row;
+        }
+        __syncthreads();                                  // this tile's halo and partial sums read
+        if (next < total) {
+            hstore();
+            __syncthreads();
         }
     }
 }
@@ -814,21 +901,37 @@ extern "C" int d8s_conv1_acc32(const D8sGemmArgs* a, int32_t* acc, void* stream)
     return conv1_launch(a, acc, (hipStream_t)stream);
 }
 
+template <int TW, int TH, int KSPL, int PT>
+static int conv2_launch(const D8sConv2Args* a, hipStream_t st, int64_t min_tiles) {
+    using S = C2Shape<TW, TH, KSPL, PT>;
+    const int tiles_x = (a->W + TW - 1) / TW, tiles_y = (a->H + TH - 1) / TH;
+    const int64_t total = (int64_t)a->N * tiles_x * tiles_y;
+    if (total < min_tiles) return -1;
+    REQUIRE(total < (1ll << 31), "d8s_conv2: too many tiles");
+    const unsigned grid = (unsigned)(total < 2 * cu_count() ? total : 2 * cu_count());
+    hipLaunchKernelGGL((k_conv2<TW, TH, KSPL, PT>), dim3(grid), dim3(256), S::HALO_BYTES + S::RED_BYTES,
+                       st, *a, tiles_x, tiles_y);
+    return launched("d8s_conv2");
+}
+
 extern "C" int d8s_conv2(const D8sConv2Args* a, void* stream) {
     REQUIRE(a != nullptr, "d8s_conv2: null arguments");
     REQUIRE(a->x && a->w && a->sc && a->wsum && a->out, "d8s_conv2: null pointer");
     REQUIRE(a->N >= 1 && a->H >= 1 && a->W >= 1, "d8s_conv2: N, H, W must be >= 1");
-    int TW = 32;
-    while (TW > 1 && TW / 2 >= a->W) TW /= 2;
-    const int TH = 256 / TW;
-    const int tiles_x = (a->W + TW - 1) / TW, tiles_y = (a->H + TH - 1) / TH;
-    const int64_t total = (int64_t)a->N * tiles_x * tiles_y;
-    REQUIRE(total < (1ll << 31), "d8s_conv2: too many tiles");
-    const size_t shm = (size_t)4 * (TH + 2) * (TW + 2) * 32;
-    const unsigned grid = (unsigned)(total < 2 * cu_count() ? total : 2 * cu_count());
-    hipLaunchKernelGGL(k_conv2, dim3(grid), dim3(256), shm, (hipStream_t)stream, *a, TW, TH,
-                       tiles_x, tiles_y);
-    return launched("d8s_conv2");
+    hipStream_t st = (hipStream_t)stream;
+    const int64_t enough = 3 * (int64_t)cu_count();        // tiles for a persistent grid to pipeline
+    if (a->W >= 32) {
+        int rc = conv2_launch<32, 8, 1, 2>(a, st, enough);
+        if (rc >= 0) return rc;
+        rc = conv2_launch<32, 4, 1, 1>(a, st, enough);
+        if (rc >= 0) return rc;
+        return conv2_launch<32, 2, 4, 2>(a, st, 0);
+    }
+    if (a->W >= 16) return conv2_launch<16, 4, 4, 2>(a, st, 0);
+    if (a->W >= 8) return conv2_launch<8, 8, 4, 2>(a, st, 0);
+    if (a->W >= 4) return conv2_launch<4, 16, 4, 2>(a, st, 0);
+    if (a->W >= 2) return conv2_launch<2, 32, 4, 2>(a, st, 0);
+    return conv2_launch<1, 64, 4, 2>(a, st, 0);
 }
 
 extern "C" int d8s_transition(const D8sGemmArgs* a, void* stream) {

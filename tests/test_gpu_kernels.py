@@ -96,6 +96,17 @@ def test_conv2_config3(dev, S):
     assert 0.001 < float((np.abs(q_x) == 127).mean()) < 0.2
 
 
+@pytest.mark.parametrize("N,H,W", [(96, 16, 16), (4, 40, 40), (3, 8, 8), (2, 5, 7), (2, 4, 4),
+                                   (1, 2, 2), (2, 3, 1), (8, 32, 32), (2, 33, 64)])
+def test_conv2_tile_variants(dev, N, H, W):
+    """Every tile shape of d8s_conv2 (wide, plane-split narrow, ragged edges) against the exact conv."""
+    c = cases.conv2_case(H, N=N, seed=23, W=W)
+    got, others = checks.run_conv2(c, dev)
+    _, q_x = checks.exact_conv2(c)
+    assert np.array_equal(got, q_x), checks.bytes_cmp(got, q_x)
+    assert np.all(others == 0x5A)
+
+
 @pytest.mark.parametrize("S,C,c0", [(128, 256, 64), (64, 512, 128), (32, 1280, 256), (16, 128, 64)])
 def test_transition(dev, S, C, c0):
     t = cases.trans_case(S, C, N=4, c0=c0)
