@@ -104,6 +104,69 @@ def family_times(enc: dense8s.Dense8SEncoder, x: torch.Tensor, reps: int, mode) 
     return fam
 
 
+def copy_probe(dev: torch.device, mib: int = 1024, reps: int = 5) -> dict:
+    """d8s_micro_copy over `mib` MiB (read + write): the practical HBM bandwidth, and the plain copy of
+    known size that calibrates the FETCH_SIZE / WRITE_SIZE counters."""
+    from rsna_knee_efficiency_amd import hip
+    n = mib << 20
+    src = torch.empty(n, dtype=torch.uint8, device=dev).fill_(1)
+    dst = torch.empty(n, dtype=torch.uint8, device=dev)
+    st = torch.cuda.current_stream(dev).cuda_stream
+    hip.call("d8s_micro_copy", src.data_ptr(), dst.data_ptr(), n, st)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        hip.call("d8s_micro_copy", src.data_ptr(), dst.data_ptr(), n, st)
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / reps
+    return {"bytes_per_launch": 2 * n, "ms": round(ms, 4), "gbs": round(2 * n / (ms * 1e-3) / 1e9, 1)}
+
+
+FAMILY = {"k_conv1": "conv1", "k_conv2": "conv2", "k_trans": "trans", "k_stem": "stem",
+          "k_final": "final", "k_copy": "copy"}
+
+
+def _family(name: str) -> str | None:
+    for k, v in FAMILY.items():
+        if k + "<" in name or k + "(" in name:
+            return v
+    return None
+
+
+def rocprof_summary(d: str) -> str:
+    """Markdown summary of a rocprofv3 CSV output directory (kernel stats and/or counter collection),
+    this library's kernels only."""
+    import csv
+    import glob
+    lines = []
+    for path in sorted(glob.glob(os.path.join(d, "**", "*kernel_stats.csv"), recursive=True)):
+        rows = [r for r in csv.DictReader(open(path)) if _family(r["Name"])]
+        lines += [f"### kernel stats ({os.path.basename(path)})", "",
+                  "| kernel | calls | avg us | total ms |", "|---|---|---|---|"]
+        for r in sorted(rows, key=lambda r: -float(r["TotalDurationNs"])):
+            lines.append(f"| `{r['Name']}` | {r['Calls']} | {float(r['AverageNs']) / 1e3:.2f} | "
+                         f"{float(r['TotalDurationNs']) / 1e6:.3f} |")
+        lines.append("")
+    for path in sorted(glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True)):
+        acc: dict = {}
+        for r in csv.DictReader(open(path)):
+            fam = _family(r.get("Kernel_Name", ""))
+            if not fam:
+                continue
+            key = (r["Kernel_Name"], r["Counter_Name"])
+            v = acc.setdefault(key, [0, 0.0])
+            v[0] += 1
+            v[1] += float(r["Counter_Value"])
+        lines += [f"### counters ({os.path.basename(path)})", "",
+                  "| kernel | counter | dispatches | mean per dispatch |", "|---|---|---|---|"]
+        for (name, ctr), (cnt, tot) in sorted(acc.items()):
+            lines.append(f"| `{name}` | {ctr} | {cnt} | {tot / cnt:.1f} |")
+        lines.append("")
+    return "\n".join(lines)
+
+
 def cpu_baseline(reps: int = 5, warmup: int = 2) -> dict:
     from oracle import fp32
     cores = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
@@ -140,7 +203,17 @@ def main() -> None:
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--prof-reps", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--copy-probe", action="store_true",
+                    help="also time d8s_micro_copy over 1 GiB (HBM floor, counter calibration)")
+    ap.add_argument("--rocprof-summary", metavar="DIR",
+                    help="print a markdown summary of rocprofv3 CSV output in DIR and exit")
+    ap.add_argument("--pmc-passes", type=int, default=0, metavar="P",
+                    help="only run P eager configuration-5 passes of one encoder (the launches of "
+                         "a counter-collection run), print the per-family times and exit")
     args = ap.parse_args()
+    if args.rocprof_summary:
+        print(rocprof_summary(args.rocprof_summary))
+        return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print(f"bench.py: this build runs on one GPU (the encoder is per-GPU, replicas need no "
               f"communication); --gpus {args.gpus} is not supported", file=sys.stderr)
@@ -153,6 +226,19 @@ def main() -> None:
     dev = torch.device("cuda:0")
     t0 = time.perf_counter()
     nb = 4 * SLICES                                     # 2 crops x 24 slices x flip
+    if args.pmc_passes:
+        enc = build_encoder(0, nb, dev)[0]
+        x = torch.from_numpy(np.concatenate([synthetic.study_u8(SLICES, IMG, seed=1234 + c)
+                                             for c in range(2)])).to(dev)
+        fam = family_times(enc, x, args.pmc_passes - 1, "tta") if args.pmc_passes > 1 else {}
+        if args.pmc_passes == 1:
+            enc(x, flip="tta")
+            torch.cuda.synchronize()
+        print(json.dumps({"passes": args.pmc_passes, "launches_per_pass": {
+            k: len(v) for k, v in kernel_bytes(enc.meta, nb).items()},
+            "bytes_per_pass": {k: sum(v) for k, v in kernel_bytes(enc.meta, nb).items()},
+            "family_ms": fam}))
+        return
     encs = [build_encoder(seed, nb, dev)[0] for seed in (0, 1)]
     log(f"encoders built in {time.perf_counter() - t0:.1f} s")
     # 4 distinct studies resident in HBM: each 2 crops x 24 slices (uint8)
@@ -230,6 +316,9 @@ def main() -> None:
                      "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None},
     }
+    if args.copy_probe:
+        out["copy_probe"] = copy_probe(dev)
+        log(f"copy probe: {out['copy_probe']}")
     if not args.no_cpu:
         log("cpu baseline ...")
         out["cpu_baseline"] = cpu_baseline()

@@ -115,7 +115,7 @@ DEV int swz(int r, int half) { return r * 2 + (half ^ ((r >> 2) & 1)); }
 // s, s + KS, ... and the partial sums are added through LDS at the end (KS > 1 fills the chip when
 // there are few pixels: the 16 x 16 and 32 x 32 blocks).  The main loop has no barrier: the store
 // bytes go global -> registers (4 groups ahead) -> prologue -> MFMA operand, the weights global ->
-// registers (2 groups ahead, L1/L2 hits: every wave reads the same layer); only the fp16 prologue
+// registers (1 group ahead, L1/L2 hits: every wave reads the same layer); only the fp16 prologue
 // table of the layer sits in LDS.
 // ------------------------------------------------------------------------------------------------
 static constexpr int C1_RED = 20;                        // dwords per lane row of the k-slice sums
@@ -167,38 +167,46 @@ __global__ __launch_bounds__(256, 2) void k_conv1(D8sGemmArgs a, int32_t* __rest
     }
 
     // this slice's groups: g_k = slice + k KS, k < nk
+    // Vector loads retire in issue order (s_waitcnt vmcnt), so each step issues the weights it will
+    // need next BEFORE the activations four steps ahead: waiting for this step's weights then leaves
+    // the later activation loads in flight.
     const int nk = (G - slice + KS - 1) / KS;
     u32x4 ra[4][2];
-    u32x4 rb[4];
+    u32x4 rb[2][4];
     auto load_a = [&](int slot, int k) {
         const int g = slice + k * KS;
         ra[slot][0] = *src(0, g);
         ra[slot][1] = *src(1, g);
     };
-    auto load_b = [&](int k) {
+    auto load_b = [&](int bslot, int k) {
         const u32x4* p = wl + (int64_t)(slice + k * KS) * 256;
 #pragma unroll
-        for (int c = 0; c < 4; ++c) rb[c] = p[64 * c];
+        for (int c = 0; c < 4; ++c) rb[bslot][c] = p[64 * c];
     };
+    // The prefetches are unconditional (past the last group they reload it): conditional loads would
+    // leave the compiler unable to count the loads in flight, and it would wait for all of them.
+    const int klast = nk - 1;
+    if (nk > 0) {
+        load_b(0, 0);
 #pragma unroll
-    for (int k = 0; k < 4; ++k)
-        if (k < nk) load_a(k, k);
-    if (nk > 0) load_b(0);
+        for (int k = 0; k < 4; ++k) load_a(k, k < klast ? k : klast);
+    }
     __syncthreads();                                      // s_abh
 
     auto step = [&](const int slot, const int k) {
         const int g = slice + k * KS;
+        load_b((slot + 1) & 1, k + 1 < klast ? k + 1 : klast);
+        asm volatile("" ::: "memory");                   // keep the weight loads ahead in issue order
         const u32x4* pp = (const u32x4*)(s_abh + g * 32 + h * 16);
         const u32x4 p0 = pp[0], p1 = pp[1], p2 = pp[2], p3 = pp[3];
         const u32x4 b0 = pro16(ra[slot][0], p0, p1, p2, p3);
         const u32x4 b1 = pro16(ra[slot][1], p0, p1, p2, p3);
-        if (k + 4 < nk) load_a(slot, k + 4);
+        load_a(slot, k + 4 < klast ? k + 4 : klast);
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
-            acc[0][c] = mfma_i8(rb[c], b0, acc[0][c]);
-            acc[1][c] = mfma_i8(rb[c], b1, acc[1][c]);
+            acc[0][c] = mfma_i8(rb[slot & 1][c], b0, acc[0][c]);
+            acc[1][c] = mfma_i8(rb[slot & 1][c], b1, acc[1][c]);
         }
-        if (k + 1 < nk) load_b(k + 1);
     };
     for (int k = 0; k < nk; k += 4) {
         step(0, k);
@@ -464,18 +472,23 @@ __global__ __launch_bounds__(256, 2) void k_conv2(D8sConv2Args a, int tiles_x, i
 }
 
 // ------------------------------------------------------------------------------------------------
-// Transition: the mean of every 2x2 square comes before the 1x1 conv (they commute).  With
-// s = sum of the four u (0..1020), s - 512 = 4 hq + lq, hq in [-128, 127], lq in [0, 3], and
-// S = sum_k w s = 4 (sum_k w hq + 128 sum_k w) + sum_k w lq: two int8 MFMAs per K group at quarter
-// resolution, exact.  Workgroup = 64 output pixels x 128 outputs (4 waves x 32 outputs); the pooled
-// operands (hq and lq bytes) of a group are built by the whole workgroup into LDS, double-buffered.
+// Transition: conv and 2x2 mean commute, so S = sum_k w[o][k] s[k] with s = the sum of the prologue
+// outputs u of the four pixels of the square: four int8 MFMAs (one per pixel, operand u - 128) into one
+// accumulator that starts at 512 sum_k w (exact int32).  A workgroup takes PT pixel tiles (32 output
+// pixels each) and ALL output channels: the prologue runs once per input byte.  The four waves split the
+// output tiles (wave w: tiles w, w + 4, ..., NT of them); the operands of a K group are built by the
+// whole workgroup into LDS (double-buffered, one barrier per group).
 // ------------------------------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void k_trans(D8sGemmArgs a) {
+template <int NT, int PT>
+__global__ __launch_bounds__(256, 2) void k_trans(D8sGemmArgs a) {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    constexpr int PX = 32 * PT;                            // output pixels per workgroup
+    constexpr int BUF = 4 * PX * 32;                       // bytes of one group's operands
     const int G = a.G, G0 = a.G0;
-    u32x4* s_b = (u32x4*)smem;                            // [2 buf][2 (hq, lq)][64 px][2]
-    uint32_t* s_abh = (uint32_t*)(smem + 8192);           // [G * 32]
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    u32x4* s_b = (u32x4*)smem;                             // [2 buf][4 sub][PX][2]
+    uint32_t* s_abh = (uint32_t*)(smem + 2 * BUF);         // [G * 32]
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int h = lane >> 5, j = lane & 31;
     const uint32_t* abh32 = (const uint32_t*)a.abh;
     for (int i = tid; i < G * 32; i += 256) s_abh[i] = abh32[i];
@@ -483,126 +496,116 @@ __global__ __launch_bounds__(256) void k_trans(D8sGemmArgs a) {
     const int64_t HW = a.HW, W = a.W;
     const int W2 = a.W >> 1, HW4 = a.HW >> 2;
     const int64_t NO = (int64_t)a.N * HW4;
-    const int64_t op0 = (int64_t)blockIdx.y * 64;
-    const int co = blockIdx.x * 4 + wave;                 // output tile of 32 channels
-    const bool co_ok = co * 32 < a.cout;
+    const int64_t op0 = (int64_t)blockIdx.x * PX;
+    const int OT = a.cout >> 5;
 
-    // staging role: output pixel pp, 8 channels 8 qq .. 8 qq + 7
-    const int pp = tid >> 2, qq = tid & 3;
-    const int8_t* base_in0;
-    const int8_t* base_seg;
-    int64_t off[4];
-    {
-        int64_t op = op0 + pp;
+    // staging items of this thread: item = tid + 256 k -> (sub-pixel sp, output pixel px, half hh)
+    const int8_t* pin[PT];
+    const int8_t* pseg[PT];
+    int sdst[PT];
+#pragma unroll
+    for (int k = 0; k < PT; ++k) {
+        const int item = tid + 256 * k;
+        const int hh = item & 1, px = (item >> 1) % PX, sp = (item >> 1) / PX;
+        int64_t op = op0 + px;
         if (op >= NO) op = NO - 1;
         const int64_t n = op / HW4, p4 = op - n * HW4;
         const int64_t oy = p4 / W2, ox = p4 - oy * W2;
-#pragma unroll
-        for (int k = 0; k < 4; ++k) off[k] = ((2 * oy + (k >> 1)) * W + 2 * ox + (k & 1)) * 32 + 8 * qq;
-        base_in0 = a.in0 + n * G0 * HW * 32;
-        base_seg = a.seg + n * HW * 32;
+        const int64_t p = (2 * oy + (sp >> 1)) * W + 2 * ox + (sp & 1);
+        pin[k] = a.in0 + (n * G0 * HW + p) * 32 + 16 * hh;
+        pseg[k] = a.seg + (n * HW + p) * 32 + 16 * hh;
+        sdst[k] = (sp * PX) * 2 + swz(px, hh);              // in 16-byte chunks within a buffer
     }
-    const int64_t seg_gs = (int64_t)a.N * HW * 32;
-    auto load_raw = [&](int g, u32x2* rx) {
-        const int8_t* s = g < G0 ? base_in0 + g * HW * 32 : base_seg + (g - G0) * seg_gs;
-#pragma unroll
-        for (int k = 0; k < 4; ++k) rx[k] = *(const u32x2*)(s + off[k]);
+    const int64_t in_gs = HW * 32, seg_gs = (int64_t)a.N * HW * 32;
+    auto src = [&](int k, int g) -> const u32x4* {
+        return (const u32x4*)(g < G0 ? pin[k] + g * in_gs : pseg[k] + (g - G0) * seg_gs);
     };
-    auto stage = [&](int g, const u32x2* rx, int buf) {
-        const u32x4* pr = (const u32x4*)(s_abh + g * 32 + qq * 8);
-        const u32x4 pa = pr[0], pb = pr[1];
-        uint32_t s[4] = {0u, 0u, 0u, 0u};
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            uint32_t rl, rh;
-            pro4_halves(rx[k].x, pa.x, pa.y, pa.z, pa.w, rl, rh);
-            s[0] += rl & 0x00ff00ffu;
-            s[1] += rh & 0x00ff00ffu;
-            pro4_halves(rx[k].y, pb.x, pb.y, pb.z, pb.w, rl, rh);
-            s[2] += rl & 0x00ff00ffu;
-            s[3] += rh & 0x00ff00ffu;
-        }
-        uint32_t hq[4], lq[4];
-        const i16x2 k512 = {512, 512};
-        const i16x2 k3 = {3, 3};
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const i16x2 sv = __builtin_bit_cast(i16x2, s[i]) - k512;
-            hq[i] = __builtin_bit_cast(uint32_t, (i16x2)(sv >> (i16x2){2, 2}));
-            lq[i] = __builtin_bit_cast(uint32_t, (i16x2)(sv & k3));
-        }
-        const u32x2 hb = {pack_low_bytes(hq[0], hq[1]), pack_low_bytes(hq[2], hq[3])};
-        const u32x2 lb = {pack_low_bytes(lq[0], lq[1]), pack_low_bytes(lq[2], lq[3])};
-        uint8_t* row_h = (uint8_t*)(s_b + (buf * 2 + 0) * 128);
-        uint8_t* row_l = (uint8_t*)(s_b + (buf * 2 + 1) * 128);
-        const int o16 = swz(pp, qq >> 1) * 16 + 8 * (qq & 1);
-        *(u32x2*)(row_h + o16) = hb;
-        *(u32x2*)(row_l + o16) = lb;
-    };
+    const int hh_item = tid & 1;                           // every item of a thread has the same half
 
-    i32x16 acch[2], accl[2];
-    {
+    // weights of this wave's output tiles: row 32 (wave + 4 i) + j, half h
+    i32x16 acc[NT][PT];
+#pragma unroll
+    for (int i = 0; i < NT; ++i) {
+        const int ot = wave + 4 * i;
         i32x16 init;
 #pragma unroll
-        for (int v = 0; v < 16; ++v) {
-            const int o = co * 32 + res_row(v, h);
-            init[v] = co_ok ? 128 * a.wsum[o] : 0;
-        }
-        acch[0] = acch[1] = init;
-        accl[0] = accl[1] = i32x16{};
+        for (int v = 0; v < 16; ++v) init[v] = ot < OT ? 512 * a.wsum[32 * ot + res_row(v, h)] : 0;
+#pragma unroll
+        for (int t = 0; t < PT; ++t) acc[i][t] = init;
     }
-    const u32x4* wrow = (const u32x4*)(a.w + ((int64_t)(co_ok ? co : 0) * 32 + j) * 32 + 16 * h);
-    const int64_t wg = (int64_t)a.cout * 2;               // 16-byte chunks per weight group
+    auto wload = [&](int g, u32x4* aw) {
+#pragma unroll
+        for (int i = 0; i < NT; ++i) {
+            const int ot = wave + 4 * i;
+            aw[i] = ot < OT ? *(const u32x4*)(a.w + (((int64_t)g * a.cout + 32 * ot + j) * 32 + 16 * h))
+                            : u32x4{0u, 0u, 0u, 0u};
+        }
+    };
 
-    u32x2 rx[4];
-    load_raw(0, rx);
-    __syncthreads();                                      // s_abh
+    u32x4 raw[PT], aw[NT];
+#pragma unroll
+    for (int k = 0; k < PT; ++k) raw[k] = *src(k, 0);
+    wload(0, aw);
+    __syncthreads();                                       // s_abh
     for (int g = 0; g < G; ++g) {
         const int buf = g & 1;
-        stage(g, rx, buf);
-        if (g + 1 < G) load_raw(g + 1, rx);
-        u32x4 aw = {0u, 0u, 0u, 0u};
-        if (co_ok) aw = wrow[g * wg];
-        __syncthreads();
-        if (co_ok) {
-            const u32x4* bh = s_b + (buf * 2 + 0) * 128;
-            const u32x4* bl = s_b + (buf * 2 + 1) * 128;
+        {
+            const u32x4* pp = (const u32x4*)(s_abh + g * 32 + hh_item * 16);
+            const u32x4 p0 = pp[0], p1 = pp[1], p2 = pp[2], p3 = pp[3];
 #pragma unroll
-            for (int t = 0; t < 2; ++t) {
-                const int px = 32 * t + j;
-                acch[t] = mfma_i8(aw, bh[swz(px, h)], acch[t]);
-                accl[t] = mfma_i8(aw, bl[swz(px, h)], accl[t]);
-            }
+            for (int k = 0; k < PT; ++k) s_b[buf * (BUF / 16) + sdst[k]] = pro16(raw[k], p0, p1, p2, p3);
         }
+        // unconditional prefetch (the last group reloads itself): the loads stay countable for the
+        // compiler's waits, so they remain in flight across the MFMAs
+        const int gn = g + 1 < G ? g + 1 : g;
+#pragma unroll
+        for (int k = 0; k < PT; ++k) raw[k] = *src(k, gn);
+        __syncthreads();
+        const u32x4* sb = s_b + buf * (BUF / 16);
+#pragma unroll
+        for (int sp = 0; sp < 4; ++sp) {
+            u32x4 b[PT];
+#pragma unroll
+            for (int t = 0; t < PT; ++t) b[t] = sb[(sp * PX) * 2 + swz(32 * t + j, h)];
+#pragma unroll
+            for (int i = 0; i < NT; ++i)
+#pragma unroll
+                for (int t = 0; t < PT; ++t) acc[i][t] = mfma_i8(aw[i], b[t], acc[i][t]);
+        }
+        wload(gn, aw);
     }
-    if (!co_ok) return;
     // epilogue: q = RNE(clamp(k' * (float(S) / 4), -127, 127)) (trans_w_body with the exact mean,
     // src/knee/dense8s_kernels.cu:3226-3245)
-    float kq[16];
 #pragma unroll
-    for (int v = 0; v < 16; ++v) kq[v] = a.gd[2 * (co * 32 + res_row(v, h))];
+    for (int i = 0; i < NT; ++i) {
+        const int ot = wave + 4 * i;
+        if (ot >= OT) break;
+        float kq[16];
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
-        uint32_t e[4];
+        for (int v = 0; v < 16; ++v) kq[v] = a.gd[2 * (32 * ot + res_row(v, h))];
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            uint32_t d = 0;
+        for (int t = 0; t < PT; ++t) {
+            uint32_t e[4];
 #pragma unroll
-            for (int rr = 0; rr < 4; ++rr) {
-                const int v = 4 * k + rr;
-                const int32_t S = 4 * acch[t][v] + accl[t][v];
-                const float x = kq[v] * ((float)S * 0.25f);
-                const float q = __builtin_rintf(__builtin_fminf(__builtin_fmaxf(x, -127.0f), 127.0f));
-                d |= ((uint32_t)(int)q & 0xffu) << (8 * rr);
+            for (int k = 0; k < 4; ++k) {
+                uint32_t d = 0;
+#pragma unroll
+                for (int rr = 0; rr < 4; ++rr) {
+                    const int v = 4 * k + rr;
+                    const float x = kq[v] * ((float)acc[i][t][v] * 0.25f);
+                    const float q = __builtin_rintf(__builtin_fminf(__builtin_fmaxf(x, -127.0f), 127.0f));
+                    d |= ((uint32_t)(int)q & 0xffu) << (8 * rr);
+                }
+                e[k] = d;
             }
-            e[k] = d;
+            const u32x4 row = xchg_rows(e[0], e[1], e[2], e[3], h);
+            const int64_t op = op0 + 32 * t + j;
+            if (op < NO) {
+                const int64_t n = op / HW4, p4 = op - n * HW4;
+                *(u32x4*)((int8_t*)a.out + ((n * a.G0n + ot) * HW4 + p4) * 32 + 16 * h) = row;
+            }
         }
-        const u32x4 row = xchg_rows(e[0], e[1], e[2], e[3], h);
-        const int64_t op = op0 + 32 * t + j;
-        if (op < NO) {
-            const int64_t n = op / HW4, p4 = op - n * HW4;
-            *(u32x4*)((int8_t*)a.out + ((n * a.G0n + co) * HW4 + p4) * 32 + 16 * h) = row;
-        }
+        asm volatile("" ::: "memory");
     }
 }
 
@@ -671,29 +674,66 @@ __global__ __launch_bounds__(256) void k_stem(D8sStemArgs a, int tiles_x, int ti
     const int ns = (a.flip == 2 && n >= half) ? n - half : n;          // source image
     const bool mirror = a.flip == 1 || (a.flip == 2 && n >= half);
 
-    // weights [64][168] -> [64][184], zero tail (K steps past 168)
-    const uint16_t* wsrc = a.w16;
-    for (int i = tid; i < 64 * ST_WROW; i += 256) {
-        const int o = i / ST_WROW, k = i - o * ST_WROW;
-        s_wt[i] = k < 168 ? __builtin_bit_cast(_Float16, wsrc[o * 168 + k]) : (_Float16)0.0f;
+    // Loads are issued all together and their data used only afterwards (a use right after a load
+    // would make every load wait for the previous one).
+    // weights [64][168] (21 chunks of 16 bytes per row) -> LDS rows of 184 fp16, zero tail
+    {
+        constexpr int NWC = 64 * 21, KW = (NWC + 255) / 256;
+        u32x4 wv[KW];
+#pragma unroll
+        for (int k = 0; k < KW; ++k) {
+            const int i = tid + 256 * k;
+            wv[k] = ((const u32x4*)a.w16)[i < NWC ? i : 0];
+        }
+        if (tid < 128) {                                  // rows' chunks 21 and 22: K 168..183
+            const u32x4 z = {0u, 0u, 0u, 0u};
+            *(u32x4*)(s_wt + (tid >> 1) * ST_WROW + 168 + 8 * (tid & 1)) = z;
+        }
+#pragma unroll
+        for (int k = 0; k < KW; ++k) {
+            const int i = tid + 256 * k;
+            if (i < NWC) *(u32x4*)(s_wt + (i / 21) * ST_WROW + 8 * (i % 21)) = wv[k];
+        }
     }
     if (a.kind == D8S_IN_U8)
         for (int i = tid; i < 3 * 256; i += 256) s_lut[i] = __builtin_bit_cast(_Float16, a.lut[i]);
-    __syncthreads();
-    for (int i = tid; i < 3 * ST_IY * ST_IX; i += 256) {
-        const int c = i / (ST_IY * ST_IX), rr = i - c * ST_IY * ST_IX;
-        const int ly = rr / ST_IX, lx = rr - ly * ST_IX;
-        const int y = iy0 + ly, x = ix0 + lx;
-        _Float16 v = (_Float16)0.0f;
-        if ((unsigned)y < (unsigned)H && (unsigned)x < (unsigned)W) {
+    {
+        constexpr int NIN = 3 * ST_IY * ST_IX, KIN = (NIN + 255) / 256;
+        uint32_t raw[KIN];
+        uint64_t okm = 0;
+        int64_t idx[KIN];
+#pragma unroll
+        for (int k = 0; k < KIN; ++k) {
+            const int i = tid + 256 * k;
+            const int c = i / (ST_IY * ST_IX), rr = i - c * (ST_IY * ST_IX);
+            const int ly = rr / ST_IX, lx = rr - ly * ST_IX;
+            const int y = iy0 + ly, x = ix0 + lx;
+            const bool ok = i < NIN && (unsigned)y < (unsigned)H && (unsigned)x < (unsigned)W;
             const int xs = mirror ? W - 1 - x : x;
-            const int64_t idx = (((int64_t)ns * 3 + c) * H + y) * W + xs;
-            if (a.kind == D8S_IN_U8)
-                v = s_lut[c * 256 + ((const uint8_t*)a.x)[idx]];
-            else
-                v = __builtin_bit_cast(_Float16, ((const uint16_t*)a.x)[idx]);
+            idx[k] = ok ? (((int64_t)ns * 3 + c) * H + y) * W + xs : 0;
+            okm |= (uint64_t)ok << k;
         }
-        s_in[i] = v;
+        if (a.kind == D8S_IN_U8) {                        // uniform: each buffer read as its own type
+            const uint8_t* x8 = (const uint8_t*)a.x;
+#pragma unroll
+            for (int k = 0; k < KIN; ++k) raw[k] = x8[idx[k]];
+        } else {
+            const uint16_t* x16 = (const uint16_t*)a.x;
+#pragma unroll
+            for (int k = 0; k < KIN; ++k) raw[k] = x16[idx[k]];
+        }
+        __syncthreads();                                  // s_lut
+#pragma unroll
+        for (int k = 0; k < KIN; ++k) {
+            const int i = tid + 256 * k;
+            if (i >= NIN) break;
+            const int c = i / (ST_IY * ST_IX);
+            _Float16 v = (_Float16)0.0f;
+            if ((okm >> k) & 1)
+                v = a.kind == D8S_IN_U8 ? s_lut[c * 256 + raw[k]]
+                                        : __builtin_bit_cast(_Float16, (uint16_t)raw[k]);
+            s_in[i] = v;
+        }
     }
     __syncthreads();
 
@@ -776,8 +816,20 @@ __global__ __launch_bounds__(256) void k_stem(D8sStemArgs a, int tiles_x, int ti
 // ------------------------------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void k_copy(const u32x4* __restrict__ src, u32x4* __restrict__ dst,
                                               int64_t n) {
-    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256)
-        dst[i] = src[i];
+    // tiles of 1024 chunks: four coalesced loads in flight per thread, then the four stores
+    for (int64_t t = (int64_t)blockIdx.x * 1024; t < n; t += (int64_t)gridDim.x * 1024) {
+        u32x4 v[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const int64_t i = t + 256 * k + threadIdx.x;
+            if (i < n) v[k] = __builtin_nontemporal_load(src + i);
+        }
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const int64_t i = t + 256 * k + threadIdx.x;
+            if (i < n) __builtin_nontemporal_store(v[k], dst + i);
+        }
+    }
 }
 
 __global__ __launch_bounds__(256) void k_mfma_loop(int iters, int32_t* sink) {
@@ -934,17 +986,33 @@ extern "C" int d8s_conv2(const D8sConv2Args* a, void* stream) {
     return conv2_launch<1, 64, 4, 2>(a, st, 0);
 }
 
+template <int NT, int PT>
+static int trans_launch(const D8sGemmArgs* a, hipStream_t st) {
+    const int64_t NO = (int64_t)a->N * (a->HW / 4);
+    const int64_t blocks = (NO + 32 * PT - 1) / (32 * PT);
+    REQUIRE(blocks < (1ll << 31), "d8s_transition: too many pixels");
+    const size_t shm = 2 * (size_t)4 * 32 * PT * 32 + (size_t)a->G * 128;
+    hipLaunchKernelGGL((k_trans<NT, PT>), dim3((unsigned)blocks), dim3(256), shm, st, *a);
+    return launched("d8s_transition");
+}
+
 extern "C" int d8s_transition(const D8sGemmArgs* a, void* stream) {
     if (int rc = check_gemm(a, "d8s_transition")) return rc;
     REQUIRE(a->out != nullptr, "d8s_transition: null output");
-    REQUIRE(a->cout >= 32 && a->cout % 32 == 0, "d8s_transition: cout must be a positive multiple of 32");
+    REQUIRE(a->cout >= 32 && a->cout % 32 == 0 && a->cout <= 1024,
+            "d8s_transition: cout must be a multiple of 32 in [32, 1024]");
     REQUIRE(a->G0n == a->cout / 32, "d8s_transition: G0n != cout / 32");
     REQUIRE(a->W % 2 == 0 && (a->HW / a->W) % 2 == 0, "d8s_transition: H and W must be even");
-    const int64_t NO = (int64_t)a->N * (a->HW / 4);
-    const dim3 grid((unsigned)((a->cout + 127) / 128), (unsigned)((NO + 63) / 64));
-    const size_t shm = 8192 + (size_t)a->G * 128;
-    hipLaunchKernelGGL(k_trans, grid, dim3(256), shm, (hipStream_t)stream, *a);
-    return launched("d8s_transition");
+    hipStream_t st = (hipStream_t)stream;
+    switch ((a->cout / 32 + 3) / 4) {                      // output tiles per wave
+        case 1: return trans_launch<1, 2>(a, st);
+        case 2: return trans_launch<2, 2>(a, st);
+        case 3: return trans_launch<3, 1>(a, st);
+        case 4: return trans_launch<4, 1>(a, st);
+        case 5: return trans_launch<5, 1>(a, st);
+        case 6: return trans_launch<6, 1>(a, st);
+        default: return trans_launch<8, 1>(a, st);
+    }
 }
 
 extern "C" int d8s_final(const int8_t* in0, int32_t G0, const int8_t* seg, int32_t N, int32_t HW,
@@ -988,8 +1056,8 @@ extern "C" const char* d8s_last_error(void) { return g_err.c_str(); }
 extern "C" int d8s_micro_copy(const void* src, void* dst, size_t bytes, void* stream) {
     REQUIRE(src && dst && bytes % 16 == 0, "d8s_micro_copy: null pointer or size not a multiple of 16");
     const int64_t n = (int64_t)(bytes / 16);
-    const int64_t want = (n + 255) / 256;
-    const unsigned grid = (unsigned)(want < 16 * cu_count() ? (want > 0 ? want : 1) : 16 * cu_count());
+    const int64_t want = (n + 1023) / 1024;
+    const unsigned grid = (unsigned)(want < 8 * cu_count() ? (want > 0 ? want : 1) : 8 * cu_count());
     hipLaunchKernelGGL(k_copy, dim3(grid), dim3(256), 0, (hipStream_t)stream, (const u32x4*)src,
                        (u32x4*)dst, n);
     return launched("d8s_micro_copy");
