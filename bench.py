@@ -9,8 +9,10 @@ encoded images per seed (48 slices + their mirrors, the flip fused in the stem),
 slices per step.  Inputs are resident in HBM (4 distinct studies, cycled); each encoder call replays
 its HIP graph.  value = 192 K / T slices/s.
 `study_latency_ms`: configuration 4, one 24-slice study through one encoder (batch 24, one pass).
-`roofline`: the dominant kernel family, from HIP events between launches on the encoder's stream over
-R eager passes of configuration 5 (algorithmic bytes of every launch / its measured time).
+The two seeds' passes of a step run from two streams (`--serial`: one after the other).
+`roofline`: the dominant kernel family: its launches of a configuration-5 pass recorded R times in a HIP
+graph and replayed between HIP events on the encoder's stream (algorithmic bytes of a launch / the
+average launch time).
 `cpu_baseline`: the float32 DenseNet169 forward (`oracle/fp32.py`) at batch 1 on the host cores.
 One JSON line on stdout.
 """
@@ -164,7 +166,95 @@ def rocprof_summary(d: str) -> str:
         for (name, ctr), (cnt, tot) in sorted(acc.items()):
             lines.append(f"| `{name}` | {ctr} | {cnt} | {tot / cnt:.1f} |")
         lines.append("")
+    for path in sorted(glob.glob(os.path.join(d, "**", "*kernel_trace.csv"), recursive=True)):
+        lines += family_run_summary(path)
     return "\n".join(lines)
+
+
+def family_run_summary(path: str) -> list[str]:
+    """From a kernel trace of a bench.py run: the dispatches of the per-family timing (each family's
+    launches of a configuration-5 pass replayed back to back, `Dense8SEncoder.time_families`), i.e. the
+    dispatches of a family that follow one of the same family on the same queue, which is how a pass
+    never orders them.  Their mean duration is the average launch time behind bench.py's roofline."""
+    import csv
+    rows = [r for r in csv.DictReader(open(path)) if _family(r["Kernel_Name"])]
+    rows.sort(key=lambda r: int(r["Start_Timestamp"]))
+    prev: dict = {}
+    acc: dict = {}
+    for r in rows:
+        fam = _family(r["Kernel_Name"])
+        q = r["Queue_Id"]
+        if prev.get(q) == fam and fam != "copy":
+            a = acc.setdefault(fam, [0, 0.0])
+            a[0] += 1
+            a[1] += (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
+        prev[q] = fam
+    out = [f"### family timing dispatches ({os.path.basename(path)})", "",
+           "Dispatches that follow one of the same family on the same queue (the back-to-back replays "
+           "of the per-family timing; the first launch of each replay is not counted).", "",
+           "| family | dispatches | mean us |", "|---|---|---|"]
+    for fam, (n, us) in sorted(acc.items()):
+        out.append(f"| {fam} | {n} | {us / n:.2f} |")
+    return out + [""]
+
+
+TRAFFIC_FILE = ROOT / "profiles" / "encoder_c5_hbm_traffic.md"
+
+
+def traffic_summary(fetch_dir: str, write_dir: str, passes: int, copy_bytes: int = 1 << 30) -> str:
+    """HBM bytes per launch of every kernel family from two counter runs of `bench.py --pmc-passes P
+    --copy-probe` (FETCH_SIZE, then WRITE_SIZE, KiB per dispatch), each scaled by what the counter
+    reads for k_copy (1 GiB read + 1 GiB written per dispatch)."""
+    import csv
+    import glob
+
+    def collect(d: str, counter: str) -> dict:
+        acc: dict = {}
+        for path in glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True):
+            for r in csv.DictReader(open(path)):
+                fam = _family(r.get("Kernel_Name", ""))
+                if fam and r["Counter_Name"] == counter:
+                    v = acc.setdefault(fam, [0, 0.0])
+                    v[0] += 1
+                    v[1] += float(r["Counter_Value"]) * 1024
+        return acc
+
+    fe, wr = collect(fetch_dir, "FETCH_SIZE"), collect(write_dir, "WRITE_SIZE")
+    kf = copy_bytes / (fe["copy"][1] / fe["copy"][0])
+    kw = copy_bytes / (wr["copy"][1] / wr["copy"][0])
+    nb = 4 * SLICES
+    meta_blocks = [{"c0": 64, "h": 128, "w": 128, "L": 6, "trans": True},
+                   {"c0": 128, "h": 64, "w": 64, "L": 12, "trans": True},
+                   {"c0": 256, "h": 32, "w": 32, "L": 32, "trans": True},
+                   {"c0": 640, "h": 16, "w": 16, "L": 32, "trans": False}]
+    alg = kernel_bytes({"img": IMG, "blocks": meta_blocks}, nb)
+    lines = [f"Calibration: k_copy moves {copy_bytes} B read + {copy_bytes} B written per dispatch; "
+             f"FETCH_SIZE scale {kf:.3f}, WRITE_SIZE scale {kw:.3f}.", "",
+             "| family | launches per pass | HBM read MB/launch | HBM write MB/launch | traffic MB/launch "
+             "| algorithmic MB/launch | traffic / algorithmic |", "|---|---|---|---|---|---|---|"]
+    machine = []
+    for fam in ("conv1", "conv2", "trans", "stem", "final"):
+        if fam not in fe or fam not in wr:
+            continue
+        n = len(alg[fam])
+        rd = fe[fam][1] * kf / (passes * n)
+        wt = wr[fam][1] * kw / (passes * n)
+        a = sum(alg[fam]) / n
+        lines.append(f"| {fam} | {n} | {rd / 1e6:.2f} | {wt / 1e6:.2f} | {(rd + wt) / 1e6:.2f} | "
+                     f"{a / 1e6:.2f} | {(rd + wt) / a:.3f} |")
+        machine.append(f"traffic_per_launch[{fam}] = {int(rd + wt)}")
+    return "\n".join(lines + ["", "```", *machine, "```"])
+
+
+def committed_traffic(family: str) -> int | None:
+    """HBM bytes per launch of `family` from the committed counter summary (None if absent)."""
+    try:
+        for line in TRAFFIC_FILE.read_text().splitlines():
+            if line.startswith(f"traffic_per_launch[{family}] = "):
+                return int(line.split("=")[1])
+    except OSError:
+        pass
+    return None
 
 
 def cpu_baseline(reps: int = 5, warmup: int = 2) -> dict:
@@ -201,8 +291,10 @@ def main() -> None:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--prof-reps", type=int, default=3)
+    ap.add_argument("--prof-reps", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--serial", action="store_true",
+                    help="run the two seeds' passes of a step back to back on one stream")
     ap.add_argument("--copy-probe", action="store_true",
                     help="also time d8s_micro_copy over 1 GiB (HBM floor, counter calibration)")
     ap.add_argument("--rocprof-summary", metavar="DIR",
@@ -210,9 +302,14 @@ def main() -> None:
     ap.add_argument("--pmc-passes", type=int, default=0, metavar="P",
                     help="only run P eager configuration-5 passes of one encoder (the launches of "
                          "a counter-collection run), print the per-family times and exit")
+    ap.add_argument("--traffic-summary", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
+                    help="print the HBM traffic per launch from two --pmc-passes counter runs")
     args = ap.parse_args()
     if args.rocprof_summary:
         print(rocprof_summary(args.rocprof_summary))
+        return
+    if args.traffic_summary:
+        print(traffic_summary(*args.traffic_summary, passes=args.pmc_passes or 3))
         return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print(f"bench.py: this build runs on one GPU (the encoder is per-GPU, replicas need no "
@@ -234,10 +331,13 @@ def main() -> None:
         if args.pmc_passes == 1:
             enc(x, flip="tta")
             torch.cuda.synchronize()
-        print(json.dumps({"passes": args.pmc_passes, "launches_per_pass": {
+        res = {"passes": args.pmc_passes, "launches_per_pass": {
             k: len(v) for k, v in kernel_bytes(enc.meta, nb).items()},
             "bytes_per_pass": {k: sum(v) for k, v in kernel_bytes(enc.meta, nb).items()},
-            "family_ms": fam}))
+            "family_ms": fam}
+        if args.copy_probe:
+            res["copy_probe"] = copy_probe(dev, reps=1)
+        print(json.dumps(res))
         return
     encs = [build_encoder(seed, nb, dev)[0] for seed in (0, 1)]
     log(f"encoders built in {time.perf_counter() - t0:.1f} s")
@@ -250,9 +350,16 @@ def main() -> None:
         e.capture(2 * SLICES, flip="tta")
     torch.cuda.synchronize()
 
+    # the two seeds' passes are independent: dense8s.encode_concurrent runs each from its own stream,
+    # so the small, latency-bound layers of one seed's pass overlap the other's.  --serial runs them
+    # back to back.
     def step(k: int) -> None:
-        for e in encs:
-            e(studies[k % len(studies)], flip="tta")
+        x = studies[k % len(studies)]
+        if args.serial:
+            for e in encs:
+                e(x, flip="tta")
+        else:
+            dense8s.encode_concurrent([(e, x, "tta") for e in encs])
 
     for k in range(args.warmup):
         step(k)
@@ -282,8 +389,9 @@ def main() -> None:
     study_ms = float(np.median(lat)) * 1e3
     log(f"config 4: study latency {study_ms:.3f} ms (median of {len(lat)})")
 
-    # per-family kernel times (eager passes, HIP events on the encoder's stream)
-    fam = family_times(encs[0], studies[0], args.prof_reps, "tta")
+    # per-family kernel times: each family's launches of a pass in a HIP graph, replayed between
+    # HIP events on the encoder's stream
+    fam = encs[0].time_families(studies[0], reps=args.prof_reps, flip="tta")
     byts = kernel_bytes(encs[0].meta, nb)
     ops = kernel_ops(encs[0].meta, nb)
     pass_ms = sum(fam.values())
@@ -308,13 +416,16 @@ def main() -> None:
                    "global_batch": nb, "seeds": 2, "image": IMG, "parallelism": "none (1 GPU)"},
         "study_latency_ms": round(study_ms, 3),
         "study_latency_config": "C4: one 24-slice study, batch 24, one encoder, HIP graph replay",
-        "pass_ms_eager": round(pass_ms, 3),
+        "step_schedule": "serial (one stream)" if args.serial else "the 2 seeds' passes on 2 streams",
+        "pass_ms_kernels": round(pass_ms, 3),
         "pass_hbm_frac": round(total_bytes / (pass_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
         "family_ms": {k: round(v, 3) for k, v in fam.items()},
         "family_gbs": fam_gbs, "family_int8_tops": fam_tops,
         "roofline": {"bound": "hbm", "kernel": f"d8s_{dom} (all {launches} launches of a pass)",
                      "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None},
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": committed_traffic(dom),
+                     "algorithmic_bytes_per_launch": int(dom_bytes / launches),
+                     "avg_launch_ms": round(avg_ms, 5)},
     }
     if args.copy_probe:
         out["copy_probe"] = copy_probe(dev)

@@ -413,7 +413,10 @@ def validate_meta(meta: dict) -> None:
 
 # --- runner ----------------------------------------------------------------------------------
 # Graph inputs shared among the encoders of one GPU (the seeds of an ensemble read the same windows):
-# {(gpu, shape, dtype): {"buf", "src", "root"}} (`src/knee/dense8s.py:911-941`).
+# {(gpu, shape, dtype): {"buf", "src", "root", "ready", "readers"}} (`src/knee/dense8s.py:911-941`).
+# "ready" is an event after the last copy into "buf", "readers" the event after each runner's last
+# replay that read it: runners called from different streams wait on them, so one runner's copy never
+# overwrites an input another is still reading, and a skipped copy still waits for the one it reuses.
 _SHARED_IN: dict = {}
 _NOVER = itertools.count()
 
@@ -422,7 +425,8 @@ def _shared_in(dev: int, shape: tuple, dtype) -> dict:
     key = (dev, tuple(shape), dtype)
     s = _SHARED_IN.get(key)
     if s is None:
-        s = {"buf": torch.zeros(shape, dtype=dtype, device=f"cuda:{dev}"), "src": None, "root": None}
+        s = {"buf": torch.zeros(shape, dtype=dtype, device=f"cuda:{dev}"), "src": None, "root": None,
+             "ready": None, "readers": {}}
         _SHARED_IN[key] = s
     return s
 
@@ -708,9 +712,15 @@ class Dense8SEncoder:
                     root, key = _src_key(x)
                     key = key + (n,)
                     if shared["src"] != key:
+                        for ev in shared["readers"].values():   # runners still reading the old input
+                            self.stream.wait_event(ev)
+                        shared["readers"].clear()
                         buf.copy_(x)
                         shared["src"], shared["root"] = key, root
+                        shared["ready"] = _record_sync(self.stream)
                         self.calls["copy"] = self.calls.get("copy", 0) + 1
+                    elif shared["ready"] is not None:              # copied by another runner's stream
+                        self.stream.wait_event(shared["ready"])
                 for g in graphs:
                     if self.max_inflight:
                         while len(self.inflight) >= self.max_inflight:
@@ -720,6 +730,7 @@ class Dense8SEncoder:
                         ev = torch.cuda.Event(blocking=True)
                         ev.record(self.stream)
                         self.inflight.append(ev)
+                shared["readers"][id(self)] = _record_sync(self.stream)
                 self.calls["graph"] += 1
             else:
                 self._enqueue(x.contiguous(), mode)
@@ -802,6 +813,31 @@ class Dense8SEncoder:
                     tot[tag] += a.elapsed_time(b)
         return {k: round(v / reps, 4) for k, v in sorted(tot.items())}
 
+    def time_families(self, x: torch.Tensor, reps: int = 5, flip=False) -> dict:
+        """GPU milliseconds per pass of each kernel family (stem, conv1, conv2, trans, final): the
+        family's launches of one pass, in pass order, recorded in a HIP graph `reps` times and replayed
+        between events on the runner's stream.  Unlike `profile` no host gap between launches is
+        counted, so the figure is the kernels' own time.  One eager pass first fills the arenas."""
+        mode = self._mode(flip)
+        self._check_input(x, mode)
+        xf = self._padded(x[:self._per_pass(mode)].contiguous(), mode)
+        st = self.stream.cuda_stream
+        fams: dict[str, list] = {"stem": [lambda: self._stem(xf.data_ptr(), mode, st)],
+                                 "conv1": [], "conv2": [], "trans": [], "final": []}
+        for bi, (layers, trans) in enumerate(self.plan_l):
+            for c1, c2 in layers:
+                fams["conv1"].append(lambda c=c1: self._conv1(c, st))
+                fams["conv2"].append(lambda c=c2: self._conv2(c, st))
+            if trans is not None:
+                fams["trans"].append(lambda t=trans: self._trans(t, st))
+            else:
+                fams["final"].append(lambda b=bi: self._final(b, self.out.data_ptr(), st))
+        with torch.cuda.device(self.dev), torch.cuda.stream(self.stream):
+            self.stream.wait_stream(torch.cuda.current_stream(self.dev))
+            self._pass(xf.data_ptr(), self.out.data_ptr(), mode)
+            out = {k: self._time(lambda fs=fs: [f() for f in fs], reps) for k, fs in fams.items()}
+        return {k: round(v, 4) for k, v in out.items()}
+
     def _time(self, fn, reps: int = 20) -> float:
         """ms per call of `fn` (launching on the runner's stream): a HIP graph of `reps` calls replayed
         once as warm-up and once under events (`src/knee/dense8s.py:1565-1581`)."""
@@ -830,6 +866,39 @@ class Dense8SEncoder:
             if trans is not None:
                 out[f"t{bi}"] = round(self._time(lambda t=trans: self._trans(t, st), reps), 4)
         return out
+
+
+def encode_concurrent(calls) -> list[torch.Tensor]:
+    """Several runners at once: `calls` = [(runner, x, flip), ...], every runner on its own stream, the
+    caller's current stream joined after all of them.  The seeds of an ensemble read the same input and
+    are independent, so one runner's small late-block layers overlap another's work.
+
+    Each call is made with the runner's own stream current: an extra stream per call would share one
+    of the device's few hardware queues with another runner, and an event recorded there would make
+    that runner wait for everything queued before it.  Returns the runners' outputs (views, as
+    `Dense8SEncoder.__call__`)."""
+    if not calls:
+        return []
+    dev = calls[0][0].dev
+    cur = torch.cuda.current_stream(dev)
+    for enc, _, _ in calls:
+        if enc.dev != dev:
+            raise ValueError("encode_concurrent: runners on different GPUs")
+        enc.stream.wait_stream(cur)
+    outs = []
+    for enc, x, flip in calls:
+        with torch.cuda.stream(enc.stream):
+            outs.append(enc(x, flip=flip))
+    for enc, _, _ in calls:
+        cur.wait_stream(enc.stream)
+    return outs
+
+
+def _record_sync(stream) -> torch.cuda.Event:
+    """An event without timing on `stream`: orders the shared graph input between runners' streams."""
+    e = torch.cuda.Event()
+    e.record(stream)
+    return e
 
 
 def _record(stream) -> torch.cuda.Event:

@@ -110,6 +110,28 @@ def test_encoder512_graph_and_flip(dev, study512):
     assert torch.equal(short, plain[:5])
 
 
+def test_reference_format_package(dev, study512):
+    """A package in the reference's format (src/knee/dense8s.py:810-868: conv2 "ours", a TensorRT stem
+    engine and a cubin present, no "input" entry, so fp16 input) loads unchanged: the engine and cubin
+    are ignored, the stem runs from the package's S_w16 / S_bias / S_inv tables.  Fed the fp16 values
+    of the uint8 table it gives bit-identical features to the uint8 package."""
+    ours = study512["pack"]
+    meta = {k: v for k, v in ours["meta"].items() if k != "input"}
+    meta.update({"stem": "trt", "stem_int8": False, "engines": ["stem"], "kernels_sha": "0123456789ab",
+                 "blocks": [dict(b, bm=["w64_pl"] * b["L"], c2=[16, 16, "t16x16_pl"], tbm="w0",
+                                 fused=None) for b in meta["blocks"]]})
+    pack = {"meta": meta, "engines": {"stem": b"\0" * 64}, "par": dict(ours["par"]), "cubin": b"\0" * 64}
+    enc = dense8s.Dense8SEncoder(pack, dev.index or 0, 24)
+    assert enc.in_dtype == torch.float16 and enc.nb == 24
+    lut = torch.from_numpy(dense8s.input_lut([0.5] * 3, [0.25] * 3).view(np.float16).astype(np.float32))
+    x16 = lut[torch.arange(3).view(1, 3, 1, 1), torch.from_numpy(study512["x"]).long()].half().to(dev)
+    got = enc(x16).clone()
+    want = study512["enc"](study512["xd"]).clone()
+    assert torch.equal(got, want)
+    with pytest.raises(ValueError):
+        enc(study512["xd"])                                 # uint8 into an fp16 package
+
+
 def test_encoder512_flip_tta(dev, study512):
     """flip="tta": N images in, 2N features out (the N images, then the N mirrored), one pass per 12
     input images (24 encoded), equal to separate plain and mirrored calls."""
@@ -123,3 +145,24 @@ def test_encoder512_flip_tta(dev, study512):
     enc.capture(12, flip="tta")
     got = enc(x[:12], flip="tta").clone()
     assert torch.equal(got[:12], plain[:12]) and torch.equal(got[12:], mirrored[:12])
+
+
+def test_two_encoders_concurrent_streams(dev, study512):
+    """Two runners at once (`dense8s.encode_concurrent`, how bench.py overlaps the two seeds' passes),
+    eager and from graphs, on inputs that change between calls (the shared graph input is copied by one
+    runner and reused by the other): each gives what it gives alone."""
+    enc, x = study512["enc"], study512["xd"]
+    other = dense8s.Dense8SEncoder(study512["pack"], dev.index or 0, 48)
+    xs = [x, torch.flip(x, dims=[0]).contiguous()]
+    want = [enc(v, flip="tta").clone() for v in xs]
+    for graphs in (False, True):
+        if graphs:
+            enc.capture(24, flip="tta")
+            other.capture(24, flip="tta")
+        for k in range(4):
+            outs = dense8s.encode_concurrent([(enc, xs[k % 2], "tta"), (other, xs[k % 2], "tta")])
+            got = [o.clone() for o in outs]
+            _ = (x.float() * 2).sum()                   # eager work between calls
+            torch.cuda.synchronize(dev)
+            assert torch.equal(got[0], want[k % 2]) and torch.equal(got[1], want[k % 2]), (graphs, k)
+    assert dense8s.encode_concurrent([]) == []
