@@ -57,41 +57,62 @@ def build_encoder(seed: int, nb: int, dev: torch.device) -> tuple[dense8s.Dense8
     return enc, plan
 
 
-def kernel_bytes(meta: dict, n: int) -> dict[str, list[float]]:
+def kernel_bytes(meta: dict, n: int, kinds: dict | None = None) -> dict[str, list[float]]:
     """Algorithmic HBM bytes of every launch of a pass of n images, per kernel family: compulsory reads
-    of the activations and writes of the outputs, plus the weights and tables (read once)."""
-    out: dict[str, list[float]] = {"stem": [], "conv1": [], "conv2": [], "trans": [], "final": []}
+    of the activations and writes of the outputs, plus the weights and tables (read once).  `kinds`
+    {block: "conv" | "tile" | "img"} (`Dense8SEncoder.fused`): a fused layer ("dense") has no bottleneck
+    in memory; a whole block ("block") reads its input and writes its layers' outputs once."""
+    kinds = kinds or {}
+    out: dict[str, list[float]] = {"stem": [], "conv1": [], "conv2": [], "dense": [], "block": [],
+                                   "trans": [], "final": []}
     img = meta["img"]
     out["stem"].append(n * 3 * img * img + n * 64 * (img // 4) ** 2 + 64 * 168 * 2 + 3 * 256 * 2)
-    for b in meta["blocks"]:
+    for bi, b in enumerate(meta["blocks"]):
         hw = b["h"] * b["w"]
         M = n * hw
+        kind = kinds.get(bi, "conv")
+        wts = 0
         for li in range(b["L"]):
             cin = b["c0"] + 32 * li
-            out["conv1"].append(M * cin + M * 128 + 128 * cin + cin * 4 + 128 * 12)
-            out["conv2"].append(M * 128 + M * 32 + 36864 + 32 * 8)
+            w = 128 * cin + cin * 4 + 128 * 12 + 36864 + 32 * 8
+            wts += w
+            if kind == "tile":
+                out["dense"].append(M * cin + M * 32 + w)
+            elif kind == "conv":
+                out["conv1"].append(M * cin + M * 128 + 128 * cin + cin * 4 + 128 * 12)
+                out["conv2"].append(M * 128 + M * 32 + 36864 + 32 * 8)
+        if kind == "img":
+            out["block"].append(M * b["c0"] + M * 32 * b["L"] + wts)
         ctot = b["c0"] + 32 * b["L"]
         if b["trans"]:
             cout = ctot // 2
             out["trans"].append(M * ctot + (M // 4) * cout + cout * ctot + ctot * 4 + cout * 12)
         else:
             out["final"].append(M * ctot + n * ctot * 4 + ctot * 8)
-    return out
+    return {k: v for k, v in out.items() if v}
 
 
-def kernel_ops(meta: dict, n: int) -> dict[str, float]:
+def kernel_ops(meta: dict, n: int, kinds: dict | None = None) -> dict[str, float]:
     """int8 MFMA operations (2 per MAC) of a pass, per family (the transition at quarter resolution)."""
+    kinds = kinds or {}
     img = meta["img"]
-    ops = {"stem": 2.0 * n * 64 * 147 * (img // 2) ** 2, "conv1": 0.0, "conv2": 0.0, "trans": 0.0}
-    for b in meta["blocks"]:
+    ops = {"stem": 2.0 * n * 64 * 147 * (img // 2) ** 2, "conv1": 0.0, "conv2": 0.0, "dense": 0.0,
+           "block": 0.0, "trans": 0.0}
+    for bi, b in enumerate(meta["blocks"]):
         M = n * b["h"] * b["w"]
+        kind = kinds.get(bi, "conv")
         for li in range(b["L"]):
-            ops["conv1"] += 2.0 * M * (b["c0"] + 32 * li) * 128
-            ops["conv2"] += 2.0 * M * 1152 * 32
+            o1 = 2.0 * M * (b["c0"] + 32 * li) * 128
+            o2 = 2.0 * M * 1152 * 32
+            if kind == "conv":
+                ops["conv1"] += o1
+                ops["conv2"] += o2
+            else:
+                ops["dense" if kind == "tile" else "block"] += o1 + o2
         if b["trans"]:
             ctot = b["c0"] + 32 * b["L"]
             ops["trans"] += 2.0 * (M // 4) * ctot * (ctot // 2)
-    return ops
+    return {k: v for k, v in ops.items() if v}
 
 
 def family_times(enc: dense8s.Dense8SEncoder, x: torch.Tensor, reps: int, mode) -> dict[str, float]:
@@ -126,7 +147,8 @@ def copy_probe(dev: torch.device, mib: int = 1024, reps: int = 5) -> dict:
     return {"bytes_per_launch": 2 * n, "ms": round(ms, 4), "gbs": round(2 * n / (ms * 1e-3) / 1e9, 1)}
 
 
-FAMILY = {"k_conv1": "conv1", "k_conv2": "conv2", "k_trans": "trans", "k_stem": "stem",
+FAMILY = {"k_conv1": "conv1", "k_conv1p": "conv1", "k_conv2": "conv2", "k_dense": "dense",
+          "k_dblock": "block", "k_trans": "trans", "k_stem": "stem",
           "k_final": "final", "k_copy": "copy"}
 
 
@@ -227,14 +249,15 @@ def traffic_summary(fetch_dir: str, write_dir: str, passes: int, copy_bytes: int
                    {"c0": 128, "h": 64, "w": 64, "L": 12, "trans": True},
                    {"c0": 256, "h": 32, "w": 32, "L": 32, "trans": True},
                    {"c0": 640, "h": 16, "w": 16, "L": 32, "trans": False}]
-    alg = kernel_bytes({"img": IMG, "blocks": meta_blocks}, nb)
+    alg = kernel_bytes({"img": IMG, "blocks": meta_blocks}, nb,
+                       dense8s.fused_blocks({"blocks": meta_blocks}))
     lines = [f"Calibration: k_copy moves {copy_bytes} B read + {copy_bytes} B written per dispatch; "
              f"FETCH_SIZE scale {kf:.3f}, WRITE_SIZE scale {kw:.3f}.", "",
              "| family | launches per pass | HBM read MB/launch | HBM write MB/launch | traffic MB/launch "
              "| algorithmic MB/launch | traffic / algorithmic |", "|---|---|---|---|---|---|---|"]
     machine = []
-    for fam in ("conv1", "conv2", "trans", "stem", "final"):
-        if fam not in fe or fam not in wr:
+    for fam in ("conv1", "conv2", "dense", "block", "trans", "stem", "final"):
+        if fam not in fe or fam not in wr or fam not in alg:
             continue
         n = len(alg[fam])
         rd = fe[fam][1] * kf / (passes * n)
@@ -331,9 +354,9 @@ def main() -> None:
         if args.pmc_passes == 1:
             enc(x, flip="tta")
             torch.cuda.synchronize()
-        res = {"passes": args.pmc_passes, "launches_per_pass": {
-            k: len(v) for k, v in kernel_bytes(enc.meta, nb).items()},
-            "bytes_per_pass": {k: sum(v) for k, v in kernel_bytes(enc.meta, nb).items()},
+        kb = kernel_bytes(enc.meta, nb, enc.fused)
+        res = {"passes": args.pmc_passes, "launches_per_pass": {k: len(v) for k, v in kb.items()},
+               "bytes_per_pass": {k: sum(v) for k, v in kb.items()},
             "family_ms": fam}
         if args.copy_probe:
             res["copy_probe"] = copy_probe(dev, reps=1)
@@ -392,10 +415,10 @@ def main() -> None:
     # per-family kernel times: each family's launches of a pass in a HIP graph, replayed between
     # HIP events on the encoder's stream
     fam = encs[0].time_families(studies[0], reps=args.prof_reps, flip="tta")
-    byts = kernel_bytes(encs[0].meta, nb)
-    ops = kernel_ops(encs[0].meta, nb)
+    byts = kernel_bytes(encs[0].meta, nb, encs[0].fused)
+    ops = kernel_ops(encs[0].meta, nb, encs[0].fused)
     pass_ms = sum(fam.values())
-    dom = max(("conv1", "conv2", "trans", "stem"), key=lambda k: fam.get(k, 0.0))
+    dom = max(("conv1", "conv2", "dense", "block", "trans", "stem"), key=lambda k: fam.get(k, 0.0))
     dom_bytes = sum(byts[dom])
     launches = len(byts[dom])
     avg_ms = fam[dom] / launches

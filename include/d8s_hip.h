@@ -73,6 +73,52 @@ typedef struct D8sConv2Args {
     int32_t N, H, W, pad_;
 } D8sConv2Args;
 
+/* Arguments of a whole dense layer, conv1 and conv2 fused (d8s_dense): the fields of D8sGemmArgs for
+ * conv1 and of D8sConv2Args for conv2, the bottleneck staying on chip.  Same role as the reference's
+ * `struct TileArg` + `struct LayerP` of its fused "tile" layer (src/knee/dense8s_kernels.cu:996-1003,
+ * 1441-1447; src/knee/dense8s.py:139-152).
+ *   in0, seg, G0, G   the block store and the groups read (as D8sGemmArgs);
+ *   w1, abh, gd, w1sum  conv1 weights [G][128][32], prologue table, epilogue table [128][2] (g, d),
+ *                     sum_k w1[o][k] [128];
+ *   w2, sc, w2sum     conv2 weights [4][9][32][32], requantisation scale [32], weight sums [32];
+ *   out               the layer's store slot [N][H*W][32];  N, H, W images and their size. */
+typedef struct D8sDenseArgs {
+    const int8_t* in0;
+    const int8_t* seg;
+    const int8_t* w1;
+    const uint16_t* abh;
+    const float* gd;
+    const int32_t* w1sum;
+    const int8_t* w2;
+    const float* sc;
+    const int32_t* w2sum;
+    int8_t* out;
+    int32_t G0, G, N, H, W, pad_;
+} D8sDenseArgs;
+
+/* The tables of one dense layer for d8s_dense_block (fields as in D8sDenseArgs).  The reference's
+ * `struct LayerP` (src/knee/dense8s_kernels.cu:996-1003) plus the weight sums. */
+typedef struct D8sLayerP {
+    const int8_t* w1;
+    const uint16_t* abh;
+    const float* gd;
+    const int32_t* w1sum;
+    const int8_t* w2;
+    const float* sc;
+    const int32_t* w2sum;
+} D8sLayerP;
+
+/* Arguments of a whole dense block (d8s_dense_block): the block store (in0 [N][G0][H*W][32], seg
+ * [L][N][H*W][32]), `layers` a DEVICE array of L D8sLayerP (layer l reads G0 + l groups and writes
+ * slot l).  The reference's `struct ImgArg` (src/knee/dense8s_kernels.cu:1005-1011,
+ * src/knee/dense8s.py:155-159). */
+typedef struct D8sBlockArgs {
+    const int8_t* in0;
+    int8_t* seg;
+    const D8sLayerP* layers;
+    int32_t N, H, W, G0, L, pad_;
+} D8sBlockArgs;
+
 /* Arguments of the stem: 7x7/2 conv (pad 3) with norm0 folded in, bias, ReLU, 3x3/2 max-pool (pad 1)
  * and per-channel int8 quantisation into the first block's in0.  Replaces the reference's TensorRT
  * fp16 stem engine + `quant_seg` (src/knee/dense8s.py:684-716,1330-1352;
@@ -116,6 +162,19 @@ int d8s_conv1_acc32(const D8sGemmArgs* a, int32_t* acc, void* stream);
  * `conv2_t8x32_pl` / `conv2_t16x16_pl` (src/knee/dense8s_kernels.cu:2679-2832, launch
  * src/knee/dense8s.py:1274-1290). */
 int d8s_conv2(const D8sConv2Args* a, void* stream);
+
+/* A dense layer in one launch: conv1 as d8s_conv1 into a bottleneck that stays in LDS, then conv2 as
+ * d8s_conv2 into the layer's store slot; the bytes written equal those of d8s_conv1 + d8s_conv2 (the
+ * same integer sums and epilogues).  The spatial tile's halo is recomputed: no bottleneck in HBM.
+ * Replaces the reference's fused layer `dense_tile7` (src/knee/dense8s_kernels.cu:1449-1699, launch
+ * src/knee/dense8s.py:1154-1203, kind "tile"). */
+int d8s_dense(const D8sDenseArgs* a, void* stream);
+
+/* Every layer of a dense block in one launch, one workgroup per image, for maps of at most 256
+ * pixels with G0 + L - 1 <= 64: the bytes of d8s_conv1 + d8s_conv2 layer after layer.  Replaces the
+ * reference's whole-block fused kernels `dense_img*` (src/knee/dense8s_kernels.cu:1005-1219, launch
+ * src/knee/dense8s.py:1154-1203). */
+int d8s_dense_block(const D8sBlockArgs* a, void* stream);
 
 /* Transition: prologue on the 4 pixels of every 2x2 square, s = sum of the four u, S = sum_k w[o][k]
  * s[k] (exact int32), q = RNE(clamp(k'_o * (float(S) / 4), -127, 127)) into the next block's in0.

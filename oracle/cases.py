@@ -66,6 +66,11 @@ class GemmCase:
     w: np.ndarray           # [128][C] int8
     w1: np.ndarray          # [G][128][32] int8
     gd: np.ndarray          # [128][2] float32
+    W: int | None = None    # image width (None: S)
+
+    @property
+    def width(self) -> int:
+        return self.S if self.W is None else self.W
 
 
 def store_from_q(q: np.ndarray, G0: int) -> tuple[np.ndarray, np.ndarray]:
@@ -79,9 +84,11 @@ def store_from_q(q: np.ndarray, G0: int) -> tuple[np.ndarray, np.ndarray]:
     return in0, seg
 
 
-def gemm_case(S: int, C: int, N: int = 24, seed: int = 11, cout: int = 128) -> GemmCase:
-    rng = np.random.default_rng([seed, S, C])
-    HW = S * S
+def gemm_case(S: int, C: int, N: int = 24, seed: int = 11, cout: int = 128,
+              W: int | None = None) -> GemmCase:
+    """C store channels of N images of S x S (or S x W) pixels, conv1 tables, 128 outputs."""
+    rng = np.random.default_rng([seed, S, C] if W is None else [seed, S, C, W])
+    HW = S * (S if W is None else W)
     x = rng.standard_normal((N, C, HW), dtype=np.float32)
     s = float(np.abs(x).max()) / 127
     q = np.clip(np.rint(x / s), -127, 127).astype(np.int8)
@@ -99,7 +106,7 @@ def gemm_case(S: int, C: int, N: int = 24, seed: int = 11, cout: int = 128) -> G
     G0 = C0_AT.get(S, C) // 32 if C >= C0_AT.get(S, C) else C // 32
     in0, seg = store_from_q(q, G0)
     return GemmCase(S, N, G0, C // 32, in0, seg, q, abh_table(ab), ab, w, chunked(w),
-                    np.stack([g, d], 1).astype(np.float32))
+                    np.stack([g, d], 1).astype(np.float32), W)
 
 
 @dataclass

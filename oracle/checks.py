@@ -49,12 +49,13 @@ def feat_cmp(a: np.ndarray, b: np.ndarray) -> dict:
 # --- conv1 ------------------------------------------------------------------------------------
 def run_conv1(c: cases.GemmCase, device, acc32: bool = True) -> tuple[np.ndarray | None, np.ndarray]:
     """(acc [M, 128] int32 or None, bottleneck [M, 128] uint8) from d8s_conv1(_acc32)."""
-    HW, M = c.S * c.S, c.N * c.S * c.S
+    HW = c.S * c.width
+    M = c.N * HW
     in0, seg, w, abh, gd = (_dev(a, device) for a in (c.in0, c.seg, c.w1, c.abh, c.gd))
     wsum = _dev(c.w1.astype(np.int64).sum(axis=(0, 2)).astype(np.int32), device)
     bott = torch.zeros(4 * M * 32, dtype=torch.uint8, device=device)
     args = hip.GemmArgs(_ptr(in0), _ptr(seg), _ptr(w), _ptr(abh), _ptr(gd), _ptr(wsum), _ptr(bott),
-                        c.G0, c.G, c.N, HW, c.S, M, 128, 0)
+                        c.G0, c.G, c.N, HW, c.width, M, 128, 0)
     acc = None
     if acc32:
         acc = torch.full((M * 128,), -7, dtype=torch.int32, device=device)
@@ -110,6 +111,37 @@ def exact_conv2(c: cases.Conv2Case) -> tuple[np.ndarray, np.ndarray]:
         accs.append(a.permute(0, 2, 3, 1).reshape(-1, 32).numpy())
     acc = np.concatenate(accs).astype(np.int32)
     return acc, lib.conv2_epilogue(acc, c.sc)
+
+
+# --- fused dense layer ------------------------------------------------------------------------
+def run_dense(c: cases.GemmCase, c2: cases.Conv2Case, device, slots: int = 3,
+              slot: int = 1) -> tuple[np.ndarray, np.ndarray]:
+    """d8s_dense on the store and conv1 tables of `c` and the conv2 tables of `c2`, into slot `slot` of
+    a `slots`-slot buffer filled with a sentinel: (the slot [M, 32] int8, the other slots' bytes)."""
+    H, W = c.S, c.width
+    M = c.N * H * W
+    in0, seg, w1, abh, gd, w2k, sc = (_dev(a, device) for a in (c.in0, c.seg, c.w1, c.abh, c.gd, c2.w2k,
+                                                                  c2.sc))
+    w1sum = _dev(c.w1.astype(np.int64).sum(axis=(0, 2)).astype(np.int32), device)
+    w2sum = _dev(c2.w2k.astype(np.int64).sum(axis=(0, 1, 3)).astype(np.int32), device)
+    store = torch.full((slots * M * 32,), 0x5A, dtype=torch.int8, device=device)
+    args = hip.DenseArgs(_ptr(in0), _ptr(seg), _ptr(w1), _ptr(abh), _ptr(gd), _ptr(w1sum), _ptr(w2k),
+                         _ptr(sc), _ptr(w2sum), _ptr(store) + slot * M * 32, c.G0, c.G, c.N, H, W, 0)
+    hip.call("d8s_dense", ctypes.byref(args), _stream(device))
+    torch.cuda.synchronize(device)
+    s = store.cpu().numpy().reshape(slots, M, 32)
+    others = np.concatenate([s[k].reshape(-1) for k in range(slots) if k != slot])
+    return s[slot], others
+
+
+def exact_dense(c: cases.GemmCase, c2: cases.Conv2Case) -> np.ndarray:
+    """q [M, 32] of conv1 then conv2: the bottleneck bytes of `exact_conv1`, the 3x3 conv of
+    `exact_conv2` on them."""
+    _, v = exact_conv1(c)                                        # [M, 128] uint8
+    H, W = c.S, c.width
+    vv = np.ascontiguousarray(v.reshape(c.N, H, W, 128).transpose(0, 3, 1, 2))
+    d = cases.Conv2Case(H, c.N, vv, None, c2.w2, c2.w2k, c2.sc)
+    return exact_conv2(d)[1]
 
 
 # --- transition -------------------------------------------------------------------------------
@@ -206,7 +238,7 @@ def check_trace(enc, trace: dict, feats: np.ndarray, par: dict, max_rows: int | 
     rng = np.random.default_rng(seed)
     meta = enc.meta
     n = enc.nb
-    worst = {"conv1": [], "conv2": [], "trans": [], "final": None}
+    worst = {"conv1": [], "conv2": [], "dense": [], "trans": [], "final": None}
 
     def pick(m):
         if max_rows is None or m <= max_rows:
@@ -220,6 +252,22 @@ def check_trace(enc, trace: dict, feats: np.ndarray, par: dict, max_rows: int | 
         for li in range(b["L"]):
             q = store_q(trace, bi, li)
             in0, seg = cases.store_from_q(q, g0)
+            if ("bott", bi, li) not in trace:
+                # fused layer: the oracle's bottleneck on the 3x3 neighbourhoods of sampled pixels,
+                # then its conv2 on them
+                sel2 = pick(n * hw)
+                nbr = neighbourhoods(sel2, h, w)
+                _, vb = lib.conv1(in0, seg, g0, g0 + li, n, hw, par[f"L{bi}_{li}_abh"],
+                                  par[f"L{bi}_{li}_w1"], par[f"L{bi}_{li}_gdu"], nbr)
+                rows = np.zeros((n * hw, 128), np.uint8)
+                rows[nbr] = vb
+                planar = np.ascontiguousarray(rows.reshape(-1, 4, 32).transpose(1, 0, 2))
+                _, want2 = lib.conv2(planar, n, h, w, par[f"L{bi}_{li}_w2k"], par[f"L{bi}_{li}_c2u"],
+                                     sel2)
+                seg_out = trace[(bi, li + 1)].cpu().numpy().astype(np.int8)
+                got2 = seg_out.reshape(n, 32, hw).transpose(0, 2, 1).reshape(n * hw, 32)[sel2]
+                worst["dense"].append(bytes_cmp(got2, want2))
+                continue
             sel = pick(n * hw)
             _, want = lib.conv1(in0, seg, g0, g0 + li, n, hw, par[f"L{bi}_{li}_abh"],
                                 par[f"L{bi}_{li}_w1"], par[f"L{bi}_{li}_gdu"], sel)
@@ -251,9 +299,23 @@ def check_trace(enc, trace: dict, feats: np.ndarray, par: dict, max_rows: int | 
     return worst
 
 
+def neighbourhoods(sel: np.ndarray, h: int, w: int) -> np.ndarray:
+    """Rows (n h w + y w + x) of the in-image 3 x 3 neighbourhoods of the rows `sel`, sorted, unique."""
+    hw = h * w
+    n, p = np.divmod(np.asarray(sel, np.int64), hw)
+    y, x = np.divmod(p, w)
+    out = []
+    for dy in (-1, 0, 1):
+        for dx in (-1, 0, 1):
+            yy, xx = y + dy, x + dx
+            ok = (yy >= 0) & (yy < h) & (xx >= 0) & (xx < w)
+            out.append((n * hw + yy * w + xx)[ok])
+    return np.unique(np.concatenate(out))
+
+
 def summarize(worst: dict) -> dict:
     out = {}
-    for k in ("conv1", "conv2", "trans"):
+    for k in ("conv1", "conv2", "dense", "trans"):
         v = worst[k]
         out[k] = {"launches": len(v), "mismatch": sum(x["mismatch"] for x in v),
                   "max_diff": max((x["max_diff"] for x in v), default=0)}

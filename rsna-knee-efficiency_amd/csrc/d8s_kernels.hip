@@ -20,6 +20,7 @@
 #include <string.h>
 
 #include <string>
+#include <type_traits>
 
 #include "d8s_hip.h"
 
@@ -28,6 +29,7 @@
 #endif
 
 #define DEV __device__ __forceinline__
+#define INLINE __attribute__((always_inline))   // lambdas: slot indices must fold to constants
 
 typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
 typedef int32_t i32x16 __attribute__((ext_vector_type(16)));
@@ -296,6 +298,192 @@ __global__ __launch_bounds__(256, 2) void k_conv1(D8sGemmArgs a, int32_t* __rest
 }
 
 // ------------------------------------------------------------------------------------------------
+// conv1, persistent: every wave streams 64-pixel tiles t = wave id, + waves in the grid, ... (no
+// workgroup-level sharing besides the layer's tables in LDS, no barrier after the start).  Per tile the
+// K loop is the one of k_conv1 over G rounded up to a multiple of 4 (padded steps multiply zero
+// operands), and the activation prefetch, 4 groups ahead, runs on into the next tile's first groups:
+// the first loads of a tile are in flight during the previous tile's last steps and epilogue, so the
+// pipeline fills once per wave instead of once per tile.  Used for the large maps (many tiles per
+// wave); the pixel offsets are 32-bit (in0 and each store slot < 4 GiB, checked on the host).
+// ------------------------------------------------------------------------------------------------
+// Activation bytes of step t of a persistent conv1 tile (see k_conv1p): t < Gp this tile's group t
+// (past G - 1 a repeat of it, unused), t >= Gp the next tile's group t - Gp (clamped).  Plain values
+// in and out: the pixel offsets of the two tiles must stay in registers (selected, never addressed).
+DEV void c1p_act(u32x4& r0, u32x4& r1, const uint8_t* in0, const uint8_t* seg, int64_t in_gs,
+                 int64_t seg_gs, int G0, int G, int Gp, int t, uint32_t ci0, uint32_t ci1, uint32_t cs0,
+                 uint32_t cs1, uint32_t ni0, uint32_t ni1, uint32_t ns0, uint32_t ns1) {
+    const bool cur = t < Gp;
+    int g = cur ? t : t - Gp;
+    g = g < G ? g : G - 1;
+    const bool in = g < G0;
+    const uint8_t* base = in ? in0 + g * in_gs : seg + (int64_t)(g - G0) * seg_gs;
+    const uint32_t o0 = cur ? (in ? ci0 : cs0) : (in ? ni0 : ns0);
+    const uint32_t o1 = cur ? (in ? ci1 : cs1) : (in ? ni1 : ns1);
+    r0 = *(const u32x4*)(base + o0);
+    r1 = *(const u32x4*)(base + o1);
+}
+
+// Byte offsets of the lane's two pixels (j, j + 32) of 64-pixel tile t in an in0 group (i0, i1) and in
+// a store slot (s0, s1); pixels past the last row repeat it.
+DEV void c1p_pixels(int t, int j, int h, int64_t rows, int64_t HW, int G0, uint32_t& i0, uint32_t& i1,
+                    uint32_t& s0, uint32_t& s1) {
+    int64_t m0 = (int64_t)t * 64 + j, m1 = m0 + 32;
+    if (m0 >= rows) m0 = rows - 1;
+    if (m1 >= rows) m1 = rows - 1;
+    const int64_t n0 = m0 / HW, p0 = m0 - n0 * HW, n1 = m1 / HW, p1 = m1 - n1 * HW;
+    i0 = (uint32_t)((n0 * G0 * HW + p0) * 32 + 16 * h);
+    i1 = (uint32_t)((n1 * G0 * HW + p1) * 32 + 16 * h);
+    s0 = (uint32_t)((n0 * HW + p0) * 32 + 16 * h);
+    s1 = (uint32_t)((n1 * HW + p1) * 32 + 16 * h);
+}
+
+template <bool ACC32>
+__global__ __launch_bounds__(256, 2) void k_conv1p(D8sGemmArgs a, int32_t* __restrict__ acc_out) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    int32_t* s_wsum = (int32_t*)smem;                     // [128]
+    float2* s_gd = (float2*)(s_wsum + 128);               // [128]
+    uint32_t* s_abh = (uint32_t*)(s_gd + 128);            // [G * 32]
+    const int G = a.G, G0 = a.G0;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int h = lane >> 5, j = lane & 31;
+    {
+        const uint32_t* abh32 = (const uint32_t*)a.abh;
+        for (int i = tid; i < G * 32; i += 256) s_abh[i] = abh32[i];
+        if (tid < 128) {
+            s_wsum[tid] = a.wsum[tid];
+            s_gd[tid] = ((const float2*)a.gd)[tid];
+        }
+    }
+    __syncthreads();
+
+    const int64_t rows = a.rows, HW = a.HW;
+    const int ntiles = (int)((rows + 63) / 64);
+    const int stride = (int)gridDim.x * 4;
+    int tile = (int)blockIdx.x * 4 + wave;
+    if (tile >= ntiles) return;                          // (uniform per wave; no barrier follows)
+
+    const uint8_t* in0 = (const uint8_t*)a.in0;
+    const uint8_t* seg = (const uint8_t*)a.seg;
+    uint8_t* out = (uint8_t*)a.out;
+    const int64_t in_gs = HW * 32, seg_gs = (int64_t)a.N * HW * 32;
+    uint32_t ci0, ci1, cs0, cs1, ni0, ni1, ns0, ns1;      // this tile's and the next tile's offsets
+    c1p_pixels(tile, j, h, rows, HW, G0, ci0, ci1, cs0, cs1);
+    int next = tile + stride;
+    c1p_pixels(next < ntiles ? next : tile, j, h, rows, HW, G0, ni0, ni1, ns0, ns1);
+
+    const int Gp = (G + 3) & ~3;
+    u32x4 ra[4][2];
+    u32x4 rb[2][4];
+    // weights: output tile c, row 32 c + j, half h of group g at w + (g * 256 + 64 c + 2 j + h) * 16
+    const u32x4* wl = (const u32x4*)a.w + j * 2 + h;
+#define C1P_LOAD_B(bslot, g)                                                                      \
+    do {                                                                                          \
+        const u32x4* p_ = wl + (int64_t)(g) * 256;                                                \
+        _Pragma("unroll") for (int c_ = 0; c_ < 4; ++c_) rb[bslot][c_] = p_[64 * c_];             \
+    } while (0)
+#define C1P_LOAD_A(slot, t)                                                                       \
+    c1p_act(ra[slot][0], ra[slot][1], in0, seg, in_gs, seg_gs, G0, G, Gp, (t), ci0, ci1, cs0, cs1,  \
+            ni0, ni1, ns0, ns1)
+
+    C1P_LOAD_B(0, 0);
+    C1P_LOAD_A(0, 0);
+    C1P_LOAD_A(1, 1);
+    C1P_LOAD_A(2, 2);
+    C1P_LOAD_A(3, 3);
+
+    for (;;) {
+        i32x16 acc[2][4];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            i32x16 init;
+#pragma unroll
+            for (int v = 0; v < 16; ++v) init[v] = 128 * s_wsum[32 * c + res_row(v, h)];
+            acc[0][c] = init;
+            acc[1][c] = init;
+        }
+        // one K step: weights of the next step first (issue order), the prologue of this step's bytes
+        // (zero operands on padded steps), the activations 4 steps ahead, the 8 MFMAs
+#define C1P_STEP(slot, k)                                                                         \
+    do {                                                                                          \
+        const int k_ = (k);                                                                       \
+        C1P_LOAD_B(((slot) + 1) & 1, k_ + 1 < G ? k_ + 1 : (k_ + 1 < Gp ? G - 1 : 0));            \
+        asm volatile("" ::: "memory");                                                            \
+        u32x4 b0_ = {0, 0, 0, 0}, b1_ = {0, 0, 0, 0};                                             \
+        if (k_ < G) {                                                                             \
+            const u32x4* pp_ = (const u32x4*)(s_abh + k_ * 32 + h * 16);                          \
+            const u32x4 p0_ = pp_[0], p1_ = pp_[1], p2_ = pp_[2], p3_ = pp_[3];                   \
+            b0_ = pro16(ra[slot][0], p0_, p1_, p2_, p3_);                                         \
+            b1_ = pro16(ra[slot][1], p0_, p1_, p2_, p3_);                                         \
+        }                                                                                         \
+        C1P_LOAD_A(slot, k_ + 4);                                                                 \
+        _Pragma("unroll") for (int c_ = 0; c_ < 4; ++c_) {                                        \
+            acc[0][c_] = mfma_i8(rb[(slot) & 1][c_], b0_, acc[0][c_]);                            \
+            acc[1][c_] = mfma_i8(rb[(slot) & 1][c_], b1_, acc[1][c_]);                            \
+        }                                                                                         \
+    } while (0)
+        int k = 0;
+        do {                                           // Gp >= 4: no path around the loop
+            C1P_STEP(0, k);
+            C1P_STEP(1, k + 1);
+            C1P_STEP(2, k + 2);
+            C1P_STEP(3, k + 3);
+            k += 4;
+        } while (k < Gp);
+#undef C1P_STEP
+
+        // epilogue as k_conv1 (conv1w_body epilogue, src/knee/dense8s_kernels.cu:595-611)
+        const int64_t mbase = (int64_t)tile * 64 + j;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+#pragma unroll
+            for (int u = 0; u < 2; ++u) {
+                const int64_t m = mbase + 32 * u;
+                if (ACC32) {
+                    if (m < rows) {
+#pragma unroll
+                        for (int kk = 0; kk < 4; ++kk) {
+                            const i32x4 q = {acc[u][c][4 * kk], acc[u][c][4 * kk + 1],
+                                             acc[u][c][4 * kk + 2], acc[u][c][4 * kk + 3]};
+                            *(i32x4*)(acc_out + m * 128 + 32 * c + 8 * kk + 4 * h) = q;
+                        }
+                    }
+                    if (out == nullptr) continue;
+                }
+                uint32_t e[4];
+#pragma unroll
+                for (int kk = 0; kk < 4; ++kk) {
+                    uint32_t d = 0;
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const int v = 4 * kk + r;
+                        const float2 prm = s_gd[32 * c + res_row(v, h)];
+                        float y = __builtin_fmaf(prm.x, (float)acc[u][c][v], prm.y);
+                        y = __builtin_fminf(__builtin_fmaxf(y, 0.0f), 1.0f);
+                        const uint32_t b = __float_as_uint(__builtin_fmaf(y, 255.0f, 8388608.0f)) & 0xffu;
+                        d |= b << (8 * r);
+                    }
+                    e[kk] = d;
+                }
+                const u32x4 row = xchg_rows(e[0], e[1], e[2], e[3], h);
+                if (m < rows) *(u32x4*)(out + ((int64_t)c * rows + m) * 32 + 16 * h) = row;
+            }
+            __builtin_amdgcn_sched_barrier(0);         // one output tile's values live at a time
+        }
+        if (next >= ntiles) break;
+        tile = next;
+        ci0 = ni0;
+        ci1 = ni1;
+        cs0 = ns0;
+        cs1 = ns1;
+        next = tile + stride;
+        c1p_pixels(next < ntiles ? next : tile, j, h, rows, HW, G0, ni0, ni1, ns0, ns1);
+    }
+#undef C1P_LOAD_A
+#undef C1P_LOAD_B
+}
+
+// ------------------------------------------------------------------------------------------------
 // conv2: 3x3 pad 1, 128 -> 32.  Persistent workgroups with the 36 KB of weights resident in LDS, one
 // spatial tile of TH x TW output pixels at a time with the halo of its 4 bottleneck planes in LDS.
 // The next tile's halo is loaded into registers while the current one is computed.
@@ -468,6 +656,551 @@ __global__ __launch_bounds__(256, 2) void k_conv2(D8sConv2Args a, int tiles_x, i
             hstore();
             __syncthreads();
         }
+    }
+}
+
+// ------------------------------------------------------------------------------------------------
+// Dense layer with conv1 and conv2 fused: the bottleneck of a spatial tile never leaves LDS.
+// A workgroup of NW waves (two per SIMD) loops over TH x TW output tiles.  For a tile it computes the
+// bottleneck of the (TH + 2) x (TW + 2) window around it (its in-image pixels, numbered row by row and
+// packed 32 to an MFMA column block: wave w takes blocks w, w + NW, ...; the halo is recomputed by the
+// neighbouring tiles), writes it to LDS as conv2 operands (u - 128, out-of-image pixels = zero
+// padding), then runs the 3x3 conv from LDS (wave w: output pixel blocks w, w + NW, ..., all 36
+// K-steps).  The K loop of conv1 runs over G rounded up to a multiple of 4 (padded steps multiply zero
+// operands) so that the activation prefetch, 4 groups ahead, runs on into the next tile's first
+// groups: they are in flight while the bottleneck epilogue and the 3x3 conv of this tile run.  Every
+// global load of the steady state is an activation or weight load and the layer's small tables sit
+// in LDS, so no wait drains the prefetch.  (No lambdas and no arrays selected at run time in the hot
+// code: either puts locals in scratch memory, whose loads wait for every load in flight.)
+// ------------------------------------------------------------------------------------------------
+template <int TW, int TH, int CPW, int NW, bool WL>
+struct DnShape {
+    static constexpr int NT = 64 * NW;                              // threads
+    static constexpr int BW = TW + 2, BH = TH + 2, WIN = BW * BH;    // bottleneck window
+    static constexpr int NB2 = TW * TH / 32;                        // output pixel blocks
+    static constexpr int PT = (NB2 + NW - 1) / NW;                  // per wave (the last may be short)
+    static constexpr size_t BOT_BYTES = (size_t)WIN * 128;          // [4][WIN][2] 16-byte chunks
+    static constexpr size_t PRM_BYTES = 128 * 4 + 128 * 8 + 32 * 4 + 32 * 4;
+    static_assert(TW * TH % 32 == 0, "output tile = whole pixel blocks");
+    static_assert(CPW == 1 || CPW == 2, "one or two conv1 column blocks per wave");
+    // bottleneck window, tables, prologue table [G][32] dwords, (WL) conv1 weights [G][256] chunks
+    static constexpr size_t lds(int G) { return BOT_BYTES + PRM_BYTES + (size_t)G * (WL ? 128 + 4096 : 128); }
+};
+
+// Tile geometry (uniform): image n, output origin (y0, x0), in-image window [ya, ya + npx / ww) x
+// [xa, xa + ww).
+struct DnGeo { int n, y0, x0, ya, xa, ww, npx; };
+
+template <int TW, int TH>
+DEV DnGeo dn_geo(int t, int tiles_x, int tiles_y, int H, int W) {
+    DnGeo g;
+    const int per = tiles_x * tiles_y;
+    g.n = t / per;
+    const int r = t - g.n * per;
+    g.y0 = (r / tiles_x) * TH;
+    g.x0 = (r % tiles_x) * TW;
+    g.ya = g.y0 > 0 ? g.y0 - 1 : 0;
+    g.xa = g.x0 > 0 ? g.x0 - 1 : 0;
+    const int yb = g.y0 + TH + 1 < H ? g.y0 + TH + 1 : H;
+    const int xb = g.x0 + TW + 1 < W ? g.x0 + TW + 1 : W;
+    g.ww = xb - g.xa;
+    g.npx = (yb - g.ya) * g.ww;
+    return g;
+}
+
+// Byte offset in a store group of window pixel q (clamped to the window's last pixel), lane half h.
+DEV uint32_t dn_pixel(const DnGeo& g, int q, int W, int h) {
+    q = q < g.npx ? q : g.npx - 1;
+    const int wy = q / g.ww, wx = q - wy * g.ww;
+    return (uint32_t)((g.ya + wy) * W + g.xa + wx) * 32u + 16u * h;
+}
+
+template <int TW, int TH, int CPW, int NW, bool WL>
+__global__ __launch_bounds__(64 * NW, 1) void k_dense(D8sDenseArgs a, int tiles_x, int tiles_y) {
+    using S = DnShape<TW, TH, CPW, NW, WL>;
+    constexpr int BW = S::BW, WIN = S::WIN, NT = S::NT, NB2 = S::NB2, PT = S::PT;
+    __shared__ __attribute__((aligned(16))) u32x4 s_w[4 * 9 * 32 * 2];    // conv2 weights, 36 KB
+    extern __shared__ __attribute__((aligned(16))) u32x4 s_dyn[];
+    u32x4* s_b = s_dyn;                                                    // [4][WIN][2]
+    int32_t* s_w1sum = (int32_t*)((uint8_t*)s_dyn + S::BOT_BYTES);        // [128]
+    float2* s_gd = (float2*)(s_w1sum + 128);                              // [128]
+    float* s_sc = (float*)(s_gd + 128);                                   // [32]
+    int32_t* s_w2sum = (int32_t*)(s_sc + 32);                             // [32]
+    uint32_t* s_abh = (uint32_t*)(s_w2sum + 32);                          // [G * 32]
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int h = lane >> 5, j = lane & 31;
+    const int G = a.G, G0 = a.G0, H = a.H, W = a.W, N = a.N;
+    u32x4* s_w1 = (u32x4*)(s_abh + G * 32);                               // [G * 256]
+    const int64_t HW = (int64_t)H * W;
+    const int total = N * tiles_x * tiles_y;
+    int tile = blockIdx.x;
+    if (tile >= total) return;
+
+    {
+        constexpr int NCH = (2304 + NT - 1) / NT;
+        u32x4 wv[NCH];
+        const u32x4* w2 = (const u32x4*)a.w2;
+#pragma unroll
+        for (int k = 0; k < NCH; ++k) wv[k] = w2[min(tid + NT * k, 2303)];
+#pragma unroll
+        for (int k = 0; k < NCH; ++k)
+            if (tid + NT * k < 2304) s_w[swz((tid + NT * k) >> 1, tid & 1)] = wv[k];
+    }
+    if (tid < 128) {
+        s_w1sum[tid] = a.w1sum[tid];
+        s_gd[tid] = ((const float2*)a.gd)[tid];
+    } else if (tid < 160) {
+        s_sc[tid - 128] = a.sc[tid - 128];
+        s_w2sum[tid - 128] = a.w2sum[tid - 128];
+    }
+    {
+        const uint32_t* abh32 = (const uint32_t*)a.abh;
+        for (int i = tid; i < G * 32; i += NT) s_abh[i] = abh32[i];
+        // the layer's conv1 weights (WL): every wave reads all of them for every tile
+        const u32x4* w1 = (const u32x4*)a.w1;
+        for (int i = tid; WL && i < G * 256; i += 4 * NT) {
+            u32x4 v[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) v[u] = w1[min(i + u * NT, G * 256 - 1)];
+#pragma unroll
+            for (int u = 0; u < 4; ++u)
+                if (i + u * NT < G * 256) s_w1[i + u * NT] = v[u];
+        }
+    }
+
+    const uint8_t* in0 = (const uint8_t*)a.in0;
+    const uint8_t* seg = (const uint8_t*)a.seg;
+    const int64_t in_img = (int64_t)G0 * HW * 32, grp = HW * 32, seg_slot = (int64_t)N * HW * 32;
+    // this tile's and the next tile's geometry and the lane's pixel offsets (column blocks 0, 1)
+    DnGeo cg = dn_geo<TW, TH>(tile, tiles_x, tiles_y, H, W);
+    int next = tile + (int)gridDim.x;
+    DnGeo ng = dn_geo<TW, TH>(next < total ? next : tile, tiles_x, tiles_y, H, W);
+    uint32_t co0 = dn_pixel(cg, 32 * wave + j, W, h), co1 = 0;
+    uint32_t no0 = dn_pixel(ng, 32 * wave + j, W, h), no1 = 0;
+    if (CPW > 1) {
+        co1 = dn_pixel(cg, 32 * (wave + NW) + j, W, h);
+        no1 = dn_pixel(ng, 32 * (wave + NW) + j, W, h);
+    }
+
+    const int Gp = (G + 3) & ~3;                       // K steps per tile
+    u32x4 ra[4][CPW];
+    u32x4 rb[WL ? 1 : 2][4];
+    // conv1 weights: output tile c, row 32 c + j, half h of group g in chunk g * 256 + 64 c + 2 j + h;
+    // from LDS for the step itself (WL), else from global memory one step ahead (double-buffered)
+    const u32x4* wl = (const u32x4*)a.w1 + j * 2 + h;
+#define DN_LOAD_B(bslot, g)                                                                       \
+    do {                                                                                          \
+        const u32x4* p_ = (WL ? (const u32x4*)s_w1 + j * 2 + h : wl) + (int64_t)(g) * 256;        \
+        _Pragma("unroll") for (int c_ = 0; c_ < 4; ++c_) rb[WL ? 0 : (bslot)][c_] = p_[64 * c_];  \
+    } while (0)
+    // activations of step t: t < Gp this tile's group t (repeats of G - 1 past it, unused), t >= Gp
+    // the next tile's group t - Gp (clamped; this tile's again when there is none).  Unconditional:
+    // the compiler can count the loads in flight instead of waiting for all of them.
+#define DN_LOAD_A(slot, t)                                                                        \
+    do {                                                                                          \
+        const int t_ = (t);                                                                       \
+        const bool cur_ = t_ < Gp;                                                                \
+        int g_ = cur_ ? t_ : t_ - Gp;                                                             \
+        g_ = g_ < G ? g_ : G - 1;                                                                 \
+        const int n_ = cur_ ? cg.n : ng.n;                                                        \
+        const uint8_t* b_ = g_ < G0 ? in0 + n_ * in_img + g_ * grp                                \
+                                    : seg + (int64_t)(g_ - G0) * seg_slot + n_ * grp;             \
+        ra[slot][0] = *(const u32x4*)(b_ + (cur_ ? co0 : no0));                                   \
+        if (CPW > 1) ra[slot][CPW - 1] = *(const u32x4*)(b_ + (cur_ ? co1 : no1));                \
+    } while (0)
+
+    if (!WL) DN_LOAD_B(0, 0);
+    DN_LOAD_A(0, 0);
+    DN_LOAD_A(1, 1);
+    DN_LOAD_A(2, 2);
+    DN_LOAD_A(3, 3);
+    __syncthreads();                                   // LDS tables and conv2 weights
+
+    for (;;) {
+        // ---- conv1 of the window: acc = 128 sum_k w + sum_k w (u - 128) ----
+        i32x16 acc[CPW][4];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            i32x16 init;
+#pragma unroll
+            for (int v = 0; v < 16; ++v) init[v] = 128 * s_w1sum[32 * c + res_row(v, h)];
+#pragma unroll
+            for (int i = 0; i < CPW; ++i) acc[i][c] = init;
+        }
+#define DN_STEP(slot, k)                                                                          \
+    do {                                                                                          \
+        const int k_ = (k);                                                                       \
+        if (WL) {                                                                                 \
+            DN_LOAD_B(0, k_ < G ? k_ : G - 1);                                                    \
+        } else {                                                                                  \
+            DN_LOAD_B(((slot) + 1) & 1, k_ + 1 < G ? k_ + 1 : (k_ + 1 < Gp ? G - 1 : 0));         \
+            asm volatile("" ::: "memory");                                                        \
+        }                                                                                         \
+        u32x4 bx_[CPW];                                                                           \
+        _Pragma("unroll") for (int i_ = 0; i_ < CPW; ++i_) bx_[i_] = u32x4{0, 0, 0, 0};           \
+        if (k_ < G) {                                                                             \
+            const u32x4* pp_ = (const u32x4*)(s_abh + k_ * 32 + h * 16);                          \
+            const u32x4 p0_ = pp_[0], p1_ = pp_[1], p2_ = pp_[2], p3_ = pp_[3];                   \
+            _Pragma("unroll") for (int i_ = 0; i_ < CPW; ++i_)                                    \
+                bx_[i_] = pro16(ra[slot][i_], p0_, p1_, p2_, p3_);                                \
+        }                                                                                         \
+        DN_LOAD_A(slot, k_ + 4);                                                                  \
+        _Pragma("unroll") for (int c_ = 0; c_ < 4; ++c_)                                          \
+            _Pragma("unroll") for (int i_ = 0; i_ < CPW; ++i_)                                    \
+                acc[i_][c_] = mfma_i8(rb[WL ? 0 : (slot) & 1][c_], bx_[i_], acc[i_][c_]);          \
+    } while (0)
+        int k = 0;
+        do {                                           // Gp >= 4: no path around the loop
+            DN_STEP(0, k);
+            DN_STEP(1, k + 1);
+            DN_STEP(2, k + 2);
+            DN_STEP(3, k + 3);
+            k += 4;
+        } while (k < Gp);
+#undef DN_STEP
+
+        // ---- bottleneck into LDS: v = low byte of fma(sat(fma(g, acc, d)), 255, 2^23), stored as
+        // v ^ 0x80 (the conv2 operand); out-of-image window pixels get 0x80 (zero padding) ----
+        const bool interior = cg.y0 >= 1 && cg.x0 >= 1 && cg.y0 + TH + 1 <= H && cg.x0 + TW + 1 <= W;
+        if (!interior) {
+            const u32x4 pad = {SIGN4, SIGN4, SIGN4, SIGN4};
+            for (int idx = tid; idx < WIN * 8; idx += NT) {
+                const int wp = idx >> 3, c = (idx >> 1) & 3, hh = idx & 1;
+                const int wy = wp / BW, wx = wp - wy * BW;
+                const int y = cg.y0 - 1 + wy, x = cg.x0 - 1 + wx;
+                if ((unsigned)y >= (unsigned)H || (unsigned)x >= (unsigned)W)
+                    s_b[c * WIN * 2 + swz(wp, hh)] = pad;
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < CPW; ++i) {
+            // the lane's window slot (-1 past the window's end)
+            const int q = 32 * (wave + NW * i) + j;
+            int dst = -1;
+            if (q < cg.npx) {
+                const int wy = q / cg.ww, wx = q - wy * cg.ww;
+                dst = (cg.ya + wy - cg.y0 + 1) * BW + (cg.xa + wx - cg.x0 + 1);
+            }
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                uint32_t e[4];
+#pragma unroll
+                for (int kk = 0; kk < 4; ++kk) {
+                    uint32_t d = 0;
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const int v = 4 * kk + r;
+                        const float2 prm = s_gd[32 * c + res_row(v, h)];
+                        float y = __builtin_fmaf(prm.x, (float)acc[i][c][v], prm.y);
+                        y = __builtin_fminf(__builtin_fmaxf(y, 0.0f), 1.0f);
+                        const uint32_t b = __float_as_uint(__builtin_fmaf(y, 255.0f, 8388608.0f)) & 0xffu;
+                        d |= b << (8 * r);
+                    }
+                    e[kk] = d ^ SIGN4;
+                }
+                const u32x4 row = xchg_rows(e[0], e[1], e[2], e[3], h);
+                if (dst >= 0) s_b[c * WIN * 2 + swz(dst, h)] = row;
+                // one accumulator tile at a time: read all of them ahead and the registers run out
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+        __syncthreads();                               // the window's bottleneck is in LDS
+
+        // ---- conv2 (3x3, pad 1) from LDS: wave w, output pixel blocks w + NW t (t < np: PT, or PT - 1
+        // for the last waves when NW does not divide NB2) ----
+        const int np = (NB2 - wave + NW - 1) / NW;
+        if (np > 0) {
+            i32x16 acc2[PT];
+            int q0[PT];
+#pragma unroll
+            for (int t = 0; t < PT; ++t) {
+                const int p = (wave + NW * t) * 32 + j;
+                q0[t] = t < np ? (p / TW) * BW + (p % TW) : 0;
+            }
+            {
+                i32x16 init2;
+#pragma unroll
+                for (int v = 0; v < 16; ++v) init2[v] = 128 * s_w2sum[res_row(v, h)];
+#pragma unroll
+                for (int t = 0; t < PT; ++t) acc2[t] = init2;
+            }
+            u32x4 aw[2], bq[2][PT];
+#define DN_FETCH(s, sl)                                                                           \
+    do {                                                                                          \
+        const int c_ = (s) / 9, tap_ = (s) % 9;                                                   \
+        const int o_ = (tap_ / 3) * BW + (tap_ % 3);                                              \
+        aw[sl] = s_w[swz((c_ * 9 + tap_) * 32 + j, h)];                                           \
+        _Pragma("unroll") for (int t_ = 0; t_ < PT; ++t_)                                         \
+            bq[sl][t_] = s_b[c_ * WIN * 2 + swz(q0[t_] + o_, h)];                                 \
+    } while (0)
+            DN_FETCH(0, 0);
+#pragma unroll
+            for (int s = 0; s < 36; ++s) {
+                if (s + 1 < 36) DN_FETCH(s + 1, (s + 1) & 1);
+                acc2[0] = mfma_i8(aw[s & 1], bq[s & 1][0], acc2[0]);
+#pragma unroll
+                for (int t = 1; t < PT; ++t)
+                    if (t < np) acc2[t] = mfma_i8(aw[s & 1], bq[s & 1][t], acc2[t]);
+                __builtin_amdgcn_sched_barrier(0);     // operands one step ahead, no further
+            }
+#undef DN_FETCH
+            // q = RNE(clamp(float(acc) * sc, -127, 127)) into the layer's store slot
+#pragma unroll
+            for (int t = 0; t < PT; ++t) {
+                if (t >= np) break;
+                uint32_t e[4];
+#pragma unroll
+                for (int kk = 0; kk < 4; ++kk) {
+                    uint32_t d = 0;
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const int v = 4 * kk + r;
+                        const float q = __builtin_rintf(__builtin_fminf(
+                            __builtin_fmaxf((float)acc2[t][v] * s_sc[res_row(v, h)], -127.0f), 127.0f));
+                        d |= ((uint32_t)(int)q & 0xffu) << (8 * r);
+                    }
+                    e[kk] = d;
+                }
+                const u32x4 row = xchg_rows(e[0], e[1], e[2], e[3], h);
+                const int p = (wave + NW * t) * 32 + j;
+                const int y = cg.y0 + p / TW, x = cg.x0 + p % TW;
+                if (y < H && x < W)
+                    *(u32x4*)(a.out + (((int64_t)cg.n * H + y) * W + x) * 32 + 16 * h) = row;
+            }
+        }
+
+        if (next >= total) break;
+        __syncthreads();                               // this tile's window is read: LDS free again
+        tile = next;
+        cg = ng;
+        co0 = no0;
+        co1 = no1;
+        next = tile + (int)gridDim.x;
+        ng = dn_geo<TW, TH>(next < total ? next : tile, tiles_x, tiles_y, H, W);
+        no0 = dn_pixel(ng, 32 * wave + j, W, h);
+        if (CPW > 1) no1 = dn_pixel(ng, 32 * (wave + NW) + j, W, h);
+    }
+#undef DN_LOAD_A
+#undef DN_LOAD_B
+}
+
+// ------------------------------------------------------------------------------------------------
+// A whole dense block per image (small maps, H W <= 256): one workgroup of 8 waves per image runs every
+// layer of the block: conv1 of the image's 256 pixels (wave w: pixels 32 w .. 32 w + 31, all 128
+// outputs, the image's store read from global memory, where it stays in L2), the bottleneck into LDS
+// (with a zero-padding ring), conv2 from LDS into the layer's store slot, a barrier, the next layer.
+// No per-layer launches and no bottleneck in memory; the layers of one image depend only on that
+// image, so workgroups never wait for each other.  The layer tables come from a device array of
+// D8sLayerP.  Per layer the first activation groups (the block input, unchanged by the layers) and
+// weights are requested before the layer's tables are staged.
+// ------------------------------------------------------------------------------------------------
+static constexpr int DB_NT = 512;                          // 8 waves: 8 x 32 pixels
+static constexpr size_t DB_PRM = 128 * 4 + 128 * 8 + 32 * 4 + 32 * 4;
+
+static size_t dblock_lds(int H, int W, int Gmax) {
+    return (size_t)(H + 2) * (W + 2) * 128 + DB_PRM + (size_t)Gmax * 128 + 2 * 8 * 4096;
+}
+
+__global__ __launch_bounds__(DB_NT, 1) void k_dblock(D8sBlockArgs a) {
+    __shared__ __attribute__((aligned(16))) u32x4 s_w[2304];              // conv2 weights, 36 KB
+    extern __shared__ __attribute__((aligned(16))) u32x4 s_dyn[];
+    const int H = a.H, W = a.W, HW = H * W, BW = W + 2, WIN = (H + 2) * (W + 2);
+    const int G0 = a.G0, L = a.L, N = a.N;
+    u32x4* s_b = s_dyn;                                                    // [4][WIN][2]
+    int32_t* s_w1sum = (int32_t*)(s_dyn + 8 * WIN);                       // [128]
+    float2* s_gd = (float2*)(s_w1sum + 128);                              // [128]
+    float* s_sc = (float*)(s_gd + 128);                                   // [32]
+    int32_t* s_w2sum = (int32_t*)(s_sc + 32);                             // [32]
+    uint32_t* s_abh = (uint32_t*)(s_w2sum + 32);                          // [Gmax * 32]
+    u32x4* s_wc = (u32x4*)(s_abh + (G0 + L - 1) * 32);                   // [2][8 * 256] weight chunks
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int h = lane >> 5, j = lane & 31;
+    const int n = blockIdx.x;
+
+    // zero-padding ring of the window (the layers write only its interior)
+    {
+        const u32x4 pad = {SIGN4, SIGN4, SIGN4, SIGN4};
+        for (int idx = tid; idx < WIN * 8; idx += DB_NT) {
+            const int wp = idx >> 3, c = (idx >> 1) & 3, hh = idx & 1;
+            const int wy = wp / BW, wx = wp - wy * BW;
+            if (wy == 0 || wy == H + 1 || wx == 0 || wx == W + 1) s_b[c * WIN * 2 + swz(wp, hh)] = pad;
+        }
+    }
+    // the lane's pixel (a repeat of the last one past the image)
+    const int p = 32 * wave + j;
+    const bool live = p < HW;
+    const int pc = live ? p : HW - 1;
+    const int py = pc / W, px = pc - py * W;
+    const uint32_t off = (uint32_t)pc * 32u + 16u * h;
+    const int dst = (py + 1) * BW + px + 1;
+    const int q0 = py * BW + px;                          // the 3 x 3 window's corner
+    const uint8_t* in0 = (const uint8_t*)a.in0 + (int64_t)n * G0 * HW * 32;
+    const uint8_t* segn = (const uint8_t*)a.seg + (int64_t)n * HW * 32;
+    const int64_t slot = (int64_t)N * HW * 32;
+
+    for (int l = 0; l < L; ++l) {
+        const D8sLayerP lp = a.layers[l];
+        const int G = G0 + l;
+        const int nk = G;
+        // conv2 weights and tables (loads first, stores to LDS after the prefetch below is issued)
+        u32x4 wv[5];
+#pragma unroll
+        for (int k = 0; k < 5; ++k) wv[k] = ((const u32x4*)lp.w2)[min(tid + DB_NT * k, 2303)];
+        int32_t t_w1sum = 0, t_w2sum = 0;
+        float2 t_gd = {0.f, 0.f};
+        float t_sc = 0.f;
+        if (tid < 128) {
+            t_w1sum = lp.w1sum[tid];
+            t_gd = ((const float2*)lp.gd)[tid];
+        } else if (tid < 160) {
+            t_sc = lp.sc[tid - 128];
+            t_w2sum = lp.w2sum[tid - 128];
+        }
+        uint32_t t_abh[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) t_abh[k] = ((const uint32_t*)lp.abh)[min(tid + DB_NT * k, G * 32 - 1)];
+        asm volatile("" ::: "memory");                   // the table loads stay ahead in issue order
+
+        // conv1 weights go through LDS in chunks of 8 groups (32 KB, double-buffered): every wave
+        // reads all of them, and from L2 one step ahead they would stall every step
+        const u32x4* w1 = (const u32x4*)lp.w1;
+        const int nch = (G + 7) / 8;
+        u32x4 stg[4];
+#define DB_STAGE_LOAD(c)                                                                          \
+    _Pragma("unroll") for (int u_ = 0; u_ < 4; ++u_)                                              \
+        stg[u_] = w1[min((c) * 2048 + tid + DB_NT * u_, G * 256 - 1)]
+#define DB_STAGE_STORE(c)                                                                         \
+    _Pragma("unroll") for (int u_ = 0; u_ < 4; ++u_) s_wc[((c) & 1) * 2048 + tid + DB_NT * u_] = stg[u_]
+#define DB_SRC(g) ((g) < G0 ? in0 + (int64_t)(g) * HW * 32 + off                                  \
+                            : segn + (int64_t)((g) - G0) * slot + off)
+        u32x4 ra[4];
+        const int klast = nk - 1;
+        DB_STAGE_LOAD(0);
+#pragma unroll
+        for (int s = 0; s < 4; ++s) ra[s] = *(const u32x4*)DB_SRC(s < klast ? s : klast);
+
+#pragma unroll
+        for (int k = 0; k < 5; ++k)
+            if (tid + DB_NT * k < 2304) s_w[swz((tid + DB_NT * k) >> 1, tid & 1)] = wv[k];
+        if (tid < 128) {
+            s_w1sum[tid] = t_w1sum;
+            s_gd[tid] = t_gd;
+        } else if (tid < 160) {
+            s_sc[tid - 128] = t_sc;
+            s_w2sum[tid - 128] = t_w2sum;
+        }
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+            if (tid + DB_NT * k < G * 32) s_abh[tid + DB_NT * k] = t_abh[k];
+        DB_STAGE_STORE(0);
+        __syncthreads();                                 // this layer's tables, weight chunk 0
+
+        // ---- conv1 of the image: acc = 128 sum_k w + sum_k w (u - 128) ----
+        i32x16 acc[4];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+#pragma unroll
+            for (int v = 0; v < 16; ++v) acc[c][v] = 128 * s_w1sum[32 * c + res_row(v, h)];
+        }
+        // step k (group k, the (k % 8)-th of chunk k / 8 in buffer (k / 8) & 1)
+#define DB_STEP(slot, k)                                                                          \
+    do {                                                                                          \
+        const int k_ = (k);                                                                       \
+        const u32x4* wq_ = s_wc + ((k_ >> 3) & 1) * 2048 + (k_ & 7) * 256 + j * 2 + h;            \
+        u32x4 rb_[4];                                                                             \
+        _Pragma("unroll") for (int c_ = 0; c_ < 4; ++c_) rb_[c_] = wq_[64 * c_];                  \
+        const u32x4* pp_ = (const u32x4*)(s_abh + k_ * 32 + h * 16);                              \
+        const u32x4 bx_ = pro16(ra[slot], pp_[0], pp_[1], pp_[2], pp_[3]);                        \
+        ra[slot] = *(const u32x4*)DB_SRC(k_ + 4 < klast ? k_ + 4 : klast);                        \
+        _Pragma("unroll") for (int c_ = 0; c_ < 4; ++c_) acc[c_] = mfma_i8(rb_[c_], bx_, acc[c_]); \
+    } while (0)
+        for (int ch = 0; ch < nch; ++ch) {
+            const int k0 = ch * 8;
+            if (ch + 1 < nch) DB_STAGE_LOAD(ch + 1);
+            DB_STEP(0, k0);
+            if (k0 + 1 < nk) DB_STEP(1, k0 + 1);
+            if (k0 + 2 < nk) DB_STEP(2, k0 + 2);
+            if (k0 + 3 < nk) DB_STEP(3, k0 + 3);
+            if (k0 + 4 < nk) DB_STEP(0, k0 + 4);
+            if (k0 + 5 < nk) DB_STEP(1, k0 + 5);
+            if (k0 + 6 < nk) DB_STEP(2, k0 + 6);
+            if (k0 + 7 < nk) DB_STEP(3, k0 + 7);
+            if (ch + 1 < nch) {
+                DB_STAGE_STORE(ch + 1);                  // its buffer was last read in chunk ch - 1
+                __syncthreads();
+            }
+        }
+#undef DB_STEP
+#undef DB_SRC
+#undef DB_STAGE_STORE
+#undef DB_STAGE_LOAD
+
+        // ---- bottleneck into LDS (v ^ 0x80, the conv2 operand) ----
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            uint32_t e[4];
+#pragma unroll
+            for (int kk = 0; kk < 4; ++kk) {
+                uint32_t d = 0;
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int v = 4 * kk + r;
+                    const float2 prm = s_gd[32 * c + res_row(v, h)];
+                    float y = __builtin_fmaf(prm.x, (float)acc[c][v], prm.y);
+                    y = __builtin_fminf(__builtin_fmaxf(y, 0.0f), 1.0f);
+                    const uint32_t b = __float_as_uint(__builtin_fmaf(y, 255.0f, 8388608.0f)) & 0xffu;
+                    d |= b << (8 * r);
+                }
+                e[kk] = d ^ SIGN4;
+            }
+            const u32x4 row = xchg_rows(e[0], e[1], e[2], e[3], h);
+            if (live) s_b[c * WIN * 2 + swz(dst, h)] = row;
+        }
+        __syncthreads();                                 // the image's bottleneck is in LDS
+
+        // ---- conv2 (3x3, pad 1) from LDS into store slot l ----
+        {
+            i32x16 acc2;
+#pragma unroll
+            for (int v = 0; v < 16; ++v) acc2[v] = 128 * s_w2sum[res_row(v, h)];
+            u32x4 aw[2], bq[2];
+#define DB_FETCH(s, sl)                                                                           \
+    do {                                                                                          \
+        const int c_ = (s) / 9, tap_ = (s) % 9;                                                   \
+        aw[sl] = s_w[swz((c_ * 9 + tap_) * 32 + j, h)];                                           \
+        bq[sl] = s_b[c_ * WIN * 2 + swz(q0 + (tap_ / 3) * BW + (tap_ % 3), h)];                   \
+    } while (0)
+            DB_FETCH(0, 0);
+#pragma unroll
+            for (int s = 0; s < 36; ++s) {
+                if (s + 1 < 36) DB_FETCH(s + 1, (s + 1) & 1);
+                acc2 = mfma_i8(aw[s & 1], bq[s & 1], acc2);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+#undef DB_FETCH
+            uint32_t e[4];
+#pragma unroll
+            for (int kk = 0; kk < 4; ++kk) {
+                uint32_t d = 0;
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int v = 4 * kk + r;
+                    const float q = __builtin_rintf(__builtin_fminf(
+                        __builtin_fmaxf((float)acc2[v] * s_sc[res_row(v, h)], -127.0f), 127.0f));
+                    d |= ((uint32_t)(int)q & 0xffu) << (8 * r);
+                }
+                e[kk] = d;
+            }
+            const u32x4 row = xchg_rows(e[0], e[1], e[2], e[3], h);
+            if (live) *(u32x4*)((uint8_t*)segn + (int64_t)l * slot + off) = row;
+        }
+        // slot l is complete (every wave's stores retired) before any wave's next conv1 reads it,
+        // and LDS is free for the next layer's tables
+        __syncthreads();
     }
 }
 
@@ -924,6 +1657,20 @@ static int conv1_launch(const D8sGemmArgs* a, int32_t* acc, hipStream_t st) {
     const int64_t want = 3 * (int64_t)cu_count() / 2;
     int ks = 1;
     while (ks < 4 && (a->rows + 64 * 4 / ks - 1) / (64 * 4 / ks) < want) ks *= 2;
+    // the persistent form when every wave of a full grid gets several tiles
+    const int64_t ntiles = (a->rows + 63) / 64;
+    const int64_t in0_bytes = (int64_t)a->N * a->G0 * a->HW * 32, slot_bytes = (int64_t)a->rows * 32;
+    if (ks == 1 && ntiles >= 2 * 8 * (int64_t)cu_count() && in0_bytes < (1ll << 32) &&
+        slot_bytes < (1ll << 32)) {
+        const int64_t want_blocks = (ntiles + 3) / 4;
+        const unsigned grid = (unsigned)(want_blocks < 2 * cu_count() ? want_blocks : 2 * cu_count());
+        const size_t shm1 = 128 * 4 + 128 * 8 + (size_t)a->G * 128;
+        if (acc)
+            hipLaunchKernelGGL((k_conv1p<true>), dim3(grid), dim3(256), shm1, st, *a, acc);
+        else
+            hipLaunchKernelGGL((k_conv1p<false>), dim3(grid), dim3(256), shm1, st, *a, nullptr);
+        return launched("d8s_conv1");
+    }
     const int px = 64 * 4 / ks;
     const unsigned blocks = (unsigned)((a->rows + px - 1) / px);
     size_t shm = (size_t)a->G * 128;
@@ -984,6 +1731,59 @@ extern "C" int d8s_conv2(const D8sConv2Args* a, void* stream) {
     if (a->W >= 4) return conv2_launch<4, 16, 4, 2>(a, st, 0);
     if (a->W >= 2) return conv2_launch<2, 32, 4, 2>(a, st, 0);
     return conv2_launch<1, 64, 4, 2>(a, st, 0);
+}
+
+template <int TW, int TH, int CPW, int NW>
+static int dense_launch(const D8sDenseArgs* a, hipStream_t st) {
+    using SL = DnShape<TW, TH, CPW, NW, true>;
+    using S = DnShape<TW, TH, CPW, NW, false>;
+    const int wh = a->H < TH + 2 ? a->H : TH + 2, ww = a->W < TW + 2 ? a->W : TW + 2;
+    REQUIRE(wh * ww <= 32 * NW * CPW, "d8s_dense: window larger than the workgroup's column blocks");
+    REQUIRE(S::lds(a->G) + 36864 <= 160 * 1024, "d8s_dense: too many groups for LDS");
+    const bool wl = SL::lds(a->G) + 36864 <= 160 * 1024;   // conv1 weights fit in LDS too
+    const int tiles_x = (a->W + TW - 1) / TW, tiles_y = (a->H + TH - 1) / TH;
+    const int64_t total = (int64_t)a->N * tiles_x * tiles_y;
+    REQUIRE(total < (1ll << 31), "d8s_dense: too many tiles");
+    const unsigned grid = (unsigned)(total < cu_count() ? total : cu_count());
+    if (wl)
+        hipLaunchKernelGGL((k_dense<TW, TH, CPW, NW, true>), dim3(grid), dim3(S::NT), SL::lds(a->G), st,
+                           *a, tiles_x, tiles_y);
+    else
+        hipLaunchKernelGGL((k_dense<TW, TH, CPW, NW, false>), dim3(grid), dim3(S::NT), S::lds(a->G), st,
+                           *a, tiles_x, tiles_y);
+    return launched("d8s_dense");
+}
+
+extern "C" int d8s_dense(const D8sDenseArgs* a, void* stream) {
+    REQUIRE(a != nullptr, "d8s_dense: null arguments");
+    REQUIRE(a->in0 && a->w1 && a->abh && a->gd && a->w1sum && a->w2 && a->sc && a->w2sum && a->out,
+            "d8s_dense: null pointer");
+    REQUIRE(a->G0 >= 1 && a->G >= 1 && a->N >= 1 && a->H >= 1 && a->W >= 1,
+            "d8s_dense: G0, G, N, H, W must be >= 1");
+    REQUIRE(a->G <= a->G0 || a->seg != nullptr, "d8s_dense: seg is null with G > G0");
+    REQUIRE(a->G <= 512, "d8s_dense: more than 512 groups");
+    REQUIRE((int64_t)a->H * a->W <= (1 << 26), "d8s_dense: more than 2^26 pixels per image");
+    hipStream_t st = (hipStream_t)stream;
+    if (a->W >= 32) return dense_launch<32, 12, 2, 8>(a, st);
+    if (a->W <= 16 && a->H <= 16) return dense_launch<16, 16, 1, 8>(a, st);
+    return dense_launch<16, 12, 1, 8>(a, st);
+}
+
+static int dblock_launch(const D8sBlockArgs* a, hipStream_t st) {
+    REQUIRE(a != nullptr, "d8s_dense_block: null arguments");
+    REQUIRE(a->in0 && a->layers && (a->L <= 0 || a->seg), "d8s_dense_block: null pointer");
+    REQUIRE(a->G0 >= 1 && a->L >= 1 && a->N >= 1 && a->H >= 1 && a->W >= 1,
+            "d8s_dense_block: G0, L, N, H, W must be >= 1");
+    REQUIRE(a->H * a->W <= DB_NT / 2, "d8s_dense_block: more than 256 pixels per image");
+    REQUIRE(a->G0 + a->L - 1 <= 4 * DB_NT / 32, "d8s_dense_block: more than 64 groups");
+    const size_t shm = dblock_lds(a->H, a->W, a->G0 + a->L - 1);
+    REQUIRE(shm + 36864 <= 160 * 1024, "d8s_dense_block: block too large for LDS");
+    hipLaunchKernelGGL(k_dblock, dim3((unsigned)a->N), dim3(DB_NT), shm, st, *a);
+    return launched("d8s_dense_block");
+}
+
+extern "C" int d8s_dense_block(const D8sBlockArgs* a, void* stream) {
+    return dblock_launch(a, (hipStream_t)stream);
 }
 
 template <int NT, int PT>

@@ -441,6 +441,45 @@ def _src_key(x: torch.Tensor) -> tuple:
     return root, (id(root), x.data_ptr(), ver, tuple(x.shape), tuple(x.stride()))
 
 
+class Layer(collections.namedtuple("Layer", "c1 c2 dense")):
+    """The launches of one dense layer: conv1 and conv2 argument structs, and the fused layer's
+    (`hip.DenseArgs`, None when the block runs the two launches)."""
+
+
+# How a block's layers run: "conv" conv1 + conv2 per layer (d8s_conv1, d8s_conv2); "tile" one fused
+# launch per layer (d8s_dense, the reference's fused kind "tile"); "img" the whole block in one launch,
+# a workgroup per image (d8s_dense_block, the reference's "img*" kinds).  The bytes are the same.
+BLOCK_KINDS = ("conv", "tile", "img")
+IMG_MAX_PX = 256                # d8s_dense_block: pixels per image
+IMG_MAX_GROUPS = 64             # and groups read by the last layer
+
+
+def img_fits(b: dict) -> bool:
+    """Whether block `b` (meta) fits d8s_dense_block."""
+    return b["h"] * b["w"] <= IMG_MAX_PX and b["c0"] // GROUP + b["L"] - 1 <= IMG_MAX_GROUPS
+
+
+def fused_blocks(meta: dict, fused=None) -> dict:
+    """{block: kind} for every block.  `fused` None -> the default: "img" where the block fits it (the
+    16 x 16 maps: one launch instead of 64, no bottleneck in memory), else "conv"; a dict {block: kind}
+    (other blocks "conv"); an iterable of blocks -> "tile" for those."""
+    nb = len(meta["blocks"])
+    if fused is None:
+        return {bi: ("img" if img_fits(b) else "conv") for bi, b in enumerate(meta["blocks"])}
+    req = dict(fused) if isinstance(fused, dict) else {int(b): "tile" for b in fused}
+    out = {bi: "conv" for bi in range(nb)}
+    for bi, kind in req.items():
+        bi = int(bi)
+        if not 0 <= bi < nb:
+            raise ValueError(f"fused block {bi}: the encoder has blocks 0..{nb - 1}")
+        if kind not in BLOCK_KINDS:
+            raise ValueError(f"block kind {kind!r}: expected one of {BLOCK_KINDS}")
+        if kind == "img" and not img_fits(meta["blocks"][bi]):
+            raise ValueError(f"block {bi} does not fit the whole-block kernel")
+        out[bi] = kind
+    return out
+
+
 def _ptr(t: torch.Tensor | None) -> int:
     return 0 if t is None else int(t.data_ptr())
 
@@ -455,11 +494,13 @@ class Dense8SEncoder:
     images, then the same images mirrored (flip TTA fused in the stem: no mirrored copy in memory).
     """
 
-    def __init__(self, pack: dict, dev: int, n_total: int, max_inflight: int | None = None) -> None:
+    def __init__(self, pack: dict, dev: int, n_total: int, max_inflight: int | None = None,
+                 fused=None) -> None:
         t0 = time.perf_counter()
         meta = pack["meta"]
         validate_meta(meta)
         self.meta, self.dev = meta, int(dev)
+        self.fused = fused_blocks(meta, fused)
         self.nb = int(meta["n"])
         self.n_out = -(-int(n_total) // self.nb) * self.nb
         self.max_inflight = max_inflight
@@ -507,6 +548,7 @@ class Dense8SEncoder:
         dev = torch.device(d)
         self.par = {k: torch.from_numpy(np.ascontiguousarray(v)).to(dev)
                     for k, v in par.items() if k not in ("S_w0", "S_b0", "S_w8f")}
+        self.out_dev = dev
         self._build_launches()
 
     def _needed_tables(self) -> list[str]:
@@ -523,6 +565,8 @@ class Dense8SEncoder:
         n, P = self.nb, lambda k: _ptr(self.par[k])  # noqa: E731
         meta = self.meta
         self.plan_l: list = []
+        self.block_args: dict = {}                   # "img" blocks: their launch
+        self._tables: dict = {}                      # and their device layer tables
         for bi, b in enumerate(meta["blocks"]):
             hw, g0 = b["h"] * b["w"], b["c0"] // GROUP
             layers = []
@@ -533,7 +577,24 @@ class Dense8SEncoder:
                 c2 = hip.Conv2Args(_ptr(self.bott), P(f"L{bi}_{li}_w2k"), P(f"L{bi}_{li}_c2u"),
                                    P(f"L{bi}_{li}_w2sum"), self.seg[bi] + li * n * hw * GROUP,
                                    n, b["h"], b["w"], 0)
-                layers.append((c1, c2))
+                dn = None
+                if self.fused[bi] == "tile":
+                    dn = hip.DenseArgs(self.in0[bi], self.seg[bi], P(f"L{bi}_{li}_w1"),
+                                       P(f"L{bi}_{li}_abh"), P(f"L{bi}_{li}_gdu"), P(f"L{bi}_{li}_w1sum"),
+                                       P(f"L{bi}_{li}_w2k"), P(f"L{bi}_{li}_c2u"), P(f"L{bi}_{li}_w2sum"),
+                                       self.seg[bi] + li * n * hw * GROUP, g0, g0 + li, n, b["h"],
+                                       b["w"], 0)
+                layers.append(Layer(c1, c2, dn))
+            if self.fused[bi] == "img":
+                lps = (hip.LayerP * b["L"])()
+                for li in range(b["L"]):
+                    lps[li] = hip.LayerP(P(f"L{bi}_{li}_w1"), P(f"L{bi}_{li}_abh"), P(f"L{bi}_{li}_gdu"),
+                                         P(f"L{bi}_{li}_w1sum"), P(f"L{bi}_{li}_w2k"), P(f"L{bi}_{li}_c2u"),
+                                         P(f"L{bi}_{li}_w2sum"))
+                table = torch.frombuffer(bytearray(bytes(lps)), dtype=torch.uint8).to(self.out_dev)
+                self._tables[bi] = table
+                self.block_args[bi] = hip.BlockArgs(self.in0[bi], self.seg[bi], _ptr(table), n, b["h"],
+                                                    b["w"], g0, b["L"], 0)
             trans = None
             if b["trans"]:
                 cout = (b["c0"] + GROWTH * b["L"]) // 2
@@ -578,6 +639,12 @@ class Dense8SEncoder:
     def _conv2(self, c2, st: int) -> None:
         hip.check(self.lib.d8s_conv2(ctypes.byref(c2), st), "d8s_conv2")
 
+    def _block(self, bi: int, st: int) -> None:
+        hip.check(self.lib.d8s_dense_block(ctypes.byref(self.block_args[bi]), st), "d8s_dense_block")
+
+    def _dense(self, d, st: int) -> None:
+        hip.check(self.lib.d8s_dense(ctypes.byref(d), st), "d8s_dense")
+
     def _trans(self, t, st: int) -> None:
         hip.check(self.lib.d8s_transition(ctypes.byref(t), st), "d8s_transition")
 
@@ -591,10 +658,18 @@ class Dense8SEncoder:
         self._stem(x_ptr, mode, st)
         mark("stem")
         for bi, (layers, trans) in enumerate(self.plan_l):
-            for c1, c2 in layers:
-                self._conv1(c1, st)
+            if bi in self.block_args:
+                self._block(bi, st)
+                mark(f"block_{bi}")
+                layers = ()
+            for L in layers:
+                if L.dense is not None:
+                    self._dense(L.dense, st)
+                    mark(f"dense_{bi}")
+                    continue
+                self._conv1(L.c1, st)
                 mark(f"conv1_{bi}")
-                self._conv2(c2, st)
+                self._conv2(L.c2, st)
                 mark(f"conv2_{bi}")
             if trans is not None:
                 self._trans(trans, st)
@@ -780,11 +855,20 @@ class Dense8SEncoder:
             for bi, (layers, trans) in enumerate(self.plan_l):
                 self.stream.synchronize()
                 out[(bi, 0)] = self.store(bi, 0).clone()
-                for li, (c1, c2) in enumerate(layers):
-                    self._conv1(c1, st)
+                if bi in self.block_args:                    # every layer in one launch
+                    self._block(bi, st)
                     self.stream.synchronize()
-                    out[("bott", bi, li)] = self.bottleneck(bi).clone()
-                    self._conv2(c2, st)
+                    for li in range(len(layers)):
+                        out[(bi, li + 1)] = self.store(bi, li + 1).clone()
+                    layers = ()
+                for li, L in enumerate(layers):
+                    if L.dense is not None:                  # no bottleneck in memory
+                        self._dense(L.dense, st)
+                    else:
+                        self._conv1(L.c1, st)
+                        self.stream.synchronize()
+                        out[("bott", bi, li)] = self.bottleneck(bi).clone()
+                        self._conv2(L.c2, st)
                     self.stream.synchronize()
                     out[(bi, li + 1)] = self.store(bi, li + 1).clone()
                 if trans is not None:
@@ -823,11 +907,18 @@ class Dense8SEncoder:
         xf = self._padded(x[:self._per_pass(mode)].contiguous(), mode)
         st = self.stream.cuda_stream
         fams: dict[str, list] = {"stem": [lambda: self._stem(xf.data_ptr(), mode, st)],
-                                 "conv1": [], "conv2": [], "trans": [], "final": []}
+                                 "conv1": [], "conv2": [], "dense": [], "block": [], "trans": [],
+                                 "final": []}
         for bi, (layers, trans) in enumerate(self.plan_l):
-            for c1, c2 in layers:
-                fams["conv1"].append(lambda c=c1: self._conv1(c, st))
-                fams["conv2"].append(lambda c=c2: self._conv2(c, st))
+            if bi in self.block_args:
+                fams["block"].append(lambda b=bi: self._block(b, st))
+                layers = ()
+            for L in layers:
+                if L.dense is not None:
+                    fams["dense"].append(lambda d=L.dense: self._dense(d, st))
+                    continue
+                fams["conv1"].append(lambda c=L.c1: self._conv1(c, st))
+                fams["conv2"].append(lambda c=L.c2: self._conv2(c, st))
             if trans is not None:
                 fams["trans"].append(lambda t=trans: self._trans(t, st))
             else:
@@ -835,7 +926,7 @@ class Dense8SEncoder:
         with torch.cuda.device(self.dev), torch.cuda.stream(self.stream):
             self.stream.wait_stream(torch.cuda.current_stream(self.dev))
             self._pass(xf.data_ptr(), self.out.data_ptr(), mode)
-            out = {k: self._time(lambda fs=fs: [f() for f in fs], reps) for k, fs in fams.items()}
+            out = {k: self._time(lambda fs=fs: [f() for f in fs], reps) for k, fs in fams.items() if fs}
         return {k: round(v, 4) for k, v in out.items()}
 
     def _time(self, fn, reps: int = 20) -> float:
@@ -860,9 +951,15 @@ class Dense8SEncoder:
         st = self.stream.cuda_stream
         out: dict = {}
         for bi, (layers, trans) in enumerate(self.plan_l):
-            for li, (c1, c2) in enumerate(layers):
-                out[f"c1 b{bi}l{li}"] = round(self._time(lambda c=c1: self._conv1(c, st), reps), 4)
-                out[f"c2 b{bi}l{li}"] = round(self._time(lambda c=c2: self._conv2(c, st), reps), 4)
+            if bi in self.block_args:
+                out[f"blk b{bi}"] = round(self._time(lambda b=bi: self._block(b, st), reps), 4)
+                layers = ()
+            for li, L in enumerate(layers):
+                if L.dense is not None:
+                    out[f"dn b{bi}l{li}"] = round(self._time(lambda d=L.dense: self._dense(d, st), reps), 4)
+                    continue
+                out[f"c1 b{bi}l{li}"] = round(self._time(lambda c=L.c1: self._conv1(c, st), reps), 4)
+                out[f"c2 b{bi}l{li}"] = round(self._time(lambda c=L.c2: self._conv2(c, st), reps), 4)
             if trans is not None:
                 out[f"t{bi}"] = round(self._time(lambda t=trans: self._trans(t, st), reps), 4)
         return out

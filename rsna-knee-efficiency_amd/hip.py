@@ -52,6 +52,27 @@ class Conv2Args(ctypes.Structure):
                 ("H", i32), ("W", i32), ("pad_", i32)]
 
 
+class DenseArgs(ctypes.Structure):
+    """`D8sDenseArgs`: a dense layer with conv1 and conv2 fused (the reference's `TileArg` + `LayerP`,
+    `src/knee/dense8s.py:139-152`)."""
+    _fields_ = [("in0", u64), ("seg", u64), ("w1", u64), ("abh", u64), ("gd", u64), ("w1sum", u64),
+                ("w2", u64), ("sc", u64), ("w2sum", u64), ("out", u64), ("G0", i32), ("G", i32),
+                ("N", i32), ("H", i32), ("W", i32), ("pad_", i32)]
+
+
+class LayerP(ctypes.Structure):
+    """`D8sLayerP`: one layer's tables for d8s_dense_block (the reference's `LayerP`,
+    `src/knee/dense8s.py:139-143`, plus the weight sums)."""
+    _fields_ = [("w1", u64), ("abh", u64), ("gd", u64), ("w1sum", u64), ("w2", u64), ("sc", u64),
+                ("w2sum", u64)]
+
+
+class BlockArgs(ctypes.Structure):
+    """`D8sBlockArgs`: a whole dense block (the reference's `ImgArg`, `src/knee/dense8s.py:155-159`)."""
+    _fields_ = [("in0", u64), ("seg", u64), ("layers", u64), ("N", i32), ("H", i32), ("W", i32),
+                ("G0", i32), ("L", i32), ("pad_", i32)]
+
+
 class StemArgs(ctypes.Structure):
     """`D8sStemArgs`: the stem with the fused uint8 normalisation / flip of the input."""
     _fields_ = [("x", u64), ("lut", u64), ("w16", u64), ("bias", u64), ("inv", u64), ("out", u64),
@@ -65,6 +86,8 @@ SIGNATURES = {
     "d8s_conv1": [ctypes.POINTER(GemmArgs), vp],
     "d8s_conv1_acc32": [ctypes.POINTER(GemmArgs), vp, vp],
     "d8s_conv2": [ctypes.POINTER(Conv2Args), vp],
+    "d8s_dense": [ctypes.POINTER(DenseArgs), vp],
+    "d8s_dense_block": [ctypes.POINTER(BlockArgs), vp],
     "d8s_transition": [ctypes.POINTER(GemmArgs), vp],
     "d8s_final": [vp, i32, vp, i32, i32, vp, vp, i32, vp],
     "d8s_stem": [ctypes.POINTER(StemArgs), vp],

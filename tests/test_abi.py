@@ -42,6 +42,10 @@ def test_struct_layouts_match_header(tmp_path):
         " offsetof(D8sConv2Args, W));\n"
         '  printf("%zu %zu %zu\\n", sizeof(D8sStemArgs), offsetof(D8sStemArgs, out),'
         " offsetof(D8sStemArgs, flip));\n"
+        '  printf("%zu %zu %zu %zu\\n", sizeof(D8sDenseArgs), offsetof(D8sDenseArgs, w2),'
+        " offsetof(D8sDenseArgs, out), offsetof(D8sDenseArgs, W));\n"
+        '  printf("%zu %zu %zu %zu\\n", sizeof(D8sBlockArgs), offsetof(D8sBlockArgs, layers),'
+        " offsetof(D8sBlockArgs, L), sizeof(D8sLayerP));\n"
         "  return 0; }\n")
     exe = tmp_path / "layout"
     subprocess.run(["gcc", f"-I{hip.HEADER.parent}", str(prog), "-o", str(exe)], check=True)
@@ -51,6 +55,10 @@ def test_struct_layouts_match_header(tmp_path):
     assert got[0] == [ctypes.sizeof(G), G.wsum.offset, G.out.offset, G.G0n.offset]
     assert got[1] == [ctypes.sizeof(C), C.out.offset, C.W.offset]
     assert got[2] == [ctypes.sizeof(S), S.out.offset, S.flip.offset]
+    D = hip.DenseArgs
+    assert got[3] == [ctypes.sizeof(D), D.w2.offset, D.out.offset, D.W.offset]
+    B = hip.BlockArgs
+    assert got[4] == [ctypes.sizeof(B), B.layers.offset, B.L.offset, ctypes.sizeof(hip.LayerP)]
 
 
 @pytest.mark.parametrize("name,args", [
@@ -59,6 +67,14 @@ def test_struct_layouts_match_header(tmp_path):
     ("d8s_transition", lambda: (ctypes.byref(hip.GemmArgs(1, 1, 1, 1, 1, 1, 1, 2, 3, 1, 16, 4, 16,
                                                           48, 1)), None)),
     ("d8s_conv2", lambda: (ctypes.byref(hip.Conv2Args(1, 1, 1, 1, 1, 0, 4, 4, 0)), None)),
+    ("d8s_dense", lambda: (None, None)),
+    ("d8s_dense_block", lambda: (None, None)),
+    ("d8s_dense_block", lambda: (ctypes.byref(hip.BlockArgs(1, 1, 1, 2, 32, 32, 4, 3, 0)), None)),
+    ("d8s_dense_block", lambda: (ctypes.byref(hip.BlockArgs(1, 1, 1, 2, 16, 16, 60, 8, 0)), None)),
+    ("d8s_dense", lambda: (ctypes.byref(hip.DenseArgs(1, 0, 1, 1, 1, 1, 1, 1, 1, 1, 2, 3, 1, 8, 8, 0)),
+                           None)),
+    ("d8s_dense", lambda: (ctypes.byref(hip.DenseArgs(1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 2, 600, 1, 8, 8,
+                                                      0)), None)),
     ("d8s_stem", lambda: (ctypes.byref(hip.StemArgs(1, 0, 1, 1, 1, 1, 1, 8, 8, 1, 0, 0)), None)),
     ("d8s_stem", lambda: (ctypes.byref(hip.StemArgs(1, 1, 1, 1, 1, 1, 3, 8, 8, 1, 2, 0)), None)),
     ("d8s_final", lambda: (1, 20, 1, 2, 256, 1, 1, 100, None)),

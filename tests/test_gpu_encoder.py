@@ -50,8 +50,11 @@ def test_encoder512_layers_exact(dev, study512):
     par = dense8s.kernel_params(study512["plan"])
     res = checks.summarize(checks.check_trace(enc, trace, feats, par, max_rows=1024))
     print(res)
-    assert res["conv1"]["mismatch"] == 0 and res["conv1"]["launches"] == 82, res
-    assert res["conv2"]["mismatch"] == 0 and res["conv2"]["launches"] == 82, res
+    blocks = study512["pack"]["meta"]["blocks"]
+    n_fused = sum(blocks[bi]["L"] for bi, kind in enc.fused.items() if kind != "conv")
+    assert res["conv1"]["mismatch"] == 0 and res["conv1"]["launches"] == 82 - n_fused, res
+    assert res["conv2"]["mismatch"] == 0 and res["conv2"]["launches"] == 82 - n_fused, res
+    assert res["dense"]["mismatch"] == 0 and res["dense"]["launches"] == n_fused, res
     assert res["trans"]["mismatch"] == 0 and res["trans"]["launches"] == 3, res
     assert res["final"]["equal"], res
     lut = dense8s.input_lut([0.5] * 3, [0.25] * 3)
@@ -166,3 +169,21 @@ def test_two_encoders_concurrent_streams(dev, study512):
             torch.cuda.synchronize(dev)
             assert torch.equal(got[0], want[k % 2]) and torch.equal(got[1], want[k % 2]), (graphs, k)
     assert dense8s.encode_concurrent([]) == []
+
+
+def test_fused_blocks_same_bytes(dev, study512):
+    """Every way of running the blocks (two launches per layer, one fused launch per layer, the whole
+    16 x 16 block in one launch) gives the same features (config 4)."""
+    enc, x = study512["enc"], study512["xd"]
+    want = enc(x).clone()
+    for fused in ({}, {0: "tile", 1: "tile", 2: "tile", 3: "tile"}, {3: "img"}, {1: "tile", 3: "conv"}):
+        other = dense8s.Dense8SEncoder(study512["pack"], dev.index or 0, 24, fused=fused)
+        assert all(other.fused[bi] == fused.get(bi, "conv") for bi in range(4))
+        got = other(x).clone()
+        assert torch.equal(got, want), fused
+        other.capture(24)
+        got = other(x).clone()
+        assert torch.equal(got, want), fused
+    for bad in ({4: "tile"}, {0: "img"}, {1: "fast"}):
+        with pytest.raises(ValueError):
+            dense8s.Dense8SEncoder(study512["pack"], dev.index or 0, 24, fused=bad)

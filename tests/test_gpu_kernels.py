@@ -6,6 +6,7 @@ fp32 epilogues); the stem (fp32 sums in the MFMA's order) within 1 LSB with < 1e
 from __future__ import annotations
 
 import ctypes
+import dataclasses
 
 import numpy as np
 import pytest
@@ -69,9 +70,10 @@ def test_conv1_config2(dev, S, C):
     assert 0.0 < zero < 0.9 and sat < 0.5, (zero, sat)
 
 
-@pytest.mark.parametrize("S,C,N", [(64, 320, 12), (8, 96, 3), (2, 64, 1)])
+@pytest.mark.parametrize("S,C,N", [(64, 320, 12), (8, 96, 3), (2, 64, 1), (100, 96, 30), (128, 32, 16)])
 def test_conv1_ks_variants(dev, S, C, N):
-    """Pixel counts that select the 2-slice and 4-slice k-split and ragged last workgroups."""
+    """Pixel counts that select the 2-slice and 4-slice k-split, the persistent form (a ragged last
+    tile; a single group) and ragged last workgroups."""
     c = cases.gemm_case(S, C, N=N, seed=17)
     acc, byt = checks.run_conv1(c, dev)
     acc_x, byt_x = checks.exact_conv1(c)
@@ -105,6 +107,80 @@ def test_conv2_tile_variants(dev, N, H, W):
     _, q_x = checks.exact_conv2(c)
     assert np.array_equal(got, q_x), checks.bytes_cmp(got, q_x)
     assert np.all(others == 0x5A)
+
+
+@pytest.mark.parametrize("H,W,C,c0,N", [
+    (128, 128, 224, 64, 2),      # block 1 geometry, wide tiles, 7 groups
+    (64, 64, 480, 128, 3),       # block 2
+    (32, 32, 1248, 256, 4),      # block 3
+    (16, 16, 1632, 640, 6),      # block 4: one tile per image
+    (16, 16, 64, 64, 2),         # 2 groups: padded K steps
+    (40, 24, 96, 64, 3),         # narrow, height not a multiple of the tile
+    (20, 12, 160, 64, 2),
+    (33, 70, 128, 64, 2),        # wide, ragged in both directions
+    (5, 7, 64, 32, 3),           # tiny
+])
+def test_dense_layer(dev, H, W, C, c0, N):
+    """d8s_dense (conv1 + conv2 fused, bottleneck in LDS): the bytes of the exact conv1 -> conv2 and of
+    the two-launch path d8s_conv1 + d8s_conv2, written into its slot only."""
+    c = cases.gemm_case(H, C, N=N, seed=41, W=W)
+    g0 = c0 // 32
+    in0, seg = cases.store_from_q(c.q, g0)
+    c = dataclasses.replace(c, G0=g0, in0=in0, seg=seg)
+    c2 = cases.conv2_case(H, N=N, seed=43, W=W)
+    print(f"dense H={H} W={W} C_in={C} G0={g0} G={c.G} N={N}", flush=True)
+    got, others = checks.run_dense(c, c2, dev)
+    want = checks.exact_dense(c, c2)
+    assert np.array_equal(got, want), checks.bytes_cmp(got, want)
+    assert np.all(others == 0x5A)
+    _, bott = checks.run_conv1(c, dev, acc32=False)
+    v = np.ascontiguousarray(bott.reshape(N, H, W, 128).transpose(0, 3, 1, 2))
+    planar = np.ascontiguousarray(bott.reshape(-1, 4, 32).transpose(1, 0, 2))
+    got2, _ = checks.run_conv2(cases.Conv2Case(H, N, v, planar, c2.w2, c2.w2k, c2.sc), dev)
+    assert np.array_equal(got, got2)
+    assert float((np.abs(want) == 127).mean()) < 0.9 and float((want == 0).mean()) < 0.9
+
+
+@pytest.mark.parametrize("H,W,c0,L,N", [(16, 16, 640, 32, 3), (16, 16, 64, 3, 2), (7, 9, 96, 5, 3),
+                                         (12, 20, 256, 4, 2)])
+def test_dense_block(dev, H, W, c0, L, N):
+    """d8s_dense_block (every layer of a block, a workgroup per image) against the oracle layer by
+    layer on its own outputs, and against the two-launch path."""
+    import dataclasses as dc
+    C = c0 + 32 * L
+    base = cases.gemm_case(H, C, N=N, seed=51, W=W)       # block input: the first c0 channels
+    g0 = c0 // 32
+    in0 = np.ascontiguousarray(cases.store_from_q(base.q, g0)[0])
+    rng = np.random.default_rng([H, W, L])
+    layers, dev_tabs = [], []
+    for li in range(L):
+        cl = cases.gemm_case(H, c0 + 32 * li, N=1, seed=60 + li, W=W)     # tables of layer li
+        c2 = cases.conv2_case(4, N=1, seed=70 + li)
+        layers.append((cl, c2))
+    t = lambda a: _t(a, dev)                                             # noqa: E731
+    tabs = []
+    for cl, c2 in layers:
+        tt = [t(cl.w1), t(cl.abh), t(cl.gd), t(cl.w1.astype(np.int64).sum(axis=(0, 2)).astype(np.int32)),
+              t(c2.w2k), t(c2.sc), t(c2.w2k.astype(np.int64).sum(axis=(0, 1, 3)).astype(np.int32))]
+        tabs.append(tt)
+    lp = (hip.LayerP * L)(*[hip.LayerP(*[x.data_ptr() for x in tt]) for tt in tabs])
+    table = torch.frombuffer(bytearray(bytes(lp)), dtype=torch.uint8).to(dev)
+    d_in0 = t(in0)
+    seg = torch.full((L * N * H * W * 32,), 0x5A, dtype=torch.int8, device=dev)
+    args = hip.BlockArgs(d_in0.data_ptr(), seg.data_ptr(), table.data_ptr(), N, H, W, g0, L, 0)
+    print(f"dense_block H={H} W={W} c0={c0} L={L} N={N}", flush=True)
+    hip.call("d8s_dense_block", ctypes.byref(args), torch.cuda.current_stream(dev).cuda_stream)
+    torch.cuda.synchronize(dev)
+    got = seg.cpu().numpy().reshape(L, N * H * W, 32)
+    # layer by layer: the exact conv1 -> conv2 of layer li on the block's own outputs so far
+    for li, (cl, c2) in enumerate(layers):
+        q = np.concatenate([in0.transpose(0, 1, 3, 2).reshape(N, c0, H * W)] +
+                           [got[k].reshape(N, H * W, 32).transpose(0, 2, 1) for k in range(li)], axis=1)
+        i_, s_ = cases.store_from_q(q, g0)
+        c = dc.replace(cl, N=N, G0=g0, G=g0 + li, in0=i_, seg=s_, q=q)
+        want = checks.exact_dense(c, c2)
+        assert np.array_equal(got[li], want), (li, checks.bytes_cmp(got[li], want))
+    del rng
 
 
 @pytest.mark.parametrize("S,C,c0", [(128, 256, 64), (64, 512, 128), (32, 1280, 256), (16, 128, 64)])
