@@ -58,9 +58,11 @@ DEV uint32_t pack_low_bytes(uint32_t lo, uint32_t hi) { return perm(hi, lo, 0x06
 
 // fp16 prologue of 4 store bytes (4 consecutive channels): q -> u = RNE(255 sat(fp16(A q + B))).
 // The byte q + 128 goes into the mantissa of fp16 1024 (exact 1024 + 128 + q), -1152 leaves q exactly,
-// one fused fp16 fma with saturation gives v, and fma(v, 255, 1024) = 1024 + RNE(255 v) (ulp 1 in
-// [1024, 2048)): u is the low byte of each half.  (a01, b01) are the fp16 pairs (A, B) of channels
-// 0-1, (a23, b23) of channels 2-3.  Returns the halves 1024 + u for channels (0, 1) and (2, 3).
+// one fused fp16 fma with saturation gives v, and fma(v, 255, 1152) = 1152 + RNE(255 v) (ulp 1 in
+// [1024, 2048); a tie goes to the even sum, i.e. to the even u, 1152 being even): the low byte of each
+// half is u + 128 mod 256 = u ^ 0x80, the MFMA operand u - 128 as a signed byte.  (a01, b01) are the
+// fp16 pairs (A, B) of channels 0-1, (a23, b23) of channels 2-3.  Returns the halves 1152 + u for
+// channels (0, 1) and (2, 3).
 // Same roundings as the reference's `pro4h` (src/knee/dense8s_kernels.cu:122-139) and its emulation
 // `emulate(f16_layers)` (src/knee/dense8s.py:584-587).
 DEV void pro4_halves(uint32_t x, uint32_t a01, uint32_t b01, uint32_t a23, uint32_t b23,
@@ -72,20 +74,20 @@ DEV void pro4_halves(uint32_t x, uint32_t a01, uint32_t b01, uint32_t a23, uint3
     const f16x2 zero = {(_Float16)0.0f, (_Float16)0.0f};
     const f16x2 one = {(_Float16)1.0f, (_Float16)1.0f};
     const f16x2 k255 = {(_Float16)255.0f, (_Float16)255.0f};
-    const f16x2 k1024 = {(_Float16)1024.0f, (_Float16)1024.0f};
+    const f16x2 k1152 = {(_Float16)1152.0f, (_Float16)1152.0f};
     f16x2 vl = __builtin_elementwise_fma(as_h2(lo) + m1152, as_h2(a01), as_h2(b01));
     f16x2 vh = __builtin_elementwise_fma(as_h2(hi) + m1152, as_h2(a23), as_h2(b23));
     vl = __builtin_elementwise_min(__builtin_elementwise_max(vl, zero), one);
     vh = __builtin_elementwise_min(__builtin_elementwise_max(vh, zero), one);
-    rl = h2_bits(__builtin_elementwise_fma(vl, k255, k1024));
-    rh = h2_bits(__builtin_elementwise_fma(vh, k255, k1024));
+    rl = h2_bits(__builtin_elementwise_fma(vl, k255, k1152));
+    rh = h2_bits(__builtin_elementwise_fma(vh, k255, k1152));
 }
 
 // The prologue of 4 store bytes as the MFMA operand: 4 bytes u - 128.
 DEV uint32_t pro4(uint32_t x, uint32_t a01, uint32_t b01, uint32_t a23, uint32_t b23) {
     uint32_t rl, rh;
     pro4_halves(x, a01, b01, a23, b23, rl, rh);
-    return pack_low_bytes(rl, rh) ^ SIGN4;
+    return pack_low_bytes(rl, rh);
 }
 
 // 16 channels: x = 4 store dwords, p = 16 parameter dwords (A01, B01, A23, B23 per store dword).
@@ -337,13 +339,22 @@ DEV void c1p_pixels(int t, int j, int h, int64_t rows, int64_t HW, int G0, uint3
     s1 = (uint32_t)((n1 * HW + p1) * 32 + 16 * h);
 }
 
-template <bool ACC32>
+// LDS of k_conv1p: tables, prologue table, the layer's weights (WM 1) or two 4-group chunks (WM 2)
+static size_t c1p_lds(int G, int wm) {
+    return 128 * 4 + 128 * 8 + (size_t)G * 128 + (wm == 1 ? (size_t)G * 4096 : 2 * 4 * 4096);
+}
+
+// WM: where the conv1 weights are read from.  1: all of the layer's in LDS, loaded once; 2: 4-group
+// chunks staged through LDS (double-buffered, one barrier per 4 steps; the waves of a workgroup run
+// in step).  From L2 one step ahead they would stall the steps once the layer no longer fits L1.
+template <bool ACC32, int WM>
 __global__ __launch_bounds__(256, 2) void k_conv1p(D8sGemmArgs a, int32_t* __restrict__ acc_out) {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     int32_t* s_wsum = (int32_t*)smem;                     // [128]
     float2* s_gd = (float2*)(s_wsum + 128);               // [128]
     uint32_t* s_abh = (uint32_t*)(s_gd + 128);            // [G * 32]
     const int G = a.G, G0 = a.G0;
+    u32x4* s_w = (u32x4*)(s_abh + G * 32);                // WM 1: [G * 256]; WM 2: [2][4 * 256]
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int h = lane >> 5, j = lane & 31;
@@ -354,14 +365,27 @@ __global__ __launch_bounds__(256, 2) void k_conv1p(D8sGemmArgs a, int32_t* __res
             s_wsum[tid] = a.wsum[tid];
             s_gd[tid] = ((const float2*)a.gd)[tid];
         }
+        const u32x4* w = (const u32x4*)a.w;
+        for (int i = tid; i < (WM == 1 ? G * 256 : 1024); i += 4 * 256) {     // WM 2: chunk 0
+            u32x4 v[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) v[u] = w[min(i + u * 256, G * 256 - 1)];
+#pragma unroll
+            for (int u = 0; u < 4; ++u)
+                if (i + u * 256 < G * 256) s_w[i + u * 256] = v[u];
+        }
     }
     __syncthreads();
 
     const int64_t rows = a.rows, HW = a.HW;
     const int ntiles = (int)((rows + 63) / 64);
     const int stride = (int)gridDim.x * 4;
-    int tile = (int)blockIdx.x * 4 + wave;
-    if (tile >= ntiles) return;                          // (uniform per wave; no barrier follows)
+    // the workgroup's tiles are first, first + 1, ..., first + 3 (then + stride ...): it runs while its
+    // first tile exists, so its waves run in step (a wave past the last tile works on a repeat of the
+    // last pixel and stores nothing)
+    int first = (int)blockIdx.x * 4;
+    if (first >= ntiles) return;                         // (uniform per workgroup)
+    int tile = first + wave;
 
     const uint8_t* in0 = (const uint8_t*)a.in0;
     const uint8_t* seg = (const uint8_t*)a.seg;
@@ -370,23 +394,27 @@ __global__ __launch_bounds__(256, 2) void k_conv1p(D8sGemmArgs a, int32_t* __res
     uint32_t ci0, ci1, cs0, cs1, ni0, ni1, ns0, ns1;      // this tile's and the next tile's offsets
     c1p_pixels(tile, j, h, rows, HW, G0, ci0, ci1, cs0, cs1);
     int next = tile + stride;
-    c1p_pixels(next < ntiles ? next : tile, j, h, rows, HW, G0, ni0, ni1, ns0, ns1);
+    c1p_pixels(next, j, h, rows, HW, G0, ni0, ni1, ns0, ns1);
 
     const int Gp = (G + 3) & ~3;
     u32x4 ra[4][2];
-    u32x4 rb[2][4];
-    // weights: output tile c, row 32 c + j, half h of group g at w + (g * 256 + 64 c + 2 j + h) * 16
-    const u32x4* wl = (const u32x4*)a.w + j * 2 + h;
-#define C1P_LOAD_B(bslot, g)                                                                      \
+    u32x4 rb[4];
+    u32x4 stg[4];                                         // WM 2: the next chunk on its way
+    int cc = 0;                                           // WM 2: chunks done (buffer cc & 1)
+    const u32x4* wg = (const u32x4*)a.w;
+    // weights of step k for the MFMA: output tile c, row 32 c + j, half h of group g (chunk
+    // g * 256 + 64 c + 2 j + h of the layer; of the chunk buffer for WM 2)
+#define C1P_LOAD_B(k)                                                                             \
     do {                                                                                          \
-        const u32x4* p_ = wl + (int64_t)(g) * 256;                                                \
-        _Pragma("unroll") for (int c_ = 0; c_ < 4; ++c_) rb[bslot][c_] = p_[64 * c_];             \
+        const int g_ = (k) < G ? (k) : G - 1;                                                     \
+        const u32x4* p_ = WM == 1 ? s_w + g_ * 256 : s_w + (cc & 1) * 1024 + ((k) & 3) * 256;     \
+        p_ += j * 2 + h;                                                                          \
+        _Pragma("unroll") for (int c_ = 0; c_ < 4; ++c_) rb[c_] = p_[64 * c_];                    \
     } while (0)
 #define C1P_LOAD_A(slot, t)                                                                       \
     c1p_act(ra[slot][0], ra[slot][1], in0, seg, in_gs, seg_gs, G0, G, Gp, (t), ci0, ci1, cs0, cs1,  \
             ni0, ni1, ns0, ns1)
 
-    C1P_LOAD_B(0, 0);
     C1P_LOAD_A(0, 0);
     C1P_LOAD_A(1, 1);
     C1P_LOAD_A(2, 2);
@@ -404,32 +432,51 @@ __global__ __launch_bounds__(256, 2) void k_conv1p(D8sGemmArgs a, int32_t* __res
         }
         // one K step: weights of the next step first (issue order), the prologue of this step's bytes
         // (zero operands on padded steps), the activations 4 steps ahead, the 8 MFMAs
-#define C1P_STEP(slot, k)                                                                         \
+#define C1P_STEP(slot, k, PAD)                                                                    \
     do {                                                                                          \
         const int k_ = (k);                                                                       \
-        C1P_LOAD_B(((slot) + 1) & 1, k_ + 1 < G ? k_ + 1 : (k_ + 1 < Gp ? G - 1 : 0));            \
-        asm volatile("" ::: "memory");                                                            \
-        u32x4 b0_ = {0, 0, 0, 0}, b1_ = {0, 0, 0, 0};                                             \
-        if (k_ < G) {                                                                             \
+        C1P_LOAD_B(k_);                                                                           \
+        u32x4 b0_, b1_;                                                                           \
+        if (!PAD || k_ < G) {                                                                     \
             const u32x4* pp_ = (const u32x4*)(s_abh + k_ * 32 + h * 16);                          \
             const u32x4 p0_ = pp_[0], p1_ = pp_[1], p2_ = pp_[2], p3_ = pp_[3];                   \
             b0_ = pro16(ra[slot][0], p0_, p1_, p2_, p3_);                                         \
             b1_ = pro16(ra[slot][1], p0_, p1_, p2_, p3_);                                         \
+        } else {                                                                                  \
+            b0_ = u32x4{0, 0, 0, 0};                                                              \
+            b1_ = u32x4{0, 0, 0, 0};                                                              \
         }                                                                                         \
         C1P_LOAD_A(slot, k_ + 4);                                                                 \
         _Pragma("unroll") for (int c_ = 0; c_ < 4; ++c_) {                                        \
-            acc[0][c_] = mfma_i8(rb[(slot) & 1][c_], b0_, acc[0][c_]);                            \
-            acc[1][c_] = mfma_i8(rb[(slot) & 1][c_], b1_, acc[1][c_]);                            \
+            acc[0][c_] = mfma_i8(rb[c_], b0_, acc[0][c_]);                                        \
+            acc[1][c_] = mfma_i8(rb[c_], b1_, acc[1][c_]);                                        \
         }                                                                                         \
     } while (0)
+        // four steps = one weight chunk; PAD: the last chunk of a tile, whose steps past G - 1 multiply
+        // zero operands (the others need no test)
+#define C1P_CHUNK(PAD)                                                                            \
+    do {                                                                                          \
+        if (WM == 2) {                             /* the next chunk (the next tile's first) */   \
+            const int nc_ = k + 4 < Gp ? (k >> 2) + 1 : 0;                                        \
+            _Pragma("unroll") for (int u_ = 0; u_ < 4; ++u_)                                      \
+                stg[u_] = wg[min(nc_ * 1024 + tid + 256 * u_, G * 256 - 1)];                      \
+        }                                                                                         \
+        C1P_STEP(0, k, PAD);                                                                      \
+        C1P_STEP(1, k + 1, PAD);                                                                  \
+        C1P_STEP(2, k + 2, PAD);                                                                  \
+        C1P_STEP(3, k + 3, PAD);                                                                  \
+        if (WM == 2) {                             /* its buffer was last read in chunk cc - 1 */ \
+            _Pragma("unroll") for (int u_ = 0; u_ < 4; ++u_)                                      \
+                s_w[((cc + 1) & 1) * 1024 + tid + 256 * u_] = stg[u_];                            \
+            __syncthreads();                                                                      \
+            ++cc;                                                                                 \
+        }                                                                                         \
+        k += 4;                                                                                   \
+    } while (0)
         int k = 0;
-        do {                                           // Gp >= 4: no path around the loop
-            C1P_STEP(0, k);
-            C1P_STEP(1, k + 1);
-            C1P_STEP(2, k + 2);
-            C1P_STEP(3, k + 3);
-            k += 4;
-        } while (k < Gp);
+        for (; k < (G & ~3);) C1P_CHUNK(false);
+        if (k < Gp) C1P_CHUNK(true);
+#undef C1P_CHUNK
 #undef C1P_STEP
 
         // epilogue as k_conv1 (conv1w_body epilogue, src/knee/dense8s_kernels.cu:595-611)
@@ -470,14 +517,15 @@ __global__ __launch_bounds__(256, 2) void k_conv1p(D8sGemmArgs a, int32_t* __res
             }
             __builtin_amdgcn_sched_barrier(0);         // one output tile's values live at a time
         }
-        if (next >= ntiles) break;
+        first += stride;
+        if (first >= ntiles) break;
         tile = next;
         ci0 = ni0;
         ci1 = ni1;
         cs0 = ns0;
         cs1 = ns1;
         next = tile + stride;
-        c1p_pixels(next < ntiles ? next : tile, j, h, rows, HW, G0, ni0, ni1, ns0, ns1);
+        c1p_pixels(next, j, h, rows, HW, G0, ni0, ni1, ns0, ns1);
     }
 #undef C1P_LOAD_A
 #undef C1P_LOAD_B
@@ -895,10 +943,11 @@ __global__ __launch_bounds__(64 * NW, 1) void k_dense(D8sDenseArgs a, int tiles_
                         const float2 prm = s_gd[32 * c + res_row(v, h)];
                         float y = __builtin_fmaf(prm.x, (float)acc[i][c][v], prm.y);
                         y = __builtin_fminf(__builtin_fmaxf(y, 0.0f), 1.0f);
-                        const uint32_t b = __float_as_uint(__builtin_fmaf(y, 255.0f, 8388608.0f)) & 0xffu;
+                        // low byte of 2^23 + 128 + RNE(255 y): u ^ 0x80, the conv2 operand
+                        const uint32_t b = __float_as_uint(__builtin_fmaf(y, 255.0f, 8388736.0f)) & 0xffu;
                         d |= b << (8 * r);
                     }
-                    e[kk] = d ^ SIGN4;
+                    e[kk] = d;
                 }
                 const u32x4 row = xchg_rows(e[0], e[1], e[2], e[3], h);
                 if (dst >= 0) s_b[c * WIN * 2 + swz(dst, h)] = row;
@@ -1152,10 +1201,11 @@ __global__ __launch_bounds__(DB_NT, 1) void k_dblock(D8sBlockArgs a) {
                     const float2 prm = s_gd[32 * c + res_row(v, h)];
                     float y = __builtin_fmaf(prm.x, (float)acc[c][v], prm.y);
                     y = __builtin_fminf(__builtin_fmaxf(y, 0.0f), 1.0f);
-                    const uint32_t b = __float_as_uint(__builtin_fmaf(y, 255.0f, 8388608.0f)) & 0xffu;
+                    // low byte of 2^23 + 128 + RNE(255 y): u ^ 0x80, the conv2 operand
+                    const uint32_t b = __float_as_uint(__builtin_fmaf(y, 255.0f, 8388736.0f)) & 0xffu;
                     d |= b << (8 * r);
                 }
-                e[kk] = d ^ SIGN4;
+                e[kk] = d;
             }
             const u32x4 row = xchg_rows(e[0], e[1], e[2], e[3], h);
             if (live) s_b[c * WIN * 2 + swz(dst, h)] = row;
@@ -1657,18 +1707,21 @@ static int conv1_launch(const D8sGemmArgs* a, int32_t* acc, hipStream_t st) {
     const int64_t want = 3 * (int64_t)cu_count() / 2;
     int ks = 1;
     while (ks < 4 && (a->rows + 64 * 4 / ks - 1) / (64 * 4 / ks) < want) ks *= 2;
-    // the persistent form when every wave of a full grid gets several tiles
+    // one k-slice: the persistent form (64-pixel tiles, the weights through LDS)
     const int64_t ntiles = (a->rows + 63) / 64;
     const int64_t in0_bytes = (int64_t)a->N * a->G0 * a->HW * 32, slot_bytes = (int64_t)a->rows * 32;
-    if (ks == 1 && ntiles >= 2 * 8 * (int64_t)cu_count() && in0_bytes < (1ll << 32) &&
-        slot_bytes < (1ll << 32)) {
+    if (ks == 1 && ntiles < (1ll << 30) && in0_bytes < (1ll << 32) && slot_bytes < (1ll << 32)) {
         const int64_t want_blocks = (ntiles + 3) / 4;
         const unsigned grid = (unsigned)(want_blocks < 2 * cu_count() ? want_blocks : 2 * cu_count());
-        const size_t shm1 = 128 * 4 + 128 * 8 + (size_t)a->G * 128;
-        if (acc)
-            hipLaunchKernelGGL((k_conv1p<true>), dim3(grid), dim3(256), shm1, st, *a, acc);
-        else
-            hipLaunchKernelGGL((k_conv1p<false>), dim3(grid), dim3(256), shm1, st, *a, nullptr);
+        const int wm = c1p_lds(a->G, 1) <= 80 * 1024 ? 1 : 2;   // two workgroups per CU still fit
+        const size_t shm1 = c1p_lds(a->G, wm);
+#define C1P_LAUNCH(ACC_, WM_)                                                                     \
+    hipLaunchKernelGGL((k_conv1p<ACC_, WM_>), dim3(grid), dim3(256), shm1, st, *a, ACC_ ? acc : nullptr)
+        if (acc && wm == 1) C1P_LAUNCH(true, 1);
+        else if (acc) C1P_LAUNCH(true, 2);
+        else if (wm == 1) C1P_LAUNCH(false, 1);
+        else C1P_LAUNCH(false, 2);
+#undef C1P_LAUNCH
         return launched("d8s_conv1");
     }
     const int px = 64 * 4 / ks;

@@ -70,10 +70,12 @@ def test_conv1_config2(dev, S, C):
     assert 0.0 < zero < 0.9 and sat < 0.5, (zero, sat)
 
 
-@pytest.mark.parametrize("S,C,N", [(64, 320, 12), (8, 96, 3), (2, 64, 1), (100, 96, 30), (128, 32, 16)])
+@pytest.mark.parametrize("S,C,N", [(64, 320, 12), (8, 96, 3), (2, 64, 1), (100, 96, 30), (128, 32, 16),
+                                   (64, 608, 64), (50, 704, 40)])
 def test_conv1_ks_variants(dev, S, C, N):
     """Pixel counts that select the 2-slice and 4-slice k-split, the persistent form (a ragged last
-    tile; a single group) and ragged last workgroups."""
+    tile; a single group; weights resident in LDS or staged in chunks; a workgroup with a wave past the
+    last tile) and ragged last workgroups."""
     c = cases.gemm_case(S, C, N=N, seed=17)
     acc, byt = checks.run_conv1(c, dev)
     acc_x, byt_x = checks.exact_conv1(c)
