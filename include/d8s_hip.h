@@ -124,8 +124,8 @@ typedef struct D8sBlockArgs {
  * fp16 stem engine + `quant_seg` (src/knee/dense8s.py:684-716,1330-1352;
  * src/knee/dense8s_kernels.cu:2365-2412), with the uint8 normalisation and flip of the input fused
  * into the load (the role of `gather_u8_to_f16`, src/knee/data/fused_uint8.py:480-506).
- *   x      input [N][3][H][W]: uint8 when kind = D8S_IN_U8 (x16 = lut[c][u]), fp16 when
- *          kind = D8S_IN_F16 (used as is);
+ *   x      input [N][3][H][W]: uint8 when kind = D8S_IN_U8 (x16 = lut[c][u]; 4-byte aligned), fp16
+ *          when kind = D8S_IN_F16 (used as is);
  *   lut    [3][256] fp16 (kind = D8S_IN_U8 only);
  *   w16    [64][168] fp16, norm0 folded in, k = (channel * 7 + ky) * 8 + kx + 1 and k % 8 = 0
  *          zero: the reference's `S_w16` table (src/knee/dense8s.py:522-530);

@@ -1478,9 +1478,49 @@ __global__ __launch_bounds__(256) void k_stem(D8sStemArgs a, int tiles_x, int ti
             if (i < NWC) *(u32x4*)(s_wt + (i / 21) * ST_WROW + 8 * (i % 21)) = wv[k];
         }
     }
-    if (a.kind == D8S_IN_U8)
+    if (a.kind == D8S_IN_U8) {
         for (int i = tid; i < 3 * 256; i += 256) s_lut[i] = __builtin_bit_cast(_Float16, a.lut[i]);
-    {
+        // uint8 input: every row of the tile (3 x 39 rows of 72 bytes, starting at x = ix0 = 4 px0 - 6,
+        // or mirrored) is fetched as 19 aligned dwords (W is a multiple of 4, so a dword is wholly in
+        // or out of the image), then each pair of bytes becomes two fp16 LUT values written as one
+        // dword: bytes (0, 1) of dword d land at lx = 4 d - 2 (mirrored: 72 - 4 d, swapped), bytes
+        // (2, 3) at lx = 4 d (mirrored: 70 - 4 d, swapped); the first pair of d = 0 and the second of
+        // d = 18 fall outside the tile.
+        constexpr int ND = 19, NROW = 3 * ST_IY, NI = NROW * ND, KD = (NI + 255) / 256;
+        const int a0 = mirror ? W - 4 * px0 - 68 : 4 * px0 - 8;          // first aligned source x
+        const uint8_t* x8 = (const uint8_t*)a.x;
+        uint32_t raw[KD];
+        uint32_t okm = 0;
+#pragma unroll
+        for (int k = 0; k < KD; ++k) {
+            const int i = tid + 256 * k;
+            const int r = i / ND, d = i - r * ND;
+            const int c = r / ST_IY, ly = r - c * ST_IY;
+            const int y = iy0 + ly, xd = a0 + 4 * d;
+            const bool ok = i < NI && (unsigned)y < (unsigned)H && (unsigned)xd < (unsigned)W;
+            const int64_t off = ok ? (((int64_t)ns * 3 + c) * H + y) * W + xd : 0;
+            raw[k] = *(const uint32_t*)(x8 + off);
+            okm |= (uint32_t)ok << k;
+        }
+        __syncthreads();                                  // s_lut
+#pragma unroll
+        for (int k = 0; k < KD; ++k) {
+            const int i = tid + 256 * k;
+            if (i >= NI) break;
+            const int r = i / ND, d = i - r * ND;
+            const int c = r / ST_IY;
+            const uint32_t v = ((okm >> k) & 1) ? raw[k] : 0u;
+            const _Float16* lt = s_lut + c * 256;
+            const uint32_t zero = 0u;
+            const uint32_t h0 = (okm >> k) & 1 ? __builtin_bit_cast(uint16_t, lt[v & 0xff]) : zero;
+            const uint32_t h1 = (okm >> k) & 1 ? __builtin_bit_cast(uint16_t, lt[(v >> 8) & 0xff]) : zero;
+            const uint32_t h2 = (okm >> k) & 1 ? __builtin_bit_cast(uint16_t, lt[(v >> 16) & 0xff]) : zero;
+            const uint32_t h3 = (okm >> k) & 1 ? __builtin_bit_cast(uint16_t, lt[v >> 24]) : zero;
+            uint32_t* row = (uint32_t*)(s_in + r * ST_IX);
+            if (d >= 1) row[mirror ? (72 - 4 * d) / 2 : (4 * d - 2) / 2] = mirror ? h1 | (h0 << 16) : h0 | (h1 << 16);
+            if (d <= 17) row[mirror ? (70 - 4 * d) / 2 : (4 * d) / 2] = mirror ? h3 | (h2 << 16) : h2 | (h3 << 16);
+        }
+    } else {
         constexpr int NIN = 3 * ST_IY * ST_IX, KIN = (NIN + 255) / 256;
         uint32_t raw[KIN];
         uint64_t okm = 0;
@@ -1496,26 +1536,14 @@ __global__ __launch_bounds__(256) void k_stem(D8sStemArgs a, int tiles_x, int ti
             idx[k] = ok ? (((int64_t)ns * 3 + c) * H + y) * W + xs : 0;
             okm |= (uint64_t)ok << k;
         }
-        if (a.kind == D8S_IN_U8) {                        // uniform: each buffer read as its own type
-            const uint8_t* x8 = (const uint8_t*)a.x;
+        const uint16_t* x16 = (const uint16_t*)a.x;
 #pragma unroll
-            for (int k = 0; k < KIN; ++k) raw[k] = x8[idx[k]];
-        } else {
-            const uint16_t* x16 = (const uint16_t*)a.x;
-#pragma unroll
-            for (int k = 0; k < KIN; ++k) raw[k] = x16[idx[k]];
-        }
-        __syncthreads();                                  // s_lut
+        for (int k = 0; k < KIN; ++k) raw[k] = x16[idx[k]];
 #pragma unroll
         for (int k = 0; k < KIN; ++k) {
             const int i = tid + 256 * k;
             if (i >= NIN) break;
-            const int c = i / (ST_IY * ST_IX);
-            _Float16 v = (_Float16)0.0f;
-            if ((okm >> k) & 1)
-                v = a.kind == D8S_IN_U8 ? s_lut[c * 256 + raw[k]]
-                                        : __builtin_bit_cast(_Float16, (uint16_t)raw[k]);
-            s_in[i] = v;
+            s_in[i] = ((okm >> k) & 1) ? __builtin_bit_cast(_Float16, (uint16_t)raw[k]) : (_Float16)0.0f;
         }
     }
     __syncthreads();
@@ -1887,6 +1915,7 @@ extern "C" int d8s_stem(const D8sStemArgs* a, void* stream) {
             "d8s_stem: kind must be D8S_IN_F16, or D8S_IN_U8 with a lut");
     REQUIRE(a->N >= 1 && a->H >= 4 && a->W >= 4 && a->H % 4 == 0 && a->W % 4 == 0,
             "d8s_stem: H and W must be positive multiples of 4");
+    REQUIRE(a->kind != D8S_IN_U8 || ((uintptr_t)a->x & 3) == 0, "d8s_stem: uint8 input not 4-byte aligned");
     REQUIRE(a->flip >= 0 && a->flip <= 2 && (a->flip != 2 || a->N % 2 == 0),
             "d8s_stem: flip must be 0, 1, or 2 (TTA pairs, N even)");
     const int Hp = a->H / 4, Wp = a->W / 4;

@@ -679,10 +679,11 @@ class Dense8SEncoder:
                 mark("final")
 
     def _padded(self, chunk: torch.Tensor, mode: int) -> torch.Tensor:
-        """One pass worth of input images: `chunk` itself if full, else copied to the head of a buffer (the
-        rest holds old images, whose outputs are computed and discarded)."""
+        """One pass worth of input images: `chunk` itself if full (copied if its data is not 16-byte
+        aligned: the stem reads uint8 rows as dwords), else copied to the head of a buffer (the rest
+        holds old images, whose outputs are computed and discarded)."""
         if chunk.shape[0] == self._per_pass(mode):
-            return chunk
+            return chunk if chunk.data_ptr() % 16 == 0 else chunk.clone()
         if self._pad is None:
             self._pad = torch.zeros((self.nb, *chunk.shape[1:]), dtype=self.in_dtype,
                                     device=f"cuda:{self.dev}")

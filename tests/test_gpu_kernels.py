@@ -224,7 +224,7 @@ def _stem_tables(seed: int = 3):
     return w16, bias, inv, lut
 
 
-@pytest.mark.parametrize("H,W,N", [(512, 512, 2), (64, 96, 3), (20, 12, 1)])
+@pytest.mark.parametrize("H,W,N", [(512, 512, 2), (64, 96, 3), (20, 12, 1), (8, 4, 3)])
 def test_stem(dev, H, W, N):
     w16, bias, inv, lut = _stem_tables()
     rng = np.random.default_rng(H + W)
