@@ -105,6 +105,11 @@ DEV u32x4 xchg_rows(uint32_t e0, uint32_t e1, uint32_t e2, uint32_t e3, int h) {
     return h ? u32x4{r1, e2, r2, e3} : u32x4{e0, r1, e1, r2};
 }
 
+// LDS position of 16-byte chunk i of a [G][128][32] conv1 weight table (chunk 64 c + 2 j + h within a
+// group: output tile c, row j, half h): 64 c + 32 h + j, so the 16 lanes one LDS cycle serves (same
+// h, consecutive j) read consecutive chunks.
+DEV int wperm(int i) { return (i & ~63) | ((i & 1) << 5) | ((i >> 1) & 31); }
+
 // Row i (output channel) of element v of a 32x32 MFMA result, for lane half h.
 DEV int res_row(int v, int h) { return 8 * (v >> 2) + 4 * h + (v & 3); }
 
@@ -373,7 +378,7 @@ __global__ __launch_bounds__(256, 2) void k_conv1p(D8sGemmArgs a, int32_t* __res
             for (int u = 0; u < 4; ++u) v[u] = w[min(i + u * 256, G * 256 - 1)];
 #pragma unroll
             for (int u = 0; u < 4; ++u)
-                if (i + u * 256 < G * 256) s_w[i + u * 256] = v[u];
+                if (i + u * 256 < G * 256) s_w[wperm(i + u * 256)] = v[u];
         }
     }
     __syncthreads();
@@ -409,7 +414,7 @@ __global__ __launch_bounds__(256, 2) void k_conv1p(D8sGemmArgs a, int32_t* __res
     do {                                                                                          \
         const int g_ = (k) < G ? (k) : G - 1;                                                     \
         const u32x4* p_ = WM == 1 ? s_w + g_ * 256 : s_w + (cc & 1) * 1024 + ((k) & 3) * 256;     \
-        p_ += j * 2 + h;                                                                          \
+        p_ += j + 32 * h;                                                                         \
         _Pragma("unroll") for (int c_ = 0; c_ < 4; ++c_) rb[c_] = p_[64 * c_];                    \
     } while (0)
 #define C1P_LOAD_A(slot, t)                                                                       \
@@ -468,7 +473,7 @@ __global__ __launch_bounds__(256, 2) void k_conv1p(D8sGemmArgs a, int32_t* __res
         C1P_STEP(3, k + 3, PAD);                                                                  \
         if (WM == 2) {                             /* its buffer was last read in chunk cc - 1 */ \
             _Pragma("unroll") for (int u_ = 0; u_ < 4; ++u_)                                      \
-                s_w[((cc + 1) & 1) * 1024 + tid + 256 * u_] = stg[u_];                            \
+                s_w[((cc + 1) & 1) * 1024 + wperm(tid + 256 * u_)] = stg[u_];                     \
             __syncthreads();                                                                      \
             ++cc;                                                                                 \
         }                                                                                         \
@@ -815,7 +820,7 @@ __global__ __launch_bounds__(64 * NW, 1) void k_dense(D8sDenseArgs a, int tiles_
             for (int u = 0; u < 4; ++u) v[u] = w1[min(i + u * NT, G * 256 - 1)];
 #pragma unroll
             for (int u = 0; u < 4; ++u)
-                if (i + u * NT < G * 256) s_w1[i + u * NT] = v[u];
+                if (i + u * NT < G * 256) s_w1[wperm(i + u * NT)] = v[u];
         }
     }
 
@@ -841,7 +846,7 @@ __global__ __launch_bounds__(64 * NW, 1) void k_dense(D8sDenseArgs a, int tiles_
     const u32x4* wl = (const u32x4*)a.w1 + j * 2 + h;
 #define DN_LOAD_B(bslot, g)                                                                       \
     do {                                                                                          \
-        const u32x4* p_ = (WL ? (const u32x4*)s_w1 + j * 2 + h : wl) + (int64_t)(g) * 256;        \
+        const u32x4* p_ = (WL ? (const u32x4*)s_w1 + j + 32 * h : wl) + (int64_t)(g) * 256;       \
         _Pragma("unroll") for (int c_ = 0; c_ < 4; ++c_) rb[WL ? 0 : (bslot)][c_] = p_[64 * c_];  \
     } while (0)
     // activations of step t: t < Gp this tile's group t (repeats of G - 1 past it, unused), t >= Gp
@@ -1124,7 +1129,7 @@ __global__ __launch_bounds__(DB_NT, 1) void k_dblock(D8sBlockArgs a) {
     _Pragma("unroll") for (int u_ = 0; u_ < 4; ++u_)                                              \
         stg[u_] = w1[min((c) * 2048 + tid + DB_NT * u_, G * 256 - 1)]
 #define DB_STAGE_STORE(c)                                                                         \
-    _Pragma("unroll") for (int u_ = 0; u_ < 4; ++u_) s_wc[((c) & 1) * 2048 + tid + DB_NT * u_] = stg[u_]
+    _Pragma("unroll") for (int u_ = 0; u_ < 4; ++u_) s_wc[((c) & 1) * 2048 + wperm(tid + DB_NT * u_)] = stg[u_]
 #define DB_SRC(g) ((g) < G0 ? in0 + (int64_t)(g) * HW * 32 + off                                  \
                             : segn + (int64_t)((g) - G0) * slot + off)
         u32x4 ra[4];
@@ -1160,7 +1165,7 @@ __global__ __launch_bounds__(DB_NT, 1) void k_dblock(D8sBlockArgs a) {
 #define DB_STEP(slot, k)                                                                          \
     do {                                                                                          \
         const int k_ = (k);                                                                       \
-        const u32x4* wq_ = s_wc + ((k_ >> 3) & 1) * 2048 + (k_ & 7) * 256 + j * 2 + h;            \
+        const u32x4* wq_ = s_wc + ((k_ >> 3) & 1) * 2048 + (k_ & 7) * 256 + j + 32 * h;           \
         u32x4 rb_[4];                                                                             \
         _Pragma("unroll") for (int c_ = 0; c_ < 4; ++c_) rb_[c_] = wq_[64 * c_];                  \
         const u32x4* pp_ = (const u32x4*)(s_abh + k_ * 32 + h * 16);                              \
