@@ -181,7 +181,7 @@ __global__ __launch_bounds__(256, 2) void k_conv1(D8sGemmArgs a, int32_t* __rest
     // need next BEFORE the activations four steps ahead: waiting for this step's weights then leaves
     // the later activation loads in flight.
     const int nk = (G - slice + KS - 1) / KS;
-    u32x4 ra[4][2];
+    u32x4 ra[4][2];                                       // [slot][block] (block 1 unused for U = 1)
     u32x4 rb[2][4];
     auto load_a = [&](int slot, int k) {
         const int g = slice + k * KS;
@@ -317,6 +317,7 @@ __global__ __launch_bounds__(256, 2) void k_conv1(D8sGemmArgs a, int32_t* __rest
 // Activation bytes of step t of a persistent conv1 tile (see k_conv1p): t < Gp this tile's group t
 // (past G - 1 a repeat of it, unused), t >= Gp the next tile's group t - Gp (clamped).  Plain values
 // in and out: the pixel offsets of the two tiles must stay in registers (selected, never addressed).
+template <int U>
 DEV void c1p_act(u32x4& r0, u32x4& r1, const uint8_t* in0, const uint8_t* seg, int64_t in_gs,
                  int64_t seg_gs, int G0, int G, int Gp, int t, uint32_t ci0, uint32_t ci1, uint32_t cs0,
                  uint32_t cs1, uint32_t ni0, uint32_t ni1, uint32_t ns0, uint32_t ns1) {
@@ -328,14 +329,15 @@ DEV void c1p_act(u32x4& r0, u32x4& r1, const uint8_t* in0, const uint8_t* seg, i
     const uint32_t o0 = cur ? (in ? ci0 : cs0) : (in ? ni0 : ns0);
     const uint32_t o1 = cur ? (in ? ci1 : cs1) : (in ? ni1 : ns1);
     r0 = *(const u32x4*)(base + o0);
-    r1 = *(const u32x4*)(base + o1);
+    if (U > 1) r1 = *(const u32x4*)(base + o1);
 }
 
-// Byte offsets of the lane's two pixels (j, j + 32) of 64-pixel tile t in an in0 group (i0, i1) and in
-// a store slot (s0, s1); pixels past the last row repeat it.
+// Byte offsets of the lane's pixels (j, j + 32) of (32 U)-pixel tile t in an in0 group (i0, i1) and
+// in a store slot (s0, s1); pixels past the last row repeat it.
+template <int U>
 DEV void c1p_pixels(int t, int j, int h, int64_t rows, int64_t HW, int G0, uint32_t& i0, uint32_t& i1,
                     uint32_t& s0, uint32_t& s1) {
-    int64_t m0 = (int64_t)t * 64 + j, m1 = m0 + 32;
+    int64_t m0 = (int64_t)t * (32 * U) + j, m1 = m0 + 32;
     if (m0 >= rows) m0 = rows - 1;
     if (m1 >= rows) m1 = rows - 1;
     const int64_t n0 = m0 / HW, p0 = m0 - n0 * HW, n1 = m1 / HW, p1 = m1 - n1 * HW;
@@ -353,8 +355,10 @@ static size_t c1p_lds(int G, int wm) {
 // WM: where the conv1 weights are read from.  1: all of the layer's in LDS, loaded once; 2: 4-group
 // chunks staged through LDS (double-buffered, one barrier per 4 steps; the waves of a workgroup run
 // in step).  From L2 one step ahead they would stall the steps once the layer no longer fits L1.
-template <bool ACC32, int WM>
-__global__ __launch_bounds__(256, 2) void k_conv1p(D8sGemmArgs a, int32_t* __restrict__ acc_out) {
+// U: 32-pixel column blocks per wave (a tile is 32 U pixels).  U = 1 halves the registers, so more
+// waves per SIMD hide the latency of layers with few tiles.
+template <bool ACC32, int WM, int U>
+__global__ __launch_bounds__(256, U == 2 ? 2 : 3) void k_conv1p(D8sGemmArgs a, int32_t* __restrict__ acc_out) {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     int32_t* s_wsum = (int32_t*)smem;                     // [128]
     float2* s_gd = (float2*)(s_wsum + 128);               // [128]
@@ -384,7 +388,7 @@ __global__ __launch_bounds__(256, 2) void k_conv1p(D8sGemmArgs a, int32_t* __res
     __syncthreads();
 
     const int64_t rows = a.rows, HW = a.HW;
-    const int ntiles = (int)((rows + 63) / 64);
+    const int ntiles = (int)((rows + 32 * U - 1) / (32 * U));
     const int stride = (int)gridDim.x * 4;
     // the workgroup's tiles are first, first + 1, ..., first + 3 (then + stride ...): it runs while its
     // first tile exists, so its waves run in step (a wave past the last tile works on a repeat of the
@@ -398,9 +402,9 @@ __global__ __launch_bounds__(256, 2) void k_conv1p(D8sGemmArgs a, int32_t* __res
     uint8_t* out = (uint8_t*)a.out;
     const int64_t in_gs = HW * 32, seg_gs = (int64_t)a.N * HW * 32;
     uint32_t ci0, ci1, cs0, cs1, ni0, ni1, ns0, ns1;      // this tile's and the next tile's offsets
-    c1p_pixels(tile, j, h, rows, HW, G0, ci0, ci1, cs0, cs1);
+    c1p_pixels<U>(tile, j, h, rows, HW, G0, ci0, ci1, cs0, cs1);
     int next = tile + stride;
-    c1p_pixels(next, j, h, rows, HW, G0, ni0, ni1, ns0, ns1);
+    c1p_pixels<U>(next, j, h, rows, HW, G0, ni0, ni1, ns0, ns1);
 
     const int Gp = (G + 3) & ~3;
     u32x4 ra[4][2];
@@ -418,7 +422,7 @@ __global__ __launch_bounds__(256, 2) void k_conv1p(D8sGemmArgs a, int32_t* __res
         _Pragma("unroll") for (int c_ = 0; c_ < 4; ++c_) rb[c_] = p_[64 * c_];                    \
     } while (0)
 #define C1P_LOAD_A(slot, t)                                                                       \
-    c1p_act(ra[slot][0], ra[slot][1], in0, seg, in_gs, seg_gs, G0, G, Gp, (t), ci0, ci1, cs0, cs1,  \
+    c1p_act<U>(ra[slot][0], ra[slot][1], in0, seg, in_gs, seg_gs, G0, G, Gp, (t), ci0, ci1, cs0, cs1, \
             ni0, ni1, ns0, ns1)
 
     C1P_LOAD_A(0, 0);
@@ -427,14 +431,14 @@ __global__ __launch_bounds__(256, 2) void k_conv1p(D8sGemmArgs a, int32_t* __res
     C1P_LOAD_A(3, 3);
 
     for (;;) {
-        i32x16 acc[2][4];
+        i32x16 acc[U][4];
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
             i32x16 init;
 #pragma unroll
             for (int v = 0; v < 16; ++v) init[v] = 128 * s_wsum[32 * c + res_row(v, h)];
-            acc[0][c] = init;
-            acc[1][c] = init;
+#pragma unroll
+            for (int u = 0; u < U; ++u) acc[u][c] = init;
         }
         // one K step: weights of the next step first (issue order), the prologue of this step's bytes
         // (zero operands on padded steps), the activations 4 steps ahead, the 8 MFMAs
@@ -447,7 +451,7 @@ __global__ __launch_bounds__(256, 2) void k_conv1p(D8sGemmArgs a, int32_t* __res
             const u32x4* pp_ = (const u32x4*)(s_abh + k_ * 32 + h * 16);                          \
             const u32x4 p0_ = pp_[0], p1_ = pp_[1], p2_ = pp_[2], p3_ = pp_[3];                   \
             b0_ = pro16(ra[slot][0], p0_, p1_, p2_, p3_);                                         \
-            b1_ = pro16(ra[slot][1], p0_, p1_, p2_, p3_);                                         \
+            if (U > 1) b1_ = pro16(ra[slot][1], p0_, p1_, p2_, p3_);                              \
         } else {                                                                                  \
             b0_ = u32x4{0, 0, 0, 0};                                                              \
             b1_ = u32x4{0, 0, 0, 0};                                                              \
@@ -455,7 +459,7 @@ __global__ __launch_bounds__(256, 2) void k_conv1p(D8sGemmArgs a, int32_t* __res
         C1P_LOAD_A(slot, k_ + 4);                                                                 \
         _Pragma("unroll") for (int c_ = 0; c_ < 4; ++c_) {                                        \
             acc[0][c_] = mfma_i8(rb[c_], b0_, acc[0][c_]);                                        \
-            acc[1][c_] = mfma_i8(rb[c_], b1_, acc[1][c_]);                                        \
+            if (U > 1) acc[U - 1][c_] = mfma_i8(rb[c_], b1_, acc[U - 1][c_]);                     \
         }                                                                                         \
     } while (0)
         // four steps = one weight chunk; PAD: the last chunk of a tile, whose steps past G - 1 multiply
@@ -486,11 +490,11 @@ __global__ __launch_bounds__(256, 2) void k_conv1p(D8sGemmArgs a, int32_t* __res
 #undef C1P_STEP
 
         // epilogue as k_conv1 (conv1w_body epilogue, src/knee/dense8s_kernels.cu:595-611)
-        const int64_t mbase = (int64_t)tile * 64 + j;
+        const int64_t mbase = (int64_t)tile * (32 * U) + j;
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
 #pragma unroll
-            for (int u = 0; u < 2; ++u) {
+            for (int u = 0; u < U; ++u) {
                 const int64_t m = mbase + 32 * u;
                 if (ACC32) {
                     if (m < rows) {
@@ -531,7 +535,7 @@ __global__ __launch_bounds__(256, 2) void k_conv1p(D8sGemmArgs a, int32_t* __res
         cs0 = ns0;
         cs1 = ns1;
         next = tile + stride;
-        c1p_pixels(next, j, h, rows, HW, G0, ni0, ni1, ns0, ns1);
+        c1p_pixels<U>(next, j, h, rows, HW, G0, ni0, ni1, ns0, ns1);
     }
 #undef C1P_LOAD_A
 #undef C1P_LOAD_B
@@ -1132,11 +1136,11 @@ __global__ __launch_bounds__(DB_NT, 1) void k_dblock(D8sBlockArgs a) {
     _Pragma("unroll") for (int u_ = 0; u_ < 4; ++u_) s_wc[((c) & 1) * 2048 + wperm(tid + DB_NT * u_)] = stg[u_]
 #define DB_SRC(g) ((g) < G0 ? in0 + (int64_t)(g) * HW * 32 + off                                  \
                             : segn + (int64_t)((g) - G0) * slot + off)
-        u32x4 ra[4];
+        u32x4 ra[8];                                     // activations 8 groups ahead
         const int klast = nk - 1;
         DB_STAGE_LOAD(0);
 #pragma unroll
-        for (int s = 0; s < 4; ++s) ra[s] = *(const u32x4*)DB_SRC(s < klast ? s : klast);
+        for (int s = 0; s < 8; ++s) ra[s] = *(const u32x4*)DB_SRC(s < klast ? s : klast);
 
 #pragma unroll
         for (int k = 0; k < 5; ++k)
@@ -1170,7 +1174,7 @@ __global__ __launch_bounds__(DB_NT, 1) void k_dblock(D8sBlockArgs a) {
         _Pragma("unroll") for (int c_ = 0; c_ < 4; ++c_) rb_[c_] = wq_[64 * c_];                  \
         const u32x4* pp_ = (const u32x4*)(s_abh + k_ * 32 + h * 16);                              \
         const u32x4 bx_ = pro16(ra[slot], pp_[0], pp_[1], pp_[2], pp_[3]);                        \
-        ra[slot] = *(const u32x4*)DB_SRC(k_ + 4 < klast ? k_ + 4 : klast);                        \
+        ra[slot] = *(const u32x4*)DB_SRC(k_ + 8 < klast ? k_ + 8 : klast);                        \
         _Pragma("unroll") for (int c_ = 0; c_ < 4; ++c_) acc[c_] = mfma_i8(rb_[c_], bx_, acc[c_]); \
     } while (0)
         for (int ch = 0; ch < nch; ++ch) {
@@ -1180,10 +1184,10 @@ __global__ __launch_bounds__(DB_NT, 1) void k_dblock(D8sBlockArgs a) {
             if (k0 + 1 < nk) DB_STEP(1, k0 + 1);
             if (k0 + 2 < nk) DB_STEP(2, k0 + 2);
             if (k0 + 3 < nk) DB_STEP(3, k0 + 3);
-            if (k0 + 4 < nk) DB_STEP(0, k0 + 4);
-            if (k0 + 5 < nk) DB_STEP(1, k0 + 5);
-            if (k0 + 6 < nk) DB_STEP(2, k0 + 6);
-            if (k0 + 7 < nk) DB_STEP(3, k0 + 7);
+            if (k0 + 4 < nk) DB_STEP(4, k0 + 4);
+            if (k0 + 5 < nk) DB_STEP(5, k0 + 5);
+            if (k0 + 6 < nk) DB_STEP(6, k0 + 6);
+            if (k0 + 7 < nk) DB_STEP(7, k0 + 7);
             if (ch + 1 < nch) {
                 DB_STAGE_STORE(ch + 1);                  // its buffer was last read in chunk ch - 1
                 __syncthreads();
@@ -1741,20 +1745,30 @@ static int conv1_launch(const D8sGemmArgs* a, int32_t* acc, hipStream_t st) {
     const int64_t want = 3 * (int64_t)cu_count() / 2;
     int ks = 1;
     while (ks < 4 && (a->rows + 64 * 4 / ks - 1) / (64 * 4 / ks) < want) ks *= 2;
-    // one k-slice: the persistent form (64-pixel tiles, the weights through LDS)
-    const int64_t ntiles = (a->rows + 63) / 64;
+    // one k-slice: the persistent form (the weights through LDS); 64-pixel tiles when every wave of
+    // two per SIMD gets at least two, else 32-pixel tiles and three waves per SIMD
     const int64_t in0_bytes = (int64_t)a->N * a->G0 * a->HW * 32, slot_bytes = (int64_t)a->rows * 32;
-    if (ks == 1 && ntiles < (1ll << 30) && in0_bytes < (1ll << 32) && slot_bytes < (1ll << 32)) {
+    if (ks == 1 && a->rows < (1ll << 34) && in0_bytes < (1ll << 32) && slot_bytes < (1ll << 32)) {
+        const int u = (a->rows + 63) / 64 >= 2 * 8 * (int64_t)cu_count() ? 2 : 1;
+        const int64_t ntiles = (a->rows + 32 * u - 1) / (32 * u);
+        const int per_cu = u == 2 ? 2 : 3;                        // workgroups per CU
         const int64_t want_blocks = (ntiles + 3) / 4;
-        const unsigned grid = (unsigned)(want_blocks < 2 * cu_count() ? want_blocks : 2 * cu_count());
-        const int wm = c1p_lds(a->G, 1) <= 80 * 1024 ? 1 : 2;   // two workgroups per CU still fit
+        const unsigned grid = (unsigned)(want_blocks < per_cu * cu_count() ? want_blocks : per_cu * cu_count());
+        const int wm = c1p_lds(a->G, 1) <= (size_t)(160 / per_cu) * 1024 ? 1 : 2;   // still per_cu per CU
         const size_t shm1 = c1p_lds(a->G, wm);
-#define C1P_LAUNCH(ACC_, WM_)                                                                     \
-    hipLaunchKernelGGL((k_conv1p<ACC_, WM_>), dim3(grid), dim3(256), shm1, st, *a, ACC_ ? acc : nullptr)
-        if (acc && wm == 1) C1P_LAUNCH(true, 1);
-        else if (acc) C1P_LAUNCH(true, 2);
-        else if (wm == 1) C1P_LAUNCH(false, 1);
-        else C1P_LAUNCH(false, 2);
+#define C1P_LAUNCH(ACC_, WM_, U_)                                                                 \
+    hipLaunchKernelGGL((k_conv1p<ACC_, WM_, U_>), dim3(grid), dim3(256), shm1, st, *a, ACC_ ? acc : nullptr)
+        if (u == 2) {
+            if (acc && wm == 1) C1P_LAUNCH(true, 1, 2);
+            else if (acc) C1P_LAUNCH(true, 2, 2);
+            else if (wm == 1) C1P_LAUNCH(false, 1, 2);
+            else C1P_LAUNCH(false, 2, 2);
+        } else {
+            if (acc && wm == 1) C1P_LAUNCH(true, 1, 1);
+            else if (acc) C1P_LAUNCH(true, 2, 1);
+            else if (wm == 1) C1P_LAUNCH(false, 1, 1);
+            else C1P_LAUNCH(false, 2, 1);
+        }
 #undef C1P_LAUNCH
         return launched("d8s_conv1");
     }
