@@ -181,7 +181,7 @@ __global__ __launch_bounds__(256, 2) void k_conv1(D8sGemmArgs a, int32_t* __rest
     // need next BEFORE the activations four steps ahead: waiting for this step's weights then leaves
     // the later activation loads in flight.
     const int nk = (G - slice + KS - 1) / KS;
-    u32x4 ra[4][2];                                       // [slot][block] (block 1 unused for U = 1)
+    u32x4 ra[4][2];
     u32x4 rb[2][4];
     auto load_a = [&](int slot, int k) {
         const int g = slice + k * KS;
@@ -356,8 +356,9 @@ static size_t c1p_lds(int G, int wm) {
 // chunks staged through LDS (double-buffered, one barrier per 4 steps; the waves of a workgroup run
 // in step).  From L2 one step ahead they would stall the steps once the layer no longer fits L1.
 // U: 32-pixel column blocks per wave (a tile is 32 U pixels).  U = 1 halves the registers, so more
-// waves per SIMD hide the latency of layers with few tiles.
-template <bool ACC32, int WM, int U>
+// waves per SIMD hide the latency of layers with few tiles.  PF: activation groups in flight (4, or 8
+// where the registers allow); the K loop runs over G rounded up to a multiple of PF.
+template <bool ACC32, int WM, int U, int PF>
 __global__ __launch_bounds__(256, U == 2 ? 2 : 3) void k_conv1p(D8sGemmArgs a, int32_t* __restrict__ acc_out) {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     int32_t* s_wsum = (int32_t*)smem;                     // [128]
@@ -406,8 +407,8 @@ __global__ __launch_bounds__(256, U == 2 ? 2 : 3) void k_conv1p(D8sGemmArgs a, i
     int next = tile + stride;
     c1p_pixels<U>(next, j, h, rows, HW, G0, ni0, ni1, ns0, ns1);
 
-    const int Gp = (G + 3) & ~3;
-    u32x4 ra[4][2];
+    const int Gp = (G + PF - 1) & ~(PF - 1);
+    u32x4 ra[PF][2];                                      // [slot][block] (block 1 unused for U = 1)
     u32x4 rb[4];
     u32x4 stg[4];                                         // WM 2: the next chunk on its way
     int cc = 0;                                           // WM 2: chunks done (buffer cc & 1)
@@ -425,10 +426,8 @@ __global__ __launch_bounds__(256, U == 2 ? 2 : 3) void k_conv1p(D8sGemmArgs a, i
     c1p_act<U>(ra[slot][0], ra[slot][1], in0, seg, in_gs, seg_gs, G0, G, Gp, (t), ci0, ci1, cs0, cs1, \
             ni0, ni1, ns0, ns1)
 
-    C1P_LOAD_A(0, 0);
-    C1P_LOAD_A(1, 1);
-    C1P_LOAD_A(2, 2);
-    C1P_LOAD_A(3, 3);
+#pragma unroll
+    for (int s0 = 0; s0 < PF; ++s0) C1P_LOAD_A(s0, s0);
 
     for (;;) {
         i32x16 acc[U][4];
@@ -456,7 +455,7 @@ __global__ __launch_bounds__(256, U == 2 ? 2 : 3) void k_conv1p(D8sGemmArgs a, i
             b0_ = u32x4{0, 0, 0, 0};                                                              \
             b1_ = u32x4{0, 0, 0, 0};                                                              \
         }                                                                                         \
-        C1P_LOAD_A(slot, k_ + 4);                                                                 \
+        C1P_LOAD_A(slot, k_ + PF);                                                                \
         _Pragma("unroll") for (int c_ = 0; c_ < 4; ++c_) {                                        \
             acc[0][c_] = mfma_i8(rb[c_], b0_, acc[0][c_]);                                        \
             if (U > 1) acc[U - 1][c_] = mfma_i8(rb[c_], b1_, acc[U - 1][c_]);                     \
@@ -464,17 +463,17 @@ __global__ __launch_bounds__(256, U == 2 ? 2 : 3) void k_conv1p(D8sGemmArgs a, i
     } while (0)
         // four steps = one weight chunk; PAD: the last chunk of a tile, whose steps past G - 1 multiply
         // zero operands (the others need no test)
-#define C1P_CHUNK(PAD)                                                                            \
+#define C1P_CHUNK(PAD, SB)                                                                        \
     do {                                                                                          \
         if (WM == 2) {                             /* the next chunk (the next tile's first) */   \
             const int nc_ = k + 4 < Gp ? (k >> 2) + 1 : 0;                                        \
             _Pragma("unroll") for (int u_ = 0; u_ < 4; ++u_)                                      \
                 stg[u_] = wg[min(nc_ * 1024 + tid + 256 * u_, G * 256 - 1)];                      \
         }                                                                                         \
-        C1P_STEP(0, k, PAD);                                                                      \
-        C1P_STEP(1, k + 1, PAD);                                                                  \
-        C1P_STEP(2, k + 2, PAD);                                                                  \
-        C1P_STEP(3, k + 3, PAD);                                                                  \
+        C1P_STEP((SB) + 0, k, PAD);                                                               \
+        C1P_STEP((SB) + 1, k + 1, PAD);                                                           \
+        C1P_STEP((SB) + 2, k + 2, PAD);                                                           \
+        C1P_STEP((SB) + 3, k + 3, PAD);                                                           \
         if (WM == 2) {                             /* its buffer was last read in chunk cc - 1 */ \
             _Pragma("unroll") for (int u_ = 0; u_ < 4; ++u_)                                      \
                 s_w[((cc + 1) & 1) * 1024 + wperm(tid + 256 * u_)] = stg[u_];                     \
@@ -483,9 +482,16 @@ __global__ __launch_bounds__(256, U == 2 ? 2 : 3) void k_conv1p(D8sGemmArgs a, i
         }                                                                                         \
         k += 4;                                                                                   \
     } while (0)
+        // chunks of 4 steps; with PF = 8 in pairs, so that step k uses activation slot k % 8
         int k = 0;
-        for (; k < (G & ~3);) C1P_CHUNK(false);
-        if (k < Gp) C1P_CHUNK(true);
+        for (; k < (G & ~(PF - 1));) {
+            C1P_CHUNK(false, 0);
+            if (PF == 8) C1P_CHUNK(false, 4);
+        }
+        if (k < Gp) {
+            C1P_CHUNK(true, 0);
+            if (PF == 8) C1P_CHUNK(true, 4);
+        }
 #undef C1P_CHUNK
 #undef C1P_STEP
 
@@ -1757,7 +1763,8 @@ static int conv1_launch(const D8sGemmArgs* a, int32_t* acc, hipStream_t st) {
         const int wm = c1p_lds(a->G, 1) <= (size_t)(160 / per_cu) * 1024 ? 1 : 2;   // still per_cu per CU
         const size_t shm1 = c1p_lds(a->G, wm);
 #define C1P_LAUNCH(ACC_, WM_, U_)                                                                 \
-    hipLaunchKernelGGL((k_conv1p<ACC_, WM_, U_>), dim3(grid), dim3(256), shm1, st, *a, ACC_ ? acc : nullptr)
+    hipLaunchKernelGGL((k_conv1p<ACC_, WM_, U_, U_ == 1 && WM_ == 1 ? 8 : 4>), dim3(grid), dim3(256), shm1,  \
+                       st, *a, ACC_ ? acc : nullptr)
         if (u == 2) {
             if (acc && wm == 1) C1P_LAUNCH(true, 1, 2);
             else if (acc) C1P_LAUNCH(true, 2, 2);
