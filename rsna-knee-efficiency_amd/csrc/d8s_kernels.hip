@@ -369,25 +369,6 @@ __global__ __launch_bounds__(256, U == 2 ? 2 : 3) void k_conv1p(D8sGemmArgs a, i
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int h = lane >> 5, j = lane & 31;
-    {
-        const uint32_t* abh32 = (const uint32_t*)a.abh;
-        for (int i = tid; i < G * 32; i += 256) s_abh[i] = abh32[i];
-        if (tid < 128) {
-            s_wsum[tid] = a.wsum[tid];
-            s_gd[tid] = ((const float2*)a.gd)[tid];
-        }
-        const u32x4* w = (const u32x4*)a.w;
-        for (int i = tid; i < (WM == 1 ? G * 256 : 1024); i += 4 * 256) {     // WM 2: chunk 0
-            u32x4 v[4];
-#pragma unroll
-            for (int u = 0; u < 4; ++u) v[u] = w[min(i + u * 256, G * 256 - 1)];
-#pragma unroll
-            for (int u = 0; u < 4; ++u)
-                if (i + u * 256 < G * 256) s_w[wperm(i + u * 256)] = v[u];
-        }
-    }
-    __syncthreads();
-
     const int64_t rows = a.rows, HW = a.HW;
     const int ntiles = (int)((rows + 32 * U - 1) / (32 * U));
     const int stride = (int)gridDim.x * 4;
@@ -426,8 +407,28 @@ __global__ __launch_bounds__(256, U == 2 ? 2 : 3) void k_conv1p(D8sGemmArgs a, i
     c1p_act<U>(ra[slot][0], ra[slot][1], in0, seg, in_gs, seg_gs, G0, G, Gp, (t), ci0, ci1, cs0, cs1, \
             ni0, ni1, ns0, ns1)
 
+    // the first activation groups are requested before the layer's tables are staged, so the two
+    // latencies overlap
 #pragma unroll
     for (int s0 = 0; s0 < PF; ++s0) C1P_LOAD_A(s0, s0);
+    {
+        const uint32_t* abh32 = (const uint32_t*)a.abh;
+        for (int i = tid; i < G * 32; i += 256) s_abh[i] = abh32[i];
+        if (tid < 128) {
+            s_wsum[tid] = a.wsum[tid];
+            s_gd[tid] = ((const float2*)a.gd)[tid];
+        }
+        const u32x4* w = (const u32x4*)a.w;
+        for (int i = tid; i < (WM == 1 ? G * 256 : 1024); i += 4 * 256) {     // WM 2: chunk 0
+            u32x4 v[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) v[u] = w[min(i + u * 256, G * 256 - 1)];
+#pragma unroll
+            for (int u = 0; u < 4; ++u)
+                if (i + u * 256 < G * 256) s_w[wperm(i + u * 256)] = v[u];
+        }
+    }
+    __syncthreads();
 
     for (;;) {
         i32x16 acc[U][4];
