@@ -125,7 +125,7 @@ typedef struct D8sBlockArgs {
  * src/knee/dense8s_kernels.cu:2365-2412), with the uint8 normalisation and flip of the input fused
  * into the load (the role of `gather_u8_to_f16`, src/knee/data/fused_uint8.py:480-506).
  *   x      input [N][3][H][W]: uint8 when kind = D8S_IN_U8 (x16 = lut[c][u]; 4-byte aligned), fp16
- *          when kind = D8S_IN_F16 (used as is);
+ *          when kind = D8S_IN_F16 (used as is; 8-byte aligned when W <= 512);
  *   lut    [3][256] fp16 (kind = D8S_IN_U8 only);
  *   w16    [64][168] fp16, norm0 folded in, k = (channel * 7 + ky) * 8 + kx + 1 and k % 8 = 0
  *          zero: the reference's `S_w16` table (src/knee/dense8s.py:522-530);
@@ -188,7 +188,8 @@ int d8s_transition(const D8sGemmArgs* a, void* stream);
 int d8s_final(const int8_t* in0, int32_t G0, const int8_t* seg, int32_t N, int32_t HW,
               const float* ab, float* out, int32_t ctot, void* stream);
 
-/* Stem (see D8sStemArgs).  H and W multiples of 4. */
+/* Stem (see D8sStemArgs).  H and W multiples of 4.  Widths up to 512 run a row-band kernel (pooling
+ * in registers, one quantisation per pooled value), wider ones a tile kernel; both give the same bytes. */
 int d8s_stem(const D8sStemArgs* a, void* stream);
 
 /* Library identification: "d8s-hip <abi> <source hash> gfx950". */

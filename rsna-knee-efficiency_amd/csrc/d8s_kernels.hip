@@ -1640,6 +1640,297 @@ __global__ __launch_bounds__(256) void k_stem(D8sStemArgs a, int tiles_x, int ti
 }
 
 // ------------------------------------------------------------------------------------------------
+// Stem, row-band form (W <= 512): the same conv, quantisation and pool as k_stem, for a workgroup
+// that owns SR rows of pooled output of one image across the whole width.  Wave w computes conv
+// columns 32 w .. 32 w + 31; B-operand column n holds conv column 32 w + 2 n (n < 16) or
+// 32 w + 2 (n - 16) + 1 (n >= 16), even columns in the first 16 lanes of each half, odd columns in
+// the last 16.  Per pooled row py a wave computes conv rows 2 py and 2 py + 1 (row 2 py - 1 is the
+// previous pooled row's second row) and pools in registers:
+//   * the max over the three conv rows, per lane;
+//   * v_permlane16_swap pairs each even column (the window's centre) with the odd column to its
+//     right in one lane (lanes 0-15 of each half for output tile 1, lanes 16-31 for tile 0), and a
+//     DPP row shift brings the odd column to its left; lane 0 of a row takes the previous wave's
+//     last column through LDS (zero at the image's edge).
+// Quantisation q = RNE(min(max(y, 0) inv, 127)) with inv > 0 is monotonic, so it commutes with the
+// max: only the pooled values are quantised, giving the same bytes as quantising every conv pixel
+// and pooling the bytes; 0 stands for the padding (q(0) = 0 is the least byte).
+// K order and weights in LDS as in k_stem (identical fp32 sums, so identical bytes); a lane's row
+// offset per K step is one of four per-lane bases plus an immediate.
+// Input rows: a ring of 16 rows per channel in LDS, each row stored twice (slots r & 15 and
+// (r & 15) + 16) so that the 13 rows a pooled row reads are consecutive slots.  The rows a pooled
+// row adds (4 per channel) are fetched into registers two pooled rows ahead (uint8 through the LUT
+// into fp16, mirrored on the way when the image is flipped).
+// ------------------------------------------------------------------------------------------------
+static constexpr int SR_NWV = 8;                           // waves at most: 256 conv columns
+static constexpr int SR_RS = 288;                          // ring row stride (dwords, = 32 mod 64)
+static constexpr int SR_CH = 32 * SR_RS + 32;              // ring channel stride (dwords, = 32 mod 64)
+static constexpr int SR_WROW = 184;                        // fp16 per weight row (176 used)
+static constexpr size_t SR_LDS = (size_t)3 * SR_CH * 4 + 64 * SR_WROW * 2 + (2 * SR_NWV * 64 + 16 + 128) * 4
+                                 + 3 * 256 * 2;
+
+// One unit of an input row: 4 fp16 values of channel c, row y, landing at columns 4 D .. 4 D + 3
+// (mirrored: source columns W - 4 D - 4 .. W - 4 D - 1 reversed).  Rows outside the image: 0.
+struct SrUnit {
+    u32x2 raw;
+    bool ok;
+};
+
+// (valid = false: an unused unit of the thread; it loads element 0 and is never stored.)  e0: the
+// element offset of the unit in row 0; the input has fewer than 2^31 elements.
+template <bool U8>
+DEV SrUnit sr_fetch(const void* x, int H, int W, int e0, int y, bool valid) {
+    SrUnit u;
+    u.ok = valid && (unsigned)y < (unsigned)H;
+    const int e = u.ok ? e0 + y * W : 0;
+    if (U8) u.raw = u32x2{*(const uint32_t*)((const uint8_t*)x + e), 0u};
+    else u.raw = *(const u32x2*)((const uint16_t*)x + e);
+    return u;
+}
+
+// element offset of unit D of row 0 of channel c of source image ns
+DEV int sr_e0(int ns, int c, int H, int W, int D, bool mirror) {
+    return ((ns * 3 + c) * H) * W + 4 * (mirror ? (W >> 2) - 1 - D : D);
+}
+
+DEV uint32_t lut2(const _Float16* lt, uint32_t b0, uint32_t b1) {
+    return (uint32_t)__builtin_bit_cast(uint16_t, lt[b0]) | ((uint32_t)__builtin_bit_cast(uint16_t, lt[b1]) << 16);
+}
+
+// q0: the unit's dword offset in ring slot 0 (channel c, column unit D: c SR_CH + 2 + 2 D)
+template <bool U8>
+DEV void sr_put(uint32_t* s_ring, const _Float16* s_lut, bool mirror, SrUnit u, int c, int q0, int y) {
+    uint32_t lo, hi;
+    if (U8) {
+        const _Float16* lt = s_lut + 256 * c;
+        const uint32_t v = u.raw.x;
+        const uint32_t b0 = v & 255u, b1 = (v >> 8) & 255u, b2 = (v >> 16) & 255u, b3 = v >> 24;
+        lo = mirror ? lut2(lt, b3, b2) : lut2(lt, b0, b1);
+        hi = mirror ? lut2(lt, b1, b0) : lut2(lt, b2, b3);
+    } else {
+        lo = mirror ? __builtin_amdgcn_alignbit(u.raw.y, u.raw.y, 16) : u.raw.x;
+        hi = mirror ? __builtin_amdgcn_alignbit(u.raw.x, u.raw.x, 16) : u.raw.y;
+    }
+    lo = u.ok ? lo : 0u;
+    hi = u.ok ? hi : 0u;
+    uint32_t* p = s_ring + q0 + (y & 15) * SR_RS;
+    *(u32x2*)p = u32x2{lo, hi};
+    *(u32x2*)(p + 16 * SR_RS) = u32x2{lo, hi};
+}
+
+// B operand: 8 fp16 at a 4-byte aligned LDS byte address.
+DEV f16x8 sr_b(const uint8_t* p) {
+    const uint32_t* q = (const uint32_t*)p;
+    return __builtin_bit_cast(f16x8, u32x4{q[0], q[1], q[2], q[3]});
+}
+
+// Conv rows whose input windows start at ring slot sb (and sb + 2 for the second row): accumulators
+// (r0t0, r0t1) and (r1t0, r1t1) for output tiles 0 and 1, started from the bias.  K step s, lane half
+// h covers row rk = 2 s + h of the (channel, ky) rows (the order of k_stem, so the sums are the same):
+// h = 1 reads the next ky of the same channel except at s = 3 (channel 0 ky 6 / channel 1 ky 0) and
+// s = 10 (rk 21 is a zero weight row: it reads rk 20 again).  pA: channels 0-1, + h rows; pB: + h
+// (channel - 6 rows); pC: channel 2, + h rows; pD: channel 2.
+DEV f32x16 ld16(const float* p) {                         // 16 result rows of a lane (4 x 4 channels)
+    f32x16 r;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const float4 v = *(const float4*)(p + 8 * q);
+        r[4 * q] = v.x; r[4 * q + 1] = v.y; r[4 * q + 2] = v.z; r[4 * q + 3] = v.w;
+    }
+    return r;
+}
+
+template <bool TWO>
+DEV void sr_rows(const uint8_t* pA, const uint8_t* pB, const uint8_t* pC, const uint8_t* pD, const _Float16* wl,
+                 const float* bl, f32x16& r0t0, f32x16& r0t1, f32x16& r1t0, f32x16& r1t1) {
+    const f32x16 bias0 = ld16(bl), bias1 = ld16(bl + 32);
+#pragma unroll
+    for (int s = 0; s < 11; ++s) {
+        const uint8_t* rp = s < 3    ? pA + 2 * s * SR_RS * 4
+                            : s == 3 ? pB + 6 * SR_RS * 4
+                            : s < 7  ? pA + SR_CH * 4 + (2 * s - 7) * SR_RS * 4
+                            : s < 10 ? pC + (2 * s - 14) * SR_RS * 4
+                                     : pD + 6 * SR_RS * 4;
+        const f16x8 w0 = *(const f16x8*)(wl + 16 * s);
+        const f16x8 w1 = *(const f16x8*)(wl + 32 * SR_WROW + 16 * s);
+        const f16x8 b0 = sr_b(rp);
+        r0t0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(w0, b0, s == 0 ? bias0 : r0t0, 0, 0, 0);
+        r0t1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(w1, b0, s == 0 ? bias1 : r0t1, 0, 0, 0);
+        if (TWO) {
+            const f16x8 b1 = sr_b(rp + 2 * SR_RS * 4);
+            r1t0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(w0, b1, s == 0 ? bias0 : r1t0, 0, 0, 0);
+            r1t1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(w1, b1, s == 0 ? bias1 : r1t1, 0, 0, 0);
+        }
+    }
+}
+
+DEV float f32_of(uint32_t x) { return __builtin_bit_cast(float, x); }
+DEV uint32_t bits_of(float x) { return __builtin_bit_cast(uint32_t, x); }
+
+// One pooled row py = py0 + T: conv rows 2 py, 2 py + 1 (into O0, O1), the ring rows of the next
+// pooled row from BUF, BUF refetched with the rows of pooled row py + 3, the pool with conv row
+// 2 py - 1 (P0, P1), quantisation and the store.  Two calls per loop iteration swap BUF and (P, O), so
+// the loop carries no register copies.
+#define SR_STEP(T, BUF, P0, P1, O0, O1)                                                                \
+    do {                                                                                             \
+        const int py_ = py0 + (T), sb_ = (4 * py_ - 3) & 15;                                         \
+        f32x16 e0_, e1_;                                                                             \
+        {                                                                                            \
+            const uint8_t* r_ = ringb + sb_ * SR_RS * 4;                                             \
+            sr_rows<true>(r_ + offA, r_ + offB, r_ + offC, r_ + offD, wl, bl, e0_, e1_, O0, O1);  \
+        }                                                                                            \
+        if ((T) + 1 < npy) {                                                                         \
+            _Pragma("unroll") for (int k = 0; k < 3; ++k) if (uv[k])                                 \
+                sr_put<U8>(s_ring, s_lut, mirror, BUF[k], uc[k], uq[k], 4 * (py_ + 1) + 2 + um[k]);  \
+        }                                                                                            \
+        _Pragma("unroll") for (int k = 0; k < 3; ++k)                                                \
+            BUF[k] = sr_fetch<U8>(a.x, a.H, a.W, ue[k], 4 * (py_ + 3) + 2 + um[k],                  \
+                                  uv[k] && (T) + 3 < npy);                                           \
+        f32x16 c_, r_;                                                                               \
+        _Pragma("unroll") for (int v = 0; v < 16; ++v) {                                             \
+            const float m0_ = __builtin_fmaxf(__builtin_fmaxf(P0[v], e0_[v]), O0[v]);               \
+            const float m1_ = __builtin_fmaxf(__builtin_fmaxf(P1[v], e1_[v]), O1[v]);               \
+            const auto sw_ = __builtin_amdgcn_permlane16_swap(bits_of(m1_), bits_of(m0_), false, false); \
+            c_[v] = f32_of(sw_[0]);                                                                  \
+            r_[v] = f32_of(sw_[1]);                                                                  \
+        }                                                                                            \
+        float* hb_ = s_halo + ((T) & 1) * SR_NWV * 64;                                               \
+        if (i == 15) {                                                                               \
+            float* hp_ = hb_ + (wave * 4 + rr + 2 * h) * 16;                                         \
+            _Pragma("unroll") for (int q = 0; q < 4; ++q)                                            \
+                *(float4*)(hp_ + 4 * q) = float4{r_[4 * q], r_[4 * q + 1], r_[4 * q + 2], r_[4 * q + 3]}; \
+        }                                                                                            \
+        __syncthreads();                                                                             \
+        const float* hl_ = (i == 0 && wave > 0) ? hb_ + ((wave - 1) * 4 + rr + 2 * h) * 16           \
+                                                : s_halo + 2 * SR_NWV * 64;                          \
+        const f32x16 invq = ld16(il);                                                                \
+        uint32_t dw_[4];                                                                             \
+        _Pragma("unroll") for (int q = 0; q < 4; ++q) {                                              \
+            const float4 hv_ = *(const float4*)(hl_ + 4 * q);                                        \
+            const float hq_[4] = {hv_.x, hv_.y, hv_.z, hv_.w};                                       \
+            uint32_t d_ = 0u;                                                                        \
+            _Pragma("unroll") for (int e = 0; e < 4; ++e) {                                          \
+                const int v = 4 * q + e;                                                             \
+                const float p_ = __builtin_fmaxf(__builtin_fmaxf(c_[v], r_[v]), hq_[e]);            \
+                const float l_ = f32_of((uint32_t)__builtin_amdgcn_update_dpp(                       \
+                    (int)bits_of(p_), (int)bits_of(r_[v]), 0x111, 0xf, 0xf, false));                 \
+                const float m_ = __builtin_amdgcn_fmed3f(p_, l_, 3.0e38f);    /* max of finite */    \
+                const float qv_ = __builtin_rintf(__builtin_amdgcn_fmed3f(m_ * invq[v], 0.0f, 127.0f)); \
+                d_ = __builtin_amdgcn_cvt_pk_u8_f32(qv_, e, d_);                                     \
+            }                                                                                        \
+            dw_[q] = d_;                                                                             \
+        }                                                                                            \
+        const auto s02_ = __builtin_amdgcn_permlane32_swap(dw_[0], dw_[2], false, false);            \
+        const auto s13_ = __builtin_amdgcn_permlane32_swap(dw_[1], dw_[3], false, false);            \
+        if (px < Wp)                                                                                 \
+            *(u32x4*)(a.out + ((((int64_t)n * 2 + (1 - rr)) * Hp + py_) * Wp + px) * 32 + 16 * h) =  \
+                u32x4{s02_[0], s02_[1], s13_[0], s13_[1]};                                           \
+    } while (0)
+
+template <bool U8>
+__global__ __launch_bounds__(512, 1) void k_stem_rows(D8sStemArgs a, int bands, int band_rows) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    uint32_t* s_ring = (uint32_t*)smem;                                 // [3][SR_CH]
+    _Float16* s_wt = (_Float16*)(s_ring + 3 * SR_CH);                   // [64][SR_WROW]
+    float* s_halo = (float*)(s_wt + 64 * SR_WROW);                      // [2][SR_NWV][4][16], 16 zeros
+    float* s_bias = s_halo + 2 * SR_NWV * 64 + 16;                      // [64]
+    float* s_inv = s_bias + 64;                                         // [64]
+    _Float16* s_lut = (_Float16*)(s_inv + 64);                          // [3][256]
+    const int nt = blockDim.x, tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int h = lane >> 5, j = lane & 31, rr = j >> 4, i = j & 15;
+    const int Hp = a.H >> 2, Wp = a.W >> 2, W4 = a.W >> 2;
+    const int n = blockIdx.x / bands, band = blockIdx.x - n * bands;
+    const int py0 = band * band_rows, npy = min(band_rows, Hp - py0);
+    const int half = a.N >> 1;
+    const int ns = (a.flip == 2 && n >= half) ? n - half : n;          // source image
+    const bool mirror = a.flip == 1 || (a.flip == 2 && n >= half);
+
+    // ring zeros (the column padding is never written again), weights, bias, inv, LUT
+    for (int k = tid; k < 3 * SR_CH / 4; k += nt) ((u32x4*)s_ring)[k] = u32x4{0u, 0u, 0u, 0u};
+    if (tid < 16) s_halo[2 * SR_NWV * 64 + tid] = 0.0f;
+    for (int k = tid; k < 64 * 22; k += nt) {                          // [64][168] + zero K 168..175
+        const int o = k / 22, rk = k - o * 22;
+        u32x4 v = {0u, 0u, 0u, 0u};
+        if (rk < 21) v = ((const u32x4*)a.w16)[o * 21 + rk];
+        *(u32x4*)(s_wt + o * SR_WROW + 8 * rk) = v;
+    }
+    if (tid < 64) {
+        s_bias[tid] = a.bias[tid];
+        s_inv[tid] = a.inv[tid];
+    }
+    if (U8)
+        for (int k = tid; k < 3 * 256; k += nt) s_lut[k] = __builtin_bit_cast(_Float16, a.lut[k]);
+    __syncthreads();
+
+    // rows 4 py0 - 5 .. 4 py0 + 5: the first pooled row's window and the conv row above it
+    {
+        constexpr int KI = 9;                                           // 33 W/4 units over >= W threads
+        SrUnit u[KI];
+#pragma unroll
+        for (int k = 0; k < KI; ++k) {
+            const int q = tid + k * nt, rb = q / W4, D = q - rb * W4, c = rb / 11;
+            u[k] = sr_fetch<U8>(a.x, a.H, a.W, sr_e0(ns, c, a.H, a.W, D, mirror), 4 * py0 - 5 + (rb - 11 * c),
+                                q < 33 * W4);
+        }
+#pragma unroll
+        for (int k = 0; k < KI; ++k) {
+            const int q = tid + k * nt, rb = q / W4, D = q - rb * W4, c = rb / 11;
+            if (q < 33 * W4)
+                sr_put<U8>(s_ring, s_lut, mirror, u[k], c, c * SR_CH + 2 + 2 * D, 4 * py0 - 5 + (rb - 11 * c));
+        }
+    }
+    // this thread's units of the 4 rows per channel a pooled row adds: (channel, row m, column unit)
+    int uc[3], um[3], ue[3], uq[3];
+    bool uv[3];
+#pragma unroll
+    for (int k = 0; k < 3; ++k) {
+        const int q = tid + k * nt, rb = q / W4, D = q - rb * W4;
+        uv[k] = q < 12 * W4;
+        uc[k] = rb >> 2;
+        um[k] = rb & 3;
+        ue[k] = sr_e0(ns, rb >> 2, a.H, a.W, D, mirror);
+        uq[k] = (rb >> 2) * SR_CH + 2 + 2 * D;
+    }
+    // rows added by pooled row py0 + t: 4 (py0 + t) + 2 + m; na holds those of odd t, nb of even t
+    SrUnit na[3], nb[3];
+#pragma unroll
+    for (int k = 0; k < 3; ++k) {
+        na[k] = sr_fetch<U8>(a.x, a.H, a.W, ue[k], 4 * (py0 + 1) + 2 + um[k], uv[k] && npy > 1);
+        nb[k] = sr_fetch<U8>(a.x, a.H, a.W, ue[k], 4 * (py0 + 2) + 2 + um[k], uv[k] && npy > 2);
+    }
+
+    // per-lane constants
+    const int cx = 32 * wave + (rr ? 2 * i + 1 : 2 * i);                // this B column's conv column
+    const int px = 16 * wave + i;                                       // this lane's pooled column
+    const uint8_t* ringb = (const uint8_t*)s_ring;
+    const int offA = 4 * cx + h * SR_RS * 4;
+    const int offB = 4 * cx + h * (SR_CH - 6 * SR_RS) * 4;
+    const int offC = 4 * cx + 2 * SR_CH * 4 + h * SR_RS * 4;
+    const int offD = 4 * cx + 2 * SR_CH * 4;
+    const _Float16* wl = s_wt + j * SR_WROW + 8 * h;
+    const float* bl = s_bias + 4 * h;                                   // this lane's result rows
+    const float* il = s_inv + 32 * (1 - rr) + 4 * h;                    // lanes 0-15: tile 1, 16-31: tile 0
+    __syncthreads();
+
+    f32x16 pa0, pa1, pb0, pb1;                                          // conv rows 2 py - 1 / 2 py + 1
+    if (py0 > 0) {
+        const int sb = (4 * py0 - 5) & 15;
+        const uint8_t* r = ringb + sb * SR_RS * 4;
+        sr_rows<false>(r + offA, r + offB, r + offC, r + offD, wl, bl, pa0, pa1, pb0, pb1);
+    } else {
+#pragma unroll
+        for (int v = 0; v < 16; ++v) pa0[v] = pa1[v] = 0.0f;
+    }
+    int t = 0;
+    for (; t + 1 < npy; t += 2) {                     // (no branch inside: exact wait counts across steps)
+        SR_STEP(t, na, pa0, pa1, pb0, pb1);
+        SR_STEP(t + 1, nb, pb0, pb1, pa0, pa1);
+    }
+    if (t < npy) SR_STEP(t, na, pa0, pa1, pb0, pb1);
+}
+#undef SR_STEP
+
+// ------------------------------------------------------------------------------------------------
 // Diagnostics
 // ------------------------------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void k_copy(const u32x4* __restrict__ src, u32x4* __restrict__ dst,
@@ -1946,7 +2237,26 @@ extern "C" int d8s_stem(const D8sStemArgs* a, void* stream) {
     REQUIRE(a->kind != D8S_IN_U8 || ((uintptr_t)a->x & 3) == 0, "d8s_stem: uint8 input not 4-byte aligned");
     REQUIRE(a->flip >= 0 && a->flip <= 2 && (a->flip != 2 || a->N % 2 == 0),
             "d8s_stem: flip must be 0, 1, or 2 (TTA pairs, N even)");
+    REQUIRE(a->kind != D8S_IN_F16 || a->W > 64 * SR_NWV || ((uintptr_t)a->x & 7) == 0,
+            "d8s_stem: fp16 input not 8-byte aligned");
     const int Hp = a->H / 4, Wp = a->W / 4;
+    if (a->W <= 64 * SR_NWV && (int64_t)(a->flip == 2 ? a->N / 2 : a->N) * 3 * a->H * a->W < (1ll << 31)) {
+        // row bands: one wave per 32 conv columns; 16 pooled rows per band while that leaves at
+        // least one workgroup per CU, else fewer
+        const int nwv = (a->W / 2 + 31) / 32;
+        int rows = 16;
+        while (rows > 2 && (int64_t)a->N * ((Hp + rows - 1) / rows) < cu_count()) rows /= 2;
+        const int bands = (Hp + rows - 1) / rows;
+        const int64_t blocks = (int64_t)a->N * bands;
+        REQUIRE(blocks < (1ll << 31), "d8s_stem: too many bands");
+        if (a->kind == D8S_IN_U8)
+            hipLaunchKernelGGL(k_stem_rows<true>, dim3((unsigned)blocks), dim3(64 * nwv), SR_LDS,
+                               (hipStream_t)stream, *a, bands, rows);
+        else
+            hipLaunchKernelGGL(k_stem_rows<false>, dim3((unsigned)blocks), dim3(64 * nwv), SR_LDS,
+                               (hipStream_t)stream, *a, bands, rows);
+        return launched("d8s_stem");
+    }
     const int tiles_x = (Wp + ST_PX - 1) / ST_PX, tiles_y = (Hp + ST_PY - 1) / ST_PY;
     const int64_t blocks = (int64_t)a->N * tiles_x * tiles_y;
     REQUIRE(blocks < (1ll << 31), "d8s_stem: too many tiles");

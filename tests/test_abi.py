@@ -78,6 +78,7 @@ def test_struct_layouts_match_header(tmp_path):
     ("d8s_stem", lambda: (ctypes.byref(hip.StemArgs(1, 0, 1, 1, 1, 1, 1, 8, 8, 1, 0, 0)), None)),
     ("d8s_stem", lambda: (ctypes.byref(hip.StemArgs(1, 1, 1, 1, 1, 1, 3, 8, 8, 1, 2, 0)), None)),
     ("d8s_stem", lambda: (ctypes.byref(hip.StemArgs(1, 1, 1, 1, 1, 1, 2, 8, 8, 1, 0, 0)), None)),
+    ("d8s_stem", lambda: (ctypes.byref(hip.StemArgs(4, 0, 1, 1, 1, 1, 1, 8, 8, 0, 0, 0)), None)),
     ("d8s_final", lambda: (1, 20, 1, 2, 256, 1, 1, 100, None)),
     ("d8s_micro_copy", lambda: (1, 1, 17, None)),
 ])

@@ -224,8 +224,9 @@ def _stem_tables(seed: int = 3):
     return w16, bias, inv, lut
 
 
-@pytest.mark.parametrize("H,W,N", [(512, 512, 2), (64, 96, 3), (20, 12, 1), (8, 4, 3)])
+@pytest.mark.parametrize("H,W,N", [(512, 512, 2), (64, 96, 3), (20, 12, 1), (8, 4, 3), (16, 576, 1)])
 def test_stem(dev, H, W, N):
+    """Widths up to 512 run the row-band kernel (k_stem_rows), wider ones the tile kernel (k_stem)."""
     w16, bias, inv, lut = _stem_tables()
     rng = np.random.default_rng(H + W)
     x = rng.integers(0, 256, (N, 3, H, W)).astype(np.uint8)
