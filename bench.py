@@ -148,8 +148,8 @@ def copy_probe(dev: torch.device, mib: int = 1024, reps: int = 5) -> dict:
 
 
 FAMILY = {"k_conv1": "conv1", "k_conv1p": "conv1", "k_conv2": "conv2", "k_dense": "dense",
-          "k_dblock": "block", "k_trans": "trans", "k_stem": "stem",
-          "k_final": "final", "k_copy": "copy"}
+          "k_band": "dense", "k_dblock": "block", "k_trans": "trans", "k_stem": "stem",
+          "k_stem_rows": "stem", "k_final": "final", "k_copy": "copy"}
 
 
 def _family(name: str) -> str | None:

@@ -21,6 +21,9 @@ HIPCC_FLAGS = [
     "-ffp-contract=off",
     # no packed fp32 arithmetic
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # `#pragma unroll` loops unrolled in full also when large (the fused kernels' interleaved K loops:
+    # a partly unrolled one computes its LDS addresses at run time)
+    "-mllvm", "-pragma-unroll-threshold=100000",
 ]
 
 

@@ -99,10 +99,45 @@ DEV u32x4 pro16(u32x4 x, u32x4 p0, u32x4 p1, u32x4 p2, u32x4 p3) {
 // Lanes l and l ^ 32 hold the same pixel: lane half h = l >> 5 has channel dwords 2k + h (channels
 // 8k + 4h .. 8k + 4h + 3, k = 0..3) of a 32-channel row.  After the exchange lane half h holds the row's
 // bytes 16h .. 16h + 15 (dwords 4h .. 4h + 3).
+// (v_permlane32_swap exchanges the upper 32 lanes of its first operand with the lower 32 of its
+// second: (e0, e2) and (e1, e3) give both halves their dwords in order.)
 DEV u32x4 xchg_rows(uint32_t e0, uint32_t e1, uint32_t e2, uint32_t e3, int h) {
-    const uint32_t r1 = (uint32_t)__shfl_xor((int)(h ? e0 : e2), 32);
-    const uint32_t r2 = (uint32_t)__shfl_xor((int)(h ? e1 : e3), 32);
-    return h ? u32x4{r1, e2, r2, e3} : u32x4{e0, r1, e1, r2};
+    (void)h;
+    const auto s02 = __builtin_amdgcn_permlane32_swap(e0, e2, false, false);
+    const auto s13 = __builtin_amdgcn_permlane32_swap(e1, e3, false, false);
+    return u32x4{s02[0], s02[1], s13[0], s13[1]};
+}
+
+// Byte 0 of each of four dwords, as one dword (a0 in byte 0).
+DEV uint32_t pack_b0(uint32_t a0, uint32_t a1, uint32_t a2, uint32_t a3) {
+    return perm(a1, a0, 0x0c0c0400u) | perm(a3, a2, 0x04000c0cu);
+}
+
+// Bottleneck bytes of 4 conv1 results (rows 4q .. 4q + 3 of a lane, consecutive channels, tables
+// gd = (g, d) of those channels): low byte of fma(sat(fma(g, acc, d)), 255, 2^23 + 128), i.e.
+// u ^ 0x80 with u = RNE(255 sat(g acc + d)), the conv2 operand.
+DEV uint32_t epi1_x80(i32x16 acc, int q, float4 gd01, float4 gd23) {
+    const float g[4] = {gd01.x, gd01.z, gd23.x, gd23.z}, d[4] = {gd01.y, gd01.w, gd23.y, gd23.w};
+    uint32_t b[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const float y = __builtin_amdgcn_fmed3f(__builtin_fmaf(g[r], (float)acc[4 * q + r], d[r]), 0.0f, 1.0f);
+        b[r] = __float_as_uint(__builtin_fmaf(y, 255.0f, 8388736.0f));
+    }
+    return pack_b0(b[0], b[1], b[2], b[3]);
+}
+
+// Store bytes of 4 conv2 results (scales sc of those channels): q = RNE(clamp(float(acc) sc, -127,
+// 127)), as the low byte of q + 1.5 * 2^23 (exact: |q| <= 127).
+DEV uint32_t epi2_q(i32x16 acc, int q, float4 sc) {
+    const float s[4] = {sc.x, sc.y, sc.z, sc.w};
+    uint32_t b[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const float t = __builtin_amdgcn_fmed3f((float)acc[4 * q + r] * s[r], -127.0f, 127.0f);
+        b[r] = __float_as_uint(t + 12582912.0f);
+    }
+    return pack_b0(b[0], b[1], b[2], b[3]);
 }
 
 // LDS position of 16-byte chunk i of a [G][128][32] conv1 weight table (chunk 64 c + 2 j + h within a
@@ -1050,6 +1085,271 @@ __global__ __launch_bounds__(64 * NW, 1) void k_dense(D8sDenseArgs a, int tiles_
     }
 #undef DN_LOAD_A
 #undef DN_LOAD_B
+}
+
+// ------------------------------------------------------------------------------------------------
+// Dense layer fused over a band of rows (W = 64 or 128): conv1 and conv2 of a layer, the bottleneck
+// kept in a ring of rows in LDS.  A workgroup of 8 waves owns band_rows output rows of one image
+// across the whole width and walks down them; each step, wave w (tile row rw = w / TPR, column
+// block cb = w % TPR) computes conv1 of one 32-pixel tile of RS new bottleneck rows (all 128
+// outputs, the store read from global memory 4 groups ahead, the prefetch running on into the next
+// step), writes it to the ring (u ^ 0x80, the conv2 operand; rows outside the image: 0x80, the
+// zero padding), then conv2 of one 32-pixel tile of RS output rows from the ring.  The first step
+// of a band computes the two bottleneck rows above it; after that no pixel is computed twice.  The
+// bytes equal those of d8s_conv1 + d8s_conv2 (the same integer sums and epilogues).
+// Ring: SL = RS + 2 slots of [4 planes][PS pixels][2 halves], PS a multiple of 16 so a lane's
+// swizzled column offset does not depend on the slot or plane; columns 0 and W + 1.. hold the
+// padding.
+// ------------------------------------------------------------------------------------------------
+template <int W_>
+struct BnShape {
+    static constexpr int TPR = W_ / 32;                            // pixel tiles per row
+    static constexpr int RS = 8 / TPR;                             // rows per step (8 waves)
+    static constexpr int SL = RS + 2;                              // ring slots
+    static constexpr int PS = (W_ + 2 + 15) / 16 * 16;             // ring row stride (pixels)
+    static constexpr size_t RING = (size_t)SL * 4 * PS * 32;
+    static constexpr size_t PRM = 128 * 4 + 128 * 8 + 32 * 4 + 32 * 4;
+    static constexpr size_t lds(int G) { return RING + PRM + (size_t)G * (128 + 4096); }
+    static_assert(W_ == 64 || W_ == 128, "band widths");
+};
+
+// conv1 row of step s of a band starting at y0 (step 0: the two rows above the band)
+DEV int bn_row(int s, int y0, int rw, int RS) { return s == 0 ? y0 - 1 + rw : y0 + 1 + (s - 1) * RS + rw; }
+
+// byte offset in a store group of pixel (ry clamped to the image, x), lane half h
+DEV uint32_t bn_off(int ry, int H, int W, int x, int h) {
+    ry = ry < 0 ? 0 : (ry >= H ? H - 1 : ry);
+    return (uint32_t)((ry * W + x) * 32 + 16 * h);
+}
+
+template <int W_, int GM>
+__global__ __launch_bounds__(512, 1) void k_band(D8sDenseArgs a, int bands, int band_rows) {
+    using S = BnShape<W_>;
+    constexpr int TPR = S::TPR, RS = S::RS, SL = S::SL, PS = S::PS, NT = 512;
+    __shared__ __attribute__((aligned(16))) u32x4 s_w[4 * 9 * 32 * 2];    // conv2 weights, 36 KB
+    extern __shared__ __attribute__((aligned(16))) u32x4 s_dyn[];
+    u32x4* s_r = s_dyn;                                                    // [SL][4][PS][2]
+    int32_t* s_w1sum = (int32_t*)((uint8_t*)s_dyn + S::RING);             // [128]
+    float2* s_gd = (float2*)(s_w1sum + 128);                              // [128]
+    float* s_sc = (float*)(s_gd + 128);                                   // [32]
+    int32_t* s_w2sum = (int32_t*)(s_sc + 32);                             // [32]
+    uint32_t* s_abh = (uint32_t*)(s_w2sum + 32);                          // [G * 32]
+    const int G = a.G, G0 = a.G0, H = a.H, N = a.N;
+    u32x4* s_w1 = (u32x4*)(s_abh + G * 32);                               // [G * 256]
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int h = lane >> 5, j = lane & 31;
+    const int rw = wave / TPR, cb = wave - rw * TPR;
+    const int x = 32 * cb + j;
+    const int n = blockIdx.x / bands, band = blockIdx.x - n * bands;
+    const int y0 = band * band_rows, nr = min(band_rows, H - y0);
+    const int M = (nr + RS - 1) / RS;                                     // conv2 steps
+    const int64_t HW = (int64_t)H * W_;
+
+    {
+        constexpr int NCH = (2304 + NT - 1) / NT;
+        u32x4 wv[NCH];
+        const u32x4* w2 = (const u32x4*)a.w2;
+#pragma unroll
+        for (int k = 0; k < NCH; ++k) wv[k] = w2[min(tid + NT * k, 2303)];
+#pragma unroll
+        for (int k = 0; k < NCH; ++k)
+            if (tid + NT * k < 2304) s_w[swz((tid + NT * k) >> 1, tid & 1)] = wv[k];
+    }
+    if (tid < 128) {                                   // the sums times 128: the accumulators' start
+        s_w1sum[tid] = 128 * a.w1sum[tid];
+        s_gd[tid] = ((const float2*)a.gd)[tid];
+    } else if (tid < 160) {
+        s_sc[tid - 128] = a.sc[tid - 128];
+        s_w2sum[tid - 128] = 128 * a.w2sum[tid - 128];
+    }
+    {
+        const uint32_t* abh32 = (const uint32_t*)a.abh;
+        for (int i = tid; i < G * 32; i += NT) s_abh[i] = abh32[i];
+        const u32x4* w1 = (const u32x4*)a.w1;
+        for (int i = tid; i < G * 256; i += 4 * NT) {
+            u32x4 v[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) v[u] = w1[min(i + u * NT, G * 256 - 1)];
+#pragma unroll
+            for (int u = 0; u < 4; ++u)
+                if (i + u * NT < G * 256) s_w1[wperm(i + u * NT)] = v[u];
+        }
+        // padding columns of every ring row: 0 and W + 1 .. PS - 1
+        constexpr int NPAD = PS - W_;
+        const u32x4 pad = {SIGN4, SIGN4, SIGN4, SIGN4};
+        for (int i = tid; i < SL * 4 * NPAD * 2; i += NT) {
+            const int row = i / (NPAD * 2), rem = i - row * (NPAD * 2), p = rem >> 1, hh = rem & 1;
+            const int xx = p == 0 ? 0 : W_ + p;
+            s_r[row * PS * 2 + swz(xx, hh)] = pad;
+        }
+    }
+
+    const uint8_t* in0n = (const uint8_t*)a.in0 + (int64_t)n * G0 * HW * 32;
+    const uint8_t* segn = (const uint8_t*)a.seg + (int64_t)n * HW * 32;
+    const int64_t grp = HW * 32, seg_slot = (int64_t)N * HW * 32;
+    // ra: the step's G groups (GM >= G registers; past G, group G - 1 again, unused), each reloaded
+    // with the next step's group right after its prologue
+    u32x4 ra[GM], rb[4];
+#define BN_LOAD_B(g)                                                                              \
+    do {                                                                                          \
+        const u32x4* p_ = (const u32x4*)s_w1 + j + 32 * h + (g) * 256;                           \
+        _Pragma("unroll") for (int c_ = 0; c_ < 4; ++c_) rb[c_] = p_[64 * c_];                    \
+    } while (0)
+    // group k (clamped to G - 1) at pixel offset o; unconditional, so the compiler counts the loads
+    // in flight instead of draining them
+#define BN_LOAD_A(k, o)                                                                           \
+    do {                                                                                          \
+        const int g_ = (k) < G ? (k) : G - 1;                                                     \
+        const uint8_t* b_ = g_ < G0 ? in0n + g_ * grp : segn + (int64_t)(g_ - G0) * seg_slot;     \
+        ra[k] = *(const u32x4*)(b_ + (o));                                                        \
+    } while (0)
+    // conv1 K step k of this step (a step past G multiplies a zero operand: no branch in the loop,
+    // whose loads would then all be drained), the register reloaded with the next step's group
+#define BN_K(k)                                                                                   \
+    do {                                                                                          \
+        const int kc_ = (k) < GM - 1 ? (k) : G - 1;      /* G is GM or GM - 1 */                  \
+        BN_LOAD_B(kc_);                                                                           \
+        const u32x4* pp_ = (const u32x4*)(s_abh + kc_ * 32 + h * 16);                             \
+        u32x4 bx_ = pro16(ra[k], pp_[0], pp_[1], pp_[2], pp_[3]);                                 \
+        if ((k) == GM - 1) bx_ &= kmask;                  /* bitwise: keeps the code branch-free */ \
+        BN_LOAD_A(k, no);                                                                         \
+        _Pragma("unroll") for (int c_ = 0; c_ < 4; ++c_) acc[c_] = mfma_i8(rb[c_], bx_, acc[c_]); \
+    } while (0)
+#define BN_INIT1()                                                                                \
+    _Pragma("unroll") for (int c_ = 0; c_ < 4; ++c_)                                              \
+        _Pragma("unroll") for (int v_ = 0; v_ < 16; ++v_) acc[c_][v_] = s_w1sum[32 * c_ + res_row(v_, h)]
+    // conv1 results -> bottleneck bytes (u ^ 0x80; 0x80 for rows outside the image), before the
+    // barrier; written to the ring after it
+#define BN_EPI1()                                                                                 \
+    do {                                                                                          \
+        const uint32_t pm_ = (unsigned)ry >= (unsigned)H ? ~0u : 0u;                              \
+        _Pragma("unroll") for (int c_ = 0; c_ < 4; ++c_) {                                        \
+            uint32_t e_[4];                                                                       \
+            _Pragma("unroll") for (int q_ = 0; q_ < 4; ++q_) {                                    \
+                const float4* pg_ = (const float4*)(s_gd + 32 * c_ + 8 * q_ + 4 * h);             \
+                e_[q_] = (epi1_x80(acc[c_], q_, pg_[0], pg_[1]) & ~pm_) | (SIGN4 & pm_);          \
+            }                                                                                     \
+            brow[c_] = xchg_rows(e_[0], e_[1], e_[2], e_[3], h);                                  \
+        }                                                                                         \
+    } while (0)
+#define BN_RING_WRITE()                                                                           \
+    do {                                                                                          \
+        const int dst_ = (((ry + 1) % SL) * 4) * PS * 2 + swz(x + 1, h);                          \
+        _Pragma("unroll") for (int c_ = 0; c_ < 4; ++c_) s_r[dst_ + c_ * PS * 2] = brow[c_];      \
+    } while (0)
+    // conv2 of output row yo: ring rows yo - 1 .. yo + 1; step st = (plane, tap).  Operand addresses
+    // are per-lane pointers plus immediates (weights: swz(K * 32 + j, h) = 64 K + swz(j, h)); two
+    // accumulators (planes 0-1, 2-3) halve the dependent MFMA chain.
+#define BN_C2_FETCH(st, sl)                                                                       \
+    do {                                                                                          \
+        const int c_ = (st) / 9, tap_ = (st) % 9, dy_ = tap_ / 3, dx_ = tap_ % 3;                 \
+        const u32x4* pr_ = dy_ == 0 ? (dx_ == 0 ? p00 : dx_ == 1 ? p01 : p02)                     \
+                         : dy_ == 1 ? (dx_ == 0 ? p10 : dx_ == 1 ? p11 : p12)                     \
+                                    : (dx_ == 0 ? p20 : dx_ == 1 ? p21 : p22);                    \
+        aw[sl] = pw2[64 * (c_ * 9 + tap_)];                                                       \
+        bq[sl] = pr_[c_ * PS * 2];                                                                \
+    } while (0)
+#define BN_C2_SETUP(yo_)                                                                          \
+    const int yo = (yo_);                                                                         \
+    const u32x4* q0_ = s_r + ((yo + 0) % SL) * 4 * PS * 2;                                        \
+    const u32x4* q1_ = s_r + ((yo + 1) % SL) * 4 * PS * 2;                                        \
+    const u32x4* q2_ = s_r + ((yo + 2) % SL) * 4 * PS * 2;                                        \
+    const u32x4 *p00 = q0_ + sx0, *p01 = q0_ + sx1, *p02 = q0_ + sx2;                             \
+    const u32x4 *p10 = q1_ + sx0, *p11 = q1_ + sx1, *p12 = q1_ + sx2;                             \
+    const u32x4 *p20 = q2_ + sx0, *p21 = q2_ + sx1, *p22 = q2_ + sx2;                             \
+    i32x16 acc2, acc2b;                                                                           \
+    _Pragma("unroll") for (int v_ = 0; v_ < 16; ++v_) {                                           \
+        acc2[v_] = s_w2sum[res_row(v_, h)];                                                       \
+        acc2b[v_] = 0;                                                                            \
+    }                                                                                             \
+    u32x4 aw[2], bq[2];                                                                           \
+    BN_C2_FETCH(0, 0)
+#define BN_C2_STEP(st)                                                                            \
+    do {                                                                                          \
+        if ((st) + 1 < 36) BN_C2_FETCH((st) + 1, ((st) + 1) & 1);                                 \
+        if ((st) < 18) acc2 = mfma_i8(aw[(st) & 1], bq[(st) & 1], acc2);                          \
+        else acc2b = mfma_i8(aw[(st) & 1], bq[(st) & 1], acc2b);                                  \
+    } while (0)
+#define BN_C2_STORE()                                                                             \
+    do {                                                                                          \
+        acc2 += acc2b;                                                                            \
+        uint32_t e_[4];                                                                           \
+        _Pragma("unroll") for (int q_ = 0; q_ < 4; ++q_)                                          \
+            e_[q_] = epi2_q(acc2, q_, *(const float4*)(s_sc + 8 * q_ + 4 * h));                   \
+        const u32x4 row_ = xchg_rows(e_[0], e_[1], e_[2], e_[3], h);                              \
+        if (yo < y0 + nr) *(u32x4*)(a.out + (((int64_t)n * H + yo) * W_ + x) * 32 + 16 * h) = row_; \
+    } while (0)
+
+    if (G < GM - 1 || G > GM) __builtin_unreachable();
+    const uint32_t km = G == GM ? ~0u : 0u;            // K step GM - 1: real, or a zero operand
+    const u32x4 kmask = {km, km, km, km};
+    int ry = bn_row(0, y0, rw, RS);
+    uint32_t no = bn_off(bn_row(1, y0, rw, RS), H, W_, x, h);
+    {
+        const uint32_t co = bn_off(ry, H, W_, x, h);
+#pragma unroll
+        for (int k = 0; k < GM; ++k) BN_LOAD_A(k, co);
+    }
+    // conv2: the lane's swizzled offsets of ring columns x + dx (dx = 0, 1, 2), its weight rows
+    const int sx0 = swz(x, h), sx1 = swz(x + 1, h), sx2 = swz(x + 2, h);
+    const u32x4* pw2 = s_w + swz(j, h);
+    i32x16 acc[4];
+    u32x4 brow[4];
+    __syncthreads();                                   // tables, weights, padding
+
+    // steps 0 and 1: conv1 only (step 0: the two rows above the band, waves of tile rows 0-1)
+    for (int s = 0; s < 2; ++s) {
+        BN_INIT1();
+#pragma unroll
+        for (int k = 0; k < GM; ++k) BN_K(k);
+        BN_EPI1();
+        __syncthreads();
+        if (s > 0 || rw < 2) BN_RING_WRITE();
+        __syncthreads();
+        ry = bn_row(s + 1, y0, rw, RS);
+        no = bn_off(bn_row(s + 2, y0, rw, RS), H, W_, x, h);
+    }
+    // steps 2 .. M: conv1 of step s with conv2 of step s - 2 (rows of conv1 steps s - 2 and s - 1)
+    // interleaved: the prologue's VALU work and the 3x3's LDS reads next to each other's MFMAs
+    for (int s = 2; s <= M; ++s) {
+        BN_INIT1();
+        {
+            BN_C2_SETUP(y0 + (s - 2) * RS + rw);
+#pragma unroll
+            for (int st = 0; st < 36; ++st) {
+                BN_C2_STEP(st);
+#pragma unroll
+                for (int k = 0; k < GM; ++k)
+                    if (st == (36 * (k + 1)) / GM - 1) BN_K(k);
+            }
+            BN_EPI1();
+            BN_C2_STORE();
+        }
+        __syncthreads();                               // the ring rows of step s - 2 are read
+        BN_RING_WRITE();
+        __syncthreads();
+        ry = bn_row(s + 1, y0, rw, RS);
+        no = bn_off(bn_row(s + 2, y0, rw, RS), H, W_, x, h);
+    }
+    // conv2 of step M - 1
+    {
+        BN_C2_SETUP(y0 + (M - 1) * RS + rw);
+#pragma unroll
+        for (int st = 0; st < 36; ++st) BN_C2_STEP(st);
+        BN_C2_STORE();
+    }
+#undef BN_C2_STORE
+#undef BN_C2_STEP
+#undef BN_C2_SETUP
+#undef BN_C2_FETCH
+#undef BN_RING_WRITE
+#undef BN_EPI1
+#undef BN_INIT1
+#undef BN_K
+#undef BN_LOAD_A
+#undef BN_LOAD_B
 }
 
 // ------------------------------------------------------------------------------------------------
@@ -2154,6 +2454,34 @@ static int dense_launch(const D8sDenseArgs* a, hipStream_t st) {
     return launched("d8s_dense");
 }
 
+// Band form for W = 64 / 128 while the layer's conv1 weights fit in LDS: bands of 32, 16, 8 .. rows
+// (a multiple of the rows per step), the largest that still gives 3 workgroups per CU.
+template <int W_>
+static int band_launch(const D8sDenseArgs* a, hipStream_t st) {
+    using S = BnShape<W_>;
+    const size_t shm = S::lds(a->G);
+    if (shm + 36864 > 160 * 1024 || a->G > 16) return -1;
+    int rows = 32;
+    while (rows > S::RS && (int64_t)a->N * ((a->H + rows - 1) / rows) < 3 * (int64_t)cu_count()) rows /= 2;
+    const int bands = (a->H + rows - 1) / rows;
+    const int64_t blocks = (int64_t)a->N * bands;
+    REQUIRE(blocks < (1ll << 31), "d8s_dense: too many bands");
+    const int gm = (a->G + 1) & ~1;                        // activation registers: G rounded up to even
+#define BN_LAUNCH(GM_) hipLaunchKernelGGL((k_band<W_, GM_>), dim3((unsigned)blocks), dim3(512), shm, st, *a, bands, rows)
+    switch (gm) {
+        case 2: BN_LAUNCH(2); break;
+        case 4: BN_LAUNCH(4); break;
+        case 6: BN_LAUNCH(6); break;
+        case 8: BN_LAUNCH(8); break;
+        case 10: BN_LAUNCH(10); break;
+        case 12: BN_LAUNCH(12); break;
+        case 14: BN_LAUNCH(14); break;
+        default: BN_LAUNCH(16); break;
+    }
+#undef BN_LAUNCH
+    return launched("d8s_dense");
+}
+
 extern "C" int d8s_dense(const D8sDenseArgs* a, void* stream) {
     REQUIRE(a != nullptr, "d8s_dense: null arguments");
     REQUIRE(a->in0 && a->w1 && a->abh && a->gd && a->w1sum && a->w2 && a->sc && a->w2sum && a->out,
@@ -2164,6 +2492,10 @@ extern "C" int d8s_dense(const D8sDenseArgs* a, void* stream) {
     REQUIRE(a->G <= 512, "d8s_dense: more than 512 groups");
     REQUIRE((int64_t)a->H * a->W <= (1 << 26), "d8s_dense: more than 2^26 pixels per image");
     hipStream_t st = (hipStream_t)stream;
+    if (a->W == 128 || a->W == 64) {
+        const int rc = a->W == 128 ? band_launch<128>(a, st) : band_launch<64>(a, st);
+        if (rc >= 0) return rc;
+    }
     if (a->W >= 32) return dense_launch<32, 12, 2, 8>(a, st);
     if (a->W <= 16 && a->H <= 16) return dense_launch<16, 16, 1, 8>(a, st);
     return dense_launch<16, 12, 1, 8>(a, st);

@@ -459,13 +459,24 @@ def img_fits(b: dict) -> bool:
     return b["h"] * b["w"] <= IMG_MAX_PX and b["c0"] // GROUP + b["L"] - 1 <= IMG_MAX_GROUPS
 
 
+BAND_W = 128                    # d8s_dense runs its band form, faster than two launches, at this width
+BAND_MAX_GROUPS = 16            # (the conv1 weights of the layer in LDS)
+
+
+def band_fits(b: dict) -> bool:
+    """Whether every layer of block `b` (meta) runs d8s_dense's band form at its best width."""
+    return b["w"] == BAND_W and b["c0"] // GROUP + b["L"] - 1 <= BAND_MAX_GROUPS
+
+
 def fused_blocks(meta: dict, fused=None) -> dict:
     """{block: kind} for every block.  `fused` None -> the default: "img" where the block fits it (the
-    16 x 16 maps: one launch instead of 64, no bottleneck in memory), else "conv"; a dict {block: kind}
-    (other blocks "conv"); an iterable of blocks -> "tile" for those."""
+    16 x 16 maps: one launch instead of 64, no bottleneck in memory), "tile" for 128-wide blocks (the
+    fused layer's band form), else "conv"; a dict {block: kind} (other blocks "conv"); an iterable of
+    blocks -> "tile" for those."""
     nb = len(meta["blocks"])
     if fused is None:
-        return {bi: ("img" if img_fits(b) else "conv") for bi, b in enumerate(meta["blocks"])}
+        return {bi: ("img" if img_fits(b) else "tile" if band_fits(b) else "conv")
+                for bi, b in enumerate(meta["blocks"])}
     req = dict(fused) if isinstance(fused, dict) else {int(b): "tile" for b in fused}
     out = {bi: "conv" for bi in range(nb)}
     for bi, kind in req.items():

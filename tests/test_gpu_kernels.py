@@ -121,6 +121,11 @@ def test_conv2_tile_variants(dev, N, H, W):
     (20, 12, 160, 64, 2),
     (33, 70, 128, 64, 2),        # wide, ragged in both directions
     (5, 7, 64, 32, 3),           # tiny
+    (37, 128, 160, 64, 2),       # band form (W = 128): odd height, last band one row
+    (40, 64, 96, 64, 3),         # band form (W = 64): height not a multiple of the band
+    (128, 64, 64, 32, 1),        # band form: 2 groups, G0 = 1
+    (6, 128, 64, 64, 2),         # band form: a band taller than the image
+    (16, 64, 512, 64, 1),        # W = 64 with 16 groups: conv1 weights too large for the band form
 ])
 def test_dense_layer(dev, H, W, C, c0, N):
     """d8s_dense (conv1 + conv2 fused, bottleneck in LDS): the bytes of the exact conv1 -> conv2 and of
