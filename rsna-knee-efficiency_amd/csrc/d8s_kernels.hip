@@ -1122,8 +1122,11 @@ DEV uint32_t bn_off(int ry, int H, int W, int x, int h) {
     return (uint32_t)((ry * W + x) * 32 + 16 * h);
 }
 
+// (LDS allows one workgroup, i.e. two waves per SIMD: the register budget is 256, and the scheduler
+// is told so, or it sinks the prefetched LDS operands next to their MFMAs to save registers)
 template <int W_, int GM>
-__global__ __launch_bounds__(512, 1) void k_band(D8sDenseArgs a, int bands, int band_rows) {
+__global__ __launch_bounds__(512, 1) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void k_band(D8sDenseArgs a, int bands, int band_rows) {
     using S = BnShape<W_>;
     constexpr int TPR = S::TPR, RS = S::RS, SL = S::SL, PS = S::PS, NT = 512;
     __shared__ __attribute__((aligned(16))) u32x4 s_w[4 * 9 * 32 * 2];    // conv2 weights, 36 KB
@@ -1191,7 +1194,9 @@ __global__ __launch_bounds__(512, 1) void k_band(D8sDenseArgs a, int bands, int 
     const int64_t grp = HW * 32, seg_slot = (int64_t)N * HW * 32;
     // ra: the step's G groups (GM >= G registers; past G, group G - 1 again, unused), each reloaded
     // with the next step's group right after its prologue
-    u32x4 ra[GM], rb[4];
+    u32x4 ra[GM], rb[4], pk[4];
+    // conv2 operands read C2D steps ahead (fewer where the activation registers leave no room)
+    constexpr int C2D = GM <= 10 ? 3 : 1;
 #define BN_LOAD_B(g)                                                                              \
     do {                                                                                          \
         const u32x4* p_ = (const u32x4*)s_w1 + j + 32 * h + (g) * 256;                           \
@@ -1207,32 +1212,44 @@ __global__ __launch_bounds__(512, 1) void k_band(D8sDenseArgs a, int bands, int 
     } while (0)
     // conv1 K step k of this step (a step past G multiplies a zero operand: no branch in the loop,
     // whose loads would then all be drained), the register reloaded with the next step's group
-#define BN_K(k)                                                                                   \
+// (split in two: the LDS operands of a K step are read well before the step runs)
+#define BN_K_FETCH(k)                                                                             \
     do {                                                                                          \
         const int kc_ = (k) < GM - 1 ? (k) : G - 1;      /* G is GM or GM - 1 */                  \
         BN_LOAD_B(kc_);                                                                           \
         const u32x4* pp_ = (const u32x4*)(s_abh + kc_ * 32 + h * 16);                             \
-        u32x4 bx_ = pro16(ra[k], pp_[0], pp_[1], pp_[2], pp_[3]);                                 \
+        _Pragma("unroll") for (int c_ = 0; c_ < 4; ++c_) pk[c_] = pp_[c_];                        \
+    } while (0)
+#define BN_K_RUN(k)                                                                               \
+    do {                                                                                          \
+        u32x4 bx_ = pro16(ra[k], pk[0], pk[1], pk[2], pk[3]);                                     \
         if ((k) == GM - 1) bx_ &= kmask;                  /* bitwise: keeps the code branch-free */ \
         BN_LOAD_A(k, no);                                                                         \
         _Pragma("unroll") for (int c_ = 0; c_ < 4; ++c_) acc[c_] = mfma_i8(rb[c_], bx_, acc[c_]); \
+    } while (0)
+#define BN_K(k)                                                                                   \
+    do {                                                                                          \
+        BN_K_FETCH(k);                                                                            \
+        BN_K_RUN(k);                                                                              \
     } while (0)
 #define BN_INIT1()                                                                                \
     _Pragma("unroll") for (int c_ = 0; c_ < 4; ++c_)                                              \
         _Pragma("unroll") for (int v_ = 0; v_ < 16; ++v_) acc[c_][v_] = s_w1sum[32 * c_ + res_row(v_, h)]
     // conv1 results -> bottleneck bytes (u ^ 0x80; 0x80 for rows outside the image), before the
     // barrier; written to the ring after it
-#define BN_EPI1()                                                                                 \
+#define BN_EPI1_C(c)                                                                              \
     do {                                                                                          \
         const uint32_t pm_ = (unsigned)ry >= (unsigned)H ? ~0u : 0u;                              \
-        _Pragma("unroll") for (int c_ = 0; c_ < 4; ++c_) {                                        \
-            uint32_t e_[4];                                                                       \
-            _Pragma("unroll") for (int q_ = 0; q_ < 4; ++q_) {                                    \
-                const float4* pg_ = (const float4*)(s_gd + 32 * c_ + 8 * q_ + 4 * h);             \
-                e_[q_] = (epi1_x80(acc[c_], q_, pg_[0], pg_[1]) & ~pm_) | (SIGN4 & pm_);          \
-            }                                                                                     \
-            brow[c_] = xchg_rows(e_[0], e_[1], e_[2], e_[3], h);                                  \
+        uint32_t e_[4];                                                                           \
+        _Pragma("unroll") for (int q_ = 0; q_ < 4; ++q_) {                                        \
+            const float4* pg_ = (const float4*)(s_gd + 32 * (c) + 8 * q_ + 4 * h);                \
+            e_[q_] = (epi1_x80(acc[c], q_, pg_[0], pg_[1]) & ~pm_) | (SIGN4 & pm_);               \
         }                                                                                         \
+        brow[c] = xchg_rows(e_[0], e_[1], e_[2], e_[3], h);                                       \
+    } while (0)
+#define BN_EPI1()                                                                                 \
+    do {                                                                                          \
+        _Pragma("unroll") for (int c_ = 0; c_ < 4; ++c_) BN_EPI1_C(c_);                           \
     } while (0)
 #define BN_RING_WRITE()                                                                           \
     do {                                                                                          \
@@ -1241,7 +1258,7 @@ __global__ __launch_bounds__(512, 1) void k_band(D8sDenseArgs a, int bands, int 
     } while (0)
     // conv2 of output row yo: ring rows yo - 1 .. yo + 1; step st = (plane, tap).  Operand addresses
     // are per-lane pointers plus immediates (weights: swz(K * 32 + j, h) = 64 K + swz(j, h)); two
-    // accumulators (planes 0-1, 2-3) halve the dependent MFMA chain.
+    // accumulators (even and odd steps) make two independent MFMA chains.
 #define BN_C2_FETCH(st, sl)                                                                       \
     do {                                                                                          \
         const int c_ = (st) / 9, tap_ = (st) % 9, dy_ = tap_ / 3, dx_ = tap_ % 3;                 \
@@ -1264,13 +1281,14 @@ __global__ __launch_bounds__(512, 1) void k_band(D8sDenseArgs a, int bands, int 
         acc2[v_] = s_w2sum[res_row(v_, h)];                                                       \
         acc2b[v_] = 0;                                                                            \
     }                                                                                             \
-    u32x4 aw[2], bq[2];                                                                           \
-    BN_C2_FETCH(0, 0)
+    u32x4 aw[4], bq[4];                                /* operands C2D steps ahead */             \
+    _Pragma("unroll") for (int f_ = 0; f_ < C2D; ++f_) BN_C2_FETCH(f_, f_)
 #define BN_C2_STEP(st)                                                                            \
     do {                                                                                          \
-        if ((st) + 1 < 36) BN_C2_FETCH((st) + 1, ((st) + 1) & 1);                                 \
-        if ((st) < 18) acc2 = mfma_i8(aw[(st) & 1], bq[(st) & 1], acc2);                          \
-        else acc2b = mfma_i8(aw[(st) & 1], bq[(st) & 1], acc2b);                                  \
+        if ((st) + C2D < 36) BN_C2_FETCH((st) + C2D, ((st) + C2D) & 3);                           \
+        __builtin_amdgcn_sched_barrier(0);             /* the reads stay C2D steps ahead */       \
+        if (((st) & 1) == 0) acc2 = mfma_i8(aw[(st) & 3], bq[(st) & 3], acc2);                    \
+        else acc2b = mfma_i8(aw[(st) & 3], bq[(st) & 3], acc2b);                                  \
     } while (0)
 #define BN_C2_STORE()                                                                             \
     do {                                                                                          \
@@ -1317,14 +1335,26 @@ __global__ __launch_bounds__(512, 1) void k_band(D8sDenseArgs a, int bands, int 
         BN_INIT1();
         {
             BN_C2_SETUP(y0 + (s - 2) * RS + rw);
+            // conv1's K steps beside the first 18 conv2 steps, its epilogue (one output tile every 4
+            // steps) beside the last 16: the VALU work of both next to conv2's MFMAs
+            BN_K_FETCH(0);
 #pragma unroll
             for (int st = 0; st < 36; ++st) {
                 BN_C2_STEP(st);
 #pragma unroll
                 for (int k = 0; k < GM; ++k)
-                    if (st == (36 * (k + 1)) / GM - 1) BN_K(k);
+                    if (st == (18 * (k + 1)) / GM - 1) {
+                        BN_K_RUN(k);
+                        if (k + 1 < GM) BN_K_FETCH(k + 1);
+                        __builtin_amdgcn_sched_barrier(0);     // read a K step ahead
+                    }
+#pragma unroll
+                for (int c = 0; c < 4; ++c)
+                    if (st == 20 + 4 * c) {
+                        BN_EPI1_C(c);
+                        __builtin_amdgcn_sched_barrier(0);
+                    }
             }
-            BN_EPI1();
             BN_C2_STORE();
         }
         __syncthreads();                               // the ring rows of step s - 2 are read
@@ -1346,8 +1376,11 @@ __global__ __launch_bounds__(512, 1) void k_band(D8sDenseArgs a, int bands, int 
 #undef BN_C2_FETCH
 #undef BN_RING_WRITE
 #undef BN_EPI1
+#undef BN_EPI1_C
 #undef BN_INIT1
 #undef BN_K
+#undef BN_K_RUN
+#undef BN_K_FETCH
 #undef BN_LOAD_A
 #undef BN_LOAD_B
 }
@@ -2466,12 +2499,17 @@ static int band_launch(const D8sDenseArgs* a, hipStream_t st) {
     const int bands = (a->H + rows - 1) / rows;
     const int64_t blocks = (int64_t)a->N * bands;
     REQUIRE(blocks < (1ll << 31), "d8s_dense: too many bands");
-    const int gm = (a->G + 1) & ~1;                        // activation registers: G rounded up to even
+    // activation registers (K steps per step): G itself up to 8, then G rounded up to even
+    const int gm = a->G <= 8 ? a->G : (a->G + 1) & ~1;
 #define BN_LAUNCH(GM_) hipLaunchKernelGGL((k_band<W_, GM_>), dim3((unsigned)blocks), dim3(512), shm, st, *a, bands, rows)
     switch (gm) {
+        case 1: BN_LAUNCH(1); break;
         case 2: BN_LAUNCH(2); break;
+        case 3: BN_LAUNCH(3); break;
         case 4: BN_LAUNCH(4); break;
+        case 5: BN_LAUNCH(5); break;
         case 6: BN_LAUNCH(6); break;
+        case 7: BN_LAUNCH(7); break;
         case 8: BN_LAUNCH(8); break;
         case 10: BN_LAUNCH(10); break;
         case 12: BN_LAUNCH(12); break;
