@@ -1440,48 +1440,56 @@ __global__ __launch_bounds__(DB_NT, 1) void k_dblock(D8sBlockArgs a) {
     const uint8_t* in0 = (const uint8_t*)a.in0 + (int64_t)n * G0 * HW * 32;
     const uint8_t* segn = (const uint8_t*)a.seg + (int64_t)n * HW * 32;
     const int64_t slot = (int64_t)N * HW * 32;
+    // group g's byte at the lane's pixel: a uniform base (scalar registers) plus the lane's 32-bit offset
+#define DB_SRC(g) (((g) < G0 ? in0 + (int64_t)(g) * HW * 32 : segn + (int64_t)((g) - G0) * slot) + offl)
+
+    // A layer's tables, its first conv1 weight chunk and its first 8 activation groups are requested
+    // during the previous layer's conv2 (layer 0: before the loop) and stored to LDS after that
+    // layer's last barrier.  (Activation groups of the previous layer's own output are requested
+    // after the barrier: when G0 + l < 8.)
+    u32x4 wv[5], stg[4], ra[8];                          // conv2 weights, chunk, activations 8 ahead
+    int32_t t_w1sum = 0, t_w2sum = 0;
+    float2 t_gd = {0.f, 0.f};
+    float t_sc = 0.f;
+    uint32_t t_abh[4];
+#define DB_TABLES(lp_, G_)                                                                        \
+    do {                                                                                          \
+        int t_ = tid;                                    /* recomputed indices, not kept live */  \
+        asm volatile("" : "+v"(t_));                                                              \
+        _Pragma("unroll") for (int k_ = 0; k_ < 5; ++k_)                                          \
+            wv[k_] = ((const u32x4*)(lp_).w2)[min(t_ + DB_NT * k_, 2303)];                       \
+        if (t_ < 128) {                                                                           \
+            t_w1sum = (lp_).w1sum[t_];                                                            \
+            t_gd = ((const float2*)(lp_).gd)[t_];                                                 \
+        } else if (t_ < 160) {                                                                    \
+            t_sc = (lp_).sc[t_ - 128];                                                            \
+            t_w2sum = (lp_).w2sum[t_ - 128];                                                      \
+        }                                                                                         \
+        _Pragma("unroll") for (int k_ = 0; k_ < 4; ++k_)                                          \
+            t_abh[k_] = ((const uint32_t*)(lp_).abh)[min(t_ + DB_NT * k_, (G_) * 32 - 1)];       \
+        const u32x4* w1_ = (const u32x4*)(lp_).w1;                                                \
+        _Pragma("unroll") for (int u_ = 0; u_ < 4; ++u_)                                          \
+            stg[u_] = w1_[min(t_ + DB_NT * u_, (G_) * 256 - 1)];                                  \
+    } while (0)
+#define DB_RA(G_)                                                                                 \
+    _Pragma("unroll") for (int s_ = 0; s_ < 8; ++s_)                                              \
+        ra[s_] = *(const u32x4*)DB_SRC(s_ < (G_) - 1 ? s_ : (G_) - 1)
+    uint32_t offl = off;                                 // (opaque per layer: no address hoisted out
+    {                                                    // of the layer loop to live in registers)
+        const D8sLayerP lp0 = a.layers[0];
+        DB_TABLES(lp0, G0);
+        DB_RA(G0);
+    }
+    bool ra_ready = true;
 
     for (int l = 0; l < L; ++l) {
+        asm volatile("" : "+v"(offl));
         const D8sLayerP lp = a.layers[l];
         const int G = G0 + l;
         const int nk = G;
-        // conv2 weights and tables (loads first, stores to LDS after the prefetch below is issued)
-        u32x4 wv[5];
-#pragma unroll
-        for (int k = 0; k < 5; ++k) wv[k] = ((const u32x4*)lp.w2)[min(tid + DB_NT * k, 2303)];
-        int32_t t_w1sum = 0, t_w2sum = 0;
-        float2 t_gd = {0.f, 0.f};
-        float t_sc = 0.f;
-        if (tid < 128) {
-            t_w1sum = lp.w1sum[tid];
-            t_gd = ((const float2*)lp.gd)[tid];
-        } else if (tid < 160) {
-            t_sc = lp.sc[tid - 128];
-            t_w2sum = lp.w2sum[tid - 128];
+        if (!ra_ready) {                                 // groups of the layer before: now complete
+            DB_RA(G);
         }
-        uint32_t t_abh[4];
-#pragma unroll
-        for (int k = 0; k < 4; ++k) t_abh[k] = ((const uint32_t*)lp.abh)[min(tid + DB_NT * k, G * 32 - 1)];
-        asm volatile("" ::: "memory");                   // the table loads stay ahead in issue order
-
-        // conv1 weights go through LDS in chunks of 8 groups (32 KB, double-buffered): every wave
-        // reads all of them, and from L2 one step ahead they would stall every step
-        const u32x4* w1 = (const u32x4*)lp.w1;
-        const int nch = (G + 7) / 8;
-        u32x4 stg[4];
-#define DB_STAGE_LOAD(c)                                                                          \
-    _Pragma("unroll") for (int u_ = 0; u_ < 4; ++u_)                                              \
-        stg[u_] = w1[min((c) * 2048 + tid + DB_NT * u_, G * 256 - 1)]
-#define DB_STAGE_STORE(c)                                                                         \
-    _Pragma("unroll") for (int u_ = 0; u_ < 4; ++u_) s_wc[((c) & 1) * 2048 + wperm(tid + DB_NT * u_)] = stg[u_]
-#define DB_SRC(g) ((g) < G0 ? in0 + (int64_t)(g) * HW * 32 + off                                  \
-                            : segn + (int64_t)((g) - G0) * slot + off)
-        u32x4 ra[8];                                     // activations 8 groups ahead
-        const int klast = nk - 1;
-        DB_STAGE_LOAD(0);
-#pragma unroll
-        for (int s = 0; s < 8; ++s) ra[s] = *(const u32x4*)DB_SRC(s < klast ? s : klast);
-
 #pragma unroll
         for (int k = 0; k < 5; ++k)
             if (tid + DB_NT * k < 2304) s_w[swz((tid + DB_NT * k) >> 1, tid & 1)] = wv[k];
@@ -1495,6 +1503,17 @@ __global__ __launch_bounds__(DB_NT, 1) void k_dblock(D8sBlockArgs a) {
 #pragma unroll
         for (int k = 0; k < 4; ++k)
             if (tid + DB_NT * k < G * 32) s_abh[tid + DB_NT * k] = t_abh[k];
+
+        // conv1 weights go through LDS in chunks of 8 groups (32 KB, double-buffered): every wave
+        // reads all of them, and from L2 one step ahead they would stall every step
+        const u32x4* w1 = (const u32x4*)lp.w1;
+        const int nch = (G + 7) / 8;
+#define DB_STAGE_LOAD(c)                                                                          \
+    _Pragma("unroll") for (int u_ = 0; u_ < 4; ++u_)                                              \
+        stg[u_] = w1[min((c) * 2048 + tid + DB_NT * u_, G * 256 - 1)]
+#define DB_STAGE_STORE(c)                                                                         \
+    _Pragma("unroll") for (int u_ = 0; u_ < 4; ++u_) s_wc[((c) & 1) * 2048 + wperm(tid + DB_NT * u_)] = stg[u_]
+        const int klast = nk - 1;
         DB_STAGE_STORE(0);
         __syncthreads();                                 // this layer's tables, weight chunk 0
 
@@ -1534,7 +1553,6 @@ __global__ __launch_bounds__(DB_NT, 1) void k_dblock(D8sBlockArgs a) {
             }
         }
 #undef DB_STEP
-#undef DB_SRC
 #undef DB_STAGE_STORE
 #undef DB_STAGE_LOAD
 
@@ -1544,23 +1562,20 @@ __global__ __launch_bounds__(DB_NT, 1) void k_dblock(D8sBlockArgs a) {
             uint32_t e[4];
 #pragma unroll
             for (int kk = 0; kk < 4; ++kk) {
-                uint32_t d = 0;
-#pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    const int v = 4 * kk + r;
-                    const float2 prm = s_gd[32 * c + res_row(v, h)];
-                    float y = __builtin_fmaf(prm.x, (float)acc[c][v], prm.y);
-                    y = __builtin_fminf(__builtin_fmaxf(y, 0.0f), 1.0f);
-                    // low byte of 2^23 + 128 + RNE(255 y): u ^ 0x80, the conv2 operand
-                    const uint32_t b = __float_as_uint(__builtin_fmaf(y, 255.0f, 8388736.0f)) & 0xffu;
-                    d |= b << (8 * r);
-                }
-                e[kk] = d;
+                const float4* pg = (const float4*)(s_gd + 32 * c + 8 * kk + 4 * h);
+                e[kk] = epi1_x80(acc[c], kk, pg[0], pg[1]);
             }
             const u32x4 row = xchg_rows(e[0], e[1], e[2], e[3], h);
             if (live) s_b[c * WIN * 2 + swz(dst, h)] = row;
+            __builtin_amdgcn_sched_barrier(0);           // one accumulator tile at a time
         }
         __syncthreads();                                 // the image's bottleneck is in LDS
+
+        // the next layer's tables and chunk 0 (its first activation groups after the 3x3's MFMAs)
+        if (l + 1 < L) {
+            const D8sLayerP ln = a.layers[l + 1];
+            DB_TABLES(ln, G + 1);
+        }
 
         // ---- conv2 (3x3, pad 1) from LDS into store slot l ----
         {
@@ -1582,19 +1597,13 @@ __global__ __launch_bounds__(DB_NT, 1) void k_dblock(D8sBlockArgs a) {
                 __builtin_amdgcn_sched_barrier(0);
             }
 #undef DB_FETCH
+            ra_ready = l + 1 < L && G0 + l >= 8;         // the next layer's groups 0..7 exist already
+            if (ra_ready) {
+                DB_RA(G + 1);
+            }
             uint32_t e[4];
 #pragma unroll
-            for (int kk = 0; kk < 4; ++kk) {
-                uint32_t d = 0;
-#pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    const int v = 4 * kk + r;
-                    const float q = __builtin_rintf(__builtin_fminf(
-                        __builtin_fmaxf((float)acc2[v] * s_sc[res_row(v, h)], -127.0f), 127.0f));
-                    d |= ((uint32_t)(int)q & 0xffu) << (8 * r);
-                }
-                e[kk] = d;
-            }
+            for (int kk = 0; kk < 4; ++kk) e[kk] = epi2_q(acc2, kk, *(const float4*)(s_sc + 8 * kk + 4 * h));
             const u32x4 row = xchg_rows(e[0], e[1], e[2], e[3], h);
             if (live) *(u32x4*)((uint8_t*)segn + (int64_t)l * slot + off) = row;
         }
@@ -1602,6 +1611,9 @@ __global__ __launch_bounds__(DB_NT, 1) void k_dblock(D8sBlockArgs a) {
         // and LDS is free for the next layer's tables
         __syncthreads();
     }
+#undef DB_RA
+#undef DB_TABLES
+#undef DB_SRC
 }
 
 // ------------------------------------------------------------------------------------------------
