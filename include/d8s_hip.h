@@ -192,6 +192,74 @@ int d8s_final(const int8_t* in0, int32_t G0, const int8_t* seg, int32_t N, int32
  * in registers, one quantisation per pooled value), wider ones a tile kernel; both give the same bytes. */
 int d8s_stem(const D8sStemArgs* a, void* stream);
 
+/* ---- Upstream preprocessing: raw uint16 crops -> resize -> exact 1/99 percentiles -> uint8 ----------
+ *
+ * The reference turns the raw crop of every series into the uint8 stacks the encoder reads on the GPU
+ * (src/knee/data/raw_crop.py:492-549 `payloads_to_uint8_torch`): per stack (one series at one crop
+ * scale) the stored uint16 values, Rescale `u * slope + intercept` in float32 (raw_crop.py:520-522),
+ * the crop box, the resize to img x img of `_resize_torch` (raw_crop.py:419-432: cv2 INTER_AREA
+ * tables when the box is taller than img, torch bilinear with align_corners=False otherwise, the
+ * values themselves at img x img), then the linear np.percentile at (1, 99) selected exactly, float64
+ * `(x - lo) * (255 / (hi - lo))` clipped to [0, 255] and truncated (`cache._to_uint8`,
+ * src/knee/data/cache.py:319-340, on the GPU `to_uint8_torch_hist_batch`, torch_uint8.py:332-357, and
+ * the NVRTC `hist_to_uint8`, fused_uint8.py:847-872), a stack whose percentiles are not finite or
+ * equal (or that holds a NaN) being all zero, and the side flip (raw_crop.py:541-545).
+ *
+ * d8s_prep runs all of it for up to D8S_PREP_MAX_STACKS stacks in one call; the resized float32
+ * values are never stored: each pass recomputes them from the uint16 region.  kind 1 starts from
+ * float32 stacks already at img x img instead (`to_uint8_torch_hist_batch(x)`; box, resc ignored).
+ * The uint8 values are bit-identical to `cache._to_uint8` of the resized stack. */
+#define D8S_PREP_MAX_STACKS 16
+#define D8S_PREP_MAX_TAPS 16
+#define D8S_FLIP_NONE 0
+#define D8S_FLIP_X 1          /* columns reversed (Coronal / Axial of a right knee) */
+#define D8S_FLIP_SLICES 2     /* slices reversed (Sagittal of a right knee) */
+
+/* One stack.  r1/g1 and r2/g2: the percentiles are lerp(sorted[r], sorted[r + 1], g) over the
+ * n = (k1 - k0) * img * img values, numpy's linear method (torch_uint8.py:31-42 `_ranks`). */
+typedef struct D8sPrepStack {
+    uint64_t src;       /* kind 0: uint16 region [K][hr][wr]; kind 1: float32 [K][img][img] (16-byte aligned) */
+    uint64_t resc;      /* kind 0: float32 [K][2] slope and intercept per slice, or 0 for none */
+    uint64_t out;       /* d8s_prep: uint8 [K][img][img] (8-byte aligned);
+                         * d8s_prep_resize: float32 [K][img][img] (16-byte aligned) */
+    int32_t K, hr, wr;  /* slices of the stack; region rows and columns (kind 0) */
+    int32_t y0, y1, x0, x1;  /* crop box in the region (kind 0) */
+    int32_t k0, k1;     /* slices [k0, k1) are computed (`read_range`, raw_crop.py:79-90); the output
+                         * slices outside the range are not written */
+    int32_t flip;       /* D8S_FLIP_*: applied to the uint8 output of d8s_prep */
+    int32_t r1, r2;     /* lower order statistics of the 1st and 99th percentile */
+    double g1, g2;      /* their gamma */
+} D8sPrepStack;
+
+/* What d8s_prep leaves at the start of the workspace for stack i: the percentiles (float64), the
+ * scale 255 / (hi - lo) and whether the stack was written as zeros. */
+typedef struct D8sPrepStat {
+    double lo, hi, scale;
+    int32_t bad, pad_;
+} D8sPrepStat;
+
+typedef struct D8sPrepArgs {
+    uint64_t workspace;   /* device memory, 256-byte aligned, d8s_prep_workspace bytes; starts with
+                           * D8sPrepStat[D8S_PREP_MAX_STACKS] */
+    uint64_t ws_bytes;
+    int32_t kind;         /* 0: uint16 regions; 1: float32 stacks at img x img */
+    int32_t img;          /* output side, a multiple of 8, 8 .. 4096 */
+    int32_t n_stacks;     /* 1 .. D8S_PREP_MAX_STACKS */
+    int32_t pad_;
+    D8sPrepStack s[D8S_PREP_MAX_STACKS];
+} D8sPrepArgs;
+
+/* Bytes of workspace d8s_prep and d8s_prep_resize need for n_stacks stacks of side img. */
+int d8s_prep_workspace(int32_t n_stacks, int32_t img, uint64_t* bytes);
+
+/* Resize + percentiles + uint8 + flip of every stack (see above).  Ranks: 0 <= r1, r1 + 1 < n,
+ * r2 + 1 < n, n >= 4; area tables (box taller than img) of at most D8S_PREP_MAX_TAPS taps per axis. */
+int d8s_prep(const D8sPrepArgs* a, void* stream);
+
+/* kind 0 only: the resized float32 stacks themselves (`_resize_torch` after the Rescale,
+ * raw_crop.py:419-432,520-527) into `out`, slices [k0, k1); flip and ranks are ignored. */
+int d8s_prep_resize(const D8sPrepArgs* a, void* stream);
+
 /* Library identification: "d8s-hip <abi> <source hash> gfx950". */
 const char* d8s_version(void);
 

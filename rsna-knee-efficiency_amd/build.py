@@ -38,7 +38,7 @@ def build_library(out: Path | None = None, verbose: bool = False) -> Path:
     out = Path(out or hip.LIB_PATH)
     tmp = out.with_suffix(f".so.tmp{os.getpid()}")
     cmd = [hipcc(), *HIPCC_FLAGS, f"-I{hip.HEADER.parent}", f'-DD8S_SRC_HASH="{hip.source_sha()}"',
-           str(hip.SOURCE), "-o", str(tmp)]
+           *(str(f) for f in hip.SOURCES if f.suffix == ".hip"), "-o", str(tmp)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"hipcc failed ({res.returncode}):\n{res.stderr[-4000:]}")

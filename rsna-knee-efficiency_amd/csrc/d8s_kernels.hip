@@ -23,6 +23,7 @@
 #include <type_traits>
 
 #include "d8s_hip.h"
+#include "d8s_host.h"
 
 #ifndef D8S_SRC_HASH
 #define D8S_SRC_HASH "unknown"
@@ -2364,6 +2365,10 @@ static int cu_count() {
     }
     return cached[dev];
 }
+
+int d8s_host_fail(int code, const std::string& msg) { return fail(code, msg); }
+int d8s_host_launched(const char* what) { return launched(what); }
+int d8s_host_cu_count() { return cu_count(); }
 
 #define REQUIRE(cond, msg) \
     do { if (!(cond)) return fail((int)hipErrorInvalidValue, msg); } while (0)

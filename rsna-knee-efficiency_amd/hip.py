@@ -20,6 +20,8 @@ from pathlib import Path
 PKG = Path(__file__).resolve().parent
 CSRC = PKG / "csrc"
 SOURCE = CSRC / "d8s_kernels.hip"
+# every file compiled into the library (the first is SOURCE)
+SOURCES = (SOURCE, CSRC / "d8s_prep.hip", CSRC / "d8s_host.h")
 HEADER = PKG.parent / "include" / "d8s_hip.h"
 LIB_PATH = PKG / "libd8s_hip.so"
 ABI_VERSION = 1
@@ -79,6 +81,29 @@ class StemArgs(ctypes.Structure):
                 ("N", i32), ("H", i32), ("W", i32), ("kind", i32), ("flip", i32), ("pad_", i32)]
 
 
+class PrepStack(ctypes.Structure):
+    """`D8sPrepStack`: one stack of the preprocessing (a series at one crop scale)."""
+    _fields_ = [("src", u64), ("resc", u64), ("out", u64), ("K", i32), ("hr", i32), ("wr", i32),
+                ("y0", i32), ("y1", i32), ("x0", i32), ("x1", i32), ("k0", i32), ("k1", i32),
+                ("flip", i32), ("r1", i32), ("r2", i32), ("g1", ctypes.c_double),
+                ("g2", ctypes.c_double)]
+
+
+PREP_MAX_STACKS = 16
+
+
+class PrepStat(ctypes.Structure):
+    """`D8sPrepStat`: the percentiles, scale and bad flag d8s_prep leaves per stack."""
+    _fields_ = [("lo", ctypes.c_double), ("hi", ctypes.c_double), ("scale", ctypes.c_double),
+                ("bad", i32), ("pad_", i32)]
+
+
+class PrepArgs(ctypes.Structure):
+    """`D8sPrepArgs`: the arguments of d8s_prep / d8s_prep_resize."""
+    _fields_ = [("workspace", u64), ("ws_bytes", u64), ("kind", i32), ("img", i32),
+                ("n_stacks", i32), ("pad_", i32), ("s", PrepStack * PREP_MAX_STACKS)]
+
+
 IN_F16, IN_U8 = 0, 1
 
 # entry point -> argument types (all return int32 status)
@@ -91,6 +116,9 @@ SIGNATURES = {
     "d8s_transition": [ctypes.POINTER(GemmArgs), vp],
     "d8s_final": [vp, i32, vp, i32, i32, vp, vp, i32, vp],
     "d8s_stem": [ctypes.POINTER(StemArgs), vp],
+    "d8s_prep_workspace": [i32, i32, ctypes.POINTER(ctypes.c_uint64)],
+    "d8s_prep": [ctypes.POINTER(PrepArgs), vp],
+    "d8s_prep_resize": [ctypes.POINTER(PrepArgs), vp],
     "d8s_micro_copy": [vp, vp, ctypes.c_size_t, vp],
     "d8s_micro_mfma": [i32, i32, vp, vp],
     "d8s_probe_mfma_i8": [vp, vp, vp, vp],
@@ -101,7 +129,9 @@ STRING_FUNCS = ("d8s_version", "d8s_last_error")
 
 def source_sha() -> str:
     """Hash of the kernel source and header: the build's `kernels_sha` (`src/knee/dense8s.py:781-783`)."""
-    h = hashlib.sha1(SOURCE.read_bytes())
+    h = hashlib.sha1()
+    for f in SOURCES:
+        h.update(f.read_bytes())
     h.update(HEADER.read_bytes())
     return h.hexdigest()[:12]
 

@@ -46,6 +46,10 @@ def test_struct_layouts_match_header(tmp_path):
         " offsetof(D8sDenseArgs, out), offsetof(D8sDenseArgs, W));\n"
         '  printf("%zu %zu %zu %zu\\n", sizeof(D8sBlockArgs), offsetof(D8sBlockArgs, layers),'
         " offsetof(D8sBlockArgs, L), sizeof(D8sLayerP));\n"
+        '  printf("%zu %zu %zu %zu\\n", sizeof(D8sPrepStack), offsetof(D8sPrepStack, K),'
+        " offsetof(D8sPrepStack, r2), offsetof(D8sPrepStack, g1));\n"
+        '  printf("%zu %zu %zu %zu\\n", sizeof(D8sPrepArgs), offsetof(D8sPrepArgs, kind),'
+        " offsetof(D8sPrepArgs, s), sizeof(D8sPrepStat));\n"
         "  return 0; }\n")
     exe = tmp_path / "layout"
     subprocess.run(["gcc", f"-I{hip.HEADER.parent}", str(prog), "-o", str(exe)], check=True)
@@ -59,6 +63,36 @@ def test_struct_layouts_match_header(tmp_path):
     assert got[3] == [ctypes.sizeof(D), D.w2.offset, D.out.offset, D.W.offset]
     B = hip.BlockArgs
     assert got[4] == [ctypes.sizeof(B), B.layers.offset, B.L.offset, ctypes.sizeof(hip.LayerP)]
+    PS, PA = hip.PrepStack, hip.PrepArgs
+    assert got[5] == [ctypes.sizeof(PS), PS.K.offset, PS.r2.offset, PS.g1.offset]
+    assert got[6] == [ctypes.sizeof(PA), PA.kind.offset, PA.s.offset, ctypes.sizeof(hip.PrepStat)]
+
+
+def _prep_args(kind=0, ws_bytes=None, box=(0, 64, 0, 64), r2=None, k=(0, 1), hr=64, out=256):
+    """A d8s_prep argument set that is valid except for the field a test changes (fake pointers: the
+    checks run before any HIP call)."""
+    a = hip.PrepArgs()
+    need = ctypes.c_uint64()
+    assert hip.library().d8s_prep_workspace(1, 64, ctypes.byref(need)) == 0
+    a.workspace, a.ws_bytes = 1 << 20, need.value if ws_bytes is None else ws_bytes
+    a.kind, a.img, a.n_stacks = kind, 64, 1
+    s = a.s[0]
+    s.src, s.out, s.K, s.hr, s.wr = 4096, out, 1, hr, 64
+    s.y0, s.y1, s.x0, s.x1 = box
+    s.k0, s.k1 = k
+    k1, k2, g1, g2 = (40, 4054, 0.95, 0.05)
+    s.r1, s.r2, s.g1, s.g2 = k1, k2 if r2 is None else r2, g1, g2
+    return a
+
+
+def test_prep_workspace_size():
+    b1, b16 = ctypes.c_uint64(), ctypes.c_uint64()
+    lib = hip.library()
+    assert lib.d8s_prep_workspace(1, 512, ctypes.byref(b1)) == 0
+    assert lib.d8s_prep_workspace(16, 512, ctypes.byref(b16)) == 0
+    assert b16.value > b1.value > 16 * ctypes.sizeof(hip.PrepStat)
+    # the stats header, then one block per stack
+    assert b16.value - b1.value == 15 * (b1.value - 1024)
 
 
 @pytest.mark.parametrize("name,args", [
@@ -80,6 +114,17 @@ def test_struct_layouts_match_header(tmp_path):
     ("d8s_stem", lambda: (ctypes.byref(hip.StemArgs(1, 1, 1, 1, 1, 1, 2, 8, 8, 1, 0, 0)), None)),
     ("d8s_stem", lambda: (ctypes.byref(hip.StemArgs(4, 0, 1, 1, 1, 1, 1, 8, 8, 0, 0, 0)), None)),
     ("d8s_final", lambda: (1, 20, 1, 2, 256, 1, 1, 100, None)),
+    ("d8s_prep_workspace", lambda: (0, 512, ctypes.byref(ctypes.c_uint64()))),
+    ("d8s_prep_workspace", lambda: (4, 500, ctypes.byref(ctypes.c_uint64()))),
+    ("d8s_prep", lambda: (None, None)),
+    ("d8s_prep", lambda: (ctypes.byref(_prep_args(kind=2)), None)),
+    ("d8s_prep", lambda: (ctypes.byref(_prep_args(ws_bytes=1024)), None)),
+    ("d8s_prep", lambda: (ctypes.byref(_prep_args(box=(0, 65, 0, 64))), None)),
+    ("d8s_prep", lambda: (ctypes.byref(_prep_args(r2=64 * 64 - 1)), None)),
+    ("d8s_prep", lambda: (ctypes.byref(_prep_args(k=(1, 1))), None)),
+    ("d8s_prep", lambda: (ctypes.byref(_prep_args(box=(0, 64 * 17, 0, 64), hr=64 * 17)), None)),
+    ("d8s_prep_resize", lambda: (ctypes.byref(_prep_args(kind=1)), None)),
+    ("d8s_prep_resize", lambda: (ctypes.byref(_prep_args(out=8)), None)),
     ("d8s_micro_copy", lambda: (1, 1, 17, None)),
 ])
 def test_invalid_arguments_fail_on_the_host(name, args):
