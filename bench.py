@@ -149,7 +149,9 @@ def copy_probe(dev: torch.device, mib: int = 1024, reps: int = 5) -> dict:
 
 FAMILY = {"k_conv1": "conv1", "k_conv1p": "conv1", "k_conv2": "conv2", "k_dense": "dense",
           "k_band": "dense", "k_dblock": "block", "k_trans": "trans", "k_stem": "stem",
-          "k_stem_rows": "stem", "k_final": "final", "k_copy": "copy"}
+          "k_stem_rows": "stem", "k_final": "final", "k_copy": "copy", "k_prep_setup": "prep_setup",
+          "k_prep_hist": "prep_hist", "k_prep_select": "prep_select", "k_prep_norm": "prep_norm",
+          "k_prep_resize": "prep_resize"}
 
 
 def _family(name: str) -> str | None:
@@ -309,6 +311,81 @@ def cpu_baseline(reps: int = 5, warmup: int = 2) -> dict:
                       f"{reps} timed, median {med * 1e3:.0f} ms; CPU {cpu}"}
 
 
+PREP_READ_SLICES = (0, 23)      # the final submission's KNEE_READ_SLICES (raw_crop.py:71-76)
+
+
+def prep_bytes(payload: dict, img: int, n_scales: int, read_slices) -> int:
+    """Algorithmic HBM bytes of one study's preparation: every stored uint16 value of the slices read
+    (each region once), the Rescale table, and every uint8 of the volume written once."""
+    from rsna_knee_efficiency_amd import prep
+    total = 0
+    for row in payload["meta"]:
+        K = int(row[prep.M_K])
+        if row[prep.M_MODE] != prep.MODE_GPU:
+            total += 2 * n_scales * K * img * img          # copied CPU series: read + write
+            continue
+        rr = prep.read_range(K, int(row[prep.M_FLIP]), read_slices) or (0, K)
+        total += 2 * (rr[1] - rr[0]) * int(row[prep.M_HR]) * int(row[prep.M_WR])
+        total += 8 * K if row[prep.M_RESC] >= 0 else 0
+        total += n_scales * K * img * img
+    return total
+
+
+def prep_cpu_baseline(payload: dict, read_slices) -> dict:
+    """The oracle's chain (C resize + numpy percentiles and normalisation) on one study, 1 core."""
+    from oracle import prep as oprep
+    t = time.perf_counter()
+    oprep.payload_to_uint8(payload, IMG, 4, 2, SLICES, read_slices=read_slices)
+    dt = time.perf_counter() - t
+    return {"value": round(1.0 / dt, 4), "unit": "studies/s", "cores": 1, "kind": "port",
+            "sample": f"one synthetic study (4 series, 2 crops, {SLICES} slices, 512 px, slices "
+                      f"{read_slices[0]}:{read_slices[1]}) through oracle/prep.py: {dt:.2f} s"}
+
+
+def bench_prep(dev: torch.device, steps: int, warmup: int, with_cpu: bool) -> dict:
+    """The preparation path (raw crops -> uint8 volume) on studies resident in HBM."""
+    from rsna_knee_efficiency_amd import prep
+    spec = prep.PrepSpec(img=IMG, slices=SLICES, n_seq=4, n_scales=2)
+    pays = [synthetic.study_payload(IMG, SLICES, seed=100 + i) for i in range(2)]
+    dpays = [{"raw": torch.from_numpy(p["raw"]).to(dev), "u8": torch.from_numpy(p["u8"]).to(dev),
+              "resc": torch.from_numpy(p["resc"]).to(dev), "meta": p["meta"]} for p in pays]
+    rs = PREP_READ_SLICES
+    for k in range(warmup):
+        prep.payloads_to_uint8([dpays[k % 2]], spec, dev, read_slices=rs)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t = time.perf_counter()
+    e0.record()
+    for k in range(steps):
+        prep.payloads_to_uint8([dpays[k % 2]], spec, dev, read_slices=rs)
+    e1.record()
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t
+    gpu_ms = e0.elapsed_time(e1) / steps
+    nbytes = sum(prep_bytes(p, IMG, 2, rs) for p in pays) / 2
+    achieved = nbytes / (gpu_ms * 1e-3) / 1e9
+    out = {
+        "metric": "study preparation (raw uint16 crops -> 8 uint8 stacks of 24 x 512 x 512) studies/s "
+                  "on 1 MI355X",
+        "value": round(steps / dt, 2), "unit": "studies/s", "n_gpus": 1, "steps": steps,
+        "warmup": warmup, "ms_per_step": round(dt / steps * 1e3, 4), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "f32/f64 (uint16 in, uint8 out)",
+        "data": "synthetic study payloads (rsna_knee_efficiency_amd.synthetic.study_payload)",
+        "config": {"workload": "one study per step: 4 series x 2 crops (110, 150 mm) x 24 slices at 512 px, "
+                               "slices 0:23 read, inputs resident in HBM (payloads_to_uint8)",
+                   "parallelism": "none (1 GPU)"},
+        "gpu_ms_per_study": round(gpu_ms, 4),
+        "roofline": {"bound": "hbm", "kernel": "d8s_prep (its 8 launches per call, between HIP events)",
+                     "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "algorithmic_bytes_per_study": int(nbytes)},
+    }
+    if with_cpu:
+        log("prep cpu baseline ...")
+        out["cpu_baseline"] = prep_cpu_baseline(pays[0], rs)
+    return out
+
+
 def main() -> None:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -325,6 +402,8 @@ def main() -> None:
     ap.add_argument("--pmc-passes", type=int, default=0, metavar="P",
                     help="only run P eager configuration-5 passes of one encoder (the launches of "
                          "a counter-collection run), print the per-family times and exit")
+    ap.add_argument("--path", choices=("encoder", "prep"), default="encoder",
+                    help="prep: the upstream preparation (raw crops -> uint8 volume) instead")
     ap.add_argument("--traffic-summary", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                     help="print the HBM traffic per launch from two --pmc-passes counter runs")
     args = ap.parse_args()
@@ -344,6 +423,9 @@ def main() -> None:
     torch.backends.cudnn.allow_tf32 = False
     torch.backends.cuda.matmul.allow_tf32 = False
     dev = torch.device("cuda:0")
+    if args.path == "prep":
+        print(json.dumps(bench_prep(dev, args.steps, args.warmup, not args.no_cpu)), flush=True)
+        return
     t0 = time.perf_counter()
     nb = 4 * SLICES                                     # 2 crops x 24 slices x flip
     if args.pmc_passes:

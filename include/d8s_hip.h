@@ -205,9 +205,10 @@ int d8s_stem(const D8sStemArgs* a, void* stream);
  * the NVRTC `hist_to_uint8`, fused_uint8.py:847-872), a stack whose percentiles are not finite or
  * equal (or that holds a NaN) being all zero, and the side flip (raw_crop.py:541-545).
  *
- * d8s_prep runs all of it for up to D8S_PREP_MAX_STACKS stacks in one call; the resized float32
- * values are never stored: each pass recomputes them from the uint16 region.  kind 1 starts from
- * float32 stacks already at img x img instead (`to_uint8_torch_hist_batch(x)`; box, resc ignored).
+ * d8s_prep runs all of it for up to D8S_PREP_MAX_STACKS stacks in one call: the resize runs once,
+ * into the caller's scratch buffer, together with the first histogram pass; the later passes read the
+ * float32 stacks.  kind 1 starts from float32 stacks already at img x img instead
+ * (`to_uint8_torch_hist_batch(x)`; box, resc and scratch ignored).
  * The uint8 values are bit-identical to `cache._to_uint8` of the resized stack. */
 #define D8S_PREP_MAX_STACKS 16
 #define D8S_PREP_MAX_TAPS 16
@@ -242,6 +243,10 @@ typedef struct D8sPrepArgs {
     uint64_t workspace;   /* device memory, 256-byte aligned, d8s_prep_workspace bytes; starts with
                            * D8sPrepStat[D8S_PREP_MAX_STACKS] */
     uint64_t ws_bytes;
+    uint64_t scratch;     /* d8s_prep, kind 0: device memory, 16-byte aligned, of at least
+                           * 4 * sum over the stacks of (k1 - k0) * img * img bytes: the resized float32
+                           * stacks (written once, read by the later passes); otherwise unused */
+    uint64_t scratch_bytes;
     int32_t kind;         /* 0: uint16 regions; 1: float32 stacks at img x img */
     int32_t img;          /* output side, a multiple of 8, 8 .. 4096 */
     int32_t n_stacks;     /* 1 .. D8S_PREP_MAX_STACKS */

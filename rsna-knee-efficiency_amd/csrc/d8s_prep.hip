@@ -12,8 +12,11 @@
 //     finds the bins holding the four ranks;  equal ranks share a histogram (at most four per level);
 //   - the last pass evaluates the pixel again and writes the uint8 value (float64 arithmetic, the
 //     reference's exact operations) at its flipped position.
-// A pass handles units of 8 consecutive output pixels of one row; a workgroup owns a contiguous run of
-// units of one stack, so neighbouring source rows are read from cache.
+// A pass works on blocks of output rows of one slice: the source rows a block needs are resized along x
+// once into LDS, then every output pixel combines them along y (the bilinear formula is separable as
+// written: fma(h0, top, h1 * bottom) with top and bottom the x interpolations of two source rows).  A
+// histogram workgroup runs several blocks of one stack before it adds its LDS counts to the global
+// histogram; the final pass runs one block per workgroup.
 //
 // Numerics (the file is compiled with -ffp-contract=off: only the explicit fmaf are fused):
 //   rescale   (float)u * slope, then + intercept (raw_crop.py:520-522);
@@ -45,6 +48,8 @@ constexpr int NT = 256;                          // threads per workgroup
 constexpr int NB1 = 2048, NB2 = 2048, NB3 = 1024;  // radix levels: key bits 31..21, 20..10, 9..0
 constexpr int MAX_S = D8S_PREP_MAX_STACKS;
 constexpr int MAX_T = D8S_PREP_MAX_TAPS;
+constexpr int UP = 4;                            // output pixels per thread step (one 16-byte LDS read)
+constexpr int STAGE = 8192;                      // LDS of the block kernels: 32 KB (resized rows + raw rows)
 
 // per-stack workspace block, in 32-bit words
 constexpr int W_H1 = 0;
@@ -79,18 +84,22 @@ struct PStack {
     const float* resc;
     void* out;
     uint32_t* ws;
+    float* sc;           // kind 0 in d8s_prep: the resized stack (slice kk at sc + kk img img)
     int K, hr, wr, y0, x0, h, w, k0, k1, flip, mode, Tx, Ty, r1, r2;
     float rh, rw;
     double g1, g2;
-    int units;       // (k1 - k0) * img * img / 8
-    int wg_hist, wg_norm;
+    int rb, bps, nblk;   // output rows per block, blocks per slice, blocks of the slices [k0, k1)
+    int ns_max, rp, dpl; // source rows a block may read; LDS dwords per staged raw row; per lane
+    float inv_rp;
+    int hb, hb2, nb;     // blocks per workgroup: histogram level 1, levels 2-3, final pass
+    int wg_hist, wg_hist2, wg_norm;  // first workgroup of this stack in each grid
 };
 
 struct PArgs {
     PStack s[MAX_S];
     D8sPrepStat* stat;
-    int n, img, upr;          // stacks, output side, units per output row (img / 8)
-    int hist_units, norm_units;
+    int n, img, upr;     // stacks, output side, UP-pixel units per output row (img / UP)
+    float inv_img, inv_upr;
 };
 
 // ---- float order keys -------------------------------------------------------------------------
@@ -145,140 +154,328 @@ int area_taps_max(int ssize, int dsize) {
 }
 
 // ---- evaluation of 8 output pixels -------------------------------------------------------------
-DEV float rescaled(uint16_t u, bool has, float sl, float ic) {
-    const float f = (float)u;
-    if (!has) return f;
-    const float p = f * sl;
-    return p + ic;
-}
-
 DEV float src_index(float scale, int d) {
     const float s = __builtin_fmaf(scale, (float)d + 0.5f, -0.5f);
     return s < 0.0f ? 0.0f : s;
 }
 
-// Values of output pixels (kk, dy, dx0 .. dx0 + 7) of stack `st` (mode MODE) into v.
+// n / d for 0 <= n < 2^22 and 1 <= d <= 4096 (inv = 1 / d): a float estimate, corrected.
+DEV int fdiv(int n, int d, float inv) {
+    int q = (int)((float)n * inv);
+    q -= q * d > n ? 1 : 0;
+    q += (q + 1) * d <= n ? 1 : 0;
+    return q;
+}
+
+// A block: output rows [r0, r0 + rb) of slice kk, reading source rows [s0, s0 + ns) of the crop.
+struct Geo {
+    int kk, r0, rb, s0, ns;
+};
+
 template <int MODE>
-DEV void eval8(const PStack& st, int img, int kk, int dy, int dx0, float v[8]) {
+DEV Geo block_geo(const PStack& st, const PArgs& a, int b) {
+    Geo g;
+    const int q = b / st.bps;
+    g.kk = st.k0 + q;
+    g.r0 = (b - q * st.bps) * st.rb;
+    g.rb = min(st.rb, a.img - g.r0);
     if constexpr (MODE == M_FLOAT) {
-        const float4* p = (const float4*)((const float*)st.src + ((int64_t)kk * img + dy) * img + dx0);
-        const float4 a = p[0], b = p[1];
-        v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
-        v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+        g.s0 = 0;
+        g.ns = 0;
+        return g;
+    } else {
+        int s1;
+        if constexpr (MODE == M_IDENT) {
+            g.s0 = g.r0;
+            s1 = g.r0 + g.rb;
+        } else if constexpr (MODE == M_BILIN) {
+            g.s0 = (int)src_index(st.rh, g.r0);
+            const int h1 = (int)src_index(st.rh, g.r0 + g.rb - 1);
+            s1 = h1 + (h1 < st.h - 1 ? 1 : 0) + 1;
+        } else {
+            const int32_t* iy = (const int32_t*)st.ws + W_TAPS + 2 * a.img * st.Tx;
+            const float* wy = (const float*)(iy + a.img * st.Ty);
+            const int last = g.r0 + g.rb - 1;
+            int t = st.Ty - 1;
+            while (t > 0 && !(wy[last * st.Ty + t] > 0.0f)) --t;   // the padding taps have weight 0
+            g.s0 = iy[g.r0 * st.Ty];
+            s1 = iy[last * st.Ty] + t + 1;
+        }
+        g.ns = min(s1 - g.s0, st.ns_max);
+        return g;
+    }
+}
+
+DEV const uint16_t* crop_row(const PStack& st, int kk, int r) {
+    return (const uint16_t*)st.src + ((int64_t)kk * st.hr + st.y0 + r) * st.wr + st.x0;
+}
+
+constexpr int NW = NT / 64;  // waves per workgroup
+
+// Copies source rows [s0, s0 + ns) of a block, crop columns [0, w), to LDS with gfx950's
+// global_load_lds (memory to LDS without registers).  Wave v copies rows v, v + NW, ...; row r starts
+// at element e_r = e0 + r wr of the dword-aligned series base, and its dwords [0, nd) from element
+// e_r & ~1 (the first and last may hold 2 bytes of the neighbouring rows, nothing outside the dwords
+// that hold the row) go to s_raw[r][0 .. nd); lanes past nd repeat the last dword, inside the row's
+// 64-dword-padded slot.  The caller waits for the copies (vmcnt) and synchronises.
+DEV void raw_stage(const PStack& st, const Geo& g, uint32_t* s_raw) {
+    const int wv = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6), lane = (int)threadIdx.x & 63;
+    const uint32_t* base = (const uint32_t*)((uintptr_t)st.src & ~(uintptr_t)3);
+    const int e0 = (int)(((uintptr_t)st.src >> 1) & 1u) + (g.kk * st.hr + st.y0 + g.s0) * st.wr + st.x0;
+    const int pitch = st.dpl * 64;
+    for (int r = wv; r < g.ns; r += NW) {
+        const int er = e0 + r * st.wr;
+        const int nd = ((er & 1) + st.w + 1) >> 1;
+        const uint32_t* row = base + (er >> 1);
+        for (int m = 0; m < st.dpl; ++m) {
+            const int d = min(lane + 64 * m, nd - 1);
+            __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)(row + d),
+                                             (__attribute__((address_space(3))) void*)(s_raw + r * pitch + 64 * m),
+                                             4, 0, 0);
+        }
+    }
+}
+
+template <bool HAS>
+DEV float rescale(uint32_t u, float sl, float ic) {
+    const float f = (float)u;
+    if constexpr (!HAS) {
+        return f;
+    } else {
+        const float p = f * sl;
+        return p + ic;
+    }
+}
+
+// The values of every block b0 .. b1-1 of stack st, UP consecutive pixels of a row at a time, handed to
+// f(kk, dy, dx0, v).  Region modes: a block's raw rows are copied to LDS (two buffers: the copy of block
+// b+1 runs while block b is computed), resized along x into
+// s_st [ns][img] (bilinear `top`/`bottom` values fma(w0, a, w1 b), area column sums, identity values),
+// and every pixel combines them along y.  A thread keeps the same output columns in the x pass, so
+// their interpolation positions are computed once.  The workgroup calls this uniformly (it holds
+// barriers).
+//
+// The area taps of an output index are consecutive source indices (raw_crop.py:361-369), so a tap's
+// source is the first index + t; a zero-weight padding tap then reads a neighbour instead of index 0,
+// which changes nothing for finite values (x * 0 = +-0 added to a sum that is never -0).
+template <int MODE, bool HAS, bool WROW, class F>
+DEV void run_blocks(const PStack& st, const PArgs& a, int b0, int b1, float* s_st, F&& f) {
+    const int img = a.img;
+    if constexpr (MODE == M_FLOAT) {
+        for (int b = b0; b < b1; ++b) {
+            const Geo g = block_geo<MODE>(st, a, b);
+            for (int u = threadIdx.x; u < g.rb * a.upr; u += NT) {
+                const int row = fdiv(u, a.upr, a.inv_upr), dx0 = (u - row * a.upr) * UP, dy = g.r0 + row;
+                const float4 x = *(const float4*)((const float*)st.src + ((int64_t)g.kk * img + dy) * img + dx0);
+                float v[UP] = {x.x, x.y, x.z, x.w};
+                f(g.kk, dy, dx0, v);
+            }
+        }
         return;
     } else {
-        const uint16_t* reg = (const uint16_t*)st.src + (int64_t)kk * st.hr * st.wr;
-        const bool has = st.resc != nullptr;
-        const float sl = has ? st.resc[2 * kk] : 1.0f, ic = has ? st.resc[2 * kk + 1] : 0.0f;
-        if constexpr (MODE == M_IDENT) {
-            const uint16_t* row = reg + (int64_t)(st.y0 + dy) * st.wr + st.x0 + dx0;
+        constexpr int CMAX = 4;                      // output columns per thread in the x pass (img <= 1024)
+        const int32_t* ix = (const int32_t*)st.ws + W_TAPS;
+        const float* wx = (const float*)(ix + img * st.Tx);
+        const int32_t* iy = (const int32_t*)(wx + img * st.Tx);
+        const float* wy = (const float*)(iy + img * st.Ty);
+        const int pitch = st.dpl * 64;               // dwords per staged raw row
+        // two raw buffers: block b+1 is copied while block b is resized
+        uint32_t* s_raw0 = (uint32_t*)(s_st + st.ns_max * img);
+        uint32_t* s_raw1 = s_raw0 + st.ns_max * pitch;
+        // x-pass mapping: img >= NT: columns tid + c NT, every row; img < NT: column tid % img, rows
+        // tid / img + P j (threads beyond P img rest)
+        const int P = img >= NT ? 1 : NT / img;
+        const int ph = img >= NT ? 0 : (int)threadIdx.x / img;
+        const int col0 = (int)threadIdx.x - ph * img;
+        const bool xact = ph < P;
+        int ca[CMAX], cb[CMAX];          // uint16 index of the two taps (bilinear) / first tap (area)
+        float cm0[CMAX], cm1[CMAX];
 #pragma unroll
-            for (int i = 0; i < 8; ++i) v[i] = rescaled(row[i], has, sl, ic);
-        } else if constexpr (MODE == M_BILIN) {
-            const float sy = src_index(st.rh, dy);
-            const int h1 = (int)sy;
-            const int h1p = h1 < st.h - 1 ? 1 : 0;
-            const float l1 = sy - (float)h1, l0 = 1.0f - l1;
-            const uint16_t* r0 = reg + (int64_t)(st.y0 + h1) * st.wr + st.x0;
-            const uint16_t* r1 = r0 + (int64_t)h1p * st.wr;
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                const float sx = src_index(st.rw, dx0 + i);
+        for (int c = 0; c < CMAX; ++c) {
+            const int dx = min(col0 + c * NT, img - 1);
+            ca[c] = cb[c] = dx;
+            cm0[c] = cm1[c] = 0.0f;
+            if constexpr (MODE == M_BILIN) {
+                const float sx = src_index(st.rw, dx);
                 const int w1 = (int)sx;
-                const int w1p = w1 < st.w - 1 ? 1 : 0;
-                const float m1 = sx - (float)w1, m0 = 1.0f - m1;
-                const float a = rescaled(r0[w1], has, sl, ic), b = rescaled(r0[w1 + w1p], has, sl, ic);
-                const float c = rescaled(r1[w1], has, sl, ic), d = rescaled(r1[w1 + w1p], has, sl, ic);
-                const float top = __builtin_fmaf(m0, a, m1 * b);
-                const float bot = __builtin_fmaf(m0, c, m1 * d);
-                v[i] = __builtin_fmaf(l0, top, l1 * bot);
+                ca[c] = w1;
+                cb[c] = w1 + (w1 < st.w - 1 ? 1 : 0);
+                cm1[c] = sx - (float)w1;
+                cm0[c] = 1.0f - cm1[c];
+            } else if constexpr (MODE == M_AREA) {
+                if (st.w != img) ca[c] = ix[dx * st.Tx];
             }
-        } else {  // M_AREA: rows of the column-resized intermediate, weighted, in table order
-            const int32_t* ix = (const int32_t*)st.ws + W_TAPS;
-            const float* wx = (const float*)(ix + img * st.Tx);
-            const int32_t* iy = (const int32_t*)(wx + img * st.Tx);
-            const float* wy = (const float*)(iy + img * st.Ty);
-            float acc[8];
+        }
+        // uint16 parity of the crop rows: row index q starts at element (src / 2) + q wr + x0
+        const int par0 = (int)((((uintptr_t)st.src >> 1) + (uintptr_t)st.x0) & 1u);
+        const int last = st.ns_max - 1;
+        // y-pass mapping: RS rows at a time, thread (tr, tc); with WROW (a row is a multiple of 64
+        // units) every wave works on one row, so the row quantities are wave-uniform
+        const int RS = NT / a.upr;
+        int tr = (int)threadIdx.x / a.upr;
+        if constexpr (WROW) tr = __builtin_amdgcn_readfirstlane(tr);
+        const int dx0 = ((int)threadIdx.x - ((int)threadIdx.x / a.upr) * a.upr) * UP;
+        const bool yact = tr < RS;
+        Geo nxt = block_geo<MODE>(st, a, b0);
+        raw_stage(st, nxt, s_raw0);
+        for (int b = b0; b < b1; ++b) {
+            const Geo g = nxt;
+            const uint16_t* raw16 = (const uint16_t*)((b - b0) & 1 ? s_raw1 : s_raw0);
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+            __syncthreads();
+            if (b + 1 < b1) {
+                nxt = block_geo<MODE>(st, a, b + 1);
+                raw_stage(st, nxt, (b - b0) & 1 ? s_raw0 : s_raw1);
+            }
+            const float sl = HAS ? st.resc[2 * g.kk] : 1.0f, ic = HAS ? st.resc[2 * g.kk + 1] : 0.0f;
+            const int e0 = par0 + (g.kk * st.hr + st.y0 + g.s0) * st.wr;
+            if (xact) {
+                for (int r = ph; r < g.ns; r += P) {
+                    const uint16_t* row = raw16 + r * 2 * pitch + ((e0 + r * st.wr) & 1);
+                    float* dst = s_st + r * img;
 #pragma unroll
-            for (int i = 0; i < 8; ++i) acc[i] = 0.0f;
-            for (int j = 0; j < st.Ty; ++j) {
-                const int sy = iy[dy * st.Ty + j];
-                const float wyj = wy[dy * st.Ty + j];
-                const uint16_t* row = reg + (int64_t)(st.y0 + sy) * st.wr + st.x0;
-#pragma unroll
-                for (int i = 0; i < 8; ++i) {
-                    const int dx = dx0 + i;
-                    float c;
-                    if (st.w == img) {
-                        c = rescaled(row[dx], has, sl, ic);
-                    } else {
-                        c = 0.0f;
-                        for (int t = 0; t < st.Tx; ++t) {
-                            const float p = rescaled(row[ix[dx * st.Tx + t]], has, sl, ic) * wx[dx * st.Tx + t];
-                            c = c + p;
+                    for (int c = 0; c < CMAX; ++c) {
+                        const int dx = col0 + c * NT;
+                        if (c * NT < img && dx < img) {
+                            float v;
+                            if constexpr (MODE == M_IDENT) {
+                                v = rescale<HAS>(row[dx], sl, ic);
+                            } else if constexpr (MODE == M_BILIN) {
+                                const float xa = rescale<HAS>(row[ca[c]], sl, ic);
+                                const float xb = rescale<HAS>(row[cb[c]], sl, ic);
+                                v = __builtin_fmaf(cm0[c], xa, cm1[c] * xb);
+                            } else if (st.w == img) {
+                                v = rescale<HAS>(row[dx], sl, ic);
+                            } else {
+                                v = 0.0f;
+                                const uint16_t* tp = row + ca[c];
+                                const float* tw = wx + dx * st.Tx;
+                                for (int t = 0; t < st.Tx; ++t) {
+                                    const float p = rescale<HAS>(tp[min(t, st.w - 1 - ca[c])], sl, ic) * tw[t];
+                                    v = v + p;
+                                }
+                            }
+                            dst[dx] = v;
                         }
                     }
-                    const float p = c * wyj;
-                    acc[i] = acc[i] + p;
                 }
             }
+            __syncthreads();
+            // combine along y: thread (row phase tr, unit column tc) runs rows tr, tr + RS, ...
+            if (yact) {
+                for (int rr = tr; rr < g.rb; rr += RS) {
+                    const int dy = g.r0 + rr;
+                    float v[UP];
+                    if constexpr (MODE == M_IDENT) {
+                        const float* p = s_st + min(dy - g.s0, last) * img + dx0;
 #pragma unroll
-            for (int i = 0; i < 8; ++i) v[i] = acc[i];
+                        for (int i = 0; i < UP; ++i) v[i] = p[i];
+                    } else if constexpr (MODE == M_BILIN) {
+                        const float sy = src_index(st.rh, dy);
+                        const int h1 = (int)sy;
+                        const int h1p = h1 < st.h - 1 ? 1 : 0;
+                        const float l1 = sy - (float)h1, l0 = 1.0f - l1;
+                        const float* p0 = s_st + min(h1 - g.s0, last) * img + dx0;
+                        const float* p1 = s_st + min(h1 + h1p - g.s0, last) * img + dx0;
+#pragma unroll
+                        for (int i = 0; i < UP; ++i) v[i] = __builtin_fmaf(l0, p0[i], l1 * p1[i]);
+                    } else {
+                        // the row's real taps in table order (its zero-weight padding taps add +0 to
+                        // a finite sum and are skipped: their source row need not be staged)
+                        const int y0t = iy[dy * st.Ty] - g.s0;
+                        const float* tw = wy + dy * st.Ty;
+#pragma unroll
+                        for (int i = 0; i < UP; ++i) v[i] = 0.0f;
+                        for (int j = 0; j < st.Ty; ++j) {
+                            const float wyj = tw[j];
+                            if (!(wyj > 0.0f)) break;
+                            const float* p = s_st + min(y0t + j, last) * img + dx0;
+#pragma unroll
+                            for (int i = 0; i < UP; ++i) {
+                                const float q = p[i] * wyj;
+                                v[i] = v[i] + q;
+                            }
+                        }
+                    }
+                    f(g.kk, dy, dx0, v);
+                }
+            }
+            __syncthreads();
         }
     }
 }
 
-// Runs f(kk, dy, dx0, v) over units [ub, ue) of stack st, thread-strided, with the mode fixed.
-template <class F>
-DEV void for_units(const PStack& st, const PArgs& a, int ub, int ue, F&& f) {
-    auto run = [&](auto mode_tag) {
-        constexpr int MODE = decltype(mode_tag)::value;
-        for (int u = ub + (int)threadIdx.x; u < ue; u += NT) {
-            const int row = u / a.upr;
-            const int dx0 = (u - row * a.upr) * 8;
-            const int kk = st.k0 + row / a.img;
-            const int dy = row - (row / a.img) * a.img;
-            float v[8];
-            eval8<MODE>(st, a.img, kk, dy, dx0, v);
-            f(kk, dy, dx0, v);
+// REGION: the kernel instance for uint16 regions (kind 0) or for float32 stacks (kind 1).  Runs
+// body(mode, rescale, wave-uniform rows) with the stack's mode, whether it has a Rescale and whether
+// an output row is a multiple of 64 units as constants.
+template <int REGION, class B>
+DEV void with_mode(const PStack& st, const PArgs& a, B&& body) {
+    using T = std::true_type;
+    using N = std::false_type;
+    if constexpr (REGION) {
+        const bool h = st.resc != nullptr;
+        auto go = [&](auto m) {
+            if (a.upr % 64 == 0)
+                h ? body(m, T{}, T{}) : body(m, N{}, T{});
+            else
+                h ? body(m, T{}, N{}) : body(m, N{}, N{});
+        };
+        switch (st.mode) {
+            case M_IDENT: go(std::integral_constant<int, M_IDENT>{}); break;
+            case M_BILIN: go(std::integral_constant<int, M_BILIN>{}); break;
+            default: go(std::integral_constant<int, M_AREA>{}); break;
         }
-    };
-    switch (st.mode) {
-        case M_IDENT: run(std::integral_constant<int, M_IDENT>{}); break;
-        case M_BILIN: run(std::integral_constant<int, M_BILIN>{}); break;
-        case M_AREA: run(std::integral_constant<int, M_AREA>{}); break;
-        default: run(std::integral_constant<int, M_FLOAT>{}); break;
+    } else {
+        body(std::integral_constant<int, M_FLOAT>{}, N{}, N{});
     }
 }
 
-DEV int stack_of(const PArgs& a, bool norm) {
+// grid 0: histogram level 1; 1: levels 2 and 3; 2: final pass and resize
+DEV int first_wg(const PStack& p, int grid) { return grid == 0 ? p.wg_hist : grid == 1 ? p.wg_hist2 : p.wg_norm; }
+
+DEV int stack_of(const PArgs& a, int grid) {
     int s = 0;
     for (int i = 1; i < a.n; ++i)
-        if ((int)blockIdx.x >= (norm ? a.s[i].wg_norm : a.s[i].wg_hist)) s = i;
+        if ((int)blockIdx.x >= first_wg(a.s[i], grid)) s = i;
     return s;
 }
 
-// LDS histogram increment; when every active lane of the wave hits the same bin (runs of equal
-// values, e.g. a zero background) one lane adds the count instead of 64 conflicting atomics.
-DEV void hist_inc(uint32_t* h, uint32_t bin) {
-    const uint32_t first = __builtin_amdgcn_readfirstlane(bin);
+// LDS histogram increment by the active lanes of a wave.  MERGE: the lowest lane's index is counted for
+// every lane that holds it with one atomic (runs of equal values or of nearby values in a coarse bin),
+// the other lanes add 1 each.  Otherwise only a wave whose lanes all hold one index (e.g. a zero
+// background) is merged.
+template <bool MERGE>
+DEV void hist_add(uint32_t* h, uint32_t idx) {
     const uint64_t act = __ballot(1);
-    const uint64_t same = __ballot(bin == first);
-    if (same == act) {
-        if ((int)__lane_id() == __builtin_ctzll(act)) atomicAdd(&h[first], (uint32_t)__popcll(act));
+    const int l = __builtin_ctzll(act);
+    const uint32_t key = __builtin_amdgcn_readlane(idx, l);
+    const uint64_t m = __ballot(idx == key);
+    if (MERGE || m == act) {
+        if ((int)__lane_id() == l) atomicAdd(&h[key], (uint32_t)__popcll(m));
+        if (idx != key) atomicAdd(&h[idx], 1u);
     } else {
-        atomicAdd(&h[bin], 1u);
+        atomicAdd(&h[idx], 1u);
     }
 }
 
 // ---- kernels ------------------------------------------------------------------------------------
 
-// Clears the histograms and selections of every stack and builds the area tables.
+// Clears the histograms and selections of every stack, writes the zeros of the output slices outside
+// [k0, k1) (d8s_prep: clear = 1) and builds the area tables.
 __global__ void __launch_bounds__(NT) k_prep_setup(PArgs a, int clear) {
     const PStack& st = a.s[blockIdx.y];
     const int gid = blockIdx.x * NT + threadIdx.x, gsz = gridDim.x * NT;
-    if (clear)
+    if (clear) {
         for (int i = gid; i < W_CLEAR; i += gsz) st.ws[i] = 0u;
+        const int per = a.img * a.img / 8;            // 8-byte words per slice
+        const int outside = (st.K - (st.k1 - st.k0)) * per;
+        for (int i = gid; i < outside; i += gsz) {
+            int kk = i / per;
+            kk = kk < st.k0 ? kk : kk + (st.k1 - st.k0);
+            const int ko = st.flip == D8S_FLIP_SLICES ? st.K - 1 - kk : kk;
+            ((uint2*)st.out)[(int64_t)ko * per + (i % per)] = make_uint2(0u, 0u);
+        }
+    }
     if (st.mode != M_AREA) return;
     int32_t* ix = (int32_t*)st.ws + W_TAPS;
     float* wx = (float*)(ix + a.img * st.Tx);
@@ -302,13 +499,14 @@ __global__ void __launch_bounds__(NT) k_prep_setup(PArgs a, int clear) {
     }
 }
 
-// One radix level over the units of a run of one stack.
-template <int LEVEL>
+// One radix level over the blocks [b0, b0 + hb) of one stack.
+template <int LEVEL, int REGION, bool STORE = false>
 __global__ void __launch_bounds__(NT) k_prep_hist(PArgs a) {
     constexpr int NB = LEVEL == 1 ? NB1 : LEVEL == 2 ? NB2 : NB3;
-    constexpr int NH = LEVEL == 1 ? 1 : 4;
+    constexpr int NH = LEVEL == 1 ? 1 : 2;    // LDS histograms; slots 2 and 3 (rare) count in memory
     __shared__ uint32_t s_h[NH * NB];
-    const int s = stack_of(a, false);
+    __shared__ float s_st[REGION ? STAGE : 1];
+    const int s = stack_of(a, LEVEL == 1 ? 0 : 1);
     const PStack& st = a.s[s];
     for (int i = threadIdx.x; i < NH * NB; i += NT) s_h[i] = 0u;
     uint32_t nslot = 0, pre[4] = {0u, 0u, 0u, 0u};
@@ -319,35 +517,43 @@ __global__ void __launch_bounds__(NT) k_prep_hist(PArgs a) {
         for (int t = 0; t < 4; ++t) pre[t] = sel->pre[t];
     }
     __syncthreads();
-    const int ub = ((int)blockIdx.x - st.wg_hist) * a.hist_units;
-    const int ue = min(ub + a.hist_units, st.units);
+    const int hb = LEVEL == 1 ? st.hb : st.hb2;
+    const int b0 = ((int)blockIdx.x - (LEVEL == 1 ? st.wg_hist : st.wg_hist2)) * hb;
+    const int b1 = min(b0 + hb, st.nblk);
     bool nan = false;
-    for_units(st, a, ub, ue, [&](int, int, int, const float* v) {
+    uint32_t* gh = st.ws + (LEVEL == 1 ? W_H1 : LEVEL == 2 ? W_H2 : W_H3);
+    auto count = [&](int kk, int dy, int dx0, const float* v) {
+        if constexpr (STORE)
+            *(float4*)(st.sc + ((int64_t)kk * a.img + dy) * a.img + dx0) = make_float4(v[0], v[1], v[2], v[3]);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
+        for (int i = 0; i < UP; ++i) {
             const uint32_t k = order_key(v[i]);
             if constexpr (LEVEL == 1) {
                 nan |= v[i] != v[i];
-                hist_inc(s_h, k >> 21);
-            } else if constexpr (LEVEL == 2) {
-                const uint32_t p = k >> 21;
-#pragma unroll
-                for (int t = 0; t < 4; ++t)
-                    if (t < (int)nslot && p == pre[t]) hist_inc(s_h + t * NB, (k >> 10) & (NB2 - 1));
+                hist_add<true>(s_h, k >> 21);
             } else {
-                const uint32_t p = k >> 10;
-#pragma unroll
-                for (int t = 0; t < 4; ++t)
-                    if (t < (int)nslot && p == pre[t]) hist_inc(s_h + t * NB, k & (NB3 - 1));
+                // unused slots hold prefix 0xffffffff, which no key has at these levels
+                const uint32_t p = LEVEL == 2 ? k >> 21 : k >> 10;
+                const uint32_t bin = LEVEL == 2 ? (k >> 10) & (NB2 - 1) : k & (NB3 - 1);
+                if (p == pre[0] || p == pre[1] || p == pre[2] || p == pre[3]) {
+                    // lanes of a wave may match different slots: hist_add merges equal LDS indices
+                    const uint32_t t = p == pre[0] ? 0u : p == pre[1] ? 1u : p == pre[2] ? 2u : 3u;
+                    if (t < (uint32_t)NH)
+                        hist_add<false>(s_h, t * NB + bin);
+                    else
+                        atomicAdd(gh + t * NB + bin, 1u);
+                }
             }
         }
+    };
+    with_mode<REGION>(st, a, [&](auto m, auto h, auto w) {
+        run_blocks<decltype(m)::value, decltype(h)::value, decltype(w)::value>(st, a, b0, b1, s_st, count);
     });
     if constexpr (LEVEL == 1) {
         if (__ballot(nan) != 0ull && (int)__lane_id() == 0) atomicOr(st.ws + W_NAN, 1u);
     }
     __syncthreads();
-    uint32_t* gh = st.ws + (LEVEL == 1 ? W_H1 : LEVEL == 2 ? W_H2 : W_H3);
-    const int nh = LEVEL == 1 ? 1 : (int)nslot;
+    const int nh = LEVEL == 1 ? 1 : min((int)nslot, NH);
     for (int i = threadIdx.x; i < nh * NB; i += NT) {
         const uint32_t c = s_h[i];
         if (c) atomicAdd(gh + i, c);
@@ -464,56 +670,109 @@ __global__ void __launch_bounds__(NT) k_prep_select(PArgs a) {
 }
 
 // Final pass: uint8 of every pixel, written at its flipped position.
+template <int REGION>
 __global__ void __launch_bounds__(NT) k_prep_norm(PArgs a) {
-    const int s = stack_of(a, true);
+    const int s = stack_of(a, 2);
     const PStack& st = a.s[s];
     const D8sPrepStat r = a.stat[s];
-    const int ub = ((int)blockIdx.x - st.wg_norm) * a.norm_units;
-    const int ue = min(ub + a.norm_units, st.units);
+    const double nlo = -r.lo;
+    __shared__ float s_st[REGION ? STAGE : 1];
+    const int b0 = ((int)blockIdx.x - st.wg_norm) * st.nb;
+    const int b1 = min(b0 + st.nb, st.nblk);
     uint8_t* out = (uint8_t*)st.out;
-    for_units(st, a, ub, ue, [&](int kk, int dy, int dx0, const float* v) {
-        uint32_t b[8];
+    auto write = [&](int kk, int dy, int dx0, const float* v) {
+        uint32_t b[UP];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            double y = (double)v[i] - r.lo;
+        for (int i = 0; i < UP; ++i) {
+            // (x - lo) * scale clipped to [0, 255] and truncated; x + (-lo) is x - lo exactly
+            double y = (double)v[i] + nlo;
             y = y * r.scale;
-            y = y < 0.0 ? 0.0 : y;
-            y = y > 255.0 ? 255.0 : y;
-            b[i] = r.bad ? 0u : (uint32_t)y;
+            y = __builtin_fmax(y, 0.0);
+            y = __builtin_fmin(y, 255.0);
+            b[i] = (uint32_t)y;
         }
         const int ko = st.flip == D8S_FLIP_SLICES ? st.K - 1 - kk : kk;
-        uint32_t lo, hi;
+        uint32_t word;
         int xo = dx0;
         if (st.flip == D8S_FLIP_X) {
-            xo = a.img - 8 - dx0;
-            lo = b[7] | (b[6] << 8) | (b[5] << 16) | (b[4] << 24);
-            hi = b[3] | (b[2] << 8) | (b[1] << 16) | (b[0] << 24);
+            xo = a.img - UP - dx0;
+            word = b[3] | (b[2] << 8) | (b[1] << 16) | (b[0] << 24);
         } else {
-            lo = b[0] | (b[1] << 8) | (b[2] << 16) | (b[3] << 24);
-            hi = b[4] | (b[5] << 8) | (b[6] << 16) | (b[7] << 24);
+            word = b[0] | (b[1] << 8) | (b[2] << 16) | (b[3] << 24);
         }
-        uint2* p = (uint2*)(out + ((int64_t)ko * a.img + dy) * a.img + xo);
-        *p = make_uint2(lo, hi);
+        *(uint32_t*)(out + ((int64_t)ko * a.img + dy) * a.img + xo) = word;
+    };
+    if (r.bad) {
+        // a stack with non-finite or equal percentiles (or a NaN) is all zeros: its rows of the blocks
+        const int per = a.img / 4;
+        for (int b = b0; b < b1; ++b) {
+            const int q = b / st.bps, kk = st.k0 + q, r0 = (b - q * st.bps) * st.rb;
+            const int rb = min(st.rb, a.img - r0);
+            const int ko = st.flip == D8S_FLIP_SLICES ? st.K - 1 - kk : kk;
+            uint32_t* o = (uint32_t*)(out + ((int64_t)ko * a.img + r0) * a.img);
+            for (int i = threadIdx.x; i < rb * per; i += NT) o[i] = 0u;
+        }
+        return;
+    }
+    with_mode<REGION>(st, a, [&](auto m, auto h, auto w) {
+        run_blocks<decltype(m)::value, decltype(h)::value, decltype(w)::value>(st, a, b0, b1, s_st, write);
     });
 }
 
 // The resized float32 values themselves.
 __global__ void __launch_bounds__(NT) k_prep_resize(PArgs a) {
-    const int s = stack_of(a, true);
+    const int s = stack_of(a, 2);
     const PStack& st = a.s[s];
-    const int ub = ((int)blockIdx.x - st.wg_norm) * a.norm_units;
-    const int ue = min(ub + a.norm_units, st.units);
+    __shared__ float s_st[STAGE];
+    const int b0 = ((int)blockIdx.x - st.wg_norm) * st.nb;
+    const int b1 = min(b0 + st.nb, st.nblk);
     float* out = (float*)st.out;
-    for_units(st, a, ub, ue, [&](int kk, int dy, int dx0, const float* v) {
-        float4* p = (float4*)(out + ((int64_t)kk * a.img + dy) * a.img + dx0);
-        p[0] = make_float4(v[0], v[1], v[2], v[3]);
-        p[1] = make_float4(v[4], v[5], v[6], v[7]);
+    auto write = [&](int kk, int dy, int dx0, const float* v) {
+        *(float4*)(out + ((int64_t)kk * a.img + dy) * a.img + dx0) = make_float4(v[0], v[1], v[2], v[3]);
+    };
+    with_mode<1>(st, a, [&](auto m, auto h, auto w) {
+        run_blocks<decltype(m)::value, decltype(h)::value, decltype(w)::value>(st, a, b0, b1, s_st, write);
     });
 }
 
 // ---- host side ----------------------------------------------------------------------------------
 #define PREQ(cond, msg) \
     do { if (!(cond)) return d8s_host_fail((int)hipErrorInvalidValue, std::string(what) + ": " + (msg)); } while (0)
+
+// The workgroup ranges of every stack in the three grids (4 blocks per workgroup); returns the size of
+// the per-block grid.
+int assign_grids(PArgs& a) {
+    int wh = 0, wh2 = 0, wn = 0;
+    for (int i = 0; i < a.n; ++i) {
+        PStack& p = a.s[i];
+        p.hb = p.hb2 = p.nb = 4;
+        p.wg_hist = wh;
+        p.wg_hist2 = wh2;
+        p.wg_norm = wn;
+        wh += (p.nblk + p.hb - 1) / p.hb;
+        wh2 += (p.nblk + p.hb2 - 1) / p.hb2;
+        wn += (p.nblk + p.nb - 1) / p.nb;
+    }
+    return wn;
+}
+
+// The float32 view of a kind-0 call after the first pass: every stack reads its resized slices from
+// the scratch buffer (M_FLOAT), in blocks of about 4096 pixels.
+PArgs float_view(const PArgs& a) {
+    PArgs f = a;
+    const int rb = a.img >= 4096 ? 1 : 4096 / a.img;
+    for (int i = 0; i < f.n; ++i) {
+        PStack& p = f.s[i];
+        p.src = p.sc;
+        p.resc = nullptr;
+        p.mode = M_FLOAT;
+        p.rb = rb;
+        p.bps = (a.img + rb - 1) / rb;
+        p.nblk = (p.k1 - p.k0) * p.bps;
+    }
+    assign_grids(f);
+    return f;
+}
 
 int prepare(const D8sPrepArgs* in, const char* what, bool resize_only, PArgs& a, int& setup_blocks) {
     PREQ(in != nullptr, "null arguments");
@@ -526,12 +785,25 @@ int prepare(const D8sPrepArgs* in, const char* what, bool resize_only, PArgs& a,
     d8s_prep_workspace(in->n_stacks, in->img, &need);
     PREQ(in->ws_bytes >= need, "workspace smaller than d8s_prep_workspace()");
     const int img = in->img;
+    if (in->kind == 0 && !resize_only) {
+        uint64_t sc = 0;
+        for (int i = 0; i < in->n_stacks; ++i) {
+            const int64_t sl = (int64_t)in->s[i].k1 - in->s[i].k0;
+            sc += 4ull * (uint64_t)(sl > 0 ? sl : 0) * img * img;
+        }
+        PREQ(in->scratch != 0 && in->scratch % 16 == 0, "scratch null or not 16-byte aligned");
+        PREQ(in->scratch_bytes >= sc, "scratch smaller than 4 * sum(k1 - k0) * img * img bytes");
+    }
     a = PArgs{};
     a.n = in->n_stacks;
     a.img = img;
-    a.upr = img / 8;
+    a.upr = img / UP;
     a.stat = (D8sPrepStat*)in->workspace;
-    int64_t total_units = 0;
+    a.inv_img = 1.0f / (float)img;
+    a.inv_upr = 1.0f / (float)a.upr;
+    PREQ(in->kind == 1 || img <= 1024, "img above 1024 is supported for float32 stacks (kind 1) only");
+    const int rb_want = 4096 / img > 1 ? 4096 / img : 1;     // about 4096 output pixels per block
+    int64_t total_px = 0, sc_off = 0;
     for (int i = 0; i < a.n; ++i) {
         const D8sPrepStack& s = in->s[i];
         PStack& p = a.s[i];
@@ -539,7 +811,7 @@ int prepare(const D8sPrepArgs* in, const char* what, bool resize_only, PArgs& a,
         PREQ(s.src != 0 && s.out != 0, at + "null src or out");
         PREQ(s.K >= 1 && s.k0 >= 0 && s.k0 < s.k1 && s.k1 <= s.K, at + "slice range outside 0 .. K");
         const int64_t n = (int64_t)(s.k1 - s.k0) * img * img;
-        PREQ(n < (1ll << 31), at + "more than 2^31 - 1 pixels");
+        PREQ((int64_t)s.K * img * img < (1ll << 31), at + "more than 2^31 - 1 pixels");
         if (!resize_only) {
             PREQ(n >= 4, at + "fewer than 4 pixels");
             PREQ(s.r1 >= 0 && (int64_t)s.r1 + 1 < n && s.r2 >= 0 && (int64_t)s.r2 + 1 < n,
@@ -554,6 +826,12 @@ int prepare(const D8sPrepArgs* in, const char* what, bool resize_only, PArgs& a,
         p.out = (void*)s.out;
         p.resc = in->kind == 0 ? (const float*)s.resc : nullptr;
         p.ws = (uint32_t*)(in->workspace + WS_HEAD) + (uint64_t)i * stack_words(img);
+        if (in->kind == 0 && !resize_only) {
+            // compact: the slices [k0, k1) of the stacks back to back; sc is offset so that slice kk
+            // is at sc + kk img img
+            p.sc = (float*)in->scratch + (int64_t)sc_off - (int64_t)s.k0 * img * img;
+            sc_off += (int64_t)(s.k1 - s.k0) * img * img;
+        }
         p.K = s.K;
         p.k0 = s.k0;
         p.k1 = s.k1;
@@ -562,61 +840,77 @@ int prepare(const D8sPrepArgs* in, const char* what, bool resize_only, PArgs& a,
         p.r2 = s.r2;
         p.g1 = s.g1;
         p.g2 = s.g2;
-        p.units = (int)(n / 8);
-        total_units += p.units;
+        total_px += n;
         if (in->kind == 1) {
             PREQ(s.src % 16 == 0, at + "float32 input not 16-byte aligned");
             p.mode = M_FLOAT;
-            continue;
-        }
-        PREQ(s.hr >= 1 && s.wr >= 1, at + "empty region");
-        PREQ(s.y0 >= 0 && s.y0 < s.y1 && s.y1 <= s.hr && s.x0 >= 0 && s.x0 < s.x1 && s.x1 <= s.wr,
-             at + "box outside the region");
-        PREQ((int64_t)s.K * s.hr * s.wr < (1ll << 40), at + "region too large");
-        p.hr = s.hr;
-        p.wr = s.wr;
-        p.y0 = s.y0;
-        p.x0 = s.x0;
-        p.h = s.y1 - s.y0;
-        p.w = s.x1 - s.x0;
-        if (p.h == img && p.w == img) {
-            p.mode = M_IDENT;
-        } else if (p.h > img) {
-            p.mode = M_AREA;
-            p.Tx = p.w != img ? area_taps_max(p.w, img) : 0;
-            p.Ty = area_taps_max(p.h, img);
-            PREQ(p.Tx <= MAX_T && p.Ty <= MAX_T, at + "area table longer than 16 taps");
+            p.rb = rb_want;
         } else {
-            p.mode = M_BILIN;
-            p.rh = (float)p.h / (float)img;
-            p.rw = (float)p.w / (float)img;
+            PREQ(s.hr >= 1 && s.wr >= 1, at + "empty region");
+            PREQ(s.y0 >= 0 && s.y0 < s.y1 && s.y1 <= s.hr && s.x0 >= 0 && s.x0 < s.x1 && s.x1 <= s.wr,
+                 at + "box outside the region");
+            PREQ((int64_t)s.K * s.hr * s.wr < (1ll << 31) - 2, at + "region of 2^31 or more values");
+            p.hr = s.hr;
+            p.wr = s.wr;
+            p.y0 = s.y0;
+            p.x0 = s.x0;
+            p.h = s.y1 - s.y0;
+            p.w = s.x1 - s.x0;
+            // LDS per block: ns_max resized rows of img floats + ns_max raw rows of rp dwords
+            p.rp = (p.w + 2) / 2;
+            p.inv_rp = 1.0f / (float)p.rp;
+            p.dpl = (p.rp + 63) / 64;
+            // the LDS holds ns_max rows of img floats and two buffers of ns_max rows of dpl * 64 raw dwords
+            const int cap = STAGE / (img + 128 * p.dpl);
+            if (p.h == img && p.w == img) {
+                p.mode = M_IDENT;
+                PREQ(cap >= 1, at + "crop too wide for this img");
+                p.rb = rb_want < cap ? rb_want : cap;
+                p.ns_max = p.rb;
+            } else if (p.h > img) {
+                p.mode = M_AREA;
+                p.Tx = p.w != img ? area_taps_max(p.w, img) : 0;
+                p.Ty = area_taps_max(p.h, img);
+                PREQ(p.Tx <= MAX_T && p.Ty <= MAX_T, at + "area table longer than 16 taps");
+                // rb output rows read at most rb * h / img + 2 source rows
+                const double scale = (double)p.h / img;
+                PREQ(scale + 2.0 <= cap, at + "area downscale factor too large for this img and width");
+                const int fit = (int)((cap - 2) / scale);
+                p.rb = rb_want < fit ? rb_want : fit;
+                p.ns_max = (int)ceil(p.rb * scale) + 2;
+            } else {
+                p.mode = M_BILIN;
+                p.rh = (float)p.h / (float)img;
+                p.rw = (float)p.w / (float)img;
+                PREQ(cap >= 2, at + "crop too wide for this img");
+                p.rb = rb_want < cap - 1 ? rb_want : cap - 1;   // rb + 1 source rows
+                p.ns_max = p.rb + 1;
+            }
         }
+        p.bps = (img + p.rb - 1) / p.rb;
+        p.nblk = (s.k1 - s.k0) * p.bps;
     }
-    // histogram passes: about 3 workgroups per CU over all stacks (each flushes its LDS histogram
-    // with global atomics, so a workgroup should see many pixels); normalisation: 4 units per thread
-    const int64_t want = 3ll * d8s_host_cu_count();
-    int64_t hu = (total_units + want - 1) / want;
-    hu = (hu + NT - 1) / NT * NT;
-    if (hu < 8 * NT) hu = 8 * NT;
-    a.hist_units = (int)hu;
-    a.norm_units = 4 * NT;
-    int wh = 0, wn = 0;
+    int outside = 0;
     for (int i = 0; i < a.n; ++i) {
-        a.s[i].wg_hist = wh;
-        a.s[i].wg_norm = wn;
-        wh += (a.s[i].units + a.hist_units - 1) / a.hist_units;
-        wn += (a.s[i].units + a.norm_units - 1) / a.norm_units;
+        const PStack& p = a.s[i];
+        const int o = (p.K - (p.k1 - p.k0)) * (img * img / 8);
+        outside = o > outside ? o : outside;
     }
+    const int wn = assign_grids(a);
     PREQ(wn < (1 << 30), "too many workgroups");
-    setup_blocks = (img + NT - 1) / NT;
-    if (setup_blocks < (W_CLEAR + NT * 4 - 1) / (NT * 4)) setup_blocks = (W_CLEAR + NT * 4 - 1) / (NT * 4);
+    int sb = (img + NT - 1) / NT;
+    const int sc = (W_CLEAR + NT * 4 - 1) / (NT * 4), so = (outside + NT * 4 - 1) / (NT * 4);
+    sb = sb > sc ? sb : sc;
+    sb = sb > so ? sb : so;
+    setup_blocks = sb < 1024 ? sb : 1024;
     return 0;
 }
 
-int grid_of(const PArgs& a, bool norm) {
+int grid_of(const PArgs& a, int grid) {
     const PStack& l = a.s[a.n - 1];
-    return (norm ? l.wg_norm : l.wg_hist) +
-           (l.units + (norm ? a.norm_units : a.hist_units) - 1) / (norm ? a.norm_units : a.hist_units);
+    return grid == 0 ? l.wg_hist + (l.nblk + l.hb - 1) / l.hb
+         : grid == 1 ? l.wg_hist2 + (l.nblk + l.hb2 - 1) / l.hb2
+                     : l.wg_norm + (l.nblk + l.nb - 1) / l.nb;
 }
 
 }  // namespace
@@ -637,14 +931,29 @@ extern "C" int d8s_prep(const D8sPrepArgs* in, void* stream) {
     hipStream_t st = (hipStream_t)stream;
     const dim3 gs(sb, a.n);
     k_prep_setup<<<gs, NT, 0, st>>>(a, 1);
-    const int gh = grid_of(a, false), gn = grid_of(a, true);
-    k_prep_hist<1><<<gh, NT, 0, st>>>(a);
-    k_prep_select<1><<<a.n, NT, 0, st>>>(a);
-    k_prep_hist<2><<<gh, NT, 0, st>>>(a);
-    k_prep_select<2><<<a.n, NT, 0, st>>>(a);
-    k_prep_hist<3><<<gh, NT, 0, st>>>(a);
-    k_prep_select<3><<<a.n, NT, 0, st>>>(a);
-    k_prep_norm<<<gn, NT, 0, st>>>(a);
+    const int gh = grid_of(a, 0), gh2 = grid_of(a, 1), gn = grid_of(a, 2);
+    if (in->kind == 0) {
+        // resize once (with the level-1 count) into the scratch stacks, then the float32 passes
+        k_prep_hist<1, 1, true><<<gh, NT, 0, st>>>(a);
+        k_prep_select<1><<<a.n, NT, 0, st>>>(a);
+        const PArgs f = float_view(a);
+        const int fh2 = grid_of(f, 1), fn = grid_of(f, 2);
+        k_prep_hist<2, 0><<<fh2, NT, 0, st>>>(f);
+        k_prep_select<2><<<f.n, NT, 0, st>>>(f);
+        k_prep_hist<3, 0><<<fh2, NT, 0, st>>>(f);
+        k_prep_select<3><<<f.n, NT, 0, st>>>(f);
+        k_prep_norm<0><<<fn, NT, 0, st>>>(f);
+        (void)gh2;
+        (void)gn;
+    } else {
+        k_prep_hist<1, 0><<<gh, NT, 0, st>>>(a);
+        k_prep_select<1><<<a.n, NT, 0, st>>>(a);
+        k_prep_hist<2, 0><<<gh2, NT, 0, st>>>(a);
+        k_prep_select<2><<<a.n, NT, 0, st>>>(a);
+        k_prep_hist<3, 0><<<gh2, NT, 0, st>>>(a);
+        k_prep_select<3><<<a.n, NT, 0, st>>>(a);
+        k_prep_norm<0><<<gn, NT, 0, st>>>(a);
+    }
     return d8s_host_launched("d8s_prep");
 }
 
@@ -654,6 +963,6 @@ extern "C" int d8s_prep_resize(const D8sPrepArgs* in, void* stream) {
     if (const int rc = prepare(in, "d8s_prep_resize", true, a, sb)) return rc;
     hipStream_t st = (hipStream_t)stream;
     k_prep_setup<<<dim3(sb, a.n), NT, 0, st>>>(a, 0);
-    k_prep_resize<<<grid_of(a, true), NT, 0, st>>>(a);
+    k_prep_resize<<<grid_of(a, 2), NT, 0, st>>>(a);
     return d8s_host_launched("d8s_prep_resize");
 }

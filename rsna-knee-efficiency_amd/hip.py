@@ -100,7 +100,8 @@ class PrepStat(ctypes.Structure):
 
 class PrepArgs(ctypes.Structure):
     """`D8sPrepArgs`: the arguments of d8s_prep / d8s_prep_resize."""
-    _fields_ = [("workspace", u64), ("ws_bytes", u64), ("kind", i32), ("img", i32),
+    _fields_ = [("workspace", u64), ("ws_bytes", u64), ("scratch", u64), ("scratch_bytes", u64),
+                ("kind", i32), ("img", i32),
                 ("n_stacks", i32), ("pad_", i32), ("s", PrepStack * PREP_MAX_STACKS)]
 
 

@@ -96,9 +96,24 @@ def _aligned_ptr(ws: torch.Tensor) -> int:
     return (p + 255) // 256 * 256
 
 
+_SCRATCH: dict = {}
+
+
+def _scratch(device: torch.device, nbytes: int) -> torch.Tensor:
+    """Device scratch for the resized float32 stacks of a kind-0 d8s_prep call (kept per device and
+    grown on demand)."""
+    key = str(device)
+    sc = _SCRATCH.get(key)
+    if sc is None or sc.numel() * 4 < nbytes:
+        sc = torch.empty((nbytes + 3) // 4, dtype=torch.float32, device=device)
+        _SCRATCH[key] = sc
+    return sc
+
+
 def _run(entry: str, kind: int, img: int, stacks: list[dict], device: torch.device) -> torch.Tensor:
     """Launches `entry` over `stacks` (dicts of D8sPrepStack fields), 16 at a time, on the current
-    stream.  Returns the workspace (its head holds the stats of the last chunk)."""
+    stream.  Returns the workspace (its head holds the stats of the last chunk).  Calls on one device
+    share the workspace and scratch: they are ordered by the stream they are issued on."""
     ws = _workspace(device, hip.PREP_MAX_STACKS, img)
     stream = torch.cuda.current_stream(device).cuda_stream
     for c in range(0, len(stacks), hip.PREP_MAX_STACKS):
@@ -106,6 +121,10 @@ def _run(entry: str, kind: int, img: int, stacks: list[dict], device: torch.devi
         a = hip.PrepArgs()
         a.workspace = _aligned_ptr(ws)
         a.ws_bytes = ws.numel() - (a.workspace - ws.data_ptr())
+        if entry == "d8s_prep" and kind == 0:
+            need = sum(4 * (s["k1"] - s["k0"]) * img * img for s in chunk)
+            sc = _scratch(device, need)
+            a.scratch, a.scratch_bytes = sc.data_ptr(), sc.numel() * 4
         a.kind, a.img, a.n_stacks = kind, img, len(chunk)
         for i, s in enumerate(chunk):
             for k, v in s.items():

@@ -68,13 +68,15 @@ def test_struct_layouts_match_header(tmp_path):
     assert got[6] == [ctypes.sizeof(PA), PA.kind.offset, PA.s.offset, ctypes.sizeof(hip.PrepStat)]
 
 
-def _prep_args(kind=0, ws_bytes=None, box=(0, 64, 0, 64), r2=None, k=(0, 1), hr=64, out=256):
+def _prep_args(kind=0, ws_bytes=None, box=(0, 64, 0, 64), r2=None, k=(0, 1), hr=64, out=256,
+               scratch_bytes=1 << 40):
     """A d8s_prep argument set that is valid except for the field a test changes (fake pointers: the
     checks run before any HIP call)."""
     a = hip.PrepArgs()
     need = ctypes.c_uint64()
     assert hip.library().d8s_prep_workspace(1, 64, ctypes.byref(need)) == 0
     a.workspace, a.ws_bytes = 1 << 20, need.value if ws_bytes is None else ws_bytes
+    a.scratch, a.scratch_bytes = 1 << 24, scratch_bytes
     a.kind, a.img, a.n_stacks = kind, 64, 1
     s = a.s[0]
     s.src, s.out, s.K, s.hr, s.wr = 4096, out, 1, hr, 64
@@ -119,6 +121,7 @@ def test_prep_workspace_size():
     ("d8s_prep", lambda: (None, None)),
     ("d8s_prep", lambda: (ctypes.byref(_prep_args(kind=2)), None)),
     ("d8s_prep", lambda: (ctypes.byref(_prep_args(ws_bytes=1024)), None)),
+    ("d8s_prep", lambda: (ctypes.byref(_prep_args(scratch_bytes=64 * 64 * 4 - 4)), None)),
     ("d8s_prep", lambda: (ctypes.byref(_prep_args(box=(0, 65, 0, 64))), None)),
     ("d8s_prep", lambda: (ctypes.byref(_prep_args(r2=64 * 64 - 1)), None)),
     ("d8s_prep", lambda: (ctypes.byref(_prep_args(k=(1, 1))), None)),
