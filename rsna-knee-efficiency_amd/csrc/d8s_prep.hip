@@ -49,7 +49,7 @@ constexpr int NB1 = 2048, NB2 = 2048, NB3 = 1024;  // radix levels: key bits 31.
 constexpr int MAX_S = D8S_PREP_MAX_STACKS;
 constexpr int MAX_T = D8S_PREP_MAX_TAPS;
 constexpr int UP = 4;                            // output pixels per thread step (one 16-byte LDS read)
-constexpr int STAGE = 8192;                      // LDS of the block kernels: 32 KB (resized rows + raw rows)
+constexpr int STAGE = 10240;                     // LDS of the block kernels: 40 KB (resized rows + raw rows)
 
 // per-stack workspace block, in 32-bit words
 constexpr int W_H1 = 0;
@@ -90,6 +90,7 @@ struct PStack {
     double g1, g2;
     int rb, bps, nblk;   // output rows per block, blocks per slice, blocks of the slices [k0, k1)
     int ns_max, rp, dpl; // source rows a block may read; LDS dwords per staged raw row; per lane
+    int dbuf;            // 1: two raw buffers (block b+1 copied during block b's x pass); 0: one
     float inv_rp;
     int hb, hb2, nb;     // blocks per workgroup: histogram level 1, levels 2-3, final pass
     int wg_hist, wg_hist2, wg_norm;  // first workgroup of this stack in each grid
@@ -279,9 +280,10 @@ DEV void run_blocks(const PStack& st, const PArgs& a, int b0, int b1, float* s_s
         const int32_t* iy = (const int32_t*)(wx + img * st.Tx);
         const float* wy = (const float*)(iy + img * st.Ty);
         const int pitch = st.dpl * 64;               // dwords per staged raw row
-        // two raw buffers: block b+1 is copied while block b is resized
+        // raw buffers: with two, block b+1 is copied during block b's x pass; with one, during its
+        // y pass
         uint32_t* s_raw0 = (uint32_t*)(s_st + st.ns_max * img);
-        uint32_t* s_raw1 = s_raw0 + st.ns_max * pitch;
+        uint32_t* s_raw1 = st.dbuf ? s_raw0 + st.ns_max * pitch : s_raw0;
         // x-pass mapping: img >= NT: columns tid + c NT, every row; img < NT: column tid % img, rows
         // tid / img + P j (threads beyond P img rest)
         const int P = img >= NT ? 1 : NT / img;
@@ -289,7 +291,8 @@ DEV void run_blocks(const PStack& st, const PArgs& a, int b0, int b1, float* s_s
         const int col0 = (int)threadIdx.x - ph * img;
         const bool xact = ph < P;
         int ca[CMAX], cb[CMAX];          // uint16 index of the two taps (bilinear) / first tap (area)
-        float cm0[CMAX], cm1[CMAX];
+        float cm0[CMAX], cm1[CMAX];      // bilinear weights / area: first and middle tap weights
+        float cwl[CMAX];                 // area: last tap weight; cb = number of real taps
 #pragma unroll
         for (int c = 0; c < CMAX; ++c) {
             const int dx = min(col0 + c * NT, img - 1);
@@ -303,7 +306,19 @@ DEV void run_blocks(const PStack& st, const PArgs& a, int b0, int b1, float* s_s
                 cm1[c] = sx - (float)w1;
                 cm0[c] = 1.0f - cm1[c];
             } else if constexpr (MODE == M_AREA) {
-                if (st.w != img) ca[c] = ix[dx * st.Tx];
+                // a table row is [first, middle ..., last] with equal middle weights
+                // (raw_crop.py:361-369), then zero padding: keep first / middle / last and the count
+                cwl[c] = 0.0f;
+                if (st.w != img) {
+                    const float* tw = wx + dx * st.Tx;
+                    ca[c] = ix[dx * st.Tx];
+                    int n = 0;
+                    for (int t = 0; t < st.Tx; ++t) n += tw[t] > 0.0f ? 1 : 0;
+                    cb[c] = n;
+                    cm0[c] = tw[0];
+                    cm1[c] = n > 2 ? tw[1] : 0.0f;
+                    cwl[c] = tw[n > 0 ? n - 1 : 0];
+                }
             }
         }
         // uint16 parity of the crop rows: row index q starts at element (src / 2) + q wr + x0
@@ -323,7 +338,7 @@ DEV void run_blocks(const PStack& st, const PArgs& a, int b0, int b1, float* s_s
             const uint16_t* raw16 = (const uint16_t*)((b - b0) & 1 ? s_raw1 : s_raw0);
             asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
             __syncthreads();
-            if (b + 1 < b1) {
+            if (st.dbuf && b + 1 < b1) {
                 nxt = block_geo<MODE>(st, a, b + 1);
                 raw_stage(st, nxt, (b - b0) & 1 ? s_raw0 : s_raw1);
             }
@@ -347,11 +362,16 @@ DEV void run_blocks(const PStack& st, const PArgs& a, int b0, int b1, float* s_s
                             } else if (st.w == img) {
                                 v = rescale<HAS>(row[dx], sl, ic);
                             } else {
+                                // every tap of the table in order; the padding taps (weight 0) read
+                                // a neighbour (x * 0 adds nothing to a finite sum)
                                 v = 0.0f;
                                 const uint16_t* tp = row + ca[c];
-                                const float* tw = wx + dx * st.Tx;
+                                const int lim = st.w - 1 - ca[c];
                                 for (int t = 0; t < st.Tx; ++t) {
-                                    const float p = rescale<HAS>(tp[min(t, st.w - 1 - ca[c])], sl, ic) * tw[t];
+                                    const float wt = t == 0 ? cm0[c]
+                                                   : t >= cb[c] ? 0.0f
+                                                   : t == cb[c] - 1 ? cwl[c] : cm1[c];
+                                    const float p = rescale<HAS>(tp[min(t, lim)], sl, ic) * wt;
                                     v = v + p;
                                 }
                             }
@@ -361,6 +381,10 @@ DEV void run_blocks(const PStack& st, const PArgs& a, int b0, int b1, float* s_s
                 }
             }
             __syncthreads();
+            if (!st.dbuf && b + 1 < b1) {
+                nxt = block_geo<MODE>(st, a, b + 1);
+                raw_stage(st, nxt, s_raw0);
+            }
             // combine along y: thread (row phase tr, unit column tc) runs rows tr, tr + RS, ...
             if (yact) {
                 for (int rr = tr; rr < g.rb; rr += RS) {
@@ -440,24 +464,6 @@ DEV int stack_of(const PArgs& a, int grid) {
     return s;
 }
 
-// LDS histogram increment by the active lanes of a wave.  MERGE: the lowest lane's index is counted for
-// every lane that holds it with one atomic (runs of equal values or of nearby values in a coarse bin),
-// the other lanes add 1 each.  Otherwise only a wave whose lanes all hold one index (e.g. a zero
-// background) is merged.
-template <bool MERGE>
-DEV void hist_add(uint32_t* h, uint32_t idx) {
-    const uint64_t act = __ballot(1);
-    const int l = __builtin_ctzll(act);
-    const uint32_t key = __builtin_amdgcn_readlane(idx, l);
-    const uint64_t m = __ballot(idx == key);
-    if (MERGE || m == act) {
-        if ((int)__lane_id() == l) atomicAdd(&h[key], (uint32_t)__popcll(m));
-        if (idx != key) atomicAdd(&h[idx], 1u);
-    } else {
-        atomicAdd(&h[idx], 1u);
-    }
-}
-
 // ---- kernels ------------------------------------------------------------------------------------
 
 // Clears the histograms and selections of every stack, writes the zeros of the output slices outside
@@ -521,34 +527,58 @@ __global__ void __launch_bounds__(NT) k_prep_hist(PArgs a) {
     const int b0 = ((int)blockIdx.x - (LEVEL == 1 ? st.wg_hist : st.wg_hist2)) * hb;
     const int b1 = min(b0 + hb, st.nblk);
     bool nan = false;
+    uint32_t run_bin = 0xffffffffu, run_n = 0u;   // the thread's current run of one histogram index
     uint32_t* gh = st.ws + (LEVEL == 1 ? W_H1 : LEVEL == 2 ? W_H2 : W_H3);
+    auto run_flush = [&]() {
+        if (LEVEL == 1 || run_bin < (uint32_t)(NH * NB))
+            atomicAdd(&s_h[run_bin], run_n);
+        else
+            atomicAdd(gh + run_bin, run_n);
+    };
     auto count = [&](int kk, int dy, int dx0, const float* v) {
         if constexpr (STORE)
             *(float4*)(st.sc + ((int64_t)kk * a.img + dy) * a.img + dx0) = make_float4(v[0], v[1], v[2], v[3]);
+        if constexpr (LEVEL == 1) {
+            // a thread's values are neighbours (UP along x, then the next row of its column), so they
+            // mostly share a (coarse) level-1 bin: the thread counts a run in a register and adds it
+            // to LDS when the bin changes
+#pragma unroll
+            for (int i = 0; i < UP; ++i) {
+                nan |= v[i] != v[i];
+                const uint32_t b = order_key(v[i]) >> 21;
+                if (b != run_bin) {
+                    if (run_n) run_flush();
+                    run_bin = b;
+                    run_n = 0u;
+                }
+                ++run_n;
+            }
+            return;
+        }
 #pragma unroll
         for (int i = 0; i < UP; ++i) {
+            // the keys under one of the slots' prefixes (unused slots hold 0xffffffff, which no key
+            // has at these levels), counted in runs as at level 1 (runs of equal values, e.g. a zero
+            // background, are common); index = slot * NB + bin, slots from NH on count in memory
             const uint32_t k = order_key(v[i]);
-            if constexpr (LEVEL == 1) {
-                nan |= v[i] != v[i];
-                hist_add<true>(s_h, k >> 21);
-            } else {
-                // unused slots hold prefix 0xffffffff, which no key has at these levels
-                const uint32_t p = LEVEL == 2 ? k >> 21 : k >> 10;
-                const uint32_t bin = LEVEL == 2 ? (k >> 10) & (NB2 - 1) : k & (NB3 - 1);
-                if (p == pre[0] || p == pre[1] || p == pre[2] || p == pre[3]) {
-                    // lanes of a wave may match different slots: hist_add merges equal LDS indices
-                    const uint32_t t = p == pre[0] ? 0u : p == pre[1] ? 1u : p == pre[2] ? 2u : 3u;
-                    if (t < (uint32_t)NH)
-                        hist_add<false>(s_h, t * NB + bin);
-                    else
-                        atomicAdd(gh + t * NB + bin, 1u);
+            const uint32_t p = LEVEL == 2 ? k >> 21 : k >> 10;
+            const uint32_t bin = LEVEL == 2 ? (k >> 10) & (NB2 - 1) : k & (NB3 - 1);
+            if (p == pre[0] || p == pre[1] || p == pre[2] || p == pre[3]) {
+                const uint32_t t = p == pre[0] ? 0u : p == pre[1] ? 1u : p == pre[2] ? 2u : 3u;
+                const uint32_t idx = t * NB + bin;
+                if (idx != run_bin) {
+                    if (run_n) run_flush();
+                    run_bin = idx;
+                    run_n = 0u;
                 }
+                ++run_n;
             }
         }
     };
     with_mode<REGION>(st, a, [&](auto m, auto h, auto w) {
         run_blocks<decltype(m)::value, decltype(h)::value, decltype(w)::value>(st, a, b0, b1, s_st, count);
     });
+    if (run_n) run_flush();
     if constexpr (LEVEL == 1) {
         if (__ballot(nan) != 0ull && (int)__lane_id() == 0) atomicOr(st.ws + W_NAN, 1u);
     }
@@ -860,8 +890,12 @@ int prepare(const D8sPrepArgs* in, const char* what, bool resize_only, PArgs& a,
             p.rp = (p.w + 2) / 2;
             p.inv_rp = 1.0f / (float)p.rp;
             p.dpl = (p.rp + 63) / 64;
-            // the LDS holds ns_max rows of img floats and two buffers of ns_max rows of dpl * 64 raw dwords
-            const int cap = STAGE / (img + 128 * p.dpl);
+            // the LDS holds ns_max rows of img floats and one or two buffers of ns_max rows of
+            // dpl * 64 raw dwords: two when that still gives blocks of rb_want rows
+            const double sc_h = p.h > img ? (double)p.h / img : 1.0;
+            const int need = (int)ceil(rb_want * sc_h) + 2;
+            p.dbuf = need * (img + 128 * p.dpl) <= STAGE ? 1 : 0;
+            const int cap = STAGE / (img + (p.dbuf ? 128 : 64) * p.dpl);
             if (p.h == img && p.w == img) {
                 p.mode = M_IDENT;
                 PREQ(cap >= 1, at + "crop too wide for this img");
