@@ -14,13 +14,22 @@ The two seeds' passes of a step run from two streams (`--serial`: one after the 
 graph and replayed between HIP events on the encoder's stream (algorithmic bytes of a launch / the
 average launch time).
 `cpu_baseline`: the float32 DenseNet169 forward (`oracle/fp32.py`) at batch 1 on the host cores.
+`prep`: the upstream preparation (raw uint16 crops -> the uint8 volume of a study, `d8s_prep`) on the
+same GPU, studies/s with the payloads resident in HBM.
 One JSON line on stdout.
+
+    python bench.py --path prep [--steps K] [--warmup W] [--no-cpu]
+
+The preparation alone, one study per step (4 series x 2 crops x 24 slices at 512 px, slices 0:23),
+with its own `roofline` (bytes of the whole d8s_prep launch sequence per study) and `cpu_baseline`
+(the oracle's chain on one study).
 """
 from __future__ import annotations
 
 import argparse
 import json
 import os
+import re
 import platform
 import sys
 import time
@@ -342,13 +351,92 @@ def prep_cpu_baseline(payload: dict, read_slices) -> dict:
                       f"{read_slices[0]}:{read_slices[1]}) through oracle/prep.py: {dt:.2f} s"}
 
 
+PREP_TRAFFIC_FILE = ROOT / "profiles" / "prep_study512_hbm_traffic.md"
+
+
+def prep_studies(dev: torch.device) -> tuple[list, list]:
+    """The two synthetic studies of the preparation benchmark: host payloads and their device copies."""
+    pays = [synthetic.study_payload(IMG, SLICES, seed=100 + i) for i in range(2)]
+    dpays = [{"raw": torch.from_numpy(p["raw"]).to(dev), "u8": torch.from_numpy(p["u8"]).to(dev),
+              "resc": torch.from_numpy(p["resc"]).to(dev), "meta": p["meta"]} for p in pays]
+    return pays, dpays
+
+
+def prep_pmc(dev: torch.device, passes: int, copy: bool) -> dict:
+    """`passes` studies through the preparation, eagerly (the launches of a counter run)."""
+    from rsna_knee_efficiency_amd import prep
+    spec = prep.PrepSpec(img=IMG, slices=SLICES, n_seq=4, n_scales=2)
+    pays, dpays = prep_studies(dev)
+    for k in range(passes):
+        prep.payloads_to_uint8([dpays[k % 2]], spec, dev, read_slices=PREP_READ_SLICES)
+    torch.cuda.synchronize()
+    res = {"passes": passes, "algorithmic_bytes_per_study": sum(prep_bytes(p, IMG, 2, PREP_READ_SLICES)
+                                                                for p in pays) / 2}
+    if copy:
+        res["copy_probe"] = copy_probe(dev, reps=1)
+    return res
+
+
+def prep_traffic_summary(fetch_dir: str, write_dir: str, passes: int, copy_bytes: int = 1 << 30) -> str:
+    """HBM bytes per study of the preparation kernels from two `bench.py --path prep --pmc-passes P
+    --copy-probe` counter runs (FETCH_SIZE, then WRITE_SIZE, KiB per dispatch), each scaled by what the
+    counter reads for k_copy (1 GiB read + 1 GiB written per dispatch)."""
+    import csv
+    import glob
+
+    def collect(d: str, counter: str) -> dict:
+        acc: dict = {}
+        for path in glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True):
+            for r in csv.DictReader(open(path)):
+                name = r.get("Kernel_Name", "")
+                fam = _family(name)
+                if fam and r["Counter_Name"] == counter:
+                    m = re.search(r"(k_prep_\w+(?:<[^>]*>)?)", name)
+                    key = "copy" if fam == "copy" else (m.group(1) if m else name)
+                    v = acc.setdefault(key, [0, 0.0])
+                    v[0] += 1
+                    v[1] += float(r["Counter_Value"]) * 1024
+        return acc
+
+    fe, wr = collect(fetch_dir, "FETCH_SIZE"), collect(write_dir, "WRITE_SIZE")
+    kf = copy_bytes / (fe["copy"][1] / fe["copy"][0])
+    kw = copy_bytes / (wr["copy"][1] / wr["copy"][0])
+    pays = [synthetic.study_payload(IMG, SLICES, seed=100 + i) for i in range(2)]
+    alg = sum(prep_bytes(p, IMG, 2, PREP_READ_SLICES) for p in pays) / 2
+    lines = [f"Calibration: k_copy moves {copy_bytes} B read + {copy_bytes} B written per dispatch; "
+             f"FETCH_SIZE scale {kf:.3f}, WRITE_SIZE scale {kw:.3f}.  {passes} studies.", "",
+             "| kernel | dispatches per study | HBM read MB/study | HBM write MB/study |",
+             "|---|---|---|---|"]
+    tot = 0.0
+    for k in sorted(set(fe) | set(wr)):
+        if k == "copy":
+            continue
+        n = fe.get(k, [0, 0.0])[0] / passes
+        rd = fe.get(k, [0, 0.0])[1] * kf / passes
+        wt = wr.get(k, [0, 0.0])[1] * kw / passes
+        tot += rd + wt
+        lines.append(f"| `{k}` | {n:g} | {rd / 1e6:.2f} | {wt / 1e6:.2f} |")
+    lines += ["", f"Traffic per study {tot / 1e6:.1f} MB; algorithmic bytes per study {alg / 1e6:.1f} MB "
+                  f"(each stored uint16 value read once, each uint8 written once); ratio "
+                  f"{tot / alg:.2f}.", "", "```", f"traffic_per_study = {int(tot)}", "```"]
+    return "\n".join(lines)
+
+
+def committed_prep_traffic() -> int | None:
+    try:
+        for line in PREP_TRAFFIC_FILE.read_text().splitlines():
+            if line.startswith("traffic_per_study = "):
+                return int(line.split("=")[1])
+    except OSError:
+        pass
+    return None
+
+
 def bench_prep(dev: torch.device, steps: int, warmup: int, with_cpu: bool) -> dict:
     """The preparation path (raw crops -> uint8 volume) on studies resident in HBM."""
     from rsna_knee_efficiency_amd import prep
     spec = prep.PrepSpec(img=IMG, slices=SLICES, n_seq=4, n_scales=2)
-    pays = [synthetic.study_payload(IMG, SLICES, seed=100 + i) for i in range(2)]
-    dpays = [{"raw": torch.from_numpy(p["raw"]).to(dev), "u8": torch.from_numpy(p["u8"]).to(dev),
-              "resc": torch.from_numpy(p["resc"]).to(dev), "meta": p["meta"]} for p in pays]
+    pays, dpays = prep_studies(dev)
     rs = PREP_READ_SLICES
     for k in range(warmup):
         prep.payloads_to_uint8([dpays[k % 2]], spec, dev, read_slices=rs)
@@ -377,7 +465,8 @@ def bench_prep(dev: torch.device, steps: int, warmup: int, with_cpu: bool) -> di
         "gpu_ms_per_study": round(gpu_ms, 4),
         "roofline": {"bound": "hbm", "kernel": "d8s_prep (its 8 launches per call, between HIP events)",
                      "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": committed_prep_traffic(),
+                     "traffic_unit": "bytes per study (profiles/prep_study512_hbm_traffic.md)",
                      "algorithmic_bytes_per_study": int(nbytes)},
     }
     if with_cpu:
@@ -411,7 +500,10 @@ def main() -> None:
         print(rocprof_summary(args.rocprof_summary))
         return
     if args.traffic_summary:
-        print(traffic_summary(*args.traffic_summary, passes=args.pmc_passes or 3))
+        if args.path == "prep":
+            print(prep_traffic_summary(*args.traffic_summary, passes=args.pmc_passes or 3))
+        else:
+            print(traffic_summary(*args.traffic_summary, passes=args.pmc_passes or 3))
         return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print(f"bench.py: this build runs on one GPU (the encoder is per-GPU, replicas need no "
@@ -424,7 +516,10 @@ def main() -> None:
     torch.backends.cuda.matmul.allow_tf32 = False
     dev = torch.device("cuda:0")
     if args.path == "prep":
-        print(json.dumps(bench_prep(dev, args.steps, args.warmup, not args.no_cpu)), flush=True)
+        if args.pmc_passes:
+            print(json.dumps(prep_pmc(dev, args.pmc_passes, args.copy_probe)), flush=True)
+        else:
+            print(json.dumps(bench_prep(dev, args.steps, args.warmup, not args.no_cpu)), flush=True)
         return
     t0 = time.perf_counter()
     nb = 4 * SLICES                                     # 2 crops x 24 slices x flip
@@ -532,6 +627,10 @@ def main() -> None:
                      "algorithmic_bytes_per_launch": int(dom_bytes / launches),
                      "avg_launch_ms": round(avg_ms, 5)},
     }
+    # the upstream preparation (raw crops -> uint8 volume), its own throughput on the same GPU
+    pr = bench_prep(dev, max(args.steps, 20), args.warmup, False)
+    out["prep"] = {k: pr[k] for k in ("metric", "value", "unit", "gpu_ms_per_study", "roofline", "config")}
+    log(f"prep: {pr['value']} studies/s, {pr['gpu_ms_per_study']} ms GPU per study")
     if args.copy_probe:
         out["copy_probe"] = copy_probe(dev)
         log(f"copy probe: {out['copy_probe']}")
