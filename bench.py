@@ -432,6 +432,31 @@ def committed_prep_traffic() -> int | None:
     return None
 
 
+def bench_zoom(dev: torch.device, reps: int = 20) -> dict:
+    """The submission's geometric view on one study: the windows of 8 slots x 11 triplets (stride 2,
+    depth 3, 24 slices) gathered from the uint8 volume and zoomed 1.10 (`tta.windows_u8`), between HIP
+    events.  Bytes: each fp16 output once plus each uint8 slice read once."""
+    from rsna_knee_efficiency_amd import tta
+    v = torch.randint(0, 256, (1, 8, SLICES, IMG, IMG), dtype=torch.uint8, device=dev)
+    starts = list(range(0, SLICES - 2, 2))
+    idx = torch.tensor([s * SLICES + t + d for s in range(8) for t in starts for d in range(3)],
+                       dtype=torch.int64, device=dev)
+    out = torch.empty((idx.numel() // 3, 3, IMG, IMG), dtype=torch.float16, device=dev)
+    for _ in range(3):
+        tta.windows_u8(v, idx, out, 1.10)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        tta.windows_u8(v, idx, out, 1.10)
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / reps
+    nbytes = out.numel() * 2 + 8 * SLICES * IMG * IMG
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    return {"windows": int(out.shape[0]), "gpu_ms": round(ms, 4), "bytes": int(nbytes), "gbs": round(gbs, 1),
+            "frac": round(gbs / HBM_PEAK_GBS, 4)}
+
+
 def bench_prep(dev: torch.device, steps: int, warmup: int, with_cpu: bool) -> dict:
     """The preparation path (raw crops -> uint8 volume) on studies resident in HBM."""
     from rsna_knee_efficiency_amd import prep
@@ -469,6 +494,7 @@ def bench_prep(dev: torch.device, steps: int, warmup: int, with_cpu: bool) -> di
                      "traffic_unit": "bytes per study (profiles/prep_study512_hbm_traffic.md)",
                      "algorithmic_bytes_per_study": int(nbytes)},
     }
+    out["zoom_view"] = bench_zoom(dev)
     if with_cpu:
         log("prep cpu baseline ...")
         out["cpu_baseline"] = prep_cpu_baseline(pays[0], rs)
@@ -629,7 +655,8 @@ def main() -> None:
     }
     # the upstream preparation (raw crops -> uint8 volume), its own throughput on the same GPU
     pr = bench_prep(dev, max(args.steps, 20), args.warmup, False)
-    out["prep"] = {k: pr[k] for k in ("metric", "value", "unit", "gpu_ms_per_study", "roofline", "config")}
+    out["prep"] = {k: pr[k] for k in ("metric", "value", "unit", "gpu_ms_per_study", "roofline", "config",
+                                      "zoom_view")}
     log(f"prep: {pr['value']} studies/s, {pr['gpu_ms_per_study']} ms GPU per study")
     if args.copy_probe:
         out["copy_probe"] = copy_probe(dev)

@@ -265,6 +265,32 @@ int d8s_prep(const D8sPrepArgs* a, void* stream);
  * raw_crop.py:419-432,520-527) into `out`, slices [k0, k1); flip and ranks are ignored. */
 int d8s_prep_resize(const D8sPrepArgs* a, void* stream);
 
+/* ---- Geometric TTA view: bilinear grid sampling of fp16 windows --------------------------------
+ *
+ * The reference's zoom / shift view (src/knee/tta.py:131-148 `affine_windows`: `F.affine_grid` once,
+ * expanded, then `F.grid_sample(mode="bilinear", padding_mode="zeros", align_corners=False)` in fp16)
+ * applied to windows gathered from the uint8 volume (src/knee/infer.py:973-1012: `gather_u8_f16`,
+ * src/knee/data/fused_uint8.py:480-506, then `affine_windows`).  One grid [H][W][2] (fp16, the output
+ * of `F.affine_grid`) is shared by every image.
+ *   kind 0: src fp16 images [N][H][W] (N = windows x depth), out[n] = sample(src[n]);
+ *   kind 1: src uint8 volume [B][SK][H][W], slice_idx int64 [M], lut fp16 [256] (u / 255):
+ *           out[b * M + m] = sample(lut[src[b][slice_idx[m]]]), N = B * M (the fused gather); with
+ *           grid = 0 the gather alone, out = lut[...] (the identity view).
+ * Arithmetic: that of torch's grid_sampler_2d kernel in float32 (source index
+ * fma(g + 1, size, -1) / 2, weights (x_se - x)(y_se - y) ..., taps accumulated by fma in the order
+ * nw, ne, sw, se, out of range taps skipped), rounded once to fp16. */
+typedef struct D8sGridArgs {
+    uint64_t src;        /* see kind */
+    uint64_t slice_idx;  /* kind 1 */
+    uint64_t lut;        /* kind 1 */
+    uint64_t grid;       /* fp16 [H][W][2] (kind 1: 0 for the gather alone) */
+    uint64_t out;        /* fp16 [N][H][W] */
+    int32_t kind, N, H, W;
+    int32_t B, SK, M, pad_;  /* kind 1 */
+} D8sGridArgs;
+
+int d8s_grid_sample(const D8sGridArgs* a, void* stream);
+
 /* Library identification: "d8s-hip <abi> <source hash> gfx950". */
 const char* d8s_version(void);
 

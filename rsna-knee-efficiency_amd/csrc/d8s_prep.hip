@@ -29,6 +29,7 @@
 //   uint8     numpy's _lerp on the order statistics (float32 difference, float64 product and sum, the
 //             t >= 0.5 form), scale = 255 / (hi - lo) (correctly rounded float64 division), then
 //             ((double)x - lo) * scale clipped to [0, 255] and truncated (cache.py:319-340).
+#include <hip/hip_fp16.h>
 #include <hip/hip_runtime.h>
 
 #include <math.h>
@@ -765,6 +766,69 @@ __global__ void __launch_bounds__(NT) k_prep_resize(PArgs a) {
     });
 }
 
+// ---- grid sampling (geometric TTA view) -------------------------------------------------------
+// A thread owns one output pixel for a group of GIMG images: the grid is shared by all images, so the
+// source taps and weights are computed once and applied to each image (torch's grid_sampler_2d
+// arithmetic in float32, as its compiler contracts it, rounded once to fp16).  KIND 1 gathers the
+// images from the uint8 volume through the u / 255 fp16 table; KIND 2 is that gather alone.
+constexpr int GIMG = 8;
+
+template <int KIND>
+__global__ void __launch_bounds__(NT) k_grid_sample(D8sGridArgs a) {
+    __shared__ uint16_t s_lut[256];
+    if constexpr (KIND >= 1) {
+        if (threadIdx.x < 256) s_lut[threadIdx.x] = ((const uint16_t*)a.lut)[threadIdx.x];
+        __syncthreads();
+    }
+    const int HW = a.H * a.W;
+    const int p = blockIdx.x * NT + threadIdx.x;
+    const int n0 = blockIdx.y * GIMG, n1 = min(n0 + GIMG, a.N);
+    if (p >= HW) return;
+    // the image n: its source plane
+    auto plane = [&](int n) -> int64_t {
+        if constexpr (KIND >= 1) {
+            const int b = n / a.M, m = n - b * a.M;
+            return ((int64_t)b * a.SK + ((const int64_t*)a.slice_idx)[m]) * HW;
+        } else {
+            return (int64_t)n * HW;
+        }
+    };
+    if constexpr (KIND == 2) {
+        for (int n = n0; n < n1; ++n)
+            ((uint16_t*)a.out)[(int64_t)n * HW + p] = s_lut[((const uint8_t*)a.src)[plane(n) + p]];
+        return;
+    } else {
+        const __half2 g = ((const __half2*)a.grid)[p];
+        const float gx = __low2float(g), gy = __high2float(g);
+        const float ix = __builtin_fmaf(gx + 1.0f, (float)a.W, -1.0f) * 0.5f;
+        const float iy = __builtin_fmaf(gy + 1.0f, (float)a.H, -1.0f) * 0.5f;
+        const int x0 = (int)floorf(ix), y0 = (int)floorf(iy);
+        const int x1 = x0 + 1, y1 = y0 + 1;
+        const float w[4] = {((float)x1 - ix) * ((float)y1 - iy), (ix - (float)x0) * ((float)y1 - iy),
+                            ((float)x1 - ix) * (iy - (float)y0), (ix - (float)x0) * (iy - (float)y0)};
+        const bool vx0 = x0 >= 0 && x0 < a.W, vx1 = x1 >= 0 && x1 < a.W;
+        const bool vy0 = y0 >= 0 && y0 < a.H, vy1 = y1 >= 0 && y1 < a.H;
+        const bool ok[4] = {vy0 && vx0, vy0 && vx1, vy1 && vx0, vy1 && vx1};
+        const int off[4] = {y0 * a.W + x0, y0 * a.W + x1, y1 * a.W + x0, y1 * a.W + x1};
+        for (int n = n0; n < n1; ++n) {
+            const int64_t pl = plane(n);
+            float acc = 0.0f;
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                if (ok[t]) {
+                    float v;
+                    if constexpr (KIND == 1)
+                        v = __half2float(__ushort_as_half(s_lut[((const uint8_t*)a.src)[pl + off[t]]]));
+                    else
+                        v = __half2float(((const __half*)a.src)[pl + off[t]]);
+                    acc = __builtin_fmaf(v, w[t], acc);
+                }
+            }
+            ((__half*)a.out)[(int64_t)n * HW + p] = __float2half_rn(acc);
+        }
+    }
+}
+
 // ---- host side ----------------------------------------------------------------------------------
 #define PREQ(cond, msg) \
     do { if (!(cond)) return d8s_host_fail((int)hipErrorInvalidValue, std::string(what) + ": " + (msg)); } while (0)
@@ -999,4 +1063,28 @@ extern "C" int d8s_prep_resize(const D8sPrepArgs* in, void* stream) {
     k_prep_setup<<<dim3(sb, a.n), NT, 0, st>>>(a, 0);
     k_prep_resize<<<grid_of(a, 2), NT, 0, st>>>(a);
     return d8s_host_launched("d8s_prep_resize");
+}
+
+extern "C" int d8s_grid_sample(const D8sGridArgs* a, void* stream) {
+    const char* what = "d8s_grid_sample";
+    PREQ(a != nullptr, "null arguments");
+    PREQ(a->kind == 0 || a->kind == 1, "kind must be 0 (fp16 images) or 1 (uint8 volume gather)");
+    PREQ(a->src && a->out && (a->grid || a->kind == 1), "null pointer");
+    PREQ(a->H >= 1 && a->W >= 1 && (int64_t)a->H * a->W < (1ll << 31), "bad image size");
+    PREQ(a->grid % 4 == 0, "grid not 4-byte aligned");
+    if (a->kind == 1) {
+        PREQ(a->slice_idx && a->lut, "null slice_idx or lut");
+        PREQ(a->B >= 1 && a->M >= 1 && a->SK >= 1, "bad B, M or SK");
+        PREQ((int64_t)a->B * a->M == a->N, "N must be B * M");
+    }
+    PREQ(a->N >= 1 && a->N < 65536 * GIMG, "N must be 1 .. 524287");
+    const dim3 grid((unsigned)(((int64_t)a->H * a->W + NT - 1) / NT), (unsigned)((a->N + GIMG - 1) / GIMG));
+    hipStream_t st = (hipStream_t)stream;
+    if (a->kind == 1 && a->grid == 0)
+        k_grid_sample<2><<<grid, NT, 0, st>>>(*a);
+    else if (a->kind == 1)
+        k_grid_sample<1><<<grid, NT, 0, st>>>(*a);
+    else
+        k_grid_sample<0><<<grid, NT, 0, st>>>(*a);
+    return d8s_host_launched("d8s_grid_sample");
 }

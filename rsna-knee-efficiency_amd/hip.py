@@ -105,6 +105,13 @@ class PrepArgs(ctypes.Structure):
                 ("n_stacks", i32), ("pad_", i32), ("s", PrepStack * PREP_MAX_STACKS)]
 
 
+class GridArgs(ctypes.Structure):
+    """`D8sGridArgs`: bilinear grid sampling of fp16 images (the geometric TTA view)."""
+    _fields_ = [("src", u64), ("slice_idx", u64), ("lut", u64), ("grid", u64), ("out", u64),
+                ("kind", i32), ("N", i32), ("H", i32), ("W", i32), ("B", i32), ("SK", i32),
+                ("M", i32), ("pad_", i32)]
+
+
 IN_F16, IN_U8 = 0, 1
 
 # entry point -> argument types (all return int32 status)
@@ -120,6 +127,7 @@ SIGNATURES = {
     "d8s_prep_workspace": [i32, i32, ctypes.POINTER(ctypes.c_uint64)],
     "d8s_prep": [ctypes.POINTER(PrepArgs), vp],
     "d8s_prep_resize": [ctypes.POINTER(PrepArgs), vp],
+    "d8s_grid_sample": [ctypes.POINTER(GridArgs), vp],
     "d8s_micro_copy": [vp, vp, ctypes.c_size_t, vp],
     "d8s_micro_mfma": [i32, i32, vp, vp],
     "d8s_probe_mfma_i8": [vp, vp, vp, vp],

@@ -50,6 +50,8 @@ def test_struct_layouts_match_header(tmp_path):
         " offsetof(D8sPrepStack, r2), offsetof(D8sPrepStack, g1));\n"
         '  printf("%zu %zu %zu %zu\\n", sizeof(D8sPrepArgs), offsetof(D8sPrepArgs, kind),'
         " offsetof(D8sPrepArgs, s), sizeof(D8sPrepStat));\n"
+        '  printf("%zu %zu %zu\\n", sizeof(D8sGridArgs), offsetof(D8sGridArgs, kind),'
+        " offsetof(D8sGridArgs, M));\n"
         "  return 0; }\n")
     exe = tmp_path / "layout"
     subprocess.run(["gcc", f"-I{hip.HEADER.parent}", str(prog), "-o", str(exe)], check=True)
@@ -66,6 +68,8 @@ def test_struct_layouts_match_header(tmp_path):
     PS, PA = hip.PrepStack, hip.PrepArgs
     assert got[5] == [ctypes.sizeof(PS), PS.K.offset, PS.r2.offset, PS.g1.offset]
     assert got[6] == [ctypes.sizeof(PA), PA.kind.offset, PA.s.offset, ctypes.sizeof(hip.PrepStat)]
+    GA = hip.GridArgs
+    assert got[7] == [ctypes.sizeof(GA), GA.kind.offset, GA.M.offset]
 
 
 def _prep_args(kind=0, ws_bytes=None, box=(0, 64, 0, 64), r2=None, k=(0, 1), hr=64, out=256,
@@ -127,6 +131,13 @@ def test_prep_workspace_size():
     ("d8s_prep", lambda: (ctypes.byref(_prep_args(k=(1, 1))), None)),
     ("d8s_prep", lambda: (ctypes.byref(_prep_args(box=(0, 64 * 17, 0, 64), hr=64 * 17)), None)),
     ("d8s_prep_resize", lambda: (ctypes.byref(_prep_args(kind=1)), None)),
+    ("d8s_grid_sample", lambda: (None, None)),
+    ("d8s_grid_sample", lambda: (ctypes.byref(hip.GridArgs(src=8, grid=8, out=8, kind=2, N=1, H=4, W=4)),
+                                 None)),
+    ("d8s_grid_sample", lambda: (ctypes.byref(hip.GridArgs(src=8, grid=0, out=8, kind=0, N=1, H=4, W=4)),
+                                 None)),
+    ("d8s_grid_sample", lambda: (ctypes.byref(hip.GridArgs(src=8, slice_idx=8, lut=8, grid=8, out=8, kind=1,
+                                                           N=3, H=4, W=4, B=1, SK=2, M=2)), None)),
     ("d8s_prep_resize", lambda: (ctypes.byref(_prep_args(out=8)), None)),
     ("d8s_micro_copy", lambda: (1, 1, 17, None)),
 ])

@@ -1,0 +1,89 @@
+"""The geometric TTA view (`d8s_grid_sample`): bit for bit against the reference's own operations on
+the same GPU (`F.affine_grid` + `F.grid_sample` in fp16, src/knee/tta.py:131-148, and the uint8
+gather through the u / 255 table, src/knee/infer.py:986-1012), and within fp16 rounding of a float64
+bilinear restatement on the CPU."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from rsna_knee_efficiency_amd import tta
+
+pytestmark = pytest.mark.gpu
+
+VIEWS = [(1.10, 0.0, 0.0), (0.95, 0.0, 0.0), (1.05, 0.0, 0.0), (1.0, 0.03, 0.0), (1.0, 0.0, -0.03),
+         (1.10, 0.03, -0.03)]
+
+
+def _reference(w: torch.Tensor, scale: float, tx: float, ty: float) -> torch.Tensor:
+    """src/knee/tta.py:131-148 as torch operations."""
+    b, k, d, h, wd = w.shape
+    x = w.reshape(b * k, d, h, wd)
+    theta = torch.tensor([[1.0 / scale, 0.0, -2.0 * tx], [0.0, 1.0 / scale, -2.0 * ty]],
+                         device=x.device, dtype=x.dtype).unsqueeze(0)
+    grid = F.affine_grid(theta, (1, d, h, wd), align_corners=False).expand(b * k, h, wd, 2)
+    x = F.grid_sample(x, grid, mode="bilinear", padding_mode="zeros", align_corners=False)
+    return x.reshape(b, k, d, h, wd)
+
+
+def _bilinear_f64(img: np.ndarray, grid: np.ndarray) -> np.ndarray:
+    """Bilinear sampling with zero padding, align_corners=False, in float64 (grid given)."""
+    h, w = img.shape
+    ix = ((grid[..., 0].astype(np.float64) + 1) * w - 1) / 2
+    iy = ((grid[..., 1].astype(np.float64) + 1) * h - 1) / 2
+    x0, y0 = np.floor(ix).astype(int), np.floor(iy).astype(int)
+    out = np.zeros(ix.shape)
+    for dy in (0, 1):
+        for dx in (0, 1):
+            xx, yy = x0 + dx, y0 + dy
+            wgt = (1 - np.abs(ix - xx)) * (1 - np.abs(iy - yy))
+            ok = (xx >= 0) & (xx < w) & (yy >= 0) & (yy < h)
+            out += np.where(ok, img[np.clip(yy, 0, h - 1), np.clip(xx, 0, w - 1)], 0.0) * wgt
+    return out
+
+
+@pytest.mark.parametrize("view", VIEWS, ids=[f"s{v[0]}_tx{v[1]}_ty{v[2]}" for v in VIEWS])
+def test_affine_windows_is_the_reference_on_the_gpu(dev, view):
+    print(f"view {view}", flush=True)
+    g = torch.Generator().manual_seed(3)
+    w = torch.rand((2, 3, 3, 96, 80), generator=g).half().to(dev)
+    got = tta.affine_windows(w, *view)
+    ref = _reference(w, *view)
+    diff = int((got != ref).sum())
+    assert diff == 0, f"{diff} values differ, max {float((got.float() - ref.float()).abs().max())}"
+    # and within fp16 rounding of the float64 restatement on the same (fp16) grid
+    grid = tta.view_grid(96, 80, 3, *view, torch.float16, dev).float().cpu().numpy()
+    want = _bilinear_f64(w[1, 2, 1].float().cpu().numpy(), grid)
+    assert np.abs(got[1, 2, 1].float().cpu().numpy() - want).max() <= 2.0 ** -11 + 1e-6
+
+
+def test_affine_windows_identity_and_full_size(dev):
+    w = torch.rand((1, 11, 3, 512, 512), device=dev).half()
+    assert tta.affine_windows(w) is w
+    got = tta.affine_windows(w, 1.10)
+    assert torch.equal(got, _reference(w, 1.10, 0.0, 0.0))
+
+
+@pytest.mark.parametrize("view", [(1.0, 0.0, 0.0), (1.10, 0.0, 0.0)])
+def test_windows_u8_is_the_reference_chain(dev, view):
+    """gather_u8_f16 + affine_windows of the submission path (infer.py:986-1012) in one kernel."""
+    b, s, k, h, w = 2, 2, 7, 64, 48
+    g = torch.Generator().manual_seed(5)
+    v = torch.randint(0, 256, (b, s, k, h, w), generator=g, dtype=torch.uint8).to(dev)
+    idx = torch.tensor([0, 1, 2, 2, 3, 4, 8, 9, 13], dtype=torch.int64, device=dev)
+    depth = 3
+    out = torch.empty((b * idx.numel() // depth, depth, h, w), dtype=torch.float16, device=dev)
+    tta.windows_u8(v, idx, out, *view)
+    lut = torch.arange(256, dtype=torch.uint8, device=dev).half().mul_(1.0 / 255.0)
+    x = lut[v.view(b, s * k, h, w).index_select(1, idx).long()].view(b * idx.numel() // depth, depth, h, w)
+    if view != (1.0, 0.0, 0.0):
+        x = _reference(x.view(-1, 1, depth, h, w), *view).view(-1, depth, h, w)
+    assert torch.equal(out, x)
+
+
+def test_lut_is_u_over_255():
+    lut = tta.lut_u8_f16("cpu").float().numpy()
+    u = np.arange(256) / 255.0
+    assert np.abs(lut - u).max() <= 2.0 ** -12 and lut[0] == 0 and lut[255] == 1
