@@ -432,6 +432,67 @@ def committed_prep_traffic() -> int | None:
     return None
 
 
+FP32_PEAK_TFLOPS = 157.3     # MI355X fp32, published
+
+
+def head_flops(w: int, d: int = 1664, cd: int = 256, ff: int = 512, t: int = 12) -> float:
+    """Multiply-adds x 2 of the head for one study of w windows (ctx_in, in_proj, attention, out_proj,
+    feed-forward, ctx_out, the attention and classifier dots)."""
+    mac = w * d * cd + w * cd * 3 * cd + 2 * w * w * cd + w * cd * cd + 2 * w * cd * ff + w * cd * d \
+        + 2 * w * d * t
+    return 2.0 * mac
+
+
+def bench_head(dev: torch.device, b: int = 8, w: int = 88, reps: int = 50, with_cpu: bool = False) -> dict:
+    """The head after the encoder (`head.KneeHead`, d8s_head) on b studies of w windows, seeded weights
+    of the final model's shapes, features resident in HBM."""
+    from rsna_knee_efficiency_amd import head as hd
+    g = torch.Generator().manual_seed(0)
+    keys = hd.KEYS.values()
+    shapes = {"slot_emb": (8, 1664), "ctx_in.weight": (256, 1664), "ctx_in.bias": (256,), "ctx_pos": (11, 256),
+              "ctx.layers.0.self_attn.in_proj_weight": (768, 256), "ctx.layers.0.self_attn.in_proj_bias": (768,),
+              "ctx.layers.0.self_attn.out_proj.weight": (256, 256), "ctx.layers.0.self_attn.out_proj.bias": (256,),
+              "ctx.layers.0.norm1.weight": (256,), "ctx.layers.0.norm1.bias": (256,),
+              "ctx.layers.0.norm2.weight": (256,), "ctx.layers.0.norm2.bias": (256,),
+              "ctx.layers.0.linear1.weight": (512, 256), "ctx.layers.0.linear1.bias": (512,),
+              "ctx.layers.0.linear2.weight": (256, 512), "ctx.layers.0.linear2.bias": (256,),
+              "ctx_out.weight": (1664, 256), "ctx_out.bias": (1664,), "attn.weight": (12, 1664),
+              "attn.bias": (12,), "cls_w": (12, 1664), "cls_b": (12,)}
+    sd = {k: torch.randn(shapes[k], generator=g) * 0.02 for k in keys}
+    head = hd.KneeHead(sd, dev)
+    z = torch.randn((b, w, 1664), generator=g).to(dev)
+    slot_of = (torch.arange(w) // 11) % 8
+    mask = torch.ones((b, 8), dtype=torch.bool)
+    for _ in range(5):
+        head(z, slot_of, mask)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t = time.perf_counter()
+    e0.record()
+    for _ in range(reps):
+        head(z, slot_of, mask)
+    e1.record()
+    torch.cuda.synchronize()
+    dt = (time.perf_counter() - t) / reps
+    ms = e0.elapsed_time(e1) / reps
+    tflops = b * head_flops(w) / (ms * 1e-3) / 1e12
+    out = {"metric": "head logits (context layer + per-finding attention pooling) studies/s on 1 MI355X",
+           "value": round(b / dt, 1), "unit": "studies/s", "studies_per_call": b, "windows": w,
+           "gpu_ms_per_call": round(ms, 4), "dtype": "f32",
+           "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": FP32_PEAK_TFLOPS,
+                        "unit": "TFLOP/s", "frac": round(tflops / FP32_PEAK_TFLOPS, 4), "traffic": None,
+                        "flops_per_study": head_flops(w)}}
+    if with_cpu:
+        from oracle import head as oh
+        torch.set_num_threads(1)
+        t = time.perf_counter()
+        oh.head_forward(sd, z[:1].cpu(), slot_of, mask[:1])
+        c = time.perf_counter() - t
+        out["cpu_baseline"] = {"value": round(1.0 / c, 2), "unit": "studies/s", "cores": 1, "kind": "port",
+                               "sample": f"one study of {w} windows through oracle/head.py (torch fp32, 1 thread)"}
+    return out
+
+
 def bench_zoom(dev: torch.device, reps: int = 20) -> dict:
     """The submission's geometric view on one study: the windows of 8 slots x 11 triplets (stride 2,
     depth 3, 24 slices) gathered from the uint8 volume and zoomed 1.10 (`tta.windows_u8`), between HIP
@@ -517,8 +578,9 @@ def main() -> None:
     ap.add_argument("--pmc-passes", type=int, default=0, metavar="P",
                     help="only run P eager configuration-5 passes of one encoder (the launches of "
                          "a counter-collection run), print the per-family times and exit")
-    ap.add_argument("--path", choices=("encoder", "prep"), default="encoder",
-                    help="prep: the upstream preparation (raw crops -> uint8 volume) instead")
+    ap.add_argument("--path", choices=("encoder", "prep", "head"), default="encoder",
+                    help="prep: the upstream preparation (raw crops -> uint8 volume); head: the head "
+                         "after the encoder")
     ap.add_argument("--traffic-summary", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                     help="print the HBM traffic per launch from two --pmc-passes counter runs")
     args = ap.parse_args()
@@ -541,6 +603,9 @@ def main() -> None:
     torch.backends.cudnn.allow_tf32 = False
     torch.backends.cuda.matmul.allow_tf32 = False
     dev = torch.device("cuda:0")
+    if args.path == "head":
+        print(json.dumps(bench_head(dev, with_cpu=not args.no_cpu)), flush=True)
+        return
     if args.path == "prep":
         if args.pmc_passes:
             print(json.dumps(prep_pmc(dev, args.pmc_passes, args.copy_probe)), flush=True)
@@ -658,6 +723,8 @@ def main() -> None:
     out["prep"] = {k: pr[k] for k in ("metric", "value", "unit", "gpu_ms_per_study", "roofline", "config",
                                       "zoom_view")}
     log(f"prep: {pr['value']} studies/s, {pr['gpu_ms_per_study']} ms GPU per study")
+    out["head"] = bench_head(dev)
+    log(f"head: {out['head']['value']} studies/s")
     if args.copy_probe:
         out["copy_probe"] = copy_probe(dev)
         log(f"copy probe: {out['copy_probe']}")

@@ -291,6 +291,42 @@ typedef struct D8sGridArgs {
 
 int d8s_grid_sample(const D8sGridArgs* a, void* stream);
 
+/* ---- The head after the encoder --------------------------------------------------------------
+ *
+ * The final model's `KneeBaseline` head on the encoder's window features (src/knee/models/
+ * baseline.py: `_features_full` :870-932, `_context` :954-977, `forward` :1083-1170; configuration
+ * configs/exp/376-full-data-v9j-287-img512.yaml: one context layer of width 256, 4 heads, attention
+ * pooling), for B studies of W windows, in float32:
+ *   f   = z + slot_emb[slot_of[w]]                                   (B, W, D)
+ *   h   = ctx_in(f) + ctx_pos[w % PER]; one pre-norm transformer encoder layer on h (self-attention,
+ *         keys of absent slots masked, all keys when no slot is present; ReLU feed-forward of FF);
+ *   f2  = f + ctx_out(h)
+ *   a   = attn(f2) (B, W, T), -inf on absent slots (0 everywhere if none is present), softmax over W
+ *   logits[b][t] = sum_w a (f2 . cls_w[t]) + cls_b[t]                 (B, T)
+ * Weights in torch's Linear layout [out][in]; the transformer layer's are those of
+ * `nn.TransformerEncoderLayer` (self_attn.in_proj, self_attn.out_proj, linear1, linear2, norm1, norm2).
+ * W <= 128, CD = 64 x heads, T <= 16.  slot_mask [B][S] uint8; the reference's window_index is not
+ * used by this configuration (context_pos None: the position is w % PER). */
+typedef struct D8sHeadArgs {
+    const float* z;            /* [B][W][D] encoder features */
+    const int32_t* slot_of;    /* [W] */
+    const uint8_t* slot_mask;  /* [B][S] */
+    const float* slot_emb;     /* [S][D] */
+    const float *ctx_in_w, *ctx_in_b, *ctx_pos;            /* [CD][D], [CD], [PER][CD] */
+    const float *in_proj_w, *in_proj_b, *out_proj_w, *out_proj_b;  /* [3CD][CD], [3CD], [CD][CD], [CD] */
+    const float *ln1_w, *ln1_b, *ln2_w, *ln2_b;            /* [CD] */
+    const float *ff1_w, *ff1_b, *ff2_w, *ff2_b;            /* [FF][CD], [FF], [CD][FF], [CD] */
+    const float *ctx_out_w, *ctx_out_b;                    /* [D][CD], [D] */
+    const float *attn_w, *attn_b, *cls_w, *cls_b;          /* [T][D], [T], [T][D], [T] */
+    float* logits;             /* [B][T] */
+    void* workspace;           /* device memory of d8s_head_workspace bytes, 256-byte aligned */
+    uint64_t ws_bytes;
+    int32_t B, W, D, S, CD, heads, FF, PER, T, ctx_layers;   /* ctx_layers must be 1 */
+} D8sHeadArgs;
+
+int d8s_head_workspace(const D8sHeadArgs* a, uint64_t* bytes);
+int d8s_head(const D8sHeadArgs* a, void* stream);
+
 /* Library identification: "d8s-hip <abi> <source hash> gfx950". */
 const char* d8s_version(void);
 

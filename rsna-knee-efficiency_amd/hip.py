@@ -21,7 +21,7 @@ PKG = Path(__file__).resolve().parent
 CSRC = PKG / "csrc"
 SOURCE = CSRC / "d8s_kernels.hip"
 # every file compiled into the library (the first is SOURCE)
-SOURCES = (SOURCE, CSRC / "d8s_prep.hip", CSRC / "d8s_host.h")
+SOURCES = (SOURCE, CSRC / "d8s_prep.hip", CSRC / "d8s_head.hip", CSRC / "d8s_host.h")
 HEADER = PKG.parent / "include" / "d8s_hip.h"
 LIB_PATH = PKG / "libd8s_hip.so"
 ABI_VERSION = 1
@@ -112,6 +112,19 @@ class GridArgs(ctypes.Structure):
                 ("M", i32), ("pad_", i32)]
 
 
+HEAD_WEIGHTS = ("slot_emb", "ctx_in_w", "ctx_in_b", "ctx_pos", "in_proj_w", "in_proj_b", "out_proj_w",
+                "out_proj_b", "ln1_w", "ln1_b", "ln2_w", "ln2_b", "ff1_w", "ff1_b", "ff2_w", "ff2_b",
+                "ctx_out_w", "ctx_out_b", "attn_w", "attn_b", "cls_w", "cls_b")
+
+
+class HeadArgs(ctypes.Structure):
+    """`D8sHeadArgs`: the head after the encoder (context layer + per-finding attention pooling)."""
+    _fields_ = ([("z", u64), ("slot_of", u64), ("slot_mask", u64)]
+                + [(n, u64) for n in HEAD_WEIGHTS]
+                + [("logits", u64), ("workspace", u64), ("ws_bytes", u64)]
+                + [(n, i32) for n in ("B", "W", "D", "S", "CD", "heads", "FF", "PER", "T", "ctx_layers")])
+
+
 IN_F16, IN_U8 = 0, 1
 
 # entry point -> argument types (all return int32 status)
@@ -128,6 +141,8 @@ SIGNATURES = {
     "d8s_prep": [ctypes.POINTER(PrepArgs), vp],
     "d8s_prep_resize": [ctypes.POINTER(PrepArgs), vp],
     "d8s_grid_sample": [ctypes.POINTER(GridArgs), vp],
+    "d8s_head_workspace": [ctypes.POINTER(HeadArgs), ctypes.POINTER(ctypes.c_uint64)],
+    "d8s_head": [ctypes.POINTER(HeadArgs), vp],
     "d8s_micro_copy": [vp, vp, ctypes.c_size_t, vp],
     "d8s_micro_mfma": [i32, i32, vp, vp],
     "d8s_probe_mfma_i8": [vp, vp, vp, vp],

@@ -52,6 +52,8 @@ def test_struct_layouts_match_header(tmp_path):
         " offsetof(D8sPrepArgs, s), sizeof(D8sPrepStat));\n"
         '  printf("%zu %zu %zu\\n", sizeof(D8sGridArgs), offsetof(D8sGridArgs, kind),'
         " offsetof(D8sGridArgs, M));\n"
+        '  printf("%zu %zu %zu\\n", sizeof(D8sHeadArgs), offsetof(D8sHeadArgs, logits),'
+        " offsetof(D8sHeadArgs, ctx_layers));\n"
         "  return 0; }\n")
     exe = tmp_path / "layout"
     subprocess.run(["gcc", f"-I{hip.HEADER.parent}", str(prog), "-o", str(exe)], check=True)
@@ -70,6 +72,8 @@ def test_struct_layouts_match_header(tmp_path):
     assert got[6] == [ctypes.sizeof(PA), PA.kind.offset, PA.s.offset, ctypes.sizeof(hip.PrepStat)]
     GA = hip.GridArgs
     assert got[7] == [ctypes.sizeof(GA), GA.kind.offset, GA.M.offset]
+    HA = hip.HeadArgs
+    assert got[8] == [ctypes.sizeof(HA), HA.logits.offset, HA.ctx_layers.offset]
 
 
 def _prep_args(kind=0, ws_bytes=None, box=(0, 64, 0, 64), r2=None, k=(0, 1), hr=64, out=256,
@@ -88,6 +92,21 @@ def _prep_args(kind=0, ws_bytes=None, box=(0, 64, 0, 64), r2=None, k=(0, 1), hr=
     s.k0, s.k1 = k
     k1, k2, g1, g2 = (40, 4054, 0.95, 0.05)
     s.r1, s.r2, s.g1, s.g2 = k1, k2 if r2 is None else r2, g1, g2
+    return a
+
+
+def _head_args(**kw):
+    """d8s_head arguments valid except for the fields given (fake pointers: checked before any HIP
+    call)."""
+    a = hip.HeadArgs()
+    for n in ("z", "slot_of", "slot_mask", "logits", "workspace", *hip.HEAD_WEIGHTS):
+        setattr(a, n, 4096)
+    a.B, a.W, a.D, a.S, a.CD, a.heads, a.FF, a.PER, a.T, a.ctx_layers = 1, 88, 1664, 8, 256, 4, 512, 11, 12, 1
+    need = ctypes.c_uint64()
+    assert hip.library().d8s_head_workspace(ctypes.byref(a), ctypes.byref(need)) == 0
+    a.ws_bytes = need.value
+    for k, v in kw.items():
+        setattr(a, k, v)
     return a
 
 
@@ -132,6 +151,12 @@ def test_prep_workspace_size():
     ("d8s_prep", lambda: (ctypes.byref(_prep_args(box=(0, 64 * 17, 0, 64), hr=64 * 17)), None)),
     ("d8s_prep_resize", lambda: (ctypes.byref(_prep_args(kind=1)), None)),
     ("d8s_grid_sample", lambda: (None, None)),
+    ("d8s_head", lambda: (None, None)),
+    ("d8s_head", lambda: (ctypes.byref(_head_args(W=129)), None)),
+    ("d8s_head", lambda: (ctypes.byref(_head_args(ctx_layers=2)), None)),
+    ("d8s_head", lambda: (ctypes.byref(_head_args(CD=200)), None)),
+    ("d8s_head", lambda: (ctypes.byref(_head_args(ws_bytes=16)), None)),
+    ("d8s_head_workspace", lambda: (None, None)),
     ("d8s_grid_sample", lambda: (ctypes.byref(hip.GridArgs(src=8, grid=8, out=8, kind=2, N=1, H=4, W=4)),
                                  None)),
     ("d8s_grid_sample", lambda: (ctypes.byref(hip.GridArgs(src=8, grid=0, out=8, kind=0, N=1, H=4, W=4)),
