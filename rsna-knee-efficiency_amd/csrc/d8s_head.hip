@@ -7,7 +7,7 @@
 // kernels.  Here it is 8 launches for all studies of a call, float32 throughout:
 //   1. k_head_gemm<PRO_SLOT, EPI_BIAS_POS>: h = (z + slot_emb[slot]) ctx_in^T + b + ctx_pos[w % per]
 //   2. k_head_gemm<PRO_LN, EPI_BIAS>:       qkv = LN1(h) in_proj^T + b
-//   3. k_head_attn:                          per (study, head) softmax(q k^T / sqrt(dh), keys of
+//   3. k_head_attn:                          per (study, head, 16 queries) softmax(q k^T / sqrt(dh), keys of
 //                                            absent slots masked) v
 //   4. k_head_gemm<PRO_NONE, EPI_BIAS_RES>:  h1 = h + att out_proj^T + b
 //   5. k_head_gemm<PRO_LN, EPI_BIAS_RELU>:   u = relu(LN2(h1) ff1^T + b)
@@ -16,7 +16,9 @@
 //                                            block the partial dots of f2 with attn.weight and cls_w
 //   8. k_head_pool:                          per study: a = attn(f2) masked, softmax over windows,
 //                                            logits = sum_w a (f2 . cls_w) + cls_b
-// (one context layer: the final model's configuration.)  The pooled vector of the reference,
+// (one context layer: the final model's configuration.)  A product whose 32 x 64 tiles are too few
+// to fill the chip (the 1664-deep ctx_in above all) is split over K into workgroups that write raw
+// sums, added in split order with the epilogue by k_head_splitk.  The pooled vector of the reference,
 // sum_w a f2, is never formed: its dot with cls_w is sum_w a (f2 . cls_w), the same value up to the
 // order of the float32 sums.
 #include <hip/hip_runtime.h>
@@ -24,6 +26,7 @@
 #include <math.h>
 #include <stdint.h>
 
+#include <algorithm>
 #include <string>
 
 #include "d8s_hip.h"
@@ -34,7 +37,7 @@
 namespace {
 
 constexpr int NT = 256;
-constexpr int TM = 16, TN = 64, KC = 64;     // GEMM tile: 16 rows x 64 columns, K in chunks of 64
+constexpr int TM = 32, TN = 64, KC = 64;     // GEMM tile: 32 rows x 64 columns, K in chunks of 64
 constexpr int WMAX = 128;                    // windows per study
 constexpr int TMAX = 16;                     // findings
 
@@ -65,109 +68,186 @@ struct GemmP {
     const float* cw;
     float* part;
     int T;
+    // split K (gridDim.z > 1): kc_per chunks of KC per split, raw sums into Cs [gridDim.z][M][N]
+    int kc_per;
+    float* Cs;
 };
+
+// split-K epilogue: C[r][n] = sum over splits of Cs[s][r][n] + bias[n] (+ pos[(r % W) % per][n]) (+ R[r][n]),
+// the splits added in order
+template <int EPI>
+__global__ void __launch_bounds__(NT) k_head_splitk(GemmP p, int splits) {
+    const int64_t i = (int64_t)blockIdx.x * NT + threadIdx.x;
+    if (i >= (int64_t)p.M * p.N) return;
+    const int r = (int)(i / p.N), n = (int)(i % p.N);
+    float x = 0.0f;
+    for (int s = 0; s < splits; ++s) x += p.Cs[(int64_t)s * p.M * p.N + i];
+    x += p.bias[n];
+    if constexpr (EPI == EPI_BIAS_POS) x += p.pos[(int64_t)((r % p.W) % p.per) * p.N + n];
+    if constexpr (EPI == EPI_BIAS_RES) x += p.R[(int64_t)r * p.N + n];
+    if constexpr (EPI == EPI_BIAS_RELU) x = fmaxf(x, 0.0f);
+    p.C[(int64_t)r * p.ldc + n] = x;
+}
 
 template <int PRO, int EPI>
 __global__ void __launch_bounds__(NT) k_head_gemm(GemmP p) {
     __shared__ float sA[TM][KC + 1];
-    __shared__ float sB[KC][TN + 4];
+    __shared__ float4 sB[KC][TN / 4];
     __shared__ float sMean[TM], sRstd[TM];
     const int tid = threadIdx.x;
-    const int ty = tid >> 4, tx = tid & 15;           // row ty, columns 4 tx .. 4 tx + 3
+    const int ty = tid >> 4, tx = tid & 15;           // rows 2 ty, 2 ty + 1; columns 4 tx .. 4 tx + 3
     const int r0 = blockIdx.x * TM, n0 = blockIdx.y * TN;
     if constexpr (PRO == PRO_LN) {
         // mean and 1/std of the tile's rows (biased variance, as torch's layer_norm), in two passes
-        // over the row: the mean, then the mean square deviation
-        const int r = r0 + ty;
+        // over the row: the mean, then the mean square deviation; 8 lanes per row
+        const int rr = tid >> 3, l8 = tid & 7;
+        const int r = r0 + rr;
         float s = 0.0f;
         if (r < p.M)
-            for (int k = tx; k < p.K; k += 16) s += p.A[(int64_t)r * p.K + k];
+            for (int k = l8; k < p.K; k += 8) s += p.A[(int64_t)r * p.K + k];
 #pragma unroll
-        for (int d = 8; d >= 1; d >>= 1) s += __shfl_xor(s, d, 16);
+        for (int d = 4; d >= 1; d >>= 1) s += __shfl_xor(s, d, 8);
         const float mean = s / (float)p.K;
         float ss = 0.0f;
         if (r < p.M)
-            for (int k = tx; k < p.K; k += 16) {
+            for (int k = l8; k < p.K; k += 8) {
                 const float x = p.A[(int64_t)r * p.K + k] - mean;
                 ss = __builtin_fmaf(x, x, ss);
             }
 #pragma unroll
-        for (int d = 8; d >= 1; d >>= 1) ss += __shfl_xor(ss, d, 16);
-        if (tx == 0) {
-            sMean[ty] = mean;
-            sRstd[ty] = 1.0f / sqrtf(ss / (float)p.K + 1e-5f);
+        for (int d = 4; d >= 1; d >>= 1) ss += __shfl_xor(ss, d, 8);
+        if (l8 == 0) {
+            sMean[rr] = mean;
+            sRstd[rr] = 1.0f / sqrtf(ss / (float)p.K + 1e-5f);
         }
         __syncthreads();
     }
-    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    for (int k0 = 0; k0 < p.K; k0 += KC) {
-        // A tile [TM][KC]: 4 values per thread
-        for (int i = tid; i < TM * KC; i += NT) {
-            const int rr = i / KC, kk = i % KC;
-            const int r = r0 + rr, k = k0 + kk;
+    float acc[2][4] = {{0.0f, 0.0f, 0.0f, 0.0f}, {0.0f, 0.0f, 0.0f, 0.0f}};
+    // this thread stages A rows tid / KC + 4 j (j < 8) at column tid % KC of each chunk: the rows'
+    // addresses (and their slot embedding rows) are fixed for the whole K loop
+    constexpr int AR = TM * KC / NT;
+    static_assert(TM * KC % NT == 0 && NT % KC == 0, "A staging");
+    const int akk = tid % KC, ar0 = tid / KC;
+    const float* arow[AR];
+    const float* srow[AR];
+#pragma unroll
+    for (int j = 0; j < AR; ++j) {
+        const int r = r0 + ar0 + (NT / KC) * j;
+        arow[j] = r < p.M ? p.A + (int64_t)r * p.K : nullptr;
+        srow[j] = nullptr;
+        if constexpr (PRO == PRO_SLOT)
+            if (r < p.M) srow[j] = p.slot_emb + (int64_t)p.slot_of[r % p.W] * p.K;
+    }
+    // split K: block z of gridDim.z takes chunks [z kc_per, (z + 1) kc_per)
+    int kbeg = 0, kend = p.K;
+    if (gridDim.z > 1) {
+        kbeg = blockIdx.z * p.kc_per * KC;
+        kend = min(p.K, kbeg + p.kc_per * KC);
+    }
+    for (int k0 = kbeg; k0 < kend; k0 += KC) {
+        const int k = k0 + akk;
+#pragma unroll
+        for (int j = 0; j < AR; ++j) {
+            const int rr = ar0 + (NT / KC) * j;
             float v = 0.0f;
-            if (r < p.M && k < p.K) {
-                v = p.A[(int64_t)r * p.K + k];
-                if constexpr (PRO == PRO_SLOT) v += p.slot_emb[(int64_t)p.slot_of[r % p.W] * p.K + k];
+            if (arow[j] != nullptr && k < kend) {
+                v = arow[j][k];
+                if constexpr (PRO == PRO_SLOT) v += srow[j][k];
                 if constexpr (PRO == PRO_LN) v = (v - sMean[rr]) * sRstd[rr] * p.ln_w[k] + p.ln_b[k];
             }
-            sA[rr][kk] = v;
+            sA[rr][akk] = v;
         }
-        // B tile: weights [n0 .. n0 + TN)[k0 .. k0 + KC) transposed into sB[k][n]
-        for (int i = tid; i < TN * KC; i += NT) {
-            const int nn = i / KC, kk = i % KC;
-            const int n = n0 + nn, k = k0 + kk;
-            sB[kk][nn] = (n < p.N && k < p.K) ? p.Bw[(int64_t)n * p.K + k] : 0.0f;
+        // weights [n0 .. n0 + TN)[k0 .. k0 + KC) transposed into sB[k][n] (4 columns per float4): lane
+        // = column, so the LDS stores of a wave fall in 64 different banks
+        float* sBf = (float*)sB;
+        const int bn = tid % TN, n = n0 + bn;
+        if ((p.K & 3) == 0 && ((uintptr_t)p.Bw & 15) == 0) {
+#pragma unroll
+            for (int q = tid / TN; q < KC / 4; q += NT / TN) {
+                const int kq = k0 + 4 * q;
+                float4 b = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                if (n < p.N && kq < kend) b = *(const float4*)(p.Bw + (int64_t)n * p.K + kq);
+                sBf[(4 * q + 0) * TN + bn] = b.x;
+                sBf[(4 * q + 1) * TN + bn] = b.y;
+                sBf[(4 * q + 2) * TN + bn] = b.z;
+                sBf[(4 * q + 3) * TN + bn] = b.w;
+            }
+        } else {
+            for (int kk = tid / TN; kk < KC; kk += NT / TN) {
+                const int kx = k0 + kk;
+                sBf[kk * TN + bn] = (n < p.N && kx < kend) ? p.Bw[(int64_t)n * p.K + kx] : 0.0f;
+            }
         }
         __syncthreads();
 #pragma unroll 8
         for (int kk = 0; kk < KC; ++kk) {
-            const float a = sA[ty][kk];
+            const float a0 = sA[2 * ty][kk], a1 = sA[2 * ty + 1][kk];
+            const float4 bv = sB[kk][tx];
+            const float bb[4] = {bv.x, bv.y, bv.z, bv.w};
 #pragma unroll
-            for (int j = 0; j < 4; ++j) acc[j] = __builtin_fmaf(a, sB[kk][4 * tx + j], acc[j]);
+            for (int j = 0; j < 4; ++j) {
+                acc[0][j] = __builtin_fmaf(a0, bb[j], acc[0][j]);
+                acc[1][j] = __builtin_fmaf(a1, bb[j], acc[1][j]);
+            }
         }
         __syncthreads();
     }
-    const int r = r0 + ty;
-    float v[4];
+    if (gridDim.z > 1) {
+        // split K: raw sums into the split's slice of Cs; k_head_splitk adds them and applies the epilogue
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const int n = n0 + 4 * tx + j;
-        v[j] = 0.0f;
-        if (r >= p.M || n >= p.N) continue;
-        float x = acc[j] + p.bias[n];
-        if constexpr (EPI == EPI_BIAS_POS) x += p.pos[(int64_t)((r % p.W) % p.per) * p.N + n];
-        if constexpr (EPI == EPI_BIAS_RES) x += p.R[(int64_t)r * p.N + n];
-        if constexpr (EPI == EPI_BIAS_RELU) x = fmaxf(x, 0.0f);
-        if constexpr (EPI == EPI_DOTS)
-            x += p.z[(int64_t)r * p.N + n] + p.slot_emb[(int64_t)p.slot_of[r % p.W] * p.N + n];
-        v[j] = x;
-        if constexpr (EPI != EPI_DOTS) p.C[(int64_t)r * p.ldc + n] = x;
-    }
-    if constexpr (EPI == EPI_DOTS) {
-        // partial dots of the row's 64 columns with the attention and classifier weights
-        __shared__ float sDot[TM][16][2 * TMAX];
-        for (int t = 0; t < p.T; ++t) {
-            float da = 0.0f, dc = 0.0f;
+        for (int i = 0; i < 2; ++i) {
+            const int r = r0 + 2 * ty + i;
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 const int n = n0 + 4 * tx + j;
-                if (n < p.N) {
-                    da = __builtin_fmaf(v[j], p.tw[(int64_t)t * p.N + n], da);
-                    dc = __builtin_fmaf(v[j], p.cw[(int64_t)t * p.N + n], dc);
+                if (r < p.M && n < p.N) p.Cs[((int64_t)blockIdx.z * p.M + r) * p.N + n] = acc[i][j];
+            }
+        }
+        return;
+    }
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int r = r0 + 2 * ty + i;
+        float v[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int n = n0 + 4 * tx + j;
+            v[j] = 0.0f;
+            if (r >= p.M || n >= p.N) continue;
+            float x = acc[i][j] + p.bias[n];
+            if constexpr (EPI == EPI_BIAS_POS) x += p.pos[(int64_t)((r % p.W) % p.per) * p.N + n];
+            if constexpr (EPI == EPI_BIAS_RES) x += p.R[(int64_t)r * p.N + n];
+            if constexpr (EPI == EPI_BIAS_RELU) x = fmaxf(x, 0.0f);
+            if constexpr (EPI == EPI_DOTS)
+                x += p.z[(int64_t)r * p.N + n] + p.slot_emb[(int64_t)p.slot_of[r % p.W] * p.N + n];
+            v[j] = x;
+            if constexpr (EPI != EPI_DOTS) p.C[(int64_t)r * p.ldc + n] = x;
+        }
+        if constexpr (EPI == EPI_DOTS) {
+            // the row's dots over these 64 columns with the attention and classifier weights: partial
+            // sums of the 16 lanes of the row combined by shuffles
+            for (int t = 0; t < p.T; ++t) {
+                float da = 0.0f, dc = 0.0f;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const int n = n0 + 4 * tx + j;
+                    if (n < p.N) {
+                        da = __builtin_fmaf(v[j], p.tw[(int64_t)t * p.N + n], da);
+                        dc = __builtin_fmaf(v[j], p.cw[(int64_t)t * p.N + n], dc);
+                    }
+                }
+#pragma unroll
+                for (int d = 8; d >= 1; d >>= 1) {
+                    da += __shfl_xor(da, d, 16);
+                    dc += __shfl_xor(dc, d, 16);
+                }
+                if (tx == 0 && r < p.M) {
+                    float* dst = p.part + ((int64_t)r * gridDim.y + blockIdx.y) * 2 * p.T;
+                    dst[t] = da;
+                    dst[p.T + t] = dc;
                 }
             }
-            sDot[ty][tx][t] = da;
-            sDot[ty][tx][TMAX + t] = dc;
         }
-        __syncthreads();
-        if (r < p.M)
-            for (int q = tx; q < 2 * p.T; q += 16) {
-                const int t = q < p.T ? q : TMAX + q - p.T;
-                float s = 0.0f;
-                for (int i = 0; i < 16; ++i) s += sDot[ty][i][t];
-                p.part[((int64_t)r * gridDim.y + blockIdx.y) * 2 * p.T + q] = s;
-            }
     }
 }
 
@@ -178,55 +258,93 @@ struct AttnP {
     int W, CD, heads;
 };
 
-// One workgroup per (study, head): every thread owns query rows; softmax(q k^T / sqrt(dh)) v over the
-// keys of present slots (all keys when no slot of the study is present).
+// One workgroup per (study, head, 16 queries), 16 lanes per query: softmax(q k^T / sqrt(dh)) v over
+// the keys of present slots (all keys when no slot of the study is present).  Lane l of a query scores
+// keys l, l + 16, ... with full 64-dim dots (q in registers), the maximum and the sum are reduced over
+// the 16 lanes, the unnormalised weights go to LDS, and lane l then accumulates output dims 4l .. 4l + 3
+// over all keys.
+constexpr int AQ = 16;   // queries per workgroup
 __global__ void __launch_bounds__(NT) k_head_attn(AttnP p) {
-    constexpr int DH = 64;
-    __shared__ float sK[WMAX][DH + 1];
-    __shared__ float sV[WMAX][DH + 1];
+    constexpr int DH = 64, LQ = NT / AQ, KPL = WMAX / LQ;
+    static_assert(LQ == 16 && DH == 4 * LQ, "attention lanes");
+    __shared__ float4 sK[WMAX][DH / 4 + 1];
+    __shared__ float4 sV[WMAX][DH / 4];
+    __shared__ float sP[AQ][WMAX];
     __shared__ uint8_t sKey[WMAX];
-    const int b = blockIdx.x, h = blockIdx.y;
+    __shared__ int sAny;
+    const int b = blockIdx.x, h = blockIdx.y, q0 = blockIdx.z * AQ;
     const int ld = 3 * p.CD;
     const float* base = p.qkv + (int64_t)b * p.W * ld;
-    for (int i = threadIdx.x; i < p.W * DH; i += NT) {
-        const int w = i / DH, d = i % DH;
-        sK[w][d] = base[(int64_t)w * ld + p.CD + h * DH + d];
-        sV[w][d] = base[(int64_t)w * ld + 2 * p.CD + h * DH + d];
+    for (int i = threadIdx.x; i < p.W * (DH / 4); i += NT) {
+        const int w = i / (DH / 4), d4 = i % (DH / 4);
+        sK[w][d4] = *(const float4*)(base + (int64_t)w * ld + p.CD + h * DH + 4 * d4);
+        sV[w][d4] = *(const float4*)(base + (int64_t)w * ld + 2 * p.CD + h * DH + 4 * d4);
     }
-    int any = 0;
-    for (int w = 0; w < p.W; ++w) any |= p.valid[(int64_t)b * p.W + w];
-    for (int w = threadIdx.x; w < p.W; w += NT) sKey[w] = any ? p.valid[(int64_t)b * p.W + w] : 1;
+    if (threadIdx.x == 0) sAny = 0;
+    __syncthreads();
+    for (int w = threadIdx.x; w < p.W; w += NT)
+        if (p.valid[(int64_t)b * p.W + w]) atomicOr(&sAny, 1);
+    __syncthreads();
+    for (int w = threadIdx.x; w < p.W; w += NT) sKey[w] = sAny ? p.valid[(int64_t)b * p.W + w] : 1;
     __syncthreads();
     const float scale = 1.0f / sqrtf((float)DH);
-    for (int qi = threadIdx.x; qi < p.W; qi += NT) {
-        float q[DH];
+    const int ql = threadIdx.x / LQ, l = threadIdx.x % LQ, qi = q0 + ql;
+    const bool act = qi < p.W;
+    float4 q[DH / 4];
 #pragma unroll
-        for (int d = 0; d < DH; ++d) q[d] = base[(int64_t)qi * ld + h * DH + d] * scale;
-        float mx = -INFINITY;
-        for (int j = 0; j < p.W; ++j) {
-            if (!sKey[j]) continue;
+    for (int d4 = 0; d4 < DH / 4; ++d4) {
+        float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        if (act) v = *(const float4*)(base + (int64_t)qi * ld + h * DH + 4 * d4);
+        q[d4] = make_float4(v.x * scale, v.y * scale, v.z * scale, v.w * scale);
+    }
+    float sc[KPL];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int m = 0; m < KPL; ++m) {
+        const int j = l + LQ * m;
+        sc[m] = -INFINITY;
+        if (j < p.W && sKey[j]) {
             float s = 0.0f;
 #pragma unroll
-            for (int d = 0; d < DH; ++d) s = __builtin_fmaf(q[d], sK[j][d], s);
+            for (int d4 = 0; d4 < DH / 4; ++d4) {
+                const float4 k = sK[j][d4];
+                s = __builtin_fmaf(q[d4].x, k.x, s);
+                s = __builtin_fmaf(q[d4].y, k.y, s);
+                s = __builtin_fmaf(q[d4].z, k.z, s);
+                s = __builtin_fmaf(q[d4].w, k.w, s);
+            }
+            sc[m] = s;
             mx = fmaxf(mx, s);
         }
-        float sum = 0.0f, o[DH];
+    }
 #pragma unroll
-        for (int d = 0; d < DH; ++d) o[d] = 0.0f;
-        for (int j = 0; j < p.W; ++j) {
-            if (!sKey[j]) continue;
-            float s = 0.0f;
+    for (int d = LQ / 2; d >= 1; d >>= 1) mx = fmaxf(mx, __shfl_xor(mx, d, LQ));
+    float sum = 0.0f;
 #pragma unroll
-            for (int d = 0; d < DH; ++d) s = __builtin_fmaf(q[d], sK[j][d], s);
-            const float e = expf(s - mx);
+    for (int m = 0; m < KPL; ++m) {
+        const int j = l + LQ * m;
+        if (j < p.W) {
+            const float e = sc[m] == -INFINITY ? 0.0f : expf(sc[m] - mx);
             sum += e;
-#pragma unroll
-            for (int d = 0; d < DH; ++d) o[d] = __builtin_fmaf(e, sV[j][d], o[d]);
+            sP[ql][j] = e;
         }
-        const float inv = 1.0f / sum;
-        float* dst = p.out + ((int64_t)b * p.W + qi) * p.CD + h * DH;
+    }
 #pragma unroll
-        for (int d = 0; d < DH; ++d) dst[d] = o[d] * inv;
+    for (int d = LQ / 2; d >= 1; d >>= 1) sum += __shfl_xor(sum, d, LQ);
+    __syncthreads();
+    float4 o = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    for (int j = 0; j < p.W; ++j) {
+        const float e = sP[ql][j];
+        const float4 v = sV[j][l];
+        o.x = __builtin_fmaf(e, v.x, o.x);
+        o.y = __builtin_fmaf(e, v.y, o.y);
+        o.z = __builtin_fmaf(e, v.z, o.z);
+        o.w = __builtin_fmaf(e, v.w, o.w);
+    }
+    if (act) {
+        const float inv = 1.0f / sum;
+        *(float4*)(p.out + ((int64_t)b * p.W + qi) * p.CD + h * DH + 4 * l) =
+            make_float4(o.x * inv, o.y * inv, o.z * inv, o.w * inv);
     }
 }
 
@@ -244,16 +362,22 @@ struct PoolP {
 __global__ void __launch_bounds__(NT) k_head_pool(PoolP p) {
     __shared__ float sA[WMAX][TMAX], sS[WMAX][TMAX];
     const int b = blockIdx.x;
-    for (int i = threadIdx.x; i < p.W * p.T; i += NT) {
-        const int w = i / p.T, t = i % p.T;
-        const float* pr = p.part + (int64_t)(b * p.W + w) * p.nblk * 2 * p.T;
-        float sa = 0.0f, sc = 0.0f;
-        for (int k = 0; k < p.nblk; ++k) {
-            sa += pr[k * 2 * p.T + t];
-            sc += pr[k * 2 * p.T + p.T + t];
+    // the partial dots of every (window, value) summed over the column blocks, 8 loads in flight
+    for (int i = threadIdx.x; i < p.W * 2 * p.T; i += NT) {
+        const int w = i / (2 * p.T), q = i % (2 * p.T);
+        const float* pr = p.part + (int64_t)(b * p.W + w) * p.nblk * 2 * p.T + q;
+        float acc[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+        int k = 0;
+        for (; k + 8 <= p.nblk; k += 8) {
+#pragma unroll
+            for (int u = 0; u < 8; ++u) acc[u] += pr[(k + u) * 2 * p.T];
         }
-        sA[w][t] = sa + p.attn_b[t];
-        sS[w][t] = sc;
+        for (; k < p.nblk; ++k) acc[0] += pr[k * 2 * p.T];
+        const float sum = ((acc[0] + acc[1]) + (acc[2] + acc[3])) + ((acc[4] + acc[5]) + (acc[6] + acc[7]));
+        if (q < p.T)
+            sA[w][q] = sum + p.attn_b[q];
+        else
+            sS[w][q - p.T] = sum;
     }
     __syncthreads();
     if (threadIdx.x < p.T) {
@@ -286,8 +410,23 @@ __global__ void __launch_bounds__(NT) k_head_valid(const uint8_t* slot_mask, con
 #define HREQ(cond, msg) \
     do { if (!(cond)) return d8s_host_fail((int)hipErrorInvalidValue, std::string(what) + ": " + (msg)); } while (0)
 
+// K split of a product of M rows, N columns and depth K: enough workgroups for the chip (about 512)
+// when the M x N tiles alone are few
+struct Split {
+    int splits, kc_per;
+};
+
+Split split_plan(int64_t M, int N, int K) {
+    const int chunks = (K + KC - 1) / KC;
+    const int64_t base = (M + TM - 1) / TM * ((N + TN - 1) / TN);
+    if (base >= 256 || chunks < 2) return {1, chunks};
+    const int want = (int)std::min<int64_t>(chunks, (512 + base - 1) / base);
+    const int kc = (chunks + want - 1) / want;
+    return {(chunks + kc - 1) / kc, kc};
+}
+
 struct Ws {
-    float *h, *qkv, *att, *h1, *u, *h2, *part;
+    float *h, *qkv, *att, *h1, *u, *h2, *part, *cs;
     uint8_t* valid;
     uint64_t bytes;
 };
@@ -310,9 +449,31 @@ Ws carve(const D8sHeadArgs* a, char* base) {
     w.u = (float*)take(ctx ? 4ull * M * a->FF : 0);
     w.h2 = (float*)take(ctx ? 4ull * M * a->CD : 0);
     w.part = (float*)take(4ull * M * nblk * 2 * a->T);
+    uint64_t cs = 0;
+    const int dims[5][2] = {{a->CD, a->D}, {3 * a->CD, a->CD}, {a->CD, a->CD}, {a->FF, a->CD}, {a->CD, a->FF}};
+    for (const auto& d : dims) {
+        const Split sp = split_plan(M, d[0], d[1]);
+        if (sp.splits > 1) cs = std::max<uint64_t>(cs, 4ull * sp.splits * M * d[0]);
+    }
+    w.cs = (float*)take(cs);
     w.valid = (uint8_t*)take((uint64_t)M);
     w.bytes = off;
     return w;
+}
+
+// one context-layer product, split over K when its tiles alone are too few for the chip
+template <int PRO, int EPI>
+void launch_gemm(GemmP g, float* cs, hipStream_t st) {
+    static_assert(EPI != EPI_DOTS, "the dots epilogue is not split");
+    const Split sp = split_plan(g.M, g.N, g.K);
+    const dim3 grid((g.M + TM - 1) / TM, (g.N + TN - 1) / TN, sp.splits);
+    g.kc_per = sp.kc_per;
+    g.Cs = cs;
+    k_head_gemm<PRO, EPI><<<grid, NT, 0, st>>>(g);
+    if (sp.splits > 1) {
+        const int64_t n = (int64_t)g.M * g.N;
+        k_head_splitk<EPI><<<(unsigned)((n + NT - 1) / NT), NT, 0, st>>>(g, sp.splits);
+    }
 }
 
 }  // namespace
@@ -348,7 +509,6 @@ extern "C" int d8s_head(const D8sHeadArgs* a, void* stream) {
     const int M = a->B * a->W;
     const int nblk = (a->D + TN - 1) / TN;
     k_head_valid<<<(M + NT - 1) / NT, NT, 0, st>>>(a->slot_mask, a->slot_of, w.valid, a->B, a->W, a->S);
-    const dim3 gcd((M + TM - 1) / TM, (a->CD + TN - 1) / TN);
     {
         GemmP g{};
         g.M = M;
@@ -358,30 +518,30 @@ extern "C" int d8s_head(const D8sHeadArgs* a, void* stream) {
         // 1. h = (z + slot_emb) ctx_in^T + b + ctx_pos[w % per]
         g.A = a->z; g.Bw = a->ctx_in_w; g.bias = a->ctx_in_b; g.C = w.h;
         g.N = a->CD; g.K = a->D; g.ldc = a->CD; g.pos = a->ctx_pos; g.per = a->PER;
-        k_head_gemm<PRO_SLOT, EPI_BIAS_POS><<<gcd, NT, 0, st>>>(g);
+        launch_gemm<PRO_SLOT, EPI_BIAS_POS>(g, w.cs, st);
         // 2. qkv = LN1(h) in_proj^T + b
         g = GemmP{}; g.M = M; g.W = a->W;
         g.A = w.h; g.Bw = a->in_proj_w; g.bias = a->in_proj_b; g.C = w.qkv;
         g.N = 3 * a->CD; g.K = a->CD; g.ldc = 3 * a->CD; g.ln_w = a->ln1_w; g.ln_b = a->ln1_b;
-        k_head_gemm<PRO_LN, EPI_BIAS><<<dim3((M + TM - 1) / TM, (3 * a->CD + TN - 1) / TN), NT, 0, st>>>(g);
+        launch_gemm<PRO_LN, EPI_BIAS>(g, w.cs, st);
         // 3. attention per (study, head)
         AttnP at{w.qkv, w.valid, w.att, a->W, a->CD, a->heads};
-        k_head_attn<<<dim3(a->B, a->heads), NT, 0, st>>>(at);
+        k_head_attn<<<dim3(a->B, a->heads, (a->W + AQ - 1) / AQ), NT, 0, st>>>(at);
         // 4. h1 = h + att out_proj^T + b
         g = GemmP{}; g.M = M; g.W = a->W;
         g.A = w.att; g.Bw = a->out_proj_w; g.bias = a->out_proj_b; g.C = w.h1;
         g.N = a->CD; g.K = a->CD; g.ldc = a->CD; g.R = w.h;
-        k_head_gemm<PRO_NONE, EPI_BIAS_RES><<<gcd, NT, 0, st>>>(g);
+        launch_gemm<PRO_NONE, EPI_BIAS_RES>(g, w.cs, st);
         // 5. u = relu(LN2(h1) ff1^T + b)
         g = GemmP{}; g.M = M; g.W = a->W;
         g.A = w.h1; g.Bw = a->ff1_w; g.bias = a->ff1_b; g.C = w.u;
         g.N = a->FF; g.K = a->CD; g.ldc = a->FF; g.ln_w = a->ln2_w; g.ln_b = a->ln2_b;
-        k_head_gemm<PRO_LN, EPI_BIAS_RELU><<<dim3((M + TM - 1) / TM, (a->FF + TN - 1) / TN), NT, 0, st>>>(g);
+        launch_gemm<PRO_LN, EPI_BIAS_RELU>(g, w.cs, st);
         // 6. h2 = h1 + u ff2^T + b
         g = GemmP{}; g.M = M; g.W = a->W;
         g.A = w.u; g.Bw = a->ff2_w; g.bias = a->ff2_b; g.C = w.h2;
         g.N = a->CD; g.K = a->FF; g.ldc = a->CD; g.R = w.h1;
-        k_head_gemm<PRO_NONE, EPI_BIAS_RES><<<gcd, NT, 0, st>>>(g);
+        launch_gemm<PRO_NONE, EPI_BIAS_RES>(g, w.cs, st);
     }
     // 7. f2 = z + slot_emb + h2 ctx_out^T + b, partial dots with attn.weight and cls_w
     GemmP g{};
