@@ -4,7 +4,7 @@
 //
 // Per study (W windows of D-dim encoder features, a few hundred KB) the head is a few small matrix
 // products with row-wise normalisations around them; the PyTorch head is ~30 launches of tiny
-// kernels.  Here it is 8 launches for all studies of a call, float32 throughout:
+// kernels.  Here it is 10 to 15 launches (with the split-K sums) for all studies of a call, float32 throughout:
 //   1. k_head_gemm<PRO_SLOT, EPI_BIAS_POS>: h = (z + slot_emb[slot]) ctx_in^T + b + ctx_pos[w % per]
 //   2. k_head_gemm<PRO_LN, EPI_BIAS>:       qkv = LN1(h) in_proj^T + b
 //   3. k_head_attn:                          per (study, head, 16 queries) softmax(q k^T / sqrt(dh), keys of
@@ -14,7 +14,8 @@
 //   6. k_head_gemm<PRO_NONE, EPI_BIAS_RES>:  h2 = h1 + u ff2^T + b
 //   7. k_head_gemm<PRO_NONE, EPI_DOTS>:      f2 = z + slot_emb + h2 ctx_out^T + b, and per 64-column
 //                                            block the partial dots of f2 with attn.weight and cls_w
-//   8. k_head_pool:                          per study: a = attn(f2) masked, softmax over windows,
+//   8. k_head_dotsum:                        the partial dots summed over the column blocks
+//   9. k_head_pool:                          per study: a = attn(f2) masked, softmax over windows,
 //                                            logits = sum_w a (f2 . cls_w) + cls_b
 // (one context layer: the final model's configuration.)  A product whose 32 x 64 tiles are too few
 // to fill the chip (the 1664-deep ctx_in above all) is split over K into workgroups that write raw
@@ -348,13 +349,32 @@ __global__ void __launch_bounds__(NT) k_head_attn(AttnP p) {
     }
 }
 
+// The partial dots of every (window row, value) summed over the column blocks of the dots product,
+// 8 loads in flight: sums[r][q] (q < T: attention logit, + attn_b; else the classifier dot)
+__global__ void __launch_bounds__(NT) k_head_dotsum(const float* part, const float* attn_b, float* sums,
+                                                    int M, int T, int nblk) {
+    const int64_t i = (int64_t)blockIdx.x * NT + threadIdx.x;
+    if (i >= (int64_t)M * 2 * T) return;
+    const int64_t r = i / (2 * T);
+    const int q = (int)(i % (2 * T));
+    const float* pr = part + r * nblk * 2 * T + q;
+    float acc[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+    int k = 0;
+    for (; k + 8 <= nblk; k += 8) {
+#pragma unroll
+        for (int u = 0; u < 8; ++u) acc[u] += pr[(k + u) * 2 * T];
+    }
+    for (; k < nblk; ++k) acc[0] += pr[k * 2 * T];
+    const float sum = ((acc[0] + acc[1]) + (acc[2] + acc[3])) + ((acc[4] + acc[5]) + (acc[6] + acc[7]));
+    sums[i] = q < T ? sum + attn_b[q] : sum;
+}
+
 struct PoolP {
-    const float* part;     // [B*W][nblk][2T]
+    const float* sums;     // [B*W][2T]
     const uint8_t* valid;  // [B][W]
-    const float* attn_b;   // [T]
     const float* cls_b;    // [T]
     float* logits;         // [B][T]
-    int W, T, nblk;
+    int W, T;
 };
 
 // One workgroup per study: a[w][t] = attn(f2[w]) + b (masked to -inf for absent slots; all zeros
@@ -362,42 +382,46 @@ struct PoolP {
 __global__ void __launch_bounds__(NT) k_head_pool(PoolP p) {
     __shared__ float sA[WMAX][TMAX], sS[WMAX][TMAX];
     const int b = blockIdx.x;
-    // the partial dots of every (window, value) summed over the column blocks, 8 loads in flight
     for (int i = threadIdx.x; i < p.W * 2 * p.T; i += NT) {
         const int w = i / (2 * p.T), q = i % (2 * p.T);
-        const float* pr = p.part + (int64_t)(b * p.W + w) * p.nblk * 2 * p.T + q;
-        float acc[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
-        int k = 0;
-        for (; k + 8 <= p.nblk; k += 8) {
-#pragma unroll
-            for (int u = 0; u < 8; ++u) acc[u] += pr[(k + u) * 2 * p.T];
-        }
-        for (; k < p.nblk; ++k) acc[0] += pr[k * 2 * p.T];
-        const float sum = ((acc[0] + acc[1]) + (acc[2] + acc[3])) + ((acc[4] + acc[5]) + (acc[6] + acc[7]));
+        const float v = p.sums[(int64_t)b * p.W * 2 * p.T + i];
         if (q < p.T)
-            sA[w][q] = sum + p.attn_b[q];
+            sA[w][q] = v;
         else
-            sS[w][q - p.T] = sum;
+            sS[w][q - p.T] = v;
+    }
+    __shared__ uint8_t sV[WMAX];
+    __shared__ int sAny;
+    if (threadIdx.x == 0) sAny = 0;
+    __syncthreads();
+    for (int w = threadIdx.x; w < p.W; w += NT) {
+        sV[w] = p.valid[(int64_t)b * p.W + w];
+        if (sV[w]) atomicOr(&sAny, 1);
     }
     __syncthreads();
-    if (threadIdx.x < p.T) {
-        const int t = threadIdx.x;
-        int any = 0;
-        for (int w = 0; w < p.W; ++w) any |= p.valid[(int64_t)b * p.W + w];
-        float mx = -INFINITY;
-        for (int w = 0; w < p.W; ++w) {
-            const float a = any ? (p.valid[(int64_t)b * p.W + w] ? sA[w][t] : -INFINITY) : 0.0f;
-            mx = fmaxf(mx, a);
-        }
-        float sum = 0.0f, acc = 0.0f;
-        for (int w = 0; w < p.W; ++w) {
-            const float a = any ? (p.valid[(int64_t)b * p.W + w] ? sA[w][t] : -INFINITY) : 0.0f;
+    // 16 lanes per finding t, lane l taking windows l, l + 16, ...: maximum, then the sums, reduced
+    // over the 16 lanes
+    const int t = threadIdx.x / 16, l = threadIdx.x % 16;
+    const bool any = sAny != 0;
+    float mx = -INFINITY;
+    if (t < p.T)
+        for (int w = l; w < p.W; w += 16) mx = fmaxf(mx, any ? (sV[w] ? sA[w][t] : -INFINITY) : 0.0f);
+#pragma unroll
+    for (int d = 8; d >= 1; d >>= 1) mx = fmaxf(mx, __shfl_xor(mx, d, 16));
+    float sum = 0.0f, acc = 0.0f;
+    if (t < p.T)
+        for (int w = l; w < p.W; w += 16) {
+            const float a = any ? (sV[w] ? sA[w][t] : -INFINITY) : 0.0f;
             const float e = expf(a - mx);
             sum += e;
             acc = __builtin_fmaf(e, sS[w][t], acc);
         }
-        p.logits[(int64_t)b * p.T + t] = acc / sum + p.cls_b[t];
+#pragma unroll
+    for (int d = 8; d >= 1; d >>= 1) {
+        sum += __shfl_xor(sum, d, 16);
+        acc += __shfl_xor(acc, d, 16);
     }
+    if (t < p.T && l == 0) p.logits[(int64_t)b * p.T + t] = acc / sum + p.cls_b[t];
 }
 
 // valid[b][w] = slot_mask[b][slot_of[w]]
@@ -426,7 +450,7 @@ Split split_plan(int64_t M, int N, int K) {
 }
 
 struct Ws {
-    float *h, *qkv, *att, *h1, *u, *h2, *part, *cs;
+    float *h, *qkv, *att, *h1, *u, *h2, *part, *sums, *cs;
     uint8_t* valid;
     uint64_t bytes;
 };
@@ -449,6 +473,7 @@ Ws carve(const D8sHeadArgs* a, char* base) {
     w.u = (float*)take(ctx ? 4ull * M * a->FF : 0);
     w.h2 = (float*)take(ctx ? 4ull * M * a->CD : 0);
     w.part = (float*)take(4ull * M * nblk * 2 * a->T);
+    w.sums = (float*)take(4ull * M * 2 * a->T);
     uint64_t cs = 0;
     const int dims[5][2] = {{a->CD, a->D}, {3 * a->CD, a->CD}, {a->CD, a->CD}, {a->FF, a->CD}, {a->CD, a->FF}};
     for (const auto& d : dims) {
@@ -550,7 +575,9 @@ extern "C" int d8s_head(const D8sHeadArgs* a, void* stream) {
     g.A = w.h2; g.Bw = a->ctx_out_w; g.bias = a->ctx_out_b; g.K = a->CD;
     k_head_gemm<PRO_NONE, EPI_DOTS><<<dim3((M + TM - 1) / TM, nblk), NT, 0, st>>>(g);
     // 8. pooling
-    PoolP pp{w.part, w.valid, a->attn_b, a->cls_b, a->logits, a->W, a->T, nblk};
+    const int64_t nsum = (int64_t)M * 2 * a->T;
+    k_head_dotsum<<<(unsigned)((nsum + NT - 1) / NT), NT, 0, st>>>(w.part, a->attn_b, w.sums, M, a->T, nblk);
+    PoolP pp{w.sums, w.valid, a->cls_b, a->logits, a->W, a->T};
     k_head_pool<<<a->B, NT, 0, st>>>(pp);
     return d8s_host_launched("d8s_head");
 }

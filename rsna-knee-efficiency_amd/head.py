@@ -50,6 +50,11 @@ class KneeHead:
         if self.CD != 64 * self.heads:
             raise ValueError(f"context width {self.CD} with {self.heads} heads: 64 per head is required")
         self._ws: torch.Tensor | None = None
+        # the last slot_of_window seen (kept alive, so identity and version name its contents) and
+        # its checked int32 copy on the device: a fixed window layout is validated once, not per call
+        self._slot_src: torch.Tensor | None = None
+        self._slot_ver = -1
+        self._slot_dev: torch.Tensor | None = None
 
     def _args(self, z, slot_of, mask, logits) -> hip.HeadArgs:
         a = hip.HeadArgs()
@@ -61,6 +66,20 @@ class KneeHead:
         a.ctx_layers = 1
         return a
 
+    def _slots(self, slot_of_window: torch.Tensor) -> torch.Tensor:
+        """slot_of_window as int32 on the device, checked to lie in 0 .. S-1 (the reference's embedding
+        lookup raises on such an index).  The check reads the values on the host, so it runs once per
+        tensor and in-place version: later calls with the same unchanged tensor reuse the checked copy."""
+        if (self._slot_src is slot_of_window and slot_of_window._version == self._slot_ver
+                and self._slot_dev is not None):
+            return self._slot_dev
+        host = slot_of_window.detach().to("cpu", torch.int64).reshape(-1)
+        if bool(((host < 0) | (host >= self.S)).any()):
+            raise ValueError("slot_of_window outside 0 .. S-1")
+        self._slot_dev = host.to(torch.int32).to(self.device)
+        self._slot_src, self._slot_ver = slot_of_window, slot_of_window._version
+        return self._slot_dev
+
     def __call__(self, encoded: torch.Tensor, slot_of_window: torch.Tensor, slot_mask: torch.Tensor,
                  window_index: torch.Tensor | None = None) -> torch.Tensor:
         """encoded (B, W, D), slot_of_window (W,), slot_mask (B, S) bool -> logits (B, T) float32.
@@ -68,12 +87,12 @@ class KneeHead:
         if encoded.dim() != 3 or encoded.shape[2] != self.D:
             raise ValueError(f"encoded must be (B, W, {self.D})")
         z = encoded.to(self.device, torch.float32).contiguous()
-        slot_of = slot_of_window.to(self.device, torch.int32).contiguous()
-        mask = slot_mask.to(self.device, torch.uint8).contiguous()
+        slot_of = self._slots(slot_of_window)
+        mask = slot_mask.to(self.device)
+        mask = mask.view(torch.uint8) if mask.dtype == torch.bool else mask.to(torch.uint8)
+        mask = mask.contiguous()
         if slot_of.numel() != z.shape[1] or mask.shape != (z.shape[0], self.S):
             raise ValueError("slot_of_window must have W entries and slot_mask (B, S)")
-        if bool(((slot_of < 0) | (slot_of >= self.S)).any()):
-            raise ValueError("slot_of_window outside 0 .. S-1")
         logits = torch.empty((z.shape[0], self.T), dtype=torch.float32, device=self.device)
         a = self._args(z, slot_of, mask, logits)
         need = ctypes.c_uint64()

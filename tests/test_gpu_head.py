@@ -45,3 +45,24 @@ def test_head_reference_init_and_repeat(dev):
     b = hd(z.to(dev), slot_of, mask)
     assert torch.equal(a, b)
     assert torch.allclose(a.cpu(), H.head_forward(sd, z, slot_of, mask), rtol=1e-4, atol=1e-4)
+
+
+def test_head_slot_indices_checked_per_version(dev):
+    """The window-to-slot map is checked once per tensor and in-place version: an in-place change to
+    another valid map gives that map's logits, one to an index outside 0 .. S-1 raises."""
+    sd = H.random_state_dict(12)
+    z, slot_of, mask = _case(2, 44, 8)
+    hd = head.KneeHead(sd, dev)
+    zd = z.to(dev)
+    a = hd(zd, slot_of, mask)
+    assert torch.allclose(a.cpu(), H.head_forward(sd, z, slot_of, mask), rtol=1e-4, atol=1e-4)
+    slot_of[:11] = 7                      # same tensor, new version
+    b = hd(zd, slot_of, mask)
+    assert torch.allclose(b.cpu(), H.head_forward(sd, z, slot_of, mask), rtol=1e-4, atol=1e-4)
+    assert not torch.equal(a, b)
+    slot_of[0] = 8
+    with pytest.raises(ValueError):
+        hd(zd, slot_of, mask)
+    dslot = (torch.arange(44) // 11).to(dev)   # a device-resident map
+    c = hd(zd, dslot, mask)
+    assert torch.allclose(c.cpu(), H.head_forward(sd, z, dslot.cpu(), mask), rtol=1e-4, atol=1e-4)
