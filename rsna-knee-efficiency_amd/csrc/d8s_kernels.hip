@@ -678,16 +678,25 @@ __global__ __launch_bounds__(256, 2) void k_conv2(D8sConv2Args a, int tiles_x, i
         }
     };
 
+    // tile order: workgroups are dispatched to the 8 XCDs round robin (workgroup b on XCD b % 8), so
+    // a persistent grid gives XCD x one contiguous eighth of the tiles, walked by its workgroups
+    // together: tiles in flight on one XCD are neighbours, and their shared halo rows hit its L2
     const int total = a.N * tiles_x * tiles_y;
-    int tile = blockIdx.x;
-    if (tile >= total) return;
+    int tile = blockIdx.x, tend = total, tstep = gridDim.x;
+    if (total > (int)gridDim.x && (gridDim.x & 7) == 0) {
+        const int chunk = (total + 7) / 8, xcd = blockIdx.x & 7;
+        tstep = gridDim.x >> 3;
+        tile = xcd * chunk + (int)(blockIdx.x >> 3);
+        tend = min(total, (xcd + 1) * chunk);
+    }
+    if (tile >= tend) return;
     hload(tile);
     __syncthreads();                                      // weights
     hstore();
     __syncthreads();
-    for (; tile < total; tile += gridDim.x) {
-        const int next = tile + gridDim.x;
-        if (next < total) hload(next);                    // in flight during this tile's MFMAs
+    for (; tile < tend; tile += tstep) {
+        const int next = tile + tstep;
+        if (next < tend) hload(next);                     // in flight during this tile's MFMAs
         i32x16 acc[PT];
 #pragma unroll
         for (int t = 0; t < PT; ++t) acc[t] = init;
@@ -753,7 +762,7 @@ __global__ __launch_bounds__(256, 2) void k_conv2(D8sConv2Args a, int tiles_x, i
             }
         }
         __syncthreads();                                  // this tile's halo and partial sums read
-        if (next < total) {
+        if (next < tend) {
             hstore();
             __syncthreads();
         }
