@@ -17,7 +17,7 @@
 //   8. k_head_dotsum:                        the partial dots summed over the column blocks
 //   9. k_head_pool:                          per study: a = attn(f2) masked, softmax over windows,
 //                                            logits = sum_w a (f2 . cls_w) + cls_b
-// (one context layer: the final model's configuration.)  A product whose 32 x 64 tiles are too few
+// (one context layer: the final model's configuration.)  A product whose 64 x 64 tiles are too few
 // to fill the chip (the 1664-deep ctx_in above all) is split over K into workgroups that write raw
 // sums, added in split order with the epilogue by k_head_splitk.  The pooled vector of the reference,
 // sum_w a f2, is never formed: its dot with cls_w is sum_w a (f2 . cls_w), the same value up to the
@@ -38,7 +38,7 @@
 namespace {
 
 constexpr int NT = 256;
-constexpr int TM = 32, TN = 64, KC = 64;     // GEMM tile: 32 rows x 64 columns, K in chunks of 64
+constexpr int TM = 64, TN = 64, KC = 64;     // product tile: 64 rows x 64 columns, K in chunks of 64
 constexpr int WMAX = 128;                    // windows per study
 constexpr int TMAX = 16;                     // findings
 
@@ -90,44 +90,51 @@ __global__ void __launch_bounds__(NT) k_head_splitk(GemmP p, int splits) {
     p.C[(int64_t)r * p.ldc + n] = x;
 }
 
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+// One workgroup = a TM x TN tile of C, the four waves its 32 x 32 quarters on v_mfma_f32_32x32x2_f32
+// (float32 operands and sums).  Lane l of a wave supplies A[l % 32][k + l / 32] and B[k + l / 32][l % 32]
+// and holds C[8 (v / 4) + 4 (l / 32) + v % 4][l % 32] in accumulator v.  K runs in chunks of KC staged
+// through LDS: A rows as they are (the prologue applied on the way: slot embedding or LayerNorm),
+// the weights transposed to [k][n] with one column per lane.
 template <int PRO, int EPI>
 __global__ void __launch_bounds__(NT) k_head_gemm(GemmP p) {
     __shared__ float sA[TM][KC + 1];
-    __shared__ float4 sB[KC][TN / 4];
+    __shared__ float sB[KC][TN + 32];          // rows 32 banks apart: the two half-waves' k rows
     __shared__ float sMean[TM], sRstd[TM];
-    const int tid = threadIdx.x;
-    const int ty = tid >> 4, tx = tid & 15;           // rows 2 ty, 2 ty + 1; columns 4 tx .. 4 tx + 3
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wr = wave >> 1, wc = wave & 1;   // the wave's quarter of the tile
+    const int l32 = lane & 31, h = lane >> 5;
     const int r0 = blockIdx.x * TM, n0 = blockIdx.y * TN;
     if constexpr (PRO == PRO_LN) {
         // mean and 1/std of the tile's rows (biased variance, as torch's layer_norm), in two passes
-        // over the row: the mean, then the mean square deviation; 8 lanes per row
-        const int rr = tid >> 3, l8 = tid & 7;
+        // over the row: the mean, then the mean square deviation; 4 lanes per row
+        const int rr = tid >> 2, l4 = tid & 3;
         const int r = r0 + rr;
         float s = 0.0f;
         if (r < p.M)
-            for (int k = l8; k < p.K; k += 8) s += p.A[(int64_t)r * p.K + k];
-#pragma unroll
-        for (int d = 4; d >= 1; d >>= 1) s += __shfl_xor(s, d, 8);
+            for (int k = l4; k < p.K; k += 4) s += p.A[(int64_t)r * p.K + k];
+        s += __shfl_xor(s, 2, 4);
+        s += __shfl_xor(s, 1, 4);
         const float mean = s / (float)p.K;
         float ss = 0.0f;
         if (r < p.M)
-            for (int k = l8; k < p.K; k += 8) {
+            for (int k = l4; k < p.K; k += 4) {
                 const float x = p.A[(int64_t)r * p.K + k] - mean;
                 ss = __builtin_fmaf(x, x, ss);
             }
-#pragma unroll
-        for (int d = 4; d >= 1; d >>= 1) ss += __shfl_xor(ss, d, 8);
-        if (l8 == 0) {
+        ss += __shfl_xor(ss, 2, 4);
+        ss += __shfl_xor(ss, 1, 4);
+        if (l4 == 0) {
             sMean[rr] = mean;
             sRstd[rr] = 1.0f / sqrtf(ss / (float)p.K + 1e-5f);
         }
         __syncthreads();
     }
-    float acc[2][4] = {{0.0f, 0.0f, 0.0f, 0.0f}, {0.0f, 0.0f, 0.0f, 0.0f}};
-    // this thread stages A rows tid / KC + 4 j (j < 8) at column tid % KC of each chunk: the rows'
+    // this thread stages A rows tid / KC + (NT / KC) j at column tid % KC of each chunk: the rows'
     // addresses (and their slot embedding rows) are fixed for the whole K loop
     constexpr int AR = TM * KC / NT;
-    static_assert(TM * KC % NT == 0 && NT % KC == 0, "A staging");
+    static_assert(TM * KC % NT == 0 && NT % KC == 0 && TM == 64 && TN == 64, "staging");
     const int akk = tid % KC, ar0 = tid / KC;
     const float* arow[AR];
     const float* srow[AR];
@@ -145,108 +152,131 @@ __global__ void __launch_bounds__(NT) k_head_gemm(GemmP p) {
         kbeg = blockIdx.z * p.kc_per * KC;
         kend = min(p.K, kbeg + p.kc_per * KC);
     }
+    const bool vec = (p.K & 3) == 0 && ((uintptr_t)p.Bw & 15) == 0;
+    const int bn = tid % TN, n = n0 + bn, bq = tid / TN;       // weights: column bn, k quads bq + 4 u
+    constexpr int BQ = KC / 16;                                  // quads per thread and chunk
+    f32x16 acc;
+#pragma unroll
+    for (int v = 0; v < 16; ++v) acc[v] = 0.0f;
+    // chunk k0's values are fetched into registers (ra, rb) one chunk ahead: their loads are in flight
+    // while the previous chunk's MFMAs run
+    float ra[AR];
+    float4 rb[BQ];
+    auto fetch = [&](int k0) {
+        const int k = k0 + akk;
+#pragma unroll
+        for (int j = 0; j < AR; ++j) {
+            float v = 0.0f;
+            if (arow[j] != nullptr && k < kend) {
+                v = arow[j][k];
+                if constexpr (PRO == PRO_SLOT) v += srow[j][k];
+            }
+            ra[j] = v;
+        }
+#pragma unroll
+        for (int u = 0; u < BQ; ++u) {
+            const int kq = k0 + 4 * (bq + 4 * u);
+            float4 w = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            if (vec) {
+                if (n < p.N && kq < kend) w = *(const float4*)(p.Bw + (int64_t)n * p.K + kq);
+            } else if (n < p.N) {
+                const float* src = p.Bw + (int64_t)n * p.K;
+                w.x = kq + 0 < kend ? src[kq + 0] : 0.0f;
+                w.y = kq + 1 < kend ? src[kq + 1] : 0.0f;
+                w.z = kq + 2 < kend ? src[kq + 2] : 0.0f;
+                w.w = kq + 3 < kend ? src[kq + 3] : 0.0f;
+            }
+            rb[u] = w;
+        }
+    };
+    fetch(kbeg);
     for (int k0 = kbeg; k0 < kend; k0 += KC) {
         const int k = k0 + akk;
 #pragma unroll
         for (int j = 0; j < AR; ++j) {
             const int rr = ar0 + (NT / KC) * j;
-            float v = 0.0f;
-            if (arow[j] != nullptr && k < kend) {
-                v = arow[j][k];
-                if constexpr (PRO == PRO_SLOT) v += srow[j][k];
-                if constexpr (PRO == PRO_LN) v = (v - sMean[rr]) * sRstd[rr] * p.ln_w[k] + p.ln_b[k];
-            }
+            float v = ra[j];
+            if constexpr (PRO == PRO_LN)
+                if (arow[j] != nullptr && k < kend) v = (v - sMean[rr]) * sRstd[rr] * p.ln_w[k] + p.ln_b[k];
             sA[rr][akk] = v;
         }
-        // weights [n0 .. n0 + TN)[k0 .. k0 + KC) transposed into sB[k][n] (4 columns per float4): lane
-        // = column, so the LDS stores of a wave fall in 64 different banks
-        float* sBf = (float*)sB;
-        const int bn = tid % TN, n = n0 + bn;
-        if ((p.K & 3) == 0 && ((uintptr_t)p.Bw & 15) == 0) {
 #pragma unroll
-            for (int q = tid / TN; q < KC / 4; q += NT / TN) {
-                const int kq = k0 + 4 * q;
-                float4 b = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-                if (n < p.N && kq < kend) b = *(const float4*)(p.Bw + (int64_t)n * p.K + kq);
-                sBf[(4 * q + 0) * TN + bn] = b.x;
-                sBf[(4 * q + 1) * TN + bn] = b.y;
-                sBf[(4 * q + 2) * TN + bn] = b.z;
-                sBf[(4 * q + 3) * TN + bn] = b.w;
-            }
-        } else {
-            for (int kk = tid / TN; kk < KC; kk += NT / TN) {
-                const int kx = k0 + kk;
-                sBf[kk * TN + bn] = (n < p.N && kx < kend) ? p.Bw[(int64_t)n * p.K + kx] : 0.0f;
-            }
+        for (int u = 0; u < BQ; ++u) {
+            const int q = bq + 4 * u;
+            sB[4 * q + 0][bn] = rb[u].x;
+            sB[4 * q + 1][bn] = rb[u].y;
+            sB[4 * q + 2][bn] = rb[u].z;
+            sB[4 * q + 3][bn] = rb[u].w;
         }
         __syncthreads();
-#pragma unroll 8
-        for (int kk = 0; kk < KC; ++kk) {
-            const float a0 = sA[2 * ty][kk], a1 = sA[2 * ty + 1][kk];
-            const float4 bv = sB[kk][tx];
-            const float bb[4] = {bv.x, bv.y, bv.z, bv.w};
+        if (k0 + KC < kend) fetch(k0 + KC);
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                acc[0][j] = __builtin_fmaf(a0, bb[j], acc[0][j]);
-                acc[1][j] = __builtin_fmaf(a1, bb[j], acc[1][j]);
-            }
+        for (int kk = 0; kk < KC; kk += 2) {
+            const float av = sA[32 * wr + l32][kk + h];
+            const float bv = sB[kk + h][32 * wc + l32];
+            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av, bv, acc, 0, 0, 0);
         }
         __syncthreads();
     }
+    const int n_out = n0 + 32 * wc + l32;
     if (gridDim.z > 1) {
         // split K: raw sums into the split's slice of Cs; k_head_splitk adds them and applies the epilogue
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            const int r = r0 + 2 * ty + i;
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const int n = n0 + 4 * tx + j;
-                if (r < p.M && n < p.N) p.Cs[((int64_t)blockIdx.z * p.M + r) * p.N + n] = acc[i][j];
-            }
+        for (int v = 0; v < 16; ++v) {
+            const int r = r0 + 32 * wr + 8 * (v >> 2) + 4 * h + (v & 3);
+            if (r < p.M && n_out < p.N) p.Cs[((int64_t)blockIdx.z * p.M + r) * p.N + n_out] = acc[v];
         }
         return;
     }
+    if constexpr (EPI != EPI_DOTS) {
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        const int r = r0 + 2 * ty + i;
-        float v[4];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int n = n0 + 4 * tx + j;
-            v[j] = 0.0f;
-            if (r >= p.M || n >= p.N) continue;
-            float x = acc[i][j] + p.bias[n];
-            if constexpr (EPI == EPI_BIAS_POS) x += p.pos[(int64_t)((r % p.W) % p.per) * p.N + n];
-            if constexpr (EPI == EPI_BIAS_RES) x += p.R[(int64_t)r * p.N + n];
+        for (int v = 0; v < 16; ++v) {
+            const int r = r0 + 32 * wr + 8 * (v >> 2) + 4 * h + (v & 3);
+            if (r >= p.M || n_out >= p.N) continue;
+            float x = acc[v] + p.bias[n_out];
+            if constexpr (EPI == EPI_BIAS_POS) x += p.pos[(int64_t)((r % p.W) % p.per) * p.N + n_out];
+            if constexpr (EPI == EPI_BIAS_RES) x += p.R[(int64_t)r * p.N + n_out];
             if constexpr (EPI == EPI_BIAS_RELU) x = fmaxf(x, 0.0f);
-            if constexpr (EPI == EPI_DOTS)
-                x += p.z[(int64_t)r * p.N + n] + p.slot_emb[(int64_t)p.slot_of[r % p.W] * p.N + n];
-            v[j] = x;
-            if constexpr (EPI != EPI_DOTS) p.C[(int64_t)r * p.ldc + n] = x;
+            p.C[(int64_t)r * p.ldc + n_out] = x;
         }
-        if constexpr (EPI == EPI_DOTS) {
-            // the row's dots over these 64 columns with the attention and classifier weights: partial
-            // sums of the 16 lanes of the row combined by shuffles
-            for (int t = 0; t < p.T; ++t) {
-                float da = 0.0f, dc = 0.0f;
+    } else {
+        // f2 = z + slot_emb + acc + bias into LDS (the A tile's space), the attention and classifier
+        // weights of these 64 columns beside it; then 4 lanes per row take 16 columns each and the
+        // row's dots are summed over the 4 lanes
+        __shared__ float sF[TM][TN + 1];
+        __shared__ float sW[2 * TMAX][TN];
 #pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const int n = n0 + 4 * tx + j;
-                    if (n < p.N) {
-                        da = __builtin_fmaf(v[j], p.tw[(int64_t)t * p.N + n], da);
-                        dc = __builtin_fmaf(v[j], p.cw[(int64_t)t * p.N + n], dc);
-                    }
-                }
+        for (int v = 0; v < 16; ++v) {
+            const int i = 32 * wr + 8 * (v >> 2) + 4 * h + (v & 3), r = r0 + i;
+            float x = 0.0f;
+            if (r < p.M && n_out < p.N)
+                x = acc[v] + p.bias[n_out] + p.z[(int64_t)r * p.N + n_out] +
+                    p.slot_emb[(int64_t)p.slot_of[r % p.W] * p.N + n_out];
+            sF[i][32 * wc + l32] = x;
+        }
+        for (int i = tid; i < 2 * p.T * TN; i += NT) {
+            const int q = i / TN, c = i % TN, nn = n0 + c;
+            const float* src = q < p.T ? p.tw + (int64_t)q * p.N : p.cw + (int64_t)(q - p.T) * p.N;
+            sW[q][c] = nn < p.N ? src[nn] : 0.0f;
+        }
+        __syncthreads();
+        const int rr = tid >> 2, c0 = 16 * (tid & 3), r = r0 + rr;
+        for (int t = 0; t < p.T; ++t) {
+            float da = 0.0f, dc = 0.0f;
 #pragma unroll
-                for (int d = 8; d >= 1; d >>= 1) {
-                    da += __shfl_xor(da, d, 16);
-                    dc += __shfl_xor(dc, d, 16);
-                }
-                if (tx == 0 && r < p.M) {
-                    float* dst = p.part + ((int64_t)r * gridDim.y + blockIdx.y) * 2 * p.T;
-                    dst[t] = da;
-                    dst[p.T + t] = dc;
-                }
+            for (int c = 0; c < 16; ++c) {
+                const float x = sF[rr][c0 + c];
+                da = __builtin_fmaf(x, sW[t][c0 + c], da);
+                dc = __builtin_fmaf(x, sW[p.T + t][c0 + c], dc);
+            }
+            da += __shfl_xor(da, 2, 4);
+            da += __shfl_xor(da, 1, 4);
+            dc += __shfl_xor(dc, 2, 4);
+            dc += __shfl_xor(dc, 1, 4);
+            if ((tid & 3) == 0 && r < p.M) {
+                float* dst = p.part + ((int64_t)r * gridDim.y + blockIdx.y) * 2 * p.T;
+                dst[t] = da;
+                dst[p.T + t] = dc;
             }
         }
     }
