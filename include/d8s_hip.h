@@ -306,7 +306,10 @@ int d8s_grid_sample(const D8sGridArgs* a, void* stream);
  * Weights in torch's Linear layout [out][in]; the transformer layer's are those of
  * `nn.TransformerEncoderLayer` (self_attn.in_proj, self_attn.out_proj, linear1, linear2, norm1, norm2).
  * W <= 128, CD = 64 x heads, T <= 16.  slot_mask [B][S] uint8; the reference's window_index is not
- * used by this configuration (context_pos None: the position is w % PER). */
+ * used by this configuration (context_pos None: the position is w % PER).  slot_of is read on the
+ * device and not checked (a check would synchronise): an entry outside 0 .. S-1 reads no memory, its
+ * windows take no slot embedding and count as absent, where the reference raises; callers validate
+ * the map once. */
 typedef struct D8sHeadArgs {
     const float* z;            /* [B][W][D] encoder features */
     const int32_t* slot_of;    /* [W] */

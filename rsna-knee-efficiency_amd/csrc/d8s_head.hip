@@ -51,10 +51,10 @@ struct GemmP {
     const float* bias;   // [N]
     float* C;            // [M][ldc]
     int M, N, K, ldc;
-    // PRO_SLOT: A row r gets + slot_emb[slot_of[r % W]]
+    // PRO_SLOT: A row r gets + slot_emb[slot_of[r % W]] (nothing for a slot outside 0 .. S-1)
     const float* slot_emb;
     const int32_t* slot_of;
-    int W;
+    int W, S;
     // PRO_LN: A row normalised with ln_w, ln_b (eps 1e-5)
     const float* ln_w;
     const float* ln_b;
@@ -144,7 +144,10 @@ __global__ void __launch_bounds__(NT) k_head_gemm(GemmP p) {
         arow[j] = r < p.M ? p.A + (int64_t)r * p.K : nullptr;
         srow[j] = nullptr;
         if constexpr (PRO == PRO_SLOT)
-            if (r < p.M) srow[j] = p.slot_emb + (int64_t)p.slot_of[r % p.W] * p.K;
+            if (r < p.M) {
+                const int sl = p.slot_of[r % p.W];
+                if ((unsigned)sl < (unsigned)p.S) srow[j] = p.slot_emb + (int64_t)sl * p.K;
+            }
     }
     // split K: block z of gridDim.z takes chunks [z kc_per, (z + 1) kc_per)
     int kbeg = 0, kend = p.K;
@@ -169,7 +172,8 @@ __global__ void __launch_bounds__(NT) k_head_gemm(GemmP p) {
             float v = 0.0f;
             if (arow[j] != nullptr && k < kend) {
                 v = arow[j][k];
-                if constexpr (PRO == PRO_SLOT) v += srow[j][k];
+                if constexpr (PRO == PRO_SLOT)
+                    if (srow[j] != nullptr) v += srow[j][k];
             }
             ra[j] = v;
         }
@@ -249,9 +253,11 @@ __global__ void __launch_bounds__(NT) k_head_gemm(GemmP p) {
         for (int v = 0; v < 16; ++v) {
             const int i = 32 * wr + 8 * (v >> 2) + 4 * h + (v & 3), r = r0 + i;
             float x = 0.0f;
-            if (r < p.M && n_out < p.N)
+            if (r < p.M && n_out < p.N) {
+                const int sl = p.slot_of[r % p.W];
                 x = acc[v] + p.bias[n_out] + p.z[(int64_t)r * p.N + n_out] +
-                    p.slot_emb[(int64_t)p.slot_of[r % p.W] * p.N + n_out];
+                    ((unsigned)sl < (unsigned)p.S ? p.slot_emb[(int64_t)sl * p.N + n_out] : 0.0f);
+            }
             sF[i][32 * wc + l32] = x;
         }
         for (int i = tid; i < 2 * p.T * TN; i += NT) {
@@ -454,11 +460,13 @@ __global__ void __launch_bounds__(NT) k_head_pool(PoolP p) {
     if (t < p.T && l == 0) p.logits[(int64_t)b * p.T + t] = acc / sum + p.cls_b[t];
 }
 
-// valid[b][w] = slot_mask[b][slot_of[w]]
+// valid[b][w] = slot_mask[b][slot_of[w]] (0 for a slot outside 0 .. S-1)
 __global__ void __launch_bounds__(NT) k_head_valid(const uint8_t* slot_mask, const int32_t* slot_of,
                                                    uint8_t* valid, int B, int W, int S) {
     const int i = blockIdx.x * NT + threadIdx.x;
-    if (i < B * W) valid[i] = slot_mask[(int64_t)(i / W) * S + slot_of[i % W]] ? 1 : 0;
+    if (i >= B * W) return;
+    const int sl = slot_of[i % W];
+    valid[i] = (unsigned)sl < (unsigned)S && slot_mask[(int64_t)(i / W) * S + sl] ? 1 : 0;
 }
 
 #define HREQ(cond, msg) \
@@ -568,6 +576,7 @@ extern "C" int d8s_head(const D8sHeadArgs* a, void* stream) {
         GemmP g{};
         g.M = M;
         g.W = a->W;
+        g.S = a->S;
         g.slot_of = a->slot_of;
         g.slot_emb = a->slot_emb;
         // 1. h = (z + slot_emb) ctx_in^T + b + ctx_pos[w % per]
@@ -600,7 +609,7 @@ extern "C" int d8s_head(const D8sHeadArgs* a, void* stream) {
     }
     // 7. f2 = z + slot_emb + h2 ctx_out^T + b, partial dots with attn.weight and cls_w
     GemmP g{};
-    g.M = M; g.W = a->W; g.slot_of = a->slot_of; g.slot_emb = a->slot_emb;
+    g.M = M; g.W = a->W; g.S = a->S; g.slot_of = a->slot_of; g.slot_emb = a->slot_emb;
     g.N = a->D; g.z = a->z; g.tw = a->attn_w; g.cw = a->cls_w; g.part = w.part; g.T = a->T;
     g.A = w.h2; g.Bw = a->ctx_out_w; g.bias = a->ctx_out_b; g.K = a->CD;
     k_head_gemm<PRO_NONE, EPI_DOTS><<<dim3((M + TM - 1) / TM, nblk), NT, 0, st>>>(g);

@@ -66,3 +66,35 @@ def test_head_slot_indices_checked_per_version(dev):
     dslot = (torch.arange(44) // 11).to(dev)   # a device-resident map
     c = hd(zd, dslot, mask)
     assert torch.allclose(c.cpu(), H.head_forward(sd, z, dslot.cpu(), mask), rtol=1e-4, atol=1e-4)
+
+
+def test_head_abi_slot_outside_range_reads_nothing(dev):
+    """Through the C ABI with a device map holding indices outside 0 .. S-1 (-1 and S): those windows
+    take no slot embedding and count as absent, which is the oracle with a zero-embedding slot S that
+    no study has."""
+    import ctypes
+    from rsna_knee_efficiency_amd import hip
+    sd = H.random_state_dict(13)
+    z, slot_of, mask = _case(2, 44, 9)
+    bad = slot_of.clone()
+    bad[3], bad[20] = -1, 8
+    hd = head.KneeHead(sd, dev)
+    zd = z.to(dev).contiguous()
+    sl = bad.to(dev, torch.int32)
+    md = mask.to(dev).view(torch.uint8).contiguous()
+    logits = torch.empty((2, 12), dtype=torch.float32, device=dev)
+    a = hd._args(zd, sl, md, logits)
+    need = ctypes.c_uint64()
+    hip.call("d8s_head_workspace", ctypes.byref(a), ctypes.byref(need))
+    ws = torch.empty(int(need.value) + 256, dtype=torch.uint8, device=dev)
+    base = (ws.data_ptr() + 255) // 256 * 256
+    a.workspace, a.ws_bytes = base, ws.numel() - (base - ws.data_ptr())
+    hip.call("d8s_head", ctypes.byref(a), ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream))
+    torch.cuda.synchronize(dev)
+    sd9 = dict(sd)
+    sd9["slot_emb"] = torch.cat([sd["slot_emb"], torch.zeros(1, 1664)])
+    ref_slot = bad.clone()
+    ref_slot[ref_slot < 0] = 8
+    ref_mask = torch.cat([mask, torch.zeros((2, 1), dtype=torch.bool)], 1)
+    want = H.head_forward(sd9, z, ref_slot, ref_mask)
+    assert torch.allclose(logits.cpu(), want, rtol=1e-4, atol=1e-4)
