@@ -280,6 +280,46 @@ def traffic_summary(fetch_dir: str, write_dir: str, passes: int, copy_bytes: int
     return "\n".join(lines + ["", "```", *machine, "```"])
 
 
+def mfma_summary(pmc_dir: str, passes: int) -> str:
+    """MFMA use per kernel family from one counter run of `bench.py --pmc-passes P` with
+    `--pmc MfmaUtil GRBM_GUI_ACTIVE SQ_INSTS_VALU_MFMA_MOPS_I8 SQ_INSTS_VALU_MFMA_MOPS_F16`:
+    MfmaUtil (SQ_VALU_MFMA_BUSY_CYCLES over GRBM_GUI_ACTIVE x SIMDs, per dispatch) averaged with the
+    dispatches' GRBM_GUI_ACTIVE as weights, and the MFMA operations issued (MOPS x 512) against the
+    algorithmic int8 operations of the family (`kernel_ops`): above 1 where K steps are padded."""
+    import csv
+    import glob
+
+    per: dict = {}
+    for path in glob.glob(os.path.join(pmc_dir, "**", "*counter_collection.csv"), recursive=True):
+        for r in csv.DictReader(open(path)):
+            fam = _family(r.get("Kernel_Name", ""))
+            if not fam:
+                continue
+            d = per.setdefault(fam, {}).setdefault(r.get("Dispatch_Id", r.get("Correlation_Id", "")), {})
+            d[r["Counter_Name"]] = d.get(r["Counter_Name"], 0.0) + float(r["Counter_Value"])
+    nb = 4 * SLICES
+    meta_blocks = [{"c0": 64, "h": 128, "w": 128, "L": 6, "trans": True},
+                   {"c0": 128, "h": 64, "w": 64, "L": 12, "trans": True},
+                   {"c0": 256, "h": 32, "w": 32, "L": 32, "trans": True},
+                   {"c0": 640, "h": 16, "w": 16, "L": 32, "trans": False}]
+    kinds = dense8s.fused_blocks({"blocks": meta_blocks})
+    alg = kernel_ops({"img": IMG, "blocks": meta_blocks}, nb, kinds)
+    lines = ["| family | dispatches | MFMA busy (% of SIMD cycles, weighted) | MFMA ops issued per pass (G) "
+             "| algorithmic int8 ops per pass (G) | issued / algorithmic |", "|---|---|---|---|---|---|"]
+    for fam in ("conv1", "conv2", "dense", "block", "trans", "stem"):
+        if fam not in per:
+            continue
+        ds = list(per[fam].values())
+        w = sum(d.get("GRBM_GUI_ACTIVE", 0.0) for d in ds)
+        util = sum(d.get("MfmaUtil", 0.0) * d.get("GRBM_GUI_ACTIVE", 0.0) for d in ds) / w if w else 0.0
+        ops = sum(d.get("SQ_INSTS_VALU_MFMA_MOPS_I8", 0.0) + d.get("SQ_INSTS_VALU_MFMA_MOPS_F16", 0.0)
+                  for d in ds) * 512 / passes
+        a = alg.get(fam, 0.0)
+        lines.append(f"| {fam} | {len(ds)} | {util:.1f} | {ops / 1e9:.1f} | {a / 1e9:.1f} | "
+                     f"{ops / a if a else float('nan'):.3f} |")
+    return "\n".join(lines)
+
+
 def committed_traffic(family: str) -> int | None:
     """HBM bytes per launch of `family` from the committed counter summary (None if absent)."""
     try:
@@ -583,9 +623,14 @@ def main() -> None:
                          "after the encoder")
     ap.add_argument("--traffic-summary", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                     help="print the HBM traffic per launch from two --pmc-passes counter runs")
+    ap.add_argument("--mfma-summary", metavar="PMC_DIR",
+                    help="print the MFMA use per family from a --pmc-passes counter run")
     args = ap.parse_args()
     if args.rocprof_summary:
         print(rocprof_summary(args.rocprof_summary))
+        return
+    if args.mfma_summary:
+        print(mfma_summary(args.mfma_summary, passes=args.pmc_passes or 3))
         return
     if args.traffic_summary:
         if args.path == "prep":
