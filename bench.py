@@ -14,6 +14,9 @@ The two seeds' passes of a step run from two streams (`--serial`: one after the 
 graph and replayed between HIP events on the encoder's stream (algorithmic bytes of a launch / the
 average launch time).
 `cpu_baseline`: the float32 DenseNet169 forward (`oracle/fp32.py`) at batch 1 on the host cores.
+`fp32_agreement`: max-abs, rel_l2 and minimum cosine of the configuration-4 study's INT8 features (and
+of a seeded 1664 -> 8 linear head's logits) against the fp32 DenseNet169 forward of the same weights
+(the package's `densenet` module in float32 on the GPU), with the reference's gate.
 `prep`: the upstream preparation (raw uint16 crops -> the uint8 volume of a study, `d8s_prep`) on the
 same GPU, studies/s with the payloads resident in HBM.
 One JSON line on stdout.
@@ -725,6 +728,25 @@ def main() -> None:
     study_ms = float(np.median(lat)) * 1e3
     log(f"config 4: study latency {study_ms:.3f} ms (median of {len(lat)})")
 
+    # agreement of the INT8 features with the fp32 DenseNet169 forward of the same weights on the same
+    # study (the GPU, float32 torch), and of the logits of a seeded 1664 -> 8 linear head
+    model4 = densenet.seeded_densenet169(0).to(dev).eval()
+    with torch.no_grad():
+        ref4 = model4(synthetic.normalise(x4)).double().cpu().numpy()
+    got4 = enc4(x4).double().cpu().numpy()
+    del model4
+    hw, hb = synthetic.linear_head(1664, 8, seed=99)
+
+    def agree(a: np.ndarray, b: np.ndarray) -> dict:
+        cos = (a * b).sum(1) / np.maximum(np.linalg.norm(a, axis=1) * np.linalg.norm(b, axis=1), 1e-30)
+        return {"max_abs": round(float(np.abs(a - b).max()), 5),
+                "rel_l2": round(float(np.linalg.norm(a - b) / max(np.linalg.norm(b), 1e-30)), 5),
+                "cos_min": round(float(cos.min()), 6)}
+
+    fp32_agreement = {"features": agree(got4, ref4), "logits": agree(got4 @ hw.T + hb, ref4 @ hw.T + hb),
+                      "slices": SLICES, "gate": "rel_l2 <= 1.05 x 0.067, cos_min >= 0.99"}
+    log(f"fp32 agreement {fp32_agreement}")
+
     # per-family kernel times: each family's launches of a pass in a HIP graph, replayed between
     # HIP events on the encoder's stream
     fam = encs[0].time_families(studies[0], reps=args.prof_reps, flip="tta")
@@ -752,6 +774,7 @@ def main() -> None:
                    "global_batch": nb, "seeds": 2, "image": IMG, "parallelism": "none (1 GPU)"},
         "study_latency_ms": round(study_ms, 3),
         "study_latency_config": "C4: one 24-slice study, batch 24, one encoder, HIP graph replay",
+        "fp32_agreement": fp32_agreement,
         "step_schedule": "serial (one stream)" if args.serial else "the 2 seeds' passes on 2 streams",
         "pass_ms_kernels": round(pass_ms, 3),
         "pass_hbm_frac": round(total_bytes / (pass_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
