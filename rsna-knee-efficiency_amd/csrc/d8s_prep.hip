@@ -793,9 +793,18 @@ __global__ void __launch_bounds__(NT) k_grid_sample(D8sGridArgs a) {
             return (int64_t)n * HW;
         }
     };
+    // the GIMG images' planes first (their slice indices are loads), then every gather of every image
+    // (loads clamped to the last image, stores predicated), so they are all in flight together
+    int64_t pl[GIMG];
+#pragma unroll
+    for (int i = 0; i < GIMG; ++i) pl[i] = plane(min(n0 + i, n1 - 1));
     if constexpr (KIND == 2) {
-        for (int n = n0; n < n1; ++n)
-            ((uint16_t*)a.out)[(int64_t)n * HW + p] = s_lut[((const uint8_t*)a.src)[plane(n) + p]];
+        uint8_t v[GIMG];
+#pragma unroll
+        for (int i = 0; i < GIMG; ++i) v[i] = ((const uint8_t*)a.src)[pl[i] + p];
+#pragma unroll
+        for (int i = 0; i < GIMG; ++i)
+            if (n0 + i < n1) ((uint16_t*)a.out)[(int64_t)(n0 + i) * HW + p] = s_lut[v[i]];
         return;
     } else {
         const __half2 g = ((const __half2*)a.grid)[p];
@@ -809,22 +818,31 @@ __global__ void __launch_bounds__(NT) k_grid_sample(D8sGridArgs a) {
         const bool vx0 = x0 >= 0 && x0 < a.W, vx1 = x1 >= 0 && x1 < a.W;
         const bool vy0 = y0 >= 0 && y0 < a.H, vy1 = y1 >= 0 && y1 < a.H;
         const bool ok[4] = {vy0 && vx0, vy0 && vx1, vy1 && vx0, vy1 && vx1};
-        const int off[4] = {y0 * a.W + x0, y0 * a.W + x1, y1 * a.W + x0, y1 * a.W + x1};
-        for (int n = n0; n < n1; ++n) {
-            const int64_t pl = plane(n);
+        // taps outside the image read the plane's first pixel and are not added
+        const int off[4] = {ok[0] ? y0 * a.W + x0 : 0, ok[1] ? y0 * a.W + x1 : 0,
+                            ok[2] ? y1 * a.W + x0 : 0, ok[3] ? y1 * a.W + x1 : 0};
+        float v[GIMG][4];
+#pragma unroll
+        for (int i = 0; i < GIMG; ++i)
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                if constexpr (KIND == 1)
+                    v[i][t] = (float)((const uint8_t*)a.src)[pl[i] + off[t]];
+                else
+                    v[i][t] = __half2float(((const __half*)a.src)[pl[i] + off[t]]);
+            }
+#pragma unroll
+        for (int i = 0; i < GIMG; ++i) {
             float acc = 0.0f;
 #pragma unroll
             for (int t = 0; t < 4; ++t) {
                 if (ok[t]) {
-                    float v;
-                    if constexpr (KIND == 1)
-                        v = __half2float(__ushort_as_half(s_lut[((const uint8_t*)a.src)[pl + off[t]]]));
-                    else
-                        v = __half2float(((const __half*)a.src)[pl + off[t]]);
-                    acc = __builtin_fmaf(v, w[t], acc);
+                    float x = v[i][t];
+                    if constexpr (KIND == 1) x = __half2float(__ushort_as_half(s_lut[(int)x]));
+                    acc = __builtin_fmaf(x, w[t], acc);
                 }
             }
-            ((__half*)a.out)[(int64_t)n * HW + p] = __float2half_rn(acc);
+            if (n0 + i < n1) ((__half*)a.out)[(int64_t)(n0 + i) * HW + p] = __float2half_rn(acc);
         }
     }
 }
