@@ -98,3 +98,23 @@ def test_head_abi_slot_outside_range_reads_nothing(dev):
     ref_mask = torch.cat([mask, torch.zeros((2, 1), dtype=torch.bool)], 1)
     want = H.head_forward(sd9, z, ref_slot, ref_mask)
     assert torch.allclose(logits.cpu(), want, rtol=1e-4, atol=1e-4)
+
+
+@pytest.mark.parametrize("d,w,slots,per,cd,targets,b", [
+    (602, 37, 5, 7, 128, 5, 3),      # depth not a multiple of 4 (scalar weight staging), odd windows
+    (640, 16, 2, 16, 192, 16, 1),    # 3 heads, 16 findings, one query group
+    (100, 129 - 1, 8, 11, 64, 1, 2),  # one head, one finding, 128 windows, a partial column tile
+])
+def test_head_other_shapes(dev, d, w, slots, per, cd, targets, b):
+    """Shapes away from the final configuration: partial product tiles in every dimension, the
+    scalar weight path, 1-3 heads, 1-16 findings, other slot and position counts."""
+    sd = H.random_state_dict(d + w, d=d, slots=slots, per=per, cd=cd, targets=targets)
+    g = torch.Generator().manual_seed(w)
+    z = torch.randn((b, w, d), generator=g) * 0.5
+    slot_of = torch.arange(w) % slots
+    mask = torch.rand((b, slots), generator=g) > 0.3
+    mask[0, 0] = True
+    want = H.head_forward(sd, z, slot_of, mask, heads=cd // 64)
+    got = head.KneeHead(sd, dev, context_heads=cd // 64)(z.to(dev), slot_of, mask).cpu()
+    assert got.shape == (b, targets)
+    assert torch.allclose(got, want, rtol=1e-4, atol=1e-4), float((got - want).abs().max())
