@@ -68,6 +68,23 @@ def affine_windows(w: torch.Tensor, scale: float = 1.0, tx: float = 0.0, ty: flo
     return out
 
 
+# the last slice-index tensor checked on each device (kept alive, so identity and version name its
+# contents) and the bound it was checked against
+_SLICES_CHECKED: dict = {}
+
+
+def _check_slices(idx: torch.Tensor, limit: int) -> None:
+    """Raise unless every index lies in 0 .. limit-1.  The check reads the values back (a
+    synchronisation), so it runs once per tensor, in-place version and bound: a fixed window layout
+    passed as the same tensor on every call is checked once."""
+    c = _SLICES_CHECKED.get(idx.device)
+    if c is not None and c[0] is idx and c[1] == idx._version and c[2] == limit:
+        return
+    if bool(((idx < 0) | (idx >= limit)).any()):
+        raise ValueError("slice_idx outside the volume")
+    _SLICES_CHECKED[idx.device] = (idx, idx._version, limit)
+
+
 def windows_u8(v_u8: torch.Tensor, slice_idx: torch.Tensor, out: torch.Tensor, scale: float = 1.0,
                tx: float = 0.0, ty: float = 0.0) -> torch.Tensor:
     """`out` (B * nw, depth, H, W) fp16 = the slices `slice_idx` (int64, nw * depth entries) of every
@@ -81,8 +98,7 @@ def windows_u8(v_u8: torch.Tensor, slice_idx: torch.Tensor, out: torch.Tensor, s
     if out.dtype != torch.float16 or not out.is_contiguous() or out.numel() != b * m * h * w:
         raise ValueError("out must be a contiguous fp16 tensor of B * len(slice_idx) images")
     idx = slice_idx.contiguous()
-    if bool(((idx < 0) | (idx >= s * k)).any()):
-        raise ValueError("slice_idx outside the volume")
+    _check_slices(idx, s * k)
     gp = 0
     if not (scale == 1.0 and tx == 0.0 and ty == 0.0):
         gp = view_grid(h, w, 1, scale, tx, ty, torch.float16, v_u8.device).data_ptr()

@@ -87,3 +87,38 @@ def test_lut_is_u_over_255():
     lut = tta.lut_u8_f16("cpu").float().numpy()
     u = np.arange(256) / 255.0
     assert np.abs(lut - u).max() <= 2.0 ** -12 and lut[0] == 0 and lut[255] == 1
+
+
+@pytest.mark.parametrize("view", [(1.0, 0.0, 0.0), (1.10, 0.0, 0.0)])
+def test_windows_u8_slice_checks(dev, view):
+    """The slice indices are checked once per tensor and in-place version: a valid in-place change is
+    seen, an index outside the volume raises; through the C ABI (no host check) such an index reads
+    nothing and its images are zeros."""
+    import ctypes
+    from rsna_knee_efficiency_amd import hip
+    b, s, k, h, w = 1, 2, 5, 32, 40
+    g = torch.Generator().manual_seed(6)
+    v = torch.randint(0, 256, (b, s, k, h, w), generator=g, dtype=torch.uint8).to(dev)
+    idx = torch.tensor([0, 1, 2, 7, 8, 9], dtype=torch.int64, device=dev)
+    out = torch.empty((2, 3, h, w), dtype=torch.float16, device=dev)
+    a = tta.windows_u8(v, idx, out, *view).clone()
+    idx[0] = 4                                     # in place, still inside the volume
+    bb = tta.windows_u8(v, idx, out, *view).clone()
+    assert torch.equal(a[1], bb[1]) and not torch.equal(a[0, 0], bb[0, 0])
+    idx[0] = 10
+    with pytest.raises(ValueError):
+        tta.windows_u8(v, idx, out, *view)
+    bad = torch.tensor([0, -1, 2, 10, 8, 9], dtype=torch.int64, device=dev)
+    gp = 0 if view == (1.0, 0.0, 0.0) else tta.view_grid(h, w, 1, *view, torch.float16, dev).data_ptr()
+    out2 = torch.full((2, 3, h, w), 7.0, dtype=torch.float16, device=dev)
+    args = hip.GridArgs(src=v.data_ptr(), slice_idx=bad.data_ptr(), lut=tta.lut_u8_f16(dev).data_ptr(),
+                        grid=gp, out=out2.data_ptr(), kind=1, N=6, H=h, W=w, B=1, SK=s * k, M=6)
+    hip.call("d8s_grid_sample", ctypes.byref(args), ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream))
+    torch.cuda.synchronize(dev)
+    good = torch.tensor([0, 0, 2, 0, 8, 9], dtype=torch.int64, device=dev)
+    ref = torch.empty_like(out2)
+    tta.windows_u8(v, good, ref, *view)
+    flat, rflat = out2.view(6, h, w), ref.view(6, h, w)
+    assert not flat[1].any() and not flat[3].any()
+    for i in (0, 2, 4, 5):
+        assert torch.equal(flat[i], rflat[i]), i
