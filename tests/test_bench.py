@@ -1,0 +1,98 @@
+"""bench.py on the CPU: the algorithmic work it divides by (closed forms of DenseNet169 at 512 px), the
+counter summaries it reads back from rocprofv3 CSV files, and its one-GPU contract."""
+from __future__ import annotations
+
+import csv
+import os
+import subprocess
+import sys
+from pathlib import Path
+
+import pytest
+
+import bench
+from rsna_knee_efficiency_amd import dense8s
+
+ROOT = Path(__file__).resolve().parents[1]
+BLOCKS = [{"c0": 64, "h": 128, "w": 128, "L": 6, "trans": True},
+          {"c0": 128, "h": 64, "w": 64, "L": 12, "trans": True},
+          {"c0": 256, "h": 32, "w": 32, "L": 32, "trans": True},
+          {"c0": 640, "h": 16, "w": 16, "L": 32, "trans": False}]
+META = {"img": 512, "blocks": BLOCKS}
+
+
+def test_ops_per_slice_closed_form():
+    """int8 operations per 512 px slice: conv1 16.14 G, conv2 13.89 G, transitions 0.96 G (pooled
+    resolution), stem 1.23 G — 32.22 G in all, counted layer by layer from the architecture."""
+    ops = bench.kernel_ops(META, 1, {})
+    conv1 = sum(2 * b["h"] * b["w"] * (b["c0"] + 32 * l) * 128 for b in BLOCKS for l in range(b["L"]))
+    conv2 = sum(2 * b["h"] * b["w"] * 1152 * 32 * b["L"] for b in BLOCKS)
+    assert ops["conv1"] == conv1 and ops["conv2"] == conv2
+    assert abs(ops["conv1"] / 1e9 - 16.14) < 0.01 and abs(ops["conv2"] / 1e9 - 13.89) < 0.01
+    assert abs(ops["trans"] / 1e9 - 0.96) < 0.01 and abs(ops["stem"] / 1e9 - 1.23) < 0.01
+    assert abs(sum(ops.values()) / 1e9 - 32.22) < 0.02
+    # fused kinds move the same work into their families
+    fused = bench.kernel_ops(META, 1, dense8s.fused_blocks(META))
+    assert abs(sum(fused.values()) - sum(ops.values())) < 1.0
+
+
+def test_bytes_scale_with_images_and_match_the_layer_sums():
+    one, four = bench.kernel_bytes(META, 1, {}), bench.kernel_bytes(META, 4, {})
+    assert len(one["conv1"]) == len(one["conv2"]) == 82 and len(one["trans"]) == 3
+    b1 = BLOCKS[1]
+    M = b1["h"] * b1["w"]
+    # conv1 of block 1, layer 0: activations in, bottleneck out, weights, tables
+    assert one["conv1"][6] == M * 128 + M * 128 + 128 * 128 + 128 * 4 + 128 * 12
+    # activation bytes scale with the images, weights and tables do not
+    assert 4 * one["conv1"][6] - four["conv1"][6] == 3 * (128 * 128 + 128 * 4 + 128 * 12)
+    # per slice at batch 24 (weights read once per batch): the 128.7 MB of the layer-by-layer design
+    b24 = bench.kernel_bytes(META, 24, {})
+    assert abs(sum(sum(v) for v in b24.values()) / 24 / 1e6 - 128.7) < 1.5
+
+
+def _counter_csv(path: Path, rows: list[tuple[int, str, str, float]]) -> None:
+    path.parent.mkdir(parents=True, exist_ok=True)
+    with open(path, "w", newline="") as f:
+        w = csv.writer(f)
+        w.writerow(["Dispatch_Id", "Kernel_Name", "Counter_Name", "Counter_Value"])
+        for r in rows:
+            w.writerow(r)
+
+
+def test_traffic_summary_scales_by_the_copy_kernel(tmp_path):
+    """FETCH_SIZE and WRITE_SIZE (KiB per dispatch) scaled by what they read for the 1 GiB copy."""
+    gib = 1 << 30
+    conv1 = "void k_conv1p<false, 1, 2, 4>(D8sGemmArgs, int*)"
+    fe = [(1, "k_copy(const u32x4*, u32x4*, long)", "FETCH_SIZE", gib / 2 / 1024)]
+    wr = [(1, "k_copy(const u32x4*, u32x4*, long)", "WRITE_SIZE", gib / 1024)]
+    for d in range(2, 2 + 44):
+        fe.append((d, conv1, "FETCH_SIZE", 50e6 / 1024))       # reads 100 MB after the x2 scale
+        wr.append((d, conv1, "WRITE_SIZE", 10e6 / 1024))
+    _counter_csv(tmp_path / "f" / "run_counter_collection.csv", fe)
+    _counter_csv(tmp_path / "w" / "run_counter_collection.csv", wr)
+    out = bench.traffic_summary(str(tmp_path / "f"), str(tmp_path / "w"), passes=1)
+    assert "FETCH_SIZE scale 2.000, WRITE_SIZE scale 1.000" in out
+    assert "traffic_per_launch[conv1] = 110000000" in out
+    assert "| conv1 | 44 | 100.00 | 10.00 | 110.00 |" in out
+
+
+def test_mfma_summary_weights_and_issued_ops(tmp_path):
+    conv2 = "void k_conv2<32, 8, 1, 2>(D8sConv2Args, int, int)"
+    rows = []
+    # two dispatches: 10 % busy over 100 cycles, 40 % busy over 300 cycles -> 32.5 % weighted
+    for d, util, gui in ((1, 10.0, 100.0), (2, 40.0, 300.0)):
+        rows += [(d, conv2, "MfmaUtil", util), (d, conv2, "GRBM_GUI_ACTIVE", gui),
+                 (d, conv2, "SQ_INSTS_VALU_MFMA_MOPS_I8", 1e6), (d, conv2, "SQ_INSTS_VALU_MFMA_MOPS_F16", 0.0)]
+    _counter_csv(tmp_path / "m" / "run_counter_collection.csv", rows)
+    out = bench.mfma_summary(str(tmp_path / "m"), passes=1)
+    line = next(ln for ln in out.splitlines() if ln.startswith("| conv2 |"))
+    cells = [c.strip() for c in line.strip("|").split("|")]
+    assert cells[1] == "2" and cells[2] == "32.5"
+    assert float(cells[3]) == pytest.approx(2e6 * 512 / 1e9, abs=0.05)
+
+
+def test_more_than_one_gpu_is_refused():
+    env = dict(os.environ, PYTHONPATH=str(ROOT))
+    r = subprocess.run([sys.executable, str(ROOT / "bench.py"), "--gpus", "2"], capture_output=True,
+                       text=True, env=env, timeout=300, cwd=ROOT)
+    assert r.returncode == 2 and "one GPU" in r.stderr
