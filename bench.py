@@ -17,6 +17,8 @@ average launch time).
 `fp32_agreement`: max-abs, rel_l2 and minimum cosine of the configuration-4 study's INT8 features (and
 of a seeded 1664 -> 8 linear head's logits) against the fp32 DenseNet169 forward of the same weights
 (the package's `densenet` module in float32 on the GPU), with the reference's gate.
+`reference_study`: ms per study at the reference's own headline shape (88 images at 288 px, one
+encoder, graph replay) beside the 34 ms the reference quotes for it on one T4.
 `prep`: the upstream preparation (raw uint16 crops -> the uint8 volume of a study, `d8s_prep`) on the
 same GPU, studies/s with the payloads resident in HBM.
 One JSON line on stdout.
@@ -747,6 +749,32 @@ def main() -> None:
                       "slices": SLICES, "gate": "rel_l2 <= 1.05 x 0.067, cos_min >= 0.99"}
     log(f"fp32 agreement {fp32_agreement}")
 
+    # the reference's own headline shape: one study of 88 images at 288 px through one encoder (graph
+    # replay), which the reference quotes at 34 ms on one T4 (kaggle/int8_pack/pack_dense8s.py:29-30)
+    ref_model = densenet.seeded_densenet169(0).to(dev)
+    with torch.no_grad():
+        cal288 = dense8s.calibrate(ref_model, [synthetic.normalise(torch.from_numpy(c).to(dev))
+                                               for c in np.split(synthetic.study_u8(32, 288, seed=8), 4)])
+    enc288 = dense8s.Dense8SEncoder(dense8s.make_pack(dense8s.make_plan(ref_model.cpu(), cal288, 288), 88,
+                                                      input_kind="u8"), dev.index or 0, 88)
+    del ref_model
+    x288 = torch.from_numpy(synthetic.study_u8(88, 288, seed=4321)).to(dev)
+    enc288.capture(88)
+    for _ in range(3):
+        enc288(x288)
+    torch.cuda.synchronize()
+    lat288 = []
+    for _ in range(max(args.steps, 5)):
+        ta = time.perf_counter()
+        enc288(x288)
+        torch.cuda.synchronize()
+        lat288.append(time.perf_counter() - ta)
+    ref_study = {"workload": "the reference's study shape: 88 images at 288 px, one encoder, HIP graph replay",
+                 "ms_per_study": round(float(np.median(lat288)) * 1e3, 3),
+                 "reference_ms_per_study": 34.0, "reference_hardware": "1 x T4 (published, not this metric)"}
+    log(f"reference study shape: {ref_study}")
+    del enc288
+
     # per-family kernel times: each family's launches of a pass in a HIP graph, replayed between
     # HIP events on the encoder's stream
     fam = encs[0].time_families(studies[0], reps=args.prof_reps, flip="tta")
@@ -775,6 +803,7 @@ def main() -> None:
         "study_latency_ms": round(study_ms, 3),
         "study_latency_config": "C4: one 24-slice study, batch 24, one encoder, HIP graph replay",
         "fp32_agreement": fp32_agreement,
+        "reference_study": ref_study,
         "step_schedule": "serial (one stream)" if args.serial else "the 2 seeds' passes on 2 streams",
         "pass_ms_kernels": round(pass_ms, 3),
         "pass_hbm_frac": round(total_bytes / (pass_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),

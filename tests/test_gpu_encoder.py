@@ -187,3 +187,33 @@ def test_fused_blocks_same_bytes(dev, study512):
     for bad in ({4: "tile"}, {0: "img"}, {1: "fast"}):
         with pytest.raises(ValueError):
             dense8s.Dense8SEncoder(study512["pack"], dev.index or 0, 24, fused=bad)
+
+
+def test_encoder288_reference_study(dev):
+    """The reference's own study shape (kaggle/int8_pack/pack_dense8s.py:29-30: 88 images at 288 px,
+    maps 72, 36, 18, 9 with ragged tiles everywhere): every launch exact against the oracle on sampled
+    pixels of its own inputs, the stem within 1 LSB, final features exact, a call equal to the trace."""
+    model = densenet.seeded_densenet169(0).to(dev)
+    cal_x = synthetic.study_u8(32, 288, seed=8)
+    cal = dense8s.calibrate(model, [synthetic.normalise(torch.from_numpy(c).to(dev))
+                                    for c in np.split(cal_x, 4)])
+    plan = dense8s.make_plan(model.cpu(), cal, 288)
+    enc = dense8s.Dense8SEncoder(dense8s.make_pack(plan, 88, input_kind="u8"), dev.index or 0, 88)
+    x = synthetic.study_u8(88, 288, seed=4321)
+    xd = torch.from_numpy(x).to(dev)
+    print("encoder 288 px, 88 images", flush=True)
+    trace, f = enc.trace(xd)
+    feats = f.cpu().numpy()
+    par = dense8s.kernel_params(plan)
+    res = checks.summarize(checks.check_trace(enc, trace, feats, par, max_rows=1024))
+    print(res)
+    for fam in ("conv1", "conv2", "dense", "trans"):
+        if fam in res:
+            assert res[fam]["mismatch"] == 0, (fam, res[fam])
+    assert res["final"]["equal"], res
+    lut = dense8s.input_lut([0.5] * 3, [0.25] * 3)
+    got0 = trace[(0, 0)].cpu().numpy().astype(np.int8)
+    want0 = checks.stem_reference(x[:2], 1, lut, False, par["S_w16"], par["S_bias"], par["S_inv"])
+    st = checks.bytes_cmp(got0[:2], want0)
+    assert st["max_diff"] <= 1 and st["mismatch_frac"] < 1e-3, st
+    assert np.array_equal(enc(xd).cpu().numpy(), feats)
