@@ -1783,7 +1783,16 @@ __global__ __launch_bounds__(256) void k_final(const int8_t* __restrict__ in0, i
         const int8_t* base = g < G0 ? in0 + ((int64_t)n * G0 + g) * HW * 32
                                     : seg + ((int64_t)(g - G0) * N + n) * HW * 32;
         const float2 p = ((const float2*)ab)[g * 32 + cc];
-        for (int s = qp; s < HW; s += 4)
+        // 8 pixels' bytes loaded before they are added (in order), so 8 loads are in flight
+        int s = qp;
+        for (; s + 28 < HW; s += 32) {
+            int8_t q[8];
+#pragma unroll
+            for (int k = 0; k < 8; ++k) q[k] = base[(int64_t)(s + 4 * k) * 32 + cc];
+#pragma unroll
+            for (int k = 0; k < 8; ++k) acc += __builtin_fmaxf(__builtin_fmaf(p.x, (float)q[k], p.y), 0.0f);
+        }
+        for (; s < HW; s += 4)
             acc += __builtin_fmaxf(__builtin_fmaf(p.x, (float)base[(int64_t)s * 32 + cc], p.y), 0.0f);
     }
     part[qp][c64] = acc;
