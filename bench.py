@@ -507,7 +507,7 @@ def bench_head(dev: torch.device, b: int = 8, w: int = 88, reps: int = 50, with_
     head = hd.KneeHead(sd, dev)
     z = torch.randn((b, w, 1664), generator=g).to(dev)
     slot_of = (torch.arange(w) // 11) % 8
-    mask = torch.ones((b, 8), dtype=torch.bool)
+    mask = torch.ones((b, 8), dtype=torch.bool).to(dev)    # every input resident on the device
     for _ in range(5):
         head(z, slot_of, mask)
     torch.cuda.synchronize()
@@ -531,7 +531,7 @@ def bench_head(dev: torch.device, b: int = 8, w: int = 88, reps: int = 50, with_
         from oracle import head as oh
         torch.set_num_threads(1)
         t = time.perf_counter()
-        oh.head_forward(sd, z[:1].cpu(), slot_of, mask[:1])
+        oh.head_forward(sd, z[:1].cpu(), slot_of, mask[:1].cpu())
         c = time.perf_counter() - t
         out["cpu_baseline"] = {"value": round(1.0 / c, 2), "unit": "studies/s", "cores": 1, "kind": "port",
                                "sample": f"one study of {w} windows through oracle/head.py (torch fp32, 1 thread)"}
