@@ -208,7 +208,10 @@ def payloads_to_uint8(payloads: list, spec: PrepSpec, device,
     uint8 1-D, `resc` float64 (m, 2), `meta` int64 (n, N_META)), as `payloads_to_uint8_torch`."""
     device = torch.device(device)
     img, n_seq = spec.img, spec.n_seq
-    vol = torch.zeros((len(payloads), *spec.shape), dtype=torch.uint8, device=device)
+    # every byte of a slot that has a series is written (the kernels write the read slices and zero
+    # the others; CPU series are copied), so only slots without a series are cleared
+    vol = torch.empty((len(payloads), *spec.shape), dtype=torch.uint8, device=device)
+    filled: set = set()
     stacks: list[dict] = []
     keep: list = []                 # device copies referenced by the launches
     for b, payload in enumerate(payloads):
@@ -225,6 +228,7 @@ def payloads_to_uint8(payloads: list, spec: PrepSpec, device,
             j, k_sl = int(row[M_SLOT]), int(row[M_K])
             if k_sl != spec.slices:
                 raise ValueError(f"series with {k_sl} slices in a spec of {spec.slices}")
+            filled.update((b, j + k * n_seq) for k in range(spec.n_scales))
             if row[M_MODE] == MODE_GPU:
                 hr, wr, off = int(row[M_HR]), int(row[M_WR]), int(row[M_RAW_OFF])
                 if off < 0 or off + k_sl * hr * wr > raw.numel():
@@ -247,6 +251,10 @@ def payloads_to_uint8(payloads: list, spec: PrepSpec, device,
                 off, n = int(row[M_U8_OFF]), k_sl * img * img
                 for k in range(spec.n_scales):
                     vol[b, j + k * n_seq] = u8[off + k * n: off + (k + 1) * n].view(k_sl, img, img)
+    for b in range(len(payloads)):
+        for slot in range(spec.shape[0]):
+            if (b, slot) not in filled:
+                vol[b, slot].zero_()
     if stacks:
         _run("d8s_prep", 0, img, stacks, device)
     return vol

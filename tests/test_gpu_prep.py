@@ -170,3 +170,22 @@ def test_payload_full_study(dev):
     want = P.payload_to_uint8(pay, img, 4, 2, K, read_slices=(0, 23))
     for s in range(8):
         assert np.array_equal(got[s], want[s]), (s, int((got[s] != want[s]).sum()))
+
+
+def test_payload_missing_series_slots_are_zero(dev):
+    """A study without one of its series: that series' slots (both crop scales) are all zeros even
+    when the volume's memory held other bytes before, the others equal the oracle's chain."""
+    img, K = 64, 6
+    pay = synthetic.study_payload(img, K, 31, series=_series(True))
+    pay = dict(pay)
+    pay["meta"] = np.delete(np.asarray(pay["meta"]), 2, axis=0)        # drop series 2
+    spec = hp.PrepSpec(img=img, slices=K, n_seq=4, n_scales=2)
+    junk = torch.full((1, *spec.shape), 77, dtype=torch.uint8, device=dev)
+    del junk                                                            # its block is reused next
+    got = hp.payloads_to_uint8([pay], spec, dev).cpu().numpy()[0]
+    want = P.payload_to_uint8(pay, img, 4, 2, K)
+    slots = {int(r[0]) for r in pay["meta"]}
+    assert 2 not in slots
+    for s in range(8):
+        assert np.array_equal(got[s], want[s]), (s, int((got[s] != want[s]).sum()))
+    assert not got[2].any() and not got[6].any()
