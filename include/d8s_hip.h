@@ -276,8 +276,8 @@ int d8s_prep_resize(const D8sPrepArgs* a, void* stream);
  *   kind 1: src uint8 volume [B][SK][H][W], slice_idx int64 [M], lut fp16 [256] (u / 255):
  *           out[b * M + m] = sample(lut[src[b][slice_idx[m]]]), N = B * M (the fused gather); with
  *           grid = 0 the gather alone, out = lut[...] (the identity view).  slice_idx is read on the
- *           device and not checked (a check would synchronise): an index outside 0 .. SK-1 reads
- *           nothing and its images are zeros; callers validate the indices once.
+ *           device and not checked (a check would synchronise): an index outside 0 .. SK-1 is clamped
+ *           into it (reads stay inside the volume); callers validate the indices once.
  * Arithmetic: that of torch's grid_sampler_2d kernel in float32 (source index
  * fma(g + 1, size, -1) / 2, weights (x_se - x)(y_se - y) ..., taps accumulated by fma in the order
  * nw, ne, sw, se, out of range taps skipped), rounded once to fp16. */

@@ -785,12 +785,13 @@ __global__ void __launch_bounds__(NT) k_grid_sample(D8sGridArgs a) {
     const int n0 = blockIdx.y * GIMG, n1 = min(n0 + GIMG, a.N);
     if (p >= HW) return;
     // the image n: its source plane
-    // (a slice index outside 0 .. SK-1 gives -1: nothing of it is read, its image is zeros)
+    // (a slice index outside 0 .. SK-1 is clamped into it, so every read stays inside the volume)
     auto plane = [&](int n) -> int64_t {
         if constexpr (KIND >= 1) {
             const int b = n / a.M, m = n - b * a.M;
-            const int64_t si = ((const int64_t*)a.slice_idx)[m];
-            return (uint64_t)si < (uint64_t)a.SK ? ((int64_t)b * a.SK + si) * HW : (int64_t)-1;
+            int64_t si = ((const int64_t*)a.slice_idx)[m];
+            si = si < 0 ? 0 : si >= a.SK ? (int64_t)a.SK - 1 : si;
+            return ((int64_t)b * a.SK + si) * HW;
         } else {
             return (int64_t)n * HW;
         }
@@ -800,19 +801,13 @@ __global__ void __launch_bounds__(NT) k_grid_sample(D8sGridArgs a) {
     int64_t pl[GIMG];
 #pragma unroll
     for (int i = 0; i < GIMG; ++i) pl[i] = plane(min(n0 + i, n1 - 1));
-    bool live[GIMG];
-#pragma unroll
-    for (int i = 0; i < GIMG; ++i) {
-        live[i] = pl[i] >= 0;
-        pl[i] = live[i] ? pl[i] : 0;
-    }
     if constexpr (KIND == 2) {
         uint8_t v[GIMG];
 #pragma unroll
         for (int i = 0; i < GIMG; ++i) v[i] = ((const uint8_t*)a.src)[pl[i] + p];
 #pragma unroll
         for (int i = 0; i < GIMG; ++i)
-            if (n0 + i < n1) ((uint16_t*)a.out)[(int64_t)(n0 + i) * HW + p] = live[i] ? s_lut[v[i]] : (uint16_t)0;
+            if (n0 + i < n1) ((uint16_t*)a.out)[(int64_t)(n0 + i) * HW + p] = s_lut[v[i]];
         return;
     } else {
         const __half2 g = ((const __half2*)a.grid)[p];
@@ -850,7 +845,7 @@ __global__ void __launch_bounds__(NT) k_grid_sample(D8sGridArgs a) {
                     acc = __builtin_fmaf(x, w[t], acc);
                 }
             }
-            if (n0 + i < n1) ((__half*)a.out)[(int64_t)(n0 + i) * HW + p] = __float2half_rn(live[i] ? acc : 0.0f);
+            if (n0 + i < n1) ((__half*)a.out)[(int64_t)(n0 + i) * HW + p] = __float2half_rn(acc);
         }
     }
 }

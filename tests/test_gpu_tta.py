@@ -92,8 +92,8 @@ def test_lut_is_u_over_255():
 @pytest.mark.parametrize("view", [(1.0, 0.0, 0.0), (1.10, 0.0, 0.0)])
 def test_windows_u8_slice_checks(dev, view):
     """The slice indices are checked once per tensor and in-place version: a valid in-place change is
-    seen, an index outside the volume raises; through the C ABI (no host check) such an index reads
-    nothing and its images are zeros."""
+    seen, an index outside the volume raises; through the C ABI (no host check) such an index is
+    clamped into the volume."""
     import ctypes
     from rsna_knee_efficiency_amd import hip
     b, s, k, h, w = 1, 2, 5, 32, 40
@@ -115,10 +115,7 @@ def test_windows_u8_slice_checks(dev, view):
                         grid=gp, out=out2.data_ptr(), kind=1, N=6, H=h, W=w, B=1, SK=s * k, M=6)
     hip.call("d8s_grid_sample", ctypes.byref(args), ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream))
     torch.cuda.synchronize(dev)
-    good = torch.tensor([0, 0, 2, 0, 8, 9], dtype=torch.int64, device=dev)
+    clamped = torch.tensor([0, 0, 2, 9, 8, 9], dtype=torch.int64, device=dev)
     ref = torch.empty_like(out2)
-    tta.windows_u8(v, good, ref, *view)
-    flat, rflat = out2.view(6, h, w), ref.view(6, h, w)
-    assert not flat[1].any() and not flat[3].any()
-    for i in (0, 2, 4, 5):
-        assert torch.equal(flat[i], rflat[i]), i
+    tta.windows_u8(v, clamped, ref, *view)
+    assert torch.equal(out2, ref)
