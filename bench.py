@@ -6,17 +6,22 @@ slices/s on 1 MI355X; 24-slice study latency in ms).
 Workload (`value`): configuration 5, sustained throughput.  A step = one synthetic study: 2 seeded
 DenseNet169 weight sets x 2 crops x 24 slices of 3 x 512 x 512 uint8 with flip TTA = one pass of 96
 encoded images per seed (48 slices + their mirrors, the flip fused in the stem), i.e. 192 encoded
-slices per step.  Inputs are resident in HBM (4 distinct studies, cycled); each encoder call replays
-its HIP graph.  value = 192 K / T slices/s.
+slices per step.  Inputs are resident in HBM: 50 distinct seeded studies (`synthetic.c5_study`, seeds
+1234..1283), step k encoding study k mod 50; each encoder call replays its HIP graph.
+value = 192 K / T slices/s.  `c5_all_studies`: the 50 studies once each, back to back.
 `study_latency_ms`: configuration 4, one 24-slice study through one encoder (batch 24, one pass).
 The two seeds' passes of a step run from two streams (`--serial`: one after the other).
 `roofline`: the dominant kernel family: its launches of a configuration-5 pass recorded R times in a HIP
 graph and replayed between HIP events on the encoder's stream (algorithmic bytes of a launch / the
 average launch time).
-`cpu_baseline`: the float32 DenseNet169 forward (`oracle/fp32.py`) at batch 1 on the host cores.
+`cpu_baseline`: the float32 DenseNet169 forward (`oracle/fp32.py`) on the host cores at batch 1
+(slices/s) and at batch 24 (one study, `study_latency_ms`).
+`mfma_probe`: the int8 MFMA rate measured on the GPU (`d8s_micro_mfma`), beside the 5.0 POP/s datasheet
+figure; `family_int8_frac_of_measured_peak` quotes each family's int8 rate against it.
 `fp32_agreement`: max-abs, rel_l2 and minimum cosine of the configuration-4 study's INT8 features (and
 of a seeded 1664 -> 8 linear head's logits) against the fp32 DenseNet169 forward of the same weights
-(the package's `densenet` module in float32 on the GPU), with the reference's gate.
+(the package's `densenet` module in float32 on the GPU), with the reference's gate; under "c5" the
+same for configuration 5's outputs (study 0, both seeds, plain and mirrored images).
 `reference_study`: ms per study at the reference's own headline shape (88 images at 288 px, one
 encoder, graph replay) beside the 34 ms the reference quotes for it on one T4.
 `prep`: the upstream preparation (raw uint16 crops -> the uint8 volume of a study, `d8s_prep`) on the
@@ -54,6 +59,7 @@ HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, published
 I8_PEAK_TOPS = 5000.0          # MI355X dense int8 MFMA, published
 IMG = 512
 SLICES = 24
+C5_STUDIES = 50                 # configuration 5 streams over 50 synthetic studies
 
 
 def log(msg: str) -> None:
@@ -69,6 +75,14 @@ def build_encoder(seed: int, nb: int, dev: torch.device) -> tuple[dense8s.Dense8
     plan = dense8s.make_plan(model.cpu(), cal, IMG)
     enc = dense8s.Dense8SEncoder(dense8s.make_pack(plan, nb, input_kind="u8"), dev.index or 0, nb)
     return enc, plan
+
+
+def agree(a: np.ndarray, b: np.ndarray) -> dict:
+    """max-abs, rel_l2 and the minimum per-row cosine of a against b."""
+    cos = (a * b).sum(1) / np.maximum(np.linalg.norm(a, axis=1) * np.linalg.norm(b, axis=1), 1e-30)
+    return {"max_abs": round(float(np.abs(a - b).max()), 5),
+            "rel_l2": round(float(np.linalg.norm(a - b) / max(np.linalg.norm(b), 1e-30)), 5),
+            "cos_min": round(float(cos.min()), 6)}
 
 
 def kernel_bytes(meta: dict, n: int, kinds: dict | None = None) -> dict[str, list[float]]:
@@ -336,14 +350,17 @@ def committed_traffic(family: str) -> int | None:
     return None
 
 
-def cpu_baseline(reps: int = 5, warmup: int = 2) -> dict:
+def cpu_baseline(reps: int = 5, warmup: int = 2, study_reps: int = 3) -> dict:
+    """The float32 DenseNet169 forward (`oracle/fp32.py`) on the host cores: batch 1 (slices/s, the
+    `value`) and one 24-slice study at batch 24 (`study_latency_ms`, configuration 4's shape)."""
     from oracle import fp32
     cores = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
     cores = min(cores or 1, int(os.environ.get("OMP_NUM_THREADS", cores or 1)))
     torch.set_num_threads(cores)
     model = densenet.seeded_densenet169(0)
     sd = model.state_dict()
-    x = synthetic.normalise(torch.from_numpy(synthetic.study_u8(1, IMG, seed=1234)))
+    study = torch.from_numpy(synthetic.c5_study(0)[:SLICES])
+    x = synthetic.normalise(study[:1])
     for _ in range(warmup):
         fp32.forward(sd, x)
     ts = []
@@ -352,6 +369,14 @@ def cpu_baseline(reps: int = 5, warmup: int = 2) -> dict:
         fp32.forward(sd, x)
         ts.append(time.perf_counter() - t)
     med = float(np.median(ts))
+    xs = synthetic.normalise(study)
+    fp32.forward(sd, xs)
+    tb = []
+    for _ in range(study_reps):
+        t = time.perf_counter()
+        fp32.forward(sd, xs)
+        tb.append(time.perf_counter() - t)
+    med24 = float(np.median(tb))
     cpu = platform.processor() or ""
     try:
         for line in Path("/proc/cpuinfo").read_text().splitlines():
@@ -361,8 +386,38 @@ def cpu_baseline(reps: int = 5, warmup: int = 2) -> dict:
     except OSError:
         pass
     return {"value": round(1.0 / med, 4), "unit": "slices/s", "cores": cores, "kind": "port",
-            "sample": f"fp32 DenseNet169 forward (oracle/fp32.py), batch 1, 512 px, {warmup} warm-up + "
-                      f"{reps} timed, median {med * 1e3:.0f} ms; CPU {cpu}"}
+            "study_latency_ms": round(med24 * 1e3, 1),
+            "study_slices_per_s": round(SLICES / med24, 3),
+            "sample": f"fp32 DenseNet169 forward (oracle/fp32.py) at 512 px: batch 1, {warmup} warm-up + "
+                      f"{reps} timed, median {med * 1e3:.0f} ms; batch {SLICES} (one study), 1 warm-up + "
+                      f"{study_reps} timed, median {med24 * 1e3:.0f} ms; CPU {cpu}"}
+
+
+def mfma_probe(dev: torch.device, blocks: int = 2048, iters: int = 4096, reps: int = 3) -> dict:
+    """Measured int8 MFMA rate: `d8s_micro_mfma` (every wave issues independent
+    v_mfma_i32_32x32x32_i8 back to back, 4 waves per workgroup, 8 workgroups per CU) between HIP
+    events on the current stream; the ceiling the MFMA fractions are also quoted against."""
+    import ctypes
+    from rsna_knee_efficiency_amd import hip
+    sink = torch.zeros(blocks, dtype=torch.int32, device=dev)
+    st = torch.cuda.current_stream(dev).cuda_stream
+    launch = lambda: hip.call("d8s_micro_mfma", blocks, iters, ctypes.c_void_p(sink.data_ptr()),  # noqa: E731
+                              ctypes.c_void_p(st))
+    launch()
+    torch.cuda.synchronize(dev)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        launch()
+    e1.record()
+    torch.cuda.synchronize(dev)
+    ms = e0.elapsed_time(e1) / reps
+    ops = blocks * 4 * iters * 4 * (32 * 32 * 32 * 2)
+    tops = ops / (ms * 1e-3) / 1e12
+    return {"i8_tops": round(tops, 1), "datasheet_i8_tops": I8_PEAK_TOPS,
+            "frac_of_datasheet": round(tops / I8_PEAK_TOPS, 4), "ms": round(ms, 4),
+            "sample": f"{blocks} workgroups x 4 waves x {iters} rounds of 4 independent "
+                      f"v_mfma_i32_32x32x32_i8"}
 
 
 PREP_READ_SLICES = (0, 23)      # the final submission's KNEE_READ_SLICES (raw_crop.py:71-76)
@@ -666,8 +721,7 @@ def main() -> None:
     nb = 4 * SLICES                                     # 2 crops x 24 slices x flip
     if args.pmc_passes:
         enc = build_encoder(0, nb, dev)[0]
-        x = torch.from_numpy(np.concatenate([synthetic.study_u8(SLICES, IMG, seed=1234 + c)
-                                             for c in range(2)])).to(dev)
+        x = torch.from_numpy(synthetic.c5_study(0)).to(dev)
         fam = family_times(enc, x, args.pmc_passes - 1, "tta") if args.pmc_passes > 1 else {}
         if args.pmc_passes == 1:
             enc(x, flip="tta")
@@ -680,13 +734,12 @@ def main() -> None:
             res["copy_probe"] = copy_probe(dev, reps=1)
         print(json.dumps(res))
         return
-    encs = [build_encoder(seed, nb, dev)[0] for seed in (0, 1)]
+    built = [build_encoder(seed, nb, dev) for seed in (0, 1)]
+    encs = [e for e, _ in built]
     log(f"encoders built in {time.perf_counter() - t0:.1f} s")
-    # 4 distinct studies resident in HBM: each 2 crops x 24 slices (uint8)
-    studies = []
-    for s in range(4):
-        crops = [synthetic.study_u8(SLICES, IMG, seed=1234 + 2 * s + c) for c in range(2)]
-        studies.append(torch.from_numpy(np.concatenate(crops)).to(dev))
+    # the 50 distinct studies of configuration 5 resident in HBM: each 2 crops x 24 slices (uint8)
+    studies = [torch.from_numpy(synthetic.c5_study(s)).to(dev) for s in range(C5_STUDIES)]
+    log(f"{len(studies)} studies generated and resident ({time.perf_counter() - t0:.1f} s)")
     for e in encs:
         e.capture(2 * SLICES, flip="tta")
     torch.cuda.synchronize()
@@ -713,6 +766,33 @@ def main() -> None:
     per_step = 2 * nb
     value = per_step * args.steps / dt
     log(f"config 5: {args.steps} studies in {dt:.3f} s: {value:.1f} slices/s")
+    # every one of the 50 studies once, back to back (beside the K timed steps)
+    torch.cuda.synchronize()
+    t = time.perf_counter()
+    for k in range(len(studies)):
+        step(k)
+    torch.cuda.synchronize()
+    dt50 = time.perf_counter() - t
+    sweep = {"studies": len(studies), "ms_per_study": round(dt50 / len(studies) * 1e3, 3),
+             "slices_per_s": round(per_step * len(studies) / dt50, 2)}
+    log(f"config 5 over all {len(studies)} studies once: {sweep}")
+    # agreement of configuration 5's outputs (study 0, both seeds, 48 plain + 48 mirrored encoded
+    # images) with the fp32 DenseNet169 forward of the same weights on the plain and mirrored images
+    hw, hb = synthetic.linear_head(1664, 8, seed=99)
+    c5_agree = {}
+    for seed, e in zip((0, 1), encs):
+        got = e(studies[0], flip="tta").double().cpu().numpy()
+        m = densenet.seeded_densenet169(seed).to(dev).eval()
+        refs = []
+        with torch.no_grad():
+            for src in (studies[0], torch.flip(studies[0], dims=[-1])):
+                for chunk in src.split(16):
+                    refs.append(m(synthetic.normalise(chunk.contiguous())).double().cpu())
+        del m
+        ref = torch.cat(refs).numpy()
+        c5_agree[f"seed{seed}"] = {"features": agree(got, ref),
+                                   "logits": agree(got @ hw.T + hb, ref @ hw.T + hb)}
+    log(f"config 5 fp32 agreement {c5_agree}")
 
     # configuration 4: one 24-slice study, batch 24, one encoder
     enc4, _ = build_encoder(0, SLICES, dev)
@@ -737,16 +817,9 @@ def main() -> None:
         ref4 = model4(synthetic.normalise(x4)).double().cpu().numpy()
     got4 = enc4(x4).double().cpu().numpy()
     del model4
-    hw, hb = synthetic.linear_head(1664, 8, seed=99)
-
-    def agree(a: np.ndarray, b: np.ndarray) -> dict:
-        cos = (a * b).sum(1) / np.maximum(np.linalg.norm(a, axis=1) * np.linalg.norm(b, axis=1), 1e-30)
-        return {"max_abs": round(float(np.abs(a - b).max()), 5),
-                "rel_l2": round(float(np.linalg.norm(a - b) / max(np.linalg.norm(b), 1e-30)), 5),
-                "cos_min": round(float(cos.min()), 6)}
-
     fp32_agreement = {"features": agree(got4, ref4), "logits": agree(got4 @ hw.T + hb, ref4 @ hw.T + hb),
-                      "slices": SLICES, "gate": "rel_l2 <= 1.05 x 0.067, cos_min >= 0.99"}
+                      "slices": SLICES, "gate": "rel_l2 <= 1.05 x 0.067, cos_min >= 0.99",
+                      "c5": dict(c5_agree, images="study 0: 48 plain + 48 mirrored, per seed")}
     log(f"fp32 agreement {fp32_agreement}")
 
     # the reference's own headline shape: one study of 88 images at 288 px through one encoder (graph
@@ -798,8 +871,11 @@ def main() -> None:
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "i8",
         "data": "synthetic (seeded uint8 slice stacks, seeded DenseNet169 weights)",
         "config": {"workload": "C5 sustained: per step one study = 2 seeds x (2 crops x 24 slices "
-                               "+ flip TTA) = 2 passes of 96 encoded 512px slices",
-                   "global_batch": nb, "seeds": 2, "image": IMG, "parallelism": "none (1 GPU)"},
+                               "+ flip TTA) = 2 passes of 96 encoded 512px slices; step k encodes "
+                               "study k mod 50 of 50 distinct resident studies",
+                   "global_batch": nb, "seeds": 2, "image": IMG, "studies": len(studies),
+                   "parallelism": "none (1 GPU)"},
+        "c5_all_studies": sweep,
         "study_latency_ms": round(study_ms, 3),
         "study_latency_config": "C4: one 24-slice study, batch 24, one encoder, HIP graph replay",
         "fp32_agreement": fp32_agreement,
@@ -822,6 +898,10 @@ def main() -> None:
     log(f"prep: {pr['value']} studies/s, {pr['gpu_ms_per_study']} ms GPU per study")
     out["head"] = bench_head(dev)
     log(f"head: {out['head']['value']} studies/s")
+    out["mfma_probe"] = mfma_probe(dev)
+    log(f"mfma probe: {out['mfma_probe']}")
+    out["family_int8_frac_of_measured_peak"] = {
+        k: round(v / out["mfma_probe"]["i8_tops"], 4) for k, v in fam_tops.items()}
     if args.copy_probe:
         out["copy_probe"] = copy_probe(dev)
         log(f"copy probe: {out['copy_probe']}")

@@ -223,35 +223,49 @@ def stem_reference(x: np.ndarray, kind: int, lut, flip: bool, w16, bias, inv) ->
 
 
 # --- whole encoder ----------------------------------------------------------------------------
-def store_q(trace: dict, bi: int, upto: int) -> np.ndarray:
-    """The traced store of block bi, segments 0..upto, as q [N][C][HW] int8."""
-    t = torch.cat([trace[(bi, j)] for j in range(upto + 1)], 1)
-    n, c, h, w = t.shape
-    return t.reshape(n, c, h * w).cpu().numpy().astype(np.int8)
+def _i8(t) -> np.ndarray:
+    """A traced tensor of integer values as int8 numpy (converted on its device first)."""
+    return t.to(torch.int8).cpu().numpy() if isinstance(t, torch.Tensor) else np.asarray(t, np.int8)
+
+
+def block_store(trace: dict, bi: int, L: int, n: int, g0: int, hw: int) -> tuple[np.ndarray, np.ndarray]:
+    """The traced store of block bi in the kernels' layout: in0 [n][g0][hw][32] and seg [L][n][hw][32]
+    (at least one slot), each segment converted once."""
+    x0 = _i8(trace[(bi, 0)]).reshape(n, g0, 32, hw)
+    in0 = np.ascontiguousarray(x0.transpose(0, 1, 3, 2))
+    if L == 0:
+        return in0, np.zeros((1, n, hw, 32), np.int8)
+    seg = np.empty((L, n, hw, 32), np.int8)
+    for j in range(L):
+        seg[j] = _i8(trace[(bi, j + 1)]).reshape(n, 32, hw).transpose(0, 2, 1)
+    return in0, seg
 
 
 def check_trace(enc, trace: dict, feats: np.ndarray, par: dict, max_rows: int | None = 2048,
                 seed: int = 0) -> dict:
     """Every layer of a traced pass against the C oracle, each on the kernels' OWN inputs (so a
     difference cannot propagate; as the reference's `unit_fused`, pack_dense8s.py:323-359).  Rows are
-    sampled (`max_rows` per launch, None = all).  Returns the worst byte comparison per kind."""
+    sampled (`max_rows` per launch, None = all).  Returns the byte comparison of every launch per
+    family: "conv1" / "conv2" (two launches per layer, the bottleneck traced), "dense" (a fused layer,
+    no bottleneck in memory), "block" (a layer of a whole-block launch, `enc.fused[b] == "img"`),
+    "trans", and "final" (features equal or not)."""
     rng = np.random.default_rng(seed)
     meta = enc.meta
     n = enc.nb
-    worst = {"conv1": [], "conv2": [], "dense": [], "trans": [], "final": None}
+    kinds = getattr(enc, "fused", {}) or {}
+    worst = {"conv1": [], "conv2": [], "dense": [], "block": [], "trans": [], "final": None}
 
     def pick(m):
         if max_rows is None or m <= max_rows:
             return np.arange(m, dtype=np.int64)
         return np.unique(np.concatenate([rng.choice(m, max_rows, replace=False), [0, m - 1]]))
 
-    derived = dense8s.derived_params(meta, par)
     for bi, b in enumerate(meta["blocks"]):
         h, w = b["h"], b["w"]
         hw, g0 = h * w, b["c0"] // 32
+        in0, seg = block_store(trace, bi, b["L"], n, g0, hw)
         for li in range(b["L"]):
-            q = store_q(trace, bi, li)
-            in0, seg = cases.store_from_q(q, g0)
+            got_seg = seg[li]                                            # [n][hw][32]
             if ("bott", bi, li) not in trace:
                 # fused layer: the oracle's bottleneck on the 3x3 neighbourhoods of sampled pixels,
                 # then its conv2 on them
@@ -264,38 +278,34 @@ def check_trace(enc, trace: dict, feats: np.ndarray, par: dict, max_rows: int | 
                 planar = np.ascontiguousarray(rows.reshape(-1, 4, 32).transpose(1, 0, 2))
                 _, want2 = lib.conv2(planar, n, h, w, par[f"L{bi}_{li}_w2k"], par[f"L{bi}_{li}_c2u"],
                                      sel2)
-                seg_out = trace[(bi, li + 1)].cpu().numpy().astype(np.int8)
-                got2 = seg_out.reshape(n, 32, hw).transpose(0, 2, 1).reshape(n * hw, 32)[sel2]
-                worst["dense"].append(bytes_cmp(got2, want2))
+                fam = "block" if kinds.get(bi) == "img" else "dense"
+                worst[fam].append(bytes_cmp(got_seg.reshape(n * hw, 32)[sel2], want2))
                 continue
             sel = pick(n * hw)
             _, want = lib.conv1(in0, seg, g0, g0 + li, n, hw, par[f"L{bi}_{li}_abh"],
                                 par[f"L{bi}_{li}_w1"], par[f"L{bi}_{li}_gdu"], sel)
-            bott = trace[("bott", bi, li)].cpu().numpy()                 # [n][128][h][w] uint8
+            bott = trace[("bott", bi, li)]
+            bott = (bott.cpu().numpy() if isinstance(bott, torch.Tensor) else np.asarray(bott))
+            bott = bott.astype(np.uint8).reshape(n, 4, 32, hw)                # [n][plane][32][hw]
             got = bott.reshape(n, 128, hw).transpose(0, 2, 1).reshape(n * hw, 128)[sel]
             worst["conv1"].append(bytes_cmp(got, want))
-            planar = np.ascontiguousarray(bott.reshape(n, 4, 32, hw).transpose(1, 0, 3, 2))
+            planar = np.ascontiguousarray(bott.transpose(1, 0, 3, 2))
             sel2 = pick(n * hw)
             _, want2 = lib.conv2(planar.reshape(4, -1, 32), n, h, w, par[f"L{bi}_{li}_w2k"],
                                  par[f"L{bi}_{li}_c2u"], sel2)
-            seg_out = trace[(bi, li + 1)].cpu().numpy().astype(np.int8)   # [n][32][h][w]
-            got2 = seg_out.reshape(n, 32, hw).transpose(0, 2, 1).reshape(n * hw, 32)[sel2]
-            worst["conv2"].append(bytes_cmp(got2, want2))
-        q = store_q(trace, bi, b["L"])
-        in0, seg = cases.store_from_q(q, g0)
+            worst["conv2"].append(bytes_cmp(got_seg.reshape(n * hw, 32)[sel2], want2))
         if b["trans"]:
             cout = (b["c0"] + 32 * b["L"]) // 2
             selt = pick(n * hw // 4)
             _, want = lib.trans(in0, seg, g0, g0 + b["L"], n, hw, w, par[f"T{bi}_abh"],
                                 par[f"T{bi}_w"], par[f"T{bi}_gdf"], cout, selt)
-            nxt = trace[(bi + 1, 0)].cpu().numpy().astype(np.int8)        # [n][cout][h/2][w/2]
+            nxt = _i8(trace[(bi + 1, 0)])                                 # [n][cout][h/2][w/2]
             got = nxt.reshape(n, cout, hw // 4).transpose(0, 2, 1).reshape(-1, cout)[selt]
             worst["trans"].append(bytes_cmp(got, want))
         else:
             want = lib.final(in0, g0, seg, n, hw, par["F_ab"], b["c0"] + 32 * b["L"])
             worst["final"] = {"max_abs": float(np.abs(feats[:n] - want).max()),
                               "equal": bool(np.array_equal(feats[:n], want))}
-    del derived
     return worst
 
 
@@ -315,7 +325,7 @@ def neighbourhoods(sel: np.ndarray, h: int, w: int) -> np.ndarray:
 
 def summarize(worst: dict) -> dict:
     out = {}
-    for k in ("conv1", "conv2", "dense", "trans"):
+    for k in ("conv1", "conv2", "dense", "block", "trans"):
         v = worst[k]
         out[k] = {"launches": len(v), "mismatch": sum(x["mismatch"] for x in v),
                   "max_diff": max((x["max_diff"] for x in v), default=0)}
@@ -356,11 +366,57 @@ def smoke_check(device: str = "cuda:0") -> dict:
         np.arange(3)[None, :, None, None], x])
     ref = emu.emulate(plan, xf, par, stem_kind="f16").numpy()
     res["vs_emulate"] = feat_cmp(feats, ref)
-    ok = (res["conv1"]["mismatch"] == 0 and res["conv2"]["mismatch"] == 0
-          and res["trans"]["mismatch"] == 0 and res["final"]["equal"]
+    return smoke_gate(res)
+
+
+def smoke_gate(res: dict) -> dict:
+    """The pass/fail rule of `smoke_check`: no byte of any checked launch family differs (conv1,
+    conv2, the fused layers, the whole-block layers and the transitions), at least one layer and one
+    transition were checked, the final features
+    are equal, the stem within 1 LSB on < 1e-3 of its bytes, a plain call equals the trace, and the
+    features are within rel_l2 1e-2 of the float64 emulation.  Raises AssertionError otherwise."""
+    fams = ("conv1", "conv2", "dense", "block", "trans")
+    ok = (all(res[k]["mismatch"] == 0 for k in fams)
+          and sum(res[k]["launches"] for k in ("conv1", "dense", "block")) > 0
+          and res["trans"]["launches"] > 0
+          and res["final"]["equal"]
           and res["stem"]["max_diff"] <= 1 and res["stem"]["mismatch_frac"] < 1e-3
           and res["call_vs_trace"] and res["vs_emulate"]["rel_l2"] < 1e-2)
     res["ok"] = ok
     if not ok:
         raise AssertionError(f"smoke check failed: {res}")
     return res
+
+
+def oracle_trace(meta: dict, par: dict, stem_q: np.ndarray, n: int) -> tuple[dict, np.ndarray]:
+    """A whole pass computed by the C oracle alone, in the format of `Dense8SEncoder.trace` for
+    fused layers (no bottleneck entries): {(block, 0): block input, (block, l + 1): layer l's 32
+    channels} as float tensors (n, c, h, w) of integers, and the final features (n, C).  `stem_q` is
+    block 0's input q [n, c0, h, w] int8.  Every pixel of every layer is computed: tiny maps only."""
+    out: dict = {}
+    cur = np.asarray(stem_q, np.int8)
+    feats = None
+    for bi, b in enumerate(meta["blocks"]):
+        h, w = b["h"], b["w"]
+        hw, g0 = h * w, b["c0"] // 32
+        out[(bi, 0)] = torch.from_numpy(cur.astype(np.float32))
+        q = cur.reshape(n, -1, hw)
+        rows = np.arange(n * hw, dtype=np.int64)
+        for li in range(b["L"]):
+            in0, seg = cases.store_from_q(q, g0)
+            _, v = lib.conv1(in0, seg, g0, g0 + li, n, hw, par[f"L{bi}_{li}_abh"],
+                             par[f"L{bi}_{li}_w1"], par[f"L{bi}_{li}_gdu"], rows)
+            planar = np.ascontiguousarray(v.reshape(-1, 4, 32).transpose(1, 0, 2))
+            _, q2 = lib.conv2(planar, n, h, w, par[f"L{bi}_{li}_w2k"], par[f"L{bi}_{li}_c2u"], rows)
+            new = q2.reshape(n, hw, 32).transpose(0, 2, 1)                  # [n][32][hw]
+            out[(bi, li + 1)] = torch.from_numpy(new.reshape(n, 32, h, w).astype(np.float32))
+            q = np.concatenate([q, new], 1)
+        in0, seg = cases.store_from_q(q, g0)
+        if b["trans"]:
+            cout = (b["c0"] + 32 * b["L"]) // 2
+            _, t = lib.trans(in0, seg, g0, g0 + b["L"], n, hw, w, par[f"T{bi}_abh"], par[f"T{bi}_w"],
+                             par[f"T{bi}_gdf"], cout, np.arange(n * hw // 4, dtype=np.int64))
+            cur = t.reshape(n, hw // 4, cout).transpose(0, 2, 1).reshape(n, cout, h // 2, w // 2)
+        else:
+            feats = lib.final(in0, g0, seg, n, hw, par["F_ab"], b["c0"] + 32 * b["L"])
+    return out, feats

@@ -823,6 +823,7 @@ class Dense8SEncoder:
                 self._enqueue(x.contiguous(), mode)
                 self.calls["plain"] += 1
             res = self._result(n, mode)
+        hip.written(self.out)
         cur.wait_stream(self.stream)
         return res
 

@@ -17,6 +17,8 @@ import hashlib
 import threading
 from pathlib import Path
 
+import torch
+
 PKG = Path(__file__).resolve().parent
 CSRC = PKG / "csrc"
 SOURCE = CSRC / "d8s_kernels.hip"
@@ -203,3 +205,12 @@ def check(rc: int, what: str) -> None:
 def call(name: str, *args) -> None:
     """Calls entry point `name` and raises D8sError on a non-zero status."""
     check(getattr(library(), name)(*args), name)
+
+
+def written(*tensors) -> None:
+    """Marks tensors a kernel wrote through a raw pointer as modified: bumps their version counter
+    (shared with their base and views), as an in-place torch op would, so a later consumer that
+    keys on (storage, version) sees new contents."""
+    for t in tensors:
+        if t is not None:
+            torch.autograd.graph.increment_version(t)

@@ -14,7 +14,8 @@ The host side of the reference's GPU preparation, same names and meaning:
   and the flips;
 - `ranks(n)`                       `torch_uint8._ranks` (torch_uint8.py:31-42).
 Every stack of a call runs through one `d8s_prep` launch sequence (up to 16 stacks per call): the
-resized float32 values are recomputed from the uint16 region in each pass instead of being stored.
+resize runs once per stack, into a float32 scratch buffer together with the first histogram pass,
+and the later passes (the other two radix levels and the uint8 write) read the stored values.
 There is no CPU path: without the library the calls raise.
 """
 from __future__ import annotations
@@ -167,6 +168,7 @@ def to_uint8_hist_batch(x: torch.Tensor, out: torch.Tensor | None = None) -> tor
     stacks = [dict(src=x.data_ptr() + 4 * r * per, out=out.data_ptr() + r * per, K=K, k0=0, k1=K,
                    flip=FLIP_NONE, **_rank_fields(per)) for r in range(R)]
     _run("d8s_prep", 1, img, stacks, x.device)
+    hip.written(out)
     return out
 
 
@@ -199,6 +201,7 @@ def resize(region: torch.Tensor, resc: torch.Tensor | None, box, img: int,
     s = _region_stack(region, resc, box, k_range)
     s["out"] = out.data_ptr()
     _run("d8s_prep_resize", 0, img, [s], region.device)
+    hip.written(out)
     return out
 
 
@@ -257,4 +260,5 @@ def payloads_to_uint8(payloads: list, spec: PrepSpec, device,
                 vol[b, slot].zero_()
     if stacks:
         _run("d8s_prep", 0, img, stacks, device)
+        hip.written(vol)
     return vol

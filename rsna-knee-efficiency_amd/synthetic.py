@@ -4,6 +4,7 @@
   slices (stack i = slices i, i+1, i+2, the reference's 3-slice windows, `src/knee/models/baseline.py:
   154-164`): a smooth low-frequency field of Gaussian blobs drifting from slice to slice, plus uniform
   noise.
+- `c5_study(s)`: study s of configuration 5 (two crops of 24 stacks, seeded 1234 + s).
 - `normalise(u8)`: x = (u / 255 - mean) / std as float32 (mean 0.5, std 0.25): the float model's input;
   the INT8 encoder applies the same map in its stem through an fp16 table.
 - `linear_head(c_in, c_out, seed)`: the 1664 -> 8 head of configuration 4 (float64 weights, bias).
@@ -22,23 +23,33 @@ import torch
 MEAN, STD = 0.5, 0.25
 
 
-def study_u8(n: int, img: int, seed: int, blobs: int = 12) -> np.ndarray:
+def study_u8(n: int, img: int, seed, blobs: int = 12) -> np.ndarray:
     rng = np.random.default_rng(seed)
-    yy, xx = np.meshgrid(np.arange(img) / img, np.arange(img) / img, indexing="ij")
+    t = np.arange(img) / img
     cy, cx = rng.uniform(0, 1, blobs), rng.uniform(0, 1, blobs)
     sig = rng.uniform(0.05, 0.25, blobs)
     amp = rng.uniform(-1, 1, blobs)
     drift = rng.uniform(-0.01, 0.01, (blobs, 2))
     vol = np.empty((n + 2, img, img), np.uint8)
     for z in range(n + 2):
-        field = np.zeros((img, img))
-        for k in range(blobs):
-            d2 = (yy - cy[k] - z * drift[k, 0]) ** 2 + (xx - cx[k] - z * drift[k, 1]) ** 2
-            field += amp[k] * np.exp(-d2 / (2 * sig[k] ** 2))
+        # each blob is separable: amp exp(-dy^2 / 2 s^2) exp(-dx^2 / 2 s^2), one outer product
+        gy = amp[:, None] * np.exp(-(t[None, :] - (cy + z * drift[:, 0])[:, None]) ** 2
+                                   / (2 * sig[:, None] ** 2))
+        gx = np.exp(-(t[None, :] - (cx + z * drift[:, 1])[:, None]) ** 2 / (2 * sig[:, None] ** 2))
+        field = gy.T @ gx
         field /= max(np.abs(field).max(), 1e-9)
         s = 128 + 90 * field + rng.uniform(-40, 40, (img, img))
         vol[z] = np.clip(np.rint(s), 0, 255).astype(np.uint8)
     return np.ascontiguousarray(np.stack([vol[i:i + 3] for i in range(n)]))
+
+
+C5_SEED0 = 1234                 # configuration 5's studies are seeded 1234, 1235, ...
+
+
+def c5_study(s: int, img: int = 512, slices: int = 24) -> np.ndarray:
+    """Study `s` of configuration 5: its two crops (110 mm, 150 mm, both at img) of `slices` stacks
+    each, (2 slices, 3, img, img) uint8, crop c seeded (C5_SEED0 + s, c)."""
+    return np.concatenate([study_u8(slices, img, seed=[C5_SEED0 + s, c]) for c in range(2)])
 
 
 def normalise(u8: torch.Tensor, mean: float = MEAN, std: float = STD) -> torch.Tensor:

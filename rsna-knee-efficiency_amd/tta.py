@@ -65,6 +65,7 @@ def affine_windows(w: torch.Tensor, scale: float = 1.0, tx: float = 0.0, ty: flo
     a = hip.GridArgs(src=x.data_ptr(), grid=g.data_ptr(), out=out.data_ptr(), kind=0,
                      N=b * k * d, H=h, W=wd)
     _sample(a, w.device)
+    hip.written(out)
     return out
 
 
@@ -105,4 +106,5 @@ def windows_u8(v_u8: torch.Tensor, slice_idx: torch.Tensor, out: torch.Tensor, s
     a = hip.GridArgs(src=v_u8.data_ptr(), slice_idx=idx.data_ptr(), lut=lut_u8_f16(v_u8.device).data_ptr(),
                      grid=gp, out=out.data_ptr(), kind=1, N=b * m, H=h, W=w, B=b, SK=s * k, M=m)
     _sample(a, v_u8.device)
+    hip.written(out)
     return out

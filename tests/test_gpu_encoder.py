@@ -51,10 +51,12 @@ def test_encoder512_layers_exact(dev, study512):
     res = checks.summarize(checks.check_trace(enc, trace, feats, par, max_rows=1024))
     print(res)
     blocks = study512["pack"]["meta"]["blocks"]
-    n_fused = sum(blocks[bi]["L"] for bi, kind in enc.fused.items() if kind != "conv")
-    assert res["conv1"]["mismatch"] == 0 and res["conv1"]["launches"] == 82 - n_fused, res
-    assert res["conv2"]["mismatch"] == 0 and res["conv2"]["launches"] == 82 - n_fused, res
-    assert res["dense"]["mismatch"] == 0 and res["dense"]["launches"] == n_fused, res
+    n_of = {k: sum(blocks[bi]["L"] for bi, kind in enc.fused.items() if kind == k)
+            for k in ("conv", "tile", "img")}
+    assert res["conv1"]["mismatch"] == 0 and res["conv1"]["launches"] == n_of["conv"], res
+    assert res["conv2"]["mismatch"] == 0 and res["conv2"]["launches"] == n_of["conv"], res
+    assert res["dense"]["mismatch"] == 0 and res["dense"]["launches"] == n_of["tile"], res
+    assert res["block"]["mismatch"] == 0 and res["block"]["launches"] == n_of["img"], res
     assert res["trans"]["mismatch"] == 0 and res["trans"]["launches"] == 3, res
     assert res["final"]["equal"], res
     lut = dense8s.input_lut([0.5] * 3, [0.25] * 3)
@@ -207,7 +209,7 @@ def test_encoder288_reference_study(dev):
     par = dense8s.kernel_params(plan)
     res = checks.summarize(checks.check_trace(enc, trace, feats, par, max_rows=1024))
     print(res)
-    for fam in ("conv1", "conv2", "dense", "trans"):
+    for fam in ("conv1", "conv2", "dense", "block", "trans"):
         if fam in res:
             assert res[fam]["mismatch"] == 0, (fam, res[fam])
     assert res["final"]["equal"], res
@@ -217,3 +219,97 @@ def test_encoder288_reference_study(dev):
     st = checks.bytes_cmp(got0[:2], want0)
     assert st["max_diff"] <= 1 and st["mismatch_frac"] < 1e-3, st
     assert np.array_equal(enc(xd).cpu().numpy(), feats)
+
+
+# --- configuration 5, as bench.py measures it ----------------------------------------------------
+C5_NB = 96                      # 2 crops x 24 slices x flip-TTA per pass
+
+
+@pytest.fixture(scope="module")
+def c5(dev):
+    """The bench's configuration-5 encoders: seeded DenseNet169 weights 0 and 1, calibration over 64
+    seeded slices (seed 7), packages of 96 images per pass with uint8 input; study 0's two crops of
+    24 slices (`synthetic.c5_study(0)`) as the 48 input images of a flip-TTA pass."""
+    torch.backends.cudnn.allow_tf32 = False
+    torch.backends.cuda.matmul.allow_tf32 = False
+    cal_x = synthetic.study_u8(64, 512, seed=7)
+    out = {"enc": [], "plan": [], "sd": []}
+    for seed in (0, 1):
+        model = densenet.seeded_densenet169(seed).to(dev)
+        cal = dense8s.calibrate(model, [synthetic.normalise(torch.from_numpy(c).to(dev))
+                                        for c in np.split(cal_x, 8)])
+        plan = dense8s.make_plan(model.cpu(), cal, 512)
+        out["plan"].append(plan)
+        out["sd"].append({k: v.clone() for k, v in model.state_dict().items()})
+        out["enc"].append(dense8s.Dense8SEncoder(dense8s.make_pack(plan, C5_NB, input_kind="u8"),
+                                                 dev.index or 0, C5_NB))
+    x = synthetic.c5_study(0)
+    out["x"], out["xd"] = x, torch.from_numpy(x).to(dev)
+    return out
+
+
+@pytest.mark.parametrize("seed", [0, 1])
+def test_encoder512_c5_layers_exact(dev, c5, seed):
+    """One flip-TTA pass (48 inputs, 96 encoded images) traced: every launch of the 82 layers and the 3
+    transitions exact against the C oracle on 1024 sampled pixels of its own inputs, the final
+    features exact, the stem within 1 LSB on plain and mirrored images."""
+    enc = c5["enc"][seed]
+    print(f"C5 trace, seed {seed}, nb {enc.nb}, blocks {enc.fused}", flush=True)
+    trace, f = enc.trace(c5["xd"], flip="tta")
+    feats = f.cpu().numpy()
+    par = dense8s.kernel_params(c5["plan"][seed])
+    res = checks.summarize(checks.check_trace(enc, trace, feats, par, max_rows=1024, seed=seed))
+    print({k: (v["launches"], v["mismatch"]) if "launches" in v else v for k, v in res.items()})
+    assert enc.fused == {0: "tile", 1: "conv", 2: "conv", 3: "img"}, enc.fused
+    want = {"conv1": 44, "conv2": 44, "dense": 6, "block": 32, "trans": 3}
+    for fam, k in want.items():
+        assert res[fam]["launches"] == k and res[fam]["mismatch"] == 0, (fam, res[fam])
+    assert res["final"]["equal"], res["final"]
+    lut = dense8s.input_lut([0.5] * 3, [0.25] * 3)
+    got0 = trace[(0, 0)].cpu().numpy().astype(np.int8)
+    for idx, flip in (([0, 47], False), ([48, 95], True)):
+        src = c5["x"][[0, 47]]
+        want0 = checks.stem_reference(src, 1, lut, flip, par["S_w16"], par["S_bias"], par["S_inv"])
+        st = checks.bytes_cmp(got0[idx], want0)
+        assert st["max_diff"] <= 1 and st["mismatch_frac"] < 1e-3, (flip, st)
+    assert np.array_equal(enc(c5["xd"], flip="tta").cpu().numpy(), feats)
+
+
+def test_encoder512_c5_vs_fp32(dev, c5):
+    """Both seeds' 96 features of a flip-TTA pass (48 plain, 48 mirrored) and the logits of a seeded
+    1664 -> 8 head against the fp32 DenseNet169 forward of the same weights on the plain and mirrored
+    images: rel_l2 <= 1.05 x 0.067 and cosine >= 0.99 for both."""
+    xd = c5["xd"]
+    head_w, head_b = synthetic.linear_head(1664, 8, seed=99)
+    for seed in (0, 1):
+        feats = c5["enc"][seed](xd, flip="tta").cpu().numpy().astype(np.float64)
+        sd = {k: v.to(dev) for k, v in c5["sd"][seed].items()}
+        refs = []
+        with torch.no_grad():
+            for src in (xd, torch.flip(xd, dims=[-1])):
+                for chunk in src.split(16):
+                    refs.append(fp32.forward(sd, synthetic.normalise(chunk.contiguous())).cpu())
+        ref = torch.cat(refs).numpy().astype(np.float64)
+        c = checks.feat_cmp(feats, ref)
+        lg = checks.feat_cmp(feats @ head_w.T + head_b, ref @ head_w.T + head_b)
+        print({"seed": seed, "features": c, "logits": lg})
+        assert c["rel_l2"] <= 1.05 * 0.067 and c["cos_min"] >= 0.99, (seed, c)
+        assert lg["rel_l2"] <= 1.05 * 0.067 and lg["cos_min"] >= 0.99, (seed, lg)
+
+
+def test_encoder512_c5_concurrent_graphs(dev, c5):
+    """bench.py's step: both seeds' flip-TTA passes from two streams (`encode_concurrent`) replaying
+    their graphs, three times with eager work between, equal to each runner's eager call."""
+    xd = c5["xd"]
+    encs = c5["enc"]
+    want = [e(xd, flip="tta").clone() for e in encs]
+    for e in encs:
+        e.capture(48, flip="tta")
+    for k in range(3):
+        outs = dense8s.encode_concurrent([(e, xd, "tta") for e in encs])
+        got = [o.clone() for o in outs]
+        _ = (xd.float() * 2).sum()
+        torch.cuda.synchronize(dev)
+        for s in (0, 1):
+            assert torch.equal(got[s], want[s]), (k, s)
+    assert all(e.calls["graph"] >= 3 for e in encs)

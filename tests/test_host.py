@@ -150,3 +150,19 @@ def test_calibrate_keys():
     assert set(cal) == want
     assert len(cal["seg0.0"]) == 64 and len(cal["conv2.1.2"]) == 32 and len(cal["seg0.1"]) == 64
     assert all(v >= 0 for v in cal["seg0.0"]) and cal["in1.0.0"] > 0
+
+
+def test_written_bumps_versions():
+    """A buffer a kernel writes through a raw pointer gets a new version (base and views share it),
+    so the encoder's graph-input key sees new contents in a reused output buffer."""
+    buf = torch.zeros((4, 3, 8, 8), dtype=torch.uint8)
+    view = buf[1:3]
+    _, key0 = dense8s._src_key(view)
+    v0 = buf._version
+    hip.written(view)
+    assert buf._version == v0 + 1 and view._version == buf._version
+    _, key1 = dense8s._src_key(view)
+    assert key1 != key0
+    with torch.inference_mode():
+        t = torch.zeros(3)
+        hip.written(t, None)                     # inference tensors and None are accepted
