@@ -332,6 +332,17 @@ typedef struct D8sHeadArgs {
 int d8s_head_workspace(const D8sHeadArgs* a, uint64_t* bytes);
 int d8s_head(const D8sHeadArgs* a, void* stream);
 
+/* d8s_head without a workspace argument and without any allocation: no counterpart in the reference;
+ * for callers that cannot allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  Same arguments and results as d8s_head; a->workspace and
+ * a->ws_bytes are ignored.  The workspace is a static device array of D8S_HEAD_SCRATCH_BYTES per GPU
+ * (32 MiB: up to 16 studies of 128 windows, or 23 of 88, at the final configuration), held until the
+ * process ends; a call whose d8s_head_workspace() exceeds it is rejected with hipErrorInvalidValue.
+ * `stream` must belong to the current device.  Every call on a GPU uses that GPU's one array, so calls
+ * that overlap on one GPU (unordered streams) race: order them on one stream or with events. */
+#define D8S_HEAD_SCRATCH_BYTES (32u << 20)
+int d8s_head_noalloc(const D8sHeadArgs* a, void* stream);
+
 /* Library identification: "d8s-hip <abi> <source hash> gfx950". */
 const char* d8s_version(void);
 

@@ -28,6 +28,7 @@
 #include <stdint.h>
 
 #include <algorithm>
+#include <mutex>
 #include <string>
 
 #include "d8s_hip.h"
@@ -549,11 +550,13 @@ extern "C" int d8s_head_workspace(const D8sHeadArgs* a, uint64_t* bytes) {
     return 0;
 }
 
-extern "C" int d8s_head(const D8sHeadArgs* a, void* stream) {
-    const char* what = "d8s_head";
+namespace {
+
+// Checks the arguments (everything but the workspace) and returns the workspace layout's size.
+int head_check(const D8sHeadArgs* a, const char* what) {
     HREQ(a != nullptr, "null arguments");
     HREQ(a->z && a->slot_of && a->slot_mask && a->slot_emb && a->attn_w && a->attn_b && a->cls_w &&
-         a->cls_b && a->logits && a->workspace, "null pointer");
+         a->cls_b && a->logits, "null pointer");
     HREQ(a->B >= 1 && a->B < 65536, "B must be 1 .. 65535");
     HREQ(a->W >= 1 && a->W <= WMAX, "W must be 1 .. 128 windows per study");
     HREQ(a->D >= 1 && a->S >= 1 && a->T >= 1 && a->T <= TMAX, "bad D, S or T (T <= 16)");
@@ -566,9 +569,12 @@ extern "C" int d8s_head(const D8sHeadArgs* a, void* stream) {
         HREQ(a->FF >= 1 && a->PER >= 1, "bad FF or PER");
     }
     HREQ((int64_t)a->B * a->W * a->D < (1ll << 31), "too many values");
-    const Ws w = carve(a, (char*)a->workspace);
-    HREQ(a->ws_bytes >= w.bytes, "workspace smaller than d8s_head_workspace()");
-    hipStream_t st = (hipStream_t)stream;
+    return 0;
+}
+
+// The launch sequence of the head over the workspace `ws` (laid out by carve).
+void head_run(const D8sHeadArgs* a, char* ws, hipStream_t st) {
+    const Ws w = carve(a, ws);
     const int M = a->B * a->W;
     const int nblk = (a->D + TN - 1) / TN;
     k_head_valid<<<(M + NT - 1) / NT, NT, 0, st>>>(a->slot_mask, a->slot_of, w.valid, a->B, a->W, a->S);
@@ -618,5 +624,68 @@ extern "C" int d8s_head(const D8sHeadArgs* a, void* stream) {
     k_head_dotsum<<<(unsigned)((nsum + NT - 1) / NT), NT, 0, st>>>(w.part, a->attn_b, w.sums, M, a->T, nblk);
     PoolP pp{w.sums, w.valid, a->cls_b, a->logits, a->W, a->T};
     k_head_pool<<<a->B, NT, 0, st>>>(pp);
-    return d8s_host_launched("d8s_head");
+}
+
+}  // namespace
+
+extern "C" int d8s_head(const D8sHeadArgs* a, void* stream) {
+    const char* what = "d8s_head";
+    if (int rc = head_check(a, what)) return rc;
+    HREQ(a->workspace, "null workspace");
+    HREQ(a->ws_bytes >= carve(a, nullptr).bytes, "workspace smaller than d8s_head_workspace()");
+    head_run(a, (char*)a->workspace, (hipStream_t)stream);
+    return d8s_host_launched(what);
+}
+
+// ---- the entry point that allocates nothing -------------------------------------------------------
+// Its workspace is this array, one copy per GPU, held until the process ends.  Host code never uses
+// the array's name as an address (on the host it is a stand-in, not device memory): the device
+// address of each GPU's copy comes from hipGetSymbolAddress, looked up once per device with that
+// device current, and is what the kernels receive.  Every call on a GPU shares that GPU's copy, so
+// calls that overlap on one GPU (different streams, no ordering between them) race.
+static __device__ __align__(256) unsigned char scratch[D8S_HEAD_SCRATCH_BYTES];
+
+namespace {
+
+constexpr int MAX_DEVICES = 64;
+std::mutex g_scratch_mu;
+void* g_scratch[MAX_DEVICES] = {};
+
+// The device address of the current device's scratch; `stream` must belong to that device.
+int scratch_ptr(hipStream_t stream, void** out, const char* what) {
+    int dev = -1;
+    hipError_t e = hipGetDevice(&dev);
+    HREQ(e == hipSuccess, std::string("hipGetDevice: ") + hipGetErrorString(e));
+    HREQ(dev >= 0 && dev < MAX_DEVICES, "device ordinal out of range");
+    if (stream != nullptr) {
+        hipDevice_t sdev = -1;
+        e = hipStreamGetDevice(stream, &sdev);
+        HREQ(e == hipSuccess, std::string("hipStreamGetDevice: ") + hipGetErrorString(e));
+        HREQ(sdev == dev, "the stream belongs to another device than the current one");
+    }
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (g_scratch[dev] == nullptr) {
+        void* p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        HREQ(e == hipSuccess && p != nullptr,
+             std::string("hipGetSymbolAddress(scratch): ") + hipGetErrorString(e));
+        g_scratch[dev] = p;
+    }
+    *out = g_scratch[dev];
+    return 0;
+}
+
+}  // namespace
+
+extern "C" int d8s_head_noalloc(const D8sHeadArgs* a, void* stream) {
+    const char* what = "d8s_head_noalloc";
+    if (int rc = head_check(a, what)) return rc;
+    const uint64_t need = carve(a, nullptr).bytes;
+    HREQ(need <= D8S_HEAD_SCRATCH_BYTES,
+         "workspace of " + std::to_string(need) + " bytes exceeds the static scratch of " +
+             std::to_string((unsigned long long)D8S_HEAD_SCRATCH_BYTES) + " bytes (fewer studies per call)");
+    void* ws = nullptr;
+    if (int rc = scratch_ptr((hipStream_t)stream, &ws, what)) return rc;
+    head_run(a, (char*)ws, (hipStream_t)stream);
+    return d8s_host_launched(what);
 }

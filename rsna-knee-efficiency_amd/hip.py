@@ -145,6 +145,7 @@ SIGNATURES = {
     "d8s_grid_sample": [ctypes.POINTER(GridArgs), vp],
     "d8s_head_workspace": [ctypes.POINTER(HeadArgs), ctypes.POINTER(ctypes.c_uint64)],
     "d8s_head": [ctypes.POINTER(HeadArgs), vp],
+    "d8s_head_noalloc": [ctypes.POINTER(HeadArgs), vp],
     "d8s_micro_copy": [vp, vp, ctypes.c_size_t, vp],
     "d8s_micro_mfma": [i32, i32, vp, vp],
     "d8s_probe_mfma_i8": [vp, vp, vp, vp],
