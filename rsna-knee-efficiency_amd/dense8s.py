@@ -4,9 +4,11 @@ Host side of the reference's `src/knee/dense8s.py` (interface `Dense8SEncoder`, 
 arithmetic on the HIP kernels of `libd8s_hip.so` (`hip.py`, C ABI `include/d8s_hip.h`):
 
 - `calibrate(encoder, batches)`: per-channel maxima of every store segment and per-tensor maxima of
-  every conv input, by forward hooks (`dense8s.py:272-318`);
+  every conv input, by walking the float network (`observe`) with the maxima kept on the device
+  (the role of `dense8s.py:272-318`);
 - `make_plan(encoder, cal, img)`: BatchNorm as affines, int8 weights per output channel with the sign
-  of norm2 folded into conv1, scales (`dense8s.py:374-433`, `dense8.py:176-188`);
+  of norm2 folded into conv1 (`fold_norm2`), scales; one helper per layer and per transition (the
+  role of `dense8s.py:374-433`, with the arithmetic of `dense8.py:176-188`);
 - `kernel_params(plan)`: the kernel tables, float64 expressions cast once to float32 / fp16
   (`dense8s.py:436-519`); `derived_params` adds the tables only this build's kernels use;
 - `pack_meta` / `save_pack` / `load_pack`: the `.npz` package (format 1, kind "dense8s",
@@ -35,6 +37,7 @@ from pathlib import Path
 
 import numpy as np
 import torch
+import torch.nn.functional as F
 
 from . import hip
 
@@ -49,50 +52,82 @@ STEM_C = 64
 
 
 # --- calibration ----------------------------------------------------------------------------
-@torch.no_grad()
+class RunningMax:
+    """Maxima of |x| over the calibration batches, kept on the tensors' device until `result()` (one
+    host transfer in all, not one per layer and batch): per channel for what goes into the store (a
+    block input, a layer's 32 new channels: their int8 scales sigma_c), per tensor for what a conv
+    reads (its u8 scale).  The maximum is exact in any order, so the values do not depend on the
+    batching."""
+
+    def __init__(self) -> None:
+        self.channel: dict[str, torch.Tensor] = {}
+        self.tensor: dict[str, torch.Tensor] = {}
+
+    @staticmethod
+    def _merge(table: dict, key: str, m: torch.Tensor) -> None:
+        old = table.get(key)
+        table[key] = m if old is None else torch.maximum(old, m)
+
+    def per_channel(self, key: str, y: torch.Tensor) -> None:
+        self._merge(self.channel, key, y.detach().float().abs().amax(dim=(0, 2, 3)))
+
+    def per_tensor(self, key: str, y: torch.Tensor) -> None:
+        self._merge(self.tensor, key, y.detach().float().abs().amax())
+
+    def result(self) -> dict:
+        out: dict = {k: v.cpu().double().numpy().tolist() for k, v in self.channel.items()}
+        out.update({k: float(v.cpu()) for k, v in self.tensor.items()})
+        return out
+
+
+def dense_stages(features) -> list[tuple]:
+    """(dense block, the transition after it or None) in network order, from the timm / torchvision
+    child names `denseblock{k}` / `transition{k}` of `features`."""
+    kids = dict(features.named_children())
+    stages = []
+    while f"denseblock{len(stages) + 1}" in kids:
+        k = len(stages) + 1
+        stages.append((kids[f"denseblock{k}"], kids.get(f"transition{k}")))
+    return stages
+
+
+def observe(features, x: torch.Tensor, rec: RunningMax) -> None:
+    """The float forward of `features` on x, recording at the points where the INT8 path quantises:
+    `seg0.{b}` block b's input (pool0 / the transition's pooled output, per channel), `conv2.{b}.{l}`
+    layer l's new channels (per channel), and per tensor the conv inputs `in1.{b}.{l}` (after norm1 +
+    ReLU), `in2.{b}.{l}` (after norm2 + ReLU) and `tin.{b}` (the transition's after its norm + ReLU).
+    It calls the modules a `densenet.DenseNet` forward calls, in the same order, so the recorded
+    values are the float model's own; the ReLU is applied as a function, which also suits norms that
+    already include their activation (applying it twice changes nothing)."""
+    y = features.pool0(F.relu(features.norm0(features.conv0(x))))
+    rec.per_channel("seg0.0", y)
+    for b, (block, trans) in enumerate(dense_stages(features)):
+        feats = [y]
+        for l, layer in enumerate(block.values()):
+            z = F.relu(layer.norm1(torch.cat(feats, 1)))
+            rec.per_tensor(f"in1.{b}.{l}", z)
+            z = F.relu(layer.norm2(layer.conv1(z)))
+            rec.per_tensor(f"in2.{b}.{l}", z)
+            feats.append(layer.conv2(z))
+            rec.per_channel(f"conv2.{b}.{l}", feats[-1])
+        y = torch.cat(feats, 1)
+        if trans is not None:
+            z = F.relu(trans.norm(y))
+            rec.per_tensor(f"tin.{b}", z)
+            y = trans.pool(trans.conv(z))
+            rec.per_channel(f"seg0.{b + 1}", y)
+
+
+@torch.inference_mode()
 def calibrate(encoder, batches) -> dict:
-    """Maxima over `batches` (tensors (N, in, H, W) on the device of the float encoder): per channel |x|
-    of every store segment (block inputs = pool0 / transition outputs, every conv2 output) and per
-    tensor the conv inputs.  Keys `seg0.{b}`, `conv2.{b}.{l}` (lists) and `in1.{b}.{l}`, `in2.{b}.{l}`,
-    `tin.{b}` (numbers), as `src/knee/dense8s.py:272-318`.
-    """
-    f = encoder.features
-    chan: dict[str, torch.Tensor] = {}
-    tens: dict[str, float] = {}
-    hooks = []
-
-    def per_channel(key):
-        def hook(_m, _inp, y):
-            v = y.detach().float().abs().amax(dim=(0, 2, 3))
-            chan[key] = v if key not in chan else torch.maximum(chan[key], v)
-        return hook
-
-    def per_tensor(key):
-        def hook(_m, inp):
-            tens[key] = max(tens.get(key, 0.0), float(inp[0].detach().float().abs().max()))
-        return hook
-
-    hooks.append(f.pool0.register_forward_hook(per_channel("seg0.0")))
-    b = 0
-    while hasattr(f, f"denseblock{b + 1}"):
-        for li, layer in enumerate(getattr(f, f"denseblock{b + 1}").values()):
-            hooks.append(layer.conv2.register_forward_hook(per_channel(f"conv2.{b}.{li}")))
-            hooks.append(layer.conv1.register_forward_pre_hook(per_tensor(f"in1.{b}.{li}")))
-            hooks.append(layer.conv2.register_forward_pre_hook(per_tensor(f"in2.{b}.{li}")))
-        if hasattr(f, f"transition{b + 1}"):
-            tr = getattr(f, f"transition{b + 1}")
-            hooks.append(tr.conv.register_forward_pre_hook(per_tensor(f"tin.{b}")))
-            hooks.append(tr.pool.register_forward_hook(per_channel(f"seg0.{b + 1}")))
-        b += 1
-    try:
-        for x in batches:
-            encoder(x)
-    finally:
-        for hk in hooks:
-            hk.remove()
-    out: dict = {k: v.cpu().numpy().astype(np.float64).tolist() for k, v in chan.items()}
-    out.update(tens)
-    return out
+    """The maxima the INT8 plan is scaled by, over `batches` (tensors (N, in, H, W) on the device of
+    the float encoder, a `densenet.DenseNet`): keys `seg0.{b}` and `conv2.{b}.{l}` (lists, one value
+    per channel), `in1.{b}.{l}`, `in2.{b}.{l}` and `tin.{b}` (numbers) -- the calibration dictionary
+    of the reference (`src/knee/dense8s.py:272-318`), computed by walking the network (`observe`)."""
+    rec = RunningMax()
+    for x in batches:
+        observe(encoder.features, x, rec)
+    return rec.result()
 
 
 # --- plan -----------------------------------------------------------------------------------
@@ -149,92 +184,110 @@ class SPlan:
 
 
 def bn_affine(bn) -> tuple[np.ndarray, np.ndarray]:
-    """BatchNorm in eval as y = s x + t (float64), `src/knee/dense8.py:176-179`."""
-    s = bn.weight.detach().double() / torch.sqrt(bn.running_var.detach().double() + bn.eps)
-    t = bn.bias.detach().double() - bn.running_mean.detach().double() * s
-    return s.cpu().numpy(), t.cpu().numpy()
+    """An eval-mode BatchNorm as y = s x + t per channel, in float64: s = gamma / sqrt(var + eps),
+    t = beta - mean s (`src/knee/dense8.py:176-179`)."""
+    as64 = lambda t: t.detach().to("cpu", torch.float64).numpy()  # noqa: E731
+    s = as64(bn.weight) / np.sqrt(as64(bn.running_var) + bn.eps)
+    return s, as64(bn.bias) - as64(bn.running_mean) * s
 
 
 def quant_weight(w: torch.Tensor) -> tuple[np.ndarray, np.ndarray]:
-    """int8 per output channel, scale = max|w| / 127, q = RNE(w / scale) in float32
-    (`src/knee/dense8.py:182-188`)."""
-    w = w.detach().float().cpu()
-    scale = w.abs().flatten(1).amax(1).clamp_min(1e-12) / QS
-    inv = (1.0 / scale).view(-1, *[1] * (w.dim() - 1))
-    q = torch.round(w * inv).clamp(-128, 127)
-    return q.to(torch.int8).numpy(), scale.numpy().astype(np.float32)
+    """Symmetric int8 per output channel in float32 arithmetic: scale = max(max|w|, 1e-12) / 127 per
+    row, q = RNE(w * (1 / scale)) clamped to int8 (`src/knee/dense8.py:182-188`).  Returns q (the
+    weight's shape) and the scales."""
+    w32 = w.detach().to("cpu", torch.float32).numpy()
+    rows = w32.reshape(w32.shape[0], -1)
+    scale = np.maximum(np.abs(rows).max(axis=1), np.float32(1e-12)) / np.float32(QS)
+    inv = (np.float32(1.0) / scale).astype(np.float32)
+    q = np.clip(np.rint(rows * inv[:, None]), -128, 127).astype(np.int8)
+    return q.reshape(w32.shape), scale.astype(np.float32)
 
 
 def store_scale(v, floor: float = 1e-6) -> np.ndarray:
-    """sigma = max(amax, floor) / 127 per channel (`src/knee/dense8s.py:374-375`)."""
+    """sigma = max(amax, floor) / 127 per channel: the store's int8 scale (`src/knee/dense8s.py:374-375`)."""
     return np.maximum(np.asarray(v, dtype=np.float64), floor) / QS
 
 
+def _input_scale(amax, levels: int) -> float:
+    """Scale of a conv input quantised to `levels` steps: max(amax, 1e-12) / levels."""
+    return max(float(amax), 1e-12) / levels
+
+
+def fold_norm2(q: np.ndarray, wscale: np.ndarray, g: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
+    """conv1's output goes through norm2, y = g acc + t, before its ReLU.  The epilogue wants a
+    positive factor, so each output row's sign of g moves into the row's weights (q_o -> -q_o where
+    g_o < 0) and |g_o| into the row scale (wscale_o |g_o|).  A channel with |g_o| < 1e-30 is dead: its
+    row is zeroed and keeps the bare weight scale.  q [cout, ...] int8, wscale [cout], g [cout]."""
+    dead = np.abs(g) < 1e-30
+    neg = g < 0
+    rows = q.reshape(q.shape[0], -1).astype(np.int16)
+    rows = np.where(neg[:, None], -rows, rows)
+    rows[dead] = 0
+    folded = rows.astype(np.int8)            # wraps like int8 arithmetic (|q| <= 127 in practice)
+    wscale64 = wscale.astype(np.float64)
+    return folded, np.where(dead, wscale64, wscale64 * np.abs(g))
+
+
+def layer_plan(layer, c_in: int, cal: dict, tag: str) -> SLayer:
+    """The plan of one dense layer (`tag` = "{block}.{layer}" in the calibration keys)."""
+    if not hasattr(layer.norm2, "running_var"):
+        raise ValueError(f"dense layer {tag}: norm2 has no running statistics (folded?): the "
+                         f"unfolded model is needed")
+    a1, b1 = bn_affine(layer.norm1)
+    g2, t2 = bn_affine(layer.norm2)
+    q1, ws1 = quant_weight(layer.conv1.weight)
+    w1, w1s = fold_norm2(q1, ws1, g2)
+    q2, ws2 = quant_weight(layer.conv2.weight)
+    return SLayer(c_in=c_in, a1=a1, b1=b1, s1=_input_scale(cal[f"in1.{tag}"], QU), w1=w1, w1s=w1s,
+                  bias1=t2, s2=_input_scale(cal[f"in2.{tag}"], QS), w2=q2,
+                  w2s=ws2.astype(np.float64), sig=store_scale(cal[f"conv2.{tag}"]))
+
+
+def transition_plan(blk: SBlock, trans, cal: dict, b: int) -> None:
+    """Fills the transition fields of `blk` from the transition module after block b."""
+    blk.ta, blk.tb = bn_affine(trans.norm)
+    q, ws = quant_weight(trans.conv.weight)
+    blk.tw, blk.tws = q.reshape(q.shape[0], -1), ws.astype(np.float64)
+    blk.ts = _input_scale(cal[f"tin.{b}"], QU)
+
+
 def make_plan(encoder, cal: dict, img: int) -> SPlan:
-    """The plan of `encoder` (a `densenet.DenseNet` in eval, BatchNorms not folded) with the maxima `cal`
-    of `calibrate` (`src/knee/dense8s.py:378-433`)."""
+    """The plan of `encoder` (a `densenet.DenseNet` in eval, BatchNorms not folded) at img x img with
+    the maxima `cal` of `calibrate`: the stem with norm0 folded into its weights, then per block its
+    layers (`layer_plan`) and transition (`transition_plan`); the block sides halve at each transition
+    (the role of `src/knee/dense8s.py:378-433`)."""
     f = encoder.features
-    a0, b0 = bn_affine(f.norm0)
-    w0 = f.conv0.weight.detach().double().cpu().numpy() * a0[:, None, None, None]
-    plan = SPlan(img=img, in_ch=int(f.conv0.weight.shape[1]), w0=w0.astype(np.float32),
-                 b0=b0.astype(np.float32))
-    h = w = img // 4
-    c = int(f.conv0.weight.shape[0])
-    sig0 = store_scale(cal["seg0.0"])
-    k = 1
-    while hasattr(f, f"denseblock{k}"):
-        bi = k - 1
-        layers = []
-        for li, layer in enumerate(getattr(f, f"denseblock{k}").values()):
-            if not hasattr(layer.norm2, "running_var"):
-                raise ValueError(f"denseblock{k}.denselayer{li + 1}: norm2 folded, the whole model "
-                                 f"is needed")
-            a1, b1 = bn_affine(layer.norm1)
-            a2, b2 = bn_affine(layer.norm2)
-            q1, s1w = quant_weight(layer.conv1.weight)
-            sign = np.where(a2 < 0, -1, 1).astype(np.int8)
-            mag = np.abs(a2)
-            dead = mag < 1e-30
-            q1 = (q1 * sign[:, None, None, None]).astype(np.int8)
-            q1[dead] = 0
-            w1s = np.where(dead, s1w, s1w * mag)
-            q2, s2w = quant_weight(layer.conv2.weight)
-            layers.append(SLayer(
-                c_in=c + GROWTH * li, a1=a1, b1=b1,
-                s1=max(float(cal[f"in1.{bi}.{li}"]), 1e-12) / QU,
-                w1=q1.reshape(BOTTLENECK, -1), w1s=w1s.astype(np.float64),
-                bias1=b2.astype(np.float64),
-                s2=max(float(cal[f"in2.{bi}.{li}"]), 1e-12) / QS, w2=q2,
-                w2s=s2w.astype(np.float64), sig=store_scale(cal[f"conv2.{bi}.{li}"])))
-        blk = SBlock(c0=c, h=h, w=w, sig0=sig0, layers=layers)
-        c = blk.c_tot
-        if hasattr(f, f"transition{k}"):
-            tr = getattr(f, f"transition{k}")
-            blk.ta, blk.tb = bn_affine(tr.norm)
-            tq, tsw = quant_weight(tr.conv.weight)
-            blk.ts = max(float(cal[f"tin.{bi}"]), 1e-12) / QU
-            blk.tw, blk.tws = tq.reshape(tq.shape[0], -1), tsw.astype(np.float64)
-            sig0 = store_scale(cal[f"seg0.{bi + 1}"])
-            c //= 2
-            h //= 2
-            w //= 2
+    s0, t0 = bn_affine(f.norm0)
+    conv0 = f.conv0.weight.detach().to("cpu", torch.float64).numpy()
+    plan = SPlan(img=img, in_ch=conv0.shape[1], w0=(conv0 * s0[:, None, None, None]).astype(np.float32),
+                 b0=t0.astype(np.float32))
+    width, side = conv0.shape[0], img // 4
+    sig_in = store_scale(cal["seg0.0"])
+    for b, (block, trans) in enumerate(dense_stages(f)):
+        layers = [layer_plan(layer, width + GROWTH * l, cal, f"{b}.{l}")
+                  for l, layer in enumerate(block.values())]
+        blk = SBlock(c0=width, h=side, w=side, sig0=sig_in, layers=layers)
+        width = blk.c_tot
+        if trans is not None:
+            transition_plan(blk, trans, cal, b)
+            sig_in = store_scale(cal[f"seg0.{b + 1}"])
+            width, side = width // 2, side // 2
         plan.blocks.append(blk)
-        k += 1
     plan.a5, plan.b5 = bn_affine(f.norm5)
     return plan
 
 
 def chunked(w: np.ndarray) -> np.ndarray:
-    """[cout, cin] -> [cin // 32, cout, 32]: the weights of one store group contiguous."""
+    """[cout, cin] -> [cin / 32, cout, 32]: each store group's 32 input channels contiguous per output."""
     cout, cin = w.shape
-    return np.ascontiguousarray(w.reshape(cout, cin // GROUP, GROUP).transpose(1, 0, 2))
+    return np.ascontiguousarray(np.swapaxes(w.reshape(cout, cin // GROUP, GROUP), 0, 1))
 
 
 def abh_table(ab: np.ndarray) -> np.ndarray:
-    """The prologue [c, 2] (A, B) as fp16 pairs: [c // 2, 4] int16 = (A_2p, A_2p+1, B_2p, B_2p+1)."""
-    h = ab.astype(np.float16)
-    return np.ascontiguousarray(
-        np.stack([h[0::2, 0], h[1::2, 0], h[0::2, 1], h[1::2, 1]], 1)).view(np.int16)
+    """The prologue [c, 2] (A, B) as fp16 [c / 2, 4] (bits as int16): per channel pair p the row
+    (A_2p, A_2p+1, B_2p, B_2p+1), one 8-byte load per two channels."""
+    h = ab.astype(np.float16).reshape(-1, 2, 2)              # [pair][channel of the pair][A or B]
+    return np.ascontiguousarray(np.swapaxes(h, 1, 2).reshape(-1, 4)).view(np.int16)
 
 
 def abh_values(abh: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
@@ -412,33 +465,69 @@ def validate_meta(meta: dict) -> None:
 
 
 # --- runner ----------------------------------------------------------------------------------
-# Graph inputs shared among the encoders of one GPU (the seeds of an ensemble read the same windows):
-# {(gpu, shape, dtype): {"buf", "src", "root", "ready", "readers"}} (`src/knee/dense8s.py:911-941`).
-# "ready" is an event after the last copy into "buf", "readers" the event after each runner's last
-# replay that read it: runners called from different streams wait on them, so one runner's copy never
-# overwrites an input another is still reading, and a skipped copy still waits for the one it reuses.
-_SHARED_IN: dict = {}
-_NOVER = itertools.count()
+@dataclass
+class GraphInput:
+    """The static input buffer of captured graphs, shared by the runners of one GPU that take inputs
+    of the same shape and type: the seeds of an ensemble encode the same images, so what one runner
+    copied in is reused by the next (the role of the reference's shared graph inputs,
+    `src/knee/dense8s.py:911-941`).  `source` is the tensor last copied in, kept alive so that its
+    address and version still name those contents, `ident` its identity (`contents_id`), `copied` an
+    event after that copy and `readers` the event after each runner's last replay that read the
+    buffer.  Runners on different streams are ordered through them: a new copy waits for every
+    reader, a reuse waits for the copy."""
+    buf: torch.Tensor
+    source: torch.Tensor | None = None
+    ident: tuple | None = None
+    copied: torch.cuda.Event | None = None
+    readers: dict = field(default_factory=dict)
+
+    def forget(self) -> None:
+        """The buffer's contents no longer come from `source` (a capture, or a caller writing it)."""
+        self.source = self.ident = None
+
+    def load(self, x: torch.Tensor, n: int, stream) -> bool:
+        """Makes buf[:n] hold x, ordered on `stream`: skips the copy when x is the last source, unchanged.
+        Returns whether it copied."""
+        ident = contents_id(x) + (n,)
+        if ident == self.ident:
+            if self.copied is not None:
+                stream.wait_event(self.copied)
+            return False
+        for ev in self.readers.values():
+            stream.wait_event(ev)
+        self.readers.clear()
+        self.buf[:n].copy_(x)
+        self.source, self.ident = x, ident
+        self.copied = _record_sync(stream)
+        return True
+
+    def read_by(self, runner, stream) -> None:
+        self.readers[id(runner)] = _record_sync(stream)
 
 
-def _shared_in(dev: int, shape: tuple, dtype) -> dict:
+_GRAPH_INPUTS: dict[tuple, GraphInput] = {}
+_FRESH = itertools.count()
+
+
+def graph_input(dev: int, shape: tuple, dtype) -> GraphInput:
+    """The shared graph input of (GPU, shape, dtype), allocated on first use."""
     key = (dev, tuple(shape), dtype)
-    s = _SHARED_IN.get(key)
-    if s is None:
-        s = {"buf": torch.zeros(shape, dtype=dtype, device=f"cuda:{dev}"), "src": None, "root": None,
-             "ready": None, "readers": {}}
-        _SHARED_IN[key] = s
-    return s
+    gi = _GRAPH_INPUTS.get(key)
+    if gi is None:
+        gi = _GRAPH_INPUTS[key] = GraphInput(torch.zeros(shape, dtype=dtype, device=f"cuda:{dev}"))
+    return gi
 
 
-def _src_key(x: torch.Tensor) -> tuple:
-    """(root tensor, key of the source): a copy into the graph input is skipped when the key repeats.
-    Inference tensors have no version counter, so their key is always new."""
-    root = x
-    while root._base is not None:
-        root = root._base
-    ver = ("inf", next(_NOVER)) if x.is_inference() else x._version
-    return root, (id(root), x.data_ptr(), ver, tuple(x.shape), tuple(x.stride()))
+def contents_id(x: torch.Tensor) -> tuple:
+    """What names the contents of x from one call to the next: its storage and place in it (storage
+    address, data address, shape, strides) and the version counter shared by the tensors of that
+    storage, which every in-place write bumps (`hip.written` too).  Tensors made in inference mode have
+    no version counter: they get a fresh token, so their contents are always copied."""
+    try:
+        ver = x._version
+    except RuntimeError:
+        ver = ("fresh", next(_FRESH))
+    return (x.untyped_storage().data_ptr(), x.data_ptr(), tuple(x.shape), tuple(x.stride()), ver)
 
 
 class Layer(collections.namedtuple("Layer", "c1 c2 dense")):
@@ -749,9 +838,9 @@ class Dense8SEncoder:
                              f"the output holds {self.out.shape[0]}")
         t = time.perf_counter()
         with torch.cuda.device(self.dev):
-            shared = _shared_in(self.dev, (n, *self.in_shape[1:]), self.in_dtype)
-            static_in = shared["buf"]
-            shared["src"] = shared["root"] = None
+            shared = graph_input(self.dev, (n, *self.in_shape[1:]), self.in_dtype)
+            static_in = shared.buf
+            shared.forget()
             with torch.cuda.stream(self.stream):
                 self.stream.wait_stream(torch.cuda.current_stream(self.dev))
                 self._enqueue(static_in[:k], mode)
@@ -779,7 +868,7 @@ class Dense8SEncoder:
     def graph_in_buf(self, n: int, flip=False) -> torch.Tensor | None:
         """The static input buffer `[:n]` of the graphs captured for `n` images, or None."""
         gs = self._graphs_for(n, self._mode(flip))
-        return None if gs is None else gs[1]["buf"][:n]
+        return None if gs is None else gs[1].buf[:n]
 
     def __call__(self, x: torch.Tensor, flip=False) -> torch.Tensor:
         mode = self._mode(flip)
@@ -791,23 +880,12 @@ class Dense8SEncoder:
             gs = self._graphs_for(n, mode)
             if gs is not None:
                 graphs, shared = gs
-                buf = shared["buf"][:n]
+                buf = shared.buf[:n]
                 if (x.data_ptr() == buf.data_ptr() and x.shape == buf.shape
                         and x.stride() == buf.stride()):
-                    shared["src"] = shared["root"] = None
-                else:
-                    root, key = _src_key(x)
-                    key = key + (n,)
-                    if shared["src"] != key:
-                        for ev in shared["readers"].values():   # runners still reading the old input
-                            self.stream.wait_event(ev)
-                        shared["readers"].clear()
-                        buf.copy_(x)
-                        shared["src"], shared["root"] = key, root
-                        shared["ready"] = _record_sync(self.stream)
-                        self.calls["copy"] = self.calls.get("copy", 0) + 1
-                    elif shared["ready"] is not None:              # copied by another runner's stream
-                        self.stream.wait_event(shared["ready"])
+                    shared.forget()                  # the caller wrote the graph input itself
+                elif shared.load(x, n, self.stream):
+                    self.calls["copy"] = self.calls.get("copy", 0) + 1
                 for g in graphs:
                     if self.max_inflight:
                         while len(self.inflight) >= self.max_inflight:
@@ -817,7 +895,7 @@ class Dense8SEncoder:
                         ev = torch.cuda.Event(blocking=True)
                         ev.record(self.stream)
                         self.inflight.append(ev)
-                shared["readers"][id(self)] = _record_sync(self.stream)
+                shared.read_by(self, self.stream)
                 self.calls["graph"] += 1
             else:
                 self._enqueue(x.contiguous(), mode)

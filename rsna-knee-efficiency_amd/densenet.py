@@ -4,7 +4,7 @@ The module names and the state_dict keys are those of `timm.create_model("densen
 num_classes=0)` (features.conv0, features.norm0, features.pool0, features.denseblock{k}.denselayer{j}
 .{norm1, conv1, norm2, conv2}, features.transition{k}.{norm, conv, pool}, features.norm5), as in the
 reference's hand-written copy `src/knee/models/densenet.py:20-114`: checkpoints load unchanged and
-`dense8s.calibrate` hooks the same modules.  Growth 32, bottleneck 4 x 32, blocks 6/12/32/32,
+`dense8s.calibrate` walks the same modules.  Growth 32, bottleneck 4 x 32, blocks 6/12/32/32,
 transitions halve the channels, 1664 output features.
 
 `seeded_densenet169(seed)` gives the synthetic weights of the benchmark configurations: He-normal

@@ -157,12 +157,13 @@ def test_written_bumps_versions():
     so the encoder's graph-input key sees new contents in a reused output buffer."""
     buf = torch.zeros((4, 3, 8, 8), dtype=torch.uint8)
     view = buf[1:3]
-    _, key0 = dense8s._src_key(view)
+    key0 = dense8s.contents_id(view)
     v0 = buf._version
     hip.written(view)
     assert buf._version == v0 + 1 and view._version == buf._version
-    _, key1 = dense8s._src_key(view)
+    key1 = dense8s.contents_id(view)
     assert key1 != key0
     with torch.inference_mode():
         t = torch.zeros(3)
         hip.written(t, None)                     # inference tensors and None are accepted
+    assert dense8s.contents_id(t) != dense8s.contents_id(t)     # no version counter: always new
