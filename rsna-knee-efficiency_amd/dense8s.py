@@ -360,11 +360,32 @@ def input_lut(mean, std) -> np.ndarray:
     return np.ascontiguousarray(((u[None, :] - m) / s).astype(np.float16)).view(np.int16)
 
 
-def derived_params(meta: dict, par: dict) -> dict[str, np.ndarray]:
+def needed_tables(meta: dict) -> list[str]:
+    """The package tables the runner's kernels read (`par_<name>` of a package): per layer the conv1
+    prologue, weights and epilogue and the conv2 weights and scale, per transition its prologue,
+    weights and epilogue, the final norm and the fp16 stem's tables."""
+    names = ["F_ab", "S_w16", "S_bias", "S_inv"]
+    for bi, b in enumerate(meta["blocks"]):
+        for li in range(b["L"]):
+            names += [f"L{bi}_{li}_{k}" for k in ("abh", "w1", "gdu", "w2k", "c2u")]
+        if b["trans"]:
+            names += [f"T{bi}_{k}" for k in ("abh", "w", "gdf")]
+    return names
+
+
+def derived_params(meta: dict, par: dict, names_only: bool = False):
     """Tables this build's kernels need beyond the reference's, derived from the package tables (so a
     package with only the reference's tables loads too): per-output weight sums for the offset of the
     unsigned activations (`L*_w1sum`, `L*_w2sum`, `T*_wsum`, int32) and the input table `S_lut`.
+    `names_only`: just their names.
     """
+    if names_only:
+        names = ["S_lut"]
+        for bi, b in enumerate(meta["blocks"]):
+            names += [f"L{bi}_{li}_{k}" for li in range(b["L"]) for k in ("w1sum", "w2sum")]
+            if b["trans"]:
+                names.append(f"T{bi}_wsum")
+        return names
     out: dict[str, np.ndarray] = {}
     for bi, b in enumerate(meta["blocks"]):
         for li in range(b["L"]):
@@ -646,19 +667,16 @@ class Dense8SEncoder:
         hw_max = max(b["h"] * b["w"] for b in blocks)
         self.bott = torch.empty(n * BOTTLENECK * hw_max, dtype=torch.uint8, device=d)
         dev = torch.device(d)
+        # only the tables the kernels read go to the device (a reference package also carries the
+        # tables of its TensorRT and int8-stem paths)
+        used = set(needed_tables(meta)) | set(derived_params(meta, {}, names_only=True))
         self.par = {k: torch.from_numpy(np.ascontiguousarray(v)).to(dev)
-                    for k, v in par.items() if k not in ("S_w0", "S_b0", "S_w8f")}
+                    for k, v in par.items() if k in used}
         self.out_dev = dev
         self._build_launches()
 
     def _needed_tables(self) -> list[str]:
-        names = ["F_ab", "S_w16", "S_bias", "S_inv"]
-        for bi, b in enumerate(self.meta["blocks"]):
-            for li in range(b["L"]):
-                names += [f"L{bi}_{li}_{k}" for k in ("abh", "w1", "gdu", "w2k", "c2u")]
-            if b["trans"]:
-                names += [f"T{bi}_{k}" for k in ("abh", "w", "gdf")]
-        return names
+        return needed_tables(self.meta)
 
     def _build_launches(self) -> None:
         """Argument structs of every launch of a pass (`src/knee/dense8s.py:1103-1152`)."""
