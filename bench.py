@@ -98,7 +98,7 @@ def kernel_bytes(meta: dict, n: int, kinds: dict | None = None) -> dict[str, lis
     for bi, b in enumerate(meta["blocks"]):
         hw = b["h"] * b["w"]
         M = n * hw
-        kind = kinds.get(bi, "conv")
+        kind = str(kinds.get(bi, "conv")).split(":")[0]
         wts = 0
         for li in range(b["L"]):
             cin = b["c0"] + 32 * li
@@ -109,7 +109,7 @@ def kernel_bytes(meta: dict, n: int, kinds: dict | None = None) -> dict[str, lis
             elif kind == "conv":
                 out["conv1"].append(M * cin + M * 128 + 128 * cin + cin * 4 + 128 * 12)
                 out["conv2"].append(M * 128 + M * 32 + 36864 + 32 * 8)
-        if kind == "img":
+        if kind in ("img", "parts"):
             out["block"].append(M * b["c0"] + M * 32 * b["L"] + wts)
         ctot = b["c0"] + 32 * b["L"]
         if b["trans"]:
@@ -128,7 +128,7 @@ def kernel_ops(meta: dict, n: int, kinds: dict | None = None) -> dict[str, float
            "block": 0.0, "trans": 0.0}
     for bi, b in enumerate(meta["blocks"]):
         M = n * b["h"] * b["w"]
-        kind = kinds.get(bi, "conv")
+        kind = str(kinds.get(bi, "conv")).split(":")[0]
         for li in range(b["L"]):
             o1 = 2.0 * M * (b["c0"] + 32 * li) * 128
             o2 = 2.0 * M * 1152 * 32
@@ -280,7 +280,7 @@ def traffic_summary(fetch_dir: str, write_dir: str, passes: int, copy_bytes: int
                    {"c0": 256, "h": 32, "w": 32, "L": 32, "trans": True},
                    {"c0": 640, "h": 16, "w": 16, "L": 32, "trans": False}]
     alg = kernel_bytes({"img": IMG, "blocks": meta_blocks}, nb,
-                       dense8s.fused_blocks({"blocks": meta_blocks}))
+                       dense8s.fused_blocks({"blocks": meta_blocks, "n": nb}))
     lines = [f"Calibration: k_copy moves {copy_bytes} B read + {copy_bytes} B written per dispatch; "
              f"FETCH_SIZE scale {kf:.3f}, WRITE_SIZE scale {kw:.3f}.", "",
              "| family | launches per pass | HBM read MB/launch | HBM write MB/launch | traffic MB/launch "
@@ -321,7 +321,7 @@ def mfma_summary(pmc_dir: str, passes: int) -> str:
                    {"c0": 128, "h": 64, "w": 64, "L": 12, "trans": True},
                    {"c0": 256, "h": 32, "w": 32, "L": 32, "trans": True},
                    {"c0": 640, "h": 16, "w": 16, "L": 32, "trans": False}]
-    kinds = dense8s.fused_blocks({"blocks": meta_blocks})
+    kinds = dense8s.fused_blocks({"blocks": meta_blocks, "n": nb})
     alg = kernel_ops({"img": IMG, "blocks": meta_blocks}, nb, kinds)
     lines = ["| family | dispatches | MFMA busy (% of SIMD cycles, weighted) | MFMA ops issued per pass (G) "
              "| algorithmic int8 ops per pass (G) | issued / algorithmic |", "|---|---|---|---|---|---|"]
@@ -418,6 +418,35 @@ def mfma_probe(dev: torch.device, blocks: int = 2048, iters: int = 4096, reps: i
             "frac_of_datasheet": round(tops / I8_PEAK_TOPS, 4), "ms": round(ms, 4),
             "sample": f"{blocks} workgroups x 4 waves x {iters} rounds of 4 independent "
                       f"v_mfma_i32_32x32x32_i8"}
+
+
+def bench_c4(dev: torch.device, passes: int, reps: int) -> dict:
+    """Configuration 4 alone: one encoder (seed 0, batch 24), the 24-slice study of study 0 replayed
+    from its graph `passes` times (wall latency per replay, median), then the per-family kernel times
+    of its pass (`Dense8SEncoder.time_families`, batch 24)."""
+    enc, _ = build_encoder(0, SLICES, dev)
+    x = torch.from_numpy(synthetic.c5_study(0)[:SLICES]).to(dev)
+    enc.capture(SLICES)
+    for _ in range(3):
+        enc(x)
+    torch.cuda.synchronize()
+    lat = []
+    for _ in range(passes):
+        t = time.perf_counter()
+        enc(x)
+        torch.cuda.synchronize()
+        lat.append(time.perf_counter() - t)
+    fam = enc.time_families(x, reps=reps)
+    byts = kernel_bytes(enc.meta, SLICES, enc.fused)
+    ops = kernel_ops(enc.meta, SLICES, enc.fused)
+    return {"config": "C4: one 24-slice study, batch 24, seed 0, HIP graph replay",
+            "passes": passes, "study_latency_ms": round(float(np.median(lat)) * 1e3, 3),
+            "pass_ms_kernels": round(sum(fam.values()), 3),
+            "family_ms": {k: round(v, 4) for k, v in fam.items()},
+            "launches_per_pass": {k: len(v) for k, v in byts.items()},
+            "family_gbs": {k: round(sum(byts[k]) / (fam[k] * 1e-3) / 1e9, 1) for k in byts if fam.get(k)},
+            "family_int8_tops": {k: round(ops[k] / (fam[k] * 1e-3) / 1e12, 1) for k in ops if fam.get(k)},
+            "blocks": {str(k): v for k, v in enc.fused.items()}}
 
 
 PREP_READ_SLICES = (0, 23)      # the final submission's KNEE_READ_SLICES (raw_crop.py:71-76)
@@ -683,6 +712,9 @@ def main() -> None:
                          "after the encoder")
     ap.add_argument("--traffic-summary", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                     help="print the HBM traffic per launch from two --pmc-passes counter runs")
+    ap.add_argument("--c4-passes", type=int, default=0, metavar="P",
+                    help="only configuration 4: P graph replays of the 24-slice study (latency per "
+                         "replay) and its per-family kernel times, one JSON line (a clean kernel trace)")
     ap.add_argument("--mfma-summary", metavar="PMC_DIR",
                     help="print the MFMA use per family from a --pmc-passes counter run")
     args = ap.parse_args()
@@ -716,6 +748,9 @@ def main() -> None:
             print(json.dumps(prep_pmc(dev, args.pmc_passes, args.copy_probe)), flush=True)
         else:
             print(json.dumps(bench_prep(dev, args.steps, args.warmup, not args.no_cpu)), flush=True)
+        return
+    if args.c4_passes:
+        print(json.dumps(bench_c4(dev, args.c4_passes, args.prof_reps)), flush=True)
         return
     t0 = time.perf_counter()
     nb = 4 * SLICES                                     # 2 crops x 24 slices x flip

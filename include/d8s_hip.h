@@ -119,6 +119,27 @@ typedef struct D8sBlockArgs {
     int32_t N, H, W, G0, L, pad_;
 } D8sBlockArgs;
 
+/* Arguments of a whole dense block with every image split into `parts` row bands (d8s_dense_block_parts):
+ * the block store and layer tables as D8sBlockArgs, plus the caller's synchronisation memory.
+ *   sync   device, D8S_PARTS_SYNC_WORDS(N * parts) uint32, all zero before the first call.  Words 0-1
+ *          (ticket and end count) are zero again after every call, word 2 counts bounded waits that
+ *          ran out (0 when the results are valid; only the caller clears it), word 3 counts the
+ *          launches (it names each launch's exchange rows);
+ *   xchg   device, D8S_PARTS_XCHG_BYTES(N * parts, W) bytes, all zero before the first call: the
+ *          bottleneck rows a part hands to its neighbours, as (value, tag) pairs;
+ *   parts  row bands per image: H % parts == 0 and (H / parts) * W in {32, 64, 128, 256}.
+ * One runner's buffers serve its calls in stream order; two launches in flight at once need their own. */
+#define D8S_PARTS_SYNC_WORDS(nparts) (64 + 0 * (nparts))
+#define D8S_PARTS_XCHG_BYTES(nparts, W) ((uint64_t)(nparts) * 1024 * (W))
+typedef struct D8sPartsArgs {
+    const int8_t* in0;
+    int8_t* seg;
+    const D8sLayerP* layers;
+    uint32_t* sync;
+    uint8_t* xchg;
+    int32_t N, H, W, G0, L, parts;
+} D8sPartsArgs;
+
 /* Arguments of the stem: 7x7/2 conv (pad 3) with norm0 folded in, bias, ReLU, 3x3/2 max-pool (pad 1)
  * and per-channel int8 quantisation into the first block's in0.  Replaces the reference's TensorRT
  * fp16 stem engine + `quant_seg` (src/knee/dense8s.py:684-716,1330-1352;
@@ -175,6 +196,14 @@ int d8s_dense(const D8sDenseArgs* a, void* stream);
  * reference's whole-block fused kernels `dense_img*` (src/knee/dense8s_kernels.cu:1005-1219, launch
  * src/knee/dense8s.py:1154-1203). */
 int d8s_dense_block(const D8sBlockArgs* a, void* stream);
+
+/* Every layer of a dense block in one launch with each image split into row bands (see D8sPartsArgs), one
+ * workgroup per band: the bytes of d8s_conv1 + d8s_conv2 layer after layer, with N * parts workgroups
+ * instead of N, for batches too small to fill the chip with one workgroup per image.  Neighbouring
+ * bands hand each other their boundary bottleneck rows once per layer through `xchg`.  The whole-block
+ * role of the reference's `dense_img*` kernels (src/knee/dense8s_kernels.cu:1005-1219), which run
+ * one image per block. */
+int d8s_dense_block_parts(const D8sPartsArgs* a, void* stream);
 
 /* Transition: prologue on the 4 pixels of every 2x2 square, s = sum of the four u, S = sum_k w[o][k]
  * s[k] (exact int32), q = RNE(clamp(k'_o * (float(S) / 4), -127, 127)) into the next block's in0.

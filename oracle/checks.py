@@ -278,7 +278,7 @@ def check_trace(enc, trace: dict, feats: np.ndarray, par: dict, max_rows: int | 
                 planar = np.ascontiguousarray(rows.reshape(-1, 4, 32).transpose(1, 0, 2))
                 _, want2 = lib.conv2(planar, n, h, w, par[f"L{bi}_{li}_w2k"], par[f"L{bi}_{li}_c2u"],
                                      sel2)
-                fam = "block" if kinds.get(bi) == "img" else "dense"
+                fam = "block" if str(kinds.get(bi, "")).split(":")[0] in ("img", "parts") else "dense"
                 worst[fam].append(bytes_cmp(got_seg.reshape(n * hw, 32)[sel2], want2))
                 continue
             sel = pick(n * hw)

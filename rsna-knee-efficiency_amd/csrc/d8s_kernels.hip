@@ -19,6 +19,7 @@
 #include <stdint.h>
 #include <string.h>
 
+#include <algorithm>
 #include <string>
 #include <type_traits>
 
@@ -1405,6 +1406,22 @@ void k_band(D8sDenseArgs a, int bands, int band_rows) {
 // D8sLayerP.  Per layer the first activation groups (the block input, unchanged by the layers) and
 // weights are requested before the layer's tables are staged.
 // ------------------------------------------------------------------------------------------------
+// Loads through pointers read from memory (the layer tables): the compiler cannot tell their address
+// space and would use flat loads, which also count as LDS operations, so every wait for an LDS read
+// would wait for them too.  These say "global".
+typedef __attribute__((address_space(1))) const u32x4 gu32x4;
+typedef __attribute__((address_space(1))) const uint32_t gu32;
+typedef __attribute__((address_space(1))) const int32_t gi32;
+typedef __attribute__((address_space(1))) const u32x2 gu32x2;
+DEV u32x4 ldg_u32x4(const void* p) { return *(gu32x4*)p; }
+DEV uint32_t ldg_u32(const void* p) { return *(gu32*)p; }
+DEV int32_t ldg_i32(const void* p) { return *(gi32*)p; }
+DEV float2 ldg_f2(const void* p) {
+    const u32x2 v = *(gu32x2*)p;
+    return make_float2(__uint_as_float(v.x), __uint_as_float(v.y));
+}
+DEV float ldg_f(const void* p) { return __uint_as_float(*(gu32*)p); }
+
 static constexpr int DB_NT = 512;                          // 8 waves: 8 x 32 pixels
 static constexpr size_t DB_PRM = 128 * 4 + 128 * 8 + 32 * 4 + 32 * 4;
 
@@ -1467,19 +1484,17 @@ __global__ __launch_bounds__(DB_NT, 1) void k_dblock(D8sBlockArgs a) {
         int t_ = tid;                                    /* recomputed indices, not kept live */  \
         asm volatile("" : "+v"(t_));                                                              \
         _Pragma("unroll") for (int k_ = 0; k_ < 5; ++k_)                                          \
-            wv[k_] = ((const u32x4*)(lp_).w2)[min(t_ + DB_NT * k_, 2303)];                       \
-        if (t_ < 128) {                                                                           \
-            t_w1sum = (lp_).w1sum[t_];                                                            \
-            t_gd = ((const float2*)(lp_).gd)[t_];                                                 \
-        } else if (t_ < 160) {                                                                    \
-            t_sc = (lp_).sc[t_ - 128];                                                            \
-            t_w2sum = (lp_).w2sum[t_ - 128];                                                      \
-        }                                                                                         \
+            wv[k_] = ldg_u32x4((const u32x4*)(lp_).w2 + min(t_ + DB_NT * k_, 2303));             \
+        const int ti_ = min(t_, 127), ts_ = min(max(t_ - 128, 0), 31);                             \
+        t_w1sum = ldg_i32((lp_).w1sum + ti_);                                                     \
+        t_gd = ldg_f2((const float2*)(lp_).gd + ti_);                                             \
+        t_sc = ldg_f((lp_).sc + ts_);                                                             \
+        t_w2sum = ldg_i32((lp_).w2sum + ts_);                                                     \
         _Pragma("unroll") for (int k_ = 0; k_ < 4; ++k_)                                          \
-            t_abh[k_] = ((const uint32_t*)(lp_).abh)[min(t_ + DB_NT * k_, (G_) * 32 - 1)];       \
+            t_abh[k_] = ldg_u32((const uint32_t*)(lp_).abh + min(t_ + DB_NT * k_, (G_) * 32 - 1)); \
         const u32x4* w1_ = (const u32x4*)(lp_).w1;                                                \
         _Pragma("unroll") for (int u_ = 0; u_ < 4; ++u_)                                          \
-            stg[u_] = w1_[min(t_ + DB_NT * u_, (G_) * 256 - 1)];                                  \
+            stg[u_] = ldg_u32x4(w1_ + min(t_ + DB_NT * u_, (G_) * 256 - 1));                      \
     } while (0)
 #define DB_RA(G_)                                                                                 \
     _Pragma("unroll") for (int s_ = 0; s_ < 8; ++s_)                                              \
@@ -1520,7 +1535,7 @@ __global__ __launch_bounds__(DB_NT, 1) void k_dblock(D8sBlockArgs a) {
         const int nch = (G + 7) / 8;
 #define DB_STAGE_LOAD(c)                                                                          \
     _Pragma("unroll") for (int u_ = 0; u_ < 4; ++u_)                                              \
-        stg[u_] = w1[min((c) * 2048 + tid + DB_NT * u_, G * 256 - 1)]
+        stg[u_] = ldg_u32x4(w1 + min((c) * 2048 + tid + DB_NT * u_, G * 256 - 1))
 #define DB_STAGE_STORE(c)                                                                         \
     _Pragma("unroll") for (int u_ = 0; u_ < 4; ++u_) s_wc[((c) & 1) * 2048 + wperm(tid + DB_NT * u_)] = stg[u_]
         const int klast = nk - 1;
@@ -1624,6 +1639,365 @@ __global__ __launch_bounds__(DB_NT, 1) void k_dblock(D8sBlockArgs a) {
 #undef DB_RA
 #undef DB_TABLES
 #undef DB_SRC
+}
+
+// ------------------------------------------------------------------------------------------------
+// A whole dense block with every image split into row bands ("parts"): K = parts bands of R = H / K
+// rows (P = R W pixels, PT = P / 32 pixel tiles), one workgroup of 8 waves per (image, band), every
+// layer in one launch.  For batches too small to fill the chip with one workgroup per image: the
+// configuration-4 study (24 images) runs its 32 x 32 and 16 x 16 blocks on ~200 CUs instead of 24 or
+// 88 latency-bound launches.  Per layer:
+//   prologue  the groups' store bytes of the band's pixels go through the fp16 prologue once, chunk by
+//          chunk (CG groups x PT pixel tiles, one 1 KB MFMA operand each), into a double-buffered LDS
+//          chunk shared by all waves: the next chunk's prologue is computed beside the current chunk's
+//          MFMAs, one barrier per chunk;
+//   conv1  wave w computes output tile c = w % 4 (32 of the 128 bottleneck channels) for its pixel
+//          tiles (the band's half w / 4 of them; for a 32-pixel band, half of the groups, the two
+//          halves added through LDS): it reads only its tile's weights, streamed from L2 four groups
+//          ahead in registers;
+//   bottleneck  the bytes of the band's rows into an LDS window of R + 2 rows (zero padding around);
+//          the band's first and last rows also go to `xchg` as (4-byte value, 4-byte tag) pairs, one
+//          64-bit store each, the tag naming the launch and the layer; the neighbours' rows come back
+//          into the window's halo rows by polling those pairs until every tag is current;
+//   conv2  split over the waves of a pixel tile by K step (36 = 4 planes x 9 taps), added through LDS,
+//          stored into the layer's slot.
+// conv1 is pixel-local: a band's next layer reads only its own pixels, so the halo rows are the only
+// data that crosses workgroups.  The exchange pairs are written and read with relaxed agent-scope
+// atomics (performed at the device's coherence point, visible across the XCDs' L2s); a 64-bit pair is
+// written in one access, so a current tag comes with its value.  Workgroups take their (image, band)
+// from a ticket counter in the order they start, so a band only ever waits for bands whose tickets are
+// adjacent to its own, taken by workgroups already running or next to start: the waits cannot form a
+// cycle whatever the dispatch order, and every wait is bounded (a wait that runs out counts in
+// sync[2] and the kernel carries on, so every workgroup reaches its end).  The last workgroup to end
+// resets the ticket and the end count and advances the launch count (sync[3]) the tags are made of,
+// so the next launch needs no clearing.  While conv2 runs, the next layer's tables, first weights and
+// first chunk's store bytes are requested.
+// ------------------------------------------------------------------------------------------------
+static constexpr int DP_NT = 512;
+static constexpr int DP_SPIN = 1 << 20;                   // polls before a wait gives up
+
+DEV uint64_t ld_agent64(const uint64_t* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+DEV void st_agent64(uint64_t* p, uint64_t v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+DEV uint32_t ld_agent(const uint32_t* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+DEV void st_agent(uint32_t* p, uint32_t v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+
+template <int PT>
+__global__ __launch_bounds__(DP_NT, 1) void k_dparts(D8sPartsArgs a) {
+    static_assert(PT == 1 || PT == 2 || PT == 4 || PT == 8, "pixel tiles per band");
+    constexpr int CG = PT == 8 ? 4 : 8;                    // groups per prologue chunk
+    constexpr int ITEMS = CG * PT;                         // (group, pixel tile) operands per chunk
+    constexpr int IPW = ITEMS / 8;                         // of them per wave
+    constexpr int NPT = PT == 1 ? 1 : PT / 2;              // conv1 pixel tiles per wave
+    constexpr int KH = PT == 1 ? 2 : 1;                    // conv1 K halves (32-pixel bands)
+    constexpr int QC = CG / KH;                            // a wave's groups per chunk
+    constexpr int DW = 4;                                  // weight groups in flight per wave
+    constexpr int S2 = PT == 8 ? 1 : (PT == 4 ? 2 : 4);    // conv2 K slices per pixel tile
+    constexpr int NRED = (PT == 1 ? 4 * 1024 : (S2 - 1) * PT * 1024) > 0 ? (PT == 1 ? 4 * 1024 : (S2 - 1) * PT * 1024) : 1;
+    static_assert(QC % DW == 0 && IPW >= 1, "chunk shape");
+    __shared__ __attribute__((aligned(16))) u32x4 s_w[2304];              // conv2 weights, 36 KB
+    __shared__ __attribute__((aligned(16))) u32x4 s_pro[2 * ITEMS * 64];  // prologue chunks
+    __shared__ __attribute__((aligned(16))) int32_t s_red[NRED];          // partial sums
+    __shared__ uint32_t s_tk[2];
+    extern __shared__ __attribute__((aligned(16))) u32x4 s_dyn[];
+    const int H = a.H, W = a.W, HW = H * W, K = a.parts, R = H / K, BW = W + 2, WIN = (R + 2) * BW;
+    const int G0 = a.G0, L = a.L, N = a.N;
+    u32x4* s_b = s_dyn;                                                    // [4][WIN][2]
+    int32_t* s_w1sum = (int32_t*)(s_dyn + 8 * WIN);                       // [128]
+    float2* s_gd = (float2*)(s_w1sum + 128);                              // [128]
+    float* s_sc = (float*)(s_gd + 128);                                   // [32]
+    int32_t* s_w2sum = (int32_t*)(s_sc + 32);                             // [32]
+    uint32_t* s_abh = (uint32_t*)(s_w2sum + 32);                          // [Gmax * 32]
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int h = lane >> 5, j = lane & 31;
+    const int c = wave & 3, hv = wave >> 2;                // conv1: output tile, half
+    uint32_t* sync = a.sync;
+    const int nparts = N * K;
+
+    if (tid == 0) {
+        s_tk[0] = __hip_atomic_fetch_add(sync, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        s_tk[1] = ld_agent(sync + 3);                      // the launch count, stable during a launch
+    }
+    __syncthreads();
+    // a ticket past the last band means the sync words were not zero at the launch: nothing to do
+    // but count it (the bands left without a workgroup make their neighbours' waits run out)
+    const bool valid = (int)s_tk[0] < nparts;
+    const int ticket = valid ? (int)s_tk[0] : 0;
+    const uint32_t epoch = s_tk[1];
+    const int n = ticket / K, part = ticket - n * K;
+    if (!valid && tid == 0) atomicAdd(sync + 2, 1u);
+    {
+        const u32x4 pad = {SIGN4, SIGN4, SIGN4, SIGN4};
+        for (int idx = tid; idx < WIN * 8; idx += DP_NT) {
+            const int wp = idx >> 3, cc = (idx >> 1) & 3, hh = idx & 1;
+            const int wy = wp / BW, wx = wp - wy * BW;
+            if ((wy == 0 && part == 0) || (wy == R + 1 && part == K - 1) || wx == 0 || wx == W + 1)
+                s_b[cc * WIN * 2 + swz(wp, hh)] = pad;
+        }
+    }
+    const int bandp = part * R * W;                        // the band's first pixel in the image
+    const uint8_t* img0 = (const uint8_t*)a.in0 + (int64_t)n * G0 * HW * 32;
+    uint8_t* segn = (uint8_t*)a.seg + (int64_t)n * HW * 32;
+    const int64_t slot = (int64_t)N * HW * 32;
+    uint64_t* xpair = (uint64_t*)a.xchg;                  // [nparts][parity][top, bottom][4][W][8]
+    bool broken = false;                                   // a wait ran out: skip the later ones
+    // store bytes of group g at band pixel 32 t + j (a uniform base plus the lane's 32-bit offset)
+#define DP_SRC(g, t) (((g) < G0 ? img0 + (int64_t)(g) * HW * 32 : segn + (int64_t)((g) - G0) * slot) + \
+                      (uint32_t)((bandp + 32 * (t) + j) * 32 + 16 * h))
+#define DP_XP(tk, par, which, cc) (xpair + ((((int64_t)(tk) * 2 + (par)) * 2 + (which)) * 4 + (cc)) * W * 8)
+    // a wave's conv1 groups: q -> g = q (PT >= 2) or 2 q + hv (32-pixel bands)
+#define DP_G(q) (KH == 1 ? (q) : 2 * (q) + hv)
+
+    // prefetched state of the next layer: tables, first weights, first chunk's store bytes
+    u32x4 t_w2[5];
+    uint32_t t_abh[4];
+    int32_t t_w1sum = 0, t_w2sum = 0;
+    float2 t_gd = {0.f, 0.f};
+    float t_sc = 0.f;
+    u32x4 rw[DW], ra[IPW];
+#define DP_TABLES(lp_, G_)                                                                        \
+    do {                                                                                          \
+        _Pragma("unroll") for (int k_ = 0; k_ < 5; ++k_)                                          \
+            t_w2[k_] = ldg_u32x4((const u32x4*)(lp_).w2 + min(tid + DP_NT * k_, 2303));          \
+        const int ti_ = min(tid, 127), ts_ = min(max(tid - 128, 0), 31);                           \
+        t_w1sum = ldg_i32((lp_).w1sum + ti_);                                                     \
+        t_gd = ldg_f2((const float2*)(lp_).gd + ti_);                                             \
+        t_sc = ldg_f((lp_).sc + ts_);                                                             \
+        t_w2sum = ldg_i32((lp_).w2sum + ts_);                                                     \
+        _Pragma("unroll") for (int k_ = 0; k_ < 4; ++k_)                                          \
+            t_abh[k_] = ldg_u32((const uint32_t*)(lp_).abh + min(tid + DP_NT * k_, (G_) * 32 - 1)); \
+    } while (0)
+    // weights of output tile c of group g (the MFMA A operand: rows 32 c + j, bytes 16 h ..)
+#define DP_W(lp_, g) ldg_u32x4((const uint8_t*)(lp_).w1 + ((int64_t)(g) * 128 + 32 * c + j) * 32 + 16 * h)
+#define DP_RW(lp_, G_)                                                                            \
+    _Pragma("unroll") for (int q_ = 0; q_ < DW; ++q_) rw[q_] = DP_W(lp_, min(DP_G(q_), (G_) - 1))
+    // store bytes of the items of chunk ch a wave prologues (item i = wave + 8 q: group i / PT, tile
+    // i % PT); `ready_` = groups that exist already (earlier layers')
+#define DP_RA(ch_, G_, ready_)                                                                    \
+    _Pragma("unroll") for (int q_ = 0; q_ < IPW; ++q_) {                                          \
+        const int i_ = wave + 8 * q_, g_ = min((ch_) * CG + i_ / PT, (ready_) - 1);                \
+        ra[q_] = *(const u32x4*)DP_SRC(g_, i_ % PT);                                              \
+    }
+
+    if (valid) {
+        const D8sLayerP lp0 = a.layers[0];
+        DP_TABLES(lp0, G0);
+        DP_RA(0, G0, G0);
+    }
+    for (int l = 0; l < (valid ? L : 0); ++l) {
+        const D8sLayerP lp = a.layers[l];
+        const int G = G0 + l;
+        const int nch = (G + CG - 1) / CG;
+        // ---- the layer's tables into LDS (fetched during the previous layer's conv2) ----
+#pragma unroll
+        for (int k = 0; k < 5; ++k)
+            if (tid + DP_NT * k < 2304) s_w[swz((tid + DP_NT * k) >> 1, tid & 1)] = t_w2[k];
+        if (tid < 128) {
+            s_w1sum[tid] = t_w1sum;
+            s_gd[tid] = t_gd;
+        } else if (tid < 160) {
+            s_sc[tid - 128] = t_sc;
+            s_w2sum[tid - 128] = t_w2sum;
+        }
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+            if (tid + DP_NT * k < G * 32) s_abh[tid + DP_NT * k] = t_abh[k];
+        // the previous layer's group, if it is in chunk 0, was not ready when chunk 0 was requested
+        if (l > 0 && G - 1 < CG) {
+#pragma unroll
+            for (int q_ = 0; q_ < IPW; ++q_) {
+                const int i_ = wave + 8 * q_;
+                if (i_ / PT == G - 1) ra[q_] = *(const u32x4*)DP_SRC(G - 1, i_ % PT);
+            }
+        }
+        __syncthreads();                                   // tables in LDS
+
+        // ---- prologue of chunk ch into LDS buffer ch & 1 ----
+#define DP_PRO(ch_)                                                                               \
+    _Pragma("unroll") for (int q_ = 0; q_ < IPW; ++q_) {                                          \
+        const int i_ = wave + 8 * q_, g_ = min((ch_) * CG + i_ / PT, G - 1);                      \
+        const u32x4* pp_ = (const u32x4*)(s_abh + g_ * 32 + h * 16);                              \
+        s_pro[(((ch_) & 1) * ITEMS + i_) * 64 + lane] = pro16(ra[q_], pp_[0], pp_[1], pp_[2], pp_[3]); \
+    }
+        DP_PRO(0);
+        // loads in the loop's order (activations two chunks ahead, then the weight ring), so the wait
+        // counts at the loop's head are the same from both of its entries: no wait for all loads
+        DP_RA(1, G, G);
+        DP_RW(lp, G);
+        __syncthreads();
+        i32x16 acc[NPT];
+        const int32_t m128 = hv == 0 || KH == 1 ? 128 : 0;      // one K half starts at 128 sum w
+#pragma unroll
+        for (int tt = 0; tt < NPT; ++tt) {
+#pragma unroll
+            for (int v = 0; v < 16; ++v) acc[tt][v] = m128 * s_w1sum[32 * c + res_row(v, h)];
+        }
+        for (int ch = 0; ch < nch; ++ch) {
+            // the next chunk's prologue beside this chunk's MFMAs
+            DP_PRO(ch + 1);                                // (past the last chunk: never read)
+            DP_RA(ch + 2, G, G);
+            // straight-line steps (no load under a branch: the wait counts stay exact and the
+            // prefetched loads stay in flight); a step past the last group multiplies zero weights
+            const u32x4* bsrc = s_pro + (ch & 1) * ITEMS * 64 + lane;
+#pragma unroll
+            for (int u = 0; u < QC; ++u) {
+                const int q = ch * QC + u, g = DP_G(q);
+                const uint32_t live = g < G ? ~0u : 0u;
+                const u32x4 wa = rw[u % DW] & u32x4{live, live, live, live};
+                rw[u % DW] = DP_W(lp, min(DP_G(q + DW), G - 1));
+                const int gi = (KH == 2 ? 2 * u + hv : u);
+#pragma unroll
+                for (int tt = 0; tt < NPT; ++tt) {
+                    const int t = KH == 2 ? 0 : hv * NPT + tt;
+                    acc[tt] = mfma_i8(wa, bsrc[(gi * PT + t) * 64], acc[tt]);
+                }
+            }
+            __syncthreads();                               // chunk ch read, chunk ch + 1 written
+        }
+        // 32-pixel bands: the two K halves of each output tile added through LDS
+        if constexpr (KH == 2) {
+            if (hv == 1) {
+                int32_t* r = s_red + c * 1024 + lane;
+#pragma unroll
+                for (int v = 0; v < 16; ++v) r[v * 64] = acc[0][v];
+            }
+            __syncthreads();
+            if (hv == 0) {
+                const int32_t* r = s_red + c * 1024 + lane;
+#pragma unroll
+                for (int v = 0; v < 16; ++v) acc[0][v] += r[v * 64];
+            }
+        }
+        // ---- bottleneck bytes (v ^ 0x80) into the window; the band's first / last row out ----
+        const int par = l & 1;
+        const uint64_t tag = (uint64_t)(epoch * 64u + (uint32_t)l + 1u) << 32;
+        if (KH == 1 || hv == 0) {
+            uint32_t e[4];
+#pragma unroll
+            for (int tt = 0; tt < NPT; ++tt) {
+                const int t = KH == 2 ? 0 : hv * NPT + tt;
+                const int pl = 32 * t + j, yl = pl / W, x = pl - yl * W;
+#pragma unroll
+                for (int kk = 0; kk < 4; ++kk) {
+                    const float4* pg = (const float4*)(s_gd + 32 * c + 8 * kk + 4 * h);
+                    e[kk] = epi1_x80(acc[tt], kk, pg[0], pg[1]);
+                }
+                const u32x4 row = xchg_rows(e[0], e[1], e[2], e[3], h);
+                s_b[c * WIN * 2 + swz((yl + 1) * BW + x + 1, h)] = row;
+                if (yl == 0 && part > 0) {
+                    uint64_t* xp = DP_XP(ticket, par, 0, c) + x * 8 + 4 * h;
+#pragma unroll
+                    for (int e4 = 0; e4 < 4; ++e4) st_agent64(xp + e4, tag | row[e4]);
+                }
+                if (yl == R - 1 && part < K - 1) {
+                    uint64_t* xp = DP_XP(ticket, par, 1, c) + x * 8 + 4 * h;
+#pragma unroll
+                    for (int e4 = 0; e4 < 4; ++e4) st_agent64(xp + e4, tag | row[e4]);
+                }
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+        // ---- the neighbours' rows into the halo rows (window row 0 = the band above's last row,
+        // row R + 1 = the band below's first row), polling each pair until its tag is current ----
+        for (int idx = tid; idx < 2 * 4 * W * 2; idx += DP_NT) {
+            const int hh = idx & 1, xx = (idx >> 1) % W, cc = ((idx >> 1) / W) & 3, below = idx / (8 * W);
+            if (below ? part < K - 1 : part > 0) {
+                const uint64_t* xp = DP_XP(below ? ticket + 1 : ticket - 1, par, below ? 0 : 1, cc) + xx * 8 + 4 * hh;
+                uint64_t v0 = 0, v1 = 0, v2 = 0, v3 = 0;
+                bool ok = false;
+                for (int it = 0; it < DP_SPIN && !broken; ++it) {
+                    v0 = ld_agent64(xp); v1 = ld_agent64(xp + 1); v2 = ld_agent64(xp + 2); v3 = ld_agent64(xp + 3);
+                    if (((v0 & v1 & v2 & v3) >> 32) == (tag >> 32) && ((v0 | v1 | v2 | v3) >> 32) == (tag >> 32)) {
+                        ok = true;
+                        break;
+                    }
+                    __builtin_amdgcn_s_sleep(1);
+                }
+                if (!ok && !broken) {
+                    broken = true;
+                    atomicAdd(sync + 2, 1u);
+                }
+                s_b[cc * WIN * 2 + swz((below ? R + 1 : 0) * BW + xx + 1, hh)] =
+                    u32x4{(uint32_t)v0, (uint32_t)v1, (uint32_t)v2, (uint32_t)v3};
+            }
+        }
+        __syncthreads();
+
+        // ---- conv2 (3x3, pad 1): pixel tile t2, K steps st = s2, s2 + S2, ... of 36 ----
+        {
+            const bool active = PT == 1 ? wave < 4 : true;
+            const int t2 = PT == 1 ? 0 : wave / S2, s2 = PT == 1 ? wave : wave % S2;
+            const int pl = 32 * t2 + j, yl = pl / W, x = pl - yl * W;
+            const int q0 = yl * BW + x;
+            i32x16 acc2;
+#pragma unroll
+            for (int v = 0; v < 16; ++v) acc2[v] = s2 == 0 ? 128 * s_w2sum[res_row(v, h)] : 0;
+            constexpr int NS = (36 + S2 - 1) / S2;
+            if (active) {
+#pragma unroll
+                for (int i = 0; i < NS; ++i) {
+                    const int st = s2 + i * S2;
+                    if (st < 36) {
+                        const int cc = st / 9, tap = st - 9 * cc, ty = tap / 3, tx = tap - 3 * ty;
+                        acc2 = mfma_i8(s_w[swz(st * 32 + j, h)], s_b[cc * WIN * 2 + swz(q0 + ty * BW + tx, h)], acc2);
+                    }
+                }
+            }
+            // the next layer's tables, first weights and first chunk's bytes (groups that exist)
+            if (l + 1 < L) {
+                const D8sLayerP ln = a.layers[l + 1];
+                DP_TABLES(ln, G + 1);
+                DP_RA(0, G + 1, G);
+            }
+            if constexpr (S2 > 1) {
+                if (active && s2 > 0) {
+                    int32_t* r = s_red + ((s2 - 1) * PT + t2) * 1024 + lane;
+#pragma unroll
+                    for (int v = 0; v < 16; ++v) r[v * 64] = acc2[v];
+                }
+                __syncthreads();
+                if (active && s2 == 0) {
+#pragma unroll
+                    for (int qq = 1; qq < S2; ++qq) {
+                        const int32_t* r = s_red + ((qq - 1) * PT + t2) * 1024 + lane;
+#pragma unroll
+                        for (int v = 0; v < 16; ++v) acc2[v] += r[v * 64];
+                    }
+                }
+            }
+            if (active && s2 == 0) {
+                uint32_t e[4];
+#pragma unroll
+                for (int kk = 0; kk < 4; ++kk) e[kk] = epi2_q(acc2, kk, *(const float4*)(s_sc + 8 * kk + 4 * h));
+                const u32x4 row = xchg_rows(e[0], e[1], e[2], e[3], h);
+                *(u32x4*)(segn + (int64_t)l * slot + (uint32_t)((bandp + pl) * 32 + 16 * h)) = row;
+            }
+        }
+        // slot l complete before any wave's next conv1 reads it; LDS free for the next layer
+        __syncthreads();
+    }
+#undef DP_PRO
+#undef DP_RA
+#undef DP_RW
+#undef DP_W
+#undef DP_TABLES
+#undef DP_G
+#undef DP_XP
+#undef DP_SRC
+    // the last workgroup to end resets the ticket and the end count, and counts the launch
+    if (tid == 0) {
+        const uint32_t done = __hip_atomic_fetch_add(sync + 1, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+        if (done == (uint32_t)nparts - 1) {
+            st_agent(sync, 0u);
+            st_agent(sync + 1, 0u);
+            st_agent(sync + 3, epoch + 1u);
+        }
+    }
 }
 
 // ------------------------------------------------------------------------------------------------
@@ -2589,6 +2963,35 @@ static int dblock_launch(const D8sBlockArgs* a, hipStream_t st) {
 
 extern "C" int d8s_dense_block(const D8sBlockArgs* a, void* stream) {
     return dblock_launch(a, (hipStream_t)stream);
+}
+
+extern "C" int d8s_dense_block_parts(const D8sPartsArgs* a, void* stream) {
+    REQUIRE(a != nullptr, "d8s_dense_block_parts: null arguments");
+    REQUIRE(a->in0 && a->seg && a->layers && a->sync && a->xchg, "d8s_dense_block_parts: null pointer");
+    REQUIRE(a->G0 >= 1 && a->L >= 1 && a->N >= 1 && a->H >= 1 && a->W >= 1 && a->parts >= 1,
+            "d8s_dense_block_parts: G0, L, N, H, W, parts must be >= 1");
+    REQUIRE(a->H % a->parts == 0, "d8s_dense_block_parts: H must be a multiple of parts");
+    const int R = a->H / a->parts, P = R * a->W;
+    REQUIRE(P == 32 || P == 64 || P == 128 || P == 256,
+            "d8s_dense_block_parts: (H / parts) * W must be 32, 64, 128 or 256 pixels");
+    REQUIRE(a->G0 + a->L - 1 <= 64, "d8s_dense_block_parts: more than 64 groups");
+    REQUIRE((int64_t)a->N * a->parts < (1 << 24), "d8s_dense_block_parts: too many parts");
+    REQUIRE((int64_t)a->N * a->H * a->W * 32 < (1ll << 31), "d8s_dense_block_parts: store slot over 2 GiB");
+    const size_t shm = (size_t)(R + 2) * (a->W + 2) * 128 + DB_PRM + (size_t)(a->G0 + a->L - 1) * 128;
+    // static LDS of k_dparts<PT>: conv2 weights, two prologue chunks, partial sums, the ticket
+    const int PT = P / 32, CG = PT == 8 ? 4 : 8, S2 = PT == 8 ? 1 : (PT == 4 ? 2 : 4);
+    const size_t nred = PT == 1 ? 4 * 1024 : (size_t)std::max(1, (S2 - 1) * PT * 1024);
+    const size_t stat = 36864 + 2 * (size_t)CG * PT * 1024 + 4 * nred + 16;
+    REQUIRE(shm + stat <= 160 * 1024, "d8s_dense_block_parts: band too large for LDS");
+    hipStream_t st = (hipStream_t)stream;
+    const dim3 grid((unsigned)(a->N * a->parts));
+    switch (P / 32) {
+        case 1: hipLaunchKernelGGL(k_dparts<1>, grid, dim3(DP_NT), shm, st, *a); break;
+        case 2: hipLaunchKernelGGL(k_dparts<2>, grid, dim3(DP_NT), shm, st, *a); break;
+        case 4: hipLaunchKernelGGL(k_dparts<4>, grid, dim3(DP_NT), shm, st, *a); break;
+        default: hipLaunchKernelGGL(k_dparts<8>, grid, dim3(DP_NT), shm, st, *a); break;
+    }
+    return launched("d8s_dense_block_parts");
 }
 
 template <int NT, int PT>

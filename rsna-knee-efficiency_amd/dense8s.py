@@ -558,15 +558,56 @@ class Layer(collections.namedtuple("Layer", "c1 c2 dense")):
 
 # How a block's layers run: "conv" conv1 + conv2 per layer (d8s_conv1, d8s_conv2); "tile" one fused
 # launch per layer (d8s_dense, the reference's fused kind "tile"); "img" the whole block in one launch,
-# a workgroup per image (d8s_dense_block, the reference's "img*" kinds).  The bytes are the same.
-BLOCK_KINDS = ("conv", "tile", "img")
+# a workgroup per image (d8s_dense_block, the reference's "img*" kinds); "parts" the whole block in one
+# launch with every image split into row bands, a workgroup per band (d8s_dense_block_parts; "parts:K"
+# for K bands, plain "parts" for as many as fill the chip).  The bytes are the same.
+BLOCK_KINDS = ("conv", "tile", "img", "parts")
 IMG_MAX_PX = 256                # d8s_dense_block: pixels per image
 IMG_MAX_GROUPS = 64             # and groups read by the last layer
+LDS_BYTES = 160 * 1024
+PARTS_TABLES = 1792             # d8s_dense_block_parts: per-layer tables besides the prologue's
+
+
+def parts_static_lds(pt: int) -> int:
+    """Fixed LDS bytes of d8s_dense_block_parts with pt pixel tiles per band: conv2 weights, two
+    prologue chunks, partial sums."""
+    cg = 4 if pt == 8 else 8
+    s2 = 1 if pt == 8 else 2 if pt == 4 else 4
+    nred = 4 * 1024 if pt == 1 else max(1, (s2 - 1) * pt * 1024)
+    return 36864 + 2 * cg * pt * 1024 + 4 * nred + 16
 
 
 def img_fits(b: dict) -> bool:
     """Whether block `b` (meta) fits d8s_dense_block."""
     return b["h"] * b["w"] <= IMG_MAX_PX and b["c0"] // GROUP + b["L"] - 1 <= IMG_MAX_GROUPS
+
+
+def parts_options(b: dict) -> list[int]:
+    """Band counts d8s_dense_block_parts can split block `b`'s images into (increasing)."""
+    groups = b["c0"] // GROUP + b["L"] - 1
+    if groups > IMG_MAX_GROUPS:
+        return []
+    out = []
+    for k in range(1, b["h"] + 1):
+        r = b["h"] // k
+        if b["h"] % k or r * b["w"] not in hip.PARTS_PIXELS:
+            continue
+        lds = (r + 2) * (b["w"] + 2) * 128 + PARTS_TABLES + groups * 128 + parts_static_lds(r * b["w"] // 32)
+        if lds > LDS_BYTES:
+            continue
+        out.append(k)
+    return out
+
+
+def parts_for(b: dict, n: int, cus: int = 256) -> int | None:
+    """The band count of block `b` at n images per pass: the most bands with n x bands <= cus
+    workgroups (one workgroup per CU: its LDS), or None if no split fits."""
+    fit = [k for k in parts_options(b) if n * k <= cus]
+    return fit[-1] if fit else None
+
+
+def _kind_name(kind) -> str:
+    return str(kind).split(":", 1)[0]
 
 
 BAND_W = 128                    # d8s_dense runs its band form, faster than two launches, at this width
@@ -578,27 +619,53 @@ def band_fits(b: dict) -> bool:
     return b["w"] == BAND_W and b["c0"] // GROUP + b["L"] - 1 <= BAND_MAX_GROUPS
 
 
-def fused_blocks(meta: dict, fused=None) -> dict:
-    """{block: kind} for every block.  `fused` None -> the default: "img" where the block fits it (the
-    16 x 16 maps: one launch instead of 64, no bottleneck in memory), "tile" for 128-wide blocks (the
-    fused layer's band form), else "conv"; a dict {block: kind} (other blocks "conv"); an iterable of
-    blocks -> "tile" for those."""
+def default_kind(b: dict, n: int, cus: int = 256) -> str:
+    """The block kind of block `b` at n images per pass: "parts" (the whole block in one launch, images
+    split into as many bands as fill the chip) where that takes 4 bands or more and the block either
+    fits a workgroup per image (the 16 x 16 maps of a 24-image study: 0.31 ms against 0.49 ms on 24
+    CUs) or splits into 8 bands (the 32 x 32 block of a 24-image study: one launch instead of 64
+    latency-bound ones); "img" where a workgroup per image fits (at 96 images: its 96 workgroups leave
+    room for a second encoder's pass on another stream, which 2-band launches of 192 did not); "tile"
+    for 128-wide blocks (the fused layer's band form); else "conv"."""
+    k = parts_for(b, n, cus)
+    if k is not None and k >= 4 and (img_fits(b) or k >= 8):
+        return f"parts:{k}"
+    return "img" if img_fits(b) else "tile" if band_fits(b) else "conv"
+
+
+def fused_blocks(meta: dict, fused=None, cus: int = 256) -> dict:
+    """{block: kind} for every block.  `fused` None -> the default (`default_kind`); a dict {block:
+    kind} (other blocks "conv"); an iterable of blocks -> "tile" for those."""
     nb = len(meta["blocks"])
     if fused is None:
-        return {bi: ("img" if img_fits(b) else "tile" if band_fits(b) else "conv")
-                for bi, b in enumerate(meta["blocks"])}
+        return {bi: default_kind(b, int(meta["n"]), cus) for bi, b in enumerate(meta["blocks"])}
     req = dict(fused) if isinstance(fused, dict) else {int(b): "tile" for b in fused}
     out = {bi: "conv" for bi in range(nb)}
     for bi, kind in req.items():
         bi = int(bi)
         if not 0 <= bi < nb:
             raise ValueError(f"fused block {bi}: the encoder has blocks 0..{nb - 1}")
-        if kind not in BLOCK_KINDS:
+        if _kind_name(kind) not in BLOCK_KINDS:
             raise ValueError(f"block kind {kind!r}: expected one of {BLOCK_KINDS}")
         if kind == "img" and not img_fits(meta["blocks"][bi]):
             raise ValueError(f"block {bi} does not fit the whole-block kernel")
+        if _kind_name(kind) == "parts":
+            b = meta["blocks"][bi]
+            k = int(kind.split(":", 1)[1]) if ":" in str(kind) else parts_for(b, int(meta["n"]), cus)
+            if k is None or k not in parts_options(b):
+                raise ValueError(f"block {bi} ({b['h']} x {b['w']}, {b['L']} layers) does not split into "
+                                 f"{k} bands (options {parts_options(b)})")
+            kind = f"parts:{k}"
         out[bi] = kind
     return out
+
+
+def _cu_count(dev: int) -> int:
+    """Compute units of GPU `dev` (256 on an MI355X; that figure when no GPU is visible, where the
+    runner fails later anyway)."""
+    if not torch.cuda.is_available():
+        return 256
+    return int(torch.cuda.get_device_properties(dev).multi_processor_count)
 
 
 def _ptr(t: torch.Tensor | None) -> int:
@@ -621,7 +688,7 @@ class Dense8SEncoder:
         meta = pack["meta"]
         validate_meta(meta)
         self.meta, self.dev = meta, int(dev)
-        self.fused = fused_blocks(meta, fused)
+        self.fused = fused_blocks(meta, fused, _cu_count(int(dev)))
         self.nb = int(meta["n"])
         self.n_out = -(-int(n_total) // self.nb) * self.nb
         self.max_inflight = max_inflight
@@ -683,8 +750,9 @@ class Dense8SEncoder:
         n, P = self.nb, lambda k: _ptr(self.par[k])  # noqa: E731
         meta = self.meta
         self.plan_l: list = []
-        self.block_args: dict = {}                   # "img" blocks: their launch
+        self.block_args: dict = {}                   # "img" / "parts" blocks: their launch
         self._tables: dict = {}                      # and their device layer tables
+        self._sync: dict = {}                        # "parts" blocks: sync words and exchange rows
         for bi, b in enumerate(meta["blocks"]):
             hw, g0 = b["h"] * b["w"], b["c0"] // GROUP
             layers = []
@@ -703,7 +771,8 @@ class Dense8SEncoder:
                                        self.seg[bi] + li * n * hw * GROUP, g0, g0 + li, n, b["h"],
                                        b["w"], 0)
                 layers.append(Layer(c1, c2, dn))
-            if self.fused[bi] == "img":
+            kind = _kind_name(self.fused[bi])
+            if kind in ("img", "parts"):
                 lps = (hip.LayerP * b["L"])()
                 for li in range(b["L"]):
                     lps[li] = hip.LayerP(P(f"L{bi}_{li}_w1"), P(f"L{bi}_{li}_abh"), P(f"L{bi}_{li}_gdu"),
@@ -711,8 +780,18 @@ class Dense8SEncoder:
                                          P(f"L{bi}_{li}_w2sum"))
                 table = torch.frombuffer(bytearray(bytes(lps)), dtype=torch.uint8).to(self.out_dev)
                 self._tables[bi] = table
-                self.block_args[bi] = hip.BlockArgs(self.in0[bi], self.seg[bi], _ptr(table), n, b["h"],
-                                                    b["w"], g0, b["L"], 0)
+                if kind == "img":
+                    self.block_args[bi] = hip.BlockArgs(self.in0[bi], self.seg[bi], _ptr(table), n,
+                                                        b["h"], b["w"], g0, b["L"], 0)
+                else:
+                    k = int(self.fused[bi].split(":", 1)[1])
+                    sync = torch.zeros(hip.parts_sync_words(n * k), dtype=torch.int32, device=self.out_dev)
+                    xchg = torch.zeros(hip.parts_xchg_bytes(n * k, b["w"]), dtype=torch.uint8,
+                                       device=self.out_dev)
+                    self._sync[bi] = (sync, xchg)
+                    self.block_args[bi] = hip.PartsArgs(self.in0[bi], self.seg[bi], _ptr(table),
+                                                        _ptr(sync), _ptr(xchg), n, b["h"], b["w"], g0,
+                                                        b["L"], k)
             trans = None
             if b["trans"]:
                 cout = (b["c0"] + GROWTH * b["L"]) // 2
@@ -758,7 +837,24 @@ class Dense8SEncoder:
         hip.check(self.lib.d8s_conv2(ctypes.byref(c2), st), "d8s_conv2")
 
     def _block(self, bi: int, st: int) -> None:
-        hip.check(self.lib.d8s_dense_block(ctypes.byref(self.block_args[bi]), st), "d8s_dense_block")
+        args = self.block_args[bi]
+        if isinstance(args, hip.PartsArgs):
+            hip.check(self.lib.d8s_dense_block_parts(ctypes.byref(args), st), "d8s_dense_block_parts")
+        else:
+            hip.check(self.lib.d8s_dense_block(ctypes.byref(args), st), "d8s_dense_block")
+
+    def sync_errors(self, clear: bool = True) -> int:
+        """Waits that ran out in the "parts" blocks' launches so far (0: every result valid); reads the
+        sync words on the runner's stream (a synchronisation) and clears the count when `clear`."""
+        total = 0
+        with torch.cuda.device(self.dev):
+            self.stream.synchronize()
+            for sync, _ in self._sync.values():
+                total += int(sync[2].item())
+                if clear:
+                    sync[2].zero_()
+            self.stream.synchronize()
+        return total
 
     def _dense(self, d, st: int) -> None:
         hip.check(self.lib.d8s_dense(ctypes.byref(d), st), "d8s_dense")

@@ -77,6 +77,25 @@ class BlockArgs(ctypes.Structure):
                 ("G0", i32), ("L", i32), ("pad_", i32)]
 
 
+class PartsArgs(ctypes.Structure):
+    """`D8sPartsArgs`: a whole dense block with every image split into row bands across workgroups."""
+    _fields_ = [("in0", u64), ("seg", u64), ("layers", u64), ("sync", u64), ("xchg", u64), ("N", i32),
+                ("H", i32), ("W", i32), ("G0", i32), ("L", i32), ("parts", i32)]
+
+
+def parts_sync_words(nparts: int) -> int:
+    """`D8S_PARTS_SYNC_WORDS`: uint32 words of d8s_dense_block_parts' synchronisation memory."""
+    return 64 + 0 * nparts
+
+
+def parts_xchg_bytes(nparts: int, w: int) -> int:
+    """`D8S_PARTS_XCHG_BYTES`: bytes of its exchange rows."""
+    return nparts * 1024 * w
+
+
+PARTS_PIXELS = (32, 64, 128, 256)        # pixels per band d8s_dense_block_parts runs
+
+
 class StemArgs(ctypes.Structure):
     """`D8sStemArgs`: the stem with the fused uint8 normalisation / flip of the input."""
     _fields_ = [("x", u64), ("lut", u64), ("w16", u64), ("bias", u64), ("inv", u64), ("out", u64),
@@ -136,6 +155,7 @@ SIGNATURES = {
     "d8s_conv2": [ctypes.POINTER(Conv2Args), vp],
     "d8s_dense": [ctypes.POINTER(DenseArgs), vp],
     "d8s_dense_block": [ctypes.POINTER(BlockArgs), vp],
+    "d8s_dense_block_parts": [ctypes.POINTER(PartsArgs), vp],
     "d8s_transition": [ctypes.POINTER(GemmArgs), vp],
     "d8s_final": [vp, i32, vp, i32, i32, vp, vp, i32, vp],
     "d8s_stem": [ctypes.POINTER(StemArgs), vp],

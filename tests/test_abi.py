@@ -54,6 +54,9 @@ def test_struct_layouts_match_header(tmp_path):
         " offsetof(D8sGridArgs, M));\n"
         '  printf("%zu %zu %zu\\n", sizeof(D8sHeadArgs), offsetof(D8sHeadArgs, logits),'
         " offsetof(D8sHeadArgs, ctx_layers));\n"
+        '  printf("%zu %zu %zu %zu %d %llu\\n", sizeof(D8sPartsArgs), offsetof(D8sPartsArgs, sync),'
+        " offsetof(D8sPartsArgs, xchg), offsetof(D8sPartsArgs, parts), D8S_PARTS_SYNC_WORDS(7),"
+        " (unsigned long long)D8S_PARTS_XCHG_BYTES(7, 16));\n"
         "  return 0; }\n")
     exe = tmp_path / "layout"
     subprocess.run(["gcc", f"-I{hip.HEADER.parent}", str(prog), "-o", str(exe)], check=True)
@@ -74,6 +77,9 @@ def test_struct_layouts_match_header(tmp_path):
     assert got[7] == [ctypes.sizeof(GA), GA.kind.offset, GA.M.offset]
     HA = hip.HeadArgs
     assert got[8] == [ctypes.sizeof(HA), HA.logits.offset, HA.ctx_layers.offset]
+    PP = hip.PartsArgs
+    assert got[9] == [ctypes.sizeof(PP), PP.sync.offset, PP.xchg.offset, PP.parts.offset,
+                      hip.parts_sync_words(7), hip.parts_xchg_bytes(7, 16)]
 
 
 def _prep_args(kind=0, ws_bytes=None, box=(0, 64, 0, 64), r2=None, k=(0, 1), hr=64, out=256,

@@ -18,7 +18,7 @@ BLOCKS = [{"c0": 64, "h": 128, "w": 128, "L": 6, "trans": True},
           {"c0": 128, "h": 64, "w": 64, "L": 12, "trans": True},
           {"c0": 256, "h": 32, "w": 32, "L": 32, "trans": True},
           {"c0": 640, "h": 16, "w": 16, "L": 32, "trans": False}]
-META = {"img": 512, "blocks": BLOCKS}
+META = {"img": 512, "blocks": BLOCKS, "n": 96}
 
 
 def test_ops_per_slice_closed_form():

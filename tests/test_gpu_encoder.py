@@ -51,12 +51,13 @@ def test_encoder512_layers_exact(dev, study512):
     res = checks.summarize(checks.check_trace(enc, trace, feats, par, max_rows=1024))
     print(res)
     blocks = study512["pack"]["meta"]["blocks"]
-    n_of = {k: sum(blocks[bi]["L"] for bi, kind in enc.fused.items() if kind == k)
-            for k in ("conv", "tile", "img")}
+    n_of = {k: sum(blocks[bi]["L"] for bi, kind in enc.fused.items() if kind.split(":")[0] == k)
+            for k in ("conv", "tile", "img", "parts")}
     assert res["conv1"]["mismatch"] == 0 and res["conv1"]["launches"] == n_of["conv"], res
     assert res["conv2"]["mismatch"] == 0 and res["conv2"]["launches"] == n_of["conv"], res
     assert res["dense"]["mismatch"] == 0 and res["dense"]["launches"] == n_of["tile"], res
-    assert res["block"]["mismatch"] == 0 and res["block"]["launches"] == n_of["img"], res
+    assert res["block"]["mismatch"] == 0 and res["block"]["launches"] == n_of["img"] + n_of["parts"], res
+    assert enc.sync_errors() == 0
     assert res["trans"]["mismatch"] == 0 and res["trans"]["launches"] == 3, res
     assert res["final"]["equal"], res
     lut = dense8s.input_lut([0.5] * 3, [0.25] * 3)
@@ -178,7 +179,8 @@ def test_fused_blocks_same_bytes(dev, study512):
     16 x 16 block in one launch) gives the same features (config 4)."""
     enc, x = study512["enc"], study512["xd"]
     want = enc(x).clone()
-    for fused in ({}, {0: "tile", 1: "tile", 2: "tile", 3: "tile"}, {3: "img"}, {1: "tile", 3: "conv"}):
+    for fused in ({}, {0: "tile", 1: "tile", 2: "tile", 3: "tile"}, {3: "img"}, {1: "tile", 3: "conv"},
+                  {2: "parts:8", 3: "parts:8"}):
         other = dense8s.Dense8SEncoder(study512["pack"], dev.index or 0, 24, fused=fused)
         assert all(other.fused[bi] == fused.get(bi, "conv") for bi in range(4))
         got = other(x).clone()
