@@ -1838,12 +1838,12 @@ __global__ __launch_bounds__(DP_NT, 1) void k_dparts(D8sPartsArgs a) {
             for (int v = 0; v < 16; ++v) acc[tt][v] = m128 * s_w1sum[32 * c + res_row(v, h)];
         }
         for (int ch = 0; ch < nch; ++ch) {
-            // the next chunk's prologue beside this chunk's MFMAs
-            DP_PRO(ch + 1);                                // (past the last chunk: never read)
-            DP_RA(ch + 2, G, G);
             // straight-line steps (no load under a branch: the wait counts stay exact and the
-            // prefetched loads stay in flight); a step past the last group multiplies zero weights
+            // prefetched loads stay in flight); a step past the last group multiplies zero weights.
+            // The next chunk's prologue items are spread between the steps, so their VALU work runs
+            // beside the MFMAs already issued (an item past the last chunk is never read).
             const u32x4* bsrc = s_pro + (ch & 1) * ITEMS * 64 + lane;
+            constexpr int EVERY = QC / IPW;                // steps per prologue item
 #pragma unroll
             for (int u = 0; u < QC; ++u) {
                 const int q = ch * QC + u, g = DP_G(q);
@@ -1856,6 +1856,16 @@ __global__ __launch_bounds__(DP_NT, 1) void k_dparts(D8sPartsArgs a) {
                     const int t = KH == 2 ? 0 : hv * NPT + tt;
                     acc[tt] = mfma_i8(wa, bsrc[(gi * PT + t) * 64], acc[tt]);
                 }
+                if ((u + 1) % EVERY == 0) {
+                    const int qi = (u + 1) / EVERY - 1;    // item wave + 8 qi of chunk ch + 1
+                    const int i_ = wave + 8 * qi, g_ = min((ch + 1) * CG + i_ / PT, G - 1);
+                    const u32x4* pp_ = (const u32x4*)(s_abh + g_ * 32 + h * 16);
+                    s_pro[(((ch + 1) & 1) * ITEMS + i_) * 64 + lane] =
+                        pro16(ra[qi], pp_[0], pp_[1], pp_[2], pp_[3]);
+                    const int g2 = min((ch + 2) * CG + i_ / PT, G - 1);
+                    ra[qi] = *(const u32x4*)DP_SRC(g2, i_ % PT);
+                }
+                __builtin_amdgcn_sched_barrier(0);
             }
             __syncthreads();                               // chunk ch read, chunk ch + 1 written
         }
