@@ -133,8 +133,9 @@ def conv2_case(S: int, N: int = 24, seed: int = 21, W: int | None = None) -> Con
     return Conv2Case(S, N, v, bott, w2, w2k, sc)
 
 
-def trans_case(S: int, C: int, N: int = 4, seed: int = 31, c0: int | None = None):
-    """A transition case: the store of a block (C channels at side S, c0 in in0) and the tables."""
+def trans_case(S: int, C: int, N: int = 4, seed: int = 31, c0: int | None = None, cout: int | None = None):
+    """A transition case: the store of a block (C channels at side S, c0 in in0) and the tables
+    (cout outputs, C / 2 by default)."""
     rng = np.random.default_rng([seed, S, C])
     HW = S * S
     q = rng.integers(-127, 128, (N, C, HW), dtype=np.int16).astype(np.int8)
@@ -143,7 +144,7 @@ def trans_case(S: int, C: int, N: int = 4, seed: int = 31, c0: int | None = None
     xs = q.astype(np.float64) * sig[None, :, None]
     s1 = max(float(np.maximum(a[None, :, None] * xs + b[None, :, None], 0).max()), 1e-12) / 255
     ab = np.stack([a * sig / (255 * s1), b / (255 * s1)], 1).astype(np.float32)
-    cout = C // 2
+    cout = C // 2 if cout is None else cout
     tw, _ = quant_weight_np(rng.normal(0, np.sqrt(2.0 / C), (cout, C)).astype(np.float32))
     # |sum_k w u| ~ 3200 sqrt(C) for these weights and bytes: k' maps that to about +-64
     kq = (rng.uniform(0.5, 1.5, cout) * 127 / (2 * 3200 * np.sqrt(C))).astype(np.float32)

@@ -1409,6 +1409,18 @@ void k_band(D8sDenseArgs a, int bands, int band_rows) {
 // Loads through pointers read from memory (the layer tables): the compiler cannot tell their address
 // space and would use flat loads, which also count as LDS operations, so every wait for an LDS read
 // would wait for them too.  These say "global".
+// Raw buffer loads: a uniform base and size (a buffer resource in scalar registers), a 32-bit lane
+// offset and a uniform scalar offset; bytes past the size read as zero.
+DEV __amdgpu_buffer_rsrc_t brsrc(const void* p, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, 0x00020000);
+}
+DEV uint32_t bload32(__amdgpu_buffer_rsrc_t r, uint32_t off, uint32_t soff) {
+    return __builtin_amdgcn_raw_buffer_load_b32(r, (int)off, (int)soff, 0);
+}
+DEV u32x4 bload128(__amdgpu_buffer_rsrc_t r, uint32_t off, uint32_t soff) {
+    return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, (int)soff, 0));
+}
+
 typedef __attribute__((address_space(1))) const u32x4 gu32x4;
 typedef __attribute__((address_space(1))) const uint32_t gu32;
 typedef __attribute__((address_space(1))) const int32_t gi32;
@@ -2011,110 +2023,200 @@ __global__ __launch_bounds__(DP_NT, 1) void k_dparts(D8sPartsArgs a) {
 }
 
 // ------------------------------------------------------------------------------------------------
-// Transition: conv and 2x2 mean commute, so S = sum_k w[o][k] s[k] with s = the sum of the prologue
-// outputs u of the four pixels of the square: four int8 MFMAs (one per pixel, operand u - 128) into one
-// accumulator that starts at 512 sum_k w (exact int32).  A workgroup takes PT pixel tiles (32 output
-// pixels each) and ALL output channels: the prologue runs once per input byte.  The four waves split the
-// output tiles (wave w: tiles w, w + 4, ..., NT of them); the operands of a K group are built by the
-// whole workgroup into LDS (double-buffered, one barrier per group).
+// Transition, pool first: conv and 2x2 mean commute, so S = sum_k w[o][k] s[k] with s[k] = the sum of the
+// prologue outputs u of channel k over the four pixels of the square (0 <= s <= 1020).  s = 256 h + l
+// (h <= 3, l <= 255) goes to the MFMAs as two int8 operands, h and l - 128, into two accumulators:
+// S = 256 acc_h + acc_l with acc_l starting at 128 sum_k w (exact int32).  Two MFMAs per output tile and
+// K group instead of one per pixel of the square.
+// A workgroup takes PT pixel tiles (32 output pixels each) and ALL output channels: the prologue runs
+// once per input byte.  Staging item = (output pixel, channel quad): four dword loads (the square's
+// pixels), the prologue's fp16 halves 0x6480 + u summed as plain integers (four halves of at most
+// 0x657f carry exactly one bit out of the low half, so the total less 4 * 0x64806480 mod 2^32 is
+// s0 | s1 << 16), the two operand bytes of the quad's channels written to LDS (double-buffered, one
+// barrier per group).  The four waves split the output tiles (wave w: tiles w, w + 4, ..., NT of them).
+// Activations are loaded D groups ahead (registers, D | G); a group's weights are loaded after its
+// predecessor's MFMAs and before the next activation loads, so waiting for them never waits for the
+// activations still in flight.  Loads take a uniform base plus a 32-bit lane offset.
 // ------------------------------------------------------------------------------------------------
-template <int NT, int PT>
-__global__ __launch_bounds__(256, 2) void k_trans(D8sGemmArgs a) {
+template <int NT, int PT, int D>
+__global__ __launch_bounds__(256, NT <= 5 ? 2 : 1) void k_trans(D8sGemmArgs a) {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     constexpr int PX = 32 * PT;                            // output pixels per workgroup
-    constexpr int BUF = 4 * PX * 32;                       // bytes of one group's operands
+    constexpr int PLANE = PX * 2;                          // 16-byte chunks of one operand plane
     const int G = a.G, G0 = a.G0;
-    u32x4* s_b = (u32x4*)smem;                             // [2 buf][4 sub][PX][2]
-    uint32_t* s_abh = (uint32_t*)(smem + 2 * BUF);         // [G * 32]
+    u32x4* s_b = (u32x4*)smem;                             // [2 buf][2 plane (l, h)][PX][2]
+    uint32_t* s_abh = (uint32_t*)(smem + 4 * PLANE * 16);  // [G * 32]
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int h = lane >> 5, j = lane & 31;
     const uint32_t* abh32 = (const uint32_t*)a.abh;
     for (int i = tid; i < G * 32; i += 256) s_abh[i] = abh32[i];
 
-    const int64_t HW = a.HW, W = a.W;
-    const int W2 = a.W >> 1, HW4 = a.HW >> 2;
-    const int64_t NO = (int64_t)a.N * HW4;
-    const int64_t op0 = (int64_t)blockIdx.x * PX;
+    // pixel counts fit 32 bits (the launcher checks N * HW)
+    const uint32_t HW = (uint32_t)a.HW, W = (uint32_t)a.W;
+    const uint32_t W2 = W >> 1, HW4 = HW >> 2;
+    const uint32_t NO = (uint32_t)a.N * HW4;
+    const uint32_t op0 = blockIdx.x * (uint32_t)PX;
     const int OT = a.cout >> 5;
 
-    // staging items of this thread: item = tid + 256 k -> (sub-pixel sp, output pixel px, half hh)
-    const int8_t* pin[PT];
-    const int8_t* pseg[PT];
-    int sdst[PT];
+    // staging items of this thread.  Narrow (PT < 4): item = tid + 256 k -> channel quad cq = item & 7,
+    // output pixel px = item >> 3, four dword loads.  Wide (PT = 4, the 128 pixels of a workgroup): item
+    // = tid -> channel half hh = tid & 1, output pixel tid >> 1, four 16-byte loads (a quarter of the
+    // load instructions per byte: the data return path is paced by instructions, not bytes).
+    constexpr bool WIDE = PT == 4;
+    constexpr int IT = WIDE ? 1 : PT, RW = WIDE ? 4 : 1;   // items per thread, registers per item
+    const int cq = tid & 7, hh = tid & 1;
+    uint32_t oin[IT], oseg[IT];                            // byte offsets of the square's top-left pixel
+    int sdst[IT];
 #pragma unroll
-    for (int k = 0; k < PT; ++k) {
-        const int item = tid + 256 * k;
-        const int hh = item & 1, px = (item >> 1) % PX, sp = (item >> 1) / PX;
-        int64_t op = op0 + px;
+    for (int k = 0; k < IT; ++k) {
+        const uint32_t px = WIDE ? (uint32_t)(tid >> 1) : (uint32_t)(tid >> 3) + 32u * k;
+        uint32_t op = op0 + px;
         if (op >= NO) op = NO - 1;
-        const int64_t n = op / HW4, p4 = op - n * HW4;
-        const int64_t oy = p4 / W2, ox = p4 - oy * W2;
-        const int64_t p = (2 * oy + (sp >> 1)) * W + 2 * ox + (sp & 1);
-        pin[k] = a.in0 + (n * G0 * HW + p) * 32 + 16 * hh;
-        pseg[k] = a.seg + (n * HW + p) * 32 + 16 * hh;
-        sdst[k] = (sp * PX) * 2 + swz(px, hh);              // in 16-byte chunks within a buffer
+        const uint32_t n = op / HW4, p4 = op - n * HW4;
+        const uint32_t oy = p4 / W2, ox = p4 - oy * W2;
+        const uint32_t p = 2 * oy * W + 2 * ox;
+        const uint32_t cb = WIDE ? 16 * hh : 4 * cq;
+        oin[k] = (n * (uint32_t)G0 * HW + p) * 32 + cb;
+        oseg[k] = (n * HW + p) * 32 + cb;
+        sdst[k] = WIDE ? swz((int)px, hh) * 16 : swz((int)px, cq >> 2) * 16 + 4 * (cq & 3);  // plane bytes
     }
-    const int64_t in_gs = HW * 32, seg_gs = (int64_t)a.N * HW * 32;
-    auto src = [&](int k, int g) -> const u32x4* {
-        return (const u32x4*)(g < G0 ? pin[k] + g * in_gs : pseg[k] + (g - G0) * seg_gs);
+    const uint32_t row = W * 32;
+    const int64_t in_gs = (int64_t)HW * 32, seg_gs = (int64_t)a.N * HW * 32;
+    const uint32_t in_bytes = (uint32_t)a.N * (uint32_t)G0 * HW * 32;
+    // the square's data of item k, group g: buffer loads (uniform base and size, the row step as the
+    // scalar offset)
+    auto ld = [&](int k, int g, u32x4* x) {
+        const bool lo = g < G0;
+        const auto r = lo ? brsrc(a.in0 + g * in_gs, in_bytes - (uint32_t)(g * in_gs))
+                          : brsrc(a.seg + (g - G0) * seg_gs, (uint32_t)seg_gs);
+        const uint32_t o = lo ? oin[k] : oseg[k];
+        if constexpr (WIDE) {
+            x[0] = bload128(r, o, 0);
+            x[1] = bload128(r, o + 32, 0);
+            x[2] = bload128(r, o, row);
+            x[3] = bload128(r, o + 32, row);
+        } else {
+            x[0].x = bload32(r, o, 0);
+            x[0].y = bload32(r, o + 32, 0);
+            x[0].z = bload32(r, o, row);
+            x[0].w = bload32(r, o + 32, row);
+        }
     };
-    const int hh_item = tid & 1;                           // every item of a thread has the same half
 
-    // weights of this wave's output tiles: row 32 (wave + 4 i) + j, half h
-    i32x16 acc[NT][PT];
+    uint32_t wof[NT];                                      // weight row offsets (clamped past OT)
+    i32x16 accl[NT][PT], acch[NT][PT];
 #pragma unroll
     for (int i = 0; i < NT; ++i) {
-        const int ot = wave + 4 * i;
+        const int ot = wave + 4 * i < OT ? wave + 4 * i : OT - 1;
+        wof[i] = (uint32_t)((32 * ot + j) * 32 + 16 * h);
         i32x16 init;
 #pragma unroll
-        for (int v = 0; v < 16; ++v) init[v] = ot < OT ? 512 * a.wsum[32 * ot + res_row(v, h)] : 0;
+        for (int v = 0; v < 16; ++v) init[v] = 128 * a.wsum[32 * ot + res_row(v, h)];
 #pragma unroll
-        for (int t = 0; t < PT; ++t) acc[i][t] = init;
+        for (int t = 0; t < PT; ++t) {
+            accl[i][t] = init;
+            acch[i][t] = i32x16{};
+        }
     }
     auto wload = [&](int g, u32x4* aw) {
+        const auto r = brsrc(a.w + (int64_t)g * a.cout * 32, (uint32_t)a.cout * 32);
 #pragma unroll
-        for (int i = 0; i < NT; ++i) {
-            const int ot = wave + 4 * i;
-            aw[i] = ot < OT ? *(const u32x4*)(a.w + (((int64_t)g * a.cout + 32 * ot + j) * 32 + 16 * h))
-                            : u32x4{0u, 0u, 0u, 0u};
+        for (int i = 0; i < NT; ++i) aw[i] = bload128(r, wof[i], 0);
+    };
+    // one staging item: prologue of the square's bytes, the sums, both operand planes to LDS (sums of
+    // channel pairs of one dword: sl = channels 0, 1, sh = 2, 3)
+    auto sum4 = [&](uint32_t x0, uint32_t x1, uint32_t x2, uint32_t x3, const u32x4& p, uint32_t& lb,
+                    uint32_t& hb) {
+        const uint32_t xs[4] = {x0, x1, x2, x3};
+        uint32_t sl = 0, sh = 0;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            uint32_t rl, rh;
+            pro4_halves(xs[c], p.x, p.y, p.z, p.w, rl, rh);
+            sl += rl;
+            sh += rh;
+        }
+        sl -= 0x92019200u;                                 // 4 * 0x64806480 mod 2^32
+        sh -= 0x92019200u;
+        lb = perm(sh, sl, 0x06040200u) ^ SIGN4;            // l - 128
+        hb = perm(sh, sl, 0x07050301u);                    // h
+    };
+    auto stage = [&](const u32x4* x, uint8_t* dst, const u32x4* prm) {
+        if constexpr (WIDE) {
+            uint32_t lb[4], hb[4];
+            sum4(x[0].x, x[1].x, x[2].x, x[3].x, prm[0], lb[0], hb[0]);
+            sum4(x[0].y, x[1].y, x[2].y, x[3].y, prm[1], lb[1], hb[1]);
+            sum4(x[0].z, x[1].z, x[2].z, x[3].z, prm[2], lb[2], hb[2]);
+            sum4(x[0].w, x[1].w, x[2].w, x[3].w, prm[3], lb[3], hb[3]);
+            *(u32x4*)dst = u32x4{lb[0], lb[1], lb[2], lb[3]};
+            *(u32x4*)(dst + PLANE * 16) = u32x4{hb[0], hb[1], hb[2], hb[3]};
+        } else {
+            uint32_t lb, hb;
+            sum4(x[0].x, x[0].y, x[0].z, x[0].w, prm[0], lb, hb);
+            *(uint32_t*)dst = lb;
+            *(uint32_t*)(dst + PLANE * 16) = hb;
         }
     };
 
-    u32x4 raw[PT], aw[NT];
+    // weights: two register sets when D is even (group g's in set g & 1, the next group's loaded before
+    // this group's prologue: a whole slot to arrive), one set otherwise (loaded after the MFMAs)
+    constexpr bool W2B = D % 2 == 0;
+    u32x4 raw[D][IT][RW], aw[W2B ? 2 : 1][NT];
 #pragma unroll
-    for (int k = 0; k < PT; ++k) raw[k] = *src(k, 0);
-    wload(0, aw);
+    for (int d = 0; d < D; ++d)
+#pragma unroll
+        for (int k = 0; k < IT; ++k) ld(k, d < G ? d : G - 1, raw[d][k]);
+    wload(0, aw[0]);
     __syncthreads();                                       // s_abh
-    for (int g = 0; g < G; ++g) {
-        const int buf = g & 1;
-        {
-            const u32x4* pp = (const u32x4*)(s_abh + g * 32 + hh_item * 16);
-            const u32x4 p0 = pp[0], p1 = pp[1], p2 = pp[2], p3 = pp[3];
+    // D groups per step; the first step is peeled so that the loop's waits see only the steady state
+    // (the preamble's load order would otherwise make them wait for every load)
+    auto step = [&](int g0) {
 #pragma unroll
-            for (int k = 0; k < PT; ++k) s_b[buf * (BUF / 16) + sdst[k]] = pro16(raw[k], p0, p1, p2, p3);
+        for (int d = 0; d < D; ++d) {
+            const int g = g0 + d;
+            u32x4* awc = aw[W2B ? d & 1 : 0];
+            if constexpr (W2B) {
+                wload(g + 1 < G ? g + 1 : g, aw[(d + 1) & 1]);
+                __builtin_amdgcn_sched_barrier(0);         // issued ahead of the prologue
+            }
+            uint8_t* sb = (uint8_t*)(s_b + (g & 1) * 2 * PLANE);
+            u32x4 prm[RW];
+#pragma unroll
+            for (int c = 0; c < RW; ++c)
+                prm[c] = *(const u32x4*)(s_abh + g * 32 + (WIDE ? hh * 16 + 4 * c : cq * 4));
+#pragma unroll
+            for (int k = 0; k < IT; ++k) stage(raw[d][k], sb + sdst[k], prm);
+            __syncthreads();
+            const u32x4* bl = (const u32x4*)sb;
+#pragma unroll
+            for (int t = 0; t < PT; ++t) {
+                const u32x4 vl = bl[swz(32 * t + j, h)], vh = bl[PLANE + swz(32 * t + j, h)];
+#pragma unroll
+                for (int i = 0; i < NT; ++i) {
+                    accl[i][t] = mfma_i8(awc[i], vl, accl[i][t]);
+                    acch[i][t] = mfma_i8(awc[i], vh, acch[i][t]);
+                }
+            }
+            // (one set: the next group's weights now, before the activations), then this slot's
+            // activations D groups on (the last groups reload the last one: the loads stay
+            // unconditional and countable)
+            if constexpr (!W2B) {
+                wload(g + 1 < G ? g + 1 : g, aw[0]);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+            const int gn = g + D < G ? g + D : G - 1;
+#pragma unroll
+            for (int k = 0; k < IT; ++k) ld(k, gn, raw[d][k]);
+            // keep the next slot's prologue below this point: hoisted, it would wait for loads still
+            // in flight
+            __builtin_amdgcn_sched_barrier(0);
         }
-        // unconditional prefetch (the last group reloads itself): the loads stay countable for the
-        // compiler's waits, so they remain in flight across the MFMAs
-        const int gn = g + 1 < G ? g + 1 : g;
-#pragma unroll
-        for (int k = 0; k < PT; ++k) raw[k] = *src(k, gn);
-        __syncthreads();
-        const u32x4* sb = s_b + buf * (BUF / 16);
-#pragma unroll
-        for (int sp = 0; sp < 4; ++sp) {
-            u32x4 b[PT];
-#pragma unroll
-            for (int t = 0; t < PT; ++t) b[t] = sb[(sp * PX) * 2 + swz(32 * t + j, h)];
-#pragma unroll
-            for (int i = 0; i < NT; ++i)
-#pragma unroll
-                for (int t = 0; t < PT; ++t) acc[i][t] = mfma_i8(aw[i], b[t], acc[i][t]);
-        }
-        wload(gn, aw);
-    }
-    // epilogue: q = RNE(clamp(k' * (float(S) / 4), -127, 127)) (trans_w_body with the exact mean,
-    // src/knee/dense8s_kernels.cu:3226-3245)
+    };
+    step(0);
+    for (int g0 = D; g0 < G; g0 += D) step(g0);
+    // epilogue: q = RNE(clamp(S * (float(k) / 4), -127, 127)) (trans_w_body with the exact mean,
+    // src/knee/dense8s_kernels.cu:3226-3245), as the low byte of q + 1.5 * 2^23
 #pragma unroll
     for (int i = 0; i < NT; ++i) {
         const int ot = wave + 4 * i;
@@ -2127,21 +2229,21 @@ __global__ __launch_bounds__(256, 2) void k_trans(D8sGemmArgs a) {
             uint32_t e[4];
 #pragma unroll
             for (int k = 0; k < 4; ++k) {
-                uint32_t d = 0;
+                uint32_t b[4];
 #pragma unroll
                 for (int rr = 0; rr < 4; ++rr) {
                     const int v = 4 * k + rr;
-                    const float x = kq[v] * ((float)acc[i][t][v] * 0.25f);
-                    const float q = __builtin_rintf(__builtin_fminf(__builtin_fmaxf(x, -127.0f), 127.0f));
-                    d |= ((uint32_t)(int)q & 0xffu) << (8 * rr);
+                    const int32_t S = acch[i][t][v] * 256 + accl[i][t][v];
+                    const float x = kq[v] * ((float)S * 0.25f);
+                    b[rr] = __float_as_uint(__builtin_amdgcn_fmed3f(x, -127.0f, 127.0f) + 12582912.0f);
                 }
-                e[k] = d;
+                e[k] = pack_b0(b[0], b[1], b[2], b[3]);
             }
-            const u32x4 row = xchg_rows(e[0], e[1], e[2], e[3], h);
-            const int64_t op = op0 + 32 * t + j;
+            const u32x4 rowv = xchg_rows(e[0], e[1], e[2], e[3], h);
+            const uint32_t op = op0 + 32 * t + j;
             if (op < NO) {
-                const int64_t n = op / HW4, p4 = op - n * HW4;
-                *(u32x4*)((int8_t*)a.out + ((n * a.G0n + ot) * HW4 + p4) * 32 + 16 * h) = row;
+                const uint32_t n = op / HW4, p4 = op - n * HW4;
+                *(u32x4*)((int8_t*)a.out + ((int64_t)(n * (uint32_t)a.G0n + ot) * HW4 + p4) * 32 + 16 * h) = rowv;
             }
         }
         asm volatile("" ::: "memory");
@@ -3004,14 +3106,23 @@ extern "C" int d8s_dense_block_parts(const D8sPartsArgs* a, void* stream) {
     return launched("d8s_dense_block_parts");
 }
 
-template <int NT, int PT>
-static int trans_launch(const D8sGemmArgs* a, hipStream_t st) {
+template <int NT, int PT, int D>
+static int trans_launch_d(const D8sGemmArgs* a, hipStream_t st) {
+    REQUIRE((int64_t)a->N * a->HW < (1ll << 31) && (int64_t)a->N * a->G0 * a->HW * 32 < (1ll << 32) &&
+            (int64_t)a->N * a->HW * 32 < (1ll << 32), "d8s_transition: too many pixels");
     const int64_t NO = (int64_t)a->N * (a->HW / 4);
     const int64_t blocks = (NO + 32 * PT - 1) / (32 * PT);
-    REQUIRE(blocks < (1ll << 31), "d8s_transition: too many pixels");
-    const size_t shm = 2 * (size_t)4 * 32 * PT * 32 + (size_t)a->G * 128;
-    hipLaunchKernelGGL((k_trans<NT, PT>), dim3((unsigned)blocks), dim3(256), shm, st, *a);
+    const size_t shm = (size_t)2 * 2 * 32 * PT * 32 + (size_t)a->G * 128;
+    hipLaunchKernelGGL((k_trans<NT, PT, D>), dim3((unsigned)blocks), dim3(256), shm, st, *a);
     return launched("d8s_transition");
+}
+
+// activation prefetch depth: the largest of 4, 2, 1 dividing the group count
+template <int NT, int PT>
+static int trans_launch(const D8sGemmArgs* a, hipStream_t st) {
+    if (a->G % 4 == 0) return trans_launch_d<NT, PT, 4>(a, st);
+    if (a->G % 2 == 0) return trans_launch_d<NT, PT, 2>(a, st);
+    return trans_launch_d<NT, PT, 1>(a, st);
 }
 
 extern "C" int d8s_transition(const D8sGemmArgs* a, void* stream) {
@@ -3023,7 +3134,7 @@ extern "C" int d8s_transition(const D8sGemmArgs* a, void* stream) {
     REQUIRE(a->W % 2 == 0 && (a->HW / a->W) % 2 == 0, "d8s_transition: H and W must be even");
     hipStream_t st = (hipStream_t)stream;
     switch ((a->cout / 32 + 3) / 4) {                      // output tiles per wave
-        case 1: return trans_launch<1, 2>(a, st);
+        case 1: return trans_launch<1, 4>(a, st);
         case 2: return trans_launch<2, 2>(a, st);
         case 3: return trans_launch<3, 1>(a, st);
         case 4: return trans_launch<4, 1>(a, st);

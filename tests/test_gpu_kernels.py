@@ -190,16 +190,20 @@ def test_dense_block(dev, H, W, c0, L, N):
     del rng
 
 
-@pytest.mark.parametrize("S,C,c0", [(128, 256, 64), (64, 512, 128), (32, 1280, 256), (16, 128, 64)])
-def test_transition(dev, S, C, c0):
-    t = cases.trans_case(S, C, N=4, c0=c0)
-    print(f"transition S={S} C={C}", flush=True)
+@pytest.mark.parametrize("S,C,c0,cout", [(128, 256, 64, None), (64, 512, 128, None), (32, 1280, 256, None),
+                                         (16, 128, 64, None), (12, 192, 64, None), (8, 320, 64, None),
+                                         (12, 640, 128, None), (6, 96, 32, 32), (4, 224, 96, 256)])
+def test_transition(dev, S, C, c0, cout):
+    """The DenseNet169 geometries, then ragged pixel counts and every activation prefetch depth (the
+    largest of 4, 2, 1 dividing the group count) and tile count per wave."""
+    t = cases.trans_case(S, C, N=4, c0=c0, cout=cout)
+    print(f"transition S={S} C={C} cout={t['cout']}", flush=True)
     got = checks.run_trans(t, dev)
     S_x, q_x = checks.exact_trans(t)
     assert np.array_equal(got, q_x), checks.bytes_cmp(got, q_x)
     rng = np.random.default_rng(C)
     n_out = t["N"] * S * S // 4
-    sel = np.unique(np.concatenate([rng.choice(n_out, 128, replace=False), [0, n_out - 1]]))
+    sel = np.unique(np.concatenate([rng.choice(n_out, min(128, n_out), replace=False), [0, n_out - 1]]))
     S_o, q_o = lib.trans(t["in0"], t["seg"], t["G0"], t["G"], t["N"], S * S, S, t["abh"], t["w"],
                          t["gdf"], t["cout"], sel)
     assert np.array_equal(S_o, S_x[sel]) and np.array_equal(q_o, got[sel])
