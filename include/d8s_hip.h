@@ -207,7 +207,8 @@ int d8s_dense_block_parts(const D8sPartsArgs* a, void* stream);
 
 /* Transition: prologue on the 4 pixels of every 2x2 square, s = sum of the four u, S = sum_k w[o][k]
  * s[k] (exact int32), q = RNE(clamp(k'_o * (float(S) / 4), -127, 127)) into the next block's in0.
- * H and W even, cout a multiple of 32.  Replaces `trans_w0` / `trans_w1`
+ * H and W even, cout a multiple of 32 (at most 1024), N * HW < 2^31 and the in0 / one seg slot below
+ * 4 GiB.  Replaces `trans_w0` / `trans_w1`
  * (src/knee/dense8s_kernels.cu:3041-3262, launch src/knee/dense8s.py:1242-1272). */
 int d8s_transition(const D8sGemmArgs* a, void* stream);
 

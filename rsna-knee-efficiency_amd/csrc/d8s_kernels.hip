@@ -1396,19 +1396,6 @@ void k_band(D8sDenseArgs a, int bands, int band_rows) {
 #undef BN_LOAD_B
 }
 
-// ------------------------------------------------------------------------------------------------
-// A whole dense block per image (small maps, H W <= 256): one workgroup of 8 waves per image runs every
-// layer of the block: conv1 of the image's 256 pixels (wave w: pixels 32 w .. 32 w + 31, all 128
-// outputs, the image's store read from global memory, where it stays in L2), the bottleneck into LDS
-// (with a zero-padding ring), conv2 from LDS into the layer's store slot, a barrier, the next layer.
-// No per-layer launches and no bottleneck in memory; the layers of one image depend only on that
-// image, so workgroups never wait for each other.  The layer tables come from a device array of
-// D8sLayerP.  Per layer the first activation groups (the block input, unchanged by the layers) and
-// weights are requested before the layer's tables are staged.
-// ------------------------------------------------------------------------------------------------
-// Loads through pointers read from memory (the layer tables): the compiler cannot tell their address
-// space and would use flat loads, which also count as LDS operations, so every wait for an LDS read
-// would wait for them too.  These say "global".
 // Raw buffer loads: a uniform base and size (a buffer resource in scalar registers), a 32-bit lane
 // offset and a uniform scalar offset; bytes past the size read as zero.
 DEV __amdgpu_buffer_rsrc_t brsrc(const void* p, uint32_t bytes) {
@@ -1421,6 +1408,9 @@ DEV u32x4 bload128(__amdgpu_buffer_rsrc_t r, uint32_t off, uint32_t soff) {
     return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, (int)soff, 0));
 }
 
+// Loads through pointers read from memory (the layer tables): the compiler cannot tell their address
+// space and would use flat loads, which also count as LDS operations, so every wait for an LDS read
+// would wait for them too.  These say "global".
 typedef __attribute__((address_space(1))) const u32x4 gu32x4;
 typedef __attribute__((address_space(1))) const uint32_t gu32;
 typedef __attribute__((address_space(1))) const int32_t gi32;
@@ -1434,6 +1424,16 @@ DEV float2 ldg_f2(const void* p) {
 }
 DEV float ldg_f(const void* p) { return __uint_as_float(*(gu32*)p); }
 
+// ------------------------------------------------------------------------------------------------
+// A whole dense block per image (small maps, H W <= 256): one workgroup of 8 waves per image runs every
+// layer of the block: conv1 of the image's 256 pixels (wave w: pixels 32 w .. 32 w + 31, all 128
+// outputs, the image's store read from global memory, where it stays in L2), the bottleneck into LDS
+// (with a zero-padding ring), conv2 from LDS into the layer's store slot, a barrier, the next layer.
+// No per-layer launches and no bottleneck in memory; the layers of one image depend only on that
+// image, so workgroups never wait for each other.  The layer tables come from a device array of
+// D8sLayerP.  Per layer the first activation groups (the block input, unchanged by the layers) and
+// weights are requested before the layer's tables are staged.
+// ------------------------------------------------------------------------------------------------
 static constexpr int DB_NT = 512;                          // 8 waves: 8 x 32 pixels
 static constexpr size_t DB_PRM = 128 * 4 + 128 * 8 + 32 * 4 + 32 * 4;
 
