@@ -125,6 +125,10 @@ def test_conv2_tile_variants(dev, N, H, W):
     (40, 64, 96, 64, 3),         # band form (W = 64): height not a multiple of the band
     (128, 64, 64, 32, 1),        # band form: 2 groups, G0 = 1
     (6, 128, 64, 64, 2),         # band form: a band taller than the image
+    (128, 128, 224, 64, 2),      # band form (W = 128), block 0's last layer: 7 groups
+    (9, 128, 288, 64, 1),        # W = 128, 9 groups: 10 K registers, the last a zero operand
+    (20, 128, 320, 96, 1),       # W = 128, 10 groups, G0 = 3
+    (64, 128, 512, 64, 1),       # W = 128, 16 groups: the most the band form takes
     (16, 64, 512, 64, 1),        # W = 64 with 16 groups: conv1 weights too large for the band form
 ])
 def test_dense_layer(dev, H, W, C, c0, N):
