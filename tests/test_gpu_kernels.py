@@ -196,10 +196,12 @@ def test_dense_block(dev, H, W, c0, L, N):
 
 @pytest.mark.parametrize("S,C,c0,cout", [(128, 256, 64, None), (64, 512, 128, None), (32, 1280, 256, None),
                                          (16, 128, 64, None), (12, 192, 64, None), (8, 320, 64, None),
-                                         (12, 640, 128, None), (6, 96, 32, 32), (4, 224, 96, 256)])
+                                         (12, 640, 128, None), (6, 96, 32, 32), (4, 224, 96, 256),
+                                         (8, 1024, 128, None), (6, 416, 64, 416), (4, 256, 64, 768),
+                                         (4, 192, 64, 1024)])
 def test_transition(dev, S, C, c0, cout):
-    """The DenseNet169 geometries, then ragged pixel counts and every activation prefetch depth (the
-    largest of 4, 2, 1 dividing the group count) and tile count per wave."""
+    """The DenseNet169 geometries, then ragged pixel counts, every activation prefetch depth (the
+    largest of 4, 2, 1 dividing the group count) and tile count per wave (1-6 and 8, ragged too)."""
     t = cases.trans_case(S, C, N=4, c0=c0, cout=cout)
     print(f"transition S={S} C={C} cout={t['cout']}", flush=True)
     got = checks.run_trans(t, dev)
