@@ -2038,8 +2038,8 @@ __global__ __launch_bounds__(DP_NT, 1) void k_dparts(D8sPartsArgs a) {
 // predecessor's MFMAs and before the next activation loads, so waiting for them never waits for the
 // activations still in flight.  Loads take a uniform base plus a 32-bit lane offset.
 // ------------------------------------------------------------------------------------------------
-template <int NT, int PT, int D>
-__global__ __launch_bounds__(256, NT <= 5 ? 2 : 1) void k_trans(D8sGemmArgs a) {
+template <int NT, int PT, int D, int WB>
+__global__ __launch_bounds__(256, NT <= 5 && WB < 4 ? 2 : 1) void k_trans(D8sGemmArgs a) {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     constexpr int PX = 32 * PT;                            // output pixels per workgroup
     constexpr int PLANE = PX * 2;                          // 16-byte chunks of one operand plane
@@ -2159,15 +2159,18 @@ __global__ __launch_bounds__(256, NT <= 5 ? 2 : 1) void k_trans(D8sGemmArgs a) {
         }
     };
 
-    // weights: two register sets when D is even (group g's in set g & 1, the next group's loaded before
-    // this group's prologue: a whole slot to arrive), one set otherwise (loaded after the MFMAs)
-    constexpr bool W2B = D % 2 == 0;
-    u32x4 raw[D][IT][RW], aw[W2B ? 2 : 1][NT];
+    // weights: WB register sets (WB | D): group g's in set g % WB, loaded WB - 1 groups ahead before
+    // a group's prologue (WB = 4 for the wide outputs, whose weights are most of the bytes and come
+    // from L2: one workgroup per CU then, the registers of four sets); one set when D is odd (loaded
+    // after the MFMAs)
+    static_assert(D % WB == 0, "weight sets divide the activation depth");
+    u32x4 raw[D][IT][RW], aw[WB][NT];
 #pragma unroll
     for (int d = 0; d < D; ++d)
 #pragma unroll
         for (int k = 0; k < IT; ++k) ld(k, d < G ? d : G - 1, raw[d][k]);
-    wload(0, aw[0]);
+#pragma unroll
+    for (int w = 0; w < (WB > 1 ? WB - 1 : 1); ++w) wload(w < G ? w : G - 1, aw[w]);
     __syncthreads();                                       // s_abh
     // D groups per step; the first step is peeled so that the loop's waits see only the steady state
     // (the preamble's load order would otherwise make them wait for every load)
@@ -2175,9 +2178,10 @@ __global__ __launch_bounds__(256, NT <= 5 ? 2 : 1) void k_trans(D8sGemmArgs a) {
 #pragma unroll
         for (int d = 0; d < D; ++d) {
             const int g = g0 + d;
-            u32x4* awc = aw[W2B ? d & 1 : 0];
-            if constexpr (W2B) {
-                wload(g + 1 < G ? g + 1 : g, aw[(d + 1) & 1]);
+            u32x4* awc = aw[d % WB];
+            if constexpr (WB > 1) {
+                const int gw = g + WB - 1 < G ? g + WB - 1 : G - 1;
+                wload(gw, aw[(d + WB - 1) % WB]);
                 __builtin_amdgcn_sched_barrier(0);         // issued ahead of the prologue
             }
             uint8_t* sb = (uint8_t*)(s_b + (g & 1) * 2 * PLANE);
@@ -2201,7 +2205,7 @@ __global__ __launch_bounds__(256, NT <= 5 ? 2 : 1) void k_trans(D8sGemmArgs a) {
             // (one set: the next group's weights now, before the activations), then this slot's
             // activations D groups on (the last groups reload the last one: the loads stay
             // unconditional and countable)
-            if constexpr (!W2B) {
+            if constexpr (WB == 1) {
                 wload(g + 1 < G ? g + 1 : g, aw[0]);
                 __builtin_amdgcn_sched_barrier(0);
             }
@@ -3106,23 +3110,32 @@ extern "C" int d8s_dense_block_parts(const D8sPartsArgs* a, void* stream) {
     return launched("d8s_dense_block_parts");
 }
 
-template <int NT, int PT, int D>
+template <int NT, int PT, int D, int WB>
 static int trans_launch_d(const D8sGemmArgs* a, hipStream_t st) {
     REQUIRE((int64_t)a->N * a->HW < (1ll << 31) && (int64_t)a->N * a->G0 * a->HW * 32 < (1ll << 32) &&
             (int64_t)a->N * a->HW * 32 < (1ll << 32), "d8s_transition: too many pixels");
     const int64_t NO = (int64_t)a->N * (a->HW / 4);
     const int64_t blocks = (NO + 32 * PT - 1) / (32 * PT);
     const size_t shm = (size_t)2 * 2 * 32 * PT * 32 + (size_t)a->G * 128;
-    hipLaunchKernelGGL((k_trans<NT, PT, D>), dim3((unsigned)blocks), dim3(256), shm, st, *a);
+    hipLaunchKernelGGL((k_trans<NT, PT, D, WB>), dim3((unsigned)blocks), dim3(256), shm, st, *a);
     return launched("d8s_transition");
 }
 
-// activation prefetch depth: the largest of 4, 2, 1 dividing the group count
+// activation prefetch depth: the largest of 4, 2, 1 dividing the group count.  Weights two groups
+// ahead (one if D is odd), or four for 4-5 output tiles per wave when the grid is at most one
+// workgroup per CU: there the weights are most of the loads and each workgroup's chain of groups is
+// the whole launch (a 24-image study's 32 x 32 transition: 52 -> 25 us); with more workgroups, two per
+// CU with two sets do better (one per CU with four: 52 -> 73 us at 96 images).
 template <int NT, int PT>
 static int trans_launch(const D8sGemmArgs* a, hipStream_t st) {
-    if (a->G % 4 == 0) return trans_launch_d<NT, PT, 4>(a, st);
-    if (a->G % 2 == 0) return trans_launch_d<NT, PT, 2>(a, st);
-    return trans_launch_d<NT, PT, 1>(a, st);
+    const int64_t blocks = ((int64_t)a->N * (a->HW / 4) + 32 * PT - 1) / (32 * PT);
+    if (a->G % 4 == 0) {
+        if constexpr (NT == 4 || NT == 5)
+            if (blocks <= cu_count()) return trans_launch_d<NT, PT, 4, 4>(a, st);
+        return trans_launch_d<NT, PT, 4, 2>(a, st);
+    }
+    if (a->G % 2 == 0) return trans_launch_d<NT, PT, 2, 2>(a, st);
+    return trans_launch_d<NT, PT, 1, 1>(a, st);
 }
 
 extern "C" int d8s_transition(const D8sGemmArgs* a, void* stream) {

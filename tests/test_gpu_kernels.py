@@ -216,6 +216,16 @@ def test_transition(dev, S, C, c0, cout):
     assert float((np.abs(q_x) == 127).mean()) < 0.2 and float((q_x == 0).mean()) < 0.5
 
 
+def test_transition_many_workgroups(dev):
+    """The 32 x 32 transition with more workgroups than CUs (two weight register sets, two workgroups
+    per CU) against the oracle; the parametrised cases above have small grids (four sets)."""
+    t = cases.trans_case(32, 1280, N=40, c0=256)
+    print("transition S=32 C=1280 N=40", flush=True)
+    got = checks.run_trans(t, dev)
+    _, q_x = checks.exact_trans(t)
+    assert np.array_equal(got, q_x), checks.bytes_cmp(got, q_x)
+
+
 @pytest.mark.parametrize("N,HW,C,c0", [(24, 256, 1664, 640), (3, 4, 128, 64), (2, 9, 96, 32)])
 def test_final(dev, N, HW, C, c0):
     rng = np.random.default_rng(HW)
