@@ -222,6 +222,21 @@ int d8s_final(const int8_t* in0, int32_t G0, const int8_t* seg, int32_t N, int32
  * in registers, one quantisation per pooled value), wider ones a tile kernel; both give the same bytes. */
 int d8s_stem(const D8sStemArgs* a, void* stream);
 
+/* Paired launches.  No counterpart in the reference: for callers running two encoders of the same
+ * geometry over the same batch shape (the final model's two weight seeds), each of these runs the
+ * same step for both in ONE launch -- the same work and bytes as the two single calls, but a 96-image
+ * pass's small late layers then fill the chip between them instead of one pass at a time (the 16 x 16
+ * whole block: 96 workgroups per pass, 192 for the pair in the time of one).  `a` and `b` must agree
+ * in every shape field (N, H, W, group counts, cout, input kind and flip); their buffers and tables
+ * are independent and must not overlap.  Kernel forms without a pair launch (split-K conv1, the 2-D
+ * fused tile, the wide-image stem) run as two launches. */
+int d8s_stem_pair(const D8sStemArgs* a, const D8sStemArgs* b, void* stream);
+int d8s_conv1_pair(const D8sGemmArgs* a, const D8sGemmArgs* b, void* stream);
+int d8s_conv2_pair(const D8sConv2Args* a, const D8sConv2Args* b, void* stream);
+int d8s_dense_pair(const D8sDenseArgs* a, const D8sDenseArgs* b, void* stream);
+int d8s_dense_block_pair(const D8sBlockArgs* a, const D8sBlockArgs* b, void* stream);
+int d8s_transition_pair(const D8sGemmArgs* a, const D8sGemmArgs* b, void* stream);
+
 /* ---- Upstream preprocessing: raw uint16 crops -> resize -> exact 1/99 percentiles -> uint8 ----------
  *
  * The reference turns the raw crop of every series into the uint8 stacks the encoder reads on the GPU

@@ -155,6 +155,19 @@ DEV int res_row(int v, int h) { return 8 * (v >> 2) + 4 * h + (v & 3); }
 // banks.  (Swapping every 4 rows leaves 2-way conflicts: measured 1.7x slower on gfx950.)
 DEV int swz(int r, int half) { return r * 2 + (half ^ ((r >> 3) & 1)); }
 
+// A launch may carry two problems of one shape (the same layer of two encoders' passes): workgroups
+// below `split` run the first arguments, the rest the second, the workgroup index and count rebased.
+// A single problem passes its arguments twice and split = the grid.
+struct PairSlot {
+    int bid, nblk;
+    bool second;
+};
+DEV PairSlot pair_slot(int split) {
+    const int b = (int)blockIdx.x;
+    const bool s = b >= split;
+    return {s ? b - split : b, s ? (int)gridDim.x - split : split, s};
+}
+
 // ------------------------------------------------------------------------------------------------
 // conv1: 1x1 GEMM, M = N*HW pixels, K = G*32 store channels, 128 outputs.
 // A wave computes 64 pixels x 128 outputs (2 x 4 MFMA tiles per K group) over the K groups of its
@@ -396,8 +409,11 @@ static size_t c1p_lds(int G, int wm) {
 // waves per SIMD hide the latency of layers with few tiles.  PF: activation groups in flight (4, or 8
 // where the registers allow); the K loop runs over G rounded up to a multiple of PF.
 template <bool ACC32, int WM, int U, int PF>
-__global__ __launch_bounds__(256, U == 2 ? 2 : 3) void k_conv1p(D8sGemmArgs a, int32_t* __restrict__ acc_out) {
+__global__ __launch_bounds__(256, U == 2 ? 2 : 3) void k_conv1p(D8sGemmArgs a0, int32_t* __restrict__ acc_out,
+                                                               D8sGemmArgs a1, int split) {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    const PairSlot ps = pair_slot(split);
+    const D8sGemmArgs a = ps.second ? a1 : a0;
     int32_t* s_wsum = (int32_t*)smem;                     // [128]
     float2* s_gd = (float2*)(s_wsum + 128);               // [128]
     uint32_t* s_abh = (uint32_t*)(s_gd + 128);            // [G * 32]
@@ -408,11 +424,11 @@ __global__ __launch_bounds__(256, U == 2 ? 2 : 3) void k_conv1p(D8sGemmArgs a, i
     const int h = lane >> 5, j = lane & 31;
     const int64_t rows = a.rows, HW = a.HW;
     const int ntiles = (int)((rows + 32 * U - 1) / (32 * U));
-    const int stride = (int)gridDim.x * 4;
+    const int stride = ps.nblk * 4;
     // the workgroup's tiles are first, first + 1, ..., first + 3 (then + stride ...): it runs while its
     // first tile exists, so its waves run in step (a wave past the last tile works on a repeat of the
     // last pixel and stores nothing)
-    int first = (int)blockIdx.x * 4;
+    int first = ps.bid * 4;
     if (first >= ntiles) return;                         // (uniform per workgroup)
     int tile = first + wave;
 
@@ -608,8 +624,11 @@ struct C2Shape {
 };
 
 template <int TW, int TH, int KSPL, int PT>
-__global__ __launch_bounds__(256, 2) void k_conv2(D8sConv2Args a, int tiles_x, int tiles_y) {
+__global__ __launch_bounds__(256, 2) void k_conv2(D8sConv2Args a0, int tiles_x, int tiles_y, D8sConv2Args a1,
+                                                  int split) {
     using S = C2Shape<TW, TH, KSPL, PT>;
+    const PairSlot ps = pair_slot(split);
+    const D8sConv2Args a = ps.second ? a1 : a0;
     constexpr int HWd = S::HWd, HP = S::HP, NCH = S::NCH;
     __shared__ __attribute__((aligned(16))) u32x4 s_w[4 * 9 * 32 * 2];
     extern __shared__ __attribute__((aligned(16))) u32x4 s_x[];       // [4][HP][2], then partial sums
@@ -683,11 +702,12 @@ __global__ __launch_bounds__(256, 2) void k_conv2(D8sConv2Args a, int tiles_x, i
     // a persistent grid gives XCD x one contiguous eighth of the tiles, walked by its workgroups
     // together: tiles in flight on one XCD are neighbours, and their shared halo rows hit its L2
     const int total = a.N * tiles_x * tiles_y;
-    int tile = blockIdx.x, tend = total, tstep = gridDim.x;
-    if (total > (int)gridDim.x && (gridDim.x & 7) == 0) {
-        const int chunk = (total + 7) / 8, xcd = blockIdx.x & 7;
-        tstep = gridDim.x >> 3;
-        tile = xcd * chunk + (int)(blockIdx.x >> 3);
+    // (a pair's split is a multiple of 8, so the rebased index keeps the XCD)
+    int tile = ps.bid, tend = total, tstep = ps.nblk;
+    if (total > ps.nblk && (ps.nblk & 7) == 0) {
+        const int chunk = (total + 7) / 8, xcd = ps.bid & 7;
+        tstep = ps.nblk >> 3;
+        tile = xcd * chunk + (ps.bid >> 3);
         tend = min(total, (xcd + 1) * chunk);
     }
     if (tile >= tend) return;
@@ -1137,8 +1157,10 @@ DEV uint32_t bn_off(int ry, int H, int W, int x, int h) {
 // is told so, or it sinks the prefetched LDS operands next to their MFMAs to save registers)
 template <int W_, int GM>
 __global__ __launch_bounds__(512, 1) __attribute__((amdgpu_waves_per_eu(2, 2)))
-void k_band(D8sDenseArgs a, int bands, int band_rows) {
+void k_band(D8sDenseArgs a0, int bands, int band_rows, D8sDenseArgs a1, int split) {
     using S = BnShape<W_>;
+    const PairSlot ps = pair_slot(split);
+    const D8sDenseArgs a = ps.second ? a1 : a0;
     constexpr int TPR = S::TPR, RS = S::RS, SL = S::SL, PS = S::PS, NT = 512;
     __shared__ __attribute__((aligned(16))) u32x4 s_w[4 * 9 * 32 * 2];    // conv2 weights, 36 KB
     extern __shared__ __attribute__((aligned(16))) u32x4 s_dyn[];
@@ -1156,7 +1178,7 @@ void k_band(D8sDenseArgs a, int bands, int band_rows) {
     const int h = lane >> 5, j = lane & 31;
     const int rw = wave / TPR, cb = wave - rw * TPR;
     const int x = 32 * cb + j;
-    const int n = blockIdx.x / bands, band = blockIdx.x - n * bands;
+    const int n = ps.bid / bands, band = ps.bid - n * bands;
     const int y0 = band * band_rows, nr = min(band_rows, H - y0);
     const int M = (nr + RS - 1) / RS;                                     // conv2 steps
     const int64_t HW = (int64_t)H * W_;
@@ -1441,7 +1463,9 @@ static size_t dblock_lds(int H, int W, int Gmax) {
     return (size_t)(H + 2) * (W + 2) * 128 + DB_PRM + (size_t)Gmax * 128 + 2 * 8 * 4096;
 }
 
-__global__ __launch_bounds__(DB_NT, 1) void k_dblock(D8sBlockArgs a) {
+__global__ __launch_bounds__(DB_NT, 1) void k_dblock(D8sBlockArgs a0, D8sBlockArgs a1, int split) {
+    const PairSlot ps = pair_slot(split);
+    const D8sBlockArgs a = ps.second ? a1 : a0;
     __shared__ __attribute__((aligned(16))) u32x4 s_w[2304];              // conv2 weights, 36 KB
     extern __shared__ __attribute__((aligned(16))) u32x4 s_dyn[];
     const int H = a.H, W = a.W, HW = H * W, BW = W + 2, WIN = (H + 2) * (W + 2);
@@ -1457,7 +1481,7 @@ __global__ __launch_bounds__(DB_NT, 1) void k_dblock(D8sBlockArgs a) {
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int h = lane >> 5, j = lane & 31;
-    const int n = blockIdx.x;
+    const int n = ps.bid;
 
     // zero-padding ring of the window (the layers write only its interior)
     {
@@ -2039,7 +2063,9 @@ __global__ __launch_bounds__(DP_NT, 1) void k_dparts(D8sPartsArgs a) {
 // activations still in flight.  Loads take a uniform base plus a 32-bit lane offset.
 // ------------------------------------------------------------------------------------------------
 template <int NT, int PT, int D, int WB>
-__global__ __launch_bounds__(256, NT <= 5 && WB < 4 ? 2 : 1) void k_trans(D8sGemmArgs a) {
+__global__ __launch_bounds__(256, NT <= 5 && WB < 4 ? 2 : 1) void k_trans(D8sGemmArgs a0, D8sGemmArgs a1, int split) {
+    const PairSlot ps = pair_slot(split);
+    const D8sGemmArgs a = ps.second ? a1 : a0;
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     constexpr int PX = 32 * PT;                            // output pixels per workgroup
     constexpr int PLANE = PX * 2;                          // 16-byte chunks of one operand plane
@@ -2056,7 +2082,7 @@ __global__ __launch_bounds__(256, NT <= 5 && WB < 4 ? 2 : 1) void k_trans(D8sGem
     const uint32_t HW = (uint32_t)a.HW, W = (uint32_t)a.W;
     const uint32_t W2 = W >> 1, HW4 = HW >> 2;
     const uint32_t NO = (uint32_t)a.N * HW4;
-    const uint32_t op0 = blockIdx.x * (uint32_t)PX;
+    const uint32_t op0 = (uint32_t)ps.bid * (uint32_t)PX;
     const int OT = a.cout >> 5;
 
     // staging items of this thread.  Narrow (PT < 4): item = tid + 256 k -> channel quad cq = item & 7,
@@ -2681,7 +2707,10 @@ DEV uint32_t bits_of(float x) { return __builtin_bit_cast(uint32_t, x); }
     } while (0)
 
 template <bool U8>
-__global__ __launch_bounds__(512, 1) void k_stem_rows(D8sStemArgs a, int bands, int band_rows) {
+__global__ __launch_bounds__(512, 1) void k_stem_rows(D8sStemArgs a0, int bands, int band_rows, D8sStemArgs a1,
+                                                      int split) {
+    const PairSlot ps = pair_slot(split);
+    const D8sStemArgs a = ps.second ? a1 : a0;
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     uint32_t* s_ring = (uint32_t*)smem;                                 // [3][SR_CH]
     _Float16* s_wt = (_Float16*)(s_ring + 3 * SR_CH);                   // [64][SR_WROW]
@@ -2693,7 +2722,7 @@ __global__ __launch_bounds__(512, 1) void k_stem_rows(D8sStemArgs a, int bands, 
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int h = lane >> 5, j = lane & 31, rr = j >> 4, i = j & 15;
     const int Hp = a.H >> 2, Wp = a.W >> 2, W4 = a.W >> 2;
-    const int n = blockIdx.x / bands, band = blockIdx.x - n * bands;
+    const int n = ps.bid / bands, band = ps.bid - n * bands;
     const int py0 = band * band_rows, npy = min(band_rows, Hp - py0);
     const int half = a.N >> 1;
     const int ns = (a.flip == 2 && n >= half) ? n - half : n;          // source image
@@ -2893,28 +2922,38 @@ static int check_gemm(const D8sGemmArgs* a, const char* what) {
     return 0;
 }
 
-static int conv1_launch(const D8sGemmArgs* a, int32_t* acc, hipStream_t st) {
+// Pairs (`b` not null): two problems of one shape in one launch (PairSlot); sizes and the variant
+// are chosen for the two problems' pixels together, persistent grids split evenly between them.
+static bool same_gemm(const D8sGemmArgs* a, const D8sGemmArgs* b) {
+    return a->G0 == b->G0 && a->G == b->G && a->N == b->N && a->HW == b->HW && a->W == b->W &&
+           a->rows == b->rows && a->cout == b->cout && a->G0n == b->G0n;
+}
+
+static int conv1_launch(const D8sGemmArgs* a, const D8sGemmArgs* b, int32_t* acc, hipStream_t st) {
     if (int rc = check_gemm(a, "d8s_conv1")) return rc;
     REQUIRE(a->cout == 128, "d8s_conv1: cout must be 128");
     REQUIRE(acc != nullptr || a->out != nullptr, "d8s_conv1: null output");
+    const int np = b ? 2 : 1;                              // problems in the launch
+    const int64_t rows = a->rows * np;
     // k-slices: the fewest that give at least 1.5 workgroups per CU
     const int64_t want = 3 * (int64_t)cu_count() / 2;
     int ks = 1;
-    while (ks < 4 && (a->rows + 64 * 4 / ks - 1) / (64 * 4 / ks) < want) ks *= 2;
+    while (ks < 4 && (rows + 64 * 4 / ks - 1) / (64 * 4 / ks) < want) ks *= 2;
     // one k-slice: the persistent form (the weights through LDS); 64-pixel tiles when every wave of
     // two per SIMD gets at least two, else 32-pixel tiles and three waves per SIMD
     const int64_t in0_bytes = (int64_t)a->N * a->G0 * a->HW * 32, slot_bytes = (int64_t)a->rows * 32;
     if (ks == 1 && a->rows < (1ll << 34) && in0_bytes < (1ll << 32) && slot_bytes < (1ll << 32)) {
-        const int u = (a->rows + 63) / 64 >= 2 * 8 * (int64_t)cu_count() ? 2 : 1;
-        const int64_t ntiles = (a->rows + 32 * u - 1) / (32 * u);
+        const int u = (rows + 63) / 64 >= 2 * 8 * (int64_t)cu_count() ? 2 : 1;
+        const int64_t ntiles = (rows + 32 * u - 1) / (32 * u);
         const int per_cu = u == 2 ? 2 : 3;                        // workgroups per CU
         const int64_t want_blocks = (ntiles + 3) / 4;
-        const unsigned grid = (unsigned)(want_blocks < per_cu * cu_count() ? want_blocks : per_cu * cu_count());
+        const int64_t all = want_blocks < per_cu * cu_count() ? want_blocks : per_cu * cu_count();
+        const unsigned split = (unsigned)((all + np - 1) / np), grid = split * np;
         const int wm = c1p_lds(a->G, 1) <= (size_t)(160 / per_cu) * 1024 ? 1 : 2;   // still per_cu per CU
         const size_t shm1 = c1p_lds(a->G, wm);
 #define C1P_LAUNCH(ACC_, WM_, U_)                                                                 \
     hipLaunchKernelGGL((k_conv1p<ACC_, WM_, U_, U_ == 1 && WM_ == 1 ? 8 : 4>), dim3(grid), dim3(256), shm1,  \
-                       st, *a, ACC_ ? acc : nullptr)
+                       st, *a, ACC_ ? acc : nullptr, b ? *b : *a, (int)split)
         if (u == 2) {
             if (acc && wm == 1) C1P_LAUNCH(true, 1, 2);
             else if (acc) C1P_LAUNCH(true, 2, 2);
@@ -2928,6 +2967,10 @@ static int conv1_launch(const D8sGemmArgs* a, int32_t* acc, hipStream_t st) {
         }
 #undef C1P_LAUNCH
         return launched("d8s_conv1");
+    }
+    if (b) {                                               // the split-K form: two launches
+        if (int rc = conv1_launch(a, nullptr, acc, st)) return rc;
+        return conv1_launch(b, nullptr, acc, st);
     }
     const int px = 64 * 4 / ks;
     const unsigned blocks = (unsigned)((a->rows + px - 1) / px);
@@ -2950,45 +2993,72 @@ static int conv1_launch(const D8sGemmArgs* a, int32_t* acc, hipStream_t st) {
 
 extern "C" int d8s_conv1(const D8sGemmArgs* a, void* stream) {
     if (a != nullptr && a->out == nullptr) return fail((int)hipErrorInvalidValue, "d8s_conv1: null output");
-    return conv1_launch(a, nullptr, (hipStream_t)stream);
+    return conv1_launch(a, nullptr, nullptr, (hipStream_t)stream);
 }
 
 extern "C" int d8s_conv1_acc32(const D8sGemmArgs* a, int32_t* acc, void* stream) {
     REQUIRE(acc != nullptr, "d8s_conv1_acc32: null accumulator buffer");
-    return conv1_launch(a, acc, (hipStream_t)stream);
+    return conv1_launch(a, nullptr, acc, (hipStream_t)stream);
+}
+
+extern "C" int d8s_conv1_pair(const D8sGemmArgs* a, const D8sGemmArgs* b, void* stream) {
+    REQUIRE(a != nullptr && b != nullptr, "d8s_conv1_pair: null arguments");
+    REQUIRE(a->out != nullptr, "d8s_conv1_pair: null output");
+    if (int rc = check_gemm(b, "d8s_conv1_pair")) return rc;
+    REQUIRE(b->out != nullptr, "d8s_conv1_pair: null output");
+    REQUIRE(same_gemm(a, b), "d8s_conv1_pair: the two problems differ in shape");
+    return conv1_launch(a, b, nullptr, (hipStream_t)stream);
 }
 
 template <int TW, int TH, int KSPL, int PT>
-static int conv2_launch(const D8sConv2Args* a, hipStream_t st, int64_t min_tiles) {
+static int conv2_launch(const D8sConv2Args* a, const D8sConv2Args* b, hipStream_t st, int64_t min_tiles) {
     using S = C2Shape<TW, TH, KSPL, PT>;
+    const int np = b ? 2 : 1;
     const int tiles_x = (a->W + TW - 1) / TW, tiles_y = (a->H + TH - 1) / TH;
-    const int64_t total = (int64_t)a->N * tiles_x * tiles_y;
-    if (total < min_tiles) return -1;
-    REQUIRE(total < (1ll << 31), "d8s_conv2: too many tiles");
-    const unsigned grid = (unsigned)(total < 2 * cu_count() ? total : 2 * cu_count());
-    hipLaunchKernelGGL((k_conv2<TW, TH, KSPL, PT>), dim3(grid), dim3(256), S::HALO_BYTES + S::RED_BYTES,
-                       st, *a, tiles_x, tiles_y);
+    const int64_t total = (int64_t)a->N * tiles_x * tiles_y;            // per problem
+    if (total * np < min_tiles) return -1;
+    REQUIRE(total * np < (1ll << 31), "d8s_conv2: too many tiles");
+    const int64_t all = total * np < 2 * cu_count() ? total * np : 2 * cu_count();
+    int64_t split = (all + np - 1) / np;
+    if (np == 2 && split > 8) split = (split + 7) / 8 * 8;   // a rebased workgroup keeps its XCD
+    hipLaunchKernelGGL((k_conv2<TW, TH, KSPL, PT>), dim3((unsigned)(split * np)), dim3(256),
+                       S::HALO_BYTES + S::RED_BYTES, st, *a, tiles_x, tiles_y, b ? *b : *a, (int)split);
     return launched("d8s_conv2");
 }
 
-extern "C" int d8s_conv2(const D8sConv2Args* a, void* stream) {
-    REQUIRE(a != nullptr, "d8s_conv2: null arguments");
-    REQUIRE(a->x && a->w && a->sc && a->wsum && a->out, "d8s_conv2: null pointer");
-    REQUIRE(a->N >= 1 && a->H >= 1 && a->W >= 1, "d8s_conv2: N, H, W must be >= 1");
-    hipStream_t st = (hipStream_t)stream;
+static int check_conv2(const D8sConv2Args* a, const char* what) {
+    REQUIRE(a != nullptr, std::string(what) + ": null arguments");
+    REQUIRE(a->x && a->w && a->sc && a->wsum && a->out, std::string(what) + ": null pointer");
+    REQUIRE(a->N >= 1 && a->H >= 1 && a->W >= 1, std::string(what) + ": N, H, W must be >= 1");
+    return 0;
+}
+
+static int conv2_dispatch(const D8sConv2Args* a, const D8sConv2Args* b, hipStream_t st) {
     const int64_t enough = 3 * (int64_t)cu_count();        // tiles for a persistent grid to pipeline
     if (a->W >= 32) {
-        int rc = conv2_launch<32, 8, 1, 2>(a, st, enough);
+        int rc = conv2_launch<32, 8, 1, 2>(a, b, st, enough);
         if (rc >= 0) return rc;
-        rc = conv2_launch<32, 4, 1, 1>(a, st, enough);
+        rc = conv2_launch<32, 4, 1, 1>(a, b, st, enough);
         if (rc >= 0) return rc;
-        return conv2_launch<32, 2, 4, 2>(a, st, 0);
+        return conv2_launch<32, 2, 4, 2>(a, b, st, 0);
     }
-    if (a->W >= 16) return conv2_launch<16, 4, 4, 2>(a, st, 0);
-    if (a->W >= 8) return conv2_launch<8, 8, 4, 2>(a, st, 0);
-    if (a->W >= 4) return conv2_launch<4, 16, 4, 2>(a, st, 0);
-    if (a->W >= 2) return conv2_launch<2, 32, 4, 2>(a, st, 0);
-    return conv2_launch<1, 64, 4, 2>(a, st, 0);
+    if (a->W >= 16) return conv2_launch<16, 4, 4, 2>(a, b, st, 0);
+    if (a->W >= 8) return conv2_launch<8, 8, 4, 2>(a, b, st, 0);
+    if (a->W >= 4) return conv2_launch<4, 16, 4, 2>(a, b, st, 0);
+    if (a->W >= 2) return conv2_launch<2, 32, 4, 2>(a, b, st, 0);
+    return conv2_launch<1, 64, 4, 2>(a, b, st, 0);
+}
+
+extern "C" int d8s_conv2(const D8sConv2Args* a, void* stream) {
+    if (int rc = check_conv2(a, "d8s_conv2")) return rc;
+    return conv2_dispatch(a, nullptr, (hipStream_t)stream);
+}
+
+extern "C" int d8s_conv2_pair(const D8sConv2Args* a, const D8sConv2Args* b, void* stream) {
+    if (int rc = check_conv2(a, "d8s_conv2_pair")) return rc;
+    if (int rc = check_conv2(b, "d8s_conv2_pair")) return rc;
+    REQUIRE(a->N == b->N && a->H == b->H && a->W == b->W, "d8s_conv2_pair: the two problems differ in shape");
+    return conv2_dispatch(a, b, (hipStream_t)stream);
 }
 
 template <int TW, int TH, int CPW, int NW>
@@ -3015,18 +3085,21 @@ static int dense_launch(const D8sDenseArgs* a, hipStream_t st) {
 // Band form for W = 64 / 128 while the layer's conv1 weights fit in LDS: bands of 32, 16, 8 .. rows
 // (a multiple of the rows per step), the largest that still gives 3 workgroups per CU.
 template <int W_>
-static int band_launch(const D8sDenseArgs* a, hipStream_t st) {
+static int band_launch(const D8sDenseArgs* a, const D8sDenseArgs* b, hipStream_t st) {
     using S = BnShape<W_>;
     const size_t shm = S::lds(a->G);
     if (shm + 36864 > 160 * 1024 || a->G > 16) return -1;
+    const int np = b ? 2 : 1;
     int rows = 32;
-    while (rows > S::RS && (int64_t)a->N * ((a->H + rows - 1) / rows) < 3 * (int64_t)cu_count()) rows /= 2;
+    while (rows > S::RS && (int64_t)a->N * np * ((a->H + rows - 1) / rows) < 3 * (int64_t)cu_count()) rows /= 2;
     const int bands = (a->H + rows - 1) / rows;
-    const int64_t blocks = (int64_t)a->N * bands;
-    REQUIRE(blocks < (1ll << 31), "d8s_dense: too many bands");
+    const int64_t blocks = (int64_t)a->N * bands;          // per problem
+    REQUIRE(blocks * np < (1ll << 31), "d8s_dense: too many bands");
     // activation registers (K steps per step): G itself up to 8, then G rounded up to even
     const int gm = a->G <= 8 ? a->G : (a->G + 1) & ~1;
-#define BN_LAUNCH(GM_) hipLaunchKernelGGL((k_band<W_, GM_>), dim3((unsigned)blocks), dim3(512), shm, st, *a, bands, rows)
+#define BN_LAUNCH(GM_)                                                                             \
+    hipLaunchKernelGGL((k_band<W_, GM_>), dim3((unsigned)(blocks * np)), dim3(512), shm, st, *a, bands, rows, \
+                       b ? *b : *a, (int)blocks)
     switch (gm) {
         case 1: BN_LAUNCH(1); break;
         case 2: BN_LAUNCH(2); break;
@@ -3045,26 +3118,47 @@ static int band_launch(const D8sDenseArgs* a, hipStream_t st) {
     return launched("d8s_dense");
 }
 
-extern "C" int d8s_dense(const D8sDenseArgs* a, void* stream) {
-    REQUIRE(a != nullptr, "d8s_dense: null arguments");
+static int check_dense(const D8sDenseArgs* a, const char* what) {
+    REQUIRE(a != nullptr, std::string(what) + ": null arguments");
     REQUIRE(a->in0 && a->w1 && a->abh && a->gd && a->w1sum && a->w2 && a->sc && a->w2sum && a->out,
-            "d8s_dense: null pointer");
+            std::string(what) + ": null pointer");
     REQUIRE(a->G0 >= 1 && a->G >= 1 && a->N >= 1 && a->H >= 1 && a->W >= 1,
-            "d8s_dense: G0, G, N, H, W must be >= 1");
-    REQUIRE(a->G <= a->G0 || a->seg != nullptr, "d8s_dense: seg is null with G > G0");
-    REQUIRE(a->G <= 512, "d8s_dense: more than 512 groups");
-    REQUIRE((int64_t)a->H * a->W <= (1 << 26), "d8s_dense: more than 2^26 pixels per image");
-    hipStream_t st = (hipStream_t)stream;
+            std::string(what) + ": G0, G, N, H, W must be >= 1");
+    REQUIRE(a->G <= a->G0 || a->seg != nullptr, std::string(what) + ": seg is null with G > G0");
+    REQUIRE(a->G <= 512, std::string(what) + ": more than 512 groups");
+    REQUIRE((int64_t)a->H * a->W <= (1 << 26), std::string(what) + ": more than 2^26 pixels per image");
+    return 0;
+}
+
+// (the 2-D tile form has no pair launch: a pair runs as two launches)
+static int dense_dispatch(const D8sDenseArgs* a, const D8sDenseArgs* b, hipStream_t st) {
     if (a->W == 128 || a->W == 64) {
-        const int rc = a->W == 128 ? band_launch<128>(a, st) : band_launch<64>(a, st);
+        const int rc = a->W == 128 ? band_launch<128>(a, b, st) : band_launch<64>(a, b, st);
         if (rc >= 0) return rc;
+    }
+    if (b) {
+        if (int rc = dense_dispatch(a, nullptr, st)) return rc;
+        return dense_dispatch(b, nullptr, st);
     }
     if (a->W >= 32) return dense_launch<32, 12, 2, 8>(a, st);
     if (a->W <= 16 && a->H <= 16) return dense_launch<16, 16, 1, 8>(a, st);
     return dense_launch<16, 12, 1, 8>(a, st);
 }
 
-static int dblock_launch(const D8sBlockArgs* a, hipStream_t st) {
+extern "C" int d8s_dense(const D8sDenseArgs* a, void* stream) {
+    if (int rc = check_dense(a, "d8s_dense")) return rc;
+    return dense_dispatch(a, nullptr, (hipStream_t)stream);
+}
+
+extern "C" int d8s_dense_pair(const D8sDenseArgs* a, const D8sDenseArgs* b, void* stream) {
+    if (int rc = check_dense(a, "d8s_dense_pair")) return rc;
+    if (int rc = check_dense(b, "d8s_dense_pair")) return rc;
+    REQUIRE(a->G0 == b->G0 && a->G == b->G && a->N == b->N && a->H == b->H && a->W == b->W,
+            "d8s_dense_pair: the two problems differ in shape");
+    return dense_dispatch(a, b, (hipStream_t)stream);
+}
+
+static int dblock_launch(const D8sBlockArgs* a, const D8sBlockArgs* b, hipStream_t st) {
     REQUIRE(a != nullptr, "d8s_dense_block: null arguments");
     REQUIRE(a->in0 && a->layers && (a->L <= 0 || a->seg), "d8s_dense_block: null pointer");
     REQUIRE(a->G0 >= 1 && a->L >= 1 && a->N >= 1 && a->H >= 1 && a->W >= 1,
@@ -3073,12 +3167,21 @@ static int dblock_launch(const D8sBlockArgs* a, hipStream_t st) {
     REQUIRE(a->G0 + a->L - 1 <= 4 * DB_NT / 32, "d8s_dense_block: more than 64 groups");
     const size_t shm = dblock_lds(a->H, a->W, a->G0 + a->L - 1);
     REQUIRE(shm + 36864 <= 160 * 1024, "d8s_dense_block: block too large for LDS");
-    hipLaunchKernelGGL(k_dblock, dim3((unsigned)a->N), dim3(DB_NT), shm, st, *a);
+    const int np = b ? 2 : 1;
+    hipLaunchKernelGGL(k_dblock, dim3((unsigned)(a->N * np)), dim3(DB_NT), shm, st, *a, b ? *b : *a, a->N);
     return launched("d8s_dense_block");
 }
 
 extern "C" int d8s_dense_block(const D8sBlockArgs* a, void* stream) {
-    return dblock_launch(a, (hipStream_t)stream);
+    return dblock_launch(a, nullptr, (hipStream_t)stream);
+}
+
+extern "C" int d8s_dense_block_pair(const D8sBlockArgs* a, const D8sBlockArgs* b, void* stream) {
+    REQUIRE(a != nullptr && b != nullptr, "d8s_dense_block_pair: null arguments");
+    REQUIRE(b->in0 && b->layers && (b->L <= 0 || b->seg), "d8s_dense_block_pair: null pointer");
+    REQUIRE(a->N == b->N && a->H == b->H && a->W == b->W && a->G0 == b->G0 && a->L == b->L,
+            "d8s_dense_block_pair: the two problems differ in shape");
+    return dblock_launch(a, b, (hipStream_t)stream);
 }
 
 extern "C" int d8s_dense_block_parts(const D8sPartsArgs* a, void* stream) {
@@ -3111,13 +3214,15 @@ extern "C" int d8s_dense_block_parts(const D8sPartsArgs* a, void* stream) {
 }
 
 template <int NT, int PT, int D, int WB>
-static int trans_launch_d(const D8sGemmArgs* a, hipStream_t st) {
+static int trans_launch_d(const D8sGemmArgs* a, const D8sGemmArgs* b, hipStream_t st) {
     REQUIRE((int64_t)a->N * a->HW < (1ll << 31) && (int64_t)a->N * a->G0 * a->HW * 32 < (1ll << 32) &&
             (int64_t)a->N * a->HW * 32 < (1ll << 32), "d8s_transition: too many pixels");
     const int64_t NO = (int64_t)a->N * (a->HW / 4);
     const int64_t blocks = (NO + 32 * PT - 1) / (32 * PT);
     const size_t shm = (size_t)2 * 2 * 32 * PT * 32 + (size_t)a->G * 128;
-    hipLaunchKernelGGL((k_trans<NT, PT, D, WB>), dim3((unsigned)blocks), dim3(256), shm, st, *a);
+    const int np = b ? 2 : 1;
+    hipLaunchKernelGGL((k_trans<NT, PT, D, WB>), dim3((unsigned)(blocks * np)), dim3(256), shm, st, *a,
+                       b ? *b : *a, (int)blocks);
     return launched("d8s_transition");
 }
 
@@ -3127,34 +3232,49 @@ static int trans_launch_d(const D8sGemmArgs* a, hipStream_t st) {
 // the whole launch (a 24-image study's 32 x 32 transition: 52 -> 25 us); with more workgroups, two per
 // CU with two sets do better (one per CU with four: 52 -> 73 us at 96 images).
 template <int NT, int PT>
-static int trans_launch(const D8sGemmArgs* a, hipStream_t st) {
-    const int64_t blocks = ((int64_t)a->N * (a->HW / 4) + 32 * PT - 1) / (32 * PT);
+static int trans_launch(const D8sGemmArgs* a, const D8sGemmArgs* b, hipStream_t st) {
+    const int64_t blocks = ((int64_t)a->N * (a->HW / 4) + 32 * PT - 1) / (32 * PT) * (b ? 2 : 1);
     if (a->G % 4 == 0) {
         if constexpr (NT == 4 || NT == 5)
-            if (blocks <= cu_count()) return trans_launch_d<NT, PT, 4, 4>(a, st);
-        return trans_launch_d<NT, PT, 4, 2>(a, st);
+            if (blocks <= cu_count()) return trans_launch_d<NT, PT, 4, 4>(a, b, st);
+        return trans_launch_d<NT, PT, 4, 2>(a, b, st);
     }
-    if (a->G % 2 == 0) return trans_launch_d<NT, PT, 2, 2>(a, st);
-    return trans_launch_d<NT, PT, 1, 1>(a, st);
+    if (a->G % 2 == 0) return trans_launch_d<NT, PT, 2, 2>(a, b, st);
+    return trans_launch_d<NT, PT, 1, 1>(a, b, st);
+}
+
+static int check_trans(const D8sGemmArgs* a, const char* what) {
+    if (int rc = check_gemm(a, what)) return rc;
+    REQUIRE(a->out != nullptr, std::string(what) + ": null output");
+    REQUIRE(a->cout >= 32 && a->cout % 32 == 0 && a->cout <= 1024,
+            std::string(what) + ": cout must be a multiple of 32 in [32, 1024]");
+    REQUIRE(a->G0n == a->cout / 32, std::string(what) + ": G0n != cout / 32");
+    REQUIRE(a->W % 2 == 0 && (a->HW / a->W) % 2 == 0, std::string(what) + ": H and W must be even");
+    return 0;
+}
+
+static int trans_dispatch(const D8sGemmArgs* a, const D8sGemmArgs* b, hipStream_t st) {
+    switch ((a->cout / 32 + 3) / 4) {                      // output tiles per wave
+        case 1: return trans_launch<1, 4>(a, b, st);
+        case 2: return trans_launch<2, 2>(a, b, st);
+        case 3: return trans_launch<3, 1>(a, b, st);
+        case 4: return trans_launch<4, 1>(a, b, st);
+        case 5: return trans_launch<5, 1>(a, b, st);
+        case 6: return trans_launch<6, 1>(a, b, st);
+        default: return trans_launch<8, 1>(a, b, st);
+    }
 }
 
 extern "C" int d8s_transition(const D8sGemmArgs* a, void* stream) {
-    if (int rc = check_gemm(a, "d8s_transition")) return rc;
-    REQUIRE(a->out != nullptr, "d8s_transition: null output");
-    REQUIRE(a->cout >= 32 && a->cout % 32 == 0 && a->cout <= 1024,
-            "d8s_transition: cout must be a multiple of 32 in [32, 1024]");
-    REQUIRE(a->G0n == a->cout / 32, "d8s_transition: G0n != cout / 32");
-    REQUIRE(a->W % 2 == 0 && (a->HW / a->W) % 2 == 0, "d8s_transition: H and W must be even");
-    hipStream_t st = (hipStream_t)stream;
-    switch ((a->cout / 32 + 3) / 4) {                      // output tiles per wave
-        case 1: return trans_launch<1, 4>(a, st);
-        case 2: return trans_launch<2, 2>(a, st);
-        case 3: return trans_launch<3, 1>(a, st);
-        case 4: return trans_launch<4, 1>(a, st);
-        case 5: return trans_launch<5, 1>(a, st);
-        case 6: return trans_launch<6, 1>(a, st);
-        default: return trans_launch<8, 1>(a, st);
-    }
+    if (int rc = check_trans(a, "d8s_transition")) return rc;
+    return trans_dispatch(a, nullptr, (hipStream_t)stream);
+}
+
+extern "C" int d8s_transition_pair(const D8sGemmArgs* a, const D8sGemmArgs* b, void* stream) {
+    if (int rc = check_trans(a, "d8s_transition_pair")) return rc;
+    if (int rc = check_trans(b, "d8s_transition_pair")) return rc;
+    REQUIRE(same_gemm(a, b), "d8s_transition_pair: the two problems differ in shape");
+    return trans_dispatch(a, b, (hipStream_t)stream);
 }
 
 extern "C" int d8s_final(const int8_t* in0, int32_t G0, const int8_t* seg, int32_t N, int32_t HW,
@@ -3169,42 +3289,65 @@ extern "C" int d8s_final(const int8_t* in0, int32_t G0, const int8_t* seg, int32
     return launched("d8s_final");
 }
 
-extern "C" int d8s_stem(const D8sStemArgs* a, void* stream) {
-    REQUIRE(a != nullptr, "d8s_stem: null arguments");
-    REQUIRE(a->x && a->w16 && a->bias && a->inv && a->out, "d8s_stem: null pointer");
+static int check_stem(const D8sStemArgs* a, const char* what) {
+    const std::string w(what);
+    REQUIRE(a != nullptr, w + ": null arguments");
+    REQUIRE(a->x && a->w16 && a->bias && a->inv && a->out, w + ": null pointer");
     REQUIRE(a->kind == D8S_IN_F16 || (a->kind == D8S_IN_U8 && a->lut != nullptr),
-            "d8s_stem: kind must be D8S_IN_F16, or D8S_IN_U8 with a lut");
+            w + ": kind must be D8S_IN_F16, or D8S_IN_U8 with a lut");
     REQUIRE(a->N >= 1 && a->H >= 4 && a->W >= 4 && a->H % 4 == 0 && a->W % 4 == 0,
-            "d8s_stem: H and W must be positive multiples of 4");
-    REQUIRE(a->kind != D8S_IN_U8 || ((uintptr_t)a->x & 3) == 0, "d8s_stem: uint8 input not 4-byte aligned");
+            w + ": H and W must be positive multiples of 4");
+    REQUIRE(a->kind != D8S_IN_U8 || ((uintptr_t)a->x & 3) == 0, w + ": uint8 input not 4-byte aligned");
     REQUIRE(a->flip >= 0 && a->flip <= 2 && (a->flip != 2 || a->N % 2 == 0),
-            "d8s_stem: flip must be 0, 1, or 2 (TTA pairs, N even)");
+            w + ": flip must be 0, 1, or 2 (TTA pairs, N even)");
     REQUIRE(a->kind != D8S_IN_F16 || a->W > 64 * SR_NWV || ((uintptr_t)a->x & 7) == 0,
-            "d8s_stem: fp16 input not 8-byte aligned");
+            w + ": fp16 input not 8-byte aligned");
+    return 0;
+}
+
+// (the tile form, for widths past the row-band form's, has no pair launch: a pair runs as two)
+static int stem_dispatch(const D8sStemArgs* a, const D8sStemArgs* b, hipStream_t st) {
     const int Hp = a->H / 4, Wp = a->W / 4;
     if (a->W <= 64 * SR_NWV && (int64_t)(a->flip == 2 ? a->N / 2 : a->N) * 3 * a->H * a->W < (1ll << 31)) {
         // row bands: one wave per 32 conv columns; 16 pooled rows per band while that leaves at
         // least one workgroup per CU, else fewer
+        const int np = b ? 2 : 1;
         const int nwv = (a->W / 2 + 31) / 32;
         int rows = 16;
-        while (rows > 2 && (int64_t)a->N * ((Hp + rows - 1) / rows) < cu_count()) rows /= 2;
+        while (rows > 2 && (int64_t)a->N * np * ((Hp + rows - 1) / rows) < cu_count()) rows /= 2;
         const int bands = (Hp + rows - 1) / rows;
-        const int64_t blocks = (int64_t)a->N * bands;
-        REQUIRE(blocks < (1ll << 31), "d8s_stem: too many bands");
+        const int64_t blocks = (int64_t)a->N * bands;      // per problem
+        REQUIRE(blocks * np < (1ll << 31), "d8s_stem: too many bands");
         if (a->kind == D8S_IN_U8)
-            hipLaunchKernelGGL(k_stem_rows<true>, dim3((unsigned)blocks), dim3(64 * nwv), SR_LDS,
-                               (hipStream_t)stream, *a, bands, rows);
+            hipLaunchKernelGGL(k_stem_rows<true>, dim3((unsigned)(blocks * np)), dim3(64 * nwv), SR_LDS, st,
+                               *a, bands, rows, b ? *b : *a, (int)blocks);
         else
-            hipLaunchKernelGGL(k_stem_rows<false>, dim3((unsigned)blocks), dim3(64 * nwv), SR_LDS,
-                               (hipStream_t)stream, *a, bands, rows);
+            hipLaunchKernelGGL(k_stem_rows<false>, dim3((unsigned)(blocks * np)), dim3(64 * nwv), SR_LDS, st,
+                               *a, bands, rows, b ? *b : *a, (int)blocks);
         return launched("d8s_stem");
+    }
+    if (b) {
+        if (int rc = stem_dispatch(a, nullptr, st)) return rc;
+        return stem_dispatch(b, nullptr, st);
     }
     const int tiles_x = (Wp + ST_PX - 1) / ST_PX, tiles_y = (Hp + ST_PY - 1) / ST_PY;
     const int64_t blocks = (int64_t)a->N * tiles_x * tiles_y;
     REQUIRE(blocks < (1ll << 31), "d8s_stem: too many tiles");
-    hipLaunchKernelGGL(k_stem, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream, *a, tiles_x,
-                       tiles_y);
+    hipLaunchKernelGGL(k_stem, dim3((unsigned)blocks), dim3(256), 0, st, *a, tiles_x, tiles_y);
     return launched("d8s_stem");
+}
+
+extern "C" int d8s_stem(const D8sStemArgs* a, void* stream) {
+    if (int rc = check_stem(a, "d8s_stem")) return rc;
+    return stem_dispatch(a, nullptr, (hipStream_t)stream);
+}
+
+extern "C" int d8s_stem_pair(const D8sStemArgs* a, const D8sStemArgs* b, void* stream) {
+    if (int rc = check_stem(a, "d8s_stem_pair")) return rc;
+    if (int rc = check_stem(b, "d8s_stem_pair")) return rc;
+    REQUIRE(a->N == b->N && a->H == b->H && a->W == b->W && a->kind == b->kind && a->flip == b->flip,
+            "d8s_stem_pair: the two problems differ in shape, input kind or flip");
+    return stem_dispatch(a, b, (hipStream_t)stream);
 }
 
 extern "C" const char* d8s_version(void) {

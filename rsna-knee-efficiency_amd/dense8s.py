@@ -1196,6 +1196,139 @@ def encode_concurrent(calls) -> list[torch.Tensor]:
     return outs
 
 
+class EncoderPair:
+    """Two encoders of one geometry over the same input images -- the final model's two weight seeds
+    on one study -- as ONE launch sequence: every step of a pass is a paired launch (`d8s_*_pair`)
+    carrying both encoders' arguments, so the two passes' small late layers fill the chip together
+    (the 16 x 16 whole block: 192 workgroups in about the time of 96) instead of overlapping by chance
+    on two streams (`encode_concurrent`).  Each encoder's outputs are exactly what it gives alone.  The
+    pair runs on the first encoder's stream and orders the second's around it.  Steps without a pair
+    launch ("parts" blocks, the final features) run as two launches in the same sequence."""
+
+    def __init__(self, a: Dense8SEncoder, b: Dense8SEncoder):
+        if a is b:
+            raise ValueError("EncoderPair: the same encoder twice")
+        if a.dev != b.dev:
+            raise ValueError(f"EncoderPair: encoders on cuda:{a.dev} and cuda:{b.dev}")
+        same = (a.nb == b.nb and a.n_out == b.n_out and a.in_dtype == b.in_dtype and a.in_shape == b.in_shape
+                and a.fused == b.fused and len(a.meta["blocks"]) == len(b.meta["blocks"])
+                and all(all(x[k] == y[k] for k in ("h", "w", "c0", "L"))
+                        for x, y in zip(a.meta["blocks"], b.meta["blocks"])))
+        if not same:
+            raise ValueError("EncoderPair: the encoders differ in geometry, batch, input or block kinds")
+        self.a, self.b = a, b
+        self.lib = a.lib
+        self.graphs: dict = {}
+        self.calls = {"graph": 0, "plain": 0, "copy": 0}
+
+    def _pass(self, x_ptr: int, fa: int, fb: int, mode: int) -> None:
+        A, B, lib = self.a, self.b, self.lib
+        st = A.stream.cuda_stream
+        for e in (A, B):
+            e.stem_args.x = x_ptr
+            e.stem_args.flip = mode
+        hip.check(lib.d8s_stem_pair(ctypes.byref(A.stem_args), ctypes.byref(B.stem_args), st), "d8s_stem_pair")
+        for bi, ((la, ta), (lb, tb)) in enumerate(zip(A.plan_l, B.plan_l)):
+            if bi in A.block_args:
+                pa, pb = A.block_args[bi], B.block_args[bi]
+                if isinstance(pa, hip.PartsArgs):
+                    A._block(bi, st)
+                    B._block(bi, st)
+                else:
+                    hip.check(lib.d8s_dense_block_pair(ctypes.byref(pa), ctypes.byref(pb), st),
+                              "d8s_dense_block_pair")
+                la = lb = ()
+            for La, Lb in zip(la, lb):
+                if La.dense is not None:
+                    hip.check(lib.d8s_dense_pair(ctypes.byref(La.dense), ctypes.byref(Lb.dense), st),
+                              "d8s_dense_pair")
+                    continue
+                hip.check(lib.d8s_conv1_pair(ctypes.byref(La.c1), ctypes.byref(Lb.c1), st), "d8s_conv1_pair")
+                hip.check(lib.d8s_conv2_pair(ctypes.byref(La.c2), ctypes.byref(Lb.c2), st), "d8s_conv2_pair")
+            if ta is not None:
+                hip.check(lib.d8s_transition_pair(ctypes.byref(ta), ctypes.byref(tb), st), "d8s_transition_pair")
+            else:
+                A._final(bi, fa, st)
+                B._final(bi, fb, st)
+
+    def _passes(self, xf: torch.Tensor, mode: int) -> None:
+        A, B = self.a, self.b
+        for i, chunk in enumerate(xf.split(A._per_pass(mode))):
+            xc = A._padded(chunk, mode)
+            self._pass(xc.data_ptr(), A.out[i * A.nb].data_ptr(), B.out[i * B.nb].data_ptr(), mode)
+
+    def capture(self, n: int, flip=False) -> float:
+        """One HIP graph per pair of passes over a batch of `n` input images; returns the seconds spent."""
+        A, B = self.a, self.b
+        mode = A._mode(flip)
+        k = A._per_pass(mode)
+        n = -(-n // k) * k
+        if n // k * A.nb > A.out.shape[0]:
+            raise ValueError(f"graph for {n} images: the encoders do {A.nb} per pass, "
+                             f"the output holds {A.out.shape[0]}")
+        t = time.perf_counter()
+        with torch.cuda.device(A.dev):
+            shared = graph_input(A.dev, (n, *A.in_shape[1:]), A.in_dtype)
+            static_in = shared.buf
+            shared.forget()
+            with torch.cuda.stream(A.stream):
+                A.stream.wait_stream(torch.cuda.current_stream(A.dev))
+                A.stream.wait_stream(B.stream)
+                self._passes(static_in[:k], mode)
+            A.stream.synchronize()
+            graphs = []
+            for i, chunk in enumerate(static_in.split(k)):
+                g = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(g, stream=A.stream, capture_error_mode="thread_local"):
+                    self._pass(chunk.data_ptr(), A.out[i * A.nb].data_ptr(), B.out[i * B.nb].data_ptr(), mode)
+                graphs.append(g)
+            A.stream.synchronize()
+        self.graphs[(n, mode)] = (graphs, shared)
+        return time.perf_counter() - t
+
+    def _graphs_for(self, n: int, mode: int):
+        gs = self.graphs.get((n, mode))
+        if gs is None:
+            k = -(-n // self.a._per_pass(mode))
+            for (m_, md), (g_, s_) in sorted(self.graphs.items()):
+                if md == mode and m_ >= k * self.a._per_pass(mode):
+                    return g_[:k], s_
+        return gs
+
+    def __call__(self, x: torch.Tensor, flip=False) -> tuple[torch.Tensor, torch.Tensor]:
+        """Both encoders' features of x: (outputs of the first, outputs of the second), as each
+        encoder's `__call__` returns them."""
+        A, B = self.a, self.b
+        mode = A._mode(flip)
+        A._check_input(x, mode)
+        B._check_input(x, mode)
+        cur = torch.cuda.current_stream(A.dev)
+        A.stream.wait_stream(cur)
+        A.stream.wait_stream(B.stream)
+        n = x.shape[0]
+        with torch.cuda.device(A.dev), torch.cuda.stream(A.stream):
+            gs = self._graphs_for(n, mode)
+            if gs is not None:
+                graphs, shared = gs
+                buf = shared.buf[:n]
+                if x.data_ptr() == buf.data_ptr() and x.shape == buf.shape and x.stride() == buf.stride():
+                    shared.forget()
+                elif shared.load(x, n, A.stream):
+                    self.calls["copy"] += 1
+                for g in graphs:
+                    g.replay()
+                shared.read_by(self, A.stream)
+                self.calls["graph"] += 1
+            else:
+                self._passes(x.contiguous(), mode)
+                self.calls["plain"] += 1
+            ra, rb = A._result(n, mode), B._result(n, mode)
+        hip.written(A.out, B.out)
+        B.stream.wait_stream(A.stream)
+        cur.wait_stream(A.stream)
+        return ra, rb
+
+
 def _record_sync(stream) -> torch.cuda.Event:
     """An event without timing on `stream`: orders the shared graph input between runners' streams."""
     e = torch.cuda.Event()

@@ -159,6 +159,12 @@ SIGNATURES = {
     "d8s_transition": [ctypes.POINTER(GemmArgs), vp],
     "d8s_final": [vp, i32, vp, i32, i32, vp, vp, i32, vp],
     "d8s_stem": [ctypes.POINTER(StemArgs), vp],
+    "d8s_stem_pair": [ctypes.POINTER(StemArgs), ctypes.POINTER(StemArgs), vp],
+    "d8s_conv1_pair": [ctypes.POINTER(GemmArgs), ctypes.POINTER(GemmArgs), vp],
+    "d8s_conv2_pair": [ctypes.POINTER(Conv2Args), ctypes.POINTER(Conv2Args), vp],
+    "d8s_dense_pair": [ctypes.POINTER(DenseArgs), ctypes.POINTER(DenseArgs), vp],
+    "d8s_dense_block_pair": [ctypes.POINTER(BlockArgs), ctypes.POINTER(BlockArgs), vp],
+    "d8s_transition_pair": [ctypes.POINTER(GemmArgs), ctypes.POINTER(GemmArgs), vp],
     "d8s_prep_workspace": [i32, i32, ctypes.POINTER(ctypes.c_uint64)],
     "d8s_prep": [ctypes.POINTER(PrepArgs), vp],
     "d8s_prep_resize": [ctypes.POINTER(PrepArgs), vp],

@@ -299,6 +299,33 @@ def test_encoder512_c5_vs_fp32(dev, c5):
         assert lg["rel_l2"] <= 1.05 * 0.067 and lg["cos_min"] >= 0.99, (seed, lg)
 
 
+def test_encoder512_c5_pair(dev, c5):
+    """Both seeds' flip-TTA passes as one sequence of paired launches (`EncoderPair`), eager and as
+    replayed graphs (three replays with eager work between, a second study in between too): each
+    seed's features equal to its own encoder's.  Encoders of different geometry are refused."""
+    xd = c5["xd"]
+    encs = c5["enc"]
+    want = [e(xd, flip="tta").clone() for e in encs]
+    x2 = torch.flip(xd, dims=[0]).contiguous()
+    want2 = [e(x2, flip="tta").clone() for e in encs]
+    pair = dense8s.EncoderPair(encs[0], encs[1])
+    got = [o.clone() for o in pair(xd, flip="tta")]
+    torch.cuda.synchronize(dev)
+    assert torch.equal(got[0], want[0]) and torch.equal(got[1], want[1])
+    pair.capture(48, flip="tta")
+    for k in range(3):
+        for x, w in ((xd, want), (x2, want2)):
+            got = [o.clone() for o in pair(x, flip="tta")]
+            _ = (xd.float() * 2).sum()
+            torch.cuda.synchronize(dev)
+            assert torch.equal(got[0], w[0]) and torch.equal(got[1], w[1]), k
+    assert pair.calls["graph"] == 6
+    # a single encoder's own call after the pair still gives its bytes (its stream ordered after)
+    assert torch.equal(encs[1](xd, flip="tta"), want[1])
+    with pytest.raises(ValueError):
+        dense8s.EncoderPair(encs[0], encs[0])
+
+
 def test_encoder512_c5_concurrent_graphs(dev, c5):
     """bench.py's step: both seeds' flip-TTA passes from two streams (`encode_concurrent`) replaying
     their graphs, three times with eager work between, equal to each runner's eager call."""
