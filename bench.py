@@ -700,6 +700,9 @@ def main() -> None:
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--serial", action="store_true",
                     help="run the two seeds' passes of a step back to back on one stream")
+    ap.add_argument("--pair", action="store_true",
+                    help="run the two seeds' passes of a step as one sequence of paired launches "
+                         "(dense8s.EncoderPair) instead of two streams")
     ap.add_argument("--copy-probe", action="store_true",
                     help="also time d8s_micro_copy over 1 GiB (HBM floor, counter calibration)")
     ap.add_argument("--rocprof-summary", metavar="DIR",
@@ -777,16 +780,22 @@ def main() -> None:
     log(f"{len(studies)} studies generated and resident ({time.perf_counter() - t0:.1f} s)")
     for e in encs:
         e.capture(2 * SLICES, flip="tta")
+    pair = None
+    if args.pair:
+        pair = dense8s.EncoderPair(encs[0], encs[1])
+        pair.capture(2 * SLICES, flip="tta")
     torch.cuda.synchronize()
 
     # the two seeds' passes are independent: dense8s.encode_concurrent runs each from its own stream,
     # so the small, latency-bound layers of one seed's pass overlap the other's.  --serial runs them
-    # back to back.
+    # back to back, --pair as paired launches.
     def step(k: int) -> None:
         x = studies[k % len(studies)]
         if args.serial:
             for e in encs:
                 e(x, flip="tta")
+        elif pair is not None:
+            pair(x, flip="tta")
         else:
             dense8s.encode_concurrent([(e, x, "tta") for e in encs])
 
@@ -915,7 +924,8 @@ def main() -> None:
         "study_latency_config": "C4: one 24-slice study, batch 24, one encoder, HIP graph replay",
         "fp32_agreement": fp32_agreement,
         "reference_study": ref_study,
-        "step_schedule": "serial (one stream)" if args.serial else "the 2 seeds' passes on 2 streams",
+        "step_schedule": ("serial (one stream)" if args.serial else
+                          "paired launches (one stream)" if args.pair else "the 2 seeds' passes on 2 streams"),
         "pass_ms_kernels": round(pass_ms, 3),
         "pass_hbm_frac": round(total_bytes / (pass_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
         "family_ms": {k: round(v, 3) for k, v in fam.items()},
