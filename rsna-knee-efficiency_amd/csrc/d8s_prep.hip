@@ -2,16 +2,17 @@
 // -> uint8 -> side flip) and their C ABI, d8s_prep / d8s_prep_resize (include/d8s_hip.h).
 //
 // The work is byte and float bookkeeping bound by memory, not matrix work.  Design:
-//   - the resized float32 stacks are never stored: every pass evaluates the resize again from the
-//     uint16 region (2 bytes per source pixel, a region of a study is ~50 MB and stays in the
-//     256 MB last-level cache between passes) instead of reading 4 bytes per output pixel of a
-//     materialised stack;
+//   - uint16 regions (kind 0): the first pass evaluates the resize from the region and writes the
+//     float32 stacks once to the workspace's scratch while it counts the first radix level; the
+//     later passes read the stored stacks (k_prep_hist<1, 1, true>, then float_view).  Evaluating
+//     the resize again in every pass instead was VALU-bound at about 40 instructions per pixel and
+//     2-3x slower.  Float32 stacks (kind 1) are read as given by every pass;
 //   - the order statistics k1, k1+1, k2, k2+1 are selected exactly by a three-level radix histogram
 //     of the float's order key (11 + 11 + 10 bits).  Each level is one pass over the stack that
 //     counts in LDS and adds the nonzero bins to a global histogram, then one workgroup per stack
 //     finds the bins holding the four ranks;  equal ranks share a histogram (at most four per level);
-//   - the last pass evaluates the pixel again and writes the uint8 value (float64 arithmetic, the
-//     reference's exact operations) at its flipped position.
+//   - the last pass writes the uint8 value of every pixel (float64 arithmetic, the reference's exact
+//     operations) at its flipped position.
 // A pass works on blocks of output rows of one slice: the source rows a block needs are resized along x
 // once into LDS, then every output pixel combines them along y (the bilinear formula is separable as
 // written: fma(h0, top, h1 * bottom) with top and bottom the x interpolations of two source rows).  A
