@@ -88,11 +88,13 @@ def agree(a: np.ndarray, b: np.ndarray) -> dict:
 def kernel_bytes(meta: dict, n: int, kinds: dict | None = None) -> dict[str, list[float]]:
     """Algorithmic HBM bytes of every launch of a pass of n images, per kernel family: compulsory reads
     of the activations and writes of the outputs, plus the weights and tables (read once).  `kinds`
-    {block: "conv" | "tile" | "img"} (`Dense8SEncoder.fused`): a fused layer ("dense") has no bottleneck
-    in memory; a whole block ("block") reads its input and writes its layers' outputs once."""
+    {block: "conv" | "chain" | "tile" | "img" | "parts"} (`Dense8SEncoder.fused`): a fused layer
+    ("dense") has no bottleneck in memory; a chained launch ("chain": conv2 of a layer and conv1 of the
+    next) does not read the new layer's channels back; a whole block ("block") reads its input and
+    writes its layers' outputs once."""
     kinds = kinds or {}
-    out: dict[str, list[float]] = {"stem": [], "conv1": [], "conv2": [], "dense": [], "block": [],
-                                   "trans": [], "final": []}
+    out: dict[str, list[float]] = {"stem": [], "conv1": [], "conv2": [], "chain": [], "dense": [],
+                                   "block": [], "trans": [], "final": []}
     img = meta["img"]
     out["stem"].append(n * 3 * img * img + n * 64 * (img // 4) ** 2 + 64 * 168 * 2 + 3 * 256 * 2)
     for bi, b in enumerate(meta["blocks"]):
@@ -104,11 +106,22 @@ def kernel_bytes(meta: dict, n: int, kinds: dict | None = None) -> dict[str, lis
             cin = b["c0"] + 32 * li
             w = 128 * cin + cin * 4 + 128 * 12 + 36864 + 32 * 8
             wts += w
+            c1 = M * cin + M * 128 + 128 * cin + cin * 4 + 128 * 12
+            c2 = M * 128 + M * 32 + 36864 + 32 * 8
             if kind == "tile":
                 out["dense"].append(M * cin + M * 32 + w)
             elif kind == "conv":
-                out["conv1"].append(M * cin + M * 128 + 128 * cin + cin * 4 + 128 * 12)
-                out["conv2"].append(M * 128 + M * 32 + 36864 + 32 * 8)
+                out["conv1"].append(c1)
+                out["conv2"].append(c2)
+            elif kind == "chain":
+                # conv1 of layer 0, then per launch conv2 of layer li - 1 with conv1 of layer li (which
+                # takes the 32 new channels from registers: M * 32 fewer bytes read), conv2 of the last
+                if li == 0:
+                    out["conv1"].append(c1)
+                else:
+                    out["chain"].append(M * 128 + M * 32 + 36864 + 32 * 8 + c1 - M * 32)
+                if li == b["L"] - 1:
+                    out["conv2"].append(c2)
         if kind in ("img", "parts"):
             out["block"].append(M * b["c0"] + M * 32 * b["L"] + wts)
         ctot = b["c0"] + 32 * b["L"]
@@ -124,8 +137,8 @@ def kernel_ops(meta: dict, n: int, kinds: dict | None = None) -> dict[str, float
     """int8 MFMA operations (2 per MAC) of a pass, per family (the transition at quarter resolution)."""
     kinds = kinds or {}
     img = meta["img"]
-    ops = {"stem": 2.0 * n * 64 * 147 * (img // 2) ** 2, "conv1": 0.0, "conv2": 0.0, "dense": 0.0,
-           "block": 0.0, "trans": 0.0}
+    ops = {"stem": 2.0 * n * 64 * 147 * (img // 2) ** 2, "conv1": 0.0, "conv2": 0.0, "chain": 0.0,
+           "dense": 0.0, "block": 0.0, "trans": 0.0}
     for bi, b in enumerate(meta["blocks"]):
         M = n * b["h"] * b["w"]
         kind = str(kinds.get(bi, "conv")).split(":")[0]
@@ -135,6 +148,9 @@ def kernel_ops(meta: dict, n: int, kinds: dict | None = None) -> dict[str, float
             if kind == "conv":
                 ops["conv1"] += o1
                 ops["conv2"] += o2
+            elif kind == "chain":
+                ops["conv1" if li == 0 else "chain"] += o1
+                ops["conv2" if li == b["L"] - 1 else "chain"] += o2
             else:
                 ops["dense" if kind == "tile" else "block"] += o1 + o2
         if b["trans"]:
@@ -175,7 +191,7 @@ def copy_probe(dev: torch.device, mib: int = 1024, reps: int = 5) -> dict:
     return {"bytes_per_launch": 2 * n, "ms": round(ms, 4), "gbs": round(2 * n / (ms * 1e-3) / 1e9, 1)}
 
 
-FAMILY = {"k_conv1": "conv1", "k_conv1p": "conv1", "k_conv2": "conv2", "k_dense": "dense",
+FAMILY = {"k_conv1": "conv1", "k_conv1p": "conv1", "k_conv2": "conv2", "k_c21": "chain", "k_dense": "dense",
           "k_band": "dense", "k_dblock": "block", "k_trans": "trans", "k_stem": "stem",
           "k_stem_rows": "stem", "k_final": "final", "k_copy": "copy", "k_prep_setup": "prep_setup",
           "k_prep_hist": "prep_hist", "k_prep_select": "prep_select", "k_prep_norm": "prep_norm",
@@ -286,7 +302,7 @@ def traffic_summary(fetch_dir: str, write_dir: str, passes: int, copy_bytes: int
              "| family | launches per pass | HBM read MB/launch | HBM write MB/launch | traffic MB/launch "
              "| algorithmic MB/launch | traffic / algorithmic |", "|---|---|---|---|---|---|---|"]
     machine = []
-    for fam in ("conv1", "conv2", "dense", "block", "trans", "stem", "final"):
+    for fam in ("conv1", "conv2", "chain", "dense", "block", "trans", "stem", "final"):
         if fam not in fe or fam not in wr or fam not in alg:
             continue
         n = len(alg[fam])
@@ -325,7 +341,7 @@ def mfma_summary(pmc_dir: str, passes: int) -> str:
     alg = kernel_ops({"img": IMG, "blocks": meta_blocks}, nb, kinds)
     lines = ["| family | dispatches | MFMA busy (% of SIMD cycles, weighted) | MFMA ops issued per pass (G) "
              "| algorithmic int8 ops per pass (G) | issued / algorithmic |", "|---|---|---|---|---|---|"]
-    for fam in ("conv1", "conv2", "dense", "block", "trans", "stem"):
+    for fam in ("conv1", "conv2", "chain", "dense", "block", "trans", "stem"):
         if fam not in per:
             continue
         ds = list(per[fam].values())
@@ -898,7 +914,7 @@ def main() -> None:
     byts = kernel_bytes(encs[0].meta, nb, encs[0].fused)
     ops = kernel_ops(encs[0].meta, nb, encs[0].fused)
     pass_ms = sum(fam.values())
-    dom = max(("conv1", "conv2", "dense", "block", "trans", "stem"), key=lambda k: fam.get(k, 0.0))
+    dom = max(("conv1", "conv2", "chain", "dense", "block", "trans", "stem"), key=lambda k: fam.get(k, 0.0))
     dom_bytes = sum(byts[dom])
     launches = len(byts[dom])
     avg_ms = fam[dom] / launches

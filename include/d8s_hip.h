@@ -191,6 +191,20 @@ int d8s_conv2(const D8sConv2Args* a, void* stream);
  * src/knee/dense8s.py:1154-1203, kind "tile"). */
 int d8s_dense(const D8sDenseArgs* a, void* stream);
 
+/* conv2 of layer l, then conv1 of layer l + 1, in one launch: c2 as for d8s_conv2 (x = layer l's
+ * bottleneck, out = layer l's store slot), c1 as for d8s_conv1 (G = G0 + l + 1 groups, the last of
+ * which is c2's output slot; out = layer l + 1's bottleneck, a buffer other than c2->x).  The bytes
+ * written equal those of d8s_conv2(c2) followed by d8s_conv1(c1): the new 32 channels reach conv1 from
+ * registers, so a block of L layers runs in L + 1 launches (conv1 of layer 0, L - 1 of these, conv2 of
+ * layer L - 1) instead of 2 L.  Maps W = 16, 32 or 64 wide with H * W a multiple of 128 and
+ * 2 <= G <= D8S_C21_MAX_GROUPS (d8s_c21_supported(H, W, G) says whether a shape is taken).  Replaces
+ * the pair of launches conv2 (layer l), conv1 (layer l + 1) of the reference's per-layer sequence
+ * (src/knee/dense8s.py:1354-1385; kernels `conv2_t8x32_pl` and `conv1_w64_pl`,
+ * src/knee/dense8s_kernels.cu:2679-2832, 479-627). */
+#define D8S_C21_MAX_GROUPS 64
+int d8s_conv2_conv1(const D8sConv2Args* c2, const D8sGemmArgs* c1, void* stream);
+int d8s_c21_supported(int32_t H, int32_t W, int32_t G);
+
 /* Every layer of a dense block in one launch, one workgroup per image, for maps of at most 256
  * pixels with G0 + L - 1 <= 64: the bytes of d8s_conv1 + d8s_conv2 layer after layer.  Replaces the
  * reference's whole-block fused kernels `dense_img*` (src/knee/dense8s_kernels.cu:1005-1219, launch

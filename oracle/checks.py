@@ -134,6 +134,34 @@ def run_dense(c: cases.GemmCase, c2: cases.Conv2Case, device, slots: int = 3,
     return s[slot], others
 
 
+def run_chain(c: cases.GemmCase, c2: cases.Conv2Case, device, fused: bool = True) -> tuple[np.ndarray, np.ndarray]:
+    """conv2 of `c2` into the store's last slot (group G - 1 of `c`), then conv1 of `c` over all G groups:
+    d8s_conv2_conv1 (`fused`) or d8s_conv2 then d8s_conv1.  The last slot starts as a sentinel (its bytes
+    in `c` are not used).  Returns (that slot [M, 32] int8, the new bottleneck [M, 128] uint8)."""
+    HW = c.S * c.width
+    M = c.N * HW
+    seg_h = c.seg.copy()
+    seg_h[c.G - 1 - c.G0] = 0x5A
+    in0, seg, w1, abh, gd, bin_, w2k, sc = (_dev(a, device) for a in (c.in0, seg_h, c.w1, c.abh, c.gd, c2.bott,
+                                                                        c2.w2k, c2.sc))
+    w1sum = _dev(c.w1.astype(np.int64).sum(axis=(0, 2)).astype(np.int32), device)
+    w2sum = _dev(c2.w2k.astype(np.int64).sum(axis=(0, 1, 3)).astype(np.int32), device)
+    bout = torch.zeros(4 * M * 32, dtype=torch.uint8, device=device)
+    slot = _ptr(seg) + (c.G - 1 - c.G0) * M * 32
+    a2 = hip.Conv2Args(_ptr(bin_), _ptr(w2k), _ptr(sc), _ptr(w2sum), slot, c.N, c.S, c.width, 0)
+    a1 = hip.GemmArgs(_ptr(in0), _ptr(seg), _ptr(w1), _ptr(abh), _ptr(gd), _ptr(w1sum), _ptr(bout),
+                      c.G0, c.G, c.N, HW, c.width, M, 128, 0)
+    if fused:
+        hip.call("d8s_conv2_conv1", ctypes.byref(a2), ctypes.byref(a1), _stream(device))
+    else:
+        hip.call("d8s_conv2", ctypes.byref(a2), _stream(device))
+        hip.call("d8s_conv1", ctypes.byref(a1), _stream(device))
+    torch.cuda.synchronize(device)
+    s = seg.cpu().numpy()[c.G - 1 - c.G0].reshape(M, 32)
+    b = bout.cpu().numpy().reshape(4, M, 32).transpose(1, 0, 2).reshape(M, 128)
+    return s, b
+
+
 def exact_dense(c: cases.GemmCase, c2: cases.Conv2Case) -> np.ndarray:
     """q [M, 32] of conv1 then conv2: the bottleneck bytes of `exact_conv1`, the 3x3 conv of
     `exact_conv2` on them."""

@@ -791,6 +791,329 @@ __global__ __launch_bounds__(256, 2) void k_conv2(D8sConv2Args a0, int tiles_x, 
 }
 
 // ------------------------------------------------------------------------------------------------
+// conv2 of layer l, then conv1 of layer l + 1, in one launch.  conv1 is pixel-local, so the 32
+// channels conv2 gives a pixel are the last K group of the next layer's conv1 on the same pixel: a
+// lane's conv2 epilogue leaves exactly the 16 bytes the conv1 B operand of that lane needs (pixel j,
+// bytes 16 h .. 16 h + 15), which stay in registers while the bytes go to the layer's store slot.
+// Only the bottleneck crosses the launch boundary, in two buffers: conv2 reads layer l's while
+// conv1 writes layer l + 1's.
+// Persistent workgroups of 4 waves over tiles of 128 pixels of one image (R = 128 / W rows, W = 16,
+// 32 or 64); wave w owns pixels 32 w .. 32 w + 31 of the tile in both phases.  One LDS region serves
+// the two phases in turn (a workgroup runs them one after the other; the workgroups sharing a CU
+// overlap each other's):
+//   conv2 (as k_conv2 with one pixel tile per wave): the tile's (R + 2) x (W + 2) halo of the 4
+//         bottleneck planes and the weights one input plane (9 KB) at a time, double-buffered;
+//   conv1 (as k_conv1p, one 32-pixel column block): activations from the store 4 groups ahead, the
+//         prefetch running on into the next tile's first groups (in flight during its conv2), the
+//         weights in 4-group chunks double-buffered.
+// Group G - 1 (the new one) is never read from memory: its step takes the conv2 result (the load of
+// that slot is clamped to G - 2 and its value unused).  With at most 64 KB of LDS per workgroup
+// (W <= 32) three workgroups share a CU (the registers are bounded for it), as many as k_conv1p runs
+// on these maps; W = 64 runs two.  Offsets are 32-bit where the host checked the sizes.
+// ------------------------------------------------------------------------------------------------
+template <int W_>
+struct CcShape {
+    static constexpr int R = 128 / W_;                    // rows of a tile
+    static constexpr int HWd = W_ + 2, HP = (R + 2) * HWd;
+    static constexpr int NCHUNK = 8 * HP;                 // 16-byte halo chunks (4 planes x 2 halves)
+    static constexpr int NCH = (NCHUNK + 255) / 256;      // per thread
+    static constexpr size_t HALO = (size_t)NCHUNK * 16;
+    static constexpr size_t W2BUF = 9 * 32 * 32;          // one input plane of the conv2 weights
+    static constexpr size_t A_BYTES = HALO + 2 * W2BUF, B_BYTES = 2 * 4 * 4096;
+    static constexpr size_t UNION = A_BYTES > B_BYTES ? A_BYTES : B_BYTES;
+    static constexpr int OCC = W_ <= 32 ? 3 : 2;          // workgroups per CU
+    static_assert(128 % W_ == 0 && R >= 2, "tile = whole rows of 128 pixels");
+};
+
+static constexpr size_t CC_TABLES = 128 * 4 + 128 * 8 + 32 * 4 + 32 * 4;
+
+template <int W_>
+static size_t cc_lds(int G) {
+    return CcShape<W_>::UNION + CC_TABLES + (size_t)G * 128;
+}
+
+// activation bytes of conv1 step t (t < Gp: this tile's group t, else the next tile's group t - Gp),
+// groups past G - 2 clamped to G - 2 (G - 1 comes from registers, padded steps are unused)
+DEV u32x4 cc_act(const uint8_t* in0, const uint8_t* seg, int64_t in_gs, int64_t seg_gs, int G0, int G, int Gp,
+                 int t, uint32_t ci, uint32_t cs, uint32_t ni, uint32_t ns) {
+    const bool cur = t < Gp;
+    int g = cur ? t : t - Gp;
+    g = g < G - 1 ? g : G - 2;
+    const bool in = g < G0;
+    const uint8_t* base = in ? in0 + g * in_gs : seg + (int64_t)(g - G0) * seg_gs;
+    const uint32_t o = cur ? (in ? ci : cs) : (in ? ni : ns);
+    return *(const u32x4*)(base + o);
+}
+
+template <int W_>
+__global__ __launch_bounds__(256, CcShape<W_>::OCC) void k_c21(D8sConv2Args c2, D8sGemmArgs c1) {
+    using S = CcShape<W_>;
+    constexpr int R = S::R, HWd = S::HWd, HP = S::HP, NCH = S::NCH, PF = 4;
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    u32x4* s_u = (u32x4*)smem;                                      // halo [4][HP][2] | chunks [2][1024]
+    u32x4* s_w2 = (u32x4*)(smem + S::HALO);                         // [2][9 * 32 * 2] swizzled planes
+    int32_t* s_wsum = (int32_t*)(smem + S::UNION);                  // [128]
+    float2* s_gd = (float2*)(s_wsum + 128);                         // [128]
+    float* s_sc2 = (float*)(s_gd + 128);                            // [32]
+    int32_t* s_ini2 = (int32_t*)(s_sc2 + 32);                       // [32] 128 sum(w2)
+    uint32_t* s_abh = (uint32_t*)(s_ini2 + 32);                     // [G * 32]
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int h = lane >> 5, j = lane & 31;
+    const int G = c1.G, G0 = c1.G0, HW = c1.HW, H = c2.H;
+    const int per_img = HW / 128, total = c1.N * per_img;
+    const int64_t M = c1.rows;
+    const int p = 32 * wave + j, ty = p / W_, tx = p - ty * W_, q0 = ty * HWd + tx;
+
+    // tile order as k_conv2: XCD x walks one contiguous eighth of the tiles
+    int tile = blockIdx.x, tend = total, tstep = gridDim.x;
+    if (total > (int)gridDim.x && (gridDim.x & 7) == 0) {
+        const int chunk = (total + 7) / 8, xcd = blockIdx.x & 7;
+        tstep = gridDim.x >> 3;
+        tile = xcd * chunk + (blockIdx.x >> 3);
+        tend = min(total, (xcd + 1) * chunk);
+    }
+    if (tile >= tend) return;                               // (uniform per workgroup)
+
+    const uint8_t* in0 = (const uint8_t*)c1.in0;
+    const uint8_t* seg = (const uint8_t*)c1.seg;
+    const int64_t in_gs = (int64_t)HW * 32, seg_gs = M * 32;
+    // conv1 pixel offsets of a tile's pixel for this lane: in0 group 0 and store slot 0
+    auto offs = [&](int t, uint32_t& oi, uint32_t& os) INLINE {
+        const int n = t / per_img, pi = (t - n * per_img) * 128 + p;
+        oi = (uint32_t)(((int64_t)n * G0 * HW + pi) * 32 + 16 * h);
+        os = (uint32_t)(((int64_t)n * HW + pi) * 32 + 16 * h);
+    };
+    uint32_t ci, cs, ni, ns;
+    offs(tile, ci, cs);
+    offs(tile + tstep < tend ? tile + tstep : tile, ni, ns);
+
+    // halo chunks of this thread: chunk i = tid + 256 k -> plane c, halo pixel (hy, hx), half hh, at
+    // byte (c M + hy W + hx) 32 + 16 hh from the pixel above-left of the tile (a buffer resource based
+    // there, uniform per tile).  Chunks outside the image (or past the halo) take an offset past the
+    // resource's range, which reads zero: u = 0 after the XOR, the padding.  The chunk geometry is
+    // recomputed per tile from an opaque copy of the thread index (kept out of registers across the
+    // phases).
+    constexpr uint32_t CC_OOB = 0xffffff00u;
+    u32x4 hreg[NCH];
+    auto hload = [&](int t) INLINE {
+        const int n = t / per_img, y0 = (t - n * per_img) * R;
+        const bool top = y0 == 0, bot = y0 + R == H;
+        const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(
+            (void*)(c2.x + ((int64_t)n * HW + (int64_t)y0 * W_ - W_ - 1) * 32), 0, 0x7fffffff, 0x00020000);
+        int t0 = tid;
+        asm volatile("" : "+v"(t0));
+#pragma unroll
+        for (int k = 0; k < NCH; ++k) {
+            const int i = t0 + 256 * k;
+            const int c = i / (2 * HP), rr = i - c * (2 * HP);
+            const int hp = rr >> 1, hh = rr & 1;
+            const int hy = hp / HWd, hx = hp - hy * HWd;
+            const bool ok = i < S::NCHUNK && hx >= 1 && hx <= W_ && !(top && hy == 0) && !(bot && hy == R + 1);
+            const uint32_t off = (uint32_t)((c * M + hy * W_ + hx) * 32 + 16 * hh);
+            hreg[k] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, ok ? off : CC_OOB, 0, 0));
+        }
+    };
+    auto hstore = [&]() INLINE {
+        int t0 = tid;
+        asm volatile("" : "+v"(t0));
+#pragma unroll
+        for (int k = 0; k < NCH; ++k) {
+            const int i = t0 + 256 * k;
+            const int c = i / (2 * HP), rr = i - c * (2 * HP);
+            if (i < S::NCHUNK) s_u[c * HP * 2 + swz(rr >> 1, rr & 1)] = hreg[k] ^ SIGN4;
+        }
+    };
+    // conv2 weights of input plane c: 576 chunks ([tap][out][half]), at most 3 per thread (buffer loads:
+    // one lane offset, the plane and part in the scalar offset; past the table they read zero, unused)
+    const __amdgpu_buffer_rsrc_t rw2 = __builtin_amdgcn_make_buffer_rsrc((void*)c2.w, 0, 36864, 0x00020000);
+    u32x4 wst[3];
+    auto w2load = [&](int c) INLINE {
+#pragma unroll
+        for (int u = 0; u < 3; ++u)
+            wst[u] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                rw2, (uint32_t)tid * 16, (uint32_t)(c * 9216 + u * 4096), 0));
+    };
+    auto w2store = [&](int buf) INLINE {
+        int t0 = tid;
+        asm volatile("" : "+v"(t0));
+#pragma unroll
+        for (int u = 0; u < 3; ++u) {
+            const int i = t0 + 256 * u;
+            if (i < 576) s_w2[buf * 576 + swz(i >> 1, i & 1)] = wst[u];
+        }
+    };
+
+    const int Gp = (G + PF - 1) & ~(PF - 1), nchunk = Gp >> 2;
+    // conv1 weights: 4-group chunks of 16 KB, 4 loads per thread, as buffer loads (past the table:
+    // zero, read only by padded steps, whose activation operand is zero)
+    const __amdgpu_buffer_rsrc_t rw1 = __builtin_amdgcn_make_buffer_rsrc((void*)c1.w, 0, G * 4096, 0x00020000);
+    auto w1load = [&](u32x4* dst, int chunk) INLINE {
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+            dst[u] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                rw1, (uint32_t)tid * 16, (uint32_t)(chunk * 16384 + u * 4096), 0));
+    };
+    auto w1store = [&](const u32x4* src, int buf) INLINE {
+        int t0 = tid;
+        asm volatile("" : "+v"(t0));
+#pragma unroll
+        for (int u = 0; u < 4; ++u) s_u[buf * 1024 + wperm(t0 + 256 * u)] = src[u];
+    };
+    // the two outputs through buffer stores: the lane's byte offset p 32 + 16 h, the tile (and plane)
+    // in the scalar offset (the host checked 4 M 32 < 2^31)
+    const __amdgpu_buffer_rsrc_t ro2 = __builtin_amdgcn_make_buffer_rsrc((void*)c2.out, 0, (int)(M * 32), 0x00020000);
+    const __amdgpu_buffer_rsrc_t ro1 = __builtin_amdgcn_make_buffer_rsrc(c1.out, 0, (int)(M * 128), 0x00020000);
+    const uint32_t lo_off = (uint32_t)(p * 32 + 16 * h);
+    u32x4 ra[PF], rb[4], stg[4];
+    // the first tile's halo, activations, conv2 plane 0 and conv1 chunk 0 in flight while the tables
+    // are staged
+    hload(tile);
+    w2load(0);
+#pragma unroll
+    for (int s = 0; s < PF; ++s)
+        ra[s] = cc_act(in0, seg, in_gs, seg_gs, G0, G, Gp, s, ci, cs, ni, ns);
+    w1load(stg, 0);
+    {
+        const uint32_t* abh32 = (const uint32_t*)c1.abh;
+        for (int i = tid; i < G * 32; i += 256) s_abh[i] = abh32[i];
+        if (tid < 128) {
+            s_wsum[tid] = c1.wsum[tid];
+            s_gd[tid] = ((const float2*)c1.gd)[tid];
+        }
+        if (tid < 32) {
+            s_sc2[tid] = c2.sc[tid];
+            s_ini2[tid] = 128 * c2.wsum[tid];
+        }
+    }
+    hstore();
+    w2store(0);
+    __syncthreads();
+
+    for (;;) {
+        const int next = tile + tstep;
+        const bool more = next < tend;
+        const uint32_t tb = (uint32_t)tile * 4096;           // the tile's first byte in a plane / slot
+
+        // ---- conv2 of layer l: per input plane c, 9 taps; plane c + 1's weights staged meanwhile ----
+        i32x16 acc2;
+#pragma unroll
+        for (int v = 0; v < 16; ++v) acc2[v] = s_ini2[res_row(v, h)];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            if (c < 3) w2load(c + 1);
+            __builtin_amdgcn_sched_barrier(0);               // (issued before the plane's MFMAs)
+            const u32x4* pw = s_w2 + (c & 1) * 576;
+            const u32x4* px = s_u + c * HP * 2;
+            u32x4 aw[2], bx[2];
+            auto fetch = [&](int tap, int slot) INLINE {
+                const int off = (tap / 3) * HWd + (tap % 3);
+                aw[slot] = pw[swz(tap * 32 + j, h)];
+                bx[slot] = px[swz(q0 + off, h)];
+            };
+            fetch(0, 0);
+#pragma unroll
+            for (int tap = 0; tap < 9; ++tap) {
+                if (tap + 1 < 9) fetch(tap + 1, (tap + 1) & 1);
+                acc2 = mfma_i8(aw[tap & 1], bx[tap & 1], acc2);
+            }
+            if (c < 3) {
+                w2store((c + 1) & 1);                        // buffer last read in plane c - 1
+                __syncthreads();
+            }
+        }
+        // epilogue (conv2t_body, src/knee/dense8s_kernels.cu:2797-2809): the layer's store bytes,
+        // kept as conv1's last group
+        u32x4 row;
+        {
+            uint32_t e[4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) e[q] = epi2_q(acc2, q, *(const float4*)(s_sc2 + 8 * q + 4 * h));
+            row = xchg_rows(e[0], e[1], e[2], e[3], h);
+            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i32x4, row), ro2, lo_off, tb, 0);
+        }
+        __syncthreads();                                     // the halo and plane 3 are read
+        w1store(stg, 0);
+        __syncthreads();
+
+        // ---- conv1 of layer l + 1 ----
+        i32x16 acc[4];
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) acc[c][v] = 128 * s_wsum[32 * c + res_row(v, h)];
+        int k = 0, cc = 0;
+#define CC_STEP(slot, PAD)                                                                        \
+    do {                                                                                          \
+        const int k_ = k + (slot);                                                                \
+        const u32x4* pw_ = s_u + (cc & 1) * 1024 + (slot) * 256 + j + 32 * h;                     \
+        _Pragma("unroll") for (int c_ = 0; c_ < 4; ++c_) rb[c_] = pw_[64 * c_];                   \
+        u32x4 b_;                                                                                 \
+        if (!PAD || k_ < G) {                                                                     \
+            const u32x4* pp_ = (const u32x4*)(s_abh + k_ * 32 + h * 16);                          \
+            const u32x4 x_ = (PAD && k_ == G - 1) ? row : ra[slot];                               \
+            b_ = pro16(x_, pp_[0], pp_[1], pp_[2], pp_[3]);                                       \
+        } else {                                                                                  \
+            b_ = u32x4{0, 0, 0, 0};                                                               \
+        }                                                                                         \
+        ra[slot] = cc_act(in0, seg, in_gs, seg_gs, G0, G, Gp, k_ + PF, ci, cs, ni, ns);           \
+        _Pragma("unroll") for (int c_ = 0; c_ < 4; ++c_) acc[c_] = mfma_i8(rb[c_], b_, acc[c_]);  \
+    } while (0)
+        // the last chunk holds group G - 1 (G - 1 >= Gp - 4) and the padded steps
+        for (; cc + 1 < nchunk; ++cc, k += 4) {
+            w1load(stg, cc + 1);
+            CC_STEP(0, false);
+            CC_STEP(1, false);
+            CC_STEP(2, false);
+            CC_STEP(3, false);
+            w1store(stg, (cc + 1) & 1);
+            __syncthreads();
+        }
+        w1load(stg, 0);                                      // the next tile's chunk 0
+        CC_STEP(0, true);
+        CC_STEP(1, true);
+        CC_STEP(2, true);
+        CC_STEP(3, true);
+#undef CC_STEP
+
+        // epilogue as k_conv1p: the planar u8 bottleneck of layer l + 1
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            uint32_t e[4];
+#pragma unroll
+            for (int kk = 0; kk < 4; ++kk) {
+                uint32_t d = 0;
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int v = 4 * kk + r;
+                    const float2 prm = s_gd[32 * c + res_row(v, h)];
+                    float y = __builtin_fmaf(prm.x, (float)acc[c][v], prm.y);
+                    y = __builtin_fminf(__builtin_fmaxf(y, 0.0f), 1.0f);
+                    const uint32_t b = __float_as_uint(__builtin_fmaf(y, 255.0f, 8388608.0f)) & 0xffu;
+                    d |= b << (8 * r);
+                }
+                e[kk] = d;
+            }
+            const u32x4 orow = xchg_rows(e[0], e[1], e[2], e[3], h);
+            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i32x4, orow), ro1, lo_off,
+                                                   (uint32_t)(c * M * 32) + tb, 0);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        if (!more) break;
+        hload(next);                                         // the next tile's halo and plane 0
+        w2load(0);
+        __syncthreads();                                     // the weight chunks are read
+        hstore();
+        w2store(0);
+        __syncthreads();
+        tile = next;
+        ci = ni;
+        cs = ns;
+        offs(tile + tstep < tend ? tile + tstep : tile, ni, ns);
+    }
+}
+
+// ------------------------------------------------------------------------------------------------
 // Dense layer with conv1 and conv2 fused: the bottleneck of a spatial tile never leaves LDS.
 // A workgroup of NW waves (two per SIMD) loops over TH x TW output tiles.  For a tile it computes the
 // bottleneck of the (TH + 2) x (TW + 2) window around it (its in-image pixels, numbered row by row and
@@ -3059,6 +3382,47 @@ extern "C" int d8s_conv2_pair(const D8sConv2Args* a, const D8sConv2Args* b, void
     if (int rc = check_conv2(b, "d8s_conv2_pair")) return rc;
     REQUIRE(a->N == b->N && a->H == b->H && a->W == b->W, "d8s_conv2_pair: the two problems differ in shape");
     return conv2_dispatch(a, b, (hipStream_t)stream);
+}
+
+// Whether d8s_conv2_conv1 takes maps of this shape and a conv1 reading G groups.
+static bool c21_shape_ok(int H, int W, int G) {
+    return (W == 16 || W == 32 || W == 64) && (H * W) % 128 == 0 && G >= 2 && G <= D8S_C21_MAX_GROUPS;
+}
+
+extern "C" int d8s_c21_supported(int H, int W, int G) { return c21_shape_ok(H, W, G) ? 1 : 0; }
+
+extern "C" int d8s_conv2_conv1(const D8sConv2Args* c2, const D8sGemmArgs* c1, void* stream) {
+    if (int rc = check_conv2(c2, "d8s_conv2_conv1")) return rc;
+    if (int rc = check_gemm(c1, "d8s_conv2_conv1")) return rc;
+    REQUIRE(c1->cout == 128, "d8s_conv2_conv1: cout must be 128");
+    REQUIRE(c1->out != nullptr, "d8s_conv2_conv1: null output");
+    REQUIRE(c2->N == c1->N && (int64_t)c2->H * c2->W == c1->HW && c2->W == c1->W,
+            "d8s_conv2_conv1: conv2 and conv1 differ in shape");
+    REQUIRE(c21_shape_ok(c2->H, c2->W, c1->G),
+            "d8s_conv2_conv1: needs W in {16, 32, 64}, H * W a multiple of 128 and 2 <= G <= " +
+                std::to_string(D8S_C21_MAX_GROUPS));
+    REQUIRE(c1->G > c1->G0, "d8s_conv2_conv1: conv1's last group must be a store slot (G > G0)");
+    const int64_t slot = (int64_t)c1->rows * 32;
+    REQUIRE((const int8_t*)c2->out == c1->seg + (int64_t)(c1->G - 1 - c1->G0) * slot,
+            "d8s_conv2_conv1: conv2's output must be conv1's last group (store slot G - 1 - G0)");
+    const uint8_t* xb = c2->x;
+    const uint8_t* ob = (const uint8_t*)c1->out;
+    REQUIRE(xb + 4 * slot <= ob || ob + 4 * slot <= xb,
+            "d8s_conv2_conv1: conv2's bottleneck and conv1's output overlap");
+    const int64_t in0_bytes = (int64_t)c1->N * c1->G0 * c1->HW * 32;
+    REQUIRE(in0_bytes < (1ll << 32) && 4 * slot + (1ll << 20) < (1ll << 31),
+            "d8s_conv2_conv1: in0 of 4 GiB or more, or a bottleneck of 2 GiB or more");
+    const int64_t total = (int64_t)c1->N * (c1->HW / 128);
+    const int occ = c2->W == 64 ? CcShape<64>::OCC : CcShape<32>::OCC;   // workgroups per CU
+    const int64_t grid = total < occ * cu_count() ? total : occ * cu_count();
+    hipStream_t st = (hipStream_t)stream;
+#define C21_LAUNCH(W_)                                                                              \
+    hipLaunchKernelGGL((k_c21<W_>), dim3((unsigned)grid), dim3(256), cc_lds<W_>(c1->G), st, *c2, *c1)
+    if (c2->W == 16) C21_LAUNCH(16);
+    else if (c2->W == 32) C21_LAUNCH(32);
+    else C21_LAUNCH(64);
+#undef C21_LAUNCH
+    return launched("d8s_conv2_conv1");
 }
 
 template <int TW, int TH, int CPW, int NW>

@@ -556,12 +556,14 @@ class Layer(collections.namedtuple("Layer", "c1 c2 dense")):
     (`hip.DenseArgs`, None when the block runs the two launches)."""
 
 
-# How a block's layers run: "conv" conv1 + conv2 per layer (d8s_conv1, d8s_conv2); "tile" one fused
-# launch per layer (d8s_dense, the reference's fused kind "tile"); "img" the whole block in one launch,
-# a workgroup per image (d8s_dense_block, the reference's "img*" kinds); "parts" the whole block in one
-# launch with every image split into row bands, a workgroup per band (d8s_dense_block_parts; "parts:K"
-# for K bands, plain "parts" for as many as fill the chip).  The bytes are the same.
-BLOCK_KINDS = ("conv", "tile", "img", "parts")
+# How a block's layers run: "conv" conv1 + conv2 per layer (d8s_conv1, d8s_conv2); "chain" conv1 of
+# layer 0, then conv2 of each layer with conv1 of the next in one launch (d8s_conv2_conv1), conv2 of the
+# last layer (L + 1 launches; the bottleneck alternates between two buffers); "tile" one fused launch per
+# layer (d8s_dense, the reference's fused kind "tile"); "img" the whole block in one launch, a workgroup
+# per image (d8s_dense_block, the reference's "img*" kinds); "parts" the whole block in one launch with
+# every image split into row bands, a workgroup per band (d8s_dense_block_parts; "parts:K" for K bands,
+# plain "parts" for as many as fill the chip).  The bytes are the same.
+BLOCK_KINDS = ("conv", "chain", "tile", "img", "parts")
 IMG_MAX_PX = 256                # d8s_dense_block: pixels per image
 IMG_MAX_GROUPS = 64             # and groups read by the last layer
 LDS_BYTES = 160 * 1024
@@ -610,6 +612,13 @@ def _kind_name(kind) -> str:
     return str(kind).split(":", 1)[0]
 
 
+def chain_fits(b: dict) -> bool:
+    """Whether block `b` (meta) runs d8s_conv2_conv1: a map width it takes, whole 128-pixel tiles, at
+    least two layers and the last layer's conv1 within its group limit."""
+    return (b["w"] in hip.C21_WIDTHS and (b["h"] * b["w"]) % 128 == 0 and b["L"] >= 2
+            and b["c0"] // GROUP + b["L"] - 1 <= hip.C21_MAX_GROUPS)
+
+
 BAND_W = 128                    # d8s_dense runs its band form, faster than two launches, at this width
 BAND_MAX_GROUPS = 16            # (the conv1 weights of the layer in LDS)
 
@@ -626,11 +635,19 @@ def default_kind(b: dict, n: int, cus: int = 256) -> str:
     CUs) or splits into 8 bands (the 32 x 32 block of a 24-image study: one launch instead of 64
     latency-bound ones); "img" where a workgroup per image fits (at 96 images: its 96 workgroups leave
     room for a second encoder's pass on another stream, which 2-band launches of 192 did not); "tile"
-    for 128-wide blocks (the fused layer's band form); else "conv"."""
+    for 128-wide blocks (the fused layer's band form); "chain" for 32-wide blocks with at least three
+    128-pixel tiles per CU (the 32 x 32 block at 96 images: 0.81 against 0.89 ms per pass; the 64-wide
+    block runs its chained launches at two workgroups per CU, slower than two launches); else "conv"."""
     k = parts_for(b, n, cus)
     if k is not None and k >= 4 and (img_fits(b) or k >= 8):
         return f"parts:{k}"
-    return "img" if img_fits(b) else "tile" if band_fits(b) else "conv"
+    if img_fits(b):
+        return "img"
+    if band_fits(b):
+        return "tile"
+    if b["w"] == 32 and chain_fits(b) and n * b["h"] * b["w"] >= 3 * 128 * cus:
+        return "chain"
+    return "conv"
 
 
 def fused_blocks(meta: dict, fused=None, cus: int = 256) -> dict:
@@ -649,6 +666,10 @@ def fused_blocks(meta: dict, fused=None, cus: int = 256) -> dict:
             raise ValueError(f"block kind {kind!r}: expected one of {BLOCK_KINDS}")
         if kind == "img" and not img_fits(meta["blocks"][bi]):
             raise ValueError(f"block {bi} does not fit the whole-block kernel")
+        if kind == "chain" and not chain_fits(meta["blocks"][bi]):
+            b = meta["blocks"][bi]
+            raise ValueError(f"block {bi} ({b['h']} x {b['w']}, {b['L']} layers) does not run chained "
+                             f"conv2 + conv1 launches (widths {hip.C21_WIDTHS}, H * W a multiple of 128)")
         if _kind_name(kind) == "parts":
             b = meta["blocks"][bi]
             k = int(kind.split(":", 1)[1]) if ":" in str(kind) else parts_for(b, int(meta["n"]), cus)
@@ -733,6 +754,10 @@ class Dense8SEncoder:
         self.seg = [self.arenas[a].data_ptr() + in0 for a, in0 in lay]
         hw_max = max(b["h"] * b["w"] for b in blocks)
         self.bott = torch.empty(n * BOTTLENECK * hw_max, dtype=torch.uint8, device=d)
+        # "chain" blocks: conv2 of a layer reads one bottleneck while conv1 of the next writes the other
+        hw_chain = [b["h"] * b["w"] for bi, b in enumerate(blocks) if self.fused[bi] == "chain"]
+        self.bott2 = (torch.empty(n * BOTTLENECK * max(hw_chain), dtype=torch.uint8, device=d)
+                      if hw_chain else None)
         dev = torch.device(d)
         # only the tables the kernels read go to the device (a reference package also carries the
         # tables of its TensorRT and int8-stem paths)
@@ -757,10 +782,11 @@ class Dense8SEncoder:
             hw, g0 = b["h"] * b["w"], b["c0"] // GROUP
             layers = []
             for li in range(b["L"]):
+                bott = _ptr(self._bott_of(bi, li))
                 c1 = hip.GemmArgs(self.in0[bi], self.seg[bi], P(f"L{bi}_{li}_w1"),
                                   P(f"L{bi}_{li}_abh"), P(f"L{bi}_{li}_gdu"), P(f"L{bi}_{li}_w1sum"),
-                                  _ptr(self.bott), g0, g0 + li, n, hw, b["w"], n * hw, BOTTLENECK, 0)
-                c2 = hip.Conv2Args(_ptr(self.bott), P(f"L{bi}_{li}_w2k"), P(f"L{bi}_{li}_c2u"),
+                                  bott, g0, g0 + li, n, hw, b["w"], n * hw, BOTTLENECK, 0)
+                c2 = hip.Conv2Args(bott, P(f"L{bi}_{li}_w2k"), P(f"L{bi}_{li}_c2u"),
                                    P(f"L{bi}_{li}_w2sum"), self.seg[bi] + li * n * hw * GROUP,
                                    n, b["h"], b["w"], 0)
                 dn = None
@@ -803,6 +829,10 @@ class Dense8SEncoder:
         self.stem_args = hip.StemArgs(0, P("S_lut"), P("S_w16"), P("S_bias"), P("S_inv"),
                                       self.in0[0], n, img, img, self.in_kind, 0, 0)
 
+    def _bott_of(self, bi: int, li: int) -> torch.Tensor:
+        """The bottleneck buffer of layer li of block bi (in "chain" blocks odd layers use the second)."""
+        return self.bott2 if self.fused[bi] == "chain" and li % 2 else self.bott
+
     # -- one pass --
     @staticmethod
     def _mode(flip) -> int:
@@ -835,6 +865,9 @@ class Dense8SEncoder:
 
     def _conv2(self, c2, st: int) -> None:
         hip.check(self.lib.d8s_conv2(ctypes.byref(c2), st), "d8s_conv2")
+
+    def _chain(self, c2, c1, st: int) -> None:
+        hip.check(self.lib.d8s_conv2_conv1(ctypes.byref(c2), ctypes.byref(c1), st), "d8s_conv2_conv1")
 
     def _block(self, bi: int, st: int) -> None:
         args = self.block_args[bi]
@@ -875,6 +908,15 @@ class Dense8SEncoder:
             if bi in self.block_args:
                 self._block(bi, st)
                 mark(f"block_{bi}")
+                layers = ()
+            if self.fused[bi] == "chain":
+                self._conv1(layers[0].c1, st)
+                mark(f"conv1_{bi}")
+                for La, Lb in zip(layers, layers[1:]):
+                    self._chain(La.c2, Lb.c1, st)
+                    mark(f"chain_{bi}")
+                self._conv2(layers[-1].c2, st)
+                mark(f"conv2_{bi}")
                 layers = ()
             for L in layers:
                 if L.dense is not None:
@@ -1035,12 +1077,12 @@ class Dense8SEncoder:
         t = a[off:off + n * hw * GROUP].view(n, hw, GROUP)
         return t.permute(0, 2, 1).reshape(n, GROUP, h, w).float()
 
-    def bottleneck(self, bi: int) -> torch.Tensor:
+    def bottleneck(self, bi: int, li: int = 0) -> torch.Tensor:
         """The planar bottleneck of the last conv1 run in block bi as uint8 (nb, 128, h, w)."""
         b = self.meta["blocks"][bi]
         n, h, w = self.nb, b["h"], b["w"]
         hw = h * w
-        t = self.bott[:4 * n * hw * GROUP].view(4, n, hw, GROUP)
+        t = self._bott_of(bi, li)[:4 * n * hw * GROUP].view(4, n, hw, GROUP)
         return t.permute(1, 0, 3, 2).reshape(n, 4 * GROUP, h, w)
 
     @torch.no_grad()
@@ -1066,13 +1108,25 @@ class Dense8SEncoder:
                     for li in range(len(layers)):
                         out[(bi, li + 1)] = self.store(bi, li + 1).clone()
                     layers = ()
+                if self.fused[bi] == "chain":                # conv2 of li and conv1 of li + 1 together
+                    self._conv1(layers[0].c1, st)
+                    for li, L in enumerate(layers):
+                        self.stream.synchronize()
+                        out[("bott", bi, li)] = self.bottleneck(bi, li).clone()
+                        if li + 1 < len(layers):
+                            self._chain(L.c2, layers[li + 1].c1, st)
+                        else:
+                            self._conv2(L.c2, st)
+                        self.stream.synchronize()
+                        out[(bi, li + 1)] = self.store(bi, li + 1).clone()
+                    layers = ()
                 for li, L in enumerate(layers):
                     if L.dense is not None:                  # no bottleneck in memory
                         self._dense(L.dense, st)
                     else:
                         self._conv1(L.c1, st)
                         self.stream.synchronize()
-                        out[("bott", bi, li)] = self.bottleneck(bi).clone()
+                        out[("bott", bi, li)] = self.bottleneck(bi, li).clone()
                         self._conv2(L.c2, st)
                     self.stream.synchronize()
                     out[(bi, li + 1)] = self.store(bi, li + 1).clone()
@@ -1112,11 +1166,17 @@ class Dense8SEncoder:
         xf = self._padded(x[:self._per_pass(mode)].contiguous(), mode)
         st = self.stream.cuda_stream
         fams: dict[str, list] = {"stem": [lambda: self._stem(xf.data_ptr(), mode, st)],
-                                 "conv1": [], "conv2": [], "dense": [], "block": [], "trans": [],
-                                 "final": []}
+                                 "conv1": [], "conv2": [], "chain": [], "dense": [], "block": [],
+                                 "trans": [], "final": []}
         for bi, (layers, trans) in enumerate(self.plan_l):
             if bi in self.block_args:
                 fams["block"].append(lambda b=bi: self._block(b, st))
+                layers = ()
+            if self.fused[bi] == "chain":
+                fams["conv1"].append(lambda c=layers[0].c1: self._conv1(c, st))
+                for La, Lb in zip(layers, layers[1:]):
+                    fams["chain"].append(lambda a=La.c2, b=Lb.c1: self._chain(a, b, st))
+                fams["conv2"].append(lambda c=layers[-1].c2: self._conv2(c, st))
                 layers = ()
             for L in layers:
                 if L.dense is not None:
@@ -1158,6 +1218,14 @@ class Dense8SEncoder:
         for bi, (layers, trans) in enumerate(self.plan_l):
             if bi in self.block_args:
                 out[f"blk b{bi}"] = round(self._time(lambda b=bi: self._block(b, st), reps), 4)
+                layers = ()
+            if self.fused[bi] == "chain":
+                out[f"c1 b{bi}l0"] = round(self._time(lambda c=layers[0].c1: self._conv1(c, st), reps), 4)
+                for li, (La, Lb) in enumerate(zip(layers, layers[1:])):
+                    out[f"cc b{bi}l{li}"] = round(self._time(lambda a=La.c2, b=Lb.c1: self._chain(a, b, st),
+                                                             reps), 4)
+                out[f"c2 b{bi}l{len(layers) - 1}"] = round(
+                    self._time(lambda c=layers[-1].c2: self._conv2(c, st), reps), 4)
                 layers = ()
             for li, L in enumerate(layers):
                 if L.dense is not None:
@@ -1203,7 +1271,8 @@ class EncoderPair:
     (the 16 x 16 whole block: 192 workgroups in about the time of 96) instead of overlapping by chance
     on two streams (`encode_concurrent`).  Each encoder's outputs are exactly what it gives alone.  The
     pair runs on the first encoder's stream and orders the second's around it.  Steps without a pair
-    launch ("parts" blocks, the final features) run as two launches in the same sequence."""
+    launch ("parts" blocks, the chained conv2 + conv1 launches of "chain" blocks, the final features)
+    run as two launches in the same sequence."""
 
     def __init__(self, a: Dense8SEncoder, b: Dense8SEncoder):
         if a is b:
@@ -1237,6 +1306,15 @@ class EncoderPair:
                 else:
                     hip.check(lib.d8s_dense_block_pair(ctypes.byref(pa), ctypes.byref(pb), st),
                               "d8s_dense_block_pair")
+                la = lb = ()
+            if A.fused[bi] == "chain":                       # no pair launch of the chained kernel
+                hip.check(lib.d8s_conv1_pair(ctypes.byref(la[0].c1), ctypes.byref(lb[0].c1), st),
+                          "d8s_conv1_pair")
+                for i in range(len(la) - 1):
+                    A._chain(la[i].c2, la[i + 1].c1, st)
+                    B._chain(lb[i].c2, lb[i + 1].c1, st)
+                hip.check(lib.d8s_conv2_pair(ctypes.byref(la[-1].c2), ctypes.byref(lb[-1].c2), st),
+                          "d8s_conv2_pair")
                 la = lb = ()
             for La, Lb in zip(la, lb):
                 if La.dense is not None:

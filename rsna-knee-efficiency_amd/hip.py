@@ -94,6 +94,8 @@ def parts_xchg_bytes(nparts: int, w: int) -> int:
 
 
 PARTS_PIXELS = (32, 64, 128, 256)        # pixels per band d8s_dense_block_parts runs
+C21_WIDTHS = (16, 32, 64)                # map widths d8s_conv2_conv1 runs (H * W a multiple of 128)
+C21_MAX_GROUPS = 64                      # `D8S_C21_MAX_GROUPS`
 
 
 class StemArgs(ctypes.Structure):
@@ -154,6 +156,8 @@ SIGNATURES = {
     "d8s_conv1_acc32": [ctypes.POINTER(GemmArgs), vp, vp],
     "d8s_conv2": [ctypes.POINTER(Conv2Args), vp],
     "d8s_dense": [ctypes.POINTER(DenseArgs), vp],
+    "d8s_conv2_conv1": [ctypes.POINTER(Conv2Args), ctypes.POINTER(GemmArgs), vp],
+    "d8s_c21_supported": [i32, i32, i32],
     "d8s_dense_block": [ctypes.POINTER(BlockArgs), vp],
     "d8s_dense_block_parts": [ctypes.POINTER(PartsArgs), vp],
     "d8s_transition": [ctypes.POINTER(GemmArgs), vp],

@@ -126,6 +126,24 @@ def test_prep_workspace_size():
     assert b16.value - b1.value == 15 * (b1.value - 1024)
 
 
+def _chain_args(W=32, G=10, out2=None, out1=1 << 30):
+    """d8s_conv2_conv1 arguments of two 32 x 32 images (G0 8) with one field changed."""
+    H, N, G0, seg = 1024 // W if W else 32, 2, 8, 4096
+    rows = N * H * W
+    out2 = seg + (G - 1 - G0) * rows * 32 if out2 is None else out2
+    c2 = hip.Conv2Args(1 << 20, 1, 1, 1, out2, N, H, W, 0)
+    c1 = hip.GemmArgs(1, seg, 1, 1, 1, 1, out1, G0, G, N, H * W, W, rows, 128, 0)
+    return ctypes.byref(c2), ctypes.byref(c1), None
+
+
+@pytest.mark.parametrize("H,W,G", [(64, 64, 5), (32, 32, 39), (16, 16, 64), (12, 12, 8), (32, 48, 8),
+                                   (32, 128, 8), (32, 32, 65), (32, 32, 1), (8, 16, 2)])
+def test_chain_supported_shapes(H, W, G):
+    """The shapes d8s_conv2_conv1 takes: W in {16, 32, 64}, H W a multiple of 128, 2 <= G <= 64."""
+    want = W in (16, 32, 64) and (H * W) % 128 == 0 and 2 <= G <= 64
+    assert hip.library().d8s_c21_supported(H, W, G) == int(want)
+
+
 @pytest.mark.parametrize("name,args", [
     ("d8s_conv1", lambda: (None, None)),
     ("d8s_conv1_acc32", lambda: (ctypes.byref(hip.GemmArgs()), None, None)),
@@ -171,6 +189,12 @@ def test_prep_workspace_size():
                                                            N=3, H=4, W=4, B=1, SK=2, M=2)), None)),
     ("d8s_prep_resize", lambda: (ctypes.byref(_prep_args(out=8)), None)),
     ("d8s_micro_copy", lambda: (1, 1, 17, None)),
+    ("d8s_conv2_conv1", lambda: (None, None, None)),
+    ("d8s_conv2_conv1", lambda: _chain_args(W=48)),                  # a width it does not take
+    ("d8s_conv2_conv1", lambda: _chain_args(G=8)),                   # conv1's last group is in in0
+    ("d8s_conv2_conv1", lambda: _chain_args(out2=999)),              # conv2 writes another slot
+    ("d8s_conv2_conv1", lambda: _chain_args(out1=(1 << 20) + 100)),  # the two bottlenecks overlap
+    ("d8s_conv2_conv1", lambda: _chain_args(G=70)),                  # more groups than the LDS takes
 ])
 def test_invalid_arguments_fail_on_the_host(name, args):
     """Every one of these is rejected before any HIP call (so it is safe without a GPU)."""

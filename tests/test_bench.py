@@ -48,6 +48,14 @@ def test_bytes_scale_with_images_and_match_the_layer_sums():
     # per slice at batch 24 (weights read once per batch): the 128.7 MB of the layer-by-layer design
     b24 = bench.kernel_bytes(META, 24, {})
     assert abs(sum(sum(v) for v in b24.values()) / 24 / 1e6 - 128.7) < 1.5
+    # a chained block (conv2 of a layer with conv1 of the next): L - 1 launches that do not read the new
+    # layer's 32 channels back, its first conv1 and last conv2 as before
+    base, ch = bench.kernel_bytes(META, 96, {}), bench.kernel_bytes(META, 96, {2: "chain"})
+    M2 = 96 * BLOCKS[2]["h"] * BLOCKS[2]["w"]
+    assert len(ch["chain"]) == 31 and len(ch["conv1"]) == len(ch["conv2"]) == 82 - 31
+    assert sum(map(sum, base.values())) - sum(map(sum, ch.values())) == 31 * M2 * 32
+    ops_ch = bench.kernel_ops(META, 96, {2: "chain"})
+    assert abs(sum(ops_ch.values()) - sum(bench.kernel_ops(META, 96, {}).values())) < 1.0
 
 
 def _counter_csv(path: Path, rows: list[tuple[int, str, str, float]]) -> None:
@@ -65,15 +73,23 @@ def test_traffic_summary_scales_by_the_copy_kernel(tmp_path):
     conv1 = "void k_conv1p<false, 1, 2, 4>(D8sGemmArgs, int*)"
     fe = [(1, "k_copy(const u32x4*, u32x4*, long)", "FETCH_SIZE", gib / 2 / 1024)]
     wr = [(1, "k_copy(const u32x4*, u32x4*, long)", "WRITE_SIZE", gib / 1024)]
-    for d in range(2, 2 + 44):
+    chain = "void k_c21<32>(D8sConv2Args, D8sGemmArgs)"
+    # a pass of the default kinds at 96 images: 13 conv1 launches (block 1, block 2's first layer),
+    # 31 chained conv2 + conv1 launches (block 2)
+    for d in range(2, 2 + 13):
         fe.append((d, conv1, "FETCH_SIZE", 50e6 / 1024))       # reads 100 MB after the x2 scale
         wr.append((d, conv1, "WRITE_SIZE", 10e6 / 1024))
+    for d in range(20, 20 + 31):
+        fe.append((d, chain, "FETCH_SIZE", 40e6 / 1024))
+        wr.append((d, chain, "WRITE_SIZE", 15e6 / 1024))
     _counter_csv(tmp_path / "f" / "run_counter_collection.csv", fe)
     _counter_csv(tmp_path / "w" / "run_counter_collection.csv", wr)
     out = bench.traffic_summary(str(tmp_path / "f"), str(tmp_path / "w"), passes=1)
     assert "FETCH_SIZE scale 2.000, WRITE_SIZE scale 1.000" in out
     assert "traffic_per_launch[conv1] = 110000000" in out
-    assert "| conv1 | 44 | 100.00 | 10.00 | 110.00 |" in out
+    assert "| conv1 | 13 | 100.00 | 10.00 | 110.00 |" in out
+    assert "traffic_per_launch[chain] = 95000000" in out
+    assert "| chain | 31 | 80.00 | 15.00 | 95.00 |" in out
 
 
 def test_mfma_summary_weights_and_issued_ops(tmp_path):

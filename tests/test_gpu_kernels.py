@@ -152,6 +152,44 @@ def test_dense_layer(dev, H, W, C, c0, N):
     assert float((np.abs(want) == 127).mean()) < 0.9 and float((want == 0).mean()) < 0.9
 
 
+@pytest.mark.parametrize("H,W,C,c0,N", [
+    (64, 64, 160, 128, 3),       # block 1's first chained launch (G0 4, G 5)
+    (64, 64, 480, 128, 2),       # block 1's last (G 15)
+    (32, 32, 288, 256, 4),       # block 2's first (G 9)
+    (32, 32, 1248, 256, 3),      # block 2's last (G 39: ten weight chunks)
+    (16, 16, 672, 640, 5),       # 16-wide maps (G0 20, G 21)
+    (16, 32, 96, 64, 2),         # H != W
+    (8, 64, 128, 32, 3),         # two-row tiles, G0 1
+    (32, 32, 64, 32, 2),         # G = 2, the fewest groups
+    (32, 32, 416, 256, 96),      # 768 tiles: persistent workgroups, tiles split by XCD
+    (64, 64, 224, 128, 24),      # 768 tiles at 64 wide
+])
+def test_chain_conv2_conv1(dev, H, W, C, c0, N):
+    """d8s_conv2_conv1 (conv2 of a layer, then conv1 of the next on its output, one launch): the new
+    store slot and bottleneck equal the exact conv2 -> conv1 and the two-launch path d8s_conv2 +
+    d8s_conv1."""
+    c = cases.gemm_case(H, C, N=N, seed=47, W=W)
+    g0 = c0 // 32
+    in0, seg = cases.store_from_q(c.q, g0)
+    c = dataclasses.replace(c, G0=g0, in0=in0, seg=seg)
+    c2 = cases.conv2_case(H, N=N, seed=49, W=W)
+    print(f"chain H={H} W={W} C_in={C} G0={g0} G={c.G} N={N}", flush=True)
+    slot, bott = checks.run_chain(c, c2, dev)
+    slot2, bott2 = checks.run_chain(c, c2, dev, fused=False)
+    assert np.array_equal(slot, slot2), checks.bytes_cmp(slot, slot2)
+    assert np.array_equal(bott, bott2), checks.bytes_cmp(bott, bott2)
+    # the exact conv2, then the exact conv1 over the store with the new slot in place
+    _, q2 = checks.exact_conv2(c2)
+    assert np.array_equal(slot, q2), checks.bytes_cmp(slot, q2)
+    HW = H * W
+    q = c.q.copy()
+    q[:, C - 32:, :] = q2.reshape(N, HW, 32).transpose(0, 2, 1)
+    in0, seg = cases.store_from_q(q, g0)
+    _, want = checks.exact_conv1(dataclasses.replace(c, q=q, in0=in0, seg=seg))
+    assert np.array_equal(bott, want), checks.bytes_cmp(bott, want)
+    assert 0.0 < float((want == 0).mean()) < 0.9 and float((np.abs(q2) == 127).mean()) < 0.2
+
+
 @pytest.mark.parametrize("H,W,c0,L,N", [(16, 16, 640, 32, 3), (16, 16, 64, 3, 2), (7, 9, 96, 5, 3),
                                          (12, 20, 256, 4, 2)])
 def test_dense_block(dev, H, W, c0, L, N):
