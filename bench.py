@@ -59,6 +59,10 @@ HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, published
 I8_PEAK_TOPS = 5000.0          # MI355X dense int8 MFMA, published
 IMG = 512
 SLICES = 24
+C5_BLOCKS = [{"c0": 64, "h": 128, "w": 128, "L": 6, "trans": True},      # DenseNet169 at 512 px
+             {"c0": 128, "h": 64, "w": 64, "L": 12, "trans": True},
+             {"c0": 256, "h": 32, "w": 32, "L": 32, "trans": True},
+             {"c0": 640, "h": 16, "w": 16, "L": 32, "trans": False}]
 C5_STUDIES = 50                 # configuration 5 streams over 50 synthetic studies
 
 
@@ -241,26 +245,45 @@ def rocprof_summary(d: str) -> str:
 
 def family_run_summary(path: str) -> list[str]:
     """From a kernel trace of a bench.py run: the dispatches of the per-family timing (each family's
-    launches of a configuration-5 pass replayed back to back, `Dense8SEncoder.time_families`), i.e. the
-    dispatches of a family that follow one of the same family on the same queue, which is how a pass
-    never orders them.  Their mean duration is the average launch time behind bench.py's roofline."""
+    launches of a configuration-5 pass replayed back to back, `Dense8SEncoder.time_families`): runs of
+    consecutive dispatches of one family on one queue longer than any run of that family within a pass
+    (a pass of the default kinds at 96 images, `kernel_bytes`), the first dispatch of each run not
+    counted.  (A pass's own runs, e.g. the 31 chained launches of the 32 x 32 block, are left out: the
+    two seeds' passes run concurrently.)  Their mean duration is the average launch time behind
+    bench.py's roofline."""
     import csv
+    nb = 4 * SLICES
+    per_pass = {k: len(v) for k, v in kernel_bytes({"img": IMG, "blocks": C5_BLOCKS}, nb,
+                                                   dense8s.fused_blocks({"blocks": C5_BLOCKS, "n": nb})).items()}
     rows = [r for r in csv.DictReader(open(path)) if _family(r["Kernel_Name"])]
     rows.sort(key=lambda r: int(r["Start_Timestamp"]))
-    prev: dict = {}
+    runs: dict = {}                                   # queue -> [family, [durations]]
     acc: dict = {}
+
+    def close(run):
+        fam, ds = run
+        if fam != "copy" and len(ds) > per_pass.get(fam, 1):
+            a = acc.setdefault(fam, [0, 0.0])
+            a[0] += len(ds) - 1
+            a[1] += sum(ds[1:])
+
     for r in rows:
         fam = _family(r["Kernel_Name"])
         q = r["Queue_Id"]
-        if prev.get(q) == fam and fam != "copy":
-            a = acc.setdefault(fam, [0, 0.0])
-            a[0] += 1
-            a[1] += (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
-        prev[q] = fam
+        us = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
+        run = runs.get(q)
+        if run is not None and run[0] == fam:
+            run[1].append(us)
+            continue
+        if run is not None:
+            close(run)
+        runs[q] = [fam, [us]]
+    for run in runs.values():
+        close(run)
     out = [f"### family timing dispatches ({os.path.basename(path)})", "",
-           "Dispatches that follow one of the same family on the same queue (the back-to-back replays "
-           "of the per-family timing; the first launch of each replay is not counted).", "",
-           "| family | dispatches | mean us |", "|---|---|---|"]
+           "Runs of dispatches of one family on one queue longer than the family's runs within a pass "
+           "(the back-to-back replays of the per-family timing; the first launch of each run not "
+           "counted).", "", "| family | dispatches | mean us |", "|---|---|---|"]
     for fam, (n, us) in sorted(acc.items()):
         out.append(f"| {fam} | {n} | {us / n:.2f} |")
     return out + [""]
@@ -291,10 +314,7 @@ def traffic_summary(fetch_dir: str, write_dir: str, passes: int, copy_bytes: int
     kf = copy_bytes / (fe["copy"][1] / fe["copy"][0])
     kw = copy_bytes / (wr["copy"][1] / wr["copy"][0])
     nb = 4 * SLICES
-    meta_blocks = [{"c0": 64, "h": 128, "w": 128, "L": 6, "trans": True},
-                   {"c0": 128, "h": 64, "w": 64, "L": 12, "trans": True},
-                   {"c0": 256, "h": 32, "w": 32, "L": 32, "trans": True},
-                   {"c0": 640, "h": 16, "w": 16, "L": 32, "trans": False}]
+    meta_blocks = C5_BLOCKS
     alg = kernel_bytes({"img": IMG, "blocks": meta_blocks}, nb,
                        dense8s.fused_blocks({"blocks": meta_blocks, "n": nb}))
     lines = [f"Calibration: k_copy moves {copy_bytes} B read + {copy_bytes} B written per dispatch; "
@@ -333,10 +353,7 @@ def mfma_summary(pmc_dir: str, passes: int) -> str:
             d = per.setdefault(fam, {}).setdefault(r.get("Dispatch_Id", r.get("Correlation_Id", "")), {})
             d[r["Counter_Name"]] = d.get(r["Counter_Name"], 0.0) + float(r["Counter_Value"])
     nb = 4 * SLICES
-    meta_blocks = [{"c0": 64, "h": 128, "w": 128, "L": 6, "trans": True},
-                   {"c0": 128, "h": 64, "w": 64, "L": 12, "trans": True},
-                   {"c0": 256, "h": 32, "w": 32, "L": 32, "trans": True},
-                   {"c0": 640, "h": 16, "w": 16, "L": 32, "trans": False}]
+    meta_blocks = C5_BLOCKS
     kinds = dense8s.fused_blocks({"blocks": meta_blocks, "n": nb})
     alg = kernel_ops({"img": IMG, "blocks": meta_blocks}, nb, kinds)
     lines = ["| family | dispatches | MFMA busy (% of SIMD cycles, weighted) | MFMA ops issued per pass (G) "
@@ -352,6 +369,42 @@ def mfma_summary(pmc_dir: str, passes: int) -> str:
         a = alg.get(fam, 0.0)
         lines.append(f"| {fam} | {len(ds)} | {util:.1f} | {ops / 1e9:.1f} | {a / 1e9:.1f} | "
                      f"{ops / a if a else float('nan'):.3f} |")
+    return "\n".join(lines)
+
+
+WAVE_COUNTERS = ("SQ_WAVES", "SQ_WAVE_CYCLES", "SQ_BUSY_CYCLES", "SQ_WAIT_ANY", "SQ_WAIT_INST_ANY",
+                 "SQ_ACTIVE_INST_ANY", "SQ_ACTIVE_INST_VALU", "SQ_INSTS_VALU")
+
+
+def wave_summary(pmc_dir: str) -> str:
+    """Where the waves' cycles go, per kernel family, from one counter run of `bench.py --pmc-passes 1`
+    with `--pmc` WAVE_COUNTERS: every counter summed over the family's dispatches; the percentages
+    are of SQ_WAVE_CYCLES (the waves' resident cycles)."""
+    import csv
+    import glob
+
+    per: dict = {}
+    for path in glob.glob(os.path.join(pmc_dir, "**", "*counter_collection.csv"), recursive=True):
+        for r in csv.DictReader(open(path)):
+            fam = _family(r.get("Kernel_Name", ""))
+            if not fam or fam == "copy":
+                continue
+            f = per.setdefault(fam, {"dispatches": set()})
+            f["dispatches"].add(r.get("Dispatch_Id", r.get("Correlation_Id", "")))
+            f[r["Counter_Name"]] = f.get(r["Counter_Name"], 0.0) + float(r["Counter_Value"])
+    lines = ["| family | dispatches | waves | cycles per wave | waiting on memory/counters (SQ_WAIT_ANY) "
+             "| ready, not issued (SQ_WAIT_INST_ANY) | issuing (SQ_ACTIVE_INST_ANY) "
+             "| VALU issuing (SQ_ACTIVE_INST_VALU) | VALU instructions per wave |",
+             "|---|---|---|---|---|---|---|---|---|"]
+    for fam in ("stem", "dense", "conv1", "conv2", "chain", "trans", "block", "final"):
+        f = per.get(fam)
+        if not f or not f.get("SQ_WAVES") or not f.get("SQ_WAVE_CYCLES"):
+            continue
+        wc = f["SQ_WAVE_CYCLES"]
+        pct = lambda c: f"{100.0 * f.get(c, 0.0) / wc:.1f} %"  # noqa: E731
+        lines.append(f"| {fam} | {len(f['dispatches'])} | {int(f['SQ_WAVES'])} | {wc / f['SQ_WAVES']:.0f} | "
+                     f"{pct('SQ_WAIT_ANY')} | {pct('SQ_WAIT_INST_ANY')} | {pct('SQ_ACTIVE_INST_ANY')} | "
+                     f"{pct('SQ_ACTIVE_INST_VALU')} | {f.get('SQ_INSTS_VALU', 0.0) / f['SQ_WAVES']:.0f} |")
     return "\n".join(lines)
 
 
@@ -736,12 +789,18 @@ def main() -> None:
                          "replay) and its per-family kernel times, one JSON line (a clean kernel trace)")
     ap.add_argument("--mfma-summary", metavar="PMC_DIR",
                     help="print the MFMA use per family from a --pmc-passes counter run")
+    ap.add_argument("--wave-summary", metavar="PMC_DIR",
+                    help="print where the waves' cycles go per family from a --pmc-passes 1 run of "
+                         "the SQ counters WAVE_COUNTERS")
     args = ap.parse_args()
     if args.rocprof_summary:
         print(rocprof_summary(args.rocprof_summary))
         return
     if args.mfma_summary:
         print(mfma_summary(args.mfma_summary, passes=args.pmc_passes or 3))
+        return
+    if args.wave_summary:
+        print(wave_summary(args.wave_summary))
         return
     if args.traffic_summary:
         if args.path == "prep":

@@ -833,11 +833,13 @@ static size_t cc_lds(int G) {
 }
 
 // activation bytes of conv1 step t (t < Gp: this tile's group t, else the next tile's group t - Gp),
-// groups past G - 2 clamped to G - 2 (G - 1 comes from registers, padded steps are unused)
+// groups past G - 2 clamped to G - 2 (G - 1 comes from registers, padded steps are unused).  Without a
+// next tile (nx false) the loads past Gp are unused too and read group G - 2 again, which the last
+// steps just read (an L2 hit, not the tile's first groups again from HBM).
 DEV u32x4 cc_act(const uint8_t* in0, const uint8_t* seg, int64_t in_gs, int64_t seg_gs, int G0, int G, int Gp,
-                 int t, uint32_t ci, uint32_t cs, uint32_t ni, uint32_t ns) {
+                 int t, uint32_t ci, uint32_t cs, uint32_t ni, uint32_t ns, bool nx) {
     const bool cur = t < Gp;
-    int g = cur ? t : t - Gp;
+    int g = cur ? t : (nx ? t - Gp : G - 2);
     g = g < G - 1 ? g : G - 2;
     const bool in = g < G0;
     const uint8_t* base = in ? in0 + g * in_gs : seg + (int64_t)(g - G0) * seg_gs;
@@ -865,9 +867,10 @@ __global__ __launch_bounds__(256, CcShape<W_>::OCC) void k_c21(D8sConv2Args c2, 
     const int64_t M = c1.rows;
     const int p = 32 * wave + j, ty = p / W_, tx = p - ty * W_, q0 = ty * HWd + tx;
 
-    // tile order as k_conv2: XCD x walks one contiguous eighth of the tiles
+    // tile order as k_conv2: XCD x walks one contiguous eighth of the tiles (also with one tile per
+    // workgroup: neighbouring tiles share halo rows in that XCD's L2)
     int tile = blockIdx.x, tend = total, tstep = gridDim.x;
-    if (total > (int)gridDim.x && (gridDim.x & 7) == 0) {
+    if (total >= (int)gridDim.x && (gridDim.x & 7) == 0) {
         const int chunk = (total + 7) / 8, xcd = blockIdx.x & 7;
         tstep = gridDim.x >> 3;
         tile = xcd * chunk + (blockIdx.x >> 3);
@@ -972,7 +975,7 @@ __global__ __launch_bounds__(256, CcShape<W_>::OCC) void k_c21(D8sConv2Args c2, 
     w2load(0);
 #pragma unroll
     for (int s = 0; s < PF; ++s)
-        ra[s] = cc_act(in0, seg, in_gs, seg_gs, G0, G, Gp, s, ci, cs, ni, ns);
+        ra[s] = cc_act(in0, seg, in_gs, seg_gs, G0, G, Gp, s, ci, cs, ni, ns, true);
     w1load(stg, 0);
     {
         const uint32_t* abh32 = (const uint32_t*)c1.abh;
@@ -1056,7 +1059,7 @@ __global__ __launch_bounds__(256, CcShape<W_>::OCC) void k_c21(D8sConv2Args c2, 
         } else {                                                                                  \
             b_ = u32x4{0, 0, 0, 0};                                                               \
         }                                                                                         \
-        ra[slot] = cc_act(in0, seg, in_gs, seg_gs, G0, G, Gp, k_ + PF, ci, cs, ni, ns);           \
+        ra[slot] = cc_act(in0, seg, in_gs, seg_gs, G0, G, Gp, k_ + PF, ci, cs, ni, ns, more);     \
         _Pragma("unroll") for (int c_ = 0; c_ < 4; ++c_) acc[c_] = mfma_i8(rb[c_], b_, acc[c_]);  \
     } while (0)
         // the last chunk holds group G - 1 (G - 1 >= Gp - 4) and the padded steps

@@ -92,6 +92,49 @@ def test_traffic_summary_scales_by_the_copy_kernel(tmp_path):
     assert "| chain | 31 | 80.00 | 15.00 | 95.00 |" in out
 
 
+def test_family_run_summary_counts_only_the_timing_replays(tmp_path):
+    """The roofline's launch time from a kernel trace: runs of one family on one queue longer than its
+    runs in a pass (a pass's 31 chained launches, concurrent with another stream, are left out), the
+    first launch of each run not counted."""
+    chain = "void k_c21<32>(D8sConv2Args, D8sGemmArgs)"
+    conv1 = "void k_conv1p<false, 1, 2, 4>(D8sGemmArgs, int*, D8sGemmArgs, int)"
+    rows, t = [], 0
+
+    def add(name, us, q=1):
+        nonlocal t
+        rows.append({"Kernel_Name": name, "Queue_Id": q, "Start_Timestamp": t,
+                     "End_Timestamp": t + int(us * 1000)})
+        t += int(us * 1000) + 500
+
+    for _ in range(31):                               # a pass's run: slower, not counted
+        add(chain, 50.0)
+    add(conv1, 40.0)
+    for _ in range(62):                               # the family timing: 2 x 31 launches
+        add(chain, 27.0)
+    for _ in range(26):                               # conv1's timing: 2 x 13 launches
+        add(conv1, 36.0)
+    path = tmp_path / "run_kernel_trace.csv"
+    with open(path, "w", newline="") as f:
+        w = csv.DictWriter(f, fieldnames=list(rows[0]))
+        w.writeheader()
+        w.writerows(rows)
+    out = "\n".join(bench.family_run_summary(str(path)))
+    assert "| chain | 61 | 27.00 |" in out and "| conv1 | 25 | 36.00 |" in out
+
+
+def test_wave_summary_percentages_of_wave_cycles(tmp_path):
+    chain = "void k_c21<32>(D8sConv2Args, D8sGemmArgs)"
+    rows = []
+    for d in (1, 2):                                  # two dispatches, summed
+        rows += [(d, chain, "SQ_WAVES", 100.0), (d, chain, "SQ_WAVE_CYCLES", 5000.0),
+                 (d, chain, "SQ_WAIT_ANY", 2000.0), (d, chain, "SQ_WAIT_INST_ANY", 1000.0),
+                 (d, chain, "SQ_ACTIVE_INST_ANY", 2000.0), (d, chain, "SQ_ACTIVE_INST_VALU", 1500.0),
+                 (d, chain, "SQ_INSTS_VALU", 30000.0)]
+    _counter_csv(tmp_path / "s" / "run_counter_collection.csv", rows)
+    out = bench.wave_summary(str(tmp_path / "s"))
+    assert "| chain | 2 | 200 | 50 | 40.0 % | 20.0 % | 40.0 % | 30.0 % | 300 |" in out
+
+
 def test_mfma_summary_weights_and_issued_ops(tmp_path):
     conv2 = "void k_conv2<32, 8, 1, 2>(D8sConv2Args, int, int)"
     rows = []
