@@ -364,7 +364,9 @@ def summarize(worst: dict) -> dict:
 def smoke_check(device: str = "cuda:0") -> dict:
     """One small pass (a DenseNet with 2 layers per block, 2 images of 64 x 64, uint8 input) on the GPU:
     every launch bit-exact against the C oracle on the kernels' own inputs, the stem within 1 LSB, the
-    features close to the float64 emulation."""
+    features close to the float64 emulation.  Block 0 (16 x 16) runs as "chain" (its conv1, one
+    chained conv2 + conv1 launch, its last conv2), block 1 (8 x 8) as "parts" (the whole block in one
+    launch, images split into row bands), blocks 2-3 as their default "img"."""
     from rsna_knee_efficiency_amd import densenet
 
     from . import emulate as emu
@@ -377,7 +379,9 @@ def smoke_check(device: str = "cuda:0") -> dict:
     cal = dense8s.calibrate(model, [norm(cal_u8)])
     plan = dense8s.make_plan(model, cal, 64)
     pack = dense8s.make_pack(plan, 2, input_kind="u8", mean=(mean,) * 3, std=(std,) * 3)
-    enc = dense8s.Dense8SEncoder(pack, 0, 2)
+    kinds = dense8s.fused_blocks(pack["meta"])
+    kinds.update({0: "chain", 1: "parts"})
+    enc = dense8s.Dense8SEncoder(pack, 0, 2, fused=kinds)
     x = rng.integers(0, 256, (2, 3, 64, 64), dtype=np.uint8)
     xd = torch.from_numpy(x).to(device)
     trace, f = enc.trace(xd)
