@@ -196,7 +196,7 @@ def copy_probe(dev: torch.device, mib: int = 1024, reps: int = 5) -> dict:
 
 
 FAMILY = {"k_conv1": "conv1", "k_conv1p": "conv1", "k_conv2": "conv2", "k_c21": "chain", "k_dense": "dense",
-          "k_band": "dense", "k_dblock": "block", "k_trans": "trans", "k_stem": "stem",
+          "k_band": "dense", "k_dblock": "block", "k_dparts": "block", "k_trans": "trans", "k_stem": "stem",
           "k_stem_rows": "stem", "k_final": "final", "k_copy": "copy", "k_prep_setup": "prep_setup",
           "k_prep_hist": "prep_hist", "k_prep_select": "prep_select", "k_prep_norm": "prep_norm",
           "k_prep_resize": "prep_resize"}
@@ -369,6 +369,51 @@ def mfma_summary(pmc_dir: str, passes: int) -> str:
         a = alg.get(fam, 0.0)
         lines.append(f"| {fam} | {len(ds)} | {util:.1f} | {ops / 1e9:.1f} | {a / 1e9:.1f} | "
                      f"{ops / a if a else float('nan'):.3f} |")
+    return "\n".join(lines)
+
+
+def c4_summary(trace_csv: str) -> str:
+    """Per-pass kernel times of a configuration-4 kernel trace (`rocprofv3 --kernel-trace` of
+    `bench.py --c4-passes P`): the trace split into passes at every stem dispatch, the segments holding
+    one final-features dispatch and a transition kept (whole passes of the graph replays), then per
+    kernel the median over passes of its launches and microseconds."""
+    import csv
+    import statistics
+
+    rows = [r for r in csv.DictReader(open(trace_csv)) if _family(r["Kernel_Name"])]
+    rows.sort(key=lambda r: int(r["Start_Timestamp"]))
+    segs, cur = [], None
+    for r in rows:
+        fam = _family(r["Kernel_Name"])
+        if fam == "stem":
+            cur = []
+            segs.append(cur)
+        if cur is not None:
+            cur.append(r)
+    passes = [sg for sg in segs if sum(_family(r["Kernel_Name"]) == "final" for r in sg) == 1
+              and any(_family(r["Kernel_Name"]) == "trans" for r in sg)]
+    if not passes:
+        return "no whole pass in the trace"
+    per: dict = {}
+    spans = []
+    for sg in passes:
+        spans.append((int(sg[-1]["End_Timestamp"]) - int(sg[0]["Start_Timestamp"])) / 1e3)
+        acc: dict = {}
+        for r in sg:
+            k = r["Kernel_Name"].split("(")[0].replace("void ", "")
+            a = acc.setdefault(k, [0, 0.0])
+            a[0] += 1
+            a[1] += (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
+        for k, (n, us) in acc.items():
+            per.setdefault(k, []).append((n, us))
+    lines = [f"{len(passes)} whole passes; median pass span {statistics.median(spans):.1f} us", "",
+             "| kernel | family | launches per pass | us per pass |", "|---|---|---|---|"]
+    tot = 0.0
+    for k, v in sorted(per.items(), key=lambda kv: -statistics.median(us for _, us in kv[1])):
+        med = statistics.median(us for _, us in v)
+        tot += med
+        lines.append(f"| `{k}` | {_family(k + '(')} | {int(statistics.median(n for n, _ in v))} | {med:.1f} |")
+    lines += ["", f"sum of the per-kernel medians: {tot:.1f} us per pass"]
     return "\n".join(lines)
 
 
@@ -789,6 +834,8 @@ def main() -> None:
                          "replay) and its per-family kernel times, one JSON line (a clean kernel trace)")
     ap.add_argument("--mfma-summary", metavar="PMC_DIR",
                     help="print the MFMA use per family from a --pmc-passes counter run")
+    ap.add_argument("--c4-summary", metavar="TRACE_CSV",
+                    help="print the per-pass kernel times of a --c4-passes kernel trace")
     ap.add_argument("--wave-summary", metavar="PMC_DIR",
                     help="print where the waves' cycles go per family from a --pmc-passes 1 run of "
                          "the SQ counters WAVE_COUNTERS")
@@ -801,6 +848,9 @@ def main() -> None:
         return
     if args.wave_summary:
         print(wave_summary(args.wave_summary))
+        return
+    if args.c4_summary:
+        print(c4_summary(args.c4_summary))
         return
     if args.traffic_summary:
         if args.path == "prep":

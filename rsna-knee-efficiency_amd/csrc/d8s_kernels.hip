@@ -807,9 +807,9 @@ __global__ __launch_bounds__(256, 2) void k_conv2(D8sConv2Args a0, int tiles_x, 
 //         prefetch running on into the next tile's first groups (in flight during its conv2), the
 //         weights in 4-group chunks double-buffered.
 // Group G - 1 (the new one) is never read from memory: its step takes the conv2 result (the load of
-// that slot is clamped to G - 2 and its value unused).  With at most 64 KB of LDS per workgroup
-// (W <= 32) three workgroups share a CU (the registers are bounded for it), as many as k_conv1p runs
-// on these maps; W = 64 runs two.  Offsets are 32-bit where the host checked the sizes.
+// that slot is clamped to G - 2 and its value unused).  At most 53 KB of LDS per workgroup (W = 64:
+// one plane buffer, two barriers per plane) and 168 VGPRs: three workgroups share a CU.  Offsets are
+// 32-bit where the host checked the sizes.
 // ------------------------------------------------------------------------------------------------
 template <int W_>
 struct CcShape {
@@ -819,9 +819,10 @@ struct CcShape {
     static constexpr int NCH = (NCHUNK + 255) / 256;      // per thread
     static constexpr size_t HALO = (size_t)NCHUNK * 16;
     static constexpr size_t W2BUF = 9 * 32 * 32;          // one input plane of the conv2 weights
-    static constexpr size_t A_BYTES = HALO + 2 * W2BUF, B_BYTES = 2 * 4 * 4096;
+    static constexpr int NW2 = W_ <= 32 ? 2 : 1;          // plane buffers (one where the halo is large)
+    static constexpr size_t A_BYTES = HALO + NW2 * W2BUF, B_BYTES = 2 * 4 * 4096;
     static constexpr size_t UNION = A_BYTES > B_BYTES ? A_BYTES : B_BYTES;
-    static constexpr int OCC = W_ <= 32 ? 3 : 2;          // workgroups per CU
+    static constexpr int OCC = 3;                         // workgroups per CU
     static_assert(128 % W_ == 0 && R >= 2, "tile = whole rows of 128 pixels");
 };
 
@@ -1004,9 +1005,14 @@ __global__ __launch_bounds__(256, CcShape<W_>::OCC) void k_c21(D8sConv2Args c2, 
         for (int v = 0; v < 16; ++v) acc2[v] = s_ini2[res_row(v, h)];
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
+            if (S::NW2 == 1 && c > 0) {                      // one buffer: plane c replaces c - 1
+                __syncthreads();
+                w2store(0);
+                __syncthreads();
+            }
             if (c < 3) w2load(c + 1);
             __builtin_amdgcn_sched_barrier(0);               // (issued before the plane's MFMAs)
-            const u32x4* pw = s_w2 + (c & 1) * 576;
+            const u32x4* pw = s_w2 + (S::NW2 == 1 ? 0 : (c & 1) * 576);
             const u32x4* px = s_u + c * HP * 2;
             u32x4 aw[2], bx[2];
             auto fetch = [&](int tap, int slot) INLINE {
@@ -1020,7 +1026,7 @@ __global__ __launch_bounds__(256, CcShape<W_>::OCC) void k_c21(D8sConv2Args c2, 
                 if (tap + 1 < 9) fetch(tap + 1, (tap + 1) & 1);
                 acc2 = mfma_i8(aw[tap & 1], bx[tap & 1], acc2);
             }
-            if (c < 3) {
+            if (S::NW2 == 2 && c < 3) {
                 w2store((c + 1) & 1);                        // buffer last read in plane c - 1
                 __syncthreads();
             }
@@ -3416,7 +3422,7 @@ extern "C" int d8s_conv2_conv1(const D8sConv2Args* c2, const D8sGemmArgs* c1, vo
     REQUIRE(in0_bytes < (1ll << 32) && 4 * slot + (1ll << 20) < (1ll << 31),
             "d8s_conv2_conv1: in0 of 4 GiB or more, or a bottleneck of 2 GiB or more");
     const int64_t total = (int64_t)c1->N * (c1->HW / 128);
-    const int occ = c2->W == 64 ? CcShape<64>::OCC : CcShape<32>::OCC;   // workgroups per CU
+    const int occ = CcShape<32>::OCC;                      // workgroups per CU (3 for every width)
     const int64_t grid = total < occ * cu_count() ? total : occ * cu_count();
     hipStream_t st = (hipStream_t)stream;
 #define C21_LAUNCH(W_)                                                                              \

@@ -635,9 +635,10 @@ def default_kind(b: dict, n: int, cus: int = 256) -> str:
     CUs) or splits into 8 bands (the 32 x 32 block of a 24-image study: one launch instead of 64
     latency-bound ones); "img" where a workgroup per image fits (at 96 images: its 96 workgroups leave
     room for a second encoder's pass on another stream, which 2-band launches of 192 did not); "tile"
-    for 128-wide blocks (the fused layer's band form); "chain" for 32-wide blocks with at least three
-    128-pixel tiles per CU (the 32 x 32 block at 96 images: 0.81 against 0.89 ms per pass; the 64-wide
-    block runs its chained launches at two workgroups per CU, slower than two launches); else "conv"."""
+    for 128-wide blocks (the fused layer's band form); "chain" where the block's 128-pixel tiles fill
+    one round of three workgroups per CU to at least two thirds (the 32 x 32 block at 96 images: 0.82
+    against 0.89 ms per pass; the 64 x 64 block at 24 images: 0.24 against 0.26 ms; at 96 images that
+    block's four tiles per workgroup run slower chained than as two launches); else "conv"."""
     k = parts_for(b, n, cus)
     if k is not None and k >= 4 and (img_fits(b) or k >= 8):
         return f"parts:{k}"
@@ -645,7 +646,8 @@ def default_kind(b: dict, n: int, cus: int = 256) -> str:
         return "img"
     if band_fits(b):
         return "tile"
-    if b["w"] == 32 and chain_fits(b) and n * b["h"] * b["w"] >= 3 * 128 * cus:
+    tiles = n * b["h"] * b["w"] // 128
+    if chain_fits(b) and 2 * cus < tiles <= 3 * cus:
         return "chain"
     return "conv"
 

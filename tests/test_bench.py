@@ -135,6 +135,39 @@ def test_wave_summary_percentages_of_wave_cycles(tmp_path):
     assert "| chain | 2 | 200 | 50 | 40.0 % | 20.0 % | 40.0 % | 30.0 % | 300 |" in out
 
 
+def test_c4_summary_medians_over_whole_passes(tmp_path):
+    """Per-pass kernel times from a configuration-4 trace: passes split at the stem, only whole ones
+    (a final-features dispatch and a transition) kept, medians over them."""
+    names = {"stem": "void k_stem_rows<true>(D8sStemArgs, int, int, D8sStemArgs, int)",
+             "chain": "void k_c21<64>(D8sConv2Args, D8sGemmArgs)",
+             "trans": "void k_trans<5, 1, 4, 2>(D8sGemmArgs, D8sGemmArgs, int)",
+             "final": "k_final(signed char const*, int, signed char const*, int, int, int, float const*, float*, int)"}
+    rows, t = [], 0
+
+    def add(fam, us):
+        nonlocal t
+        rows.append({"Kernel_Name": names[fam], "Queue_Id": 1, "Start_Timestamp": t,
+                     "End_Timestamp": t + int(us * 1000)})
+        t += int(us * 1000) + 100
+
+    for p, extra in enumerate((0.0, 1.0, 2.0)):       # three passes: chain 10 + extra us, twice
+        add("stem", 60.0)
+        add("chain", 10.0 + extra)
+        add("chain", 10.0 + extra)
+        add("trans", 20.0)
+        add("final", 5.0)
+    add("stem", 60.0)                                 # a partial pass: not counted
+    add("chain", 99.0)
+    path = tmp_path / "run_kernel_trace.csv"
+    with open(path, "w", newline="") as f:
+        w = csv.DictWriter(f, fieldnames=list(rows[0]))
+        w.writeheader()
+        w.writerows(rows)
+    out = bench.c4_summary(str(path))
+    assert out.startswith("3 whole passes")
+    assert "| `k_c21<64>` | chain | 2 | 22.0 |" in out and "| `k_stem_rows<true>` | stem | 1 | 60.0 |" in out
+
+
 def test_mfma_summary_weights_and_issued_ops(tmp_path):
     conv2 = "void k_conv2<32, 8, 1, 2>(D8sConv2Args, int, int)"
     rows = []
