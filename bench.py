@@ -7,8 +7,9 @@ Workload (`value`): configuration 5, sustained throughput.  A step = one synthet
 DenseNet169 weight sets x 2 crops x 24 slices of 3 x 512 x 512 uint8 with flip TTA = one pass of 96
 encoded images per seed (48 slices + their mirrors, the flip fused in the stem), i.e. 192 encoded
 slices per step.  Inputs are resident in HBM: 50 distinct seeded studies (`synthetic.c5_study`, seeds
-1234..1283), step k encoding study k mod 50; each encoder call replays its HIP graph.
-value = 192 K / T slices/s.  `c5_all_studies`: the 50 studies once each, back to back.
+1234..1283), step k encoding study k mod 50 (K = 50 by default: every study once); each encoder
+call replays its HIP graph.  value = 192 K / T slices/s.  `c5_all_studies`: the 50 studies once each,
+back to back, after the timed steps.
 `study_latency_ms`: configuration 4, one 24-slice study through one encoder (batch 24, one pass).
 The two seeds' passes of a step run from two streams (`--serial`: one after the other).
 `roofline`: the dominant kernel family: its launches of a configuration-5 pass recorded R times in a HIP
@@ -808,7 +809,7 @@ def bench_prep(dev: torch.device, steps: int, warmup: int, with_cpu: bool) -> di
 def main() -> None:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--prof-reps", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true")
