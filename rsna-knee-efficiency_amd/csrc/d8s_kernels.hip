@@ -929,14 +929,15 @@ __global__ __launch_bounds__(256, CcShape<W_>::OCC) void k_c21(D8sConv2Args c2, 
         }
     };
     // conv2 weights of input plane c: 576 chunks ([tap][out][half]), at most 3 per thread (buffer loads:
-    // one lane offset, the plane and part in the scalar offset; past the table they read zero, unused)
+    // one lane offset, the plane and part in the scalar offset; every read inside the table: the third
+    // part's chunks 512-575 are read by lanes tid & 63, the other lanes' copies unused)
     const __amdgpu_buffer_rsrc_t rw2 = __builtin_amdgcn_make_buffer_rsrc((void*)c2.w, 0, 36864, 0x00020000);
     u32x4 wst[3];
     auto w2load = [&](int c) INLINE {
 #pragma unroll
         for (int u = 0; u < 3; ++u)
             wst[u] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                rw2, (uint32_t)tid * 16, (uint32_t)(c * 9216 + u * 4096), 0));
+                rw2, (uint32_t)((u < 2 ? tid : tid & 63) * 16), (uint32_t)(c * 9216 + u * 4096), 0));
     };
     auto w2store = [&](int buf) INLINE {
         int t0 = tid;
@@ -949,14 +950,15 @@ __global__ __launch_bounds__(256, CcShape<W_>::OCC) void k_c21(D8sConv2Args c2, 
     };
 
     const int Gp = (G + PF - 1) & ~(PF - 1), nchunk = Gp >> 2;
-    // conv1 weights: 4-group chunks of 16 KB, 4 loads per thread, as buffer loads (past the table:
-    // zero, read only by padded steps, whose activation operand is zero)
+    // conv1 weights: 4-group chunks of 16 KB, 4 loads per thread (one group each), as buffer loads with
+    // the group in the scalar offset, clamped to group G - 1 past the table (read only by padded steps,
+    // whose activation operand is zero): every read inside the table
     const __amdgpu_buffer_rsrc_t rw1 = __builtin_amdgcn_make_buffer_rsrc((void*)c1.w, 0, G * 4096, 0x00020000);
     auto w1load = [&](u32x4* dst, int chunk) INLINE {
 #pragma unroll
         for (int u = 0; u < 4; ++u)
             dst[u] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                rw1, (uint32_t)tid * 16, (uint32_t)(chunk * 16384 + u * 4096), 0));
+                rw1, (uint32_t)tid * 16, (uint32_t)(min(4 * chunk + u, G - 1) * 4096), 0));
     };
     auto w1store = [&](const u32x4* src, int buf) INLINE {
         int t0 = tid;
