@@ -232,6 +232,12 @@ int d8s_transition(const D8sGemmArgs* a, void* stream);
 int d8s_final(const int8_t* in0, int32_t G0, const int8_t* seg, int32_t N, int32_t HW,
               const float* ab, float* out, int32_t ctot, void* stream);
 
+/* Linear head on the final features: out[n][k] = b[k] + sum_c x[n][c] w[k][c] in float32 (x [N][C],
+ * w [K][C], b [K], out [N][K]; K <= 4096).  Configuration 4's 1664 -> 8 logits after the encoder; the
+ * reference runs its head right after the encoder on the same device (src/knee/infer.py:1015-1017). */
+int d8s_linear(const float* x, int32_t N, int32_t C, const float* w, const float* b, int32_t K, float* out,
+               void* stream);
+
 /* Stem (see D8sStemArgs).  H and W multiples of 4.  Widths up to 512 run a row-band kernel (pooling
  * in registers, one quantisation per pooled value), wider ones a tile kernel; both give the same bytes. */
 int d8s_stem(const D8sStemArgs* a, void* stream);

@@ -2615,6 +2615,27 @@ __global__ __launch_bounds__(256, NT <= 5 && WB < 4 ? 2 : 1) void k_trans(D8sGem
 }
 
 // ------------------------------------------------------------------------------------------------
+// Linear head on the final features (configuration 4's 1664 -> 8 logits): out[n][k] = b[k] + the
+// float32 dot product of x[n][.] and w[k][.].  Workgroup = one image, wave = output k (k, k + 4, ...):
+// lane l sums c = l, l + 64, ... with fma in that order, then the 64 lane sums are added by a butterfly
+// (xor 32, 16, ..., 1), and b[k] last.
+// ------------------------------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void k_linear(const float* __restrict__ x, int C, const float* __restrict__ w,
+                                                const float* __restrict__ b, int K, float* __restrict__ out) {
+    const int n = blockIdx.x, lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
+    const float* xn = x + (int64_t)n * C;
+    for (int k = wave; k < K; k += 4) {
+        const float* wk = w + (int64_t)k * C;
+        float s = 0.0f;
+        for (int c = lane; c < C; c += 64) s = __builtin_fmaf(xn[c], wk[c], s);
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off, 64);
+        if (lane == 0) out[(int64_t)n * K + k] = s + b[k];
+    }
+}
+
+// ------------------------------------------------------------------------------------------------
 // Final features: out[n][c] = (((P0 + P1) + P2) + P3) / HW with P_q = sum over pixels s = q, q + 4, ...
 // (in order) of relu(fma(a_c, q_s, b_c)): the summation order of the reference's `final_q`
 // (src/knee/dense8s_kernels.cu:2304-2323), so the fp32 result is the same.  Workgroup = one image x 2
@@ -3662,6 +3683,15 @@ extern "C" int d8s_final(const int8_t* in0, int32_t G0, const int8_t* seg, int32
     hipLaunchKernelGGL(k_final, dim3((unsigned)N, (unsigned)((G + 1) / 2)), dim3(256), 0,
                        (hipStream_t)stream, in0, G0, seg, N, HW, G, ab, out, ctot);
     return launched("d8s_final");
+}
+
+extern "C" int d8s_linear(const float* x, int32_t N, int32_t C, const float* w, const float* b, int32_t K,
+                          float* out, void* stream) {
+    REQUIRE(x && w && b && out, "d8s_linear: null pointer");
+    REQUIRE(N >= 1 && C >= 1 && K >= 1 && K <= 4096, "d8s_linear: N, C >= 1 and 1 <= K <= 4096");
+    REQUIRE(N < (1 << 30), "d8s_linear: N too large");
+    hipLaunchKernelGGL(k_linear, dim3((unsigned)N), dim3(256), 0, (hipStream_t)stream, x, C, w, b, K, out);
+    return launched("d8s_linear");
 }
 
 static int check_stem(const D8sStemArgs* a, const char* what) {

@@ -104,3 +104,35 @@ class KneeHead:
         stream = torch.cuda.current_stream(self.device).cuda_stream
         hip.call("d8s_head", ctypes.byref(a), ctypes.c_void_p(stream))
         return logits
+
+
+class LinearHead:
+    """A linear head on the encoder's features on the GPU (`d8s_linear`): (N, C) float32 features ->
+    (N, K) logits = x W^T + b in float32, on the current stream.  Configuration 4's 1664 -> 8 head after
+    the encoder (the reference runs its head right after the encoder on the same device,
+    src/knee/infer.py:1015-1017).  There is no CPU path: without the library the call raises."""
+
+    def __init__(self, w, b, device) -> None:
+        self.device = torch.device(device)
+        self.w = torch.as_tensor(w, dtype=torch.float32).to(self.device).contiguous()
+        self.b = torch.as_tensor(b, dtype=torch.float32).to(self.device).contiguous()
+        if self.w.dim() != 2 or self.b.shape != (self.w.shape[0],):
+            raise ValueError("w must be (K, C) and b (K,)")
+        self.K, self.C = self.w.shape
+        self._out: torch.Tensor | None = None
+
+    def __call__(self, x: torch.Tensor) -> torch.Tensor:
+        """x (N, C) float32 on the head's device -> logits (N, K) float32, in a buffer of the head's own
+        (valid until the next call with as many rows or more)."""
+        if x.dim() != 2 or x.shape[1] != self.C or x.dtype != torch.float32 or x.device != self.device:
+            raise ValueError(f"x must be (N, {self.C}) float32 on {self.device}")
+        x = x.contiguous()
+        n = x.shape[0]
+        if self._out is None or self._out.shape[0] < n:
+            self._out = torch.empty((n, self.K), dtype=torch.float32, device=self.device)
+        out = self._out[:n]
+        stream = torch.cuda.current_stream(self.device).cuda_stream
+        hip.call("d8s_linear", x.data_ptr(), n, self.C, self.w.data_ptr(), self.b.data_ptr(), self.K,
+                 out.data_ptr(), ctypes.c_void_p(stream))
+        hip.written(out)
+        return out

@@ -162,6 +162,7 @@ SIGNATURES = {
     "d8s_dense_block_parts": [ctypes.POINTER(PartsArgs), vp],
     "d8s_transition": [ctypes.POINTER(GemmArgs), vp],
     "d8s_final": [vp, i32, vp, i32, i32, vp, vp, i32, vp],
+    "d8s_linear": [vp, i32, i32, vp, vp, i32, vp, vp],
     "d8s_stem": [ctypes.POINTER(StemArgs), vp],
     "d8s_stem_pair": [ctypes.POINTER(StemArgs), ctypes.POINTER(StemArgs), vp],
     "d8s_conv1_pair": [ctypes.POINTER(GemmArgs), ctypes.POINTER(GemmArgs), vp],

@@ -189,6 +189,9 @@ def test_chain_supported_shapes(H, W, G):
                                                            N=3, H=4, W=4, B=1, SK=2, M=2)), None)),
     ("d8s_prep_resize", lambda: (ctypes.byref(_prep_args(out=8)), None)),
     ("d8s_micro_copy", lambda: (1, 1, 17, None)),
+    ("d8s_linear", lambda: (None, 2, 1664, 8, 8, 8, 8, None)),
+    ("d8s_linear", lambda: (8, 0, 1664, 8, 8, 8, 8, None)),
+    ("d8s_linear", lambda: (8, 2, 1664, 8, 8, 5000, 8, None)),
     ("d8s_conv2_conv1", lambda: (None, None, None)),
     ("d8s_conv2_conv1", lambda: _chain_args(W=48)),                  # a width it does not take
     ("d8s_conv2_conv1", lambda: _chain_args(G=8)),                   # conv1's last group is in in0

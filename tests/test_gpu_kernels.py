@@ -277,6 +277,25 @@ def test_final(dev, N, HW, C, c0):
     assert np.abs(got - ref).max() / np.abs(ref).max() < 1e-5
 
 
+@pytest.mark.parametrize("N,C,K", [(24, 1664, 8), (96, 1664, 8), (5, 100, 3), (1, 64, 4), (3, 1664, 9)])
+def test_linear_head(dev, N, C, K):
+    """d8s_linear (configuration 4's 1664 -> 8 logits on the device) against the float64 product: every
+    logit within 2e-6 of the sum of |x w| over its terms plus |b| (float32 fma chains of C / 64 terms
+    per lane and a 64-lane butterfly)."""
+    from rsna_knee_efficiency_amd import head as head_mod
+    rng = np.random.default_rng(N * C + K)
+    x = rng.normal(0, 1, (N, C)).astype(np.float32)
+    w = rng.normal(0, 1 / np.sqrt(C), (K, C)).astype(np.float32)
+    b = rng.normal(0, 0.1, K).astype(np.float32)
+    lin = head_mod.LinearHead(w, b, dev)
+    got = lin(_t(x, dev)).cpu().numpy()
+    ref = x.astype(np.float64) @ w.astype(np.float64).T + b
+    scale = np.abs(x.astype(np.float64)) @ np.abs(w.astype(np.float64)).T + np.abs(b)
+    assert np.all(np.abs(got - ref) <= 2e-6 * scale), float((np.abs(got - ref) / scale).max())
+    # the same launch twice gives the same bits (fixed summation order)
+    assert np.array_equal(lin(_t(x, dev)).cpu().numpy(), got)
+
+
 def _stem_tables(seed: int = 3):
     rng = np.random.default_rng(seed)
     w = rng.normal(0, np.sqrt(2 / 147), (64, 3, 7, 7)).astype(np.float32)
