@@ -265,13 +265,33 @@ template <int MODE, bool HAS, bool WROW, class F>
 DEV void run_blocks(const PStack& st, const PArgs& a, int b0, int b1, float* s_st, F&& f) {
     const int img = a.img;
     if constexpr (MODE == M_FLOAT) {
+        // a thread's units u = tid + NT i of a block in batches of FB: the batch's loads are issued
+        // before any of its values is used (the histogram passes' LDS atomics would otherwise keep
+        // each load behind the previous unit's counting); units past the block load its last unit
+        // again and are not used
+        constexpr int FB = 4;
         for (int b = b0; b < b1; ++b) {
             const Geo g = block_geo<MODE>(st, a, b);
-            for (int u = threadIdx.x; u < g.rb * a.upr; u += NT) {
-                const int row = fdiv(u, a.upr, a.inv_upr), dx0 = (u - row * a.upr) * UP, dy = g.r0 + row;
-                const float4 x = *(const float4*)((const float*)st.src + ((int64_t)g.kk * img + dy) * img + dx0);
-                float v[UP] = {x.x, x.y, x.z, x.w};
-                f(g.kk, dy, dx0, v);
+            const int n = g.rb * a.upr;
+            const float* base = (const float*)st.src + (int64_t)g.kk * img * img;
+            for (int u0 = threadIdx.x; u0 < n; u0 += FB * NT) {
+                float4 x[FB];
+                int dy[FB], dx0[FB];
+#pragma unroll
+                for (int i = 0; i < FB; ++i) {
+                    const int u = min(u0 + i * NT, n - 1);
+                    const int row = fdiv(u, a.upr, a.inv_upr);
+                    dx0[i] = (u - row * a.upr) * UP;
+                    dy[i] = g.r0 + row;
+                    x[i] = *(const float4*)(base + (int64_t)dy[i] * img + dx0[i]);
+                }
+#pragma unroll
+                for (int i = 0; i < FB; ++i) {
+                    if (u0 + i * NT < n) {
+                        float v[UP] = {x[i].x, x[i].y, x[i].z, x[i].w};
+                        f(g.kk, dy[i], dx0[i], v);
+                    }
+                }
             }
         }
         return;

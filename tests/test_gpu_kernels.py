@@ -163,6 +163,8 @@ def test_dense_layer(dev, H, W, C, c0, N):
     (32, 32, 64, 32, 2),         # G = 2, the fewest groups
     (32, 32, 416, 256, 96),      # 768 tiles: persistent workgroups, tiles split by XCD
     (64, 64, 224, 128, 24),      # 768 tiles at 64 wide
+    (32, 32, 288, 256, 100),     # 800 tiles: workgroups with two tiles (the next tile's prefetch)
+    (64, 64, 352, 128, 30),      # 960 tiles at 64 wide
 ])
 def test_chain_conv2_conv1(dev, H, W, C, c0, N):
     """d8s_conv2_conv1 (conv2 of a layer, then conv1 of the next on its output, one launch): the new
