@@ -35,6 +35,7 @@
 #include "d8s_host.h"
 
 #define DEV __device__ __forceinline__
+#define INLINE_H __attribute__((always_inline))
 
 namespace {
 
@@ -97,8 +98,9 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 // (float32 operands and sums).  Lane l of a wave supplies A[l % 32][k + l / 32] and B[k + l / 32][l % 32]
 // and holds C[8 (v / 4) + 4 (l / 32) + v % 4][l % 32] in accumulator v.  K runs in chunks of KC staged
 // through LDS: A rows as they are (the prologue applied on the way: slot embedding or LayerNorm),
-// the weights transposed to [k][n] with one column per lane.
-template <int PRO, int EPI>
+// the weights transposed to [k][n] with one column per lane.  VEC: K % 4 == 0 and the weights 16-byte
+// aligned (each lane's four k of a column in one 16-byte load).
+template <int PRO, int EPI, bool VEC>
 __global__ void __launch_bounds__(NT) k_head_gemm(GemmP p) {
     __shared__ float sA[TM][KC + 1];
     __shared__ float sB[KC][TN + 32];          // rows 32 banks apart: the two half-waves' k rows
@@ -110,20 +112,40 @@ __global__ void __launch_bounds__(NT) k_head_gemm(GemmP p) {
     if constexpr (PRO == PRO_LN) {
         // mean and 1/std of the tile's rows (biased variance, as torch's layer_norm), in two passes
         // over the row: the mean, then the mean square deviation; 4 lanes per row
+        // (lane l4 of a row takes its quads l4, l4 + 4, ..., LQ of them per round, all loaded before
+        // the first is added; K % 4 == 0 for these products; rows past M read row M - 1, unused)
         const int rr = tid >> 2, l4 = tid & 3;
         const int r = r0 + rr;
+        const float4* row4 = (const float4*)(p.A + (int64_t)min(r, p.M - 1) * p.K);
+        const int nq = p.K >> 2;
+        constexpr int LQ = 8;
         float s = 0.0f;
-        if (r < p.M)
-            for (int k = l4; k < p.K; k += 4) s += p.A[(int64_t)r * p.K + k];
+        for (int q0 = l4; q0 < nq; q0 += 4 * LQ) {
+            float4 x[LQ];
+#pragma unroll
+            for (int i = 0; i < LQ; ++i) x[i] = row4[min(q0 + 4 * i, nq - 1)];
+#pragma unroll
+            for (int i = 0; i < LQ; ++i)
+                if (q0 + 4 * i < nq) s += x[i].x + x[i].y + x[i].z + x[i].w;
+        }
         s += __shfl_xor(s, 2, 4);
         s += __shfl_xor(s, 1, 4);
         const float mean = s / (float)p.K;
         float ss = 0.0f;
-        if (r < p.M)
-            for (int k = l4; k < p.K; k += 4) {
-                const float x = p.A[(int64_t)r * p.K + k] - mean;
-                ss = __builtin_fmaf(x, x, ss);
-            }
+        for (int q0 = l4; q0 < nq; q0 += 4 * LQ) {
+            float4 x[LQ];
+#pragma unroll
+            for (int i = 0; i < LQ; ++i) x[i] = row4[min(q0 + 4 * i, nq - 1)];
+#pragma unroll
+            for (int i = 0; i < LQ; ++i)
+                if (q0 + 4 * i < nq) {
+                    const float a = x[i].x - mean, b = x[i].y - mean, c = x[i].z - mean, d = x[i].w - mean;
+                    ss = __builtin_fmaf(a, a, ss);
+                    ss = __builtin_fmaf(b, b, ss);
+                    ss = __builtin_fmaf(c, c, ss);
+                    ss = __builtin_fmaf(d, d, ss);
+                }
+        }
         ss += __shfl_xor(ss, 2, 4);
         ss += __shfl_xor(ss, 1, 4);
         if (l4 == 0) {
@@ -136,19 +158,26 @@ __global__ void __launch_bounds__(NT) k_head_gemm(GemmP p) {
     // addresses (and their slot embedding rows) are fixed for the whole K loop
     constexpr int AR = TM * KC / NT;
     static_assert(TM * KC % NT == 0 && NT % KC == 0 && TM == 64 && TN == 64, "staging");
+    // Every load of the K loop is unconditional, from an address clamped into its table (rows past M
+    // read row M - 1, columns past the split's end its last column, an absent slot row 0), and the
+    // value is zeroed afterwards by an integer mask (a select of a loaded value is turned back into a
+    // branch around the load, and a load under a branch waits for every load in flight before it).
     const int akk = tid % KC, ar0 = tid / KC;
     const float* arow[AR];
     const float* srow[AR];
+    uint32_t rmask = 0u, smask = 0u;                 // bit j: row j is inside M / has a slot row
 #pragma unroll
     for (int j = 0; j < AR; ++j) {
         const int r = r0 + ar0 + (NT / KC) * j;
-        arow[j] = r < p.M ? p.A + (int64_t)r * p.K : nullptr;
+        if (r < p.M) rmask |= 1u << j;
+        arow[j] = p.A + (int64_t)min(r, p.M - 1) * p.K;
         srow[j] = nullptr;
-        if constexpr (PRO == PRO_SLOT)
-            if (r < p.M) {
-                const int sl = p.slot_of[r % p.W];
-                if ((unsigned)sl < (unsigned)p.S) srow[j] = p.slot_emb + (int64_t)sl * p.K;
-            }
+        if constexpr (PRO == PRO_SLOT) {
+            const int sl = r < p.M ? p.slot_of[r % p.W] : -1;
+            const bool has = (unsigned)sl < (unsigned)p.S;
+            if (has) smask |= 1u << j;
+            srow[j] = p.slot_emb + (int64_t)(has ? sl : 0) * p.K;
+        }
     }
     // split K: block z of gridDim.z takes chunks [z kc_per, (z + 1) kc_per)
     int kbeg = 0, kend = p.K;
@@ -156,7 +185,6 @@ __global__ void __launch_bounds__(NT) k_head_gemm(GemmP p) {
         kbeg = blockIdx.z * p.kc_per * KC;
         kend = min(p.K, kbeg + p.kc_per * KC);
     }
-    const bool vec = (p.K & 3) == 0 && ((uintptr_t)p.Bw & 15) == 0;
     const int bn = tid % TN, n = n0 + bn, bq = tid / TN;       // weights: column bn, k quads bq + 4 u
     constexpr int BQ = KC / 16;                                  // quads per thread and chunk
     f32x16 acc;
@@ -164,54 +192,77 @@ __global__ void __launch_bounds__(NT) k_head_gemm(GemmP p) {
     for (int v = 0; v < 16; ++v) acc[v] = 0.0f;
     // chunk k0's values are fetched into registers (ra, rb) one chunk ahead: their loads are in flight
     // while the previous chunk's MFMAs run
-    float ra[AR];
+    float ra[AR], rs[PRO == PRO_SLOT ? AR : 1];
     float4 rb[BQ];
+    float rlw = 0.0f, rlb = 0.0f;                    // PRO_LN: the column's ln_w, ln_b
+    const float* bcol = p.Bw + (int64_t)min(n, p.N - 1) * p.K;
+    const bool nin = n < p.N;
+    auto keep = [](float x, bool on) INLINE_H {
+        uint32_t m = on ? ~0u : 0u;
+        asm volatile("" : "+v"(m));                  // (opaque: the AND is not turned into a select)
+        return __uint_as_float(__float_as_uint(x) & m);
+    };
+    // the raw values of chunk k0 (in flight during the previous chunk's MFMAs)
     auto fetch = [&](int k0) {
-        const int k = k0 + akk;
+        const int kc = min(k0 + akk, kend - 1);
+        if constexpr (PRO == PRO_LN) {
+            rlw = p.ln_w[kc];
+            rlb = p.ln_b[kc];
+        }
 #pragma unroll
         for (int j = 0; j < AR; ++j) {
-            float v = 0.0f;
-            if (arow[j] != nullptr && k < kend) {
-                v = arow[j][k];
-                if constexpr (PRO == PRO_SLOT)
-                    if (srow[j] != nullptr) v += srow[j][k];
-            }
-            ra[j] = v;
+            ra[j] = arow[j][kc];
+            if constexpr (PRO == PRO_SLOT) rs[j] = srow[j][kc];
         }
 #pragma unroll
         for (int u = 0; u < BQ; ++u) {
             const int kq = k0 + 4 * (bq + 4 * u);
-            float4 w = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-            if (vec) {
-                if (n < p.N && kq < kend) w = *(const float4*)(p.Bw + (int64_t)n * p.K + kq);
-            } else if (n < p.N) {
-                const float* src = p.Bw + (int64_t)n * p.K;
-                w.x = kq + 0 < kend ? src[kq + 0] : 0.0f;
-                w.y = kq + 1 < kend ? src[kq + 1] : 0.0f;
-                w.z = kq + 2 < kend ? src[kq + 2] : 0.0f;
-                w.w = kq + 3 < kend ? src[kq + 3] : 0.0f;
+            if constexpr (VEC) {
+                // K % 4 == 0, so kend (a multiple of KC, or K) is too: kend - 4 starts a whole quad
+                rb[u] = *(const float4*)(bcol + min(kq, kend - 4));
+            } else {
+                rb[u] = make_float4(bcol[min(kq + 0, kend - 1)], bcol[min(kq + 1, kend - 1)],
+                                    bcol[min(kq + 2, kend - 1)], bcol[min(kq + 3, kend - 1)]);
             }
-            rb[u] = w;
         }
     };
     fetch(kbeg);
     for (int k0 = kbeg; k0 < kend; k0 += KC) {
+        // stage chunk k0: the values outside the matrix or the split zeroed, the prologue applied
         const int k = k0 + akk;
+        const bool kin = k < kend;
 #pragma unroll
         for (int j = 0; j < AR; ++j) {
             const int rr = ar0 + (NT / KC) * j;
+            const bool on = kin && ((rmask >> j) & 1u);
             float v = ra[j];
-            if constexpr (PRO == PRO_LN)
-                if (arow[j] != nullptr && k < kend) v = (v - sMean[rr]) * sRstd[rr] * p.ln_w[k] + p.ln_b[k];
+            if constexpr (PRO == PRO_SLOT) {
+                const float vs = v + rs[j];
+                v = ((smask >> j) & 1u) ? vs : v;
+            }
+            v = keep(v, on);
+            if constexpr (PRO == PRO_LN) {
+                const float y = (v - sMean[rr]) * sRstd[rr] * rlw + rlb;
+                v = on ? y : v;
+            }
             sA[rr][akk] = v;
         }
 #pragma unroll
         for (int u = 0; u < BQ; ++u) {
             const int q = bq + 4 * u;
-            sB[4 * q + 0][bn] = rb[u].x;
-            sB[4 * q + 1][bn] = rb[u].y;
-            sB[4 * q + 2][bn] = rb[u].z;
-            sB[4 * q + 3][bn] = rb[u].w;
+            const int kq = k0 + 4 * q;
+            float4 w = rb[u];
+            if constexpr (VEC) {
+                const bool on = nin && kq < kend;
+                w = make_float4(keep(w.x, on), keep(w.y, on), keep(w.z, on), keep(w.w, on));
+            } else {
+                w = make_float4(keep(w.x, nin && kq + 0 < kend), keep(w.y, nin && kq + 1 < kend),
+                                keep(w.z, nin && kq + 2 < kend), keep(w.w, nin && kq + 3 < kend));
+            }
+            sB[4 * q + 0][bn] = w.x;
+            sB[4 * q + 1][bn] = w.y;
+            sB[4 * q + 2][bn] = w.z;
+            sB[4 * q + 3][bn] = w.w;
         }
         __syncthreads();
         if (k0 + KC < kend) fetch(k0 + KC);
@@ -233,14 +284,24 @@ __global__ void __launch_bounds__(NT) k_head_gemm(GemmP p) {
         }
         return;
     }
+    // the epilogues' loads, too, are issued together from clamped addresses before any is used
+    const int nc = min(n_out, p.N - 1);
+    const float bias_n = p.bias[nc];
     if constexpr (EPI != EPI_DOTS) {
+        float ex[16];
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+            const int rc = min(r0 + 32 * wr + 8 * (v >> 2) + 4 * h + (v & 3), p.M - 1);
+            ex[v] = 0.0f;
+            if constexpr (EPI == EPI_BIAS_POS) ex[v] = p.pos[(int64_t)((rc % p.W) % p.per) * p.N + nc];
+            if constexpr (EPI == EPI_BIAS_RES) ex[v] = p.R[(int64_t)rc * p.N + nc];
+        }
 #pragma unroll
         for (int v = 0; v < 16; ++v) {
             const int r = r0 + 32 * wr + 8 * (v >> 2) + 4 * h + (v & 3);
             if (r >= p.M || n_out >= p.N) continue;
-            float x = acc[v] + p.bias[n_out];
-            if constexpr (EPI == EPI_BIAS_POS) x += p.pos[(int64_t)((r % p.W) % p.per) * p.N + n_out];
-            if constexpr (EPI == EPI_BIAS_RES) x += p.R[(int64_t)r * p.N + n_out];
+            float x = acc[v] + bias_n;
+            if constexpr (EPI == EPI_BIAS_POS || EPI == EPI_BIAS_RES) x += ex[v];
             if constexpr (EPI == EPI_BIAS_RELU) x = fmaxf(x, 0.0f);
             p.C[(int64_t)r * p.ldc + n_out] = x;
         }
@@ -250,21 +311,42 @@ __global__ void __launch_bounds__(NT) k_head_gemm(GemmP p) {
         // row's dots are summed over the 4 lanes
         __shared__ float sF[TM][TN + 1];
         __shared__ float sW[2 * TMAX][TN];
+        // z and the slot indices of the lane's 16 rows, then their slot embedding rows (row 0 for
+        // an absent slot, unused), then f2 = ((acc + b) + z) + (slot embedding or +0)
+        int slv[16];
+        float zv[16], sev[16];
+        uint32_t hasm = 0u;
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+            const int rc = min(r0 + 32 * wr + 8 * (v >> 2) + 4 * h + (v & 3), p.M - 1);
+            slv[v] = p.slot_of[rc % p.W];
+            zv[v] = p.z[(int64_t)rc * p.N + nc];
+        }
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+            const bool has = (unsigned)slv[v] < (unsigned)p.S;
+            if (has) hasm |= 1u << v;
+            sev[v] = p.slot_emb[(int64_t)(has ? slv[v] : 0) * p.N + nc];
+        }
 #pragma unroll
         for (int v = 0; v < 16; ++v) {
             const int i = 32 * wr + 8 * (v >> 2) + 4 * h + (v & 3), r = r0 + i;
-            float x = 0.0f;
-            if (r < p.M && n_out < p.N) {
-                const int sl = p.slot_of[r % p.W];
-                x = acc[v] + p.bias[n_out] + p.z[(int64_t)r * p.N + n_out] +
-                    ((unsigned)sl < (unsigned)p.S ? p.slot_emb[(int64_t)sl * p.N + n_out] : 0.0f);
-            }
-            sF[i][32 * wc + l32] = x;
+            const float x = acc[v] + bias_n + zv[v] + keep(sev[v], (hasm >> v) & 1u);
+            sF[i][32 * wc + l32] = keep(x, r < p.M && n_out < p.N);
         }
-        for (int i = tid; i < 2 * p.T * TN; i += NT) {
-            const int q = i / TN, c = i % TN, nn = n0 + c;
+        // the attention and classifier weights of these columns (rows T of tw, then T of cw)
+        constexpr int WI = 2 * TMAX * TN / NT;
+        float wv[WI];
+#pragma unroll
+        for (int u = 0; u < WI; ++u) {
+            const int i = tid + u * NT, q = min(i / TN, 2 * p.T - 1), c = i % TN;
             const float* src = q < p.T ? p.tw + (int64_t)q * p.N : p.cw + (int64_t)(q - p.T) * p.N;
-            sW[q][c] = nn < p.N ? src[nn] : 0.0f;
+            wv[u] = src[min(n0 + c, p.N - 1)];
+        }
+#pragma unroll
+        for (int u = 0; u < WI; ++u) {
+            const int i = tid + u * NT, q = i / TN, c = i % TN;
+            if (i < 2 * p.T * TN) sW[q][c] = keep(wv[u], n0 + c < p.N);
         }
         __syncthreads();
         const int rr = tid >> 2, c0 = 16 * (tid & 3), r = r0 + rr;
@@ -525,6 +607,9 @@ Ws carve(const D8sHeadArgs* a, char* base) {
     return w;
 }
 
+// whether a product's weights can be read as 16-byte quads along K
+bool gemm_vec(const GemmP& g) { return (g.K & 3) == 0 && ((uintptr_t)g.Bw & 15) == 0; }
+
 // one context-layer product, split over K when its tiles alone are too few for the chip
 template <int PRO, int EPI>
 void launch_gemm(GemmP g, float* cs, hipStream_t st) {
@@ -533,7 +618,10 @@ void launch_gemm(GemmP g, float* cs, hipStream_t st) {
     const dim3 grid((g.M + TM - 1) / TM, (g.N + TN - 1) / TN, sp.splits);
     g.kc_per = sp.kc_per;
     g.Cs = cs;
-    k_head_gemm<PRO, EPI><<<grid, NT, 0, st>>>(g);
+    if (gemm_vec(g))
+        k_head_gemm<PRO, EPI, true><<<grid, NT, 0, st>>>(g);
+    else
+        k_head_gemm<PRO, EPI, false><<<grid, NT, 0, st>>>(g);
     if (sp.splits > 1) {
         const int64_t n = (int64_t)g.M * g.N;
         k_head_splitk<EPI><<<(unsigned)((n + NT - 1) / NT), NT, 0, st>>>(g, sp.splits);
@@ -618,7 +706,10 @@ void head_run(const D8sHeadArgs* a, char* ws, hipStream_t st) {
     g.M = M; g.W = a->W; g.S = a->S; g.slot_of = a->slot_of; g.slot_emb = a->slot_emb;
     g.N = a->D; g.z = a->z; g.tw = a->attn_w; g.cw = a->cls_w; g.part = w.part; g.T = a->T;
     g.A = w.h2; g.Bw = a->ctx_out_w; g.bias = a->ctx_out_b; g.K = a->CD;
-    k_head_gemm<PRO_NONE, EPI_DOTS><<<dim3((M + TM - 1) / TM, nblk), NT, 0, st>>>(g);
+    if (gemm_vec(g))
+        k_head_gemm<PRO_NONE, EPI_DOTS, true><<<dim3((M + TM - 1) / TM, nblk), NT, 0, st>>>(g);
+    else
+        k_head_gemm<PRO_NONE, EPI_DOTS, false><<<dim3((M + TM - 1) / TM, nblk), NT, 0, st>>>(g);
     // 8. pooling
     const int64_t nsum = (int64_t)M * 2 * a->T;
     k_head_dotsum<<<(unsigned)((nsum + NT - 1) / NT), NT, 0, st>>>(w.part, a->attn_b, w.sums, M, a->T, nblk);
