@@ -83,8 +83,20 @@ __global__ void __launch_bounds__(NT) k_head_splitk(GemmP p, int splits) {
     const int64_t i = (int64_t)blockIdx.x * NT + threadIdx.x;
     if (i >= (int64_t)p.M * p.N) return;
     const int r = (int)(i / p.N), n = (int)(i % p.N);
+    // eight splits' sums loaded before the first is added (indices past the last split read it
+    // again, unused), added in split order
+    const int64_t mn = (int64_t)p.M * p.N;
     float x = 0.0f;
-    for (int s = 0; s < splits; ++s) x += p.Cs[(int64_t)s * p.M * p.N + i];
+    for (int s0 = 0; s0 < splits; s0 += 8) {
+        float v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) v[u] = p.Cs[(int64_t)min(s0 + u, splits - 1) * mn + i];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const float xs = x + v[u];
+            x = s0 + u < splits ? xs : x;
+        }
+    }
     x += p.bias[n];
     if constexpr (EPI == EPI_BIAS_POS) x += p.pos[(int64_t)((r % p.W) % p.per) * p.N + n];
     if constexpr (EPI == EPI_BIAS_RES) x += p.R[(int64_t)r * p.N + n];
@@ -395,10 +407,25 @@ __global__ void __launch_bounds__(NT) k_head_attn(AttnP p) {
     const int b = blockIdx.x, h = blockIdx.y, q0 = blockIdx.z * AQ;
     const int ld = 3 * p.CD;
     const float* base = p.qkv + (int64_t)b * p.W * ld;
-    for (int i = threadIdx.x; i < p.W * (DH / 4); i += NT) {
-        const int w = i / (DH / 4), d4 = i % (DH / 4);
-        sK[w][d4] = *(const float4*)(base + (int64_t)w * ld + p.CD + h * DH + 4 * d4);
-        sV[w][d4] = *(const float4*)(base + (int64_t)w * ld + 2 * p.CD + h * DH + 4 * d4);
+    {
+        // the keys and values of the study, all loads issued before the first LDS store (items past
+        // W * 16 read the last one again and fill rows W .. WMAX - 1, which no score or output reads)
+        constexpr int KV = WMAX * (DH / 4) / NT;
+        float4 kv[2 * KV];
+        const int n = p.W * (DH / 4);
+#pragma unroll
+        for (int u = 0; u < KV; ++u) {
+            const int i = min((int)threadIdx.x + u * NT, n - 1), w = i / (DH / 4), d4 = i % (DH / 4);
+            kv[2 * u] = *(const float4*)(base + (int64_t)w * ld + p.CD + h * DH + 4 * d4);
+            kv[2 * u + 1] = *(const float4*)(base + (int64_t)w * ld + 2 * p.CD + h * DH + 4 * d4);
+        }
+        static_assert(KV * NT == WMAX * (DH / 4), "one item per row and quad of sK / sV");
+#pragma unroll
+        for (int u = 0; u < KV; ++u) {
+            const int i = (int)threadIdx.x + u * NT, w = i / (DH / 4), d4 = i % (DH / 4);
+            sK[w][d4] = kv[2 * u];
+            sV[w][d4] = kv[2 * u + 1];
+        }
     }
     if (threadIdx.x == 0) sAny = 0;
     __syncthreads();
@@ -410,11 +437,12 @@ __global__ void __launch_bounds__(NT) k_head_attn(AttnP p) {
     const float scale = 1.0f / sqrtf((float)DH);
     const int ql = threadIdx.x / LQ, l = threadIdx.x % LQ, qi = q0 + ql;
     const bool act = qi < p.W;
+    // (a query past W reads the last one: its scores and output are computed and not stored)
+    const int qc = min(qi, p.W - 1);
     float4 q[DH / 4];
 #pragma unroll
     for (int d4 = 0; d4 < DH / 4; ++d4) {
-        float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        if (act) v = *(const float4*)(base + (int64_t)qi * ld + h * DH + 4 * d4);
+        const float4 v = *(const float4*)(base + (int64_t)qc * ld + h * DH + 4 * d4);
         q[d4] = make_float4(v.x * scale, v.y * scale, v.z * scale, v.w * scale);
     }
     float sc[KPL];
@@ -501,13 +529,23 @@ struct PoolP {
 __global__ void __launch_bounds__(NT) k_head_pool(PoolP p) {
     __shared__ float sA[WMAX][TMAX], sS[WMAX][TMAX];
     const int b = blockIdx.x;
-    for (int i = threadIdx.x; i < p.W * 2 * p.T; i += NT) {
-        const int w = i / (2 * p.T), q = i % (2 * p.T);
-        const float v = p.sums[(int64_t)b * p.W * 2 * p.T + i];
-        if (q < p.T)
-            sA[w][q] = v;
-        else
-            sS[w][q - p.T] = v;
+    {
+        // all of the study's sums loaded before the first LDS store (past W * 2T: the last, unused)
+        constexpr int PN = WMAX * 2 * TMAX / NT;
+        const int n = p.W * 2 * p.T;
+        float v[PN];
+#pragma unroll
+        for (int u = 0; u < PN; ++u) v[u] = p.sums[(int64_t)b * n + min((int)threadIdx.x + u * NT, n - 1)];
+#pragma unroll
+        for (int u = 0; u < PN; ++u) {
+            const int i = (int)threadIdx.x + u * NT, w = i / (2 * p.T), q = i % (2 * p.T);
+            if (i < n) {
+                if (q < p.T)
+                    sA[w][q] = v[u];
+                else
+                    sS[w][q - p.T] = v[u];
+            }
+        }
     }
     __shared__ uint8_t sV[WMAX];
     __shared__ int sAny;
