@@ -560,37 +560,62 @@ __global__ void __launch_bounds__(NT) k_prep_hist(PArgs a) {
     auto count = [&](int kk, int dy, int dx0, const float* v) {
         if constexpr (STORE)
             *(float4*)(st.sc + ((int64_t)kk * a.img + dy) * a.img + dx0) = make_float4(v[0], v[1], v[2], v[3]);
+        // The UP values of a unit are counted in one step when every counted one continues the
+        // thread's run (the common case: no branch taken); otherwise value by value.
         if constexpr (LEVEL == 1) {
             // a thread's values are neighbours (UP along x, then the next row of its column), so they
             // mostly share a (coarse) level-1 bin: the thread counts a run in a register and adds it
             // to LDS when the bin changes
+            uint32_t b[UP];
+            bool same = true;
 #pragma unroll
             for (int i = 0; i < UP; ++i) {
                 nan |= v[i] != v[i];
-                const uint32_t b = order_key(v[i]) >> 21;
-                if (b != run_bin) {
+                b[i] = order_key(v[i]) >> 21;
+                same &= b[i] == run_bin;
+            }
+            if (same) {
+                run_n += UP;
+                return;
+            }
+#pragma unroll
+            for (int i = 0; i < UP; ++i) {
+                if (b[i] != run_bin) {
                     if (run_n) run_flush();
-                    run_bin = b;
+                    run_bin = b[i];
                     run_n = 0u;
                 }
                 ++run_n;
             }
             return;
         }
+        // the keys under one of the slots' prefixes (unused slots hold 0xffffffff, which no key has at
+        // these levels), counted in runs as at level 1 (runs of equal values, e.g. a zero background,
+        // are common); index = slot * NB + bin, slots from NH on count in memory
+        uint32_t idx[UP];
+        bool ok[UP], same = true;
+        uint32_t add = 0u;
 #pragma unroll
         for (int i = 0; i < UP; ++i) {
-            // the keys under one of the slots' prefixes (unused slots hold 0xffffffff, which no key
-            // has at these levels), counted in runs as at level 1 (runs of equal values, e.g. a zero
-            // background, are common); index = slot * NB + bin, slots from NH on count in memory
             const uint32_t k = order_key(v[i]);
             const uint32_t p = LEVEL == 2 ? k >> 21 : k >> 10;
             const uint32_t bin = LEVEL == 2 ? (k >> 10) & (NB2 - 1) : k & (NB3 - 1);
-            if (p == pre[0] || p == pre[1] || p == pre[2] || p == pre[3]) {
-                const uint32_t t = p == pre[0] ? 0u : p == pre[1] ? 1u : p == pre[2] ? 2u : 3u;
-                const uint32_t idx = t * NB + bin;
-                if (idx != run_bin) {
+            ok[i] = p == pre[0] || p == pre[1] || p == pre[2] || p == pre[3];
+            const uint32_t t = p == pre[0] ? 0u : p == pre[1] ? 1u : p == pre[2] ? 2u : 3u;
+            idx[i] = t * NB + bin;
+            same &= !ok[i] || idx[i] == run_bin;
+            add += ok[i] ? 1u : 0u;
+        }
+        if (same) {
+            run_n += add;
+            return;
+        }
+#pragma unroll
+        for (int i = 0; i < UP; ++i) {
+            if (ok[i]) {
+                if (idx[i] != run_bin) {
                     if (run_n) run_flush();
-                    run_bin = idx;
+                    run_bin = idx[i];
                     run_n = 0u;
                 }
                 ++run_n;
