@@ -883,10 +883,16 @@ __global__ __launch_bounds__(256, CcShape<W_>::OCC) void k_c21(D8sConv2Args c2, 
     const uint8_t* seg = (const uint8_t*)c1.seg;
     const int64_t in_gs = (int64_t)HW * 32, seg_gs = M * 32;
     // conv1 pixel offsets of a tile's pixel for this lane: in0 group 0 and store slot 0
+    // (the lane's pixel and half recomputed from an opaque copy of the thread index: kept across the
+    // tile loop they were spilled, and their reload at each tile's start waited for every load in
+    // flight)
     auto offs = [&](int t, uint32_t& oi, uint32_t& os) INLINE {
-        const int n = t / per_img, pi = (t - n * per_img) * 128 + p;
-        oi = (uint32_t)(((int64_t)n * G0 * HW + pi) * 32 + 16 * h);
-        os = (uint32_t)(((int64_t)n * HW + pi) * 32 + 16 * h);
+        int t0 = tid;
+        asm volatile("" : "+v"(t0));
+        const int lp = 32 * (t0 >> 6) + (t0 & 31), lh = 16 * ((t0 >> 5) & 1);
+        const int n = t / per_img, pi = (t - n * per_img) * 128 + lp;
+        oi = (uint32_t)(((int64_t)n * G0 * HW + pi) * 32 + lh);
+        os = (uint32_t)(((int64_t)n * HW + pi) * 32 + lh);
     };
     uint32_t ci, cs, ni, ns;
     offs(tile, ci, cs);
