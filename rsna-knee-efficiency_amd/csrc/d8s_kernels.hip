@@ -2064,7 +2064,10 @@ DEV void st_agent(uint32_t* p, uint32_t v) { __hip_atomic_store(p, v, __ATOMIC_R
 template <int PT>
 __global__ __launch_bounds__(DP_NT, 1) void k_dparts(D8sPartsArgs a) {
     static_assert(PT == 1 || PT == 2 || PT == 4 || PT == 8, "pixel tiles per band");
-    constexpr int CG = PT == 8 ? 4 : 8;                    // groups per prologue chunk
+    // groups per prologue chunk: 4 for 128- and 256-pixel bands (for 128: a 24-image study's 32 x 32
+    // block 0.76-0.77 against 0.79-0.82 ms with 8, 0.78-0.80 with 2), 8 for the narrower ones (a
+    // 32-pixel band needs 8 for one operand per wave; 16 was slower)
+    constexpr int CG = PT == 4 || PT == 8 ? 4 : 8;
     constexpr int ITEMS = CG * PT;                         // (group, pixel tile) operands per chunk
     constexpr int IPW = ITEMS / 8;                         // of them per wave
     constexpr int NPT = PT == 1 ? 1 : PT / 2;              // conv1 pixel tiles per wave
