@@ -3603,7 +3603,7 @@ extern "C" int d8s_dense_block_parts(const D8sPartsArgs* a, void* stream) {
     REQUIRE((int64_t)a->N * a->H * a->W * 32 < (1ll << 31), "d8s_dense_block_parts: store slot over 2 GiB");
     const size_t shm = (size_t)(R + 2) * (a->W + 2) * 128 + DB_PRM + (size_t)(a->G0 + a->L - 1) * 128;
     // static LDS of k_dparts<PT>: conv2 weights, two prologue chunks, partial sums, the ticket
-    const int PT = P / 32, CG = PT == 8 ? 4 : 8, S2 = PT == 8 ? 1 : (PT == 4 ? 2 : 4);
+    const int PT = P / 32, CG = PT == 4 || PT == 8 ? 4 : 8, S2 = PT == 8 ? 1 : (PT == 4 ? 2 : 4);
     const size_t nred = PT == 1 ? 4 * 1024 : (size_t)std::max(1, (S2 - 1) * PT * 1024);
     const size_t stat = 36864 + 2 * (size_t)CG * PT * 1024 + 4 * nred + 16;
     REQUIRE(shm + stat <= 160 * 1024, "d8s_dense_block_parts: band too large for LDS");
