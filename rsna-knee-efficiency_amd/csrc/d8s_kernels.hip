@@ -2038,16 +2038,23 @@ __global__ __launch_bounds__(DB_NT, 1) void k_dblock(D8sBlockArgs a0, D8sBlockAr
 //   conv2  split over the waves of a pixel tile by K step (36 = 4 planes x 9 taps), added through LDS,
 //          stored into the layer's slot.
 // conv1 is pixel-local: a band's next layer reads only its own pixels, so the halo rows are the only
-// data that crosses workgroups.  The exchange pairs are written and read with relaxed agent-scope
+// data that crosses workgroups, and only conv2 waits for them.  A layer's conv1 over every group but
+// the newest (the previous layer's conv2 output) runs before that conv2, while the previous layer's
+// rows are on their way between the bands: pass i is conv1 of layer i over its older groups, then the
+// neighbours' rows of layer i - 1 and its conv2, whose output bytes (the newest group of layer i, this
+// band's own pixels) go through layer i's prologue straight into LDS, then that group's MFMAs and
+// layer i's epilogue and rows out.  The exchange pairs are written and read with relaxed agent-scope
 // atomics (performed at the device's coherence point, visible across the XCDs' L2s); a 64-bit pair is
-// written in one access, so a current tag comes with its value.  Workgroups take their (image, band)
-// from a ticket counter in the order they start, so a band only ever waits for bands whose tickets are
-// adjacent to its own, taken by workgroups already running or next to start: the waits cannot form a
-// cycle whatever the dispatch order, and every wait is bounded (a wait that runs out counts in
-// sync[2] and the kernel carries on, so every workgroup reaches its end).  The last workgroup to end
-// resets the ticket and the end count and advances the launch count (sync[3]) the tags are made of,
-// so the next launch needs no clearing.  While conv2 runs, the next layer's tables, first weights and
-// first chunk's store bytes are requested.
+// written in one access, so a current tag comes with its value.  A band sends layer i's rows only
+// after it has read its neighbours' rows of layer i - 1, which they sent after reading its rows of
+// layer i - 2: two buffers (by layer parity) are never overwritten before they are read.  Workgroups
+// take their (image, band) from a ticket counter in the order they start, so a band only ever waits
+// for bands whose tickets are adjacent to its own, taken by workgroups already running or next to
+// start: the waits cannot form a cycle whatever the dispatch order, and every wait is bounded (a wait
+// that runs out counts in sync[2] and the kernel carries on, so every workgroup reaches its end).  The
+// last workgroup to end resets the ticket and the end count and advances the launch count (sync[3])
+// the tags are made of, so the next launch needs no clearing.  Tables, weights and the next pass's
+// first chunk of store bytes are requested a phase ahead of their use.
 // ------------------------------------------------------------------------------------------------
 static constexpr int DP_NT = 512;
 static constexpr int DP_SPIN = 1 << 20;                   // polls before a wait gives up
@@ -2132,193 +2139,184 @@ __global__ __launch_bounds__(DP_NT, 1) void k_dparts(D8sPartsArgs a) {
     // a wave's conv1 groups: q -> g = q (PT >= 2) or 2 q + hv (32-pixel bands)
 #define DP_G(q) (KH == 1 ? (q) : 2 * (q) + hv)
 
-    // prefetched state of the next layer: tables, first weights, first chunk's store bytes
+    // prefetched state: conv1 tables of the next conv1 pass (t_abh, t_w1sum, t_gd), conv2 tables of the
+    // next conv2 (t_w2, t_sc, t_w2sum), the weights of a layer's newest group (t_wn)
     u32x4 t_w2[5];
     uint32_t t_abh[4];
     int32_t t_w1sum = 0, t_w2sum = 0;
     float2 t_gd = {0.f, 0.f};
     float t_sc = 0.f;
+    u32x4 t_wn = {0u, 0u, 0u, 0u};
     u32x4 rw[DW], ra[IPW];
-#define DP_TABLES(lp_, G_)                                                                        \
+#define DP_TAB1(lp_, G_)                                                                          \
+    do {                                                                                          \
+        const int ti_ = min(tid, 127);                                                            \
+        t_w1sum = ldg_i32((lp_).w1sum + ti_);                                                     \
+        t_gd = ldg_f2((const float2*)(lp_).gd + ti_);                                             \
+        _Pragma("unroll") for (int k_ = 0; k_ < 4; ++k_)                                          \
+            t_abh[k_] = ldg_u32((const uint32_t*)(lp_).abh + min(tid + DP_NT * k_, (G_) * 32 - 1)); \
+    } while (0)
+#define DP_TAB2(lp_)                                                                              \
     do {                                                                                          \
         _Pragma("unroll") for (int k_ = 0; k_ < 5; ++k_)                                          \
             t_w2[k_] = ldg_u32x4((const u32x4*)(lp_).w2 + min(tid + DP_NT * k_, 2303));          \
-        const int ti_ = min(tid, 127), ts_ = min(max(tid - 128, 0), 31);                           \
-        t_w1sum = ldg_i32((lp_).w1sum + ti_);                                                     \
-        t_gd = ldg_f2((const float2*)(lp_).gd + ti_);                                             \
+        const int ts_ = min(max(tid - 128, 0), 31);                                               \
         t_sc = ldg_f((lp_).sc + ts_);                                                             \
         t_w2sum = ldg_i32((lp_).w2sum + ts_);                                                     \
-        _Pragma("unroll") for (int k_ = 0; k_ < 4; ++k_)                                          \
-            t_abh[k_] = ldg_u32((const uint32_t*)(lp_).abh + min(tid + DP_NT * k_, (G_) * 32 - 1)); \
     } while (0)
     // weights of output tile c of group g (the MFMA A operand: rows 32 c + j, bytes 16 h ..)
 #define DP_W(lp_, g) ldg_u32x4((const uint8_t*)(lp_).w1 + ((int64_t)(g) * 128 + 32 * c + j) * 32 + 16 * h)
 #define DP_RW(lp_, G_)                                                                            \
     _Pragma("unroll") for (int q_ = 0; q_ < DW; ++q_) rw[q_] = DP_W(lp_, min(DP_G(q_), (G_) - 1))
     // store bytes of the items of chunk ch a wave prologues (item i = wave + 8 q: group i / PT, tile
-    // i % PT); `ready_` = groups that exist already (earlier layers')
+    // i % PT); `ready_` = groups that exist already
 #define DP_RA(ch_, G_, ready_)                                                                    \
     _Pragma("unroll") for (int q_ = 0; q_ < IPW; ++q_) {                                          \
         const int i_ = wave + 8 * q_, g_ = min((ch_) * CG + i_ / PT, (ready_) - 1);                \
         ra[q_] = *(const u32x4*)DP_SRC(g_, i_ % PT);                                              \
     }
+#define DP_XCH_TAG(l_) ((uint64_t)(epoch * 64u + (uint32_t)(l_) + 1u) << 32)
 
     if (valid) {
         const D8sLayerP lp0 = a.layers[0];
-        DP_TABLES(lp0, G0);
+        DP_TAB1(lp0, G0);
+        DP_TAB2(lp0);
         DP_RA(0, G0, G0);
     }
-    for (int l = 0; l < (valid ? L : 0); ++l) {
-        const D8sLayerP lp = a.layers[l];
-        const int G = G0 + l;
-        const int nch = (G + CG - 1) / CG;
-        // ---- the layer's tables into LDS (fetched during the previous layer's conv2) ----
+    // Pass i: (A) conv1 of layer i over the groups that exist before layer i - 1's conv2 (all but the
+    // newest), (B) layer i - 1's halo rows and its conv2, whose output (the newest group) goes
+    // through layer i's prologue straight into LDS, (C) that group's MFMAs, layer i's epilogue into
+    // the window and its first / last rows out to the neighbours.  The neighbours' rows of layer i are
+    // waited for only in pass i + 1, after its conv1: the exchange runs beside that conv1.
+    i32x16 acc[NPT];
+    for (int i = 0; i <= (valid ? L : -1); ++i) {
+        // ==== (A) conv1 of layer i over its groups 0 .. G - 1 ====
+        if (i < L) {
+            const D8sLayerP lp = a.layers[i];
+            const int G = i == 0 ? G0 : G0 + i - 1;
+            const int nch = (G + CG - 1) / CG;
+            if (i > 0) __syncthreads();                    // layer i - 1's epilogue has read its tables
+            if (i == 0) {
 #pragma unroll
-        for (int k = 0; k < 5; ++k)
-            if (tid + DP_NT * k < 2304) s_w[swz((tid + DP_NT * k) >> 1, tid & 1)] = t_w2[k];
-        if (tid < 128) {
-            s_w1sum[tid] = t_w1sum;
-            s_gd[tid] = t_gd;
-        } else if (tid < 160) {
-            s_sc[tid - 128] = t_sc;
-            s_w2sum[tid - 128] = t_w2sum;
-        }
-#pragma unroll
-        for (int k = 0; k < 4; ++k)
-            if (tid + DP_NT * k < G * 32) s_abh[tid + DP_NT * k] = t_abh[k];
-        // the previous layer's group, if it is in chunk 0, was not ready when chunk 0 was requested
-        if (l > 0 && G - 1 < CG) {
-#pragma unroll
-            for (int q_ = 0; q_ < IPW; ++q_) {
-                const int i_ = wave + 8 * q_;
-                if (i_ / PT == G - 1) ra[q_] = *(const u32x4*)DP_SRC(G - 1, i_ % PT);
+                for (int k = 0; k < 5; ++k)
+                    if (tid + DP_NT * k < 2304) s_w[swz((tid + DP_NT * k) >> 1, tid & 1)] = t_w2[k];
+                if (tid >= 128 && tid < 160) {
+                    s_sc[tid - 128] = t_sc;
+                    s_w2sum[tid - 128] = t_w2sum;
+                }
             }
-        }
-        __syncthreads();                                   // tables in LDS
+            if (tid < 128) {
+                s_w1sum[tid] = t_w1sum;
+                s_gd[tid] = t_gd;
+            }
+#pragma unroll
+            for (int k = 0; k < 4; ++k)
+                if (tid + DP_NT * k < (G0 + i) * 32) s_abh[tid + DP_NT * k] = t_abh[k];
+            // group G - 1 (layer i - 2's output), if it is in chunk 0, was not ready when chunk 0 was
+            // requested
+            if (i > 1 && G - 1 < CG) {
+#pragma unroll
+                for (int q_ = 0; q_ < IPW; ++q_) {
+                    const int i_ = wave + 8 * q_;
+                    if (i_ / PT == G - 1) ra[q_] = *(const u32x4*)DP_SRC(G - 1, i_ % PT);
+                }
+            }
+            __syncthreads();                               // tables in LDS
 
-        // ---- prologue of chunk ch into LDS buffer ch & 1 ----
+            // ---- prologue of chunk ch into LDS buffer ch & 1 ----
 #define DP_PRO(ch_)                                                                               \
     _Pragma("unroll") for (int q_ = 0; q_ < IPW; ++q_) {                                          \
         const int i_ = wave + 8 * q_, g_ = min((ch_) * CG + i_ / PT, G - 1);                      \
         const u32x4* pp_ = (const u32x4*)(s_abh + g_ * 32 + h * 16);                              \
         s_pro[(((ch_) & 1) * ITEMS + i_) * 64 + lane] = pro16(ra[q_], pp_[0], pp_[1], pp_[2], pp_[3]); \
     }
-        DP_PRO(0);
-        // loads in the loop's order (activations two chunks ahead, then the weight ring), so the wait
-        // counts at the loop's head are the same from both of its entries: no wait for all loads
-        DP_RA(1, G, G);
-        DP_RW(lp, G);
-        __syncthreads();
-        i32x16 acc[NPT];
-        const int32_t m128 = hv == 0 || KH == 1 ? 128 : 0;      // one K half starts at 128 sum w
-#pragma unroll
-        for (int tt = 0; tt < NPT; ++tt) {
-#pragma unroll
-            for (int v = 0; v < 16; ++v) acc[tt][v] = m128 * s_w1sum[32 * c + res_row(v, h)];
-        }
-        for (int ch = 0; ch < nch; ++ch) {
-            // straight-line steps (no load under a branch: the wait counts stay exact and the
-            // prefetched loads stay in flight); a step past the last group multiplies zero weights.
-            // The next chunk's prologue items are spread between the steps, so their VALU work runs
-            // beside the MFMAs already issued (an item past the last chunk is never read).
-            const u32x4* bsrc = s_pro + (ch & 1) * ITEMS * 64 + lane;
-            constexpr int EVERY = QC / IPW;                // steps per prologue item
-#pragma unroll
-            for (int u = 0; u < QC; ++u) {
-                const int q = ch * QC + u, g = DP_G(q);
-                const uint32_t live = g < G ? ~0u : 0u;
-                const u32x4 wa = rw[u % DW] & u32x4{live, live, live, live};
-                rw[u % DW] = DP_W(lp, min(DP_G(q + DW), G - 1));
-                const int gi = (KH == 2 ? 2 * u + hv : u);
-#pragma unroll
-                for (int tt = 0; tt < NPT; ++tt) {
-                    const int t = KH == 2 ? 0 : hv * NPT + tt;
-                    acc[tt] = mfma_i8(wa, bsrc[(gi * PT + t) * 64], acc[tt]);
-                }
-                if ((u + 1) % EVERY == 0) {
-                    const int qi = (u + 1) / EVERY - 1;    // item wave + 8 qi of chunk ch + 1
-                    const int i_ = wave + 8 * qi, g_ = min((ch + 1) * CG + i_ / PT, G - 1);
-                    const u32x4* pp_ = (const u32x4*)(s_abh + g_ * 32 + h * 16);
-                    s_pro[(((ch + 1) & 1) * ITEMS + i_) * 64 + lane] =
-                        pro16(ra[qi], pp_[0], pp_[1], pp_[2], pp_[3]);
-                    const int g2 = min((ch + 2) * CG + i_ / PT, G - 1);
-                    ra[qi] = *(const u32x4*)DP_SRC(g2, i_ % PT);
-                }
-                __builtin_amdgcn_sched_barrier(0);
+            DP_PRO(0);
+            // the next layer's conv1 tables and this layer's newest-group weights (unconditional, a
+            // clamped layer: a load under a branch makes later waits wait for every load), then the
+            // loads in the loop's order (activations two chunks ahead, then the weight ring), so the
+            // wait counts at the loop's head are the same from both of its entries
+            {
+                const int ln_ = min(i + 1, L - 1);
+                const D8sLayerP ln = a.layers[ln_];
+                DP_TAB1(ln, G0 + ln_);
+                t_wn = DP_W(lp, G0 + i - 1);                 // (i = 0: group G0 - 1, unused)
             }
-            __syncthreads();                               // chunk ch read, chunk ch + 1 written
-        }
-        // 32-pixel bands: the two K halves of each output tile added through LDS
-        if constexpr (KH == 2) {
-            if (hv == 1) {
-                int32_t* r = s_red + c * 1024 + lane;
-#pragma unroll
-                for (int v = 0; v < 16; ++v) r[v * 64] = acc[0][v];
-            }
+            DP_RA(1, G, G);
+            DP_RW(lp, G);
             __syncthreads();
-            if (hv == 0) {
-                const int32_t* r = s_red + c * 1024 + lane;
-#pragma unroll
-                for (int v = 0; v < 16; ++v) acc[0][v] += r[v * 64];
-            }
-        }
-        // ---- bottleneck bytes (v ^ 0x80) into the window; the band's first / last row out ----
-        const int par = l & 1;
-        const uint64_t tag = (uint64_t)(epoch * 64u + (uint32_t)l + 1u) << 32;
-        if (KH == 1 || hv == 0) {
-            uint32_t e[4];
+            const int32_t m128 = hv == 0 || KH == 1 ? 128 : 0;      // one K half starts at 128 sum w
 #pragma unroll
             for (int tt = 0; tt < NPT; ++tt) {
-                const int t = KH == 2 ? 0 : hv * NPT + tt;
-                const int pl = 32 * t + j, yl = pl / W, x = pl - yl * W;
 #pragma unroll
-                for (int kk = 0; kk < 4; ++kk) {
-                    const float4* pg = (const float4*)(s_gd + 32 * c + 8 * kk + 4 * h);
-                    e[kk] = epi1_x80(acc[tt], kk, pg[0], pg[1]);
-                }
-                const u32x4 row = xchg_rows(e[0], e[1], e[2], e[3], h);
-                s_b[c * WIN * 2 + swz((yl + 1) * BW + x + 1, h)] = row;
-                if (yl == 0 && part > 0) {
-                    uint64_t* xp = DP_XP(ticket, par, 0, c) + x * 8 + 4 * h;
-#pragma unroll
-                    for (int e4 = 0; e4 < 4; ++e4) st_agent64(xp + e4, tag | row[e4]);
-                }
-                if (yl == R - 1 && part < K - 1) {
-                    uint64_t* xp = DP_XP(ticket, par, 1, c) + x * 8 + 4 * h;
-#pragma unroll
-                    for (int e4 = 0; e4 < 4; ++e4) st_agent64(xp + e4, tag | row[e4]);
-                }
-                __builtin_amdgcn_sched_barrier(0);
+                for (int v = 0; v < 16; ++v) acc[tt][v] = m128 * s_w1sum[32 * c + res_row(v, h)];
             }
-        }
-        // ---- the neighbours' rows into the halo rows (window row 0 = the band above's last row,
-        // row R + 1 = the band below's first row), polling each pair until its tag is current ----
-        for (int idx = tid; idx < 2 * 4 * W * 2; idx += DP_NT) {
-            const int hh = idx & 1, xx = (idx >> 1) % W, cc = ((idx >> 1) / W) & 3, below = idx / (8 * W);
-            if (below ? part < K - 1 : part > 0) {
-                const uint64_t* xp = DP_XP(below ? ticket + 1 : ticket - 1, par, below ? 0 : 1, cc) + xx * 8 + 4 * hh;
-                uint64_t v0 = 0, v1 = 0, v2 = 0, v3 = 0;
-                bool ok = false;
-                for (int it = 0; it < DP_SPIN && !broken; ++it) {
-                    v0 = ld_agent64(xp); v1 = ld_agent64(xp + 1); v2 = ld_agent64(xp + 2); v3 = ld_agent64(xp + 3);
-                    if (((v0 & v1 & v2 & v3) >> 32) == (tag >> 32) && ((v0 | v1 | v2 | v3) >> 32) == (tag >> 32)) {
-                        ok = true;
-                        break;
+            for (int ch = 0; ch < nch; ++ch) {
+                // straight-line steps (no load under a branch: the wait counts stay exact and the
+                // prefetched loads stay in flight); a step past the last group multiplies zero weights.
+                // The next chunk's prologue items are spread between the steps, so their VALU work runs
+                // beside the MFMAs already issued (an item past the last chunk is never read).
+                const u32x4* bsrc = s_pro + (ch & 1) * ITEMS * 64 + lane;
+                constexpr int EVERY = QC / IPW;            // steps per prologue item
+#pragma unroll
+                for (int u = 0; u < QC; ++u) {
+                    const int q = ch * QC + u, g = DP_G(q);
+                    const uint32_t live = g < G ? ~0u : 0u;
+                    const u32x4 wa = rw[u % DW] & u32x4{live, live, live, live};
+                    rw[u % DW] = DP_W(lp, min(DP_G(q + DW), G - 1));
+                    const int gi = (KH == 2 ? 2 * u + hv : u);
+#pragma unroll
+                    for (int tt = 0; tt < NPT; ++tt) {
+                        const int t = KH == 2 ? 0 : hv * NPT + tt;
+                        acc[tt] = mfma_i8(wa, bsrc[(gi * PT + t) * 64], acc[tt]);
                     }
-                    __builtin_amdgcn_s_sleep(1);
+                    if ((u + 1) % EVERY == 0) {
+                        const int qi = (u + 1) / EVERY - 1;    // item wave + 8 qi of chunk ch + 1
+                        const int i_ = wave + 8 * qi, g_ = min((ch + 1) * CG + i_ / PT, G - 1);
+                        const u32x4* pp_ = (const u32x4*)(s_abh + g_ * 32 + h * 16);
+                        s_pro[(((ch + 1) & 1) * ITEMS + i_) * 64 + lane] =
+                            pro16(ra[qi], pp_[0], pp_[1], pp_[2], pp_[3]);
+                        const int g2 = min((ch + 2) * CG + i_ / PT, G - 1);
+                        ra[qi] = *(const u32x4*)DP_SRC(g2, i_ % PT);
+                    }
+                    __builtin_amdgcn_sched_barrier(0);
                 }
-                if (!ok && !broken) {
-                    broken = true;
-                    atomicAdd(sync + 2, 1u);
-                }
-                s_b[cc * WIN * 2 + swz((below ? R + 1 : 0) * BW + xx + 1, hh)] =
-                    u32x4{(uint32_t)v0, (uint32_t)v1, (uint32_t)v2, (uint32_t)v3};
+                __syncthreads();                           // chunk ch read, chunk ch + 1 written
             }
+            // the next pass's first chunk: its groups but the newest exist (that one: see above)
+            DP_RA(0, G0 + i, G);
         }
-        __syncthreads();
 
-        // ---- conv2 (3x3, pad 1): pixel tile t2, K steps st = s2, s2 + S2, ... of 36 ----
-        {
+        // ==== (B) layer i - 1's halo rows and conv2 ====
+        if (i > 0) {
+            const int lc = i - 1, par = lc & 1;
+            const uint64_t tag = DP_XCH_TAG(lc);
+            // the neighbours' rows into the halo rows (window row 0 = the band above's last row, row
+            // R + 1 = the band below's first row), polling each pair until its tag is current
+            for (int idx = tid; idx < 2 * 4 * W * 2; idx += DP_NT) {
+                const int hh = idx & 1, xx = (idx >> 1) % W, cc = ((idx >> 1) / W) & 3, below = idx / (8 * W);
+                if (below ? part < K - 1 : part > 0) {
+                    const uint64_t* xp = DP_XP(below ? ticket + 1 : ticket - 1, par, below ? 0 : 1, cc) + xx * 8 + 4 * hh;
+                    uint64_t v0 = 0, v1 = 0, v2 = 0, v3 = 0;
+                    bool ok = false;
+                    for (int it = 0; it < DP_SPIN && !broken; ++it) {
+                        v0 = ld_agent64(xp); v1 = ld_agent64(xp + 1); v2 = ld_agent64(xp + 2); v3 = ld_agent64(xp + 3);
+                        if (((v0 & v1 & v2 & v3) >> 32) == (tag >> 32) && ((v0 | v1 | v2 | v3) >> 32) == (tag >> 32)) {
+                            ok = true;
+                            break;
+                        }
+                        __builtin_amdgcn_s_sleep(1);
+                    }
+                    if (!ok && !broken) {
+                        broken = true;
+                        atomicAdd(sync + 2, 1u);
+                    }
+                    s_b[cc * WIN * 2 + swz((below ? R + 1 : 0) * BW + xx + 1, hh)] =
+                        u32x4{(uint32_t)v0, (uint32_t)v1, (uint32_t)v2, (uint32_t)v3};
+                }
+            }
+            __syncthreads();
+
+            // ---- conv2 (3x3, pad 1): pixel tile t2, K steps st = s2, s2 + S2, ... of 36 ----
             const bool active = PT == 1 ? wave < 4 : true;
             const int t2 = PT == 1 ? 0 : wave / S2, s2 = PT == 1 ? wave : wave % S2;
             const int pl = 32 * t2 + j, yl = pl / W, x = pl - yl * W;
@@ -2329,19 +2327,18 @@ __global__ __launch_bounds__(DP_NT, 1) void k_dparts(D8sPartsArgs a) {
             constexpr int NS = (36 + S2 - 1) / S2;
             if (active) {
 #pragma unroll
-                for (int i = 0; i < NS; ++i) {
-                    const int st = s2 + i * S2;
+                for (int k = 0; k < NS; ++k) {
+                    const int st = s2 + k * S2;
                     if (st < 36) {
                         const int cc = st / 9, tap = st - 9 * cc, ty = tap / 3, tx = tap - 3 * ty;
                         acc2 = mfma_i8(s_w[swz(st * 32 + j, h)], s_b[cc * WIN * 2 + swz(q0 + ty * BW + tx, h)], acc2);
                     }
                 }
             }
-            // the next layer's tables, first weights and first chunk's bytes (groups that exist)
-            if (l + 1 < L) {
-                const D8sLayerP ln = a.layers[l + 1];
-                DP_TABLES(ln, G + 1);
-                DP_RA(0, G + 1, G);
+            // layer i's conv2 tables (stored at the start of (C))
+            {
+                const D8sLayerP ln = a.layers[min(i, L - 1)];
+                DP_TAB2(ln);
             }
             if constexpr (S2 > 1) {
                 if (active && s2 > 0) {
@@ -2364,17 +2361,91 @@ __global__ __launch_bounds__(DP_NT, 1) void k_dparts(D8sPartsArgs a) {
 #pragma unroll
                 for (int kk = 0; kk < 4; ++kk) e[kk] = epi2_q(acc2, kk, *(const float4*)(s_sc + 8 * kk + 4 * h));
                 const u32x4 row = xchg_rows(e[0], e[1], e[2], e[3], h);
-                *(u32x4*)(segn + (int64_t)l * slot + (uint32_t)((bandp + pl) * 32 + 16 * h)) = row;
+                *(u32x4*)(segn + (int64_t)lc * slot + (uint32_t)((bandp + pl) * 32 + 16 * h)) = row;
+                // the new group's bytes of pixel tile t2 through layer i's prologue: exactly the MFMA B
+                // operand of that tile (pixel j, bytes 16 h ..)
+                if (i < L) {
+                    const u32x4* pp_ = (const u32x4*)(s_abh + (G0 + i - 1) * 32 + h * 16);
+                    s_pro[t2 * 64 + lane] = pro16(row, pp_[0], pp_[1], pp_[2], pp_[3]);
+                }
+            }
+            // slot i - 1 stored and the new group's operands written; the conv2 weights read
+            __syncthreads();
+        }
+
+        // ==== (C) layer i's newest group, epilogue, rows out ====
+        if (i < L) {
+            if (i > 0) {
+                // layer i's conv2 tables (before the rows go out: a wait after those stores would
+                // wait for them)
+#pragma unroll
+                for (int k = 0; k < 5; ++k)
+                    if (tid + DP_NT * k < 2304) s_w[swz((tid + DP_NT * k) >> 1, tid & 1)] = t_w2[k];
+                if (tid >= 128 && tid < 160) {
+                    s_sc[tid - 128] = t_sc;
+                    s_w2sum[tid - 128] = t_w2sum;
+                }
+                // 32-pixel bands: the group belongs to the K half of its parity
+                const uint32_t live = KH == 1 || ((G0 + i - 1) & 1) == hv ? ~0u : 0u;
+                const u32x4 wa = t_wn & u32x4{live, live, live, live};
+#pragma unroll
+                for (int tt = 0; tt < NPT; ++tt) {
+                    const int t = KH == 2 ? 0 : hv * NPT + tt;
+                    acc[tt] = mfma_i8(wa, s_pro[t * 64 + lane], acc[tt]);
+                }
+            }
+            // 32-pixel bands: the two K halves of each output tile added through LDS
+            if constexpr (KH == 2) {
+                if (hv == 1) {
+                    int32_t* r = s_red + c * 1024 + lane;
+#pragma unroll
+                    for (int v = 0; v < 16; ++v) r[v * 64] = acc[0][v];
+                }
+                __syncthreads();
+                if (hv == 0) {
+                    const int32_t* r = s_red + c * 1024 + lane;
+#pragma unroll
+                    for (int v = 0; v < 16; ++v) acc[0][v] += r[v * 64];
+                }
+            }
+            // ---- bottleneck bytes (v ^ 0x80) into the window; the band's first / last row out ----
+            const int par = i & 1;
+            const uint64_t tag = DP_XCH_TAG(i);
+            if (KH == 1 || hv == 0) {
+                uint32_t e[4];
+#pragma unroll
+                for (int tt = 0; tt < NPT; ++tt) {
+                    const int t = KH == 2 ? 0 : hv * NPT + tt;
+                    const int pl = 32 * t + j, yl = pl / W, x = pl - yl * W;
+#pragma unroll
+                    for (int kk = 0; kk < 4; ++kk) {
+                        const float4* pg = (const float4*)(s_gd + 32 * c + 8 * kk + 4 * h);
+                        e[kk] = epi1_x80(acc[tt], kk, pg[0], pg[1]);
+                    }
+                    const u32x4 row = xchg_rows(e[0], e[1], e[2], e[3], h);
+                    s_b[c * WIN * 2 + swz((yl + 1) * BW + x + 1, h)] = row;
+                    if (yl == 0 && part > 0) {
+                        uint64_t* xp = DP_XP(ticket, par, 0, c) + x * 8 + 4 * h;
+#pragma unroll
+                        for (int e4 = 0; e4 < 4; ++e4) st_agent64(xp + e4, tag | row[e4]);
+                    }
+                    if (yl == R - 1 && part < K - 1) {
+                        uint64_t* xp = DP_XP(ticket, par, 1, c) + x * 8 + 4 * h;
+#pragma unroll
+                        for (int e4 = 0; e4 < 4; ++e4) st_agent64(xp + e4, tag | row[e4]);
+                    }
+                    __builtin_amdgcn_sched_barrier(0);
+                }
             }
         }
-        // slot l complete before any wave's next conv1 reads it; LDS free for the next layer
-        __syncthreads();
     }
 #undef DP_PRO
 #undef DP_RA
 #undef DP_RW
 #undef DP_W
-#undef DP_TABLES
+#undef DP_TAB1
+#undef DP_TAB2
+#undef DP_XCH_TAG
 #undef DP_G
 #undef DP_XP
 #undef DP_SRC
