@@ -2213,12 +2213,13 @@ __global__ __launch_bounds__(DP_NT, 1) void k_dparts(D8sPartsArgs a) {
             for (int k = 0; k < 4; ++k)
                 if (tid + DP_NT * k < (G0 + i) * 32) s_abh[tid + DP_NT * k] = t_abh[k];
             // group G - 1 (layer i - 2's output), if it is in chunk 0, was not ready when chunk 0 was
-            // requested
+            // requested: its bytes from the copy conv2 left in LDS (a global load here would make the
+            // prologue below wait for every store in flight)
             if (i > 1 && G - 1 < CG) {
 #pragma unroll
                 for (int q_ = 0; q_ < IPW; ++q_) {
                     const int i_ = wave + 8 * q_;
-                    if (i_ / PT == G - 1) ra[q_] = *(const u32x4*)DP_SRC(G - 1, i_ % PT);
+                    if (i_ / PT == G - 1) ra[q_] = s_pro[(ITEMS + i_ % PT) * 64 + lane];
                 }
             }
             __syncthreads();                               // tables in LDS
@@ -2367,6 +2368,7 @@ __global__ __launch_bounds__(DP_NT, 1) void k_dparts(D8sPartsArgs a) {
                 if (i < L) {
                     const u32x4* pp_ = (const u32x4*)(s_abh + (G0 + i - 1) * 32 + h * 16);
                     s_pro[t2 * 64 + lane] = pro16(row, pp_[0], pp_[1], pp_[2], pp_[3]);
+                    s_pro[(ITEMS + t2) * 64 + lane] = row;   // the raw bytes, for the next pass's chunk 0
                 }
             }
             // slot i - 1 stored and the new group's operands written; the conv2 weights read
