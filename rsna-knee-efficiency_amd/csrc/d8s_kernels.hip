@@ -2088,6 +2088,10 @@ __global__ __launch_bounds__(DP_NT, 1) void k_dparts(D8sPartsArgs a) {
     __shared__ __attribute__((aligned(16))) u32x4 s_pro[2 * ITEMS * 64];  // prologue chunks
     __shared__ __attribute__((aligned(16))) int32_t s_red[NRED];          // partial sums
     __shared__ uint32_t s_tk[2];
+    // the layers' descriptors (L <= 64: the launch checks G0 + L - 1 <= 64), so that a layer's table
+    // and weight pointers are an LDS read away, not a global load the table loads depend on
+    __shared__ uint64_t s_lp[64 * 7];
+    static_assert(sizeof(D8sLayerP) == 7 * sizeof(uint64_t), "descriptor layout");
     extern __shared__ __attribute__((aligned(16))) u32x4 s_dyn[];
     const int H = a.H, W = a.W, HW = H * W, K = a.parts, R = H / K, BW = W + 2, WIN = (R + 2) * BW;
     const int G0 = a.G0, L = a.L, N = a.N;
@@ -2109,7 +2113,9 @@ __global__ __launch_bounds__(DP_NT, 1) void k_dparts(D8sPartsArgs a) {
         s_tk[0] = __hip_atomic_fetch_add(sync, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         s_tk[1] = ld_agent(sync + 3);                      // the launch count, stable during a launch
     }
+    for (int q = tid; q < min(a.L, 64) * 7; q += DP_NT) s_lp[q] = ((const uint64_t*)a.layers)[q];
     __syncthreads();
+#define DP_LP(l_) (*(const D8sLayerP*)(s_lp + 7 * (l_)))
     // a ticket past the last band means the sync words were not zero at the launch: nothing to do
     // but count it (the bands left without a workgroup make their neighbours' waits run out)
     const bool valid = (int)s_tk[0] < nparts;
@@ -2178,7 +2184,7 @@ __global__ __launch_bounds__(DP_NT, 1) void k_dparts(D8sPartsArgs a) {
 #define DP_XCH_TAG(l_) ((uint64_t)(epoch * 64u + (uint32_t)(l_) + 1u) << 32)
 
     if (valid) {
-        const D8sLayerP lp0 = a.layers[0];
+        const D8sLayerP lp0 = DP_LP(0);
         DP_TAB1(lp0, G0);
         DP_TAB2(lp0);
         DP_RA(0, G0, G0);
@@ -2192,7 +2198,7 @@ __global__ __launch_bounds__(DP_NT, 1) void k_dparts(D8sPartsArgs a) {
     for (int i = 0; i <= (valid ? L : -1); ++i) {
         // ==== (A) conv1 of layer i over its groups 0 .. G - 1 ====
         if (i < L) {
-            const D8sLayerP lp = a.layers[i];
+            const D8sLayerP lp = DP_LP(i);
             const int G = i == 0 ? G0 : G0 + i - 1;
             const int nch = (G + CG - 1) / CG;
             if (i > 0) __syncthreads();                    // layer i - 1's epilogue has read its tables
@@ -2238,7 +2244,7 @@ __global__ __launch_bounds__(DP_NT, 1) void k_dparts(D8sPartsArgs a) {
             // wait counts at the loop's head are the same from both of its entries
             {
                 const int ln_ = min(i + 1, L - 1);
-                const D8sLayerP ln = a.layers[ln_];
+                const D8sLayerP ln = DP_LP(ln_);
                 DP_TAB1(ln, G0 + ln_);
                 t_wn = DP_W(lp, G0 + i - 1);                 // (i = 0: group G0 - 1, unused)
             }
@@ -2338,7 +2344,7 @@ __global__ __launch_bounds__(DP_NT, 1) void k_dparts(D8sPartsArgs a) {
             }
             // layer i's conv2 tables (stored at the start of (C))
             {
-                const D8sLayerP ln = a.layers[min(i, L - 1)];
+                const D8sLayerP ln = DP_LP(min(i, L - 1));
                 DP_TAB2(ln);
             }
             if constexpr (S2 > 1) {
@@ -2448,6 +2454,7 @@ __global__ __launch_bounds__(DP_NT, 1) void k_dparts(D8sPartsArgs a) {
 #undef DP_TAB1
 #undef DP_TAB2
 #undef DP_XCH_TAG
+#undef DP_LP
 #undef DP_G
 #undef DP_XP
 #undef DP_SRC
