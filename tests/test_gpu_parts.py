@@ -91,3 +91,33 @@ def test_parts_two_runners_at_once(dev, c4):
         torch.cuda.synchronize(dev)
         assert torch.equal(got[0], want[0]) and torch.equal(got[1], want[1]), k
     assert sum(e.sync_errors() for e in encs) == 0
+
+
+@pytest.fixture(scope="module")
+def small_first(dev):
+    """A seeded DenseNet with 4 layers in its first block at 128 px: that block is 32 x 32 with 2
+    groups in (below every prologue chunk of the banded kernel)."""
+    model = densenet.seeded_densenet169(5, blocks=(4, 1, 2, 2)).to(dev)
+    x_u8 = synthetic.study_u8(8, 128, seed=3)
+    cal = dense8s.calibrate(model, [synthetic.normalise(torch.from_numpy(x_u8).to(dev))])
+    pack = dense8s.make_pack(dense8s.make_plan(model.cpu(), cal, 128), 8, input_kind="u8")
+    assert pack["meta"]["blocks"][0]["c0"] // 32 == 2 and pack["meta"]["blocks"][0]["L"] == 4
+    x = torch.from_numpy(x_u8).to(dev)
+    kinds = dense8s.fused_blocks(pack["meta"], None)
+    kinds[0] = "conv"
+    want = dense8s.Dense8SEncoder(pack, dev.index or 0, 8, fused=kinds)(x).clone()
+    return {"pack": pack, "x": x, "kinds": kinds, "want": want}
+
+
+@pytest.mark.parametrize("parts", [4, 8, 16, 32])
+def test_parts_groups_below_first_chunk(dev, small_first, parts):
+    """Layers whose second-newest group falls in the first prologue chunk (it is stored by the conv2
+    that runs after the chunk was requested, and comes from conv2's copy in LDS): every band size
+    (256, 128, 64 and 32 pixels) gives the bytes of two launches per layer."""
+    print(f"small first block, parts:{parts}", flush=True)
+    kinds = dict(small_first["kinds"])
+    kinds[0] = f"parts:{parts}"
+    enc = dense8s.Dense8SEncoder(small_first["pack"], dev.index or 0, 8, fused=kinds)
+    got = enc(small_first["x"]).clone()
+    assert enc.sync_errors() == 0
+    assert torch.equal(got, small_first["want"])
