@@ -2297,21 +2297,59 @@ __global__ __launch_bounds__(DP_NT, 1) void k_dparts(D8sPartsArgs a) {
         if (i > 0) {
             const int lc = i - 1, par = lc & 1;
             const uint64_t tag = DP_XCH_TAG(lc);
+            // the last pass has no (A): its barriers ordered the window rows (C) wrote before this
+            if (i == L) __syncthreads();
+            // conv2's pixel tile t2 and K steps st = s2, s2 + S2, ... of 36 for this wave; a tile whose
+            // rows all lie inside the band (rows 1 .. R - 2) reads no halo row, so its MFMAs run while
+            // the neighbours' rows are read
+            const bool active = PT == 1 ? wave < 4 : true;
+            const int t2 = PT == 1 ? 0 : wave / S2, s2 = PT == 1 ? wave : wave % S2;
+            const int pl = 32 * t2 + j, yl = pl / W, x = pl - yl * W;
+            const int q0 = yl * BW + x;
+            const bool inner = (32 * t2) / W >= 1 && (32 * t2 + 31) / W <= R - 2;
+            i32x16 acc2;
+#pragma unroll
+            for (int v = 0; v < 16; ++v) acc2[v] = s2 == 0 ? 128 * s_w2sum[res_row(v, h)] : 0;
+            constexpr int NS = (36 + S2 - 1) / S2;
+#define DP_CONV2()                                                                                \
+    _Pragma("unroll") for (int k_ = 0; k_ < NS; ++k_) {                                           \
+        const int st_ = s2 + k_ * S2;                                                             \
+        if (st_ < 36) {                                                                           \
+            const int cc_ = st_ / 9, tap_ = st_ - 9 * cc_, ty_ = tap_ / 3, tx_ = tap_ - 3 * ty_;   \
+            acc2 = mfma_i8(s_w[swz(st_ * 32 + j, h)], s_b[cc_ * WIN * 2 + swz(q0 + ty_ * BW + tx_, h)], acc2); \
+        }                                                                                         \
+    }
             // the neighbours' rows into the halo rows (window row 0 = the band above's last row, row
-            // R + 1 = the band below's first row), polling each pair until its tag is current
+            // R + 1 = the band below's first row), polling each pair until its tag is current; a
+            // thread's first pair is read before the inner tiles' MFMAs (an edge band reads its own
+            // pairs there, unused)
+            uint64_t f[4];
+            {
+                const int idx = min(tid, 16 * W - 1);
+                const int hh = idx & 1, xx = (idx >> 1) % W, cc = ((idx >> 1) / W) & 3, below = idx / (8 * W);
+                const bool has = below ? part < K - 1 : part > 0;
+                const int tk = has ? (below ? ticket + 1 : ticket - 1) : ticket;
+                const uint64_t* xp = DP_XP(tk, par, below ? 0 : 1, cc) + xx * 8 + 4 * hh;
+#pragma unroll
+                for (int e4 = 0; e4 < 4; ++e4) f[e4] = ld_agent64(xp + e4);
+            }
+            if (active && inner) {
+                DP_CONV2();
+            }
             for (int idx = tid; idx < 2 * 4 * W * 2; idx += DP_NT) {
                 const int hh = idx & 1, xx = (idx >> 1) % W, cc = ((idx >> 1) / W) & 3, below = idx / (8 * W);
                 if (below ? part < K - 1 : part > 0) {
                     const uint64_t* xp = DP_XP(below ? ticket + 1 : ticket - 1, par, below ? 0 : 1, cc) + xx * 8 + 4 * hh;
-                    uint64_t v0 = 0, v1 = 0, v2 = 0, v3 = 0;
-                    bool ok = false;
-                    for (int it = 0; it < DP_SPIN && !broken; ++it) {
+                    uint64_t v0 = f[0], v1 = f[1], v2 = f[2], v3 = f[3];
+                    bool ok = idx == tid && ((v0 & v1 & v2 & v3) >> 32) == (tag >> 32) &&
+                              ((v0 | v1 | v2 | v3) >> 32) == (tag >> 32);
+                    for (int it = 0; it < DP_SPIN && !ok && !broken; ++it) {
+                        __builtin_amdgcn_s_sleep(1);
                         v0 = ld_agent64(xp); v1 = ld_agent64(xp + 1); v2 = ld_agent64(xp + 2); v3 = ld_agent64(xp + 3);
                         if (((v0 & v1 & v2 & v3) >> 32) == (tag >> 32) && ((v0 | v1 | v2 | v3) >> 32) == (tag >> 32)) {
                             ok = true;
                             break;
                         }
-                        __builtin_amdgcn_s_sleep(1);
                     }
                     if (!ok && !broken) {
                         broken = true;
@@ -2323,25 +2361,11 @@ __global__ __launch_bounds__(DP_NT, 1) void k_dparts(D8sPartsArgs a) {
             }
             __syncthreads();
 
-            // ---- conv2 (3x3, pad 1): pixel tile t2, K steps st = s2, s2 + S2, ... of 36 ----
-            const bool active = PT == 1 ? wave < 4 : true;
-            const int t2 = PT == 1 ? 0 : wave / S2, s2 = PT == 1 ? wave : wave % S2;
-            const int pl = 32 * t2 + j, yl = pl / W, x = pl - yl * W;
-            const int q0 = yl * BW + x;
-            i32x16 acc2;
-#pragma unroll
-            for (int v = 0; v < 16; ++v) acc2[v] = s2 == 0 ? 128 * s_w2sum[res_row(v, h)] : 0;
-            constexpr int NS = (36 + S2 - 1) / S2;
-            if (active) {
-#pragma unroll
-                for (int k = 0; k < NS; ++k) {
-                    const int st = s2 + k * S2;
-                    if (st < 36) {
-                        const int cc = st / 9, tap = st - 9 * cc, ty = tap / 3, tx = tap - 3 * ty;
-                        acc2 = mfma_i8(s_w[swz(st * 32 + j, h)], s_b[cc * WIN * 2 + swz(q0 + ty * BW + tx, h)], acc2);
-                    }
-                }
+            // ---- conv2 (3x3, pad 1) of the tiles next to the halo rows ----
+            if (active && !inner) {
+                DP_CONV2();
             }
+#undef DP_CONV2
             // layer i's conv2 tables (stored at the start of (C))
             {
                 const D8sLayerP ln = DP_LP(min(i, L - 1));
