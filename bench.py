@@ -537,6 +537,146 @@ def mfma_probe(dev: torch.device, blocks: int = 2048, iters: int = 4096, reps: i
                       f"v_mfma_i32_32x32x32_i8"}
 
 
+def graph_ms(fn, reps: int, stream) -> float:
+    """ms per call of `fn` (which launches on `stream`): `reps` calls in one HIP graph, one warm replay,
+    then the median of three timed replays."""
+    with torch.cuda.stream(stream):
+        fn()
+        stream.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=stream, capture_error_mode="thread_local"):
+            for _ in range(reps):
+                fn()
+        g.replay()
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
+        ev[0].record(stream)
+        for e in ev[1:]:
+            g.replay()
+            e.record(stream)
+        stream.synchronize()
+    return sorted(a.elapsed_time(b) for a, b in zip(ev, ev[1:]))[1] / reps
+
+
+def bench_kernels(dev: torch.device, reps: int = 20, peak_tops: float | None = None) -> dict:
+    """Configurations 2 and 3 case by case: the 12 fused-prologue 1 x 1 GEMMs (`d8s_conv1`) and the 4
+    3 x 3 convs (`d8s_conv2`) at batch 24 on the benchmark's own inputs (`synthetic.c2_case` /
+    `c3_case`, seeds 11/12 and 21/22), each timed alone (`graph_ms`): ms, algorithmic GB/s (conv1:
+    M C_in + M 128 + its tables; conv2: M 128 + M 32 + 36 KB of weights), int8 TOP/s (2 per MAC) and
+    the fractions of 8 TB/s, of the 5.0 POP/s datasheet peak and of `peak_tops` (the rate measured on
+    the box by `mfma_probe`)."""
+    import ctypes
+    from rsna_knee_efficiency_amd import hip
+    stream = torch.cuda.Stream(dev)
+    T = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)  # noqa: E731
+
+    def row(case: dict, ms: float, byts: float, ops: float) -> dict:
+        gbs, tops = byts / (ms * 1e-3) / 1e9, ops / (ms * 1e-3) / 1e12
+        r = {**case, "ms": round(ms, 5), "gbs": round(gbs, 1), "int8_tops": round(tops, 1),
+             "frac_hbm": round(gbs / HBM_PEAK_GBS, 4), "frac_mfma_datasheet": round(tops / I8_PEAK_TOPS, 4)}
+        if peak_tops:
+            r["frac_mfma_measured"] = round(tops / peak_tops, 4)
+        return r
+
+    c2 = []
+    for S, cin in synthetic.C2_CASES:
+        d = synthetic.c2_case(S, cin)
+        M = d["N"] * S * S
+        t = {k: T(d[k]) for k in ("in0", "seg", "w1", "abh", "gdu", "w1sum")}
+        bott = torch.empty(4 * M * 32, dtype=torch.uint8, device=dev)
+        args = hip.GemmArgs(t["in0"].data_ptr(), t["seg"].data_ptr(), t["w1"].data_ptr(), t["abh"].data_ptr(),
+                            t["gdu"].data_ptr(), t["w1sum"].data_ptr(), bott.data_ptr(), d["G0"], d["G"],
+                            d["N"], S * S, S, M, 128, 0)
+        ms = graph_ms(lambda: hip.call("d8s_conv1", ctypes.byref(args), stream.cuda_stream), reps, stream)
+        byts = M * cin + M * 128 + 128 * cin + cin * 4 + 128 * 12
+        c2.append(row({"S": S, "C_in": cin, "batch": d["N"]}, ms, byts, 2.0 * M * cin * 128))
+        del t, bott
+    c3 = []
+    for S in synthetic.C3_SIDES:
+        d = synthetic.c3_case(S)
+        M = d["N"] * S * S
+        t = {k: T(d[k]) for k in ("bott", "w2k", "c2u", "w2sum")}
+        slot = torch.empty(M * 32, dtype=torch.int8, device=dev)
+        args = hip.Conv2Args(t["bott"].data_ptr(), t["w2k"].data_ptr(), t["c2u"].data_ptr(),
+                             t["w2sum"].data_ptr(), slot.data_ptr(), d["N"], S, S, 0)
+        ms = graph_ms(lambda: hip.call("d8s_conv2", ctypes.byref(args), stream.cuda_stream), reps, stream)
+        byts = M * 128 + M * 32 + 36864 + 32 * 8
+        c3.append(row({"S": S, "batch": d["N"]}, ms, byts, 2.0 * M * 1152 * 32))
+        del t, slot
+    return {"config": "C2: fused BN + ReLU prologue 1x1 INT8 GEMM -> u8 bottleneck (d8s_conv1); C3: 3x3 "
+                      "pad-1 INT8 conv 128 -> 32 into a store slot (d8s_conv2); batch 24, each case alone, "
+                      f"{reps} launches per HIP graph, median of 3 replays",
+            "c2_cases": c2, "c3_cases": c3}
+
+
+def block_work(b: dict, n: int) -> tuple[float, float]:
+    """(algorithmic bytes, int8 operations) of a whole dense block of n images in one launch: its input
+    read once, its layers' outputs written once, the weights read once."""
+    M = n * b["h"] * b["w"]
+    byts, ops = M * b["c0"] + M * 32 * b["L"], 0.0
+    for li in range(b["L"]):
+        cin = b["c0"] + 32 * li
+        byts += 128 * cin + cin * 4 + 128 * 12 + 36864 + 32 * 8
+        ops += 2.0 * M * cin * 128 + 2.0 * M * 1152 * 32
+    return byts, ops
+
+
+def c4_roofline(enc, reps: int, peak_tops: float | None) -> dict:
+    """Configuration 4's dominant launch (from `time_layers` on the study's store): its int8 rate against
+    the MFMA peak (a whole block of a 24-image study: thousands of operations per byte, far right of the
+    ridge, so the bound is the matrix cores) and its algorithmic GB/s."""
+    layers = enc.time_layers(reps=reps)
+    label = max(layers, key=layers.get)
+    ms = layers[label]
+    out = {"kernel": label, "ms": round(ms, 5), "pass_launch_ms": {k: v for k, v in layers.items() if v >= 0.05}}
+    if label.startswith("blk b"):
+        bi = int(label[5:])
+        byts, ops = block_work(enc.meta["blocks"][bi], enc.nb)
+        tops = ops / (ms * 1e-3) / 1e12
+        out.update({"entry": "d8s_dense_block_parts" if enc.fused[bi].startswith("parts") else "d8s_dense_block",
+                    "kind": enc.fused[bi], "bound": "mfma", "achieved": round(tops, 1), "peak": I8_PEAK_TOPS,
+                    "unit": "TOP/s", "frac": round(tops / I8_PEAK_TOPS, 4),
+                    "gbs": round(byts / (ms * 1e-3) / 1e9, 1), "algorithmic_bytes": int(byts), "ops": ops})
+        if peak_tops:
+            out["frac_of_measured_peak"] = round(tops / peak_tops, 4)
+    return out
+
+
+def chain_in_schedule(encs, x, reps: int, bytes_per_launch: float) -> dict:
+    """The chained conv2 + conv1 launches timed inside configuration 5's schedule: seed 1's pass replays
+    its graph on its stream while seed 0's pass is launched on its own, with events only before the
+    first and after the last chained launch; the span / launches, mean over `reps` steps (after a warm
+    one), and the algorithmic bytes per launch over it against 8 TB/s."""
+    enc = encs[0]
+    prog = enc.program
+    idx = [i for i, s in enumerate(prog) if s.family == "chain"]
+    if not idx:
+        return {}
+    before, last = prog[idx[0] - 1], prog[idx[-1]]
+    spans = []
+    for r in range(reps + 1):
+        ev = {}
+
+        def after(step, ev=ev):
+            if step is before or step is last:
+                e = torch.cuda.Event(enable_timing=True)
+                e.record(enc.stream)
+                ev["a" if step is before else "b"] = e
+        torch.cuda.synchronize()
+        with torch.cuda.stream(encs[1].stream):
+            encs[1](x, flip="tta")
+        with torch.cuda.stream(enc.stream):
+            enc.launch(x, flip="tta", after=after)
+        torch.cuda.synchronize()
+        if r:
+            spans.append(ev["a"].elapsed_time(ev["b"]) / len(idx))
+    ms = float(np.mean(spans))
+    gbs = bytes_per_launch / (ms * 1e-3) / 1e9
+    return {"launches": len(idx), "avg_launch_ms": round(ms, 5), "gbs": round(gbs, 1),
+            "frac": round(gbs / HBM_PEAK_GBS, 4),
+            "schedule": "seed 0 eager with events at the chained run's ends, seed 1's graph replay on "
+                        "its own stream at the same time"}
+
+
 def bench_c4(dev: torch.device, passes: int, reps: int) -> dict:
     """Configuration 4 alone: one encoder (seed 0, batch 24), the 24-slice study of study 0 replayed
     from its graph `passes` times (wall latency per replay, median), then the per-family kernel times
@@ -830,9 +970,9 @@ def main() -> None:
     ap.add_argument("--pmc-passes", type=int, default=0, metavar="P",
                     help="only run P eager configuration-5 passes of one encoder (the launches of "
                          "a counter-collection run), print the per-family times and exit")
-    ap.add_argument("--path", choices=("encoder", "prep", "head"), default="encoder",
+    ap.add_argument("--path", choices=("encoder", "prep", "head", "kernels"), default="encoder",
                     help="prep: the upstream preparation (raw crops -> uint8 volume); head: the head "
-                         "after the encoder")
+                         "after the encoder; kernels: configurations 2 and 3 case by case")
     ap.add_argument("--traffic-summary", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                     help="print the HBM traffic per launch from two --pmc-passes counter runs")
     ap.add_argument("--c4-passes", type=int, default=0, metavar="P",
@@ -876,6 +1016,12 @@ def main() -> None:
     dev = torch.device("cuda:0")
     if args.path == "head":
         print(json.dumps(bench_head(dev, with_cpu=not args.no_cpu)), flush=True)
+        return
+    if args.path == "kernels":
+        peak = mfma_probe(dev)
+        res = bench_kernels(dev, peak_tops=peak["i8_tops"])
+        res["mfma_probe"] = peak
+        print(json.dumps(res), flush=True)
         return
     if args.path == "prep":
         if args.pmc_passes:
@@ -985,7 +1131,13 @@ def main() -> None:
         torch.cuda.synchronize()
         lat.append(time.perf_counter() - ta)
     study_ms = float(np.median(lat)) * 1e3
-    log(f"config 4: study latency {study_ms:.3f} ms to the logits (median of {len(lat)})")
+    c4_wait_errors = enc4.sync_errors()
+    if c4_wait_errors:
+        raise RuntimeError(f"config 4: {c4_wait_errors} bounded waits of the banded blocks ran out")
+    log(f"config 4: study latency {study_ms:.3f} ms to the logits (median of {len(lat)}), "
+        f"banded-block wait errors {c4_wait_errors}")
+    roof4 = c4_roofline(enc4, args.prof_reps, None)
+    log(f"config 4 dominant launch: {roof4}")
 
     # agreement of the INT8 features with the fp32 DenseNet169 forward of the same weights on the same
     # study (the GPU, float32 torch), and of the logits of a seeded 1664 -> 8 linear head
@@ -1042,6 +1194,10 @@ def main() -> None:
     fam_tops = {k: round(ops[k] / (fam[k] * 1e-3) / 1e12, 1) for k in ops if fam.get(k)}
     log(f"pass of {nb}: {pass_ms:.3f} ms; families ms {json.dumps({k: round(v, 3) for k, v in fam.items()})}")
     log(f"families GB/s {fam_gbs}; int8 TOP/s {fam_tops}")
+    # the dominant family inside configuration 5's own two-stream schedule (the isolated figure above
+    # replays its launches back to back)
+    in_pass = chain_in_schedule(encs, studies[0], args.prof_reps, dom_bytes / launches) if dom == "chain" else {}
+    log(f"{dom} launches inside the two-stream schedule: {in_pass}")
     total_bytes = sum(sum(v) for v in byts.values())
     out = {
         "metric": "512px DenseNet169 INT8 slices/sec on 1 MI355X; 24-slice study latency ms",
@@ -1056,6 +1212,7 @@ def main() -> None:
                    "parallelism": "none (1 GPU)"},
         "c5_all_studies": sweep,
         "study_latency_ms": round(study_ms, 3),
+        "study_wait_errors": c4_wait_errors,
         "study_latency_config": "C4: one 24-slice study, batch 24, one encoder (HIP graph replay), then "
                                 "the 1664 -> 8 linear head on the device (d8s_linear), to the logits",
         "fp32_agreement": fp32_agreement,
@@ -1070,7 +1227,9 @@ def main() -> None:
                      "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": committed_traffic(dom),
                      "algorithmic_bytes_per_launch": int(dom_bytes / launches),
-                     "avg_launch_ms": round(avg_ms, 5)},
+                     "avg_launch_ms": round(avg_ms, 5),
+                     "frac_in_pass": in_pass.get("frac"), "in_pass": in_pass},
+        "roofline_c4": roof4,
     }
     # the upstream preparation (raw crops -> uint8 volume), its own throughput on the same GPU
     pr = bench_prep(dev, max(args.steps, 20), args.warmup, False)
@@ -1083,6 +1242,11 @@ def main() -> None:
     log(f"mfma probe: {out['mfma_probe']}")
     out["family_int8_frac_of_measured_peak"] = {
         k: round(v / out["mfma_probe"]["i8_tops"], 4) for k, v in fam_tops.items()}
+    if "achieved" in roof4:
+        roof4["frac_of_measured_peak"] = round(roof4["achieved"] / out["mfma_probe"]["i8_tops"], 4)
+    out["kernels"] = bench_kernels(dev, peak_tops=out["mfma_probe"]["i8_tops"])
+    log(f"kernels: c2 {[(r['S'], r['C_in'], r['gbs']) for r in out['kernels']['c2_cases']]}; "
+        f"c3 {[(r['S'], r['gbs']) for r in out['kernels']['c3_cases']]}")
     if args.copy_probe:
         out["copy_probe"] = copy_probe(dev)
         log(f"copy probe: {out['copy_probe']}")

@@ -127,8 +127,16 @@ typedef struct D8sBlockArgs {
  *          launches (it names each launch's exchange rows);
  *   xchg   device, D8S_PARTS_XCHG_BYTES(N * parts, W) bytes, all zero before the first call: the
  *          bottleneck rows a part hands to its neighbours, as (value, tag) pairs;
- *   parts  row bands per image: H % parts == 0 and (H / parts) * W in {32, 64, 128, 256}.
- * One runner's buffers serve its calls in stream order; two launches in flight at once need their own. */
+ *   parts  row bands per image: H % parts == 0, (H / parts) * W in {32, 64, 128, 256}, parts at most
+ *          the device's compute units (d8s_parts_supported(H, W, G0 + L - 1, parts) says whether a
+ *          shape is taken).
+ * One runner's buffers serve its calls in stream order; two launches in flight at once need their own.
+ * Forward progress: a workgroup takes the next (image, band) ticket when it starts, so the running
+ * workgroups of a launch always hold a prefix of its tickets, and every image wholly inside that prefix
+ * completes without waiting for anything else.  The waits therefore end whenever the launches in flight
+ * on the device together have no more bands per image than it has compute units: a wait can only run
+ * out (word 2) when other work keeps CUs busy for about a second.  Callers that must never use such
+ * results pass word 2 to d8s_final_checked, which then writes NaN features. */
 #define D8S_PARTS_SYNC_WORDS(nparts) (64 + 0 * (nparts))
 #define D8S_PARTS_XCHG_BYTES(nparts, W) ((uint64_t)(nparts) * 1024 * (W))
 typedef struct D8sPartsArgs {
@@ -218,6 +226,7 @@ int d8s_dense_block(const D8sBlockArgs* a, void* stream);
  * role of the reference's `dense_img*` kernels (src/knee/dense8s_kernels.cu:1005-1219), which run
  * one image per block. */
 int d8s_dense_block_parts(const D8sPartsArgs* a, void* stream);
+int d8s_parts_supported(int32_t H, int32_t W, int32_t G, int32_t parts);
 
 /* Transition: prologue on the 4 pixels of every 2x2 square, s = sum of the four u, S = sum_k w[o][k]
  * s[k] (exact int32), q = RNE(clamp(k'_o * (float(S) / 4), -127, 127)) into the next block's in0.
@@ -231,6 +240,21 @@ int d8s_transition(const D8sGemmArgs* a, void* stream);
  * (src/knee/dense8s_kernels.cu:2304-2323, launch src/knee/dense8s.py:1380-1384); same arguments. */
 int d8s_final(const int8_t* in0, int32_t G0, const int8_t* seg, int32_t N, int32_t HW,
               const float* ab, float* out, int32_t ctot, void* stream);
+
+/* d8s_final for a pass with banded whole-block launches (d8s_dense_block_parts): `status` is the
+ * device word those launches count expired waits in (D8sPartsArgs.sync + 2).  When it is not zero,
+ * every feature of the pass is NaN instead of values computed from stale halo rows.  `report` (may
+ * be NULL) is a host-mapped word (d8s_host_mapped) that receives the status word, so that the host
+ * can see an error after the pass without a synchronisation.  No counterpart in the reference, whose
+ * whole-block kernel runs one workgroup per image and never waits on another (the role of its
+ * `final_q`, src/knee/dense8s_kernels.cu:2304-2323). */
+int d8s_final_checked(const int8_t* in0, int32_t G0, const int8_t* seg, int32_t N, int32_t HW,
+                      const float* ab, float* out, int32_t ctot, const uint32_t* status, uint32_t* report,
+                      void* stream);
+
+/* The device address of pinned host memory (hipHostGetDevicePointer), for d8s_final_checked's
+ * `report`.  Plumbing without a reference counterpart (the reference reads its results with copies). */
+int d8s_host_mapped(void* host, void** dev);
 
 /* Linear head on the final features: out[n][k] = b[k] + sum_c x[n][c] w[k][c] in float32 (x [N][C],
  * w [K][C], b [K], out [N][K]; K <= 4096).  Configuration 4's 1664 -> 8 logits after the encoder; the

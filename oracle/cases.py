@@ -153,3 +153,20 @@ def trans_case(S: int, C: int, N: int = 4, seed: int = 31, c0: int | None = None
     in0, seg = store_from_q(q, G0)
     return {"S": S, "N": N, "C": C, "G0": G0, "G": C // 32, "q": q, "in0": in0, "seg": seg,
             "abh": abh_table(ab), "ab": ab, "tw": tw, "w": chunked(tw), "gdf": gdf, "cout": cout}
+
+
+def gemm_case_c2(S: int, C: int, N: int = 24) -> GemmCase:
+    """Configuration 2's case with the benchmark's own distributions and seeds (activations 11, weights
+    12: `synthetic.c2_case`), as a GemmCase."""
+    from rsna_knee_efficiency_amd import synthetic
+    d = synthetic.c2_case(S, C, N)
+    return GemmCase(S, N, d["G0"], d["G"], d["in0"], d["seg"], d["q"], d["abh"], d["ab"], d["w"], d["w1"],
+                    d["gdu"])
+
+
+def conv2_case_c3(S: int, N: int = 24) -> Conv2Case:
+    """Configuration 3's case with the benchmark's own distributions and seeds (activations 21, weights
+    22: `synthetic.c3_case`), as a Conv2Case."""
+    from rsna_knee_efficiency_amd import synthetic
+    d = synthetic.c3_case(S, N)
+    return Conv2Case(S, N, d["v"], d["bott"], d["w2"], d["w2k"], d["c2u"])

@@ -276,7 +276,8 @@ def check_trace(enc, trace: dict, feats: np.ndarray, par: dict, max_rows: int | 
     sampled (`max_rows` per launch, None = all).  Returns the byte comparison of every launch per
     family: "conv1" / "conv2" (two launches per layer, the bottleneck traced), "dense" (a fused layer,
     no bottleneck in memory), "block" (a layer of a whole-block launch, `enc.fused[b] == "img"`),
-    "trans", and "final" (features equal or not)."""
+    "trans", and "final" (features equal or not).  Fused layers are also checked on every pixel of the
+    rows where their kernel's bands meet (`band_edges`), besides the sample."""
     rng = np.random.default_rng(seed)
     meta = enc.meta
     n = enc.nb
@@ -297,7 +298,7 @@ def check_trace(enc, trace: dict, feats: np.ndarray, par: dict, max_rows: int | 
             if ("bott", bi, li) not in trace:
                 # fused layer: the oracle's bottleneck on the 3x3 neighbourhoods of sampled pixels,
                 # then its conv2 on them
-                sel2 = pick(n * hw)
+                sel2 = np.union1d(pick(n * hw), band_edges(kinds.get(bi, ""), n, h, w))
                 nbr = neighbourhoods(sel2, h, w)
                 _, vb = lib.conv1(in0, seg, g0, g0 + li, n, hw, par[f"L{bi}_{li}_abh"],
                                   par[f"L{bi}_{li}_w1"], par[f"L{bi}_{li}_gdu"], nbr)
@@ -335,6 +336,24 @@ def check_trace(enc, trace: dict, feats: np.ndarray, par: dict, max_rows: int | 
             worst["final"] = {"max_abs": float(np.abs(feats[:n] - want).max()),
                               "equal": bool(np.array_equal(feats[:n], want))}
     return worst
+
+
+def band_edges(kind, n: int, h: int, w: int) -> np.ndarray:
+    """Rows (n h w + y w + x) where a fused kernel's work split meets itself, for the first and last
+    image: "parts:K" (d8s_dense_block_parts) the last row of each band and the first of the next
+    (their halo rows cross workgroups), "tile" (d8s_dense's row bands of 8 or 16 rows, or its 2-D
+    tiles) every row y with y % 8 in {7, 0}; nothing for the other kinds."""
+    kind = str(kind)
+    if kind.startswith("parts:"):
+        r = h // int(kind.split(":", 1)[1])
+        ys = sorted({y for k in range(1, h // r) for y in (k * r - 1, k * r)})
+    elif kind == "tile":
+        ys = [y for y in range(h) if y % 8 in (7, 0)]
+    else:
+        return np.zeros(0, np.int64)
+    ys = np.asarray(ys, np.int64)
+    out = [img * h * w + (ys[:, None] * w + np.arange(w)[None, :]).reshape(-1) for img in sorted({0, n - 1})]
+    return np.concatenate(out) if ys.size else np.zeros(0, np.int64)
 
 
 def neighbourhoods(sel: np.ndarray, h: int, w: int) -> np.ndarray:

@@ -35,14 +35,32 @@ def hipcc() -> str:
 
 
 def build_library(out: Path | None = None, verbose: bool = False) -> Path:
+    """Compiles every `.hip` source of the library to an object in parallel (one hipcc per file), then
+    links them into `out` (default: the package's libd8s_hip.so), replacing it atomically."""
     out = Path(out or hip.LIB_PATH)
-    tmp = out.with_suffix(f".so.tmp{os.getpid()}")
-    cmd = [hipcc(), *HIPCC_FLAGS, f"-I{hip.HEADER.parent}", f'-DD8S_SRC_HASH="{hip.source_sha()}"',
-           *(str(f) for f in hip.SOURCES if f.suffix == ".hip"), "-o", str(tmp)]
-    res = subprocess.run(cmd, capture_output=True, text=True)
-    if res.returncode != 0:
-        raise RuntimeError(f"hipcc failed ({res.returncode}):\n{res.stderr[-4000:]}")
-    if verbose and res.stderr:
-        print(res.stderr[-2000:])
-    os.replace(tmp, out)
+    tag = f"{os.getpid()}"
+    common = [*HIPCC_FLAGS, f"-I{hip.HEADER.parent}", f'-DD8S_SRC_HASH="{hip.source_sha()}"']
+    srcs = [f for f in hip.SOURCES if f.suffix == ".hip"]
+    objs = [out.with_name(f"{f.stem}.{tag}.o") for f in srcs]
+    procs = [subprocess.Popen([hipcc(), *common, "-c", str(f), "-o", str(o)], stdout=subprocess.PIPE,
+                              stderr=subprocess.PIPE, text=True) for f, o in zip(srcs, objs)]
+    errs = []
+    for f, pr in zip(srcs, procs):
+        _, err = pr.communicate()
+        if pr.returncode != 0:
+            errs.append(f"{f.name}: hipcc failed ({pr.returncode}):\n{err[-4000:]}")
+        elif verbose and err:
+            print(err[-2000:])
+    try:
+        if errs:
+            raise RuntimeError("\n".join(errs))
+        tmp = out.with_suffix(f".so.tmp{tag}")
+        res = subprocess.run([hipcc(), *HIPCC_FLAGS, *(str(o) for o in objs), "-o", str(tmp)],
+                             capture_output=True, text=True)
+        if res.returncode != 0:
+            raise RuntimeError(f"link failed ({res.returncode}):\n{res.stderr[-4000:]}")
+        os.replace(tmp, out)
+    finally:
+        for o in objs:
+            o.unlink(missing_ok=True)
     return out

@@ -2068,21 +2068,35 @@ DEV uint32_t ld_agent(const uint32_t* p) {
 }
 DEV void st_agent(uint32_t* p, uint32_t v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
 
+// Shape constants of k_dparts<PT>, shared by the kernel's static LDS arrays and the host's LDS check.
 template <int PT>
-__global__ __launch_bounds__(DP_NT, 1) void k_dparts(D8sPartsArgs a) {
+struct DpShape {
     static_assert(PT == 1 || PT == 2 || PT == 4 || PT == 8, "pixel tiles per band");
     // groups per prologue chunk: 4 for 128- and 256-pixel bands (for 128: a 24-image study's 32 x 32
     // block 0.76-0.77 against 0.79-0.82 ms with 8, 0.78-0.80 with 2), 8 for the narrower ones (a
     // 32-pixel band needs 8 for one operand per wave; 16 was slower)
-    constexpr int CG = PT == 4 || PT == 8 ? 4 : 8;
-    constexpr int ITEMS = CG * PT;                         // (group, pixel tile) operands per chunk
+    static constexpr int CG = PT == 4 || PT == 8 ? 4 : 8;
+    static constexpr int ITEMS = CG * PT;                  // (group, pixel tile) operands per chunk
+    static constexpr int S2 = PT == 8 ? 1 : (PT == 4 ? 2 : 4);   // conv2 K slices per pixel tile
+    static constexpr int NRED = PT == 1 ? 4 * 1024 : ((S2 - 1) * PT * 1024 > 0 ? (S2 - 1) * PT * 1024 : 1);
+    static constexpr int NLP = 64 * 7;                     // layer descriptors (at most 64 layers)
+    // static LDS bytes: conv2 weights, two prologue chunks, partial sums, the ticket words and the
+    // descriptors (the arrays of k_dparts, in that order), plus 64 bytes for their alignment
+    static constexpr size_t STATIC = 2304 * 16 + 2 * ITEMS * 64 * 16 + NRED * 4 + 2 * 4 + NLP * 8 + 64;
+};
+
+template <int PT>
+__global__ __launch_bounds__(DP_NT, 1) void k_dparts(D8sPartsArgs a) {
+    using SH = DpShape<PT>;
+    constexpr int CG = SH::CG;
+    constexpr int ITEMS = SH::ITEMS;                       // (group, pixel tile) operands per chunk
     constexpr int IPW = ITEMS / 8;                         // of them per wave
     constexpr int NPT = PT == 1 ? 1 : PT / 2;              // conv1 pixel tiles per wave
     constexpr int KH = PT == 1 ? 2 : 1;                    // conv1 K halves (32-pixel bands)
     constexpr int QC = CG / KH;                            // a wave's groups per chunk
     constexpr int DW = 4;                                  // weight groups in flight per wave
-    constexpr int S2 = PT == 8 ? 1 : (PT == 4 ? 2 : 4);    // conv2 K slices per pixel tile
-    constexpr int NRED = (PT == 1 ? 4 * 1024 : (S2 - 1) * PT * 1024) > 0 ? (PT == 1 ? 4 * 1024 : (S2 - 1) * PT * 1024) : 1;
+    constexpr int S2 = SH::S2;                             // conv2 K slices per pixel tile
+    constexpr int NRED = SH::NRED;
     static_assert(QC % DW == 0 && IPW >= 1, "chunk shape");
     __shared__ __attribute__((aligned(16))) u32x4 s_w[2304];              // conv2 weights, 36 KB
     __shared__ __attribute__((aligned(16))) u32x4 s_pro[2 * ITEMS * 64];  // prologue chunks
@@ -2090,7 +2104,7 @@ __global__ __launch_bounds__(DP_NT, 1) void k_dparts(D8sPartsArgs a) {
     __shared__ uint32_t s_tk[2];
     // the layers' descriptors (L <= 64: the launch checks G0 + L - 1 <= 64), so that a layer's table
     // and weight pointers are an LDS read away, not a global load the table loads depend on
-    __shared__ uint64_t s_lp[64 * 7];
+    __shared__ uint64_t s_lp[SH::NLP];
     static_assert(sizeof(D8sLayerP) == 7 * sizeof(uint64_t), "descriptor layout");
     extern __shared__ __attribute__((aligned(16))) u32x4 s_dyn[];
     const int H = a.H, W = a.W, HW = H * W, K = a.parts, R = H / K, BW = W + 2, WIN = (R + 2) * BW;
@@ -2753,12 +2767,20 @@ __global__ __launch_bounds__(256) void k_linear(const float* __restrict__ x, int
 // (in order) of relu(fma(a_c, q_s, b_c)): the summation order of the reference's `final_q`
 // (src/knee/dense8s_kernels.cu:2304-2323), so the fp32 result is the same.  Workgroup = one image x 2
 // groups: 64 channels x 4 partials.
+// `status` (may be null): the pass's error word (the banded whole-block launches' count of bounded waits
+// that ran out).  When it is not zero the features of the pass are NaN instead, so that features built
+// from stale halo rows cannot pass for valid ones; `report` (may be null, host-mapped memory) receives
+// the word from one thread, for the host to read without a synchronisation.
 // ------------------------------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void k_final(const int8_t* __restrict__ in0, int G0,
                                                const int8_t* __restrict__ seg, int N, int HW, int G,
                                                const float* __restrict__ ab, float* __restrict__ out,
-                                               int ctot) {
+                                               int ctot, const uint32_t* __restrict__ status,
+                                               uint32_t* __restrict__ report) {
     __shared__ float part[4][64];
+    const uint32_t err = status ? status[0] : 0u;
+    if (report && blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0)   // to host memory, past the caches
+        __hip_atomic_store(report, err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
     const int n = blockIdx.x;
     const int c64 = threadIdx.x & 63, qp = threadIdx.x >> 6;
     const int g = blockIdx.y * 2 + (c64 >> 5), cc = c64 & 31;
@@ -2783,7 +2805,7 @@ __global__ __launch_bounds__(256) void k_final(const int8_t* __restrict__ in0, i
     __syncthreads();
     if (qp == 0 && g < G)
         out[(int64_t)n * ctot + g * 32 + cc] =
-            (((part[0][c64] + part[1][c64]) + part[2][c64]) + part[3][c64]) / (float)HW;
+            err ? __builtin_nanf("") : (((part[0][c64] + part[1][c64]) + part[2][c64]) + part[3][c64]) / (float)HW;
 }
 
 // ------------------------------------------------------------------------------------------------
@@ -3703,24 +3725,56 @@ extern "C" int d8s_dense_block_pair(const D8sBlockArgs* a, const D8sBlockArgs* b
     return dblock_launch(a, b, (hipStream_t)stream);
 }
 
+// The shape checks of d8s_dense_block_parts (H, W, groups read by the last layer, bands per image):
+// nullptr if it runs, else the reason; *shm = its dynamic LDS bytes.
+static const char* parts_shape(int H, int W, int G, int parts, size_t* shm) {
+    if (H < 1 || W < 1 || G < 1 || parts < 1) return "H, W, groups and parts must be >= 1";
+    if (H % parts) return "H must be a multiple of parts";
+    const int R = H / parts, P = R * W;
+    if (P != 32 && P != 64 && P != 128 && P != 256) return "(H / parts) * W must be 32, 64, 128 or 256 pixels";
+    if (G > 64) return "more than 64 groups";
+    // the band's window (R + 2 rows of W + 2 pixels, 4 planes), the layer tables, the prologue tables
+    const size_t dyn = (size_t)(R + 2) * (W + 2) * 128 + DB_PRM + (size_t)G * 128;
+    const size_t stat = P == 32 ? DpShape<1>::STATIC : P == 64 ? DpShape<2>::STATIC
+                      : P == 128 ? DpShape<4>::STATIC : DpShape<8>::STATIC;
+    if (dyn + stat > 160 * 1024) return "band too large for LDS";
+    if (shm) *shm = dyn;
+    return nullptr;
+}
+
+extern "C" int d8s_parts_supported(int32_t H, int32_t W, int32_t G, int32_t parts) {
+    return parts_shape(H, W, G, parts, nullptr) == nullptr ? 1 : 0;
+}
+
 extern "C" int d8s_dense_block_parts(const D8sPartsArgs* a, void* stream) {
     REQUIRE(a != nullptr, "d8s_dense_block_parts: null arguments");
     REQUIRE(a->in0 && a->seg && a->layers && a->sync && a->xchg, "d8s_dense_block_parts: null pointer");
     REQUIRE(a->G0 >= 1 && a->L >= 1 && a->N >= 1 && a->H >= 1 && a->W >= 1 && a->parts >= 1,
             "d8s_dense_block_parts: G0, L, N, H, W, parts must be >= 1");
-    REQUIRE(a->H % a->parts == 0, "d8s_dense_block_parts: H must be a multiple of parts");
-    const int R = a->H / a->parts, P = R * a->W;
-    REQUIRE(P == 32 || P == 64 || P == 128 || P == 256,
-            "d8s_dense_block_parts: (H / parts) * W must be 32, 64, 128 or 256 pixels");
-    REQUIRE(a->G0 + a->L - 1 <= 64, "d8s_dense_block_parts: more than 64 groups");
+    size_t shm = 0;
+    const char* why = parts_shape(a->H, a->W, a->G0 + a->L - 1, a->parts, &shm);
+    REQUIRE(why == nullptr, std::string("d8s_dense_block_parts: ") + (why ? why : ""));
     REQUIRE((int64_t)a->N * a->parts < (1 << 24), "d8s_dense_block_parts: too many parts");
     REQUIRE((int64_t)a->N * a->H * a->W * 32 < (1ll << 31), "d8s_dense_block_parts: store slot over 2 GiB");
-    const size_t shm = (size_t)(R + 2) * (a->W + 2) * 128 + DB_PRM + (size_t)(a->G0 + a->L - 1) * 128;
-    // static LDS of k_dparts<PT>: conv2 weights, two prologue chunks, partial sums, the ticket
-    const int PT = P / 32, CG = PT == 4 || PT == 8 ? 4 : 8, S2 = PT == 8 ? 1 : (PT == 4 ? 2 : 4);
-    const size_t nred = PT == 1 ? 4 * 1024 : (size_t)std::max(1, (S2 - 1) * PT * 1024);
-    const size_t stat = 36864 + 2 * (size_t)CG * PT * 1024 + 4 * nred + 16;
-    REQUIRE(shm + stat <= 160 * 1024, "d8s_dense_block_parts: band too large for LDS");
+    REQUIRE(a->parts <= cu_count(), "d8s_dense_block_parts: more bands per image than compute units");
+    const int P = (a->H / a->parts) * a->W;
+    // the LDS check above counts DpShape<PT>::STATIC bytes of static LDS: make sure the compiled kernel
+    // uses no more (checked once per band size)
+    {
+        static int checked[9] = {0};
+        const int PT = P / 32;
+        if (!checked[PT]) {
+            hipFuncAttributes at{};
+            const void* fn = PT == 1 ? (const void*)k_dparts<1> : PT == 2 ? (const void*)k_dparts<2>
+                           : PT == 4 ? (const void*)k_dparts<4> : (const void*)k_dparts<8>;
+            const size_t want = PT == 1 ? DpShape<1>::STATIC : PT == 2 ? DpShape<2>::STATIC
+                              : PT == 4 ? DpShape<4>::STATIC : DpShape<8>::STATIC;
+            const hipError_t e = hipFuncGetAttributes(&at, fn);
+            if (e != hipSuccess) return fail((int)e, std::string("d8s_dense_block_parts: ") + hipGetErrorString(e));
+            REQUIRE(at.sharedSizeBytes <= want, "d8s_dense_block_parts: the kernel's static LDS exceeds its estimate");
+            checked[PT] = 1;
+        }
+    }
     hipStream_t st = (hipStream_t)stream;
     const dim3 grid((unsigned)(a->N * a->parts));
     switch (P / 32) {
@@ -3796,16 +3850,36 @@ extern "C" int d8s_transition_pair(const D8sGemmArgs* a, const D8sGemmArgs* b, v
     return trans_dispatch(a, b, (hipStream_t)stream);
 }
 
-extern "C" int d8s_final(const int8_t* in0, int32_t G0, const int8_t* seg, int32_t N, int32_t HW,
-                         const float* ab, float* out, int32_t ctot, void* stream) {
-    REQUIRE(in0 && ab && out, "d8s_final: null pointer");
+static int final_launch(const int8_t* in0, int32_t G0, const int8_t* seg, int32_t N, int32_t HW,
+                        const float* ab, float* out, int32_t ctot, const uint32_t* status, uint32_t* report,
+                        void* stream, const char* what) {
+    REQUIRE(in0 && ab && out, std::string(what) + ": null pointer");
     REQUIRE(G0 >= 1 && N >= 1 && HW >= 1 && ctot >= 32 * G0 && ctot % 32 == 0,
-            "d8s_final: bad sizes (G0, N, HW >= 1, ctot a multiple of 32 and >= 32 G0)");
-    REQUIRE(ctot == 32 * G0 || seg != nullptr, "d8s_final: seg is null with ctot > 32 G0");
+            std::string(what) + ": bad sizes (G0, N, HW >= 1, ctot a multiple of 32 and >= 32 G0)");
+    REQUIRE(ctot == 32 * G0 || seg != nullptr, std::string(what) + ": seg is null with ctot > 32 G0");
     const int G = ctot / 32;
     hipLaunchKernelGGL(k_final, dim3((unsigned)N, (unsigned)((G + 1) / 2)), dim3(256), 0,
-                       (hipStream_t)stream, in0, G0, seg, N, HW, G, ab, out, ctot);
-    return launched("d8s_final");
+                       (hipStream_t)stream, in0, G0, seg, N, HW, G, ab, out, ctot, status, report);
+    return launched(what);
+}
+
+extern "C" int d8s_final(const int8_t* in0, int32_t G0, const int8_t* seg, int32_t N, int32_t HW,
+                         const float* ab, float* out, int32_t ctot, void* stream) {
+    return final_launch(in0, G0, seg, N, HW, ab, out, ctot, nullptr, nullptr, stream, "d8s_final");
+}
+
+extern "C" int d8s_final_checked(const int8_t* in0, int32_t G0, const int8_t* seg, int32_t N, int32_t HW,
+                                 const float* ab, float* out, int32_t ctot, const uint32_t* status,
+                                 uint32_t* report, void* stream) {
+    REQUIRE(status != nullptr, "d8s_final_checked: null status word");
+    return final_launch(in0, G0, seg, N, HW, ab, out, ctot, status, report, stream, "d8s_final_checked");
+}
+
+extern "C" int d8s_host_mapped(void* host, void** dev) {
+    REQUIRE(host && dev, "d8s_host_mapped: null pointer");
+    const hipError_t e = hipHostGetDevicePointer(dev, host, 0);
+    if (e != hipSuccess) return fail((int)e, std::string("d8s_host_mapped: ") + hipGetErrorString(e));
+    return 0;
 }
 
 extern "C" int d8s_linear(const float* x, int32_t N, int32_t C, const float* w, const float* b, int32_t K,

@@ -406,14 +406,18 @@ RUNTIME_TABLES = ("_abh", "_w1", "_gdu", "_w2k", "_c2u", "_w", "_gdf")
 
 
 def pack_meta(plan: SPlan, n: int, input_kind: str = "u8", mean=(0.5, 0.5, 0.5),
-              std=(0.25, 0.25, 0.25)) -> dict:
+              std=(0.25, 0.25, 0.25), fused: dict | None = None) -> dict:
     """Package metadata: format 1, kind "dense8s" (`src/knee/dense8s.py:810-830`).  `n` = images per
     pass (graph block); `input`: "u8" (raw slices, normalised in the stem with mean / std) or "f16"
-    (already normalised fp16, the reference's input)."""
+    (already normalised fp16, the reference's input); `fused` {block: kind} (keys ints or "b{block}"):
+    the block kinds to record, e.g. `Dense8SEncoder.tune_kinds`'s choice, which runners of the package
+    then use (the reference's per-block "fused" field)."""
     if input_kind not in ("u8", "f16"):
         raise ValueError(f"input kind {input_kind!r}: expected 'u8' or 'f16'")
-    blocks = [{"c0": b.c0, "h": b.h, "w": b.w, "L": len(b.layers), "trans": b.ta is not None}
-              for b in plan.blocks]
+    fused = fused or {}
+    blocks = [{"c0": b.c0, "h": b.h, "w": b.w, "L": len(b.layers), "trans": b.ta is not None,
+               "fused": fused.get(bi) or fused.get(f"b{bi}")}
+              for bi, b in enumerate(plan.blocks)]
     return {"format": PACK_FORMAT, "kind": KIND, "n": int(n), "img": plan.img,
             "in_ch": plan.in_ch, "kernels_sha": hip.source_sha(), "n_features": plan.n_features,
             "stem_c": int(plan.w0.shape[0]), "conv2": "ours", "stem": "hip", "conv2_int8": True,
@@ -551,11 +555,6 @@ def contents_id(x: torch.Tensor) -> tuple:
     return (x.untyped_storage().data_ptr(), x.data_ptr(), tuple(x.shape), tuple(x.stride()), ver)
 
 
-class Layer(collections.namedtuple("Layer", "c1 c2 dense")):
-    """The launches of one dense layer: conv1 and conv2 argument structs, and the fused layer's
-    (`hip.DenseArgs`, None when the block runs the two launches)."""
-
-
 # How a block's layers run: "conv" conv1 + conv2 per layer (d8s_conv1, d8s_conv2); "chain" conv1 of
 # layer 0, then conv2 of each layer with conv1 of the next in one launch (d8s_conv2_conv1), conv2 of the
 # last layer (L + 1 launches; the bottleneck alternates between two buffers); "tile" one fused launch per
@@ -566,39 +565,27 @@ class Layer(collections.namedtuple("Layer", "c1 c2 dense")):
 BLOCK_KINDS = ("conv", "chain", "tile", "img", "parts")
 IMG_MAX_PX = 256                # d8s_dense_block: pixels per image
 IMG_MAX_GROUPS = 64             # and groups read by the last layer
-LDS_BYTES = 160 * 1024
-PARTS_TABLES = 1792             # d8s_dense_block_parts: per-layer tables besides the prologue's
+# the reference's fused kinds (`src/knee/dense8s.py:174-176`) as this runner's: its whole-block kinds
+# ("img3", "band2", "slide", "slide2": one image per thread block) are "img"; "tile" is "tile"
+REFERENCE_KINDS = {"img3": "img", "band2": "img", "slide": "img", "slide2": "img", "tile": "tile"}
 
 
-def parts_static_lds(pt: int) -> int:
-    """Fixed LDS bytes of d8s_dense_block_parts with pt pixel tiles per band: conv2 weights, two
-    prologue chunks, partial sums."""
-    cg = 4 if pt == 8 else 8
-    s2 = 1 if pt == 8 else 2 if pt == 4 else 4
-    nred = 4 * 1024 if pt == 1 else max(1, (s2 - 1) * pt * 1024)
-    return 36864 + 2 * cg * pt * 1024 + 4 * nred + 16
+def block_groups(b: dict) -> int:
+    """Store groups the last layer of block `b` (meta) reads."""
+    return b["c0"] // GROUP + b["L"] - 1
 
 
 def img_fits(b: dict) -> bool:
     """Whether block `b` (meta) fits d8s_dense_block."""
-    return b["h"] * b["w"] <= IMG_MAX_PX and b["c0"] // GROUP + b["L"] - 1 <= IMG_MAX_GROUPS
+    return b["h"] * b["w"] <= IMG_MAX_PX and block_groups(b) <= IMG_MAX_GROUPS
 
 
 def parts_options(b: dict) -> list[int]:
-    """Band counts d8s_dense_block_parts can split block `b`'s images into (increasing)."""
-    groups = b["c0"] // GROUP + b["L"] - 1
-    if groups > IMG_MAX_GROUPS:
-        return []
-    out = []
-    for k in range(1, b["h"] + 1):
-        r = b["h"] // k
-        if b["h"] % k or r * b["w"] not in hip.PARTS_PIXELS:
-            continue
-        lds = (r + 2) * (b["w"] + 2) * 128 + PARTS_TABLES + groups * 128 + parts_static_lds(r * b["w"] // 32)
-        if lds > LDS_BYTES:
-            continue
-        out.append(k)
-    return out
+    """Band counts d8s_dense_block_parts can split block `b`'s images into (increasing): the library's
+    own shape and LDS check (`d8s_parts_supported`)."""
+    lib = hip.library()
+    g = block_groups(b)
+    return [k for k in range(1, b["h"] + 1) if lib.d8s_parts_supported(b["h"], b["w"], g, k)]
 
 
 def parts_for(b: dict, n: int, cus: int = 256) -> int | None:
@@ -616,7 +603,7 @@ def chain_fits(b: dict) -> bool:
     """Whether block `b` (meta) runs d8s_conv2_conv1: a map width it takes, whole 128-pixel tiles, at
     least two layers and the last layer's conv1 within its group limit."""
     return (b["w"] in hip.C21_WIDTHS and (b["h"] * b["w"]) % 128 == 0 and b["L"] >= 2
-            and b["c0"] // GROUP + b["L"] - 1 <= hip.C21_MAX_GROUPS)
+            and block_groups(b) <= hip.C21_MAX_GROUPS)
 
 
 BAND_W = 128                    # d8s_dense runs its band form, faster than two launches, at this width
@@ -625,7 +612,7 @@ BAND_MAX_GROUPS = 16            # (the conv1 weights of the layer in LDS)
 
 def band_fits(b: dict) -> bool:
     """Whether every layer of block `b` (meta) runs d8s_dense's band form at its best width."""
-    return b["w"] == BAND_W and b["c0"] // GROUP + b["L"] - 1 <= BAND_MAX_GROUPS
+    return b["w"] == BAND_W and block_groups(b) <= BAND_MAX_GROUPS
 
 
 def default_kind(b: dict, n: int, cus: int = 256) -> str:
@@ -652,34 +639,71 @@ def default_kind(b: dict, n: int, cus: int = 256) -> str:
     return "conv"
 
 
+def valid_kind(b: dict, bi: int, kind, n: int, cus: int = 256) -> str:
+    """`kind` for block `b` (meta, index bi) at n images per pass, checked and normalised ("parts" ->
+    "parts:K"); ValueError if the block cannot run it."""
+    name = _kind_name(kind)
+    if name not in BLOCK_KINDS:
+        raise ValueError(f"block kind {kind!r}: expected one of {BLOCK_KINDS}")
+    if name == "img" and not img_fits(b):
+        raise ValueError(f"block {bi} does not fit the whole-block kernel")
+    if name == "chain" and not chain_fits(b):
+        raise ValueError(f"block {bi} ({b['h']} x {b['w']}, {b['L']} layers) does not run chained "
+                         f"conv2 + conv1 launches (widths {hip.C21_WIDTHS}, H * W a multiple of 128)")
+    if name == "parts":
+        k = int(str(kind).split(":", 1)[1]) if ":" in str(kind) else parts_for(b, n, cus)
+        if k is None or k not in parts_options(b):
+            raise ValueError(f"block {bi} ({b['h']} x {b['w']}, {b['L']} layers) does not split into "
+                             f"{k} bands (options {parts_options(b)})")
+        return f"parts:{k}"
+    return name
+
+
+def recorded_kind(b: dict, bi: int, n: int, cus: int = 256) -> str | None:
+    """The kind a package records for block `b` (meta field "fused", as the reference's packages carry
+    their tuned choice, `kaggle/int8_pack/pack_dense8s.py:141-147`), or None if it records none.  This
+    runner's own kinds are checked (ValueError if the block cannot run them); the reference's kinds
+    map onto this runner's (`REFERENCE_KINDS`), and a whole-block kind whose block does not fit one
+    workgroup per image falls back to the default."""
+    rec = b.get("fused")
+    if not rec:
+        return None
+    if rec in REFERENCE_KINDS:
+        mapped = REFERENCE_KINDS[rec]
+        return mapped if mapped != "img" or img_fits(b) else None
+    return valid_kind(b, bi, rec, n, cus)
+
+
 def fused_blocks(meta: dict, fused=None, cus: int = 256) -> dict:
-    """{block: kind} for every block.  `fused` None -> the default (`default_kind`); a dict {block:
-    kind} (other blocks "conv"); an iterable of blocks -> "tile" for those."""
-    nb = len(meta["blocks"])
+    """{block: kind} for every block.  `fused` None -> what the package records per block
+    (`recorded_kind`), else the default (`default_kind`); a dict {block: kind} (other blocks "conv");
+    an iterable of blocks -> "tile" for those."""
+    nb, n = len(meta["blocks"]), int(meta["n"])
     if fused is None:
-        return {bi: default_kind(b, int(meta["n"]), cus) for bi, b in enumerate(meta["blocks"])}
+        out = {}
+        for bi, b in enumerate(meta["blocks"]):
+            rec = recorded_kind(b, bi, n, cus)
+            out[bi] = rec if rec is not None else default_kind(b, n, cus)
+        return out
     req = dict(fused) if isinstance(fused, dict) else {int(b): "tile" for b in fused}
     out = {bi: "conv" for bi in range(nb)}
     for bi, kind in req.items():
         bi = int(bi)
         if not 0 <= bi < nb:
             raise ValueError(f"fused block {bi}: the encoder has blocks 0..{nb - 1}")
-        if _kind_name(kind) not in BLOCK_KINDS:
-            raise ValueError(f"block kind {kind!r}: expected one of {BLOCK_KINDS}")
-        if kind == "img" and not img_fits(meta["blocks"][bi]):
-            raise ValueError(f"block {bi} does not fit the whole-block kernel")
-        if kind == "chain" and not chain_fits(meta["blocks"][bi]):
-            b = meta["blocks"][bi]
-            raise ValueError(f"block {bi} ({b['h']} x {b['w']}, {b['L']} layers) does not run chained "
-                             f"conv2 + conv1 launches (widths {hip.C21_WIDTHS}, H * W a multiple of 128)")
-        if _kind_name(kind) == "parts":
-            b = meta["blocks"][bi]
-            k = int(kind.split(":", 1)[1]) if ":" in str(kind) else parts_for(b, int(meta["n"]), cus)
-            if k is None or k not in parts_options(b):
-                raise ValueError(f"block {bi} ({b['h']} x {b['w']}, {b['L']} layers) does not split into "
-                                 f"{k} bands (options {parts_options(b)})")
-            kind = f"parts:{k}"
-        out[bi] = kind
+        out[bi] = valid_kind(meta["blocks"][bi], bi, kind, n, cus)
+    return out
+
+
+def kind_options(b: dict, n: int) -> list[str]:
+    """Every kind block `b` (meta) can run at n images per pass (what `Dense8SEncoder.tune_kinds` times)."""
+    out = ["conv"]
+    if chain_fits(b):
+        out.append("chain")
+    out.append("tile")              # d8s_dense takes any map (its band form at 64 and 128 wide)
+    if img_fits(b):
+        out.append("img")
+    out += [f"parts:{k}" for k in parts_options(b)]
     return out
 
 
@@ -695,149 +719,132 @@ def _ptr(t: torch.Tensor | None) -> int:
     return 0 if t is None else int(t.data_ptr())
 
 
-class Dense8SEncoder:
-    """The INT8 encoder on GPU `dev`: `enc(x)` with x (N, 3, img, img) on that GPU, uint8 (package input
-    "u8") or fp16 ("f16"); returns (N, n_features) float32 in its own buffer (valid until the next
-    call).  Blocks of `nb` images per pass; N is padded up to a multiple of `nb`.  Interface of the
-    reference's runner (`src/knee/dense8s.py:944-1488`): own stream, `max_inflight`, `capture(n)`,
-    `graph_in_buf(n)`, `nb`, `graphs`, `calls`, `load_s`, `in_dtype`, `in_shape`, `stream`, `out`.
-    `__call__(x, flip=True)` encodes the horizontally mirrored images; `flip="tta"` returns (2N, C): the N
-    images, then the same images mirrored (flip TTA fused in the stem: no mirrored copy in memory).
-    """
+class PartsWaitError(hip.D8sError):
+    """A banded whole-block launch (d8s_dense_block_parts) had bounded waits that ran out: the features
+    of the passes since the last check were written as NaN.  The runner has cleared the error words."""
 
-    def __init__(self, pack: dict, dev: int, n_total: int, max_inflight: int | None = None,
-                 fused=None) -> None:
-        t0 = time.perf_counter()
-        meta = pack["meta"]
-        validate_meta(meta)
-        self.meta, self.dev = meta, int(dev)
-        self.fused = fused_blocks(meta, fused, _cu_count(int(dev)))
-        self.nb = int(meta["n"])
-        self.n_out = -(-int(n_total) // self.nb) * self.nb
-        self.max_inflight = max_inflight
-        self.inflight: collections.deque = collections.deque()
-        self.graphs: dict = {}
-        self.calls = {"graph": 0, "plain": 0}
-        self._pad: torch.Tensor | None = None
-        self.lib = hip.library()
-        self.library_version = hip.version()
-        self.pack_sha = meta.get("kernels_sha")
-        inp = meta.get("input", {"kind": "f16"})
-        self.in_kind = hip.IN_U8 if inp.get("kind", "f16") == "u8" else hip.IN_F16
-        self.in_dtype = torch.uint8 if self.in_kind == hip.IN_U8 else torch.float16
-        self.in_shape = (self.nb, int(meta["in_ch"]), int(meta["img"]), int(meta["img"]))
-        missing = [k for k in self._needed_tables() if k not in pack["par"]]
-        if missing:
-            raise ValueError(f"package tables missing: {missing[:4]}{'...' if len(missing) > 4 else ''}")
-        d = f"cuda:{self.dev}"
-        with torch.cuda.device(self.dev):
-            self.stream = torch.cuda.Stream(self.dev)
-            self._buffers(pack, d)
-            self.out = torch.empty((self.n_out, meta["n_features"]), dtype=torch.float32, device=d)
-        self.load_s = time.perf_counter() - t0
 
-    # -- initialisation --
-    def _buffers(self, pack: dict, d: str) -> None:
-        meta, n = self.meta, self.nb
-        blocks = meta["blocks"]
-        par = dict(pack["par"])
-        par.update(derived_params(meta, par))
-        # two alternating arenas: block b reads arena b % 2, its transition writes the other one
-        sizes, lay = [0, 0], []
-        for bi, b in enumerate(blocks):
-            hw = b["h"] * b["w"]
-            in0 = n * (b["c0"] // GROUP) * hw * GROUP
-            seg = b["L"] * n * hw * GROUP
-            lay.append((bi % 2, in0))
-            sizes[bi % 2] = max(sizes[bi % 2], in0 + seg)
-        self.arenas = [torch.empty(max(s, 16), dtype=torch.int8, device=d) for s in sizes]
-        self.arena_mb = round(sum(sizes) / 2**20, 1)
-        self.in0 = [self.arenas[a].data_ptr() for a, _ in lay]
-        self.seg = [self.arenas[a].data_ptr() + in0 for a, in0 in lay]
-        hw_max = max(b["h"] * b["w"] for b in blocks)
-        self.bott = torch.empty(n * BOTTLENECK * hw_max, dtype=torch.uint8, device=d)
-        # "chain" blocks: conv2 of a layer reads one bottleneck while conv1 of the next writes the other
-        hw_chain = [b["h"] * b["w"] for bi, b in enumerate(blocks) if self.fused[bi] == "chain"]
-        self.bott2 = (torch.empty(n * BOTTLENECK * max(hw_chain), dtype=torch.uint8, device=d)
-                      if hw_chain else None)
-        dev = torch.device(d)
-        # only the tables the kernels read go to the device (a reference package also carries the
-        # tables of its TensorRT and int8-stem paths)
-        used = set(needed_tables(meta)) | set(derived_params(meta, {}, names_only=True))
-        self.par = {k: torch.from_numpy(np.ascontiguousarray(v)).to(dev)
-                    for k, v in par.items() if k in used}
-        self.out_dev = dev
-        self._build_launches()
+class Regions:
+    """One device allocation carved into aligned named regions: sizes are reserved first (byte offsets
+    known before anything is allocated), then one tensor holds them all."""
 
-    def _needed_tables(self) -> list[str]:
-        return needed_tables(self.meta)
+    ALIGN = 256
 
-    def _build_launches(self) -> None:
-        """Argument structs of every launch of a pass (`src/knee/dense8s.py:1103-1152`)."""
-        n, P = self.nb, lambda k: _ptr(self.par[k])  # noqa: E731
-        meta = self.meta
-        self.plan_l: list = []
-        self.block_args: dict = {}                   # "img" / "parts" blocks: their launch
-        self._tables: dict = {}                      # and their device layer tables
-        self._sync: dict = {}                        # "parts" blocks: sync words and exchange rows
-        for bi, b in enumerate(meta["blocks"]):
-            hw, g0 = b["h"] * b["w"], b["c0"] // GROUP
-            layers = []
-            for li in range(b["L"]):
-                bott = _ptr(self._bott_of(bi, li))
-                c1 = hip.GemmArgs(self.in0[bi], self.seg[bi], P(f"L{bi}_{li}_w1"),
-                                  P(f"L{bi}_{li}_abh"), P(f"L{bi}_{li}_gdu"), P(f"L{bi}_{li}_w1sum"),
-                                  bott, g0, g0 + li, n, hw, b["w"], n * hw, BOTTLENECK, 0)
-                c2 = hip.Conv2Args(bott, P(f"L{bi}_{li}_w2k"), P(f"L{bi}_{li}_c2u"),
-                                   P(f"L{bi}_{li}_w2sum"), self.seg[bi] + li * n * hw * GROUP,
-                                   n, b["h"], b["w"], 0)
-                dn = None
-                if self.fused[bi] == "tile":
-                    dn = hip.DenseArgs(self.in0[bi], self.seg[bi], P(f"L{bi}_{li}_w1"),
-                                       P(f"L{bi}_{li}_abh"), P(f"L{bi}_{li}_gdu"), P(f"L{bi}_{li}_w1sum"),
-                                       P(f"L{bi}_{li}_w2k"), P(f"L{bi}_{li}_c2u"), P(f"L{bi}_{li}_w2sum"),
-                                       self.seg[bi] + li * n * hw * GROUP, g0, g0 + li, n, b["h"],
-                                       b["w"], 0)
-                layers.append(Layer(c1, c2, dn))
-            kind = _kind_name(self.fused[bi])
-            if kind in ("img", "parts"):
-                lps = (hip.LayerP * b["L"])()
-                for li in range(b["L"]):
-                    lps[li] = hip.LayerP(P(f"L{bi}_{li}_w1"), P(f"L{bi}_{li}_abh"), P(f"L{bi}_{li}_gdu"),
-                                         P(f"L{bi}_{li}_w1sum"), P(f"L{bi}_{li}_w2k"), P(f"L{bi}_{li}_c2u"),
-                                         P(f"L{bi}_{li}_w2sum"))
-                table = torch.frombuffer(bytearray(bytes(lps)), dtype=torch.uint8).to(self.out_dev)
-                self._tables[bi] = table
-                if kind == "img":
-                    self.block_args[bi] = hip.BlockArgs(self.in0[bi], self.seg[bi], _ptr(table), n,
-                                                        b["h"], b["w"], g0, b["L"], 0)
-                else:
-                    k = int(self.fused[bi].split(":", 1)[1])
-                    sync = torch.zeros(hip.parts_sync_words(n * k), dtype=torch.int32, device=self.out_dev)
-                    xchg = torch.zeros(hip.parts_xchg_bytes(n * k, b["w"]), dtype=torch.uint8,
-                                       device=self.out_dev)
-                    self._sync[bi] = (sync, xchg)
-                    self.block_args[bi] = hip.PartsArgs(self.in0[bi], self.seg[bi], _ptr(table),
-                                                        _ptr(sync), _ptr(xchg), n, b["h"], b["w"], g0,
-                                                        b["L"], k)
-            trans = None
-            if b["trans"]:
-                cout = (b["c0"] + GROWTH * b["L"]) // 2
-                trans = hip.GemmArgs(self.in0[bi], self.seg[bi], P(f"T{bi}_w"), P(f"T{bi}_abh"),
-                                     P(f"T{bi}_gdf"), P(f"T{bi}_wsum"), self.in0[bi + 1], g0,
-                                     g0 + b["L"], n, hw, b["w"], n * hw, cout, cout // GROUP)
-            self.plan_l.append((layers, trans))
-        img = int(meta["img"])
-        self.stem_args = hip.StemArgs(0, P("S_lut"), P("S_w16"), P("S_bias"), P("S_inv"),
-                                      self.in0[0], n, img, img, self.in_kind, 0, 0)
+    def __init__(self) -> None:
+        self.spans: dict[str, tuple[int, int]] = {}
+        self.size = 0
+        self.mem: torch.Tensor | None = None
 
-    def _bott_of(self, bi: int, li: int) -> torch.Tensor:
-        """The bottleneck buffer of layer li of block bi (in "chain" blocks odd layers use the second)."""
-        return self.bott2 if self.fused[bi] == "chain" and li % 2 else self.bott
+    def reserve(self, name: str, nbytes: int) -> None:
+        start = -(-self.size // self.ALIGN) * self.ALIGN
+        self.spans[name] = (start, int(nbytes))
+        self.size = start + int(nbytes)
 
-    # -- one pass --
-    @staticmethod
-    def _mode(flip) -> int:
+    def allocate(self, device) -> None:
+        self.mem = torch.empty(max(self.size, self.ALIGN), dtype=torch.uint8, device=device)
+
+    def __contains__(self, name: str) -> bool:
+        return name in self.spans
+
+    def addr(self, name: str, offset: int = 0) -> int:
+        return self.mem.data_ptr() + self.spans[name][0] + offset
+
+    def view(self, name: str, offset: int = 0, nbytes: int | None = None) -> torch.Tensor:
+        start, size = self.spans[name]
+        nbytes = size - offset if nbytes is None else nbytes
+        return self.mem[start + offset:start + offset + nbytes]
+
+
+@dataclass
+class Step:
+    """One launch of a pass.  `family` names the kernel family (stem, conv1, conv2, chain, dense,
+    block, trans, final), `block` / `layer` where it sits (layer -1: the whole block or none), `makes`
+    the trace keys whose contents it completes ((b, j): store segment j of block b, ("bott", b, l):
+    layer l's bottleneck), `entry` the C entry point and `args` its argument struct (None for the
+    stem's and the final's, whose pointers change per pass)."""
+    family: str
+    block: int
+    layer: int
+    makes: tuple
+    entry: str
+    args: object = None
+
+    def tag(self) -> str:
+        return self.family if self.family in ("stem", "final") else f"{self.family}_{self.block}"
+
+    def label(self) -> str:
+        short = {"conv1": "c1", "conv2": "c2", "chain": "cc", "dense": "dn"}
+        if self.family in short:
+            return f"{short[self.family]} b{self.block}l{self.layer}"
+        return {"block": f"blk b{self.block}", "trans": f"t{self.block}"}.get(self.family, self.family)
+
+
+class InflightGate:
+    """At most `limit` passes in flight on a stream (None: no limit): `admit()` blocks the host on the
+    oldest pass's event while the limit is reached, `done(stream)` marks the end of a pass (the role of
+    the reference's `max_inflight`, `src/knee/dense8s.py:1400-1408`)."""
+
+    def __init__(self, limit: int | None) -> None:
+        self.limit = limit
+        self.events: collections.deque = collections.deque()
+
+    def admit(self) -> None:
+        while self.limit and len(self.events) >= self.limit:
+            self.events.popleft().synchronize()
+
+    def done(self, stream) -> None:
+        if self.limit:
+            ev = torch.cuda.Event(blocking=True)
+            ev.record(stream)
+            self.events.append(ev)
+
+    def clear(self) -> None:
+        self.events.clear()
+
+
+class GraphBook:
+    """Captured graphs by flip mode: for each mode, batch size -> (graphs, shared input).  A batch of n
+    images replays the graphs captured for n, else the first ceil(n / per-pass) graphs of the smallest
+    capture that covers them (a short batch: the rows past n hold old images, whose outputs are
+    computed and discarded)."""
+
+    def __init__(self) -> None:
+        self.by_mode: dict[int, dict[int, tuple]] = {}
+
+    def add(self, n: int, mode: int, graphs: list, shared: GraphInput) -> None:
+        self.by_mode.setdefault(mode, {})[n] = (graphs, shared)
+
+    def find(self, n: int, mode: int, per_pass: int):
+        book = self.by_mode.get(mode, {})
+        if n in book:
+            return book[n]
+        passes = -(-n // per_pass)
+        covering = [m for m in book if m >= passes * per_pass]
+        if not covering:
+            return None
+        graphs, shared = book[min(covering)]
+        return graphs[:passes], shared
+
+    def items(self):
+        return [((n, mode), v) for mode, book in self.by_mode.items() for n, v in book.items()]
+
+    def __len__(self) -> int:
+        return sum(len(b) for b in self.by_mode.values())
+
+    def __bool__(self) -> bool:
+        return len(self) > 0
+
+    def clear(self) -> None:
+        self.by_mode.clear()
+
+
+class _PassRunner:
+    """What the runner and the pair share: a batch as passes of `nb` encoded images on one launch
+    stream, eagerly or by replaying captured graphs, with the input shared between the runners of a GPU
+    (`GraphInput`).  Subclasses give `_launch_pass(x_ptr, index, mode)` (the launches of pass `index`
+    reading x_ptr), `_accept(x, mode)` (input checks), `_outputs(n, mode)` and `_mark_written()`."""
+
+    def _mode(self, flip) -> int:
         """flip -> stem mode: False 0 (as is), True 1 (every image mirrored), "tta" 2 (flip-TTA pairs: a
         pass encodes nb/2 input images, then the same images mirrored)."""
         if isinstance(flip, str):
@@ -850,116 +857,337 @@ class Dense8SEncoder:
         """Input images one pass of `nb` encoded images consumes."""
         return self.nb // 2 if mode == 2 else self.nb
 
-    def _stem(self, x_ptr: int, mode: int, st: int) -> None:
-        self.stem_args.x = x_ptr
-        self.stem_args.flip = mode
-        hip.check(self.lib.d8s_stem(ctypes.byref(self.stem_args), st), "d8s_stem")
+    def _staged(self, chunk: torch.Tensor, mode: int) -> int:
+        """Address of one pass worth of input: the chunk itself when it is whole and 16-byte aligned (the
+        stem reads uint8 rows as dwords), else a copy at the head of the staging buffer (whose other rows
+        hold old images: their outputs are computed and discarded)."""
+        if chunk.shape[0] == self._per_pass(mode) and chunk.data_ptr() % 16 == 0:
+            return chunk.data_ptr()
+        if self._staging is None:
+            self._staging = torch.zeros(self.in_shape, dtype=self.in_dtype, device=f"cuda:{self.dev}")
+        self._staging[:chunk.shape[0]].copy_(chunk)
+        return self._staging.data_ptr()
 
-    def _final(self, bi: int, f_ptr: int, st: int, n: int | None = None) -> None:
-        b = self.meta["blocks"][bi]
-        n = self.nb if n is None else n
-        hip.check(self.lib.d8s_final(self.in0[bi], b["c0"] // GROUP, self.seg[bi], n,
-                                     b["h"] * b["w"], _ptr(self.par["F_ab"]), f_ptr,
-                                     self.meta["n_features"], st), "d8s_final")
+    def _run_eager(self, x: torch.Tensor, mode: int) -> None:
+        per = self._per_pass(mode)
+        for index in range(-(-x.shape[0] // per)):
+            self._gate.admit()
+            self._launch_pass(self._staged(x[index * per:(index + 1) * per], mode), index, mode)
+            self._gate.done(self.stream)
 
-    def _conv1(self, c1, st: int) -> None:
-        hip.check(self.lib.d8s_conv1(ctypes.byref(c1), st), "d8s_conv1")
+    def _run_graphs(self, x: torch.Tensor, graphs: list, shared: GraphInput) -> None:
+        n = x.shape[0]
+        own = shared.buf[:n]
+        if x.data_ptr() == own.data_ptr() and x.shape == own.shape and x.stride() == own.stride():
+            shared.forget()                   # the caller wrote the graph input in place
+        elif shared.load(x, n, self.stream):
+            self.calls["copy"] = self.calls.get("copy", 0) + 1
+        for g in graphs:
+            self._gate.admit()
+            g.replay()
+            self._gate.done(self.stream)
+        shared.read_by(self, self.stream)
 
-    def _conv2(self, c2, st: int) -> None:
-        hip.check(self.lib.d8s_conv2(ctypes.byref(c2), st), "d8s_conv2")
-
-    def _chain(self, c2, c1, st: int) -> None:
-        hip.check(self.lib.d8s_conv2_conv1(ctypes.byref(c2), ctypes.byref(c1), st), "d8s_conv2_conv1")
-
-    def _block(self, bi: int, st: int) -> None:
-        args = self.block_args[bi]
-        if isinstance(args, hip.PartsArgs):
-            hip.check(self.lib.d8s_dense_block_parts(ctypes.byref(args), st), "d8s_dense_block_parts")
-        else:
-            hip.check(self.lib.d8s_dense_block(ctypes.byref(args), st), "d8s_dense_block")
-
-    def sync_errors(self, clear: bool = True) -> int:
-        """Waits that ran out in the "parts" blocks' launches so far (0: every result valid); reads the
-        sync words on the runner's stream (a synchronisation) and clears the count when `clear`."""
-        total = 0
+    def capture(self, n: int, flip=False) -> float:
+        """One HIP graph per pass over a batch of `n` input images (the reference's `capture`,
+        `src/knee/dense8s.py:1410-1433`), recorded on the launch stream after one eager pass (which does
+        any lazy set-up outside the capture); returns the seconds spent."""
+        mode = self._mode(flip)
+        per = self._per_pass(mode)
+        passes = -(-n // per)
+        if passes * self.nb > self.n_out:
+            raise ValueError(f"graph for {n} images: the encoder does {self.nb} per pass, "
+                             f"the output holds {self.n_out}")
+        t0 = time.perf_counter()
         with torch.cuda.device(self.dev):
+            shared = graph_input(self.dev, (passes * per, *self.in_shape[1:]), self.in_dtype)
+            shared.forget()
+            self._join(torch.cuda.current_stream(self.dev))
+            with torch.cuda.stream(self.stream):
+                self._launch_pass(shared.buf.data_ptr(), 0, mode)
             self.stream.synchronize()
-            for sync, _ in self._sync.values():
-                total += int(sync[2].item())
-                if clear:
-                    sync[2].zero_()
+            self._gate.clear()
+            graphs = []
+            for index in range(passes):
+                g = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(g, stream=self.stream, capture_error_mode="thread_local"):
+                    self._launch_pass(shared.buf[index * per].data_ptr(), index, mode)
+                graphs.append(g)
             self.stream.synchronize()
-        return total
+        self.graphs.add(passes * per, mode, graphs, shared)
+        return time.perf_counter() - t0
 
-    def _dense(self, d, st: int) -> None:
-        hip.check(self.lib.d8s_dense(ctypes.byref(d), st), "d8s_dense")
+    def graph_in_buf(self, n: int, flip=False) -> torch.Tensor | None:
+        """The static input buffer `[:n]` of the graphs that a batch of `n` images replays, or None."""
+        mode = self._mode(flip)
+        hit = self.graphs.find(n, mode, self._per_pass(mode))
+        return None if hit is None else hit[1].buf[:n]
 
-    def _trans(self, t, st: int) -> None:
-        hip.check(self.lib.d8s_transition(ctypes.byref(t), st), "d8s_transition")
+    def _join(self, caller) -> None:
+        self.stream.wait_stream(caller)
 
-    def _pass(self, x_ptr: int, f_ptr: int, mode: int = 0, events: list | None = None) -> None:
-        """The launch sequence of one pass (`src/knee/dense8s.py:1354-1385`): stem, then per block
-        conv1 / conv2 of every layer, the transition or the final features."""
-        st = self.stream.cuda_stream
-        mark = ((lambda tag: events.append((tag, _record(self.stream)))) if events is not None
-                else (lambda tag: None))
-        mark("start")
-        self._stem(x_ptr, mode, st)
-        mark("stem")
-        for bi, (layers, trans) in enumerate(self.plan_l):
-            if bi in self.block_args:
-                self._block(bi, st)
-                mark(f"block_{bi}")
-                layers = ()
-            if self.fused[bi] == "chain":
-                self._conv1(layers[0].c1, st)
-                mark(f"conv1_{bi}")
-                for La, Lb in zip(layers, layers[1:]):
-                    self._chain(La.c2, Lb.c1, st)
-                    mark(f"chain_{bi}")
-                self._conv2(layers[-1].c2, st)
-                mark(f"conv2_{bi}")
-                layers = ()
-            for L in layers:
-                if L.dense is not None:
-                    self._dense(L.dense, st)
-                    mark(f"dense_{bi}")
-                    continue
-                self._conv1(L.c1, st)
-                mark(f"conv1_{bi}")
-                self._conv2(L.c2, st)
-                mark(f"conv2_{bi}")
-            if trans is not None:
-                self._trans(trans, st)
-                mark(f"trans{bi}")
+    def _encode(self, x: torch.Tensor, flip):
+        """Encodes x on the launch stream, ordered after the caller's current stream and before what the
+        caller enqueues next; returns `_outputs`."""
+        mode = self._mode(flip)
+        self._accept(x, mode)
+        caller = torch.cuda.current_stream(self.dev)
+        self._join(caller)
+        with torch.cuda.device(self.dev), torch.cuda.stream(self.stream):
+            hit = self.graphs.find(x.shape[0], mode, self._per_pass(mode))
+            if hit is None:
+                self._run_eager(x.contiguous(), mode)
+                self.calls["plain"] += 1
             else:
-                self._final(bi, f_ptr, st)
-                mark("final")
+                self._run_graphs(x, *hit)
+                self.calls["graph"] += 1
+            res = self._outputs(x.shape[0], mode)
+        self._mark_written()
+        caller.wait_stream(self.stream)
+        return res
 
-    def _padded(self, chunk: torch.Tensor, mode: int) -> torch.Tensor:
-        """One pass worth of input images: `chunk` itself if full (copied if its data is not 16-byte
-        aligned: the stem reads uint8 rows as dwords), else copied to the head of a buffer (the rest
-        holds old images, whose outputs are computed and discarded)."""
-        if chunk.shape[0] == self._per_pass(mode):
-            return chunk if chunk.data_ptr() % 16 == 0 else chunk.clone()
-        if self._pad is None:
-            self._pad = torch.zeros((self.nb, *chunk.shape[1:]), dtype=self.in_dtype,
-                                    device=f"cuda:{self.dev}")
-        self._pad[:chunk.shape[0]].copy_(chunk)
-        return self._pad
 
-    def _enqueue(self, xf: torch.Tensor, mode: int) -> None:
-        for i, chunk in enumerate(xf.split(self._per_pass(mode))):
-            if self.max_inflight:
-                while len(self.inflight) >= self.max_inflight:
-                    self.inflight.popleft().synchronize()
-            self._pass(self._padded(chunk, mode).data_ptr(), self.out[i * self.nb].data_ptr(), mode)
-            if self.max_inflight:
-                ev = torch.cuda.Event(blocking=True)
-                ev.record(self.stream)
-                self.inflight.append(ev)
+class Dense8SEncoder(_PassRunner):
+    """The INT8 encoder on GPU `dev`: `enc(x)` with x (N, 3, img, img) on that GPU, uint8 (package input
+    "u8") or fp16 ("f16"); returns (N, n_features) float32 in its own buffer (valid until the next
+    call).  Blocks of `nb` images per pass; N is padded up to a multiple of `nb`.  Interface of the
+    reference's runner (`src/knee/dense8s.py:944-1488`): own stream, `max_inflight`, `capture(n)`,
+    `graph_in_buf(n)`, `nb`, `graphs`, `calls`, `load_s`, `in_dtype`, `in_shape`, `stream`, `out`.
+    `__call__(x, flip=True)` encodes the horizontally mirrored images; `flip="tta"` returns (2N, C): the N
+    images, then the same images mirrored (flip TTA fused in the stem: no mirrored copy in memory).
 
-    def _check_input(self, x: torch.Tensor, mode: int = 0) -> None:
+    A pass is a program of `Step`s compiled once from the package and the block kinds (`fused`,
+    `fused_blocks`); running, tracing, profiling and timing a pass all walk that one program.
+    """
+
+    def __init__(self, pack: dict, dev: int, n_total: int, max_inflight: int | None = None,
+                 fused=None) -> None:
+        t0 = time.perf_counter()
+        meta = pack["meta"]
+        validate_meta(meta)
+        missing = [k for k in needed_tables(meta) if k not in pack["par"]]
+        if missing:
+            raise ValueError(f"package tables missing: {missing[:4]}{'...' if len(missing) > 4 else ''}")
+        self.meta, self.dev = meta, int(dev)
+        self.lib = hip.library()
+        self.library_version = hip.version()
+        self.pack_sha = meta.get("kernels_sha")
+        self.nb = int(meta["n"])
+        self.fused = fused_blocks(meta, fused, _cu_count(self.dev))
+        self.n_out = -(-int(n_total) // self.nb) * self.nb
+        self.max_inflight = max_inflight
+        self._gate = InflightGate(max_inflight)
+        self.graphs = GraphBook()
+        self.calls = {"graph": 0, "plain": 0}
+        inp = meta.get("input", {"kind": "f16"})
+        self.in_kind = hip.IN_U8 if inp.get("kind", "f16") == "u8" else hip.IN_F16
+        self.in_dtype = torch.uint8 if self.in_kind == hip.IN_U8 else torch.float16
+        self.in_shape = (self.nb, int(meta["in_ch"]), int(meta["img"]), int(meta["img"]))
+        self._staging: torch.Tensor | None = None
+        self._extra: dict = {}                   # per (block, kind): buffers a kind needs beyond the store
+        with torch.cuda.device(self.dev):
+            self.stream = torch.cuda.Stream(self.dev)
+            self._upload(pack)
+            self._lay_out()
+            self.out = torch.empty((self.n_out, meta["n_features"]), dtype=torch.float32,
+                                   device=f"cuda:{self.dev}")
+            self._compile()
+        self.load_s = time.perf_counter() - t0
+
+    # -- set-up --
+    def _upload(self, pack: dict) -> None:
+        """The tables the kernels read, on the device (a reference package also carries the tables of
+        its TensorRT and int8-stem paths, which stay behind), with this build's derived ones."""
+        tables = dict(pack["par"])
+        tables.update(derived_params(self.meta, tables))
+        wanted = set(needed_tables(self.meta)) | set(derived_params(self.meta, {}, names_only=True))
+        dev = torch.device(f"cuda:{self.dev}")
+        self.par = {k: torch.from_numpy(np.ascontiguousarray(v)).to(dev)
+                    for k, v in tables.items() if k in wanted}
+
+    def _lay_out(self) -> None:
+        """Device memory of a pass: the block stores in two regions used in turn (block b in region
+        b % 2: its transition writes the next block's input into the other one), the planar bottleneck
+        [4][nb * HW][32] of the largest map, the banded blocks' synchronisation words."""
+        n = self.nb
+        self.mem = Regions()
+        need = [0, 0]
+        for bi, b in enumerate(self.meta["blocks"]):
+            need[bi % 2] = max(need[bi % 2], self._in0_bytes(bi) + b["L"] * self._slot_bytes(bi))
+        self.mem.reserve("store0", need[0])
+        self.mem.reserve("store1", need[1])
+        self.mem.reserve("bott", n * BOTTLENECK * max(b["h"] * b["w"] for b in self.meta["blocks"]))
+        self.mem.reserve("sync", 4 * hip.parts_sync_words(0))
+        self.mem.allocate(f"cuda:{self.dev}")
+        self.mem.view("sync").zero_()
+        self.arena_mb = round(sum(need) / 2**20, 1)
+        self.in0 = [self.mem.addr(f"store{bi % 2}") for bi in range(len(self.meta["blocks"]))]
+        self.seg = [self.mem.addr(f"store{bi % 2}", self._in0_bytes(bi))
+                    for bi in range(len(self.meta["blocks"]))]
+        self._sync = self.mem.view("sync").view(torch.int32)
+        self._report: torch.Tensor | None = None
+        self._report_dev = 0
+
+    def _in0_bytes(self, bi: int) -> int:
+        b = self.meta["blocks"][bi]
+        return self.nb * b["c0"] * b["h"] * b["w"]
+
+    def _slot_bytes(self, bi: int) -> int:
+        b = self.meta["blocks"][bi]
+        return self.nb * b["h"] * b["w"] * GROUP
+
+    def _slot(self, bi: int, li: int) -> int:
+        return self.seg[bi] + li * self._slot_bytes(bi)
+
+    def _buffer(self, key: tuple, make) -> torch.Tensor:
+        """A buffer a block kind needs (made on first use and kept)."""
+        t = self._extra.get(key)
+        if t is None:
+            t = self._extra[key] = make()
+        return t
+
+    def _bottleneck_buf(self, bi: int, li: int, kind: str) -> torch.Tensor:
+        """Layer li's bottleneck buffer: the shared one, or for a "chain" block the second buffer on odd
+        layers (conv2 of a layer reads one while conv1 of the next writes the other)."""
+        if kind == "chain" and li % 2:
+            b = self.meta["blocks"][bi]
+            size = self.nb * BOTTLENECK * b["h"] * b["w"]
+            return self._buffer(("bott2", size), lambda: torch.empty(size, dtype=torch.uint8,
+                                                                     device=f"cuda:{self.dev}"))
+        return self.mem.view("bott")
+
+    def _bottleneck(self, bi: int, li: int, kind: str) -> int:
+        return _ptr(self._bottleneck_buf(bi, li, kind))
+
+    def _layer_table(self, bi: int) -> int:
+        """Device array of block bi's `D8sLayerP` descriptors (for the whole-block kinds)."""
+        def make():
+            L = self.meta["blocks"][bi]["L"]
+            arr = (hip.LayerP * L)(*[hip.LayerP(*(self._tab(bi, li, k) for k in
+                                                  ("w1", "abh", "gdu", "w1sum", "w2k", "c2u", "w2sum")))
+                                     for li in range(L)])
+            return torch.frombuffer(bytearray(bytes(arr)), dtype=torch.uint8).to(f"cuda:{self.dev}")
+        return _ptr(self._buffer(("layers", bi), make))
+
+    def _tab(self, bi: int, li: int, name: str) -> int:
+        return _ptr(self.par[f"L{bi}_{li}_{name}"])
+
+    def _conv1_args(self, bi: int, li: int, kind: str) -> hip.GemmArgs:
+        b = self.meta["blocks"][bi]
+        hw, g0 = b["h"] * b["w"], b["c0"] // GROUP
+        return hip.GemmArgs(self.in0[bi], self.seg[bi], self._tab(bi, li, "w1"), self._tab(bi, li, "abh"),
+                            self._tab(bi, li, "gdu"), self._tab(bi, li, "w1sum"),
+                            self._bottleneck(bi, li, kind), g0, g0 + li, self.nb, hw, b["w"], self.nb * hw,
+                            BOTTLENECK, 0)
+
+    def _conv2_args(self, bi: int, li: int, kind: str) -> hip.Conv2Args:
+        b = self.meta["blocks"][bi]
+        return hip.Conv2Args(self._bottleneck(bi, li, kind), self._tab(bi, li, "w2k"), self._tab(bi, li, "c2u"),
+                             self._tab(bi, li, "w2sum"), self._slot(bi, li), self.nb, b["h"], b["w"], 0)
+
+    def block_steps(self, bi: int, kind: str) -> list[Step]:
+        """The launches of block bi's layers run as `kind`."""
+        b = self.meta["blocks"][bi]
+        L, name = b["L"], _kind_name(kind)
+        if name in ("img", "parts"):
+            g0 = b["c0"] // GROUP
+            makes = tuple((bi, j) for j in range(1, L + 1))
+            if name == "img":
+                args = hip.BlockArgs(self.in0[bi], self.seg[bi], self._layer_table(bi), self.nb,
+                                     b["h"], b["w"], g0, L, 0)
+                return [Step("block", bi, -1, makes, "d8s_dense_block", args)]
+            k = int(kind.split(":", 1)[1])
+            size = hip.parts_xchg_bytes(self.nb * k, b["w"])
+            xchg = self._buffer(("xchg", bi, k), lambda: torch.zeros(size, dtype=torch.uint8,
+                                                                      device=f"cuda:{self.dev}"))
+            args = hip.PartsArgs(self.in0[bi], self.seg[bi], self._layer_table(bi), _ptr(self._sync),
+                                 _ptr(xchg), self.nb, b["h"], b["w"], g0, L, k)
+            return [Step("block", bi, -1, makes, "d8s_dense_block_parts", args)]
+        if name == "tile":
+            steps = []
+            for li in range(L):
+                g0 = b["c0"] // GROUP
+                args = hip.DenseArgs(self.in0[bi], self.seg[bi], *(self._tab(bi, li, k) for k in
+                                     ("w1", "abh", "gdu", "w1sum", "w2k", "c2u", "w2sum")),
+                                     self._slot(bi, li), g0, g0 + li, self.nb, b["h"], b["w"], 0)
+                steps.append(Step("dense", bi, li, ((bi, li + 1),), "d8s_dense", args))
+            return steps
+        if name == "chain":
+            steps = [Step("conv1", bi, 0, (("bott", bi, 0),), "d8s_conv1", self._conv1_args(bi, 0, kind))]
+            for li in range(L - 1):
+                pair = (self._conv2_args(bi, li, kind), self._conv1_args(bi, li + 1, kind))
+                steps.append(Step("chain", bi, li, ((bi, li + 1), ("bott", bi, li + 1)), "d8s_conv2_conv1",
+                                  pair))
+            steps.append(Step("conv2", bi, L - 1, ((bi, L),), "d8s_conv2", self._conv2_args(bi, L - 1, kind)))
+            return steps
+        steps = []
+        for li in range(L):
+            steps.append(Step("conv1", bi, li, (("bott", bi, li),), "d8s_conv1", self._conv1_args(bi, li, kind)))
+            steps.append(Step("conv2", bi, li, ((bi, li + 1),), "d8s_conv2", self._conv2_args(bi, li, kind)))
+        return steps
+
+    def _compile(self) -> None:
+        """The program of one pass: the stem, each block's layers as its kind, its transition, and the
+        final features (the launch sequence of the reference's `_pass`, `src/knee/dense8s.py:1354-1385`)."""
+        img = int(self.meta["img"])
+        self.stem_args = hip.StemArgs(0, _ptr(self.par["S_lut"]), _ptr(self.par["S_w16"]),
+                                      _ptr(self.par["S_bias"]), _ptr(self.par["S_inv"]), self.in0[0],
+                                      self.nb, img, img, self.in_kind, 0, 0)
+        prog = [Step("stem", 0, -1, ((0, 0),), "d8s_stem", self.stem_args)]
+        for bi, b in enumerate(self.meta["blocks"]):
+            prog += self.block_steps(bi, self.fused[bi])
+            if b["trans"]:
+                g0, hw = b["c0"] // GROUP, b["h"] * b["w"]
+                cout = (b["c0"] + GROWTH * b["L"]) // 2
+                args = hip.GemmArgs(self.in0[bi], self.seg[bi], _ptr(self.par[f"T{bi}_w"]),
+                                    _ptr(self.par[f"T{bi}_abh"]), _ptr(self.par[f"T{bi}_gdf"]),
+                                    _ptr(self.par[f"T{bi}_wsum"]), self.in0[bi + 1], g0, g0 + b["L"], self.nb,
+                                    hw, b["w"], self.nb * hw, cout, cout // GROUP)
+                prog.append(Step("trans", bi, -1, ((bi + 1, 0),), "d8s_transition", args))
+            else:
+                prog.append(Step("final", bi, -1, (), "d8s_final"))
+        self.program = prog
+        self._checked = any(s.entry == "d8s_dense_block_parts" for s in prog)
+        if self._checked and self._report is None:
+            # a host-mapped word the final kernel copies the banded blocks' error count into
+            self._report = torch.zeros(2, dtype=torch.int32).pin_memory()
+            dptr = ctypes.c_void_p()
+            hip.check(self.lib.d8s_host_mapped(self._report.data_ptr(), ctypes.byref(dptr)), "d8s_host_mapped")
+            self._report_dev = int(dptr.value or 0)
+
+    # -- launches --
+    def _launch(self, step: Step, st: int, x_ptr: int = 0, f_ptr: int = 0, mode: int = 0) -> None:
+        lib = self.lib
+        if step.family == "stem":
+            step.args.x = x_ptr
+            step.args.flip = mode
+            rc = lib.d8s_stem(ctypes.byref(step.args), st)
+        elif step.family == "final":
+            b = self.meta["blocks"][step.block]
+            common = (self.in0[step.block], b["c0"] // GROUP, self.seg[step.block], self.nb,
+                      b["h"] * b["w"], _ptr(self.par["F_ab"]), f_ptr, self.meta["n_features"])
+            if self._checked:
+                rc = lib.d8s_final_checked(*common, _ptr(self._sync) + 8, self._report_dev, st)
+            else:
+                rc = lib.d8s_final(*common, st)
+        elif step.family == "chain":
+            rc = lib.d8s_conv2_conv1(ctypes.byref(step.args[0]), ctypes.byref(step.args[1]), st)
+        else:
+            rc = getattr(lib, step.entry)(ctypes.byref(step.args), st)
+        hip.check(rc, step.entry)
+
+    def _launch_pass(self, x_ptr: int, index: int, mode: int, after=None) -> None:
+        """The program on the runner's stream, reading x_ptr and writing the features of pass `index`;
+        `after(step)` (optional) runs after every launch."""
+        st = self.stream.cuda_stream
+        f_ptr = self.out[index * self.nb].data_ptr()
+        for step in self.program:
+            self._launch(step, st, x_ptr, f_ptr, mode)
+            if after is not None:
+                after(step)
+
+    # -- calls --
+    def _accept(self, x: torch.Tensor, mode: int) -> None:
         if x.dtype != self.in_dtype:
             raise ValueError(f"input {x.dtype}: this package takes {self.in_dtype}")
         if tuple(x.shape[1:]) != self.in_shape[1:]:
@@ -969,281 +1197,216 @@ class Dense8SEncoder:
             raise ValueError(f"input on {x.device}, encoder on cuda:{self.dev}")
         if mode == 2 and self.nb % 2:
             raise ValueError(f"flip-TTA pairs need an even images-per-pass, the package has {self.nb}")
-        k = self._per_pass(mode)
-        if -(-x.shape[0] // k) * self.nb > self.n_out:
+        if -(-x.shape[0] // self._per_pass(mode)) * self.nb > self.n_out:
             raise ValueError(f"{x.shape[0]} images: the output holds {self.n_out} encoded images")
+        self._raise_wait_errors()
 
-    def _result(self, n: int, mode: int) -> torch.Tensor:
+    def _outputs(self, n: int, mode: int) -> torch.Tensor:
         """The features of `n` input images: (n, C) views of `out`, or for flip-TTA (2n, C) with the n
-        plain images first, then the n mirrored ones."""
+        plain images first, then the n mirrored ones (pass p holds its images' plain features in rows
+        p nb .. p nb + nb/2 - 1, the mirrored ones in the next nb/2 rows)."""
         if mode != 2:
             return self.out[:n]
-        k = self.nb // 2
-        if n == k:
+        half = self.nb // 2
+        if n == half:
             return self.out[:self.nb]
-        idx = torch.arange(n, device=self.out.device)
-        rows = (idx // k) * self.nb + idx % k
-        return self.out.index_select(0, torch.cat([rows, rows + k]))
+        i = torch.arange(n, device=self.out.device)
+        plain = i + (i // half) * half
+        return self.out.index_select(0, torch.cat([plain, plain + half]))
 
-    def capture(self, n: int, flip=False) -> float:
-        """One HIP graph per pass over a batch of `n` input images (`src/knee/dense8s.py:1410-1433`);
-        returns the seconds spent."""
-        mode = self._mode(flip)
-        k = self._per_pass(mode)
-        n = -(-n // k) * k
-        if n // k * self.nb > self.out.shape[0]:
-            raise ValueError(f"graph for {n} images: the encoder does {self.nb} per pass, "
-                             f"the output holds {self.out.shape[0]}")
-        t = time.perf_counter()
-        with torch.cuda.device(self.dev):
-            shared = graph_input(self.dev, (n, *self.in_shape[1:]), self.in_dtype)
-            static_in = shared.buf
-            shared.forget()
-            with torch.cuda.stream(self.stream):
-                self.stream.wait_stream(torch.cuda.current_stream(self.dev))
-                self._enqueue(static_in[:k], mode)
-            self.stream.synchronize()
-            self.inflight.clear()
-            graphs = []
-            for i, chunk in enumerate(static_in.split(k)):
-                g = torch.cuda.CUDAGraph()
-                with torch.cuda.graph(g, stream=self.stream, capture_error_mode="thread_local"):
-                    self._pass(chunk.data_ptr(), self.out[i * self.nb].data_ptr(), mode)
-                graphs.append(g)
-            self.stream.synchronize()
-        self.graphs[(n, mode)] = (graphs, shared)
-        return time.perf_counter() - t
-
-    def _graphs_for(self, n: int, mode: int):
-        gs = self.graphs.get((n, mode))
-        if gs is None:
-            k = -(-n // self._per_pass(mode))
-            for (m_, md), (g_, s_) in sorted(self.graphs.items()):
-                if md == mode and m_ >= k * self._per_pass(mode):
-                    return g_[:k], s_
-        return gs
-
-    def graph_in_buf(self, n: int, flip=False) -> torch.Tensor | None:
-        """The static input buffer `[:n]` of the graphs captured for `n` images, or None."""
-        gs = self._graphs_for(n, self._mode(flip))
-        return None if gs is None else gs[1].buf[:n]
+    def _mark_written(self) -> None:
+        hip.written(self.out)
 
     def __call__(self, x: torch.Tensor, flip=False) -> torch.Tensor:
-        mode = self._mode(flip)
-        self._check_input(x, mode)
-        cur = torch.cuda.current_stream(self.dev)
-        self.stream.wait_stream(cur)
-        n = x.shape[0]
-        with torch.cuda.device(self.dev), torch.cuda.stream(self.stream):
-            gs = self._graphs_for(n, mode)
-            if gs is not None:
-                graphs, shared = gs
-                buf = shared.buf[:n]
-                if (x.data_ptr() == buf.data_ptr() and x.shape == buf.shape
-                        and x.stride() == buf.stride()):
-                    shared.forget()                  # the caller wrote the graph input itself
-                elif shared.load(x, n, self.stream):
-                    self.calls["copy"] = self.calls.get("copy", 0) + 1
-                for g in graphs:
-                    if self.max_inflight:
-                        while len(self.inflight) >= self.max_inflight:
-                            self.inflight.popleft().synchronize()
-                    g.replay()
-                    if self.max_inflight:
-                        ev = torch.cuda.Event(blocking=True)
-                        ev.record(self.stream)
-                        self.inflight.append(ev)
-                shared.read_by(self, self.stream)
-                self.calls["graph"] += 1
-            else:
-                self._enqueue(x.contiguous(), mode)
-                self.calls["plain"] += 1
-            res = self._result(n, mode)
-        hip.written(self.out)
-        cur.wait_stream(self.stream)
-        return res
+        return self._encode(x, flip)
+
+    # -- the banded blocks' bounded waits --
+    def _raise_wait_errors(self) -> None:
+        """Raises PartsWaitError if a pass since the last check reported expired waits (the host-mapped
+        word the final kernel writes: read without a synchronisation; a pass still running is seen at
+        a later call or by `sync_errors`)."""
+        if self._report is None or int(self._report[0]) == 0:
+            return
+        count = self._clear_wait_errors()
+        raise PartsWaitError("d8s_dense_block_parts", 1,
+                             f"{count} bounded waits ran out: features written as NaN since the last "
+                             f"check; the error words are cleared")
+
+    def _clear_wait_errors(self) -> int:
+        """Waits for the runner's stream, then zeroes the banded blocks' ticket, end and error words
+        (the launch count stays: it names the exchange rows) and the host report; returns the count."""
+        with torch.cuda.device(self.dev):
+            self.stream.synchronize()
+            count = int(self._sync[2].item())
+            self._sync[:3].zero_()
+            torch.cuda.synchronize(self.dev)
+        if self._report is not None:
+            self._report.zero_()
+        return count
+
+    def sync_errors(self, clear: bool = True) -> int:
+        """Bounded waits that ran out in the banded blocks' launches so far (0: every result valid),
+        read after the runner's stream (a synchronisation); `clear` zeroes the words."""
+        if clear:
+            return self._clear_wait_errors()
+        with torch.cuda.device(self.dev):
+            self.stream.synchronize()
+            return int(self._sync[2].item())
 
     # -- diagnostics --
     def store(self, bi: int, j: int) -> torch.Tensor:
-        """Store segment (bi, j) as a float tensor (nb, c, h, w) of integers (j = 0 block input, j >= 1
-        output of layer j - 1), `src/knee/dense8s.py:1491-1508`."""
+        """Store segment j of block bi as a float tensor (nb, c, h, w) of its integers: j = 0 the block
+        input (c = c0), j >= 1 the output of layer j - 1 (c = 32)."""
         b = self.meta["blocks"][bi]
-        n, h, w = self.nb, b["h"], b["w"]
-        hw, g0 = h * w, b["c0"] // GROUP
-        a = self.arenas[bi % 2]
+        h, w = b["h"], b["w"]
+        region = f"store{bi % 2}"
         if j == 0:
-            off = self.in0[bi] - a.data_ptr()
-            t = a[off:off + n * g0 * hw * GROUP].view(n, g0, hw, GROUP)
-            return t.permute(0, 1, 3, 2).reshape(n, g0 * GROUP, h, w).float()
-        off = self.seg[bi] - a.data_ptr() + (j - 1) * n * hw * GROUP
-        t = a[off:off + n * hw * GROUP].view(n, hw, GROUP)
-        return t.permute(0, 2, 1).reshape(n, GROUP, h, w).float()
+            raw = self.mem.view(region, 0, self._in0_bytes(bi)).view(torch.int8)
+            groups = raw.view(self.nb, b["c0"] // GROUP, h * w, GROUP).transpose(2, 3)
+            return groups.reshape(self.nb, b["c0"], h, w).float()
+        off = self._in0_bytes(bi) + (j - 1) * self._slot_bytes(bi)
+        raw = self.mem.view(region, off, self._slot_bytes(bi)).view(torch.int8)
+        return raw.view(self.nb, h * w, GROUP).transpose(1, 2).reshape(self.nb, GROUP, h, w).float()
 
     def bottleneck(self, bi: int, li: int = 0) -> torch.Tensor:
-        """The planar bottleneck of the last conv1 run in block bi as uint8 (nb, 128, h, w)."""
+        """Layer li's planar bottleneck in block bi as uint8 (nb, 128, h, w) (the last one written there)."""
         b = self.meta["blocks"][bi]
-        n, h, w = self.nb, b["h"], b["w"]
-        hw = h * w
-        t = self._bott_of(bi, li)[:4 * n * hw * GROUP].view(4, n, hw, GROUP)
-        return t.permute(1, 0, 3, 2).reshape(n, 4 * GROUP, h, w)
+        hw = b["h"] * b["w"]
+        raw = self._bottleneck_buf(bi, li, self.fused[bi])[:4 * self.nb * hw * GROUP]
+        return raw.view(4, self.nb, hw, GROUP).permute(1, 0, 3, 2).reshape(self.nb, 4 * GROUP, b["h"], b["w"])
+
+    def launch(self, x: torch.Tensor, flip=False, after=None) -> None:
+        """Enqueues one eager pass over the first images of x on the runner's stream (after the caller's
+        current stream), writing `out[:nb]`, without waiting for it; `after(step)` is called after each
+        launch is enqueued (e.g. to record events at chosen steps)."""
+        mode = self._mode(flip)
+        x_ptr = self._pass_input(x, mode)
+        with torch.cuda.device(self.dev), torch.cuda.stream(self.stream):
+            self._join(torch.cuda.current_stream(self.dev))
+            self._launch_pass(x_ptr, 0, mode, after)
+
+    def _pass_input(self, x: torch.Tensor, mode: int) -> int:
+        self._accept(x, mode)
+        return self._staged(x[:self._per_pass(mode)].contiguous(), mode)
 
     @torch.no_grad()
     def trace(self, x: torch.Tensor, flip=False) -> tuple[dict, torch.Tensor]:
-        """One pass over the first images stopping after every launch: the store {(block, j): tensor},
-        the bottleneck {("bott", block, layer): tensor} and the features (`src/knee/dense8s.py:1510-1546`)."""
+        """One pass over the first images with a synchronisation after every launch: what each launch
+        completed -- store segments {(block, j): tensor} and bottlenecks {("bott", block, layer): tensor}
+        -- and the features (the reference's `trace`, `src/knee/dense8s.py:1510-1546`)."""
         mode = self._mode(flip)
-        self._check_input(x, mode)
-        xf = self._padded(x[:self._per_pass(mode)].contiguous(), mode)
-        out: dict = {}
+        x_ptr = self._pass_input(x, mode)
+        snaps: dict = {}
+        f = torch.zeros((self.nb, self.meta["n_features"]), dtype=torch.float32, device=f"cuda:{self.dev}")
+
+        def snapshot(step: Step) -> None:
+            self.stream.synchronize()
+            for key in step.makes:
+                snaps[key] = (self.bottleneck(key[1], key[2]) if key[0] == "bott" else self.store(*key)).clone()
+
         st = self.stream.cuda_stream
         with torch.cuda.device(self.dev), torch.cuda.stream(self.stream):
-            self.stream.wait_stream(torch.cuda.current_stream(self.dev))
-            f = torch.zeros((self.nb, self.meta["n_features"]), dtype=torch.float32,
-                            device=f"cuda:{self.dev}")
-            self._stem(xf.data_ptr(), mode, st)
-            for bi, (layers, trans) in enumerate(self.plan_l):
-                self.stream.synchronize()
-                out[(bi, 0)] = self.store(bi, 0).clone()
-                if bi in self.block_args:                    # every layer in one launch
-                    self._block(bi, st)
-                    self.stream.synchronize()
-                    for li in range(len(layers)):
-                        out[(bi, li + 1)] = self.store(bi, li + 1).clone()
-                    layers = ()
-                if self.fused[bi] == "chain":                # conv2 of li and conv1 of li + 1 together
-                    self._conv1(layers[0].c1, st)
-                    for li, L in enumerate(layers):
-                        self.stream.synchronize()
-                        out[("bott", bi, li)] = self.bottleneck(bi, li).clone()
-                        if li + 1 < len(layers):
-                            self._chain(L.c2, layers[li + 1].c1, st)
-                        else:
-                            self._conv2(L.c2, st)
-                        self.stream.synchronize()
-                        out[(bi, li + 1)] = self.store(bi, li + 1).clone()
-                    layers = ()
-                for li, L in enumerate(layers):
-                    if L.dense is not None:                  # no bottleneck in memory
-                        self._dense(L.dense, st)
-                    else:
-                        self._conv1(L.c1, st)
-                        self.stream.synchronize()
-                        out[("bott", bi, li)] = self.bottleneck(bi, li).clone()
-                        self._conv2(L.c2, st)
-                    self.stream.synchronize()
-                    out[(bi, li + 1)] = self.store(bi, li + 1).clone()
-                if trans is not None:
-                    self._trans(trans, st)
-                else:
-                    self._final(bi, f.data_ptr(), st)
-            self.stream.synchronize()
-        return out, f
+            self._join(torch.cuda.current_stream(self.dev))
+            for step in self.program:
+                self._launch(step, st, x_ptr, f.data_ptr(), mode)
+                snapshot(step)
+        return snaps, f
 
     def profile(self, x: torch.Tensor, reps: int = 3, flip=False) -> dict:
-        """GPU milliseconds per item (stem, conv1 / conv2 per block, transitions, final) of a pass of
-        `nb` images, from HIP events between launches (`src/knee/dense8s.py:1548-1563`)."""
+        """GPU milliseconds per `Step.tag` (stem, conv1 / conv2 / chain / dense / block per block,
+        transitions, final) of one pass, mean of `reps` passes after a warm one, from HIP events
+        recorded between the launches."""
         mode = self._mode(flip)
-        self._check_input(x, mode)
-        xf = self._padded(x[:self._per_pass(mode)].contiguous(), mode)
-        tot: dict[str, float] = collections.defaultdict(float)
+        x_ptr = self._pass_input(x, mode)
+        sums: dict[str, float] = collections.defaultdict(float)
         with torch.cuda.device(self.dev), torch.cuda.stream(self.stream):
-            self.stream.wait_stream(torch.cuda.current_stream(self.dev))
+            self._join(torch.cuda.current_stream(self.dev))
             for r in range(reps + 1):
-                ev: list = []
-                self._pass(xf.data_ptr(), self.out.data_ptr(), mode, ev)
+                marks = [(None, _record(self.stream))]
+                self._launch_pass(x_ptr, 0, mode, after=lambda s: marks.append((s.tag(), _record(self.stream))))
                 self.stream.synchronize()
-                if r == 0:
-                    continue
-                for (_, a), (tag, b) in zip(ev, ev[1:]):
-                    tot[tag] += a.elapsed_time(b)
-        return {k: round(v / reps, 4) for k, v in sorted(tot.items())}
+                if r:
+                    for (_, e0), (tag, e1) in zip(marks, marks[1:]):
+                        sums[tag] += e0.elapsed_time(e1)
+        return {tag: round(ms / reps, 4) for tag, ms in sorted(sums.items())}
 
-    def time_families(self, x: torch.Tensor, reps: int = 5, flip=False) -> dict:
-        """GPU milliseconds per pass of each kernel family (stem, conv1, conv2, trans, final): the
-        family's launches of one pass, in pass order, recorded in a HIP graph `reps` times and replayed
-        between events on the runner's stream.  Unlike `profile` no host gap between launches is
-        counted, so the figure is the kernels' own time.  One eager pass first fills the arenas."""
-        mode = self._mode(flip)
-        self._check_input(x, mode)
-        xf = self._padded(x[:self._per_pass(mode)].contiguous(), mode)
+    def _graph_ms(self, steps: list[Step], reps: int, x_ptr: int = 0, mode: int = 0) -> float:
+        """ms per run of `steps`: a HIP graph holding `reps` runs of them back to back, replayed three
+        times between events after one warm replay; the median replay."""
         st = self.stream.cuda_stream
-        fams: dict[str, list] = {"stem": [lambda: self._stem(xf.data_ptr(), mode, st)],
-                                 "conv1": [], "conv2": [], "chain": [], "dense": [], "block": [],
-                                 "trans": [], "final": []}
-        for bi, (layers, trans) in enumerate(self.plan_l):
-            if bi in self.block_args:
-                fams["block"].append(lambda b=bi: self._block(b, st))
-                layers = ()
-            if self.fused[bi] == "chain":
-                fams["conv1"].append(lambda c=layers[0].c1: self._conv1(c, st))
-                for La, Lb in zip(layers, layers[1:]):
-                    fams["chain"].append(lambda a=La.c2, b=Lb.c1: self._chain(a, b, st))
-                fams["conv2"].append(lambda c=layers[-1].c2: self._conv2(c, st))
-                layers = ()
-            for L in layers:
-                if L.dense is not None:
-                    fams["dense"].append(lambda d=L.dense: self._dense(d, st))
-                    continue
-                fams["conv1"].append(lambda c=L.c1: self._conv1(c, st))
-                fams["conv2"].append(lambda c=L.c2: self._conv2(c, st))
-            if trans is not None:
-                fams["trans"].append(lambda t=trans: self._trans(t, st))
-            else:
-                fams["final"].append(lambda b=bi: self._final(b, self.out.data_ptr(), st))
+        f_ptr = self.out.data_ptr()
         with torch.cuda.device(self.dev), torch.cuda.stream(self.stream):
-            self.stream.wait_stream(torch.cuda.current_stream(self.dev))
-            self._pass(xf.data_ptr(), self.out.data_ptr(), mode)
-            out = {k: self._time(lambda fs=fs: [f() for f in fs], reps) for k, fs in fams.items() if fs}
-        return {k: round(v, 4) for k, v in out.items()}
-
-    def _time(self, fn, reps: int = 20) -> float:
-        """ms per call of `fn` (launching on the runner's stream): a HIP graph of `reps` calls replayed
-        once as warm-up and once under events (`src/knee/dense8s.py:1565-1581`)."""
-        with torch.cuda.device(self.dev), torch.cuda.stream(self.stream):
-            fn()
+            for s in steps:
+                self._launch(s, st, x_ptr, f_ptr, mode)
             self.stream.synchronize()
             g = torch.cuda.CUDAGraph()
             with torch.cuda.graph(g, stream=self.stream, capture_error_mode="thread_local"):
                 for _ in range(reps):
-                    fn()
+                    for s in steps:
+                        self._launch(s, st, x_ptr, f_ptr, mode)
             g.replay()
-            e0 = _record(self.stream)
-            g.replay()
-            e1 = _record(self.stream)
+            marks = [_record(self.stream)]
+            for _ in range(3):
+                g.replay()
+                marks.append(_record(self.stream))
             self.stream.synchronize()
-        return e0.elapsed_time(e1) / reps
+        times = sorted(a.elapsed_time(b) for a, b in zip(marks, marks[1:]))
+        return times[1] / reps
+
+    def _warm(self, x: torch.Tensor, flip) -> tuple[int, int]:
+        """One eager pass over x (fills the store every later timing reads); returns (x_ptr, mode)."""
+        mode = self._mode(flip)
+        x_ptr = self._pass_input(x, mode)
+        with torch.cuda.device(self.dev), torch.cuda.stream(self.stream):
+            self._join(torch.cuda.current_stream(self.dev))
+            self._launch_pass(x_ptr, 0, mode)
+        return x_ptr, mode
+
+    def time_families(self, x: torch.Tensor, reps: int = 5, flip=False) -> dict:
+        """GPU milliseconds per pass of each kernel family (stem, conv1, conv2, chain, dense, block,
+        trans, final): the family's launches of one pass, in pass order, `reps` times in one HIP graph
+        (`_graph_ms`).  Unlike `profile` no host gap between launches is counted: the kernels' own time."""
+        x_ptr, mode = self._warm(x, flip)
+        by_family: dict[str, list] = {}
+        for step in self.program:
+            by_family.setdefault(step.family, []).append(step)
+        return {fam: round(self._graph_ms(steps, reps, x_ptr, mode), 4) for fam, steps in by_family.items()}
 
     def time_layers(self, reps: int = 20) -> dict:
-        """ms of every conv1, conv2 and transition on the current store."""
-        st = self.stream.cuda_stream
+        """ms of every launch of the pass but the stem and the final features, on the current store
+        (`Step.label`: "c1 b{b}l{l}", "c2 ...", "cc ..." chained, "dn ..." fused layer, "blk b{b}", "t{b}")."""
+        return {s.label(): round(self._graph_ms([s], reps), 4) for s in self.program
+                if s.family not in ("stem", "final")}
+
+    def tune_kinds(self, x: torch.Tensor, reps: int = 10, flip=False, apply: bool = False) -> dict:
+        """For every block the ms of its layers run as each kind it can take (`kind_options`), on the
+        store a pass over x leaves: {"b{block}": {kind: ms}} (the role of the reference's on-device
+        tuners `tune_bm` / `tune_trans` / `tune_c2`, `src/knee/dense8s.py:1598-1651`, for this build's
+        choice, the block kind).  Every kind writes the same bytes.  `apply`: the runner then uses the
+        fastest kind per block (its graphs are dropped: capture again); `pack_meta(fused=...)` records
+        such a choice in a package."""
+        self._warm(x, flip)
         out: dict = {}
-        for bi, (layers, trans) in enumerate(self.plan_l):
-            if bi in self.block_args:
-                out[f"blk b{bi}"] = round(self._time(lambda b=bi: self._block(b, st), reps), 4)
-                layers = ()
-            if self.fused[bi] == "chain":
-                out[f"c1 b{bi}l0"] = round(self._time(lambda c=layers[0].c1: self._conv1(c, st), reps), 4)
-                for li, (La, Lb) in enumerate(zip(layers, layers[1:])):
-                    out[f"cc b{bi}l{li}"] = round(self._time(lambda a=La.c2, b=Lb.c1: self._chain(a, b, st),
-                                                             reps), 4)
-                out[f"c2 b{bi}l{len(layers) - 1}"] = round(
-                    self._time(lambda c=layers[-1].c2: self._conv2(c, st), reps), 4)
-                layers = ()
-            for li, L in enumerate(layers):
-                if L.dense is not None:
-                    out[f"dn b{bi}l{li}"] = round(self._time(lambda d=L.dense: self._dense(d, st), reps), 4)
-                    continue
-                out[f"c1 b{bi}l{li}"] = round(self._time(lambda c=L.c1: self._conv1(c, st), reps), 4)
-                out[f"c2 b{bi}l{li}"] = round(self._time(lambda c=L.c2: self._conv2(c, st), reps), 4)
-            if trans is not None:
-                out[f"t{bi}"] = round(self._time(lambda t=trans: self._trans(t, st), reps), 4)
+        for bi, b in enumerate(self.meta["blocks"]):
+            times = {}
+            for kind in kind_options(b, self.nb):
+                times[kind] = round(self._graph_ms(self.block_steps(bi, kind), reps), 4)
+            out[f"b{bi}"] = times
+        if apply:
+            self.fused = {bi: min(out[f"b{bi}"].items(), key=lambda kv: kv[1])[0]
+                          for bi in range(len(self.meta["blocks"]))}
+            self.graphs.clear()
+            self._compile()
         return out
 
 
 def encode_concurrent(calls) -> list[torch.Tensor]:
     """Several runners at once: `calls` = [(runner, x, flip), ...], every runner on its own stream, the
     caller's current stream joined after all of them.  The seeds of an ensemble read the same input and
-    are independent, so one runner's small late-block layers overlap another's work.
+    are independent, so one runner's small late-block layers overlap another's work.  Runners with
+    banded whole blocks ("parts" kinds) run one after another instead (each one's stream waits for the
+    previous one's), so that two banded launches are never in flight together: their workgroups wait
+    for their neighbour bands, which must be resident at the same time.
 
     Each call is made with the runner's own stream current: an extra stream per call would share one
     of the device's few hardware queues with another runner, and an event recorded there would make
@@ -1252,161 +1415,104 @@ def encode_concurrent(calls) -> list[torch.Tensor]:
     if not calls:
         return []
     dev = calls[0][0].dev
-    cur = torch.cuda.current_stream(dev)
+    if any(enc.dev != dev for enc, _, _ in calls):
+        raise ValueError("encode_concurrent: runners on different GPUs")
+    caller = torch.cuda.current_stream(dev)
     for enc, _, _ in calls:
-        if enc.dev != dev:
-            raise ValueError("encode_concurrent: runners on different GPUs")
-        enc.stream.wait_stream(cur)
+        enc.stream.wait_stream(caller)
     outs = []
-    for enc, x, flip in calls:
+    for (enc, x, flip), after in zip(calls, concurrent_order([enc for enc, _, _ in calls])):
+        if after is not None:
+            enc.stream.wait_stream(calls[after][0].stream)
         with torch.cuda.stream(enc.stream):
             outs.append(enc(x, flip=flip))
     for enc, _, _ in calls:
-        cur.wait_stream(enc.stream)
+        caller.wait_stream(enc.stream)
     return outs
 
 
-class EncoderPair:
+def concurrent_order(runners) -> list[int | None]:
+    """For each runner of `encode_concurrent`, the index of the runner whose stream it must wait for
+    first (None: none): each runner with banded whole blocks (`_checked`) waits for the previous such
+    runner, the others run free."""
+    order, last = [], None
+    for i, enc in enumerate(runners):
+        if getattr(enc, "_checked", False):
+            order.append(last)
+            last = i
+        else:
+            order.append(None)
+    return order
+
+
+PAIR_ENTRIES = {"d8s_stem": "d8s_stem_pair", "d8s_conv1": "d8s_conv1_pair", "d8s_conv2": "d8s_conv2_pair",
+                "d8s_dense": "d8s_dense_pair", "d8s_dense_block": "d8s_dense_block_pair",
+                "d8s_transition": "d8s_transition_pair"}
+
+
+class EncoderPair(_PassRunner):
     """Two encoders of one geometry over the same input images -- the final model's two weight seeds
-    on one study -- as ONE launch sequence: every step of a pass is a paired launch (`d8s_*_pair`)
-    carrying both encoders' arguments, so the two passes' small late layers fill the chip together
-    (the 16 x 16 whole block: 192 workgroups in about the time of 96) instead of overlapping by chance
-    on two streams (`encode_concurrent`).  Each encoder's outputs are exactly what it gives alone.  The
-    pair runs on the first encoder's stream and orders the second's around it.  Steps without a pair
-    launch ("parts" blocks, the chained conv2 + conv1 launches of "chain" blocks, the final features)
-    run as two launches in the same sequence."""
+    on one study -- as ONE launch sequence: the two programs side by side, each step that has a paired
+    entry point (`PAIR_ENTRIES`, `d8s_*_pair`) one launch carrying both encoders' arguments, so the two
+    passes' small late layers fill the chip together (the 16 x 16 whole block: 192 workgroups in about
+    the time of 96) instead of overlapping by chance on two streams (`encode_concurrent`); the other
+    steps (banded blocks, chained launches, final features) as two launches in the same sequence.  Each
+    encoder's outputs are exactly what it gives alone.  The pair launches on the first encoder's stream
+    and orders the second's around it."""
 
     def __init__(self, a: Dense8SEncoder, b: Dense8SEncoder):
         if a is b:
             raise ValueError("EncoderPair: the same encoder twice")
         if a.dev != b.dev:
             raise ValueError(f"EncoderPair: encoders on cuda:{a.dev} and cuda:{b.dev}")
-        same = (a.nb == b.nb and a.n_out == b.n_out and a.in_dtype == b.in_dtype and a.in_shape == b.in_shape
-                and a.fused == b.fused and len(a.meta["blocks"]) == len(b.meta["blocks"])
-                and all(all(x[k] == y[k] for k in ("h", "w", "c0", "L"))
-                        for x, y in zip(a.meta["blocks"], b.meta["blocks"])))
-        if not same:
+        geometry = lambda e: (e.nb, e.n_out, e.in_dtype, e.in_shape, e.fused,  # noqa: E731
+                              [(x["h"], x["w"], x["c0"], x["L"]) for x in e.meta["blocks"]])
+        if geometry(a) != geometry(b):
             raise ValueError("EncoderPair: the encoders differ in geometry, batch, input or block kinds")
         self.a, self.b = a, b
+        self.dev, self.nb, self.n_out = a.dev, a.nb, a.n_out
+        self.in_shape, self.in_dtype = a.in_shape, a.in_dtype
+        self.stream = a.stream
         self.lib = a.lib
-        self.graphs: dict = {}
+        self.graphs = GraphBook()
         self.calls = {"graph": 0, "plain": 0, "copy": 0}
+        self._gate = InflightGate(None)
+        self._staging: torch.Tensor | None = None
 
-    def _pass(self, x_ptr: int, fa: int, fb: int, mode: int) -> None:
-        A, B, lib = self.a, self.b, self.lib
-        st = A.stream.cuda_stream
-        for e in (A, B):
-            e.stem_args.x = x_ptr
-            e.stem_args.flip = mode
-        hip.check(lib.d8s_stem_pair(ctypes.byref(A.stem_args), ctypes.byref(B.stem_args), st), "d8s_stem_pair")
-        for bi, ((la, ta), (lb, tb)) in enumerate(zip(A.plan_l, B.plan_l)):
-            if bi in A.block_args:
-                pa, pb = A.block_args[bi], B.block_args[bi]
-                if isinstance(pa, hip.PartsArgs):
-                    A._block(bi, st)
-                    B._block(bi, st)
-                else:
-                    hip.check(lib.d8s_dense_block_pair(ctypes.byref(pa), ctypes.byref(pb), st),
-                              "d8s_dense_block_pair")
-                la = lb = ()
-            if A.fused[bi] == "chain":                       # no pair launch of the chained kernel
-                hip.check(lib.d8s_conv1_pair(ctypes.byref(la[0].c1), ctypes.byref(lb[0].c1), st),
-                          "d8s_conv1_pair")
-                for i in range(len(la) - 1):
-                    A._chain(la[i].c2, la[i + 1].c1, st)
-                    B._chain(lb[i].c2, lb[i + 1].c1, st)
-                hip.check(lib.d8s_conv2_pair(ctypes.byref(la[-1].c2), ctypes.byref(lb[-1].c2), st),
-                          "d8s_conv2_pair")
-                la = lb = ()
-            for La, Lb in zip(la, lb):
-                if La.dense is not None:
-                    hip.check(lib.d8s_dense_pair(ctypes.byref(La.dense), ctypes.byref(Lb.dense), st),
-                              "d8s_dense_pair")
-                    continue
-                hip.check(lib.d8s_conv1_pair(ctypes.byref(La.c1), ctypes.byref(Lb.c1), st), "d8s_conv1_pair")
-                hip.check(lib.d8s_conv2_pair(ctypes.byref(La.c2), ctypes.byref(Lb.c2), st), "d8s_conv2_pair")
-            if ta is not None:
-                hip.check(lib.d8s_transition_pair(ctypes.byref(ta), ctypes.byref(tb), st), "d8s_transition_pair")
-            else:
-                A._final(bi, fa, st)
-                B._final(bi, fb, st)
+    def _join(self, caller) -> None:
+        self.stream.wait_stream(caller)
+        self.stream.wait_stream(self.b.stream)
 
-    def _passes(self, xf: torch.Tensor, mode: int) -> None:
-        A, B = self.a, self.b
-        for i, chunk in enumerate(xf.split(A._per_pass(mode))):
-            xc = A._padded(chunk, mode)
-            self._pass(xc.data_ptr(), A.out[i * A.nb].data_ptr(), B.out[i * B.nb].data_ptr(), mode)
+    def _accept(self, x: torch.Tensor, mode: int) -> None:
+        self.a._accept(x, mode)
+        self.b._accept(x, mode)
 
-    def capture(self, n: int, flip=False) -> float:
-        """One HIP graph per pair of passes over a batch of `n` input images; returns the seconds spent."""
-        A, B = self.a, self.b
-        mode = A._mode(flip)
-        k = A._per_pass(mode)
-        n = -(-n // k) * k
-        if n // k * A.nb > A.out.shape[0]:
-            raise ValueError(f"graph for {n} images: the encoders do {A.nb} per pass, "
-                             f"the output holds {A.out.shape[0]}")
-        t = time.perf_counter()
-        with torch.cuda.device(A.dev):
-            shared = graph_input(A.dev, (n, *A.in_shape[1:]), A.in_dtype)
-            static_in = shared.buf
-            shared.forget()
-            with torch.cuda.stream(A.stream):
-                A.stream.wait_stream(torch.cuda.current_stream(A.dev))
-                A.stream.wait_stream(B.stream)
-                self._passes(static_in[:k], mode)
-            A.stream.synchronize()
-            graphs = []
-            for i, chunk in enumerate(static_in.split(k)):
-                g = torch.cuda.CUDAGraph()
-                with torch.cuda.graph(g, stream=A.stream, capture_error_mode="thread_local"):
-                    self._pass(chunk.data_ptr(), A.out[i * A.nb].data_ptr(), B.out[i * B.nb].data_ptr(), mode)
-                graphs.append(g)
-            A.stream.synchronize()
-        self.graphs[(n, mode)] = (graphs, shared)
-        return time.perf_counter() - t
+    def _launch_pass(self, x_ptr: int, index: int, mode: int) -> None:
+        A, B, st = self.a, self.b, self.stream.cuda_stream
+        fa, fb = A.out[index * A.nb].data_ptr(), B.out[index * B.nb].data_ptr()
+        for sa, sb in zip(A.program, B.program):
+            paired = PAIR_ENTRIES.get(sa.entry)
+            if paired is None:
+                A._launch(sa, st, x_ptr, fa, mode)
+                B._launch(sb, st, x_ptr, fb, mode)
+                continue
+            if sa.family == "stem":
+                for s in (sa, sb):
+                    s.args.x, s.args.flip = x_ptr, mode
+            hip.check(getattr(self.lib, paired)(ctypes.byref(sa.args), ctypes.byref(sb.args), st), paired)
 
-    def _graphs_for(self, n: int, mode: int):
-        gs = self.graphs.get((n, mode))
-        if gs is None:
-            k = -(-n // self.a._per_pass(mode))
-            for (m_, md), (g_, s_) in sorted(self.graphs.items()):
-                if md == mode and m_ >= k * self.a._per_pass(mode):
-                    return g_[:k], s_
-        return gs
+    def _outputs(self, n: int, mode: int):
+        return self.a._outputs(n, mode), self.b._outputs(n, mode)
+
+    def _mark_written(self) -> None:
+        hip.written(self.a.out, self.b.out)
 
     def __call__(self, x: torch.Tensor, flip=False) -> tuple[torch.Tensor, torch.Tensor]:
         """Both encoders' features of x: (outputs of the first, outputs of the second), as each
         encoder's `__call__` returns them."""
-        A, B = self.a, self.b
-        mode = A._mode(flip)
-        A._check_input(x, mode)
-        B._check_input(x, mode)
-        cur = torch.cuda.current_stream(A.dev)
-        A.stream.wait_stream(cur)
-        A.stream.wait_stream(B.stream)
-        n = x.shape[0]
-        with torch.cuda.device(A.dev), torch.cuda.stream(A.stream):
-            gs = self._graphs_for(n, mode)
-            if gs is not None:
-                graphs, shared = gs
-                buf = shared.buf[:n]
-                if x.data_ptr() == buf.data_ptr() and x.shape == buf.shape and x.stride() == buf.stride():
-                    shared.forget()
-                elif shared.load(x, n, A.stream):
-                    self.calls["copy"] += 1
-                for g in graphs:
-                    g.replay()
-                shared.read_by(self, A.stream)
-                self.calls["graph"] += 1
-            else:
-                self._passes(x.contiguous(), mode)
-                self.calls["plain"] += 1
-            ra, rb = A._result(n, mode), B._result(n, mode)
-        hip.written(A.out, B.out)
-        B.stream.wait_stream(A.stream)
-        cur.wait_stream(A.stream)
-        return ra, rb
+        res = self._encode(x, flip)
+        self.b.stream.wait_stream(self.stream)
+        return res
 
 
 def _record_sync(stream) -> torch.cuda.Event:

@@ -162,6 +162,9 @@ SIGNATURES = {
     "d8s_dense_block_parts": [ctypes.POINTER(PartsArgs), vp],
     "d8s_transition": [ctypes.POINTER(GemmArgs), vp],
     "d8s_final": [vp, i32, vp, i32, i32, vp, vp, i32, vp],
+    "d8s_final_checked": [vp, i32, vp, i32, i32, vp, vp, i32, vp, vp, vp],
+    "d8s_host_mapped": [vp, ctypes.POINTER(vp)],
+    "d8s_parts_supported": [i32, i32, i32, i32],
     "d8s_linear": [vp, i32, i32, vp, vp, i32, vp, vp],
     "d8s_stem": [ctypes.POINTER(StemArgs), vp],
     "d8s_stem_pair": [ctypes.POINTER(StemArgs), ctypes.POINTER(StemArgs), vp],
@@ -194,9 +197,30 @@ def source_sha() -> str:
     return h.hexdigest()[:12]
 
 
+class StaleLibrary(D8sError):
+    """The library on disk was built from other sources than the ones beside it."""
+
+
+def check_fresh(lib: ctypes.CDLL, where: Path) -> str:
+    """The source hash compiled into `lib`; raises StaleLibrary when the kernel sources are present and
+    hash otherwise -- the library would run kernels other than the ones in the tree (the reference
+    checks its package's cubin against `kernels_sha` and recompiles, `src/knee/dense8s.py:883-908`;
+    here rebuilding is `__graft_entry__.build()`, outside the runtime)."""
+    fn = lib.d8s_version
+    fn.argtypes, fn.restype = [], ctypes.c_char_p
+    fields = fn().decode().split()
+    built = fields[2] if len(fields) >= 3 else ""
+    if all(f.is_file() for f in SOURCES) and HEADER.is_file():
+        want = source_sha()
+        if built != want:
+            raise StaleLibrary("library", 0, f"{where} was built from sources {built or '?'}, the tree's "
+                                             f"hash {want}: run __graft_entry__.build()")
+    return built
+
+
 def library(path: Path | None = None) -> ctypes.CDLL:
-    """The loaded library (once per process).  Raises FileNotFoundError / OSError if it is missing:
-    the encoder has no other implementation.
+    """The loaded library (once per process), checked against the kernel sources (`check_fresh`).
+    Raises FileNotFoundError / OSError if it is missing: the encoder has no other implementation.
     """
     with _LOCK:
         lib = _STATE.get("lib")
@@ -207,6 +231,7 @@ def library(path: Path | None = None) -> ctypes.CDLL:
             raise FileNotFoundError(f"{p}: the HIP kernel library is not built "
                                     f"(run __graft_entry__.build())")
         lib = ctypes.CDLL(str(p))
+        check_fresh(lib, p)
         for name, argtypes in SIGNATURES.items():
             fn = getattr(lib, name)
             fn.argtypes = argtypes

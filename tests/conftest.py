@@ -31,5 +31,7 @@ def dev():
     if not torch.cuda.is_available():
         pytest.skip("no GPU")
     from rsna_knee_efficiency_amd import hip
-    hip.library()          # raises if the HIP library is missing: no fallback
+    hip.library()          # raises if the HIP library is missing (no fallback) or stale
+    assert hip.built_sha() == hip.source_sha(), "libd8s_hip.so is not built from the tree's sources"
+    print(f"\nlibrary {hip.version()}", flush=True)
     return torch.device("cuda:0")

@@ -31,6 +31,41 @@ def test_version_is_this_source():
     assert hip.built_sha() == hip.source_sha(), "libd8s_hip.so is stale: run __graft_entry__.build()"
 
 
+def test_stale_library_is_refused(tmp_path):
+    """A library whose compiled-in source hash is not the tree's is refused at load (StaleLibrary);
+    one with the tree's hash is accepted.  Stub libraries exporting only d8s_version stand in for
+    builds from other sources."""
+    def stub(tag: str):
+        src = tmp_path / f"v_{tag}.c"
+        src.write_text(f'const char* d8s_version(void) {{ return "d8s-hip 1 {tag} gfx950"; }}\n')
+        so = tmp_path / f"libv_{tag}.so"
+        subprocess.run(["gcc", "-shared", "-fPIC", str(src), "-o", str(so)], check=True)
+        return ctypes.CDLL(str(so)), so
+    lib, so = stub("0123456789ab")
+    with pytest.raises(hip.StaleLibrary, match="0123456789ab"):
+        hip.check_fresh(lib, so)
+    lib, so = stub(hip.source_sha())
+    assert hip.check_fresh(lib, so) == hip.source_sha()
+
+
+def test_parts_supported_matches_the_launch():
+    """d8s_parts_supported (what the runner's band options come from) and the launcher agree: a shape
+    it refuses fails on the host with hipErrorInvalidValue, at the LDS limit (the 32 x 32 block with
+    64 groups fits 256-pixel bands; the 128-wide map with 2-row bands does not)."""
+    lib = hip.library()
+    assert lib.d8s_parts_supported(32, 32, 64, 4) == 1
+    assert lib.d8s_parts_supported(128, 128, 7, 64) == 0          # 256 px bands of a 128-wide map
+    assert lib.d8s_parts_supported(128, 128, 7, 128) == 1
+    assert lib.d8s_parts_supported(16, 16, 65, 8) == 0            # more than 64 groups
+    assert lib.d8s_parts_supported(16, 16, 51, 3) == 0            # H not a multiple of parts
+    lay = (hip.LayerP * 1)()
+    buf = (ctypes.c_uint8 * 64)()
+    args = hip.PartsArgs(ctypes.addressof(buf), ctypes.addressof(buf), ctypes.addressof(lay),
+                         ctypes.addressof(buf), ctypes.addressof(buf), 1, 128, 128, 2, 6, 64)
+    assert lib.d8s_dense_block_parts(ctypes.byref(args), None) == 1
+    assert "LDS" in lib.d8s_last_error().decode()
+
+
 def test_struct_layouts_match_header(tmp_path):
     prog = tmp_path / "layout.c"
     prog.write_text(

@@ -70,6 +70,33 @@ def test_conv1_config2(dev, S, C):
     assert 0.0 < zero < 0.9 and sat < 0.5, (zero, sat)
 
 
+@pytest.mark.parametrize("S,C", cases.GEMM_CASES)
+def test_conv1_config2_baseline_seeds(dev, S, C):
+    """Config 2 with the benchmark's definition of its inputs (activations from N(0, 1) per tensor,
+    seed 11; weights N(0, 2 / C_in), seed 12; calibrated BN prologue and bottleneck scale): int32
+    accumulators and u8 bottleneck exact, and the bottleneck neither all zero nor saturated."""
+    c = cases.gemm_case_c2(S, C)
+    print(f"conv1 (seeds 11/12) S={S} C_in={C}", flush=True)
+    acc, byt = checks.run_conv1(c, dev)
+    acc_x, byt_x = checks.exact_conv1(c)
+    assert np.array_equal(acc, acc_x), f"accumulators: {checks.bytes_cmp(acc, acc_x)}"
+    assert np.array_equal(byt, byt_x), f"bottleneck: {checks.bytes_cmp(byt, byt_x)}"
+    assert 0.05 < float((byt_x == 0).mean()) < 0.95 and int(byt_x.max()) >= 128
+
+
+@pytest.mark.parametrize("S", cases.CONV2_SIDES)
+def test_conv2_config3_baseline_seeds(dev, S):
+    """Config 3 with the benchmark's definition of its inputs (activations seed 21 through a BN + ReLU
+    to the u8 bottleneck, weights seed 22, per-channel requantisation scale): exact into its slot."""
+    c = cases.conv2_case_c3(S)
+    print(f"conv2 (seeds 21/22) S={S}", flush=True)
+    got, others = checks.run_conv2(c, dev)
+    _, q_x = checks.exact_conv2(c)
+    assert np.array_equal(got, q_x), checks.bytes_cmp(got, q_x)
+    assert np.all(others == 0x5A)
+    assert int(np.abs(q_x.astype(np.int32)).max()) >= 100
+
+
 @pytest.mark.parametrize("S,C,N", [(64, 320, 12), (8, 96, 3), (2, 64, 1), (100, 96, 30), (128, 32, 16),
                                    (64, 608, 64), (50, 704, 40)])
 def test_conv1_ks_variants(dev, S, C, N):

@@ -3,7 +3,8 @@
 gives the bytes of the default encoder (two launches per layer / one workgroup per image), exact
 against the C oracle on sampled pixels of its own inputs, under graph replay too (the kernel clears its
 own synchronisation words for the next launch), with no bounded wait running out.  Two such runners on
-two streams at once stay exact."""
+two streams at once stay exact.  The 64- and 128-wide blocks split into bands give the same bytes too,
+and an error word planted from the host makes the pass's features NaN and the next call raise."""
 from __future__ import annotations
 
 import numpy as np
@@ -121,3 +122,38 @@ def test_parts_groups_below_first_chunk(dev, small_first, parts):
     got = enc(small_first["x"]).clone()
     assert enc.sync_errors() == 0
     assert torch.equal(got, small_first["want"])
+
+
+@pytest.mark.parametrize("kinds", [{1: "parts:16"}, {1: "parts:32"}, {1: "parts:64"}, {0: "parts:128"}])
+def test_parts_wide_maps(dev, c4, kinds):
+    """The 64 x 64 block (12 layers) in 256-, 128- and 64-pixel bands and the 128 x 128 block (6 layers)
+    in one-row bands: more bands than compute units (384 to 3072 workgroups), so images start as
+    earlier ones finish; the bytes of the default encoder."""
+    print(f"wide parts {kinds}", flush=True)
+    enc = dense8s.Dense8SEncoder(c4["pack"], dev.index or 0, 24, fused={0: "tile", **kinds})
+    got = enc(c4["x"]).clone()
+    assert enc.sync_errors() == 0
+    assert torch.equal(got, c4["want"])
+
+
+def test_parts_wait_error_surfaces(dev, c4):
+    """A non-zero error word (planted by the host, as an expired wait would leave it) makes the pass's
+    features NaN, reaches the host-mapped report, and makes the next call raise PartsWaitError, which
+    clears it: the call after that is exact again.  The same under graph replay."""
+    enc = dense8s.Dense8SEncoder(c4["pack"], dev.index or 0, 24, fused={0: "tile", 2: "parts", 3: "parts"})
+    assert enc._checked and enc._report is not None
+    for graphs in (False, True):
+        if graphs:
+            enc.capture(24)
+        assert torch.equal(enc(c4["x"]).clone(), c4["want"])
+        torch.cuda.synchronize(dev)
+        enc._sync[2].fill_(3)
+        bad = enc(c4["x"]).clone()
+        torch.cuda.synchronize(dev)
+        assert torch.isnan(bad).all(), graphs
+        assert int(enc._report[0]) == 3, graphs
+        with pytest.raises(dense8s.PartsWaitError):
+            enc(c4["x"])
+        assert int(enc._report[0]) == 0 and enc.sync_errors(clear=False) == 0
+        assert torch.equal(enc(c4["x"]).clone(), c4["want"]), graphs
+    assert enc.calls["graph"] >= 2

@@ -167,3 +167,12 @@ def test_written_bumps_versions():
         t = torch.zeros(3)
         hip.written(t, None)                     # inference tensors and None are accepted
     assert dense8s.contents_id(t) != dense8s.contents_id(t)     # no version counter: always new
+
+
+def test_concurrent_order_serialises_banded_runners():
+    """encode_concurrent: runners with banded whole blocks wait for the previous such runner's stream
+    (two banded launches never in flight together), the others run free."""
+    import types
+    rs = [types.SimpleNamespace(_checked=c) for c in (True, False, True, True, False)]
+    assert dense8s.concurrent_order(rs) == [None, None, 0, 2, None]
+    assert dense8s.concurrent_order([]) == []
