@@ -420,6 +420,81 @@ def c4_summary(trace_csv: str) -> str:
     return "\n".join(lines)
 
 
+def _dispatch_counters(d: str) -> dict:
+    """{(kernel base name, dispatch id): {counter: value}} of every library dispatch in a rocprofv3
+    counter-collection output directory."""
+    import csv
+    import glob
+    out: dict = {}
+    for path in glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True):
+        for r in csv.DictReader(open(path)):
+            name = r.get("Kernel_Name", "")
+            if not _family(name):
+                continue
+            key = (name.split("(")[0].replace("void ", ""), r.get("Dispatch_Id", r.get("Correlation_Id", "")))
+            c = out.setdefault(key, {})
+            c[r["Counter_Name"]] = c.get(r["Counter_Name"], 0.0) + float(r["Counter_Value"])
+    return out
+
+
+def c4_counter_summary(fetch_dir: str, write_dir: str, mfma_dir: str, wave_dir: str, passes: int,
+                       copy_bytes: int = 1 << 30) -> str:
+    """Configuration 4's banded whole-block launches (k_dparts, blocks 2 and 3 of a 24-image pass) from
+    four counter runs of `bench.py --pmc-passes P --pmc-nb 24 --copy-probe` (FETCH_SIZE; WRITE_SIZE;
+    MfmaUtil GRBM_GUI_ACTIVE SQ_INSTS_VALU_MFMA_MOPS_I8; WAVE_COUNTERS): per kernel the HBM bytes per
+    launch (scaled by k_copy's reading, as `traffic_summary`) against the algorithmic bytes
+    (`block_work`), the MFMA busy fraction and issued operations against the algorithmic ones, and
+    where the waves' cycles go."""
+    fe, wr, mf, wv = (_dispatch_counters(d) for d in (fetch_dir, write_dir, mfma_dir, wave_dir))
+
+    def per_kernel(tab: dict, counter: str) -> dict:
+        acc: dict = {}
+        for (k, _), c in tab.items():
+            if counter in c:
+                a = acc.setdefault(k, [0, 0.0])
+                a[0] += 1
+                a[1] += c[counter]
+        return acc
+
+    cf, cw = per_kernel(fe, "FETCH_SIZE"), per_kernel(wr, "WRITE_SIZE")
+    kf = copy_bytes / (cf["k_copy"][1] * 1024 / cf["k_copy"][0])
+    kw = copy_bytes / (cw["k_copy"][1] * 1024 / cw["k_copy"][0])
+    n = SLICES
+    kinds = dense8s.fused_blocks({"blocks": C5_BLOCKS, "n": n})
+    work = {}
+    for bi, b in enumerate(C5_BLOCKS):
+        if str(kinds[bi]).startswith("parts:"):
+            pt = b["h"] // int(kinds[bi].split(":")[1]) * b["w"] // 32
+            work[f"k_dparts<{pt}>"] = (bi, kinds[bi]) + block_work(b, n)
+    lines = [f"Calibration: k_copy moves {copy_bytes} B read + {copy_bytes} B written per dispatch; "
+             f"FETCH_SIZE scale {kf:.3f}, WRITE_SIZE scale {kw:.3f}.", "",
+             "| kernel | block (kind) | launches | HBM read MB | HBM write MB | traffic / algorithmic "
+             "| MFMA busy % | MFMA ops issued (G) | algorithmic ops (G) | waiting % | ready, not issued % "
+             "| issuing % | VALU issuing % |", "|---|---|---|---|---|---|---|---|---|---|---|---|---|"]
+    for k, (bi, kind, byts, ops) in sorted(work.items()):
+        if k not in cf or k not in cw:
+            continue
+        cnt = cf[k][0]
+        rd = cf[k][1] * 1024 * kf / cnt
+        wt = cw[k][1] * 1024 * kw / cw[k][0]
+        ds = [c for (kk, _), c in mf.items() if kk == k]
+        w = sum(c.get("GRBM_GUI_ACTIVE", 0.0) for c in ds)
+        util = sum(c.get("MfmaUtil", 0.0) * c.get("GRBM_GUI_ACTIVE", 0.0) for c in ds) / w if w else 0.0
+        issued = sum(c.get("SQ_INSTS_VALU_MFMA_MOPS_I8", 0.0) for c in ds) * 512 / max(len(ds), 1)
+        wsum: dict = {}
+        for (kk, _), c in wv.items():
+            if kk == k:
+                for name, v in c.items():
+                    wsum[name] = wsum.get(name, 0.0) + v
+        cyc = wsum.get("SQ_WAVE_CYCLES", 0.0) or float("nan")
+        pct = lambda c: 100.0 * wsum.get(c, 0.0) / cyc  # noqa: E731
+        lines.append(f"| `{k}` | {bi} ({kind}) | {cnt} | {rd / 1e6:.2f} | {wt / 1e6:.2f} | {(rd + wt) / byts:.3f} "
+                     f"| {util:.1f} | {issued / 1e9:.1f} | {ops / 1e9:.1f} | {pct('SQ_WAIT_ANY'):.1f} "
+                     f"| {pct('SQ_WAIT_INST_ANY'):.1f} | {pct('SQ_ACTIVE_INST_ANY'):.1f} "
+                     f"| {pct('SQ_ACTIVE_INST_VALU'):.1f} |")
+    return "\n".join(lines)
+
+
 WAVE_COUNTERS = ("SQ_WAVES", "SQ_WAVE_CYCLES", "SQ_BUSY_CYCLES", "SQ_WAIT_ANY", "SQ_WAIT_INST_ANY",
                  "SQ_ACTIVE_INST_ANY", "SQ_ACTIVE_INST_VALU", "SQ_INSTS_VALU")
 
@@ -641,26 +716,35 @@ def c4_roofline(enc, reps: int, peak_tops: float | None) -> dict:
     return out
 
 
-def chain_in_schedule(encs, x, reps: int, bytes_per_launch: float) -> dict:
-    """The chained conv2 + conv1 launches timed inside configuration 5's schedule: seed 1's pass replays
-    its graph on its stream while seed 0's pass is launched on its own, with events only before the
-    first and after the last chained launch; the span / launches, mean over `reps` steps (after a warm
-    one), and the algorithmic bytes per launch over it against 8 TB/s."""
+def family_in_schedule(encs, x, reps: int, family: str, bytes_per_launch: float) -> dict:
+    """One family's launches timed inside configuration 5's schedule: seed 1's pass replays its graph on
+    its stream while seed 0's pass is launched on its own, with events only around the family's
+    launches (before the first and after the last of each contiguous run of them: block 2's chained
+    launches, block 0's fused layers); the summed spans / launches, mean over `reps` steps (after a
+    warm one), and the algorithmic bytes per launch over it against 8 TB/s."""
     enc = encs[0]
     prog = enc.program
-    idx = [i for i, s in enumerate(prog) if s.family == "chain"]
-    if not idx:
+    idx = [i for i, s in enumerate(prog) if s.family == family]
+    if not idx or idx[0] == 0:
         return {}
-    before, last = prog[idx[0] - 1], prog[idx[-1]]
+    runs = []                                         # (step before the run, last step of the run)
+    for i in idx:
+        if runs and runs[-1][2] == i - 1:
+            runs[-1][1], runs[-1][2] = prog[i], i
+        else:
+            runs.append([prog[i - 1], prog[i], i])
+    marks = {id(a): ("a", k) for k, (a, _, _) in enumerate(runs)}
+    marks.update({id(b): ("b", k) for k, (_, b, _) in enumerate(runs)})
     spans = []
     for r in range(reps + 1):
-        ev = {}
+        ev: dict = {}
 
         def after(step, ev=ev):
-            if step is before or step is last:
+            m = marks.get(id(step))
+            if m is not None:
                 e = torch.cuda.Event(enable_timing=True)
                 e.record(enc.stream)
-                ev["a" if step is before else "b"] = e
+                ev[m] = e
         torch.cuda.synchronize()
         with torch.cuda.stream(encs[1].stream):
             encs[1](x, flip="tta")
@@ -668,13 +752,13 @@ def chain_in_schedule(encs, x, reps: int, bytes_per_launch: float) -> dict:
             enc.launch(x, flip="tta", after=after)
         torch.cuda.synchronize()
         if r:
-            spans.append(ev["a"].elapsed_time(ev["b"]) / len(idx))
+            spans.append(sum(ev[("a", k)].elapsed_time(ev[("b", k)]) for k in range(len(runs))) / len(idx))
     ms = float(np.mean(spans))
     gbs = bytes_per_launch / (ms * 1e-3) / 1e9
-    return {"launches": len(idx), "avg_launch_ms": round(ms, 5), "gbs": round(gbs, 1),
+    return {"family": family, "launches": len(idx), "avg_launch_ms": round(ms, 5), "gbs": round(gbs, 1),
             "frac": round(gbs / HBM_PEAK_GBS, 4),
-            "schedule": "seed 0 eager with events at the chained run's ends, seed 1's graph replay on "
-                        "its own stream at the same time"}
+            "schedule": "seed 0 eager with events around the family's runs of launches, seed 1's graph "
+                        "replay on its own stream at the same time"}
 
 
 def bench_c4(dev: torch.device, passes: int, reps: int) -> dict:
@@ -982,6 +1066,12 @@ def main() -> None:
                     help="print the MFMA use per family from a --pmc-passes counter run")
     ap.add_argument("--c4-summary", metavar="TRACE_CSV",
                     help="print the per-pass kernel times of a --c4-passes kernel trace")
+    ap.add_argument("--pmc-nb", type=int, choices=(96, 24), default=96,
+                    help="with --pmc-passes: 96 = a configuration-5 flip-TTA pass, 24 = a "
+                         "configuration-4 study (plain)")
+    ap.add_argument("--c4-counter-summary", nargs=4, metavar=("FETCH_DIR", "WRITE_DIR", "MFMA_DIR", "WAVE_DIR"),
+                    help="print configuration 4's banded-block counters from four --pmc-passes "
+                         "--pmc-nb 24 runs")
     ap.add_argument("--wave-summary", metavar="PMC_DIR",
                     help="print where the waves' cycles go per family from a --pmc-passes 1 run of "
                          "the SQ counters WAVE_COUNTERS")
@@ -997,6 +1087,9 @@ def main() -> None:
         return
     if args.c4_summary:
         print(c4_summary(args.c4_summary))
+        return
+    if args.c4_counter_summary:
+        print(c4_counter_summary(*args.c4_counter_summary, passes=args.pmc_passes or 3))
         return
     if args.traffic_summary:
         if args.path == "prep":
@@ -1035,11 +1128,15 @@ def main() -> None:
     t0 = time.perf_counter()
     nb = 4 * SLICES                                     # 2 crops x 24 slices x flip
     if args.pmc_passes:
+        nb = args.pmc_nb
+        mode = "tta" if nb == 4 * SLICES else False
         enc = build_encoder(0, nb, dev)[0]
         x = torch.from_numpy(synthetic.c5_study(0)).to(dev)
-        fam = family_times(enc, x, args.pmc_passes - 1, "tta") if args.pmc_passes > 1 else {}
+        if nb != 4 * SLICES:
+            x = x[:nb].contiguous()
+        fam = family_times(enc, x, args.pmc_passes - 1, mode) if args.pmc_passes > 1 else {}
         if args.pmc_passes == 1:
-            enc(x, flip="tta")
+            enc(x, flip=mode)
             torch.cuda.synchronize()
         kb = kernel_bytes(enc.meta, nb, enc.fused)
         res = {"passes": args.pmc_passes, "launches_per_pass": {k: len(v) for k, v in kb.items()},
@@ -1196,7 +1293,7 @@ def main() -> None:
     log(f"families GB/s {fam_gbs}; int8 TOP/s {fam_tops}")
     # the dominant family inside configuration 5's own two-stream schedule (the isolated figure above
     # replays its launches back to back)
-    in_pass = chain_in_schedule(encs, studies[0], args.prof_reps, dom_bytes / launches) if dom == "chain" else {}
+    in_pass = family_in_schedule(encs, studies[0], args.prof_reps, dom, dom_bytes / launches)
     log(f"{dom} launches inside the two-stream schedule: {in_pass}")
     total_bytes = sum(sum(v) for v in byts.values())
     out = {

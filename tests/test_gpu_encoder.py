@@ -195,6 +195,32 @@ def test_fused_blocks_same_bytes(dev, study512):
             dense8s.Dense8SEncoder(study512["pack"], dev.index or 0, 24, fused=bad)
 
 
+def test_tune_kinds_and_recorded_kinds(dev, study512):
+    """`tune_kinds` times every kind each block can take (so every option runs) and, applied, leaves the
+    fastest per block, with the same features; a package recording kinds in its meta (`pack_meta(fused=
+    ...)`, the reference's per-block "fused" field) gives runners with those kinds and the same features,
+    the reference's own kind names included."""
+    enc, x = study512["enc"], study512["xd"]
+    want = enc(x).clone()
+    runner = dense8s.Dense8SEncoder(study512["pack"], dev.index or 0, 24)
+    times = runner.tune_kinds(x, reps=2, apply=True)
+    print(times, flush=True)
+    for bi, b in enumerate(study512["pack"]["meta"]["blocks"]):
+        kinds = times[f"b{bi}"]
+        assert set(kinds) == set(dense8s.kind_options(b, 24)) and all(v > 0 for v in kinds.values())
+        assert runner.fused[bi] == min(kinds, key=kinds.get)
+    assert runner.sync_errors() == 0
+    assert torch.equal(runner(x).clone(), want)
+    meta = dense8s.pack_meta(study512["plan"], 24, input_kind="u8", fused=runner.fused)
+    rec = dense8s.Dense8SEncoder(dict(study512["pack"], meta=meta), dev.index or 0, 24)
+    assert rec.fused == runner.fused
+    assert torch.equal(rec(x).clone(), want)
+    meta2 = dense8s.pack_meta(study512["plan"], 24, input_kind="u8", fused={"b3": "img3", "b0": "tile"})
+    r2 = dense8s.Dense8SEncoder(dict(study512["pack"], meta=meta2), dev.index or 0, 24)
+    assert r2.fused[3] == "img" and r2.fused[0] == "tile"
+    assert torch.equal(r2(x).clone(), want)
+
+
 def test_encoder288_reference_study(dev):
     """The reference's own study shape (kaggle/int8_pack/pack_dense8s.py:29-30: 88 images at 288 px,
     maps 72, 36, 18, 9 with ragged tiles everywhere): every launch exact against the oracle on sampled

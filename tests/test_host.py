@@ -176,3 +176,24 @@ def test_concurrent_order_serialises_banded_runners():
     rs = [types.SimpleNamespace(_checked=c) for c in (True, False, True, True, False)]
     assert dense8s.concurrent_order(rs) == [None, None, 0, 2, None]
     assert dense8s.concurrent_order([]) == []
+
+
+def test_recorded_block_kinds(plan169):
+    """A package's per-block "fused" field (pack_meta(fused=...)) is what fused_blocks returns when the
+    caller asks for none: this runner's kinds as recorded (checked: a kind the block cannot run is a
+    ValueError), the reference's names mapped ("img3" -> "img" where a workgroup per image fits, else
+    the default; "tile" -> "tile"), unrecorded blocks at their default."""
+    _, plan = plan169
+    default = dense8s.fused_blocks(dense8s.pack_meta(plan, 24))
+    assert default == {0: "tile", 1: "chain", 2: "parts:8", 3: "parts:8"}
+    meta = dense8s.pack_meta(plan, 24, fused={0: "conv", "b2": "chain", 3: "img"})
+    assert [b["fused"] for b in meta["blocks"]] == ["conv", None, "chain", "img"]
+    assert dense8s.fused_blocks(meta) == {0: "conv", 1: "chain", 2: "chain", 3: "img"}
+    ref = dense8s.pack_meta(plan, 24, fused={"b3": "img3", "b2": "img3", "b1": "tile"})
+    assert dense8s.fused_blocks(ref) == {0: "tile", 1: "tile", 2: "parts:8", 3: "img"}
+    with pytest.raises(ValueError):
+        dense8s.fused_blocks(dense8s.pack_meta(plan, 24, fused={0: "img"}))
+    assert dense8s.fused_blocks(meta, {1: "tile"}) == {0: "conv", 1: "tile", 2: "conv", 3: "conv"}
+    opts = dense8s.kind_options(meta["blocks"][3], 24)
+    assert opts[:4] == ["conv", "chain", "tile", "img"] and "parts:8" in opts
+    assert dense8s.kind_options(meta["blocks"][0], 24) == ["conv", "tile", "parts:128"]
