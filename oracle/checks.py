@@ -417,6 +417,7 @@ def smoke_check(device: str = "cuda:0") -> dict:
         np.arange(3)[None, :, None, None], x])
     ref = emu.emulate(plan, xf, par, stem_kind="f16").numpy()
     res["vs_emulate"] = feat_cmp(feats, ref)
+    res["wait_errors"] = enc.sync_errors()
     return smoke_gate(res)
 
 
@@ -424,15 +425,17 @@ def smoke_gate(res: dict) -> dict:
     """The pass/fail rule of `smoke_check`: no byte of any checked launch family differs (conv1,
     conv2, the fused layers, the whole-block layers and the transitions), at least one layer and one
     transition were checked, the final features
-    are equal, the stem within 1 LSB on < 1e-3 of its bytes, a plain call equals the trace, and the
-    features are within rel_l2 1e-2 of the float64 emulation.  Raises AssertionError otherwise."""
+    are equal, the stem within 1 LSB on < 1e-3 of its bytes, a plain call equals the trace, the
+    features are within rel_l2 1e-2 of the float64 emulation, and no bounded wait of the banded block
+    ran out.  Raises AssertionError otherwise."""
     fams = ("conv1", "conv2", "dense", "block", "trans")
     ok = (all(res[k]["mismatch"] == 0 for k in fams)
           and sum(res[k]["launches"] for k in ("conv1", "dense", "block")) > 0
           and res["trans"]["launches"] > 0
           and res["final"]["equal"]
           and res["stem"]["max_diff"] <= 1 and res["stem"]["mismatch_frac"] < 1e-3
-          and res["call_vs_trace"] and res["vs_emulate"]["rel_l2"] < 1e-2)
+          and res["call_vs_trace"] and res["vs_emulate"]["rel_l2"] < 1e-2
+          and res.get("wait_errors", 0) == 0)
     res["ok"] = ok
     if not ok:
         raise AssertionError(f"smoke check failed: {res}")

@@ -1148,6 +1148,8 @@ class Dense8SEncoder(_PassRunner):
                 prog.append(Step("final", bi, -1, (), "d8s_final"))
         self.program = prog
         self._checked = any(s.entry == "d8s_dense_block_parts" for s in prog)
+        # bands per image of the widest banded launch: its share of the CUs a wait needs resident
+        self.max_bands = max((s.args.parts for s in prog if s.entry == "d8s_dense_block_parts"), default=0)
         if self._checked and self._report is None:
             # a host-mapped word the final kernel copies the banded blocks' error count into
             self._report = torch.zeros(2, dtype=torch.int32).pin_memory()
@@ -1404,9 +1406,9 @@ def encode_concurrent(calls) -> list[torch.Tensor]:
     """Several runners at once: `calls` = [(runner, x, flip), ...], every runner on its own stream, the
     caller's current stream joined after all of them.  The seeds of an ensemble read the same input and
     are independent, so one runner's small late-block layers overlap another's work.  Runners with
-    banded whole blocks ("parts" kinds) run one after another instead (each one's stream waits for the
-    previous one's), so that two banded launches are never in flight together: their workgroups wait
-    for their neighbour bands, which must be resident at the same time.
+    banded whole blocks ("parts" kinds) overlap only while their bands per image fit the CUs together
+    (`concurrent_order`): a banded workgroup waits for its neighbour bands, which must be resident at
+    the same time.
 
     Each call is made with the runner's own stream current: an extra stream per call would share one
     of the device's few hardware queues with another runner, and an event recorded there would make
@@ -1421,9 +1423,10 @@ def encode_concurrent(calls) -> list[torch.Tensor]:
     for enc, _, _ in calls:
         enc.stream.wait_stream(caller)
     outs = []
-    for (enc, x, flip), after in zip(calls, concurrent_order([enc for enc, _, _ in calls])):
-        if after is not None:
-            enc.stream.wait_stream(calls[after][0].stream)
+    runners = [enc for enc, _, _ in calls]
+    for (enc, x, flip), after in zip(calls, concurrent_order(runners, _cu_count(dev))):
+        for j in after:
+            enc.stream.wait_stream(runners[j].stream)
         with torch.cuda.stream(enc.stream):
             outs.append(enc(x, flip=flip))
     for enc, _, _ in calls:
@@ -1431,17 +1434,26 @@ def encode_concurrent(calls) -> list[torch.Tensor]:
     return outs
 
 
-def concurrent_order(runners) -> list[int | None]:
-    """For each runner of `encode_concurrent`, the index of the runner whose stream it must wait for
-    first (None: none): each runner with banded whole blocks (`_checked`) waits for the previous such
-    runner, the others run free."""
-    order, last = [], None
+def concurrent_order(runners, cus: int = 256) -> list[list[int]]:
+    """For each runner of `encode_concurrent`, the runners whose streams it waits for first.  A banded
+    launch progresses while the banded launches in flight together have at most `cus` bands per image
+    in all (each then has a whole image resident), so runners with banded blocks (`max_bands` > 0:
+    their launches follow each other on their own stream) are grouped in order while their bands per
+    image fit `cus`; a runner that does not fit waits for every runner of the group before it and
+    starts the next group.  Runners without banded blocks run free."""
+    order, group, load = [], [], 0
     for i, enc in enumerate(runners):
-        if getattr(enc, "_checked", False):
-            order.append(last)
-            last = i
+        k = int(getattr(enc, "max_bands", 0) or 0)
+        if not k:
+            order.append([])
+            continue
+        if group and load + k > cus:
+            order.append(list(group))
+            group, load = [], 0
         else:
-            order.append(None)
+            order.append([])
+        group.append(i)
+        load += k
     return order
 
 

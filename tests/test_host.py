@@ -169,31 +169,13 @@ def test_written_bumps_versions():
     assert dense8s.contents_id(t) != dense8s.contents_id(t)     # no version counter: always new
 
 
-def test_concurrent_order_serialises_banded_runners():
-    """encode_concurrent: runners with banded whole blocks wait for the previous such runner's stream
-    (two banded launches never in flight together), the others run free."""
+def test_concurrent_order_keeps_banded_runners_within_the_cus():
+    """encode_concurrent: runners with banded whole blocks overlap while their bands per image sum to at
+    most the CU count; one that does not fit waits for every banded runner before it (the group), the
+    others run free."""
     import types
-    rs = [types.SimpleNamespace(_checked=c) for c in (True, False, True, True, False)]
-    assert dense8s.concurrent_order(rs) == [None, None, 0, 2, None]
+    rs = [types.SimpleNamespace(max_bands=k) for k in (8, 0, 8, 200, 100, 0, 8)]
+    assert dense8s.concurrent_order(rs, 256) == [[], [], [], [], [0, 2, 3], [], []]
+    assert dense8s.concurrent_order(rs, 16) == [[], [], [], [0, 2], [3], [], [4]]
+    assert dense8s.concurrent_order([types.SimpleNamespace(max_bands=8)] * 3, 256) == [[], [], []]
     assert dense8s.concurrent_order([]) == []
-
-
-def test_recorded_block_kinds(plan169):
-    """A package's per-block "fused" field (pack_meta(fused=...)) is what fused_blocks returns when the
-    caller asks for none: this runner's kinds as recorded (checked: a kind the block cannot run is a
-    ValueError), the reference's names mapped ("img3" -> "img" where a workgroup per image fits, else
-    the default; "tile" -> "tile"), unrecorded blocks at their default."""
-    _, plan = plan169
-    default = dense8s.fused_blocks(dense8s.pack_meta(plan, 24))
-    assert default == {0: "tile", 1: "chain", 2: "parts:8", 3: "parts:8"}
-    meta = dense8s.pack_meta(plan, 24, fused={0: "conv", "b2": "chain", 3: "img"})
-    assert [b["fused"] for b in meta["blocks"]] == ["conv", None, "chain", "img"]
-    assert dense8s.fused_blocks(meta) == {0: "conv", 1: "chain", 2: "chain", 3: "img"}
-    ref = dense8s.pack_meta(plan, 24, fused={"b3": "img3", "b2": "img3", "b1": "tile"})
-    assert dense8s.fused_blocks(ref) == {0: "tile", 1: "tile", 2: "parts:8", 3: "img"}
-    with pytest.raises(ValueError):
-        dense8s.fused_blocks(dense8s.pack_meta(plan, 24, fused={0: "img"}))
-    assert dense8s.fused_blocks(meta, {1: "tile"}) == {0: "conv", 1: "tile", 2: "conv", 3: "conv"}
-    opts = dense8s.kind_options(meta["blocks"][3], 24)
-    assert opts[:4] == ["conv", "chain", "tile", "img"] and "parts:8" in opts
-    assert dense8s.kind_options(meta["blocks"][0], 24) == ["conv", "tile", "parts:128"]

@@ -82,3 +82,10 @@ def test_gate_needs_checked_launches(small_pass):
     res["block"] = {"launches": 0, "mismatch": 0, "max_diff": 0}
     with pytest.raises(AssertionError):
         checks.smoke_gate(res)
+
+
+def test_expired_band_wait_fails_the_gate(small_pass):
+    res = _res(small_pass, small_pass["trace"])
+    res["wait_errors"] = 2
+    with pytest.raises(AssertionError):
+        checks.smoke_gate(res)
