@@ -3621,13 +3621,15 @@ static int band_launch(const D8sDenseArgs* a, const D8sDenseArgs* b, hipStream_t
     const size_t shm = S::lds(a->G);
     if (shm + 36864 > 160 * 1024 || a->G > 16) return -1;
     const int np = b ? 2 : 1;
-    // band height: the least of rounds x (rows + 2) over 32, 16, ... down to RS (one workgroup per CU;
-    // each band also computes the two bottleneck rows above it): 16 rows at 96 images; at 24, 16
-    // rows in one round instead of 4 in three took the study from 1.489-1.493 to 1.454-1.459 ms
+    // band height: the least of rounds x (rows + 2) over the multiples of RS up to 32 (one workgroup
+    // per CU; each band also computes the two bottleneck rows above it; ties go to the taller band):
+    // 16 rows at 96 images (768 bands, three rounds); 14 at 24 (240 bands in one round: 16 row-steps
+    // of work instead of 18 with 16-row bands, which took the study from 1.489-1.493 to 1.454-1.459
+    // ms against 4-row bands in three rounds)
     int rows = 32;
     {
         int64_t best = -1;
-        for (int r = 32; r >= S::RS; r /= 2) {
+        for (int r = 32; r >= S::RS; r -= S::RS) {
             const int64_t nb = (int64_t)a->N * np * ((a->H + r - 1) / r);
             const int64_t cost = (nb + cu_count() - 1) / cu_count() * (r + 2);
             if (best < 0 || cost < best) { best = cost; rows = r; }
@@ -3911,12 +3913,21 @@ static int check_stem(const D8sStemArgs* a, const char* what) {
 static int stem_dispatch(const D8sStemArgs* a, const D8sStemArgs* b, hipStream_t st) {
     const int Hp = a->H / 4, Wp = a->W / 4;
     if (a->W <= 64 * SR_NWV && (int64_t)(a->flip == 2 ? a->N / 2 : a->N) * 3 * a->H * a->W < (1ll << 31)) {
-        // row bands: one wave per 32 conv columns; 16 pooled rows per band while that leaves at
-        // least one workgroup per CU, else fewer
+        // row bands: one wave per 32 conv columns, one workgroup per CU; the band height is the least
+        // of rounds x (rows + 1) over 2 .. 16 pooled rows (a band's first pooled row also needs the
+        // conv row above it; ties go to the taller band): 16 rows at 96 images of 512 px (768 bands,
+        // three rounds), 13 at 24 (240 bands in one round instead of 192 of 16 rows)
         const int np = b ? 2 : 1;
         const int nwv = (a->W / 2 + 31) / 32;
         int rows = 16;
-        while (rows > 2 && (int64_t)a->N * np * ((Hp + rows - 1) / rows) < cu_count()) rows /= 2;
+        {
+            int64_t best = -1;
+            for (int r = 16; r >= 2; --r) {
+                const int64_t nb = (int64_t)a->N * np * ((Hp + r - 1) / r);
+                const int64_t cost = (nb + cu_count() - 1) / cu_count() * (r + 1);
+                if (best < 0 || cost < best) { best = cost; rows = r; }
+            }
+        }
         const int bands = (Hp + rows - 1) / rows;
         const int64_t blocks = (int64_t)a->N * bands;      // per problem
         REQUIRE(blocks * np < (1ll << 31), "d8s_stem: too many bands");
