@@ -15,7 +15,10 @@ back to back, after the timed steps.
 The two seeds' passes of a step run from two streams (`--serial`: one after the other).
 `roofline`: the dominant kernel family: its launches of a configuration-5 pass recorded R times in a HIP
 graph and replayed between HIP events on the encoder's stream (algorithmic bytes of a launch / the
-average launch time).
+average launch time); `frac_in_pass` the same family timed inside a whole pass, `in_schedule` inside a
+pass that shares the GPU with the other seed's; `step_hbm_frac`: both passes' algorithmic bytes over
+the timed step time.  `roofline_c4`: configuration 4's dominant launch (the 32 x 32 banded block)
+against the int8 MFMA peak.  `kernels`: configurations 2 and 3 case by case (`--path kernels` alone).
 `cpu_baseline`: the float32 DenseNet169 forward (`oracle/fp32.py`) on the host cores at batch 1
 (slices/s) and at batch 24 (one study, `study_latency_ms`).
 `mfma_probe`: the int8 MFMA rate measured on the GPU (`d8s_micro_mfma`), beside the 5.0 POP/s datasheet
@@ -716,18 +719,20 @@ def c4_roofline(enc, reps: int, peak_tops: float | None) -> dict:
     return out
 
 
-def family_in_schedule(encs, x, reps: int, family: str, bytes_per_launch: float) -> dict:
-    """One family's launches timed inside configuration 5's schedule: seed 1's pass replays its graph on
-    its stream while seed 0's pass is launched on its own, with events only around the family's
-    launches (before the first and after the last of each contiguous run of them: block 2's chained
-    launches, block 0's fused layers); the summed spans / launches, mean over `reps` steps (after a
-    warm one), and the algorithmic bytes per launch over it against 8 TB/s."""
+def family_in_pass(encs, x, reps: int, family: str, bytes_per_launch: float, concurrent: bool) -> dict:
+    """One family's launches timed inside a whole configuration-5 pass of seed 0 (launched eagerly after a
+    5 ms hold of its stream, during which the host enqueues every launch, so the pass runs as its graph
+    would), with events only around the family's launches (before the first and after the last of each
+    contiguous run: block 2's chained launches, block 0's fused layers); the summed spans / launches,
+    mean over `reps` passes after a warm one, and the algorithmic bytes per launch over it against 8 TB/s.
+    `concurrent`: seed 1's pass replays its graph on its own stream starting with it (the two passes
+    then share the GPU phase by phase, the most the two-stream schedule can overlap them)."""
     enc = encs[0]
     prog = enc.program
     idx = [i for i, s in enumerate(prog) if s.family == family]
     if not idx or idx[0] == 0:
         return {}
-    runs = []                                         # (step before the run, last step of the run)
+    runs = []                                         # [step before the run, last step of the run, index]
     for i in idx:
         if runs and runs[-1][2] == i - 1:
             runs[-1][1], runs[-1][2] = prog[i], i
@@ -746,15 +751,14 @@ def family_in_schedule(encs, x, reps: int, family: str, bytes_per_launch: float)
                 e.record(enc.stream)
                 ev[m] = e
         torch.cuda.synchronize()
-        # both passes start together after a 5 ms hold on seed 0's stream, during which the host
-        # enqueues seed 0's launches: the eager pass then runs as fast as its graph would
         with torch.cuda.stream(enc.stream):
             torch.cuda._sleep(12_000_000)
             gate = torch.cuda.Event()
             gate.record(enc.stream)
-        encs[1].stream.wait_event(gate)
-        with torch.cuda.stream(encs[1].stream):
-            encs[1](x, flip="tta")
+        if concurrent:
+            encs[1].stream.wait_event(gate)
+            with torch.cuda.stream(encs[1].stream):
+                encs[1](x, flip="tta")
         with torch.cuda.stream(enc.stream):
             enc.launch(x, flip="tta", after=after)
         torch.cuda.synchronize()
@@ -764,9 +768,8 @@ def family_in_schedule(encs, x, reps: int, family: str, bytes_per_launch: float)
     gbs = bytes_per_launch / (ms * 1e-3) / 1e9
     return {"family": family, "launches": len(idx), "avg_launch_ms": round(ms, 5), "gbs": round(gbs, 1),
             "frac": round(gbs / HBM_PEAK_GBS, 4),
-            "schedule": "seed 0 eager (enqueued during a hold of its stream, so no host gap) with events "
-                        "around the family's runs of launches, seed 1's graph replay on its own stream "
-                        "starting with it"}
+            "timed": ("inside seed 0's pass with seed 1's pass on another stream from the same start "
+                      "(the two share the GPU)" if concurrent else "inside seed 0's pass, alone")}
 
 
 def bench_c4(dev: torch.device, passes: int, reps: int) -> dict:
@@ -1299,10 +1302,11 @@ def main() -> None:
     fam_tops = {k: round(ops[k] / (fam[k] * 1e-3) / 1e12, 1) for k in ops if fam.get(k)}
     log(f"pass of {nb}: {pass_ms:.3f} ms; families ms {json.dumps({k: round(v, 3) for k, v in fam.items()})}")
     log(f"families GB/s {fam_gbs}; int8 TOP/s {fam_tops}")
-    # the dominant family inside configuration 5's own two-stream schedule (the isolated figure above
-    # replays its launches back to back)
-    in_pass = family_in_schedule(encs, studies[0], args.prof_reps, dom, dom_bytes / launches)
-    log(f"{dom} launches inside the two-stream schedule: {in_pass}")
+    # the dominant family inside a whole pass, alone and beside the other seed's pass (the isolated
+    # figure above replays its launches back to back)
+    in_pass = family_in_pass(encs, studies[0], args.prof_reps, dom, dom_bytes / launches, False)
+    in_sched = family_in_pass(encs, studies[0], args.prof_reps, dom, dom_bytes / launches, True)
+    log(f"{dom} launches inside a pass: {in_pass}; beside the other seed's pass: {in_sched}")
     total_bytes = sum(sum(v) for v in byts.values())
     out = {
         "metric": "512px DenseNet169 INT8 slices/sec on 1 MI355X; 24-slice study latency ms",
@@ -1333,7 +1337,8 @@ def main() -> None:
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": committed_traffic(dom),
                      "algorithmic_bytes_per_launch": int(dom_bytes / launches),
                      "avg_launch_ms": round(avg_ms, 5),
-                     "frac_in_pass": in_pass.get("frac"), "in_pass": in_pass},
+                     "frac_in_pass": in_pass.get("frac"), "in_pass": in_pass, "in_schedule": in_sched},
+        "step_hbm_frac": round(2 * total_bytes / (dt / args.steps) / 1e9 / HBM_PEAK_GBS, 4),
         "roofline_c4": roof4,
     }
     # the upstream preparation (raw crops -> uint8 volume), its own throughput on the same GPU

@@ -28,6 +28,7 @@ Quantisation (as the reference's final path: fp16 prologues everywhere, u8 bottl
 from __future__ import annotations
 
 import collections
+import contextlib
 import ctypes
 import itertools
 import json
@@ -520,14 +521,20 @@ class GraphInput:
             return False
         for ev in self.readers.values():
             stream.wait_event(ev)
-        self.readers.clear()
         self.buf[:n].copy_(x)
         self.source, self.ident = x, ident
-        self.copied = _record_sync(stream)
+        if self.copied is None:
+            self.copied = torch.cuda.Event()
+        self.copied.record(stream)
         return True
 
     def read_by(self, runner, stream) -> None:
-        self.readers[id(runner)] = _record_sync(stream)
+        """Marks the end of `runner`'s last replay reading the buffer (one event per runner, recorded
+        again each time: a wait enqueued earlier keeps the record it saw)."""
+        ev = self.readers.get(id(runner))
+        if ev is None:
+            ev = self.readers[id(runner)] = torch.cuda.Event()
+        ev.record(stream)
 
 
 _GRAPH_INPUTS: dict[tuple, GraphInput] = {}
@@ -875,22 +882,22 @@ class _PassRunner:
             self._launch_pass(self._staged(x[index * per:(index + 1) * per], mode), index, mode)
             self._gate.done(self.stream)
 
-    def _run_graphs(self, x: torch.Tensor, graphs: list, shared: GraphInput) -> None:
+    def _run_graphs(self, x: torch.Tensor, graphs: list, shared: GraphInput, launch) -> None:
         n = x.shape[0]
         own = shared.buf[:n]
         if x.data_ptr() == own.data_ptr() and x.shape == own.shape and x.stride() == own.stride():
             shared.forget()                   # the caller wrote the graph input in place
-        elif shared.load(x, n, self.stream):
+        elif shared.load(x, n, launch):
             self.calls["copy"] = self.calls.get("copy", 0) + 1
         for g in graphs:
             self._gate.admit()
             g.replay()
-            self._gate.done(self.stream)
-        shared.read_by(self, self.stream)
+            self._gate.done(launch)
+        shared.read_by(self, launch)
 
     def capture(self, n: int, flip=False) -> float:
         """One HIP graph per pass over a batch of `n` input images (the reference's `capture`,
-        `src/knee/dense8s.py:1410-1433`), recorded on the launch stream after one eager pass (which does
+        `src/knee/dense8s.py:1410-1433`), recorded on the runner's stream after one eager pass (which does
         any lazy set-up outside the capture); returns the seconds spent."""
         mode = self._mode(flip)
         per = self._per_pass(mode)
@@ -899,12 +906,10 @@ class _PassRunner:
             raise ValueError(f"graph for {n} images: the encoder does {self.nb} per pass, "
                              f"the output holds {self.n_out}")
         t0 = time.perf_counter()
-        with torch.cuda.device(self.dev):
-            shared = graph_input(self.dev, (passes * per, *self.in_shape[1:]), self.in_dtype)
-            shared.forget()
-            self._join(torch.cuda.current_stream(self.dev))
-            with torch.cuda.stream(self.stream):
-                self._launch_pass(shared.buf.data_ptr(), 0, mode)
+        shared = graph_input(self.dev, (passes * per, *self.in_shape[1:]), self.in_dtype)
+        shared.forget()
+        with self._launching():
+            self._launch_pass(shared.buf.data_ptr(), 0, mode)
             self.stream.synchronize()
             self._gate.clear()
             graphs = []
@@ -913,7 +918,7 @@ class _PassRunner:
                 with torch.cuda.graph(g, stream=self.stream, capture_error_mode="thread_local"):
                     self._launch_pass(shared.buf[index * per].data_ptr(), index, mode)
                 graphs.append(g)
-            self.stream.synchronize()
+        self.stream.synchronize()
         self.graphs.add(passes * per, mode, graphs, shared)
         return time.perf_counter() - t0
 
@@ -923,27 +928,69 @@ class _PassRunner:
         hit = self.graphs.find(n, mode, self._per_pass(mode))
         return None if hit is None else hit[1].buf[:n]
 
-    def _join(self, caller) -> None:
-        self.stream.wait_stream(caller)
+    def _event(self, name: str) -> torch.cuda.Event:
+        """A synchronisation event of this runner, made once and recorded again at every use (a wait
+        enqueued on it keeps the record it saw): no event is created per call."""
+        ev = self.__dict__.get(name)
+        if ev is None:
+            ev = self.__dict__[name] = torch.cuda.Event()
+        return ev
+
+    # Ordering.  Every launch of a runner (calls, captures, diagnostics) is made inside `_launching`:
+    # on the launch stream, after the caller's current stream's work so far and after the runner's own
+    # previous launches (on whichever stream they ran: its buffers are reused), and before what the
+    # caller enqueues next.  Each cross-stream dependency is one event wait, which the host pays for
+    # (about 16 us on this stack for a pending event): a graph replay of a call is therefore made on
+    # the caller's own stream when the runner allows it (`_adopt`), where stream order gives all of
+    # that with no wait at all as long as the calls come from one stream.
+    _adopt = False
+    _tail = None                          # the stream of the runner's last launches (None: none yet)
+
+    def _owners(self) -> tuple:
+        """The runners whose buffers this one's launches use (itself; both encoders for a pair)."""
+        return (self,)
+
+    @contextlib.contextmanager
+    def _launching(self, adopt: bool = False):
+        switch = torch.cuda.current_device() != self.dev
+        with torch.cuda.device(self.dev) if switch else contextlib.nullcontext():
+            caller = torch.cuda.current_stream()
+            launch = caller if adopt else self.stream
+            if launch != caller:
+                ev = self._event("_ev_in")
+                ev.record(caller)
+                launch.wait_event(ev)
+            for r in self._owners():
+                if r._tail is not None and r._tail != launch:
+                    launch.wait_event(r._event("_ev_tail"))
+            with torch.cuda.stream(launch) if launch != caller else contextlib.nullcontext():
+                yield launch
+            for r in self._owners():
+                r._event("_ev_tail").record(launch)
+                r._tail = launch
+            if launch != caller:
+                caller.wait_event(self._owners()[0]._event("_ev_tail"))
+
+    def _settle(self) -> None:
+        """Waits on the host for the runner's launches so far."""
+        for r in self._owners():
+            (r._tail or r.stream).synchronize()
 
     def _encode(self, x: torch.Tensor, flip):
-        """Encodes x on the launch stream, ordered after the caller's current stream and before what the
-        caller enqueues next; returns `_outputs`."""
+        """Encodes x, ordered after the caller's current stream and before what the caller enqueues next;
+        returns `_outputs`."""
         mode = self._mode(flip)
         self._accept(x, mode)
-        caller = torch.cuda.current_stream(self.dev)
-        self._join(caller)
-        with torch.cuda.device(self.dev), torch.cuda.stream(self.stream):
-            hit = self.graphs.find(x.shape[0], mode, self._per_pass(mode))
+        hit = self.graphs.find(x.shape[0], mode, self._per_pass(mode))
+        with self._launching(adopt=self._adopt and hit is not None) as launch:
             if hit is None:
                 self._run_eager(x.contiguous(), mode)
                 self.calls["plain"] += 1
             else:
-                self._run_graphs(x, *hit)
+                self._run_graphs(x, *hit, launch)
                 self.calls["graph"] += 1
             res = self._outputs(x.shape[0], mode)
         self._mark_written()
-        caller.wait_stream(self.stream)
         return res
 
 
@@ -969,6 +1016,7 @@ class Dense8SEncoder(_PassRunner):
         if missing:
             raise ValueError(f"package tables missing: {missing[:4]}{'...' if len(missing) > 4 else ''}")
         self.meta, self.dev = meta, int(dev)
+        self.device = torch.device(f"cuda:{self.dev}")
         self.lib = hip.library()
         self.library_version = hip.version()
         self.pack_sha = meta.get("kernels_sha")
@@ -1153,6 +1201,7 @@ class Dense8SEncoder(_PassRunner):
         if self._checked and self._report is None:
             # a host-mapped word the final kernel copies the banded blocks' error count into
             self._report = torch.zeros(2, dtype=torch.int32).pin_memory()
+            self._report_np = self._report.numpy()
             dptr = ctypes.c_void_p()
             hip.check(self.lib.d8s_host_mapped(self._report.data_ptr(), ctypes.byref(dptr)), "d8s_host_mapped")
             self._report_dev = int(dptr.value or 0)
@@ -1195,7 +1244,7 @@ class Dense8SEncoder(_PassRunner):
         if tuple(x.shape[1:]) != self.in_shape[1:]:
             raise ValueError(f"input {tuple(x.shape)}: expected (N, "
                              f"{', '.join(map(str, self.in_shape[1:]))})")
-        if x.device != torch.device(f"cuda:{self.dev}"):
+        if x.device != self.device:
             raise ValueError(f"input on {x.device}, encoder on cuda:{self.dev}")
         if mode == 2 and self.nb % 2:
             raise ValueError(f"flip-TTA pairs need an even images-per-pass, the package has {self.nb}")
@@ -1219,6 +1268,8 @@ class Dense8SEncoder(_PassRunner):
     def _mark_written(self) -> None:
         hip.written(self.out)
 
+    _adopt = True                         # a call's graph replay runs on the caller's stream
+
     def __call__(self, x: torch.Tensor, flip=False) -> torch.Tensor:
         return self._encode(x, flip)
 
@@ -1227,7 +1278,7 @@ class Dense8SEncoder(_PassRunner):
         """Raises PartsWaitError if a pass since the last check reported expired waits (the host-mapped
         word the final kernel writes: read without a synchronisation; a pass still running is seen at
         a later call or by `sync_errors`)."""
-        if self._report is None or int(self._report[0]) == 0:
+        if self._report is None or self._report_np[0] == 0:
             return
         count = self._clear_wait_errors()
         raise PartsWaitError("d8s_dense_block_parts", 1,
@@ -1238,7 +1289,7 @@ class Dense8SEncoder(_PassRunner):
         """Waits for the runner's stream, then zeroes the banded blocks' ticket, end and error words
         (the launch count stays: it names the exchange rows) and the host report; returns the count."""
         with torch.cuda.device(self.dev):
-            self.stream.synchronize()
+            self._settle()
             count = int(self._sync[2].item())
             self._sync[:3].zero_()
             torch.cuda.synchronize(self.dev)
@@ -1252,7 +1303,7 @@ class Dense8SEncoder(_PassRunner):
         if clear:
             return self._clear_wait_errors()
         with torch.cuda.device(self.dev):
-            self.stream.synchronize()
+            self._settle()
             return int(self._sync[2].item())
 
     # -- diagnostics --
@@ -1283,8 +1334,7 @@ class Dense8SEncoder(_PassRunner):
         launch is enqueued (e.g. to record events at chosen steps)."""
         mode = self._mode(flip)
         x_ptr = self._pass_input(x, mode)
-        with torch.cuda.device(self.dev), torch.cuda.stream(self.stream):
-            self._join(torch.cuda.current_stream(self.dev))
+        with self._launching():
             self._launch_pass(x_ptr, 0, mode, after)
 
     def _pass_input(self, x: torch.Tensor, mode: int) -> int:
@@ -1307,8 +1357,7 @@ class Dense8SEncoder(_PassRunner):
                 snaps[key] = (self.bottleneck(key[1], key[2]) if key[0] == "bott" else self.store(*key)).clone()
 
         st = self.stream.cuda_stream
-        with torch.cuda.device(self.dev), torch.cuda.stream(self.stream):
-            self._join(torch.cuda.current_stream(self.dev))
+        with self._launching():
             for step in self.program:
                 self._launch(step, st, x_ptr, f.data_ptr(), mode)
                 snapshot(step)
@@ -1321,8 +1370,7 @@ class Dense8SEncoder(_PassRunner):
         mode = self._mode(flip)
         x_ptr = self._pass_input(x, mode)
         sums: dict[str, float] = collections.defaultdict(float)
-        with torch.cuda.device(self.dev), torch.cuda.stream(self.stream):
-            self._join(torch.cuda.current_stream(self.dev))
+        with self._launching():
             for r in range(reps + 1):
                 marks = [(None, _record(self.stream))]
                 self._launch_pass(x_ptr, 0, mode, after=lambda s: marks.append((s.tag(), _record(self.stream))))
@@ -1337,7 +1385,7 @@ class Dense8SEncoder(_PassRunner):
         times between events after one warm replay; the median replay."""
         st = self.stream.cuda_stream
         f_ptr = self.out.data_ptr()
-        with torch.cuda.device(self.dev), torch.cuda.stream(self.stream):
+        with self._launching():
             for s in steps:
                 self._launch(s, st, x_ptr, f_ptr, mode)
             self.stream.synchronize()
@@ -1359,8 +1407,7 @@ class Dense8SEncoder(_PassRunner):
         """One eager pass over x (fills the store every later timing reads); returns (x_ptr, mode)."""
         mode = self._mode(flip)
         x_ptr = self._pass_input(x, mode)
-        with torch.cuda.device(self.dev), torch.cuda.stream(self.stream):
-            self._join(torch.cuda.current_stream(self.dev))
+        with self._launching():
             self._launch_pass(x_ptr, 0, mode)
         return x_ptr, mode
 
@@ -1486,14 +1533,14 @@ class EncoderPair(_PassRunner):
         self.in_shape, self.in_dtype = a.in_shape, a.in_dtype
         self.stream = a.stream
         self.lib = a.lib
+        self.device = a.device
         self.graphs = GraphBook()
         self.calls = {"graph": 0, "plain": 0, "copy": 0}
         self._gate = InflightGate(None)
         self._staging: torch.Tensor | None = None
 
-    def _join(self, caller) -> None:
-        self.stream.wait_stream(caller)
-        self.stream.wait_stream(self.b.stream)
+    def _owners(self) -> tuple:
+        return (self.a, self.b)
 
     def _accept(self, x: torch.Tensor, mode: int) -> None:
         self.a._accept(x, mode)
@@ -1522,16 +1569,7 @@ class EncoderPair(_PassRunner):
     def __call__(self, x: torch.Tensor, flip=False) -> tuple[torch.Tensor, torch.Tensor]:
         """Both encoders' features of x: (outputs of the first, outputs of the second), as each
         encoder's `__call__` returns them."""
-        res = self._encode(x, flip)
-        self.b.stream.wait_stream(self.stream)
-        return res
-
-
-def _record_sync(stream) -> torch.cuda.Event:
-    """An event without timing on `stream`: orders the shared graph input between runners' streams."""
-    e = torch.cuda.Event()
-    e.record(stream)
-    return e
+        return self._encode(x, flip)
 
 
 def _record(stream) -> torch.cuda.Event:
