@@ -183,6 +183,51 @@ def test_mfma_summary_weights_and_issued_ops(tmp_path):
     assert float(cells[3]) == pytest.approx(2e6 * 512 / 1e9, abs=0.05)
 
 
+def test_block_work_closed_form():
+    """A whole block's algorithmic work: its input read once, 32 new channels per layer written, the
+    weights once; operations 2 per MAC of every conv1 and conv2 (block 2 of a 24-image study: 209.4 G)."""
+    b = BLOCKS[2]
+    byts, ops = bench.block_work(b, 24)
+    M = 24 * b["h"] * b["w"]
+    w = sum(128 * (b["c0"] + 32 * l) + (b["c0"] + 32 * l) * 4 + 128 * 12 + 36864 + 32 * 8 for l in range(b["L"]))
+    assert byts == M * b["c0"] + M * 32 * b["L"] + w
+    assert ops == sum(2.0 * M * (b["c0"] + 32 * l) * 128 + 2.0 * M * 1152 * 32 for l in range(b["L"]))
+    assert abs(ops / 1e9 - 209.38) < 0.01
+    # the same work as the block's launches counted layer by layer
+    per = bench.kernel_ops({"img": 512, "blocks": BLOCKS}, 24, {2: "parts:8"})
+    assert abs(per["block"] - ops) < 1.0
+
+
+def test_c4_counter_summary_per_banded_kernel(tmp_path):
+    """Configuration 4's banded-block counters: traffic per launch scaled by the copy kernel against
+    `block_work`, MfmaUtil weighted by GRBM_GUI_ACTIVE, the wave cycles as percentages."""
+    gib = 1 << 30
+    copy = "k_copy(const u32x4*, u32x4*, long)"
+    k4, k1 = "void k_dparts<4>(D8sPartsArgs)", "void k_dparts<1>(D8sPartsArgs)"
+    fe = [(1, copy, "FETCH_SIZE", gib / 2 / 1024)] + [(d, k4, "FETCH_SIZE", 10e6 / 1024) for d in (2, 3)]
+    fe += [(d, k1, "FETCH_SIZE", 5e6 / 1024) for d in (4, 5)]
+    wr = [(1, copy, "WRITE_SIZE", gib / 1024)] + [(d, k4, "WRITE_SIZE", 30e6 / 1024) for d in (2, 3)]
+    wr += [(d, k1, "WRITE_SIZE", 4e6 / 1024) for d in (4, 5)]
+    mf = [(2, k4, "MfmaUtil", 10.0), (2, k4, "GRBM_GUI_ACTIVE", 100.0), (2, k4, "SQ_INSTS_VALU_MFMA_MOPS_I8", 1e6),
+          (3, k4, "MfmaUtil", 20.0), (3, k4, "GRBM_GUI_ACTIVE", 300.0), (3, k4, "SQ_INSTS_VALU_MFMA_MOPS_I8", 1e6)]
+    wv = [(2, k4, "SQ_WAVE_CYCLES", 1000.0), (2, k4, "SQ_WAIT_ANY", 450.0), (2, k4, "SQ_WAIT_INST_ANY", 150.0),
+          (2, k4, "SQ_ACTIVE_INST_ANY", 400.0), (2, k4, "SQ_ACTIVE_INST_VALU", 200.0)]
+    for name, rows in (("f", fe), ("w", wr), ("m", mf), ("s", wv)):
+        _counter_csv(tmp_path / name / "run_counter_collection.csv", rows)
+    out = bench.c4_counter_summary(*(str(tmp_path / d) for d in "fwms"), passes=1)
+    line = next(ln for ln in out.splitlines() if ln.startswith("| `k_dparts<4>`"))
+    cells = [c.strip() for c in line.strip("|").split("|")]
+    byts, ops = bench.block_work(BLOCKS[2], 24)
+    assert cells[1] == "2 (parts:8)" and cells[2] == "2"
+    assert float(cells[3]) == pytest.approx(20.0, abs=0.01) and float(cells[4]) == pytest.approx(30.0, abs=0.01)
+    assert float(cells[5]) == pytest.approx(50e6 / byts, abs=1e-3)
+    assert float(cells[6]) == pytest.approx(17.5, abs=0.05)              # (10 x 100 + 20 x 300) / 400
+    assert float(cells[7]) == pytest.approx(1e6 * 512 / 1e9, abs=0.05)  # per launch
+    assert float(cells[8]) == pytest.approx(ops / 1e9, abs=0.05)
+    assert cells[9:13] == ["45.0", "15.0", "40.0", "20.0"]
+    assert any(ln.startswith("| `k_dparts<1>`") for ln in out.splitlines())
+
+
 def test_more_than_one_gpu_is_refused():
     env = dict(os.environ, PYTHONPATH=str(ROOT))
     r = subprocess.run([sys.executable, str(ROOT / "bench.py"), "--gpus", "2"], capture_output=True,

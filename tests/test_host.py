@@ -179,3 +179,46 @@ def test_concurrent_order_keeps_banded_runners_within_the_cus():
     assert dense8s.concurrent_order(rs, 16) == [[], [], [], [0, 2], [3], [], [4]]
     assert dense8s.concurrent_order([types.SimpleNamespace(max_bands=8)] * 3, 256) == [[], [], []]
     assert dense8s.concurrent_order([]) == []
+
+
+def test_graph_book_finds_the_smallest_covering_capture():
+    """A batch replays the graphs captured for its size, else the first passes of the smallest capture
+    that covers it (per flip mode), else none."""
+    book = dense8s.GraphBook()
+    book.add(48, 0, ["a0", "a1"], "s48")
+    book.add(96, 0, ["b0", "b1", "b2", "b3"], "s96")
+    book.add(24, 2, ["t0", "t1"], "st")
+    assert book.find(48, 0, 24) == (["a0", "a1"], "s48")
+    assert book.find(20, 0, 24) == (["a0"], "s48")
+    assert book.find(60, 0, 24) == (["b0", "b1", "b2"], "s96")
+    assert book.find(97, 0, 24) is None
+    assert book.find(12, 2, 12) == (["t0"], "st") and book.find(24, 1, 24) is None
+    assert len(book) == 3 and bool(book)
+    book.clear()
+    assert not book
+
+
+def test_regions_are_aligned_and_disjoint():
+    r = dense8s.Regions()
+    r.reserve("a", 1000)
+    r.reserve("b", 10)
+    r.reserve("c", 300)
+    spans = sorted(r.spans.values())
+    assert all(start % dense8s.Regions.ALIGN == 0 for start, _ in spans)
+    assert all(s0 + n0 <= s1 for (s0, n0), (s1, _) in zip(spans, spans[1:]))
+    assert r.size == spans[-1][0] + spans[-1][1] and "b" in r and "z" not in r
+
+
+def test_step_names_follow_the_family():
+    s = dense8s.Step("chain", 2, 5, ((2, 6), ("bott", 2, 6)), "d8s_conv2_conv1")
+    assert s.tag() == "chain_2" and s.label() == "cc b2l5"
+    assert dense8s.Step("trans", 1, -1, ((2, 0),), "d8s_transition").label() == "t1"
+    assert dense8s.Step("block", 3, -1, (), "d8s_dense_block").label() == "blk b3"
+    assert dense8s.Step("stem", 0, -1, ((0, 0),), "d8s_stem").tag() == "stem"
+
+
+def test_inflight_gate_without_a_limit_records_nothing():
+    g = dense8s.InflightGate(None)
+    g.admit()
+    g.done(None)
+    assert len(g.events) == 0
