@@ -134,46 +134,60 @@ def calibrate(encoder, batches) -> dict:
 # --- plan -----------------------------------------------------------------------------------
 @dataclass
 class SLayer:
+    """What the INT8 path needs of one dense layer reading `c_in` store channels.
+
+    conv1 side: norm1 as the float64 affine (a1, b1) over the c_in inputs and the u8 input scale s1;
+    the int8 weights w1 [128, c_in] with norm2's sign folded into their rows (`fold_norm2`), w1s the
+    positive per-row factor (weight scale times |norm2 gain|) and bias1 norm2's shift.  conv2 side:
+    the int8 input scale s2, the int8 weights w2 [32, 128, 3, 3] with their per-row scales w2s, and
+    sig, the store scale of the 32 channels the layer appends."""
     c_in: int
-    a1: np.ndarray              # norm1 as an affine [c_in] (float64)
+    a1: np.ndarray
     b1: np.ndarray
-    s1: float                   # u8 scale of the conv1 input
-    w1: np.ndarray              # int8 [128, c_in], sign of norm2 inside
-    w1s: np.ndarray             # [128] > 0: weight scale times |a2|
-    bias1: np.ndarray           # [128] = b2 of norm2
-    s2: float                   # int8 scale of the conv2 input (amax / 127)
-    w2: np.ndarray              # int8 [32, 128, 3, 3]
-    w2s: np.ndarray             # [32]
-    sig: np.ndarray             # [32] per-channel scale of the output in the store
+    s1: float
+    w1: np.ndarray
+    w1s: np.ndarray
+    bias1: np.ndarray
+    s2: float
+    w2: np.ndarray
+    w2s: np.ndarray
+    sig: np.ndarray
 
 
 @dataclass
 class SBlock:
+    """A dense block of `layers` on h x w maps whose input has c0 channels stored at scales sig0, and,
+    for every block but the last, its transition: the norm affine (ta, tb) over all c_tot channels,
+    the u8 input scale ts, the int8 1 x 1 weights tw [c_tot / 2, c_tot] and their row scales tws."""
     c0: int
     h: int
     w: int
-    sig0: np.ndarray            # [c0] per-channel scale of the block input
+    sig0: np.ndarray
     layers: list[SLayer]
-    ta: np.ndarray | None = None        # transition: norm as an affine [c_tot]
+    ta: np.ndarray | None = None
     tb: np.ndarray | None = None
-    ts: float | None = None             # u8 scale of the transition conv input
-    tw: np.ndarray | None = None        # int8 [c_tot // 2, c_tot]
-    tws: np.ndarray | None = None       # [c_tot // 2]
+    ts: float | None = None
+    tw: np.ndarray | None = None
+    tws: np.ndarray | None = None
 
     @property
     def c_tot(self) -> int:
+        """Channels of the store after the last layer."""
         return self.c0 + GROWTH * len(self.layers)
 
     @property
     def sig_all(self) -> np.ndarray:
-        return np.concatenate([self.sig0] + [L.sig for L in self.layers])
+        """Store scale of every channel after the last layer, in store order."""
+        return np.concatenate([self.sig0, *(layer.sig for layer in self.layers)])
 
 
 @dataclass
 class SPlan:
+    """The whole encoder at img x img: the stem (w0 [64, in_ch, 7, 7] float32 with norm0's gain folded
+    in, b0 its shift), the blocks, and the final norm as the affine (a5, b5)."""
     img: int
     in_ch: int
-    w0: np.ndarray              # stem with norm0 folded in, float32 [64, in_ch, 7, 7]
+    w0: np.ndarray
     b0: np.ndarray
     blocks: list[SBlock] = field(default_factory=list)
     a5: np.ndarray | None = None
@@ -181,6 +195,7 @@ class SPlan:
 
     @property
     def n_features(self) -> int:
+        """Length of the pooled feature vector (the last block's channels)."""
         return self.blocks[-1].c_tot
 
 
