@@ -255,7 +255,9 @@ def family_run_summary(path: str) -> list[str]:
     consecutive dispatches of one family on one queue longer than any run of that family within a pass
     (a pass of the default kinds at 96 images, `kernel_bytes`), the first dispatch of each run not
     counted.  (A pass's own runs, e.g. the 31 chained launches of the 32 x 32 block, are left out: the
-    two seeds' passes run concurrently.)  Their mean duration is the average launch time behind
+    two seeds' passes run concurrently.)  Runs are summed per family and the set of kernels (name and
+    template arguments) they hold, so the 64 x 64 chain of the 24-image study does not mix into the
+    32 x 32 chain of the 96-image pass.  Their mean duration is the average launch time behind
     bench.py's roofline."""
     import csv
     nb = 4 * SLICES
@@ -263,35 +265,37 @@ def family_run_summary(path: str) -> list[str]:
                                                    dense8s.fused_blocks({"blocks": C5_BLOCKS, "n": nb})).items()}
     rows = [r for r in csv.DictReader(open(path)) if _family(r["Kernel_Name"])]
     rows.sort(key=lambda r: int(r["Start_Timestamp"]))
-    runs: dict = {}                                   # queue -> [family, [durations]]
+    runs: dict = {}                                   # queue -> [family, [durations], {kernels}]
     acc: dict = {}
 
     def close(run):
-        fam, ds = run
+        fam, ds, names = run
         if fam != "copy" and len(ds) > per_pass.get(fam, 1):
-            a = acc.setdefault(fam, [0, 0.0])
+            a = acc.setdefault((fam, ", ".join(f"`{k}`" for k in sorted(names))), [0, 0.0])
             a[0] += len(ds) - 1
             a[1] += sum(ds[1:])
 
     for r in rows:
-        fam = _family(r["Kernel_Name"])
+        name = r["Kernel_Name"]
+        fam = _family(name)
         q = r["Queue_Id"]
         us = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
         run = runs.get(q)
-        if run is not None and run[0] == fam:
-            run[1].append(us)
-            continue
-        if run is not None:
-            close(run)
-        runs[q] = [fam, [us]]
+        if run is None or run[0] != fam:
+            if run is not None:
+                close(run)
+            run = runs[q] = [fam, [], set()]
+        run[1].append(us)
+        run[2].add(name.split("(")[0].replace("void ", "").strip())
     for run in runs.values():
         close(run)
     out = [f"### family timing dispatches ({os.path.basename(path)})", "",
            "Runs of dispatches of one family on one queue longer than the family's runs within a pass "
            "(the back-to-back replays of the per-family timing; the first launch of each run not "
-           "counted).", "", "| family | dispatches | mean us |", "|---|---|---|"]
-    for fam, (n, us) in sorted(acc.items()):
-        out.append(f"| {fam} | {n} | {us / n:.2f} |")
+           "counted), by the kernels a run holds.", "", "| family | kernels | dispatches | mean us |",
+           "|---|---|---|---|"]
+    for (fam, kerns), (n, us) in sorted(acc.items()):
+        out.append(f"| {fam} | {kerns} | {n} | {us / n:.2f} |")
     return out + [""]
 
 
@@ -699,13 +703,14 @@ def block_work(b: dict, n: int) -> tuple[float, float]:
 
 
 def c4_roofline(enc, reps: int, peak_tops: float | None) -> dict:
-    """Configuration 4's dominant launch (from `time_layers` on the study's store): its int8 rate against
-    the MFMA peak (a whole block of a 24-image study: thousands of operations per byte, far right of the
-    ridge, so the bound is the matrix cores) and its algorithmic GB/s."""
-    layers = enc.time_layers(reps=reps)
+    """Configuration 4's dominant launch, a whole banded block (`time_layers` of the block launches on the
+    study's store; the other launches of the pass are shorter, `profiles/encoder_c4_kernel_trace.md`):
+    its int8 rate against the MFMA peak (thousands of operations per byte, far right of the ridge, so the
+    bound is the matrix cores) and its algorithmic GB/s."""
+    layers = enc.time_layers(reps=reps, families=("block",))
     label = max(layers, key=layers.get)
     ms = layers[label]
-    out = {"kernel": label, "ms": round(ms, 5), "pass_launch_ms": {k: v for k, v in layers.items() if v >= 0.05}}
+    out = {"kernel": label, "ms": round(ms, 5), "block_launch_ms": layers}
     if label.startswith("blk b"):
         bi = int(label[5:])
         byts, ops = block_work(enc.meta["blocks"][bi], enc.nb)

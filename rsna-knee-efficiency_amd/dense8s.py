@@ -1436,11 +1436,12 @@ class Dense8SEncoder(_PassRunner):
             by_family.setdefault(step.family, []).append(step)
         return {fam: round(self._graph_ms(steps, reps, x_ptr, mode), 4) for fam, steps in by_family.items()}
 
-    def time_layers(self, reps: int = 20) -> dict:
-        """ms of every launch of the pass but the stem and the final features, on the current store
-        (`Step.label`: "c1 b{b}l{l}", "c2 ...", "cc ..." chained, "dn ..." fused layer, "blk b{b}", "t{b}")."""
+    def time_layers(self, reps: int = 20, families=None) -> dict:
+        """ms of every launch of the pass but the stem and the final features (or only those of the
+        kernel families named in `families`), on the current store (`Step.label`: "c1 b{b}l{l}",
+        "c2 ...", "cc ..." chained, "dn ..." fused layer, "blk b{b}", "t{b}")."""
         return {s.label(): round(self._graph_ms([s], reps), 4) for s in self.program
-                if s.family not in ("stem", "final")}
+                if s.family not in ("stem", "final") and (families is None or s.family in families)}
 
     def tune_kinds(self, x: torch.Tensor, reps: int = 10, flip=False, apply: bool = False) -> dict:
         """For every block the ms of its layers run as each kind it can take (`kind_options`), on the

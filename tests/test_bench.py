@@ -113,13 +113,21 @@ def test_family_run_summary_counts_only_the_timing_replays(tmp_path):
         add(chain, 27.0)
     for _ in range(26):                               # conv1's timing: 2 x 13 launches
         add(conv1, 36.0)
+    for _ in range(40):                               # another configuration's chain: its own line
+        add("void k_c21<64>(D8sConv2Args, D8sGemmArgs)", 20.0)
+    for _ in range(8):                                # a family of several kernels: one run
+        for r in (2, 3):
+            add(f"void k_band<128, {r}>(D8sDenseArgs, int, int, D8sDenseArgs, int)", 100.0 + r)
     path = tmp_path / "run_kernel_trace.csv"
     with open(path, "w", newline="") as f:
         w = csv.DictWriter(f, fieldnames=list(rows[0]))
         w.writeheader()
         w.writerows(rows)
     out = "\n".join(bench.family_run_summary(str(path)))
-    assert "| chain | 61 | 27.00 |" in out and "| conv1 | 25 | 36.00 |" in out
+    assert "| chain | `k_c21<32>` | 61 | 27.00 |" in out
+    assert "| conv1 | `k_conv1p<false, 1, 2, 4>` | 25 | 36.00 |" in out
+    assert "| chain | `k_c21<64>` | 39 | 20.00 |" in out
+    assert "| dense | `k_band<128, 2>`, `k_band<128, 3>` | 15 | 102.53 |" in out
 
 
 def test_wave_summary_percentages_of_wave_cycles(tmp_path):
