@@ -978,13 +978,15 @@ class _PassRunner:
             for r in self._owners():
                 if r._tail is not None and r._tail != launch:
                     launch.wait_event(r._event("_ev_tail"))
-            with torch.cuda.stream(launch) if launch != caller else contextlib.nullcontext():
-                yield launch
-            for r in self._owners():
-                r._event("_ev_tail").record(launch)
-                r._tail = launch
-            if launch != caller:
-                caller.wait_event(self._owners()[0]._event("_ev_tail"))
+            try:
+                with torch.cuda.stream(launch) if launch != caller else contextlib.nullcontext():
+                    yield launch
+            finally:                      # also after a failed launch: what was enqueued stays ordered
+                for r in self._owners():
+                    r._event("_ev_tail").record(launch)
+                    r._tail = launch
+                if launch != caller:
+                    caller.wait_event(self._owners()[0]._event("_ev_tail"))
 
     def _settle(self) -> None:
         """Waits on the host for the runner's launches so far."""
