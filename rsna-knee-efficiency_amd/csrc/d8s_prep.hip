@@ -353,6 +353,20 @@ DEV void run_blocks(const PStack& st, const PArgs& a, int b0, int b1, float* s_s
         if constexpr (WROW) tr = __builtin_amdgcn_readfirstlane(tr);
         const int dx0 = ((int)threadIdx.x - ((int)threadIdx.x / a.upr) * a.upr) * UP;
         const bool yact = tr < RS;
+        // bilinear: the taps and weights of the thread's UP output columns dx0 .. dx0 + UP - 1
+        int ba[UP], bb[UP];
+        float bw0[UP], bw1[UP];
+        if constexpr (MODE == M_BILIN) {
+#pragma unroll
+            for (int i = 0; i < UP; ++i) {
+                const float sx = src_index(st.rw, dx0 + i);
+                const int w1 = (int)sx;
+                ba[i] = w1;
+                bb[i] = w1 + (w1 < st.w - 1 ? 1 : 0);
+                bw1[i] = sx - (float)w1;
+                bw0[i] = 1.0f - bw1[i];
+            }
+        }
         Geo nxt = block_geo<MODE>(st, a, b0);
         raw_stage(st, nxt, s_raw0);
         for (int b = b0; b < b1; ++b) {
@@ -366,6 +380,62 @@ DEV void run_blocks(const PStack& st, const PArgs& a, int b0, int b1, float* s_s
             }
             const float sl = HAS ? st.resc[2 * g.kk] : 1.0f, ic = HAS ? st.resc[2 * g.kk + 1] : 0.0f;
             const int e0 = par0 + (g.kk * st.hr + st.y0 + g.s0) * st.wr;
+            if constexpr (MODE == M_BILIN) {
+                // one pass: thread (tr, tc) walks the contiguous rows tr rpg .. (tr + 1) rpg - 1 of the
+                // block down its UP columns and keeps the horizontal interpolations of the two source
+                // rows it combines in registers (consecutive output rows mostly share them when
+                // upsampling); the same operations as the x and y passes below, in the same order
+                if (yact) {
+                    const int rpg = (g.rb + RS - 1) / RS;
+                    const int rr1 = min(g.rb, (tr + 1) * rpg);
+                    int cq0 = -1, cq1 = -1;
+                    float X0[UP], X1[UP];
+                    auto xrow = [&](int q, float* X) {
+                        const uint16_t* row = raw16 + q * 2 * pitch + ((e0 + q * st.wr) & 1);
+#pragma unroll
+                        for (int i = 0; i < UP; ++i)
+                            X[i] = __builtin_fmaf(bw0[i], rescale<HAS>(row[ba[i]], sl, ic),
+                                                  bw1[i] * rescale<HAS>(row[bb[i]], sl, ic));
+                    };
+                    for (int rr = tr * rpg; rr < rr1; ++rr) {
+                        const int dy = g.r0 + rr;
+                        const float sy = src_index(st.rh, dy);
+                        const int h1 = (int)sy;
+                        const int h1p = h1 < st.h - 1 ? 1 : 0;
+                        const float l1 = sy - (float)h1, l0 = 1.0f - l1;
+                        const int q0 = min(h1 - g.s0, last), q1 = min(h1 + h1p - g.s0, last);
+                        if (q0 != cq0) {
+                            if (q0 == cq1) {
+#pragma unroll
+                                for (int i = 0; i < UP; ++i) X0[i] = X1[i];
+                            } else {
+                                xrow(q0, X0);
+                            }
+                            cq0 = q0;
+                            cq1 = -1;
+                        }
+                        if (q1 != cq1) {
+                            if (q1 == q0) {
+#pragma unroll
+                                for (int i = 0; i < UP; ++i) X1[i] = X0[i];
+                            } else {
+                                xrow(q1, X1);
+                            }
+                            cq1 = q1;
+                        }
+                        float v[UP];
+#pragma unroll
+                        for (int i = 0; i < UP; ++i) v[i] = __builtin_fmaf(l0, X0[i], l1 * X1[i]);
+                        f(g.kk, dy, dx0, v);
+                    }
+                }
+                if (!st.dbuf && b + 1 < b1) {
+                    __syncthreads();                      // every thread is done with this block's rows
+                    nxt = block_geo<MODE>(st, a, b + 1);
+                    raw_stage(st, nxt, s_raw0);
+                }
+                continue;
+            }
             if (xact) {
                 for (int r = ph; r < g.ns; r += P) {
                     const uint16_t* row = raw16 + r * 2 * pitch + ((e0 + r * st.wr) & 1);
