@@ -186,6 +186,26 @@ int d8s_conv1(const D8sGemmArgs* a, void* stream);
  * (kaggle/int8_pack/pack_dense8s.py:246-283); here they are compared bit for bit. */
 int d8s_conv1_acc32(const D8sGemmArgs* a, int32_t* acc, void* stream);
 
+/* Kernel variants of conv1, conv2 and the transition, for tuning on the device: the same bytes from a
+ * chosen kernel.  The role of the reference's `tune_bm` / `tune_c2` / `tune_trans`
+ * (src/knee/dense8s.py:1598-1651), whose packages record a kernel per layer and block
+ * (kaggle/int8_pack/pack_dense8s.py:141-147).  d8s_*_variant(a, v) returns the variant that a launch
+ * with v runs: v itself, or for v = 0 the choice of d8s_conv1 / d8s_conv2 / d8s_transition; -1 where
+ * the arguments or the shape do not take v.  d8s_*_as(a, v, stream) launches it (an error where it
+ * is not taken).
+ *   conv1       1 persistent, 32-pixel tiles; 2 persistent, 64-pixel tiles (both: rows < 2^34, in0
+ *               and a slot below 4 GiB); 3, 4, 5 one pass with 1, 2, 4 k-slices.
+ *   conv2       tile TW x TH: 1 32x8, 2 32x4, 3 32x2, 4 16x4, 5 8x8, 6 4x16, 7 2x32, 8 1x64 (from 3
+ *               on the K steps split over 4 waves), for maps at least TW wide.
+ *   transition  activation prefetch depth / weight sets: 1 4/2 (G a multiple of 4), 2 4/4 (G a
+ *               multiple of 4, cout in 416..640), 3 2/2 (G even), 4 1/1. */
+int d8s_conv1_variant(const D8sGemmArgs* a, int32_t variant);
+int d8s_conv1_as(const D8sGemmArgs* a, int32_t variant, void* stream);
+int d8s_conv2_variant(const D8sConv2Args* a, int32_t variant);
+int d8s_conv2_as(const D8sConv2Args* a, int32_t variant, void* stream);
+int d8s_transition_variant(const D8sGemmArgs* a, int32_t variant);
+int d8s_transition_as(const D8sGemmArgs* a, int32_t variant, void* stream);
+
 /* conv2 of a dense layer: acc = sum over taps and input channels (zero padding) of w u (int32,
  * i8 MFMA), q = RNE(clamp(float(acc) * sc[o], -127, 127)) into the store slot.  Replaces
  * `conv2_t8x32_pl` / `conv2_t16x16_pl` (src/knee/dense8s_kernels.cu:2679-2832, launch

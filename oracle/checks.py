@@ -47,8 +47,28 @@ def feat_cmp(a: np.ndarray, b: np.ndarray) -> dict:
 
 
 # --- conv1 ------------------------------------------------------------------------------------
-def run_conv1(c: cases.GemmCase, device, acc32: bool = True) -> tuple[np.ndarray | None, np.ndarray]:
-    """(acc [M, 128] int32 or None, bottleneck [M, 128] uint8) from d8s_conv1(_acc32)."""
+def conv1_args(c: cases.GemmCase, device) -> tuple:
+    """(d8s_conv1 arguments of case c on the device, the tensors they point into)."""
+    HW = c.S * c.width
+    M = c.N * HW
+    in0, seg, w, abh, gd = (_dev(a, device) for a in (c.in0, c.seg, c.w1, c.abh, c.gd))
+    wsum = _dev(c.w1.astype(np.int64).sum(axis=(0, 2)).astype(np.int32), device)
+    bott = torch.zeros(4 * M * 32, dtype=torch.uint8, device=device)
+    args = hip.GemmArgs(_ptr(in0), _ptr(seg), _ptr(w), _ptr(abh), _ptr(gd), _ptr(wsum), _ptr(bott),
+                        c.G0, c.G, c.N, HW, c.width, M, 128, 0)
+    return args, (in0, seg, w, abh, gd, wsum, bott)
+
+
+def run_conv1(c: cases.GemmCase, device, acc32: bool = True,
+              variant: int = 0) -> tuple[np.ndarray | None, np.ndarray]:
+    """(acc [M, 128] int32 or None, bottleneck [M, 128] uint8) from d8s_conv1(_acc32); `variant` != 0
+    (no accumulators): d8s_conv1_as with that kernel variant."""
+    if variant:
+        args, keep = conv1_args(c, device)
+        M = c.N * c.S * c.width
+        hip.call("d8s_conv1_as", ctypes.byref(args), variant, _stream(device))
+        torch.cuda.synchronize(device)
+        return None, keep[-1].cpu().numpy().reshape(4, M, 32).transpose(1, 0, 2).reshape(M, 128)
     HW = c.S * c.width
     M = c.N * HW
     in0, seg, w, abh, gd = (_dev(a, device) for a in (c.in0, c.seg, c.w1, c.abh, c.gd))
@@ -83,9 +103,11 @@ def exact_conv1(c: cases.GemmCase) -> tuple[np.ndarray, np.ndarray]:
 
 
 # --- conv2 ------------------------------------------------------------------------------------
-def run_conv2(c: cases.Conv2Case, device, slots: int = 3, slot: int = 1) -> tuple[np.ndarray, np.ndarray]:
-    """Runs d8s_conv2 into slot `slot` of a `slots`-slot store filled with a sentinel; returns (the slot
-    [M, 32] int8, the other slots' bytes) so a write outside the slot shows."""
+def run_conv2(c: cases.Conv2Case, device, slots: int = 3, slot: int = 1,
+              variant: int = 0) -> tuple[np.ndarray, np.ndarray]:
+    """Runs d8s_conv2 (`variant` != 0: d8s_conv2_as with that tile) into slot `slot` of a `slots`-slot
+    store filled with a sentinel; returns (the slot [M, 32] int8, the other slots' bytes) so a write
+    outside the slot shows."""
     N, _, H, W = c.v.shape
     M = N * H * W
     bott, w2k, sc = (_dev(a, device) for a in (c.bott, c.w2k, c.sc))
@@ -93,7 +115,10 @@ def run_conv2(c: cases.Conv2Case, device, slots: int = 3, slot: int = 1) -> tupl
     store = torch.full((slots * M * 32,), 0x5A, dtype=torch.int8, device=device)
     args = hip.Conv2Args(_ptr(bott), _ptr(w2k), _ptr(sc), _ptr(wsum), _ptr(store) + slot * M * 32,
                          N, H, W, 0)
-    hip.call("d8s_conv2", ctypes.byref(args), _stream(device))
+    if variant:
+        hip.call("d8s_conv2_as", ctypes.byref(args), variant, _stream(device))
+    else:
+        hip.call("d8s_conv2", ctypes.byref(args), _stream(device))
     torch.cuda.synchronize(device)
     s = store.cpu().numpy().reshape(slots, M, 32)
     others = np.concatenate([s[k].reshape(-1) for k in range(slots) if k != slot]) if slots > 1 \
@@ -173,8 +198,28 @@ def exact_dense(c: cases.GemmCase, c2: cases.Conv2Case) -> np.ndarray:
 
 
 # --- transition -------------------------------------------------------------------------------
-def run_trans(t: dict, device) -> np.ndarray:
-    """Output [N * HW/4, cout] int8 of d8s_transition (from the next block's in0 layout)."""
+def trans_args(t: dict, device) -> tuple:
+    """(d8s_transition arguments of case t on the device, the tensors they point into)."""
+    S, N, cout = t["S"], t["N"], t["cout"]
+    HW = S * S
+    in0, seg, w, abh, gdf = (_dev(t[k], device) for k in ("in0", "seg", "w", "abh", "gdf"))
+    wsum = _dev(t["w"].astype(np.int64).sum(axis=(0, 2)).astype(np.int32), device)
+    out = torch.full((N * (cout // 32) * (HW // 4) * 32,), 0x5A, dtype=torch.int8, device=device)
+    args = hip.GemmArgs(_ptr(in0), _ptr(seg), _ptr(w), _ptr(abh), _ptr(gdf), _ptr(wsum), _ptr(out),
+                        t["G0"], t["G"], N, HW, S, N * HW, cout, cout // 32)
+    return args, (in0, seg, w, abh, gdf, wsum, out)
+
+
+def run_trans(t: dict, device, variant: int = 0) -> np.ndarray:
+    """Output [N * HW/4, cout] int8 of d8s_transition (`variant` != 0: d8s_transition_as with that
+    variant), from the next block's in0 layout."""
+    if variant:
+        S, N, cout = t["S"], t["N"], t["cout"]
+        args, keep = trans_args(t, device)
+        hip.call("d8s_transition_as", ctypes.byref(args), variant, _stream(device))
+        torch.cuda.synchronize(device)
+        o = keep[-1].cpu().numpy().reshape(N, cout // 32, S * S // 4, 32)
+        return o.transpose(0, 2, 1, 3).reshape(N * (S * S // 4), cout)
     S, N, cout = t["S"], t["N"], t["cout"]
     HW = S * S
     in0, seg, w, abh, gdf = (_dev(t[k], device) for k in ("in0", "seg", "w", "abh", "gdf"))

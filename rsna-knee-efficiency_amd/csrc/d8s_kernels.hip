@@ -3419,21 +3419,42 @@ static bool same_gemm(const D8sGemmArgs* a, const D8sGemmArgs* b) {
            a->rows == b->rows && a->cout == b->cout && a->G0n == b->G0n;
 }
 
-static int conv1_launch(const D8sGemmArgs* a, const D8sGemmArgs* b, int32_t* acc, hipStream_t st) {
-    if (int rc = check_gemm(a, "d8s_conv1")) return rc;
-    REQUIRE(a->cout == 128, "d8s_conv1: cout must be 128");
-    REQUIRE(acc != nullptr || a->out != nullptr, "d8s_conv1: null output");
+// conv1 kernel variants (d8s_conv1_as): 1, 2 the persistent form with 32- / 64-pixel tiles (three /
+// two workgroups per CU), 3, 4, 5 the one-pass form with 1, 2, 4 k-slices; 0 the choice below.
+enum { C1V_P32 = 1, C1V_P64 = 2, C1V_K1 = 3, C1V_K2 = 4, C1V_K4 = 5, C1V_MAX = 5 };
+
+// The variant a launch of conv1 with `variant` runs (the choice for 0), or -1 where the shape does
+// not take it (the persistent form keeps 32-bit offsets: rows < 2^34, in0 and a slot below 4 GiB).
+static int conv1_variant(const D8sGemmArgs* a, const D8sGemmArgs* b, int variant) {
     const int np = b ? 2 : 1;                              // problems in the launch
     const int64_t rows = a->rows * np;
+    const int64_t in0_bytes = (int64_t)a->N * a->G0 * a->HW * 32, slot_bytes = (int64_t)a->rows * 32;
+    const bool p_ok = a->rows < (1ll << 34) && in0_bytes < (1ll << 32) && slot_bytes < (1ll << 32);
+    if (variant != 0) {
+        if (variant < 1 || variant > C1V_MAX) return -1;
+        return variant <= C1V_P64 && !p_ok ? -1 : variant;
+    }
     // k-slices: the fewest that give at least 1.5 workgroups per CU
     const int64_t want = 3 * (int64_t)cu_count() / 2;
     int ks = 1;
     while (ks < 4 && (rows + 64 * 4 / ks - 1) / (64 * 4 / ks) < want) ks *= 2;
     // one k-slice: the persistent form (the weights through LDS); 64-pixel tiles when every wave of
     // two per SIMD gets at least two, else 32-pixel tiles and three waves per SIMD
-    const int64_t in0_bytes = (int64_t)a->N * a->G0 * a->HW * 32, slot_bytes = (int64_t)a->rows * 32;
-    if (ks == 1 && a->rows < (1ll << 34) && in0_bytes < (1ll << 32) && slot_bytes < (1ll << 32)) {
-        const int u = (rows + 63) / 64 >= 2 * 8 * (int64_t)cu_count() ? 2 : 1;
+    if (ks == 1 && p_ok) return (rows + 63) / 64 >= 2 * 8 * (int64_t)cu_count() ? C1V_P64 : C1V_P32;
+    return ks == 1 ? C1V_K1 : ks == 2 ? C1V_K2 : C1V_K4;
+}
+
+static int conv1_launch(const D8sGemmArgs* a, const D8sGemmArgs* b, int32_t* acc, hipStream_t st,
+                        int variant = 0) {
+    if (int rc = check_gemm(a, "d8s_conv1")) return rc;
+    REQUIRE(a->cout == 128, "d8s_conv1: cout must be 128");
+    REQUIRE(acc != nullptr || a->out != nullptr, "d8s_conv1: null output");
+    const int v = conv1_variant(a, b, variant);
+    REQUIRE(v >= 1, "d8s_conv1: variant " + std::to_string(variant) + " is not taken for this shape");
+    const int np = b ? 2 : 1;                              // problems in the launch
+    const int64_t rows = a->rows * np;
+    if (v == C1V_P32 || v == C1V_P64) {
+        const int u = v == C1V_P64 ? 2 : 1;
         const int64_t ntiles = (rows + 32 * u - 1) / (32 * u);
         const int per_cu = u == 2 ? 2 : 3;                        // workgroups per CU
         const int64_t want_blocks = (ntiles + 3) / 4;
@@ -3459,9 +3480,10 @@ static int conv1_launch(const D8sGemmArgs* a, const D8sGemmArgs* b, int32_t* acc
         return launched("d8s_conv1");
     }
     if (b) {                                               // the split-K form: two launches
-        if (int rc = conv1_launch(a, nullptr, acc, st)) return rc;
-        return conv1_launch(b, nullptr, acc, st);
+        if (int rc = conv1_launch(a, nullptr, acc, st, variant)) return rc;
+        return conv1_launch(b, nullptr, acc, st, variant);
     }
+    const int ks = v == C1V_K1 ? 1 : v == C1V_K2 ? 2 : 4;
     const int px = 64 * 4 / ks;
     const unsigned blocks = (unsigned)((a->rows + px - 1) / px);
     size_t shm = (size_t)a->G * 128;
@@ -3484,6 +3506,16 @@ static int conv1_launch(const D8sGemmArgs* a, const D8sGemmArgs* b, int32_t* acc
 extern "C" int d8s_conv1(const D8sGemmArgs* a, void* stream) {
     if (a != nullptr && a->out == nullptr) return fail((int)hipErrorInvalidValue, "d8s_conv1: null output");
     return conv1_launch(a, nullptr, nullptr, (hipStream_t)stream);
+}
+
+extern "C" int d8s_conv1_variant(const D8sGemmArgs* a, int32_t variant) {
+    if (a == nullptr || check_gemm(a, "d8s_conv1_variant") != 0 || a->cout != 128) return -1;
+    return conv1_variant(a, nullptr, variant);
+}
+
+extern "C" int d8s_conv1_as(const D8sGemmArgs* a, int32_t variant, void* stream) {
+    if (a != nullptr && a->out == nullptr) return fail((int)hipErrorInvalidValue, "d8s_conv1_as: null output");
+    return conv1_launch(a, nullptr, nullptr, (hipStream_t)stream, variant);
 }
 
 extern "C" int d8s_conv1_acc32(const D8sGemmArgs* a, int32_t* acc, void* stream) {
@@ -3523,7 +3555,39 @@ static int check_conv2(const D8sConv2Args* a, const char* what) {
     return 0;
 }
 
-static int conv2_dispatch(const D8sConv2Args* a, const D8sConv2Args* b, hipStream_t st) {
+// conv2 kernel variants (d8s_conv2_as), the tile shapes TW x TH: 1 32 x 8, 2 32 x 4, 3 32 x 2 (K split
+// in 4), 4 16 x 4, 5 8 x 8, 6 4 x 16, 7 2 x 32, 8 1 x 64 (K split in 4 from 3 on), each taken for maps
+// at least TW wide; 0 the choice below (the widest tile that fits, and for 32-wide tiles the tallest
+// that still gives three tiles per CU).
+static const int C2V_TW[9] = {0, 32, 32, 32, 16, 8, 4, 2, 1};
+
+static int conv2_variant(const D8sConv2Args* a, int variant) {
+    if (variant < 0 || variant > 8) return -1;
+    if (variant != 0) return C2V_TW[variant] <= a->W ? variant : -1;
+    if (a->W >= 32) {
+        const int64_t enough = 3 * (int64_t)cu_count();
+        if ((int64_t)a->N * ((a->W + 31) / 32) * ((a->H + 7) / 8) >= enough) return 1;
+        if ((int64_t)a->N * ((a->W + 31) / 32) * ((a->H + 3) / 4) >= enough) return 2;
+        return 3;
+    }
+    return a->W >= 16 ? 4 : a->W >= 8 ? 5 : a->W >= 4 ? 6 : a->W >= 2 ? 7 : 8;
+}
+
+static int conv2_dispatch(const D8sConv2Args* a, const D8sConv2Args* b, hipStream_t st, int variant) {
+    if (variant != 0) {
+        REQUIRE(conv2_variant(a, variant) >= 1,
+                "d8s_conv2: variant " + std::to_string(variant) + " is not taken for this shape");
+        switch (variant) {
+            case 1: return conv2_launch<32, 8, 1, 2>(a, b, st, 0);
+            case 2: return conv2_launch<32, 4, 1, 1>(a, b, st, 0);
+            case 3: return conv2_launch<32, 2, 4, 2>(a, b, st, 0);
+            case 4: return conv2_launch<16, 4, 4, 2>(a, b, st, 0);
+            case 5: return conv2_launch<8, 8, 4, 2>(a, b, st, 0);
+            case 6: return conv2_launch<4, 16, 4, 2>(a, b, st, 0);
+            case 7: return conv2_launch<2, 32, 4, 2>(a, b, st, 0);
+            default: return conv2_launch<1, 64, 4, 2>(a, b, st, 0);
+        }
+    }
     const int64_t enough = 3 * (int64_t)cu_count();        // tiles for a persistent grid to pipeline
     if (a->W >= 32) {
         int rc = conv2_launch<32, 8, 1, 2>(a, b, st, enough);
@@ -3541,14 +3605,24 @@ static int conv2_dispatch(const D8sConv2Args* a, const D8sConv2Args* b, hipStrea
 
 extern "C" int d8s_conv2(const D8sConv2Args* a, void* stream) {
     if (int rc = check_conv2(a, "d8s_conv2")) return rc;
-    return conv2_dispatch(a, nullptr, (hipStream_t)stream);
+    return conv2_dispatch(a, nullptr, (hipStream_t)stream, 0);
+}
+
+extern "C" int d8s_conv2_variant(const D8sConv2Args* a, int32_t variant) {
+    if (a == nullptr || check_conv2(a, "d8s_conv2_variant") != 0) return -1;
+    return conv2_variant(a, variant);
+}
+
+extern "C" int d8s_conv2_as(const D8sConv2Args* a, int32_t variant, void* stream) {
+    if (int rc = check_conv2(a, "d8s_conv2_as")) return rc;
+    return conv2_dispatch(a, nullptr, (hipStream_t)stream, variant);
 }
 
 extern "C" int d8s_conv2_pair(const D8sConv2Args* a, const D8sConv2Args* b, void* stream) {
     if (int rc = check_conv2(a, "d8s_conv2_pair")) return rc;
     if (int rc = check_conv2(b, "d8s_conv2_pair")) return rc;
     REQUIRE(a->N == b->N && a->H == b->H && a->W == b->W, "d8s_conv2_pair: the two problems differ in shape");
-    return conv2_dispatch(a, b, (hipStream_t)stream);
+    return conv2_dispatch(a, b, (hipStream_t)stream, 0);
 }
 
 // Whether d8s_conv2_conv1 takes maps of this shape and a conv1 reading G groups.
@@ -3801,20 +3875,35 @@ static int trans_launch_d(const D8sGemmArgs* a, const D8sGemmArgs* b, hipStream_
     return launched("d8s_transition");
 }
 
-// activation prefetch depth: the largest of 4, 2, 1 dividing the group count.  Weights two groups
-// ahead (one if D is odd), or four for 4-5 output tiles per wave when the grid is at most one
-// workgroup per CU: there the weights are most of the loads and each workgroup's chain of groups is
-// the whole launch (a 24-image study's 32 x 32 transition: 52 -> 25 us); with more workgroups, two per
-// CU with two sets do better (one per CU with four: 52 -> 73 us at 96 images).
-template <int NT, int PT>
-static int trans_launch(const D8sGemmArgs* a, const D8sGemmArgs* b, hipStream_t st) {
-    const int64_t blocks = ((int64_t)a->N * (a->HW / 4) + 32 * PT - 1) / (32 * PT) * (b ? 2 : 1);
-    if (a->G % 4 == 0) {
-        if constexpr (NT == 4 || NT == 5)
-            if (blocks <= cu_count()) return trans_launch_d<NT, PT, 4, 4>(a, b, st);
-        return trans_launch_d<NT, PT, 4, 2>(a, b, st);
+// Transition variants (d8s_transition_as), activation prefetch depth D (groups ahead; D divides the
+// group count) and weight register sets WB (groups of weights ahead): 1 D 4 WB 2 (G a multiple of 4),
+// 2 D 4 WB 4 (G a multiple of 4, 4 or 5 output tiles per wave), 3 D 2 WB 2 (G even), 4 D 1 WB 1.  0
+// (the launches' own choice): D 2 WB 2 where G is even, else D 1.  Measured per transition of the
+// 512-px encoder (each variant's launches replayed back to back, three rounds on one box): 128 x 128
+// (G 8) 89-91 against 95-103 us with D 4 at 96 images, 22.7-23.1 against 25.4-26.7 us at 24; 64 x 64
+// (G 16) 47.6-48.0 against 50.1-51.0 and 16.2 against 17.3-17.4 us; 32 x 32 (G 40) 51.6-51.9 against
+// 51.3-52.2 us at 96 and 23.8-23.9 against 23.8 us at 24 images, where four weight sets took 25.0 us.
+static int trans_variant(const D8sGemmArgs* a, const D8sGemmArgs* b, int variant) {
+    (void)b;
+    const int nt = (a->cout / 32 + 3) / 4;                 // output tiles per wave
+    switch (variant) {
+        case 0: return a->G % 2 == 0 ? 3 : 4;
+        case 1: return a->G % 4 == 0 ? 1 : -1;
+        case 2: return a->G % 4 == 0 && (nt == 4 || nt == 5) ? 2 : -1;
+        case 3: return a->G % 2 == 0 ? 3 : -1;
+        case 4: return 4;
+        default: return -1;
     }
-    if (a->G % 2 == 0) return trans_launch_d<NT, PT, 2, 2>(a, b, st);
+}
+
+template <int NT, int PT>
+static int trans_launch(const D8sGemmArgs* a, const D8sGemmArgs* b, hipStream_t st, int variant) {
+    const int v = trans_variant(a, b, variant);
+    REQUIRE(v >= 1, "d8s_transition: variant " + std::to_string(variant) + " is not taken for this shape");
+    if constexpr (NT == 4 || NT == 5)
+        if (v == 2) return trans_launch_d<NT, PT, 4, 4>(a, b, st);
+    if (v == 1) return trans_launch_d<NT, PT, 4, 2>(a, b, st);
+    if (v == 3) return trans_launch_d<NT, PT, 2, 2>(a, b, st);
     return trans_launch_d<NT, PT, 1, 1>(a, b, st);
 }
 
@@ -3828,28 +3917,38 @@ static int check_trans(const D8sGemmArgs* a, const char* what) {
     return 0;
 }
 
-static int trans_dispatch(const D8sGemmArgs* a, const D8sGemmArgs* b, hipStream_t st) {
+static int trans_dispatch(const D8sGemmArgs* a, const D8sGemmArgs* b, hipStream_t st, int variant) {
     switch ((a->cout / 32 + 3) / 4) {                      // output tiles per wave
-        case 1: return trans_launch<1, 4>(a, b, st);
-        case 2: return trans_launch<2, 2>(a, b, st);
-        case 3: return trans_launch<3, 1>(a, b, st);
-        case 4: return trans_launch<4, 1>(a, b, st);
-        case 5: return trans_launch<5, 1>(a, b, st);
-        case 6: return trans_launch<6, 1>(a, b, st);
-        default: return trans_launch<8, 1>(a, b, st);
+        case 1: return trans_launch<1, 4>(a, b, st, variant);
+        case 2: return trans_launch<2, 2>(a, b, st, variant);
+        case 3: return trans_launch<3, 1>(a, b, st, variant);
+        case 4: return trans_launch<4, 1>(a, b, st, variant);
+        case 5: return trans_launch<5, 1>(a, b, st, variant);
+        case 6: return trans_launch<6, 1>(a, b, st, variant);
+        default: return trans_launch<8, 1>(a, b, st, variant);
     }
 }
 
 extern "C" int d8s_transition(const D8sGemmArgs* a, void* stream) {
     if (int rc = check_trans(a, "d8s_transition")) return rc;
-    return trans_dispatch(a, nullptr, (hipStream_t)stream);
+    return trans_dispatch(a, nullptr, (hipStream_t)stream, 0);
+}
+
+extern "C" int d8s_transition_variant(const D8sGemmArgs* a, int32_t variant) {
+    if (a == nullptr || check_trans(a, "d8s_transition_variant") != 0) return -1;
+    return trans_variant(a, nullptr, variant);
+}
+
+extern "C" int d8s_transition_as(const D8sGemmArgs* a, int32_t variant, void* stream) {
+    if (int rc = check_trans(a, "d8s_transition_as")) return rc;
+    return trans_dispatch(a, nullptr, (hipStream_t)stream, variant);
 }
 
 extern "C" int d8s_transition_pair(const D8sGemmArgs* a, const D8sGemmArgs* b, void* stream) {
     if (int rc = check_trans(a, "d8s_transition_pair")) return rc;
     if (int rc = check_trans(b, "d8s_transition_pair")) return rc;
     REQUIRE(same_gemm(a, b), "d8s_transition_pair: the two problems differ in shape");
-    return trans_dispatch(a, b, (hipStream_t)stream);
+    return trans_dispatch(a, b, (hipStream_t)stream, 0);
 }
 
 static int final_launch(const int8_t* in0, int32_t G0, const int8_t* seg, int32_t N, int32_t HW,

@@ -33,7 +33,7 @@ import ctypes
 import itertools
 import json
 import time
-from dataclasses import dataclass, field
+from dataclasses import dataclass, field, replace
 from pathlib import Path
 
 import numpy as np
@@ -422,17 +422,29 @@ RUNTIME_TABLES = ("_abh", "_w1", "_gdu", "_w2k", "_c2u", "_w", "_gdf")
 
 
 def pack_meta(plan: SPlan, n: int, input_kind: str = "u8", mean=(0.5, 0.5, 0.5),
-              std=(0.25, 0.25, 0.25), fused: dict | None = None) -> dict:
+              std=(0.25, 0.25, 0.25), fused: dict | None = None, bm: dict | None = None,
+              c2: dict | None = None, tbm: dict | None = None) -> dict:
     """Package metadata: format 1, kind "dense8s" (`src/knee/dense8s.py:810-830`).  `n` = images per
     pass (graph block); `input`: "u8" (raw slices, normalised in the stem with mean / std) or "f16"
     (already normalised fp16, the reference's input); `fused` {block: kind} (keys ints or "b{block}"):
     the block kinds to record, e.g. `Dense8SEncoder.tune_kinds`'s choice, which runners of the package
-    then use (the reference's per-block "fused" field)."""
+    then use (the reference's per-block "fused" field).  `bm` {"b{block}l{layer}": conv1 variant},
+    `c2` {side: conv2 variant}, `tbm` {"t{block}": transition variant}: kernel variants to record
+    (`C1_VARIANTS`, `C2_VARIANTS`, `TRANS_VARIANTS`; e.g. the fastest of `tune_bm`, `tune_c2`,
+    `tune_trans`), kept per block as the reference's packages keep theirs ("bm" a list per layer, "c2",
+    "tbm"; `src/knee/dense8s.py:818-826`)."""
     if input_kind not in ("u8", "f16"):
         raise ValueError(f"input kind {input_kind!r}: expected 'u8' or 'f16'")
-    fused = fused or {}
+    fused, bm, c2, tbm = fused or {}, bm or {}, c2 or {}, tbm or {}
+    for table, names in ((bm, C1_VARIANTS), (c2, C2_VARIANTS), (tbm, TRANS_VARIANTS)):
+        for key, name in table.items():
+            if name not in names.values():
+                raise ValueError(f"variant {name!r} for {key!r}: expected one of {sorted(names.values())}")
     blocks = [{"c0": b.c0, "h": b.h, "w": b.w, "L": len(b.layers), "trans": b.ta is not None,
-               "fused": fused.get(bi) or fused.get(f"b{bi}")}
+               "fused": fused.get(bi) or fused.get(f"b{bi}"),
+               "bm": [bm.get(f"b{bi}l{li}") for li in range(len(b.layers))],
+               "c2": c2.get(b.h, c2.get(str(b.h))),
+               "tbm": tbm.get(f"t{bi}") if b.ta is not None else None}
               for bi, b in enumerate(plan.blocks)]
     return {"format": PACK_FORMAT, "kind": KIND, "n": int(n), "img": plan.img,
             "in_ch": plan.in_ch, "kernels_sha": hip.source_sha(), "n_features": plan.n_features,
@@ -637,6 +649,41 @@ def band_fits(b: dict) -> bool:
     return b["w"] == BAND_W and block_groups(b) <= BAND_MAX_GROUPS
 
 
+# Kernel variants of the per-layer launches (include/d8s_hip.h, d8s_conv1_as / d8s_conv2_as /
+# d8s_transition_as): id -> name.  Every variant writes the same bytes; 0 is the library's own choice.
+C1_VARIANTS = {1: "p32", 2: "p64", 3: "k1", 4: "k2", 5: "k4"}
+C2_VARIANTS = {1: "32x8", 2: "32x4", 3: "32x2", 4: "16x4", 5: "8x8", 6: "4x16", 7: "2x32", 8: "1x64"}
+TRANS_VARIANTS = {1: "d4w2", 2: "d4w4", 3: "d2w2", 4: "d1w1"}
+VARIANTS = {"conv1": C1_VARIANTS, "conv2": C2_VARIANTS, "trans": TRANS_VARIANTS}
+
+
+def _variant_id(table: dict, name) -> int:
+    for v, n in table.items():
+        if n == name:
+            return v
+    return 0
+
+
+def recorded_variants(meta: dict) -> dict:
+    """The kernel variants a package records (per block "bm" per layer, "c2", "tbm", as the reference's
+    packages record theirs, `kaggle/int8_pack/pack_dense8s.py:141-147`): {("conv1", block, layer) |
+    ("conv2", block) | ("trans", block): variant id}.  Names of this library's variants only: the
+    reference's kernel names (CUDA kernels, `src/knee/dense8s.py:818-826`) name nothing here and leave
+    the library's choice."""
+    out = {}
+    for bi, b in enumerate(meta["blocks"]):
+        bm = b.get("bm")
+        if isinstance(bm, (list, tuple)):
+            for li, name in enumerate(bm):
+                if isinstance(name, str) and _variant_id(C1_VARIANTS, name):
+                    out[("conv1", bi, li)] = _variant_id(C1_VARIANTS, name)
+        for fam, key in (("conv2", "c2"), ("trans", "tbm")):
+            name = b.get(key)
+            if isinstance(name, str) and _variant_id(VARIANTS[fam], name):
+                out[(fam, bi)] = _variant_id(VARIANTS[fam], name)
+    return out
+
+
 def default_kind(b: dict, n: int, cus: int = 256) -> str:
     """The block kind of block `b` at n images per pass: "parts" (the whole block in one launch, images
     split into as many bands as fill the chip) where that takes 4 bands or more and the block either
@@ -783,13 +830,15 @@ class Step:
     block, trans, final), `block` / `layer` where it sits (layer -1: the whole block or none), `makes`
     the trace keys whose contents it completes ((b, j): store segment j of block b, ("bott", b, l):
     layer l's bottleneck), `entry` the C entry point and `args` its argument struct (None for the
-    stem's and the final's, whose pointers change per pass)."""
+    stem's and the final's, whose pointers change per pass), `variant` the kernel variant of a conv1,
+    conv2 or transition launch (0: the library's choice)."""
     family: str
     block: int
     layer: int
     makes: tuple
     entry: str
     args: object = None
+    variant: int = 0
 
     def tag(self) -> str:
         return self.family if self.family in ("stem", "final") else f"{self.family}_{self.block}"
@@ -1039,6 +1088,7 @@ class Dense8SEncoder(_PassRunner):
         self.pack_sha = meta.get("kernels_sha")
         self.nb = int(meta["n"])
         self.fused = fused_blocks(meta, fused, _cu_count(self.dev))
+        self.variants = recorded_variants(meta)  # {(family, block[, layer]): kernel variant}
         self.n_out = -(-int(n_total) // self.nb) * self.nb
         self.max_inflight = max_inflight
         self._gate = InflightGate(max_inflight)
@@ -1211,6 +1261,14 @@ class Dense8SEncoder(_PassRunner):
                 prog.append(Step("trans", bi, -1, ((bi + 1, 0),), "d8s_transition", args))
             else:
                 prog.append(Step("final", bi, -1, (), "d8s_final"))
+        for step in prog:
+            v = self._variant_of(step)
+            if v:
+                got = getattr(self.lib, step.entry + "_variant")(ctypes.byref(step.args), v)
+                if got != v:
+                    raise ValueError(f"{step.label()}: kernel variant {VARIANTS[step.family][v]!r} is not "
+                                     f"taken for this shape")
+                step.variant = v
         self.program = prog
         self._checked = any(s.entry == "d8s_dense_block_parts" for s in prog)
         # bands per image of the widest banded launch: its share of the CUs a wait needs resident
@@ -1222,6 +1280,14 @@ class Dense8SEncoder(_PassRunner):
             dptr = ctypes.c_void_p()
             hip.check(self.lib.d8s_host_mapped(self._report.data_ptr(), ctypes.byref(dptr)), "d8s_host_mapped")
             self._report_dev = int(dptr.value or 0)
+
+    def _variant_of(self, step: Step) -> int:
+        """The kernel variant `variants` gives a conv1, conv2 or transition launch (0: none)."""
+        if step.family == "conv1":
+            return self.variants.get(("conv1", step.block, step.layer), 0)
+        if step.family in ("conv2", "trans"):
+            return self.variants.get((step.family, step.block), 0)
+        return 0
 
     # -- launches --
     def _launch(self, step: Step, st: int, x_ptr: int = 0, f_ptr: int = 0, mode: int = 0) -> None:
@@ -1240,6 +1306,8 @@ class Dense8SEncoder(_PassRunner):
                 rc = lib.d8s_final(*common, st)
         elif step.family == "chain":
             rc = lib.d8s_conv2_conv1(ctypes.byref(step.args[0]), ctypes.byref(step.args[1]), st)
+        elif step.variant:
+            rc = getattr(lib, step.entry + "_as")(ctypes.byref(step.args), step.variant, st)
         else:
             rc = getattr(lib, step.entry)(ctypes.byref(step.args), st)
         hip.check(rc, step.entry)
@@ -1466,6 +1534,65 @@ class Dense8SEncoder(_PassRunner):
             self._compile()
         return out
 
+    def _tune_variants(self, steps: list, reps: int) -> dict:
+        """{variant name: ms} of the first of `steps` (one family) run as every kernel variant its shape
+        takes (`d8s_*_variant`), on the current store."""
+        step = steps[0]
+        names = VARIANTS[step.family]
+        query = getattr(self.lib, step.entry + "_variant")
+        return {name: round(self._graph_ms([replace(step, variant=v)], reps), 4)
+                for v, name in names.items() if query(ctypes.byref(step.args), v) == v}
+
+    def _apply_variants(self, choices: dict) -> None:
+        """Runs the launches with the variants chosen ({(family, block[, layer]): id}); graphs dropped."""
+        self.variants.update(choices)
+        self.graphs.clear()
+        self._compile()
+
+    def tune_bm(self, reps: int = 20, apply: bool = False) -> dict:
+        """For every conv1 launch of the pass the ms of every conv1 kernel variant its shape takes
+        (`C1_VARIANTS`): {"b{block}l{layer}": {variant: ms}}, on the current store (the reference's
+        `tune_bm`, `src/knee/dense8s.py:1598-1617`; here the layers of blocks run as "conv", and the first
+        layer of a "chain" block, have conv1 launches of their own).  Every variant writes the same bytes.
+        `apply`: the runner then uses the fastest per layer; `pack_meta(bm=...)` records such a choice."""
+        out, pick = {}, {}
+        for s in self.program:
+            if s.family == "conv1":
+                res = out[f"b{s.block}l{s.layer}"] = self._tune_variants([s], reps)
+                pick[("conv1", s.block, s.layer)] = _variant_id(C1_VARIANTS, min(res, key=res.get))
+        if apply:
+            self._apply_variants(pick)
+        return out
+
+    def tune_c2(self, reps: int = 20, apply: bool = False) -> dict:
+        """For every block with conv2 launches of its own the ms of its first one as every conv2 tile the
+        map takes (`C2_VARIANTS`): {side: {variant: ms}}, on the current store (the reference's `tune_c2`,
+        `src/knee/dense8s.py:1636-1651`, layer 0's conv2 per side).  `apply`: the block's conv2 launches
+        then use the fastest; `pack_meta(c2=...)` records such a choice."""
+        out, pick = {}, {}
+        for bi, b in enumerate(self.meta["blocks"]):
+            steps = [s for s in self.program if s.family == "conv2" and s.block == bi]
+            if steps:
+                res = out[b["h"]] = self._tune_variants(steps, reps)
+                pick[("conv2", bi)] = _variant_id(C2_VARIANTS, min(res, key=res.get))
+        if apply:
+            self._apply_variants(pick)
+        return out
+
+    def tune_trans(self, reps: int = 20, apply: bool = False) -> dict:
+        """For every transition the ms of every transition variant its shape takes (`TRANS_VARIANTS`):
+        {"t{block}": {variant: ms}}, on the current store (the reference's `tune_trans`,
+        `src/knee/dense8s.py:1619-1634`).  `apply`: the runner then uses the fastest;
+        `pack_meta(tbm=...)` records such a choice."""
+        out, pick = {}, {}
+        for s in self.program:
+            if s.family == "trans":
+                res = out[f"t{s.block}"] = self._tune_variants([s], reps)
+                pick[("trans", s.block)] = _variant_id(TRANS_VARIANTS, min(res, key=res.get))
+        if apply:
+            self._apply_variants(pick)
+        return out
+
 
 def encode_concurrent(calls) -> list[torch.Tensor]:
     """Several runners at once: `calls` = [(runner, x, flip), ...], every runner on its own stream, the
@@ -1568,7 +1695,7 @@ class EncoderPair(_PassRunner):
         A, B, st = self.a, self.b, self.stream.cuda_stream
         fa, fb = A.out[index * A.nb].data_ptr(), B.out[index * B.nb].data_ptr()
         for sa, sb in zip(A.program, B.program):
-            paired = PAIR_ENTRIES.get(sa.entry)
+            paired = None if sa.variant or sb.variant else PAIR_ENTRIES.get(sa.entry)
             if paired is None:
                 A._launch(sa, st, x_ptr, fa, mode)
                 B._launch(sb, st, x_ptr, fb, mode)

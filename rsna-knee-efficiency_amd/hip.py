@@ -154,6 +154,12 @@ IN_F16, IN_U8 = 0, 1
 SIGNATURES = {
     "d8s_conv1": [ctypes.POINTER(GemmArgs), vp],
     "d8s_conv1_acc32": [ctypes.POINTER(GemmArgs), vp, vp],
+    "d8s_conv1_variant": [ctypes.POINTER(GemmArgs), ctypes.c_int32],
+    "d8s_conv1_as": [ctypes.POINTER(GemmArgs), ctypes.c_int32, vp],
+    "d8s_conv2_variant": [ctypes.POINTER(Conv2Args), ctypes.c_int32],
+    "d8s_conv2_as": [ctypes.POINTER(Conv2Args), ctypes.c_int32, vp],
+    "d8s_transition_variant": [ctypes.POINTER(GemmArgs), ctypes.c_int32],
+    "d8s_transition_as": [ctypes.POINTER(GemmArgs), ctypes.c_int32, vp],
     "d8s_conv2": [ctypes.POINTER(Conv2Args), vp],
     "d8s_dense": [ctypes.POINTER(DenseArgs), vp],
     "d8s_conv2_conv1": [ctypes.POINTER(Conv2Args), ctypes.POINTER(GemmArgs), vp],

@@ -248,3 +248,47 @@ def test_no_fallback_when_library_is_missing(tmp_path, monkeypatch):
     monkeypatch.setattr(hip, "_STATE", {})
     with pytest.raises(FileNotFoundError):
         hip.library(tmp_path / "libd8s_hip.so")
+
+
+def test_kernel_variant_queries():
+    """d8s_conv1 / d8s_conv2 / d8s_transition_variant: the variant a launch with v runs (v itself, or
+    for 0 the choice of d8s_conv1 / d8s_conv2 / d8s_transition, here at 256 CUs), -1 where the shape
+    does not take v; a launch with a variant its shape does not take fails on the host."""
+    lib = hip.library()
+    buf = (ctypes.c_uint8 * 64)()
+    p = ctypes.addressof(buf)
+
+    def gemm(N, HW, W, G0, G, cout=128, G0n=0):
+        return ctypes.byref(hip.GemmArgs(p, p, p, p, p, p, p, G0, G, N, HW, W, N * HW, cout, G0n))
+
+    def trans(N, HW, W, G0, G, cout):
+        return gemm(N, HW, W, G0, G, cout, cout // 32)
+
+    def conv2(N, H, W):
+        return ctypes.byref(hip.Conv2Args(p, p, p, p, p, N, H, W, 0))
+
+    # conv1: 393216 rows -> persistent, 64-pixel tiles; 98304 -> 32-pixel tiles; 1024 -> 4 k-slices
+    assert lib.d8s_conv1_variant(gemm(96, 4096, 64, 4, 10), 0) == 2
+    assert lib.d8s_conv1_variant(gemm(24, 4096, 64, 4, 10), 0) == 1
+    small = gemm(1, 1024, 32, 8, 10)
+    assert [lib.d8s_conv1_variant(small, v) for v in range(7)] == [5, 1, 2, 3, 4, 5, -1]
+    big = gemm(64, 1 << 20, 1024, 2, 3)                     # in0 of 4 GiB: no persistent form
+    assert [lib.d8s_conv1_variant(big, v) for v in range(1, 6)] == [-1, -1, 3, 4, 5]
+    assert lib.d8s_conv1_variant(gemm(24, 4096, 64, 4, 10, cout=256), 1) == -1
+    # conv2: tiles at most the map's width wide; 0 the widest, for 32 the tallest giving 3 tiles per CU
+    assert [lib.d8s_conv2_variant(conv2(96, 16, 16), v) for v in range(10)] == [4, -1, -1, -1, 4, 5, 6, 7, 8, -1]
+    assert lib.d8s_conv2_variant(conv2(96, 64, 64), 0) == 1
+    assert lib.d8s_conv2_variant(conv2(24, 32, 32), 0) == 3
+    assert lib.d8s_conv2_variant(conv2(1, 2, 2), 0) == 7
+    # transition: depth 4 for G a multiple of 4, four weight sets for 4-5 output tiles per wave; the
+    # choice: depth 2 where G is even, else 1
+    t = trans(24, 1024, 32, 8, 40, 640)
+    assert [lib.d8s_transition_variant(t, v) for v in range(6)] == [3, 1, 2, 3, 4, -1]
+    assert [lib.d8s_transition_variant(trans(24, 1024, 32, 8, 38, 640), v) for v in range(5)] == [3, -1, -1, 3, 4]
+    assert [lib.d8s_transition_variant(trans(24, 4096, 64, 2, 8, 128), v) for v in range(5)] == [3, 1, -1, 3, 4]
+    assert lib.d8s_transition_variant(trans(4, 1024, 32, 8, 9, 96), 0) == 4
+    assert lib.d8s_transition_variant(gemm(24, 4096, 64, 2, 8, cout=128), 1) == -1      # G0n != cout / 32
+    assert lib.d8s_conv2_as(conv2(96, 16, 16), 1, None) == 1
+    assert "variant 1" in lib.d8s_last_error().decode()
+    assert lib.d8s_transition_as(trans(24, 1024, 32, 8, 38, 640), 1, None) == 1
+    assert lib.d8s_conv1_as(big, 2, None) == 1

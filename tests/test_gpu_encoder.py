@@ -10,12 +10,14 @@ Tolerances (stated here, reported in every assertion message):
 """
 from __future__ import annotations
 
+import ctypes
+
 import numpy as np
 import pytest
 import torch
 
 from oracle import checks, emulate as emu, fp32
-from rsna_knee_efficiency_amd import dense8s, densenet, synthetic
+from rsna_knee_efficiency_amd import dense8s, densenet, hip, synthetic
 
 pytestmark = pytest.mark.gpu
 
@@ -219,6 +221,61 @@ def test_tune_kinds_and_recorded_kinds(dev, study512):
     r2 = dense8s.Dense8SEncoder(dict(study512["pack"], meta=meta2), dev.index or 0, 24)
     assert r2.fused[3] == "img" and r2.fused[0] == "tile"
     assert torch.equal(r2(x).clone(), want)
+
+
+def test_kernel_variant_tuners(dev, study512):
+    """`tune_bm` / `tune_c2` / `tune_trans` (the reference's per-layer tuners) time every kernel variant
+    each conv1, conv2 and transition launch takes; applied, the runner uses the fastest, with the same
+    features; every launch forced to each variant it takes gives the same features; a package recording
+    variants (`pack_meta(bm=, c2=, tbm=)`) gives runners with those variants and the same features, and
+    the reference's kernel names in a package leave the library's choice."""
+    enc, x = study512["enc"], study512["xd"]
+    want = enc(x).clone()
+    kinds = {0: "tile", 3: "img"}                          # blocks 1 and 2 as conv1 + conv2 launches
+    runner = dense8s.Dense8SEncoder(study512["pack"], dev.index or 0, 24, fused=kinds)
+    assert torch.equal(runner(x).clone(), want)
+    blocks = study512["pack"]["meta"]["blocks"]
+    bm = runner.tune_bm(reps=2, apply=True)
+    c2 = runner.tune_c2(reps=2, apply=True)
+    tb = runner.tune_trans(reps=2, apply=True)
+    print({k: bm[k] for k in ("b1l0", "b2l31")}, c2, tb, flush=True)
+    assert set(bm) == {f"b{b}l{l}" for b in (1, 2) for l in range(blocks[b]["L"])}
+    assert set(c2) == {64, 32} and set(tb) == {"t0", "t1", "t2"}
+    for res, table in ((bm, dense8s.C1_VARIANTS), (c2, dense8s.C2_VARIANTS), (tb, dense8s.TRANS_VARIANTS)):
+        for times in res.values():
+            assert times and set(times) <= set(table.values()) and all(v > 0 for v in times.values())
+    assert set(bm["b1l0"]) == set(dense8s.C1_VARIANTS.values()) and "d4w4" in tb["t2"]
+    assert runner.variants[("conv1", 2, 31)] == dense8s._variant_id(dense8s.C1_VARIANTS, min(bm["b2l31"], key=bm["b2l31"].get))
+    assert torch.equal(runner(x).clone(), want)
+    # every launch of a family forced to each variant it takes
+    lib = hip.library()
+    for fam, table in (("conv1", dense8s.C1_VARIANTS), ("conv2", dense8s.C2_VARIANTS),
+                       ("trans", dense8s.TRANS_VARIANTS)):
+        for v in table:
+            choice = {}
+            for s in runner.program:
+                if s.family == fam and getattr(lib, s.entry + "_variant")(ctypes.byref(s.args), v) == v:
+                    choice[(fam, s.block, s.layer) if fam == "conv1" else (fam, s.block)] = v
+            if choice:
+                runner._apply_variants(choice)
+                print(f"{fam} variant {table[v]}: {len(choice)} launches", flush=True)
+                assert torch.equal(runner(x).clone(), want), (fam, table[v])
+    # recorded in a package
+    pick = lambda res: {k: min(t, key=t.get) for k, t in res.items()}   # noqa: E731
+    meta = dense8s.pack_meta(study512["plan"], 24, input_kind="u8", fused=kinds, bm=pick(bm), c2=pick(c2),
+                             tbm=pick(tb))
+    rec = dense8s.Dense8SEncoder(dict(study512["pack"], meta=meta), dev.index or 0, 24)
+    want_v = {("conv1", b, l): dense8s._variant_id(dense8s.C1_VARIANTS, n) for k, n in pick(bm).items()
+              for b, l in [tuple(int(p) for p in k[1:].split("l"))]}
+    assert all(rec.variants[k] == v for k, v in want_v.items())
+    assert [s.variant for s in rec.program if s.family == "trans"] == \
+        [dense8s._variant_id(dense8s.TRANS_VARIANTS, pick(tb)[f"t{b}"]) for b in range(3)]
+    assert torch.equal(rec(x).clone(), want)
+    for b in meta["blocks"]:
+        b["bm"], b["c2"], b["tbm"] = ["w64_pl"] * b["L"], [16, 8, "p4u_pl"], "q128"
+    ref = dense8s.Dense8SEncoder(dict(study512["pack"], meta=meta), dev.index or 0, 24)
+    assert ref.variants == {} and all(s.variant == 0 for s in ref.program)
+    assert torch.equal(ref(x).clone(), want)
 
 
 def test_encoder288_reference_study(dev):

@@ -109,6 +109,21 @@ def test_conv1_ks_variants(dev, S, C, N):
     assert np.array_equal(acc, acc_x) and np.array_equal(byt, byt_x)
 
 
+@pytest.mark.parametrize("S,C,N", [(64, 320, 24), (16, 640, 24), (8, 96, 3), (100, 96, 30), (128, 224, 2)])
+def test_conv1_every_variant(dev, S, C, N):
+    """Every conv1 kernel variant (d8s_conv1_as: the persistent form with 32- and 64-pixel tiles, one
+    pass with 1, 2 and 4 k-slices) writes the exact bottleneck."""
+    c = cases.gemm_case(S, C, N=N, seed=29)
+    _, byt_x = checks.exact_conv1(c)
+    args, _keep = checks.conv1_args(c, dev)
+    taken = [v for v in dense8s.C1_VARIANTS if hip.library().d8s_conv1_variant(ctypes.byref(args), v) == v]
+    assert taken == list(dense8s.C1_VARIANTS)
+    for v in taken:
+        print(f"conv1 S={S} C={C} N={N} variant {dense8s.C1_VARIANTS[v]}", flush=True)
+        _, byt = checks.run_conv1(c, dev, variant=v)
+        assert np.array_equal(byt, byt_x), (dense8s.C1_VARIANTS[v], checks.bytes_cmp(byt, byt_x))
+
+
 @pytest.mark.parametrize("S", cases.CONV2_SIDES)
 def test_conv2_config3(dev, S):
     """Config 3: 3x3 pad-1 conv 128 -> 32, batch 24, written into its slot of a store (the other slots
@@ -136,6 +151,19 @@ def test_conv2_tile_variants(dev, N, H, W):
     _, q_x = checks.exact_conv2(c)
     assert np.array_equal(got, q_x), checks.bytes_cmp(got, q_x)
     assert np.all(others == 0x5A)
+
+
+@pytest.mark.parametrize("N,H,W", [(24, 64, 64), (24, 32, 32), (24, 16, 16), (3, 9, 9), (2, 33, 40)])
+def test_conv2_every_variant(dev, N, H, W):
+    """Every conv2 tile the map takes (d8s_conv2_as, TW <= W) writes the exact slot and nothing else."""
+    c = cases.conv2_case(H, N=N, seed=31, W=W)
+    _, q_x = checks.exact_conv2(c)
+    taken = [v for v, tw in zip(range(1, 9), (32, 32, 32, 16, 8, 4, 2, 1)) if tw <= W]
+    for v in taken:
+        print(f"conv2 N={N} H={H} W={W} variant {dense8s.C2_VARIANTS[v]}", flush=True)
+        got, others = checks.run_conv2(c, dev, variant=v)
+        assert np.array_equal(got, q_x), (dense8s.C2_VARIANTS[v], checks.bytes_cmp(got, q_x))
+        assert np.all(others == 0x5A)
 
 
 @pytest.mark.parametrize("H,W,C,c0,N", [
@@ -267,8 +295,9 @@ def test_dense_block(dev, H, W, c0, L, N):
                                          (8, 1024, 128, None), (6, 416, 64, 416), (4, 256, 64, 768),
                                          (4, 192, 64, 1024)])
 def test_transition(dev, S, C, c0, cout):
-    """The DenseNet169 geometries, then ragged pixel counts, every activation prefetch depth (the
-    largest of 4, 2, 1 dividing the group count) and tile count per wave (1-6 and 8, ragged too)."""
+    """The DenseNet169 geometries, then ragged pixel counts, both default activation prefetch depths (2
+    for an even group count, else 1; every variant in `test_transition_every_variant`) and tile count
+    per wave (1-6 and 8, ragged too)."""
     t = cases.trans_case(S, C, N=4, c0=c0, cout=cout)
     print(f"transition S={S} C={C} cout={t['cout']}", flush=True)
     got = checks.run_trans(t, dev)
@@ -281,6 +310,24 @@ def test_transition(dev, S, C, c0, cout):
                          t["gdf"], t["cout"], sel)
     assert np.array_equal(S_o, S_x[sel]) and np.array_equal(q_o, got[sel])
     assert float((np.abs(q_x) == 127).mean()) < 0.2 and float((q_x == 0).mean()) < 0.5
+
+
+@pytest.mark.parametrize("S,C,c0,cout,N", [(32, 1280, 256, None, 4), (32, 1280, 256, None, 40),
+                                           (8, 320, 64, None, 4), (12, 640, 128, 512, 3), (6, 96, 32, 32, 2),
+                                           (16, 128, 64, None, 2)])
+def test_transition_every_variant(dev, S, C, c0, cout, N):
+    """Every transition variant the shape takes (d8s_transition_as: activation prefetch depth 4, 2, 1,
+    two or four weight register sets) writes the exact outputs."""
+    t = cases.trans_case(S, C, N=N, c0=c0, cout=cout)
+    _, q_x = checks.exact_trans(t)
+    args, _keep = checks.trans_args(t, dev)
+    q = hip.library().d8s_transition_variant
+    taken = [v for v in dense8s.TRANS_VARIANTS if q(ctypes.byref(args), v) == v]
+    assert 4 in taken and (1 in taken) == (t["G"] % 4 == 0) and (3 in taken) == (t["G"] % 2 == 0)
+    for v in taken:
+        print(f"transition S={S} C={C} cout={t['cout']} N={N} variant {dense8s.TRANS_VARIANTS[v]}", flush=True)
+        got = checks.run_trans(t, dev, variant=v)
+        assert np.array_equal(got, q_x), (dense8s.TRANS_VARIANTS[v], checks.bytes_cmp(got, q_x))
 
 
 def test_transition_many_workgroups(dev):

@@ -2,6 +2,8 @@
 errors (the reference's ValueError paths, src/knee/dense8s.py:954-956,1121-1124,1259-1260,1279-1280)."""
 from __future__ import annotations
 
+import json
+
 import numpy as np
 import pytest
 import torch
@@ -222,3 +224,30 @@ def test_inflight_gate_without_a_limit_records_nothing():
     g.admit()
     g.done(None)
     assert len(g.events) == 0
+
+
+def test_recorded_kernel_variants(plan169):
+    """Kernel variants recorded per block (`pack_meta(bm=, c2=, tbm=)`: "bm" a list per layer, "c2" per
+    side, "tbm" per transition, as the reference's packages record their kernels) map back to variant
+    ids; the reference's own kernel names (CUDA kernels) name none and leave the library's choice;
+    names that are no variant are refused."""
+    _, plan = plan169
+    meta = dense8s.pack_meta(plan, 24, bm={"b1l0": "p64", "b2l3": "k2"}, c2={64: "32x4", "32": "16x4"},
+                             tbm={"t2": "d4w4"})
+    blocks = meta["blocks"]
+    assert blocks[1]["bm"][0] == "p64" and blocks[2]["bm"][3] == "k2" and blocks[0]["bm"] == [None] * 6
+    assert blocks[1]["c2"] == "32x4" and blocks[2]["c2"] == "16x4" and blocks[0]["c2"] is None
+    assert blocks[2]["tbm"] == "d4w4" and blocks[3]["tbm"] is None
+    assert dense8s.recorded_variants(meta) == {("conv1", 1, 0): 2, ("conv1", 2, 3): 4, ("conv2", 1): 2,
+                                               ("conv2", 2): 4, ("trans", 2): 2}
+    dense8s.validate_meta(meta)
+    ref = json.loads(json.dumps(meta))
+    for b in ref["blocks"]:
+        b["bm"], b["c2"], b["tbm"] = ["w64_pl"] * b["L"], [16, 8, "p4u_pl"], "q128"
+    assert dense8s.recorded_variants(ref) == {}
+    for kw in ({"bm": {"b1l0": "u128h"}}, {"c2": {64: "8x32"}}, {"tbm": {"t0": "q128"}}):
+        with pytest.raises(ValueError, match="variant"):
+            dense8s.pack_meta(plan, 24, **kw)
+    names = [set(t.values()) for t in (dense8s.C1_VARIANTS, dense8s.C2_VARIANTS, dense8s.TRANS_VARIANTS)]
+    assert all(len(n) == len(t) for n, t in zip(names, (dense8s.C1_VARIANTS, dense8s.C2_VARIANTS,
+                                                        dense8s.TRANS_VARIANTS)))
