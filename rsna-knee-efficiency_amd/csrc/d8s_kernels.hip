@@ -2278,6 +2278,19 @@ __global__ __launch_bounds__(DP_NT, 1) void k_dparts(D8sPartsArgs a) {
                 // beside the MFMAs already issued (an item past the last chunk is never read).
                 const u32x4* bsrc = s_pro + (ch & 1) * ITEMS * 64 + lane;
                 constexpr int EVERY = QC / IPW;            // steps per prologue item
+                // the chunk's operands read from LDS together, so the steps wait for one latency (where
+                // the registers allow: up to 8 operands)
+                constexpr bool BX = QC * NPT <= 8;
+                u32x4 bx[BX ? QC : 1][BX ? NPT : 1];
+                if constexpr (BX) {
+#pragma unroll
+                    for (int u = 0; u < QC; ++u) {
+                        const int gi = (KH == 2 ? 2 * u + hv : u);
+#pragma unroll
+                        for (int tt = 0; tt < NPT; ++tt)
+                            bx[u][tt] = bsrc[(gi * PT + (KH == 2 ? 0 : hv * NPT + tt)) * 64];
+                    }
+                }
 #pragma unroll
                 for (int u = 0; u < QC; ++u) {
                     const int q = ch * QC + u, g = DP_G(q);
@@ -2288,7 +2301,7 @@ __global__ __launch_bounds__(DP_NT, 1) void k_dparts(D8sPartsArgs a) {
 #pragma unroll
                     for (int tt = 0; tt < NPT; ++tt) {
                         const int t = KH == 2 ? 0 : hv * NPT + tt;
-                        acc[tt] = mfma_i8(wa, bsrc[(gi * PT + t) * 64], acc[tt]);
+                        acc[tt] = mfma_i8(wa, BX ? bx[BX ? u : 0][BX ? tt : 0] : bsrc[(gi * PT + t) * 64], acc[tt]);
                     }
                     if ((u + 1) % EVERY == 0) {
                         const int qi = (u + 1) / EVERY - 1;    // item wave + 8 qi of chunk ch + 1
