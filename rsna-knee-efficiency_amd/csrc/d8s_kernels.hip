@@ -1983,18 +1983,21 @@ __global__ __launch_bounds__(DB_NT, 1) void k_dblock(D8sBlockArgs a0, D8sBlockAr
             i32x16 acc2;
 #pragma unroll
             for (int v = 0; v < 16; ++v) acc2[v] = 128 * s_w2sum[res_row(v, h)];
-            u32x4 aw[2], bq[2];
+            // operands read C2D steps ahead (an LDS read takes longer than one MFMA step)
+            constexpr int C2D = 3;
+            u32x4 aw[4], bq[4];
 #define DB_FETCH(s, sl)                                                                           \
     do {                                                                                          \
         const int c_ = (s) / 9, tap_ = (s) % 9;                                                   \
         aw[sl] = s_w[swz((c_ * 9 + tap_) * 32 + j, h)];                                           \
         bq[sl] = s_b[c_ * WIN * 2 + swz(q0 + (tap_ / 3) * BW + (tap_ % 3), h)];                   \
     } while (0)
-            DB_FETCH(0, 0);
+#pragma unroll
+            for (int f = 0; f < C2D; ++f) DB_FETCH(f, f);
 #pragma unroll
             for (int s = 0; s < 36; ++s) {
-                if (s + 1 < 36) DB_FETCH(s + 1, (s + 1) & 1);
-                acc2 = mfma_i8(aw[s & 1], bq[s & 1], acc2);
+                if (s + C2D < 36) DB_FETCH(s + C2D, (s + C2D) & 3);
+                acc2 = mfma_i8(aw[s & 3], bq[s & 3], acc2);
                 __builtin_amdgcn_sched_barrier(0);
             }
 #undef DB_FETCH
