@@ -2341,14 +2341,26 @@ __global__ __launch_bounds__(DP_NT, 1) void k_dparts(D8sPartsArgs a) {
 #pragma unroll
             for (int v = 0; v < 16; ++v) acc2[v] = s2 == 0 ? 128 * s_w2sum[res_row(v, h)] : 0;
             constexpr int NS = (36 + S2 - 1) / S2;
+            // the steps' operands read C2D steps ahead (an LDS read takes longer than one MFMA step;
+            // the compiler on its own waits for each pair of reads), where the registers allow
+            constexpr int C2D = PT <= 4 ? 3 : 1;
+#define DP_C2F(k_, sl_)                                                                           \
+    do {                                                                                          \
+        const int st_ = min(s2 + (k_) * S2, 35);                                                  \
+        const int cc_ = st_ / 9, tap_ = st_ - 9 * cc_, ty_ = tap_ / 3, tx_ = tap_ - 3 * ty_;       \
+        c2w[sl_] = s_w[swz(st_ * 32 + j, h)];                                                     \
+        c2b[sl_] = s_b[cc_ * WIN * 2 + swz(q0 + ty_ * BW + tx_, h)];                              \
+    } while (0)
 #define DP_CONV2()                                                                                \
-    _Pragma("unroll") for (int k_ = 0; k_ < NS; ++k_) {                                           \
-        const int st_ = s2 + k_ * S2;                                                             \
-        if (st_ < 36) {                                                                           \
-            const int cc_ = st_ / 9, tap_ = st_ - 9 * cc_, ty_ = tap_ / 3, tx_ = tap_ - 3 * ty_;   \
-            acc2 = mfma_i8(s_w[swz(st_ * 32 + j, h)], s_b[cc_ * WIN * 2 + swz(q0 + ty_ * BW + tx_, h)], acc2); \
+    do {                                                                                          \
+        u32x4 c2w[4], c2b[4];                                                                     \
+        _Pragma("unroll") for (int f_ = 0; f_ < C2D; ++f_) DP_C2F(f_, f_);                        \
+        _Pragma("unroll") for (int k_ = 0; k_ < NS; ++k_) {                                       \
+            if (k_ + C2D < NS) DP_C2F(k_ + C2D, (k_ + C2D) & 3);                                  \
+            if (s2 + k_ * S2 < 36) acc2 = mfma_i8(c2w[k_ & 3], c2b[k_ & 3], acc2);                \
+            __builtin_amdgcn_sched_barrier(0);                                                    \
         }                                                                                         \
-    }
+    } while (0)
             // the neighbours' rows into the halo rows (window row 0 = the band above's last row, row
             // R + 1 = the band below's first row), polling each pair until its tag is current; a
             // thread's first pair is read before the inner tiles' MFMAs (an edge band reads its own
@@ -2396,6 +2408,7 @@ __global__ __launch_bounds__(DP_NT, 1) void k_dparts(D8sPartsArgs a) {
                 DP_CONV2();
             }
 #undef DP_CONV2
+#undef DP_C2F
             // layer i's conv2 tables (stored at the start of (C))
             {
                 const D8sLayerP ln = DP_LP(min(i, L - 1));
