@@ -721,22 +721,26 @@ __global__ __launch_bounds__(256, 2) void k_conv2(D8sConv2Args a0, int tiles_x, 
         i32x16 acc[PT];
 #pragma unroll
         for (int t = 0; t < PT; ++t) acc[t] = init;
-        // K steps (plane, tap); the operands of step s + 1 are read from LDS before step s's MFMAs
+        // K steps (plane, tap); the operands of step s + FD are read from LDS before step s's MFMAs (an
+        // LDS read takes longer than a step's MFMAs: FD 3 for one pixel tile, 2 for two)
         constexpr int NS = KSPL == 1 ? 36 : 9;
-        u32x4 aw[2], bx[2][PT];
-        auto fetch = [&](int s, int slot) {
+        constexpr int FD = PT == 1 ? 3 : PT == 2 ? 2 : 1;
+        u32x4 aw[4], bx[4][PT];
+        auto fetch = [&](int s, int slot) INLINE {
             const int c = KSPL == 1 ? s / 9 : wave, tap = s % 9;
             const int off = (tap / 3) * HWd + (tap % 3);
             aw[slot] = s_w[swz((c * 9 + tap) * 32 + j, h)];
 #pragma unroll
             for (int t = 0; t < PT; ++t) bx[slot][t] = s_x[c * HP * 2 + swz(q0[t] + off, h)];
         };
-        fetch(0, 0);
+#pragma unroll
+        for (int f = 0; f < FD; ++f) fetch(f, f);
 #pragma unroll
         for (int s = 0; s < NS; ++s) {
-            if (s + 1 < NS) fetch(s + 1, (s + 1) & 1);
+            if (s + FD < NS) fetch(s + FD, (s + FD) & 3);
 #pragma unroll
-            for (int t = 0; t < PT; ++t) acc[t] = mfma_i8(aw[s & 1], bx[s & 1][t], acc[t]);
+            for (int t = 0; t < PT; ++t) acc[t] = mfma_i8(aw[s & 3], bx[s & 3][t], acc[t]);
+            if constexpr (FD > 1) __builtin_amdgcn_sched_barrier(0);
         }
         if (KSPL > 1) {
             // waves 1..3 hand their partial sums to wave 0 (rows of 16 int32 per lane, padded)
