@@ -16,8 +16,10 @@ The two seeds' passes of a step run from two streams (`--serial`: one after the 
 `roofline`: the dominant kernel family: its launches of a configuration-5 pass recorded R times in a HIP
 graph and replayed between HIP events on the encoder's stream (algorithmic bytes of a launch / the
 average launch time); `frac_in_pass` the same family timed inside a whole pass, `in_schedule` inside a
-pass that shares the GPU with the other seed's; `step_hbm_frac`: both passes' algorithmic bytes over
-the timed step time.  `roofline_c4`: configuration 4's dominant launch (the 32 x 32 banded block)
+pass that shares the GPU with the other seed's; `roofline_runner_up`: the second family by time (the
+band layers of block 0 and the chained launches of block 2 take about as long, so either can lead),
+against HBM and the int8 MFMA peak; `step_hbm_frac`: both passes' algorithmic bytes over the timed
+step time.  `roofline_c4`: configuration 4's dominant launch (the 32 x 32 banded block)
 against the int8 MFMA peak.  `kernels`: configurations 2 and 3 case by case (`--path kernels` alone).
 `cpu_baseline`: the float32 DenseNet169 forward (`oracle/fp32.py`) on the host cores at batch 1
 (slices/s) and at batch 24 (one study, `study_latency_ms`).
@@ -380,6 +382,19 @@ def mfma_summary(pmc_dir: str, passes: int) -> str:
         lines.append(f"| {fam} | {len(ds)} | {util:.1f} | {ops / 1e9:.1f} | {a / 1e9:.1f} | "
                      f"{ops / a if a else float('nan'):.3f} |")
     return "\n".join(lines)
+
+
+def family_roofline(f: str, fam: dict, byts: dict, ops: dict) -> dict:
+    """HBM and int8 MFMA roofline figures of a kernel family from its per-pass time (`time_families`),
+    bytes (`kernel_bytes`) and operations (`kernel_ops`)."""
+    launches = len(byts[f])
+    avg_ms = fam[f] / launches
+    gbs = sum(byts[f]) / launches / (avg_ms * 1e-3) / 1e9
+    tops = ops.get(f, 0.0) / (fam[f] * 1e-3) / 1e12
+    return {"kernel": f"d8s_{f} (all {launches} launches of a pass)", "bound": "hbm",
+            "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
+            "avg_launch_ms": round(avg_ms, 5), "algorithmic_bytes_per_launch": int(sum(byts[f]) / launches),
+            "int8_tops": round(tops, 1), "frac_mfma_datasheet": round(tops / I8_PEAK_TOPS, 4)}
 
 
 def c4_summary(trace_csv: str) -> str:
@@ -1298,7 +1313,8 @@ def main() -> None:
     byts = kernel_bytes(encs[0].meta, nb, encs[0].fused)
     ops = kernel_ops(encs[0].meta, nb, encs[0].fused)
     pass_ms = sum(fam.values())
-    dom = max(("conv1", "conv2", "chain", "dense", "block", "trans", "stem"), key=lambda k: fam.get(k, 0.0))
+    ranked = sorted(("conv1", "conv2", "chain", "dense", "block", "trans", "stem"), key=lambda k: -fam.get(k, 0.0))
+    dom = ranked[0]
     dom_bytes = sum(byts[dom])
     launches = len(byts[dom])
     avg_ms = fam[dom] / launches
@@ -1344,6 +1360,7 @@ def main() -> None:
                      "avg_launch_ms": round(avg_ms, 5),
                      "frac_in_pass": in_pass.get("frac"), "in_pass": in_pass, "in_schedule": in_sched},
         "step_hbm_frac": round(2 * total_bytes / (dt / args.steps) / 1e9 / HBM_PEAK_GBS, 4),
+        "roofline_runner_up": family_roofline(ranked[1], fam, byts, ops),
         "roofline_c4": roof4,
     }
     # the upstream preparation (raw crops -> uint8 volume), its own throughput on the same GPU

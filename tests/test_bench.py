@@ -236,6 +236,17 @@ def test_c4_counter_summary_per_banded_kernel(tmp_path):
     assert any(ln.startswith("| `k_dparts<1>`") for ln in out.splitlines())
 
 
+def test_family_roofline_divides_per_launch():
+    # 31 launches of 100.8 MB in 0.837 ms per pass: 27 us per launch, 3.733 TB/s; 1 POP per pass
+    fam, byts, ops = {"chain": 0.837}, {"chain": [100.8e6] * 31}, {"chain": 1e15 * 0.837e-3}
+    r = bench.family_roofline("chain", fam, byts, ops)
+    assert r["avg_launch_ms"] == pytest.approx(0.027, abs=1e-5)
+    assert r["achieved"] == pytest.approx(100.8e6 / 27e-6 / 1e9, abs=0.1)
+    assert r["frac"] == pytest.approx(r["achieved"] / bench.HBM_PEAK_GBS, abs=1e-4)
+    assert r["int8_tops"] == pytest.approx(1000.0, abs=0.1) and r["frac_mfma_datasheet"] == pytest.approx(0.2)
+    assert r["algorithmic_bytes_per_launch"] == int(100.8e6) and "31 launches" in r["kernel"]
+
+
 def test_more_than_one_gpu_is_refused():
     env = dict(os.environ, PYTHONPATH=str(ROOT))
     r = subprocess.run([sys.executable, str(ROOT / "bench.py"), "--gpus", "2"], capture_output=True,
