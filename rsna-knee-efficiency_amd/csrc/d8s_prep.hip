@@ -966,6 +966,120 @@ __global__ void __launch_bounds__(NT) k_grid_sample(D8sGridArgs a) {
     }
 }
 
+// The uint8 gather + table + bilinear view (KIND 1 above) with four consecutive output pixels of a row
+// per thread (W a multiple of 4, the grid 16-byte aligned).  Where the four pixels share their source
+// rows and all their taps lie in one 8-byte aligned window of those rows inside the image (a zoom or
+// shift of at most about 1.75 source pixels per output pixel), each image's taps come from two dword
+// loads per row instead of sixteen byte loads; elsewhere each pixel takes KIND 1's taps.  Per pixel the
+// arithmetic is KIND 1's (the same values, weights and fma order), so the outputs are identical.
+__global__ void __launch_bounds__(NT) k_grid_sample4(D8sGridArgs a) {
+    __shared__ uint16_t s_lut[256];
+    if (threadIdx.x < 256) s_lut[threadIdx.x] = ((const uint16_t*)a.lut)[threadIdx.x];
+    __syncthreads();
+    const int HW = a.H * a.W;
+    const int p0 = 4 * (blockIdx.x * NT + threadIdx.x);
+    const int n0 = blockIdx.y * GIMG, n1 = min(n0 + GIMG, a.N);
+    if (p0 >= HW) return;
+    int64_t pl[GIMG];
+#pragma unroll
+    for (int i = 0; i < GIMG; ++i) {
+        const int n = min(n0 + i, n1 - 1), b = n / a.M, m = n - b * a.M;
+        int64_t si = ((const int64_t*)a.slice_idx)[m];
+        si = si < 0 ? 0 : si >= a.SK ? (int64_t)a.SK - 1 : si;
+        pl[i] = ((int64_t)b * a.SK + si) * HW;
+    }
+    const uint4 gq = ((const uint4*)a.grid)[p0 >> 2];         // 4 pixels x (gx, gy) fp16
+    const uint32_t gw[4] = {gq.x, gq.y, gq.z, gq.w};
+    float w[4][4];
+    int x0[4], y0[4];
+    bool ok[4][4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const __half2 g = __builtin_bit_cast(__half2, gw[k]);
+        const float gx = __low2float(g), gy = __high2float(g);
+        const float ix = __builtin_fmaf(gx + 1.0f, (float)a.W, -1.0f) * 0.5f;
+        const float iy = __builtin_fmaf(gy + 1.0f, (float)a.H, -1.0f) * 0.5f;
+        x0[k] = (int)floorf(ix);
+        y0[k] = (int)floorf(iy);
+        const int x1 = x0[k] + 1, y1 = y0[k] + 1;
+        w[k][0] = ((float)x1 - ix) * ((float)y1 - iy);
+        w[k][1] = (ix - (float)x0[k]) * ((float)y1 - iy);
+        w[k][2] = ((float)x1 - ix) * (iy - (float)y0[k]);
+        w[k][3] = (ix - (float)x0[k]) * (iy - (float)y0[k]);
+        const bool vx0 = x0[k] >= 0 && x0[k] < a.W, vx1 = x1 >= 0 && x1 < a.W;
+        const bool vy0 = y0[k] >= 0 && y0[k] < a.H, vy1 = y1 >= 0 && y1 < a.H;
+        ok[k][0] = vy0 && vx0;
+        ok[k][1] = vy0 && vx1;
+        ok[k][2] = vy1 && vx0;
+        ok[k][3] = vy1 && vx1;
+    }
+    const int xmin = min(min(x0[0], x0[1]), min(x0[2], x0[3])), xmax = max(max(x0[0], x0[1]), max(x0[2], x0[3]));
+    const int base = xmin & ~3;
+    const bool fast = y0[0] == y0[1] && y0[0] == y0[2] && y0[0] == y0[3] && y0[0] >= 0 && y0[0] + 1 < a.H &&
+                      xmin >= 0 && xmax + 1 - base <= 7 && base + 8 <= a.W;
+    float acc[GIMG][4];
+    if (fast) {
+        // rows y0, y0 + 1 of each image: bytes base .. base + 7 as two dwords per row
+        const int r0 = y0[0] * a.W + base;
+        uint32_t d[GIMG][4];
+#pragma unroll
+        for (int i = 0; i < GIMG; ++i) {
+            const uint32_t* q0 = (const uint32_t*)((const uint8_t*)a.src + pl[i] + r0);
+            const uint32_t* q1 = (const uint32_t*)((const uint8_t*)a.src + pl[i] + r0 + a.W);
+            d[i][0] = q0[0];
+            d[i][1] = q0[1];
+            d[i][2] = q1[0];
+            d[i][3] = q1[1];
+        }
+#pragma unroll
+        for (int i = 0; i < GIMG; ++i) {
+            const uint64_t row0 = (uint64_t)d[i][0] | ((uint64_t)d[i][1] << 32);
+            const uint64_t row1 = (uint64_t)d[i][2] | ((uint64_t)d[i][3] << 32);
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const int o = 8 * (x0[k] - base);
+                const uint32_t t0 = (uint32_t)(row0 >> o), t1 = (uint32_t)(row1 >> o);
+                const float v[4] = {__half2float(__ushort_as_half(s_lut[t0 & 0xffu])),
+                                    __half2float(__ushort_as_half(s_lut[(t0 >> 8) & 0xffu])),
+                                    __half2float(__ushort_as_half(s_lut[t1 & 0xffu])),
+                                    __half2float(__ushort_as_half(s_lut[(t1 >> 8) & 0xffu]))};
+                float s = 0.0f;
+#pragma unroll
+                for (int t = 0; t < 4; ++t) s = __builtin_fmaf(v[t], w[k][t], s);
+                acc[i][k] = s;
+            }
+        }
+    } else {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const int off[4] = {ok[k][0] ? y0[k] * a.W + x0[k] : 0, ok[k][1] ? y0[k] * a.W + x0[k] + 1 : 0,
+                                ok[k][2] ? (y0[k] + 1) * a.W + x0[k] : 0, ok[k][3] ? (y0[k] + 1) * a.W + x0[k] + 1 : 0};
+            float v[GIMG][4];
+#pragma unroll
+            for (int i = 0; i < GIMG; ++i)
+#pragma unroll
+                for (int t = 0; t < 4; ++t) v[i][t] = (float)((const uint8_t*)a.src)[pl[i] + off[t]];
+#pragma unroll
+            for (int i = 0; i < GIMG; ++i) {
+                float s = 0.0f;
+#pragma unroll
+                for (int t = 0; t < 4; ++t)
+                    if (ok[k][t]) s = __builtin_fmaf(__half2float(__ushort_as_half(s_lut[(int)v[i][t]])), w[k][t], s);
+                acc[i][k] = s;
+            }
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < GIMG; ++i)
+        if (n0 + i < n1) {
+            const uint32_t lo = (uint32_t)__half_as_ushort(__float2half_rn(acc[i][0])) |
+                                ((uint32_t)__half_as_ushort(__float2half_rn(acc[i][1])) << 16);
+            const uint32_t hi = (uint32_t)__half_as_ushort(__float2half_rn(acc[i][2])) |
+                                ((uint32_t)__half_as_ushort(__float2half_rn(acc[i][3])) << 16);
+            *(uint2*)((uint16_t*)a.out + (int64_t)(n0 + i) * HW + p0) = make_uint2(lo, hi);
+        }
+}
+
 // ---- host side ----------------------------------------------------------------------------------
 #define PREQ(cond, msg) \
     do { if (!(cond)) return d8s_host_fail((int)hipErrorInvalidValue, std::string(what) + ": " + (msg)); } while (0)
@@ -1217,7 +1331,10 @@ extern "C" int d8s_grid_sample(const D8sGridArgs* a, void* stream) {
     PREQ(a->N >= 1 && a->N < 65536 * GIMG, "N must be 1 .. 524287");
     const dim3 grid((unsigned)(((int64_t)a->H * a->W + NT - 1) / NT), (unsigned)((a->N + GIMG - 1) / GIMG));
     hipStream_t st = (hipStream_t)stream;
-    if (a->kind == 1 && a->grid == 0)
+    if (a->kind == 1 && a->grid != 0 && a->W % 4 == 0 && a->grid % 16 == 0 && a->out % 8 == 0 && a->src % 4 == 0) {
+        const dim3 grid4((unsigned)(((int64_t)a->H * a->W / 4 + NT - 1) / NT), grid.y);
+        k_grid_sample4<<<grid4, NT, 0, st>>>(*a);
+    } else if (a->kind == 1 && a->grid == 0)
         k_grid_sample<2><<<grid, NT, 0, st>>>(*a);
     else if (a->kind == 1)
         k_grid_sample<1><<<grid, NT, 0, st>>>(*a);

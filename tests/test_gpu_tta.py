@@ -66,13 +66,22 @@ def test_affine_windows_identity_and_full_size(dev):
     assert torch.equal(got, _reference(w, 1.10, 0.0, 0.0))
 
 
-@pytest.mark.parametrize("view", [(1.0, 0.0, 0.0), (1.10, 0.0, 0.0)])
-def test_windows_u8_is_the_reference_chain(dev, view):
-    """gather_u8_f16 + affine_windows of the submission path (infer.py:986-1012) in one kernel."""
-    b, s, k, h, w = 2, 2, 7, 64, 48
+U8_SHAPES = [(64, 48), (40, 46), (512, 512)]
+
+
+@pytest.mark.parametrize("view", [(1.0, 0.0, 0.0)] + VIEWS, ids=["identity"] + [f"s{v[0]}_tx{v[1]}_ty{v[2]}" for v in VIEWS])
+@pytest.mark.parametrize("hw", U8_SHAPES, ids=[f"{h}x{w}" for h, w in U8_SHAPES])
+def test_windows_u8_is_the_reference_chain(dev, view, hw):
+    """gather_u8_f16 + affine_windows of the submission path (infer.py:986-1012) in one kernel: every
+    view, on widths that take the four-pixel kernel (a multiple of 4, both its window path and its
+    per-pixel path at the borders) and one that does not."""
+    h, w = hw
+    b, s, k = (2, 2, 7) if h < 512 else (1, 1, 9)
+    print(f"windows_u8 view {view} {h}x{w}", flush=True)
     g = torch.Generator().manual_seed(5)
     v = torch.randint(0, 256, (b, s, k, h, w), generator=g, dtype=torch.uint8).to(dev)
-    idx = torch.tensor([0, 1, 2, 2, 3, 4, 8, 9, 13], dtype=torch.int64, device=dev)
+    idx = torch.tensor([0, 1, 2, 2, 3, 4, 8, 9, 13] if s * k > 13 else [0, 1, 2, 2, 3, 4, 6, 7, 8],
+                       dtype=torch.int64, device=dev)
     depth = 3
     out = torch.empty((b * idx.numel() // depth, depth, h, w), dtype=torch.float16, device=dev)
     tta.windows_u8(v, idx, out, *view)
