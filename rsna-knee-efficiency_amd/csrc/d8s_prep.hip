@@ -972,17 +972,19 @@ __global__ void __launch_bounds__(NT) k_grid_sample(D8sGridArgs a) {
 // shift of at most about 1.75 source pixels per output pixel), each image's taps come from two dword
 // loads per row instead of sixteen byte loads; elsewhere each pixel takes KIND 1's taps.  Per pixel the
 // arithmetic is KIND 1's (the same values, weights and fma order), so the outputs are identical.
+// GIMG4 images per thread (16 measured 8 % faster than 8 and than 4 at the submission's shape).
+constexpr int GIMG4 = 16;
 __global__ void __launch_bounds__(NT) k_grid_sample4(D8sGridArgs a) {
     __shared__ uint16_t s_lut[256];
     if (threadIdx.x < 256) s_lut[threadIdx.x] = ((const uint16_t*)a.lut)[threadIdx.x];
     __syncthreads();
     const int HW = a.H * a.W;
     const int p0 = 4 * (blockIdx.x * NT + threadIdx.x);
-    const int n0 = blockIdx.y * GIMG, n1 = min(n0 + GIMG, a.N);
+    const int n0 = blockIdx.y * GIMG4, n1 = min(n0 + GIMG4, a.N);
     if (p0 >= HW) return;
-    int64_t pl[GIMG];
+    int64_t pl[GIMG4];
 #pragma unroll
-    for (int i = 0; i < GIMG; ++i) {
+    for (int i = 0; i < GIMG4; ++i) {
         const int n = min(n0 + i, n1 - 1), b = n / a.M, m = n - b * a.M;
         int64_t si = ((const int64_t*)a.slice_idx)[m];
         si = si < 0 ? 0 : si >= a.SK ? (int64_t)a.SK - 1 : si;
@@ -1017,13 +1019,13 @@ __global__ void __launch_bounds__(NT) k_grid_sample4(D8sGridArgs a) {
     const int base = xmin & ~3;
     const bool fast = y0[0] == y0[1] && y0[0] == y0[2] && y0[0] == y0[3] && y0[0] >= 0 && y0[0] + 1 < a.H &&
                       xmin >= 0 && xmax + 1 - base <= 7 && base + 8 <= a.W;
-    float acc[GIMG][4];
+    float acc[GIMG4][4];
     if (fast) {
         // rows y0, y0 + 1 of each image: bytes base .. base + 7 as two dwords per row
         const int r0 = y0[0] * a.W + base;
-        uint32_t d[GIMG][4];
+        uint32_t d[GIMG4][4];
 #pragma unroll
-        for (int i = 0; i < GIMG; ++i) {
+        for (int i = 0; i < GIMG4; ++i) {
             const uint32_t* q0 = (const uint32_t*)((const uint8_t*)a.src + pl[i] + r0);
             const uint32_t* q1 = (const uint32_t*)((const uint8_t*)a.src + pl[i] + r0 + a.W);
             d[i][0] = q0[0];
@@ -1032,7 +1034,7 @@ __global__ void __launch_bounds__(NT) k_grid_sample4(D8sGridArgs a) {
             d[i][3] = q1[1];
         }
 #pragma unroll
-        for (int i = 0; i < GIMG; ++i) {
+        for (int i = 0; i < GIMG4; ++i) {
             const uint64_t row0 = (uint64_t)d[i][0] | ((uint64_t)d[i][1] << 32);
             const uint64_t row1 = (uint64_t)d[i][2] | ((uint64_t)d[i][3] << 32);
 #pragma unroll
@@ -1054,13 +1056,13 @@ __global__ void __launch_bounds__(NT) k_grid_sample4(D8sGridArgs a) {
         for (int k = 0; k < 4; ++k) {
             const int off[4] = {ok[k][0] ? y0[k] * a.W + x0[k] : 0, ok[k][1] ? y0[k] * a.W + x0[k] + 1 : 0,
                                 ok[k][2] ? (y0[k] + 1) * a.W + x0[k] : 0, ok[k][3] ? (y0[k] + 1) * a.W + x0[k] + 1 : 0};
-            float v[GIMG][4];
+            float v[GIMG4][4];
 #pragma unroll
-            for (int i = 0; i < GIMG; ++i)
+            for (int i = 0; i < GIMG4; ++i)
 #pragma unroll
                 for (int t = 0; t < 4; ++t) v[i][t] = (float)((const uint8_t*)a.src)[pl[i] + off[t]];
 #pragma unroll
-            for (int i = 0; i < GIMG; ++i) {
+            for (int i = 0; i < GIMG4; ++i) {
                 float s = 0.0f;
 #pragma unroll
                 for (int t = 0; t < 4; ++t)
@@ -1070,7 +1072,7 @@ __global__ void __launch_bounds__(NT) k_grid_sample4(D8sGridArgs a) {
         }
     }
 #pragma unroll
-    for (int i = 0; i < GIMG; ++i)
+    for (int i = 0; i < GIMG4; ++i)
         if (n0 + i < n1) {
             const uint32_t lo = (uint32_t)__half_as_ushort(__float2half_rn(acc[i][0])) |
                                 ((uint32_t)__half_as_ushort(__float2half_rn(acc[i][1])) << 16);
@@ -1332,7 +1334,7 @@ extern "C" int d8s_grid_sample(const D8sGridArgs* a, void* stream) {
     const dim3 grid((unsigned)(((int64_t)a->H * a->W + NT - 1) / NT), (unsigned)((a->N + GIMG - 1) / GIMG));
     hipStream_t st = (hipStream_t)stream;
     if (a->kind == 1 && a->grid != 0 && a->W % 4 == 0 && a->grid % 16 == 0 && a->out % 8 == 0 && a->src % 4 == 0) {
-        const dim3 grid4((unsigned)(((int64_t)a->H * a->W / 4 + NT - 1) / NT), grid.y);
+        const dim3 grid4((unsigned)(((int64_t)a->H * a->W / 4 + NT - 1) / NT), (unsigned)((a->N + GIMG4 - 1) / GIMG4));
         k_grid_sample4<<<grid4, NT, 0, st>>>(*a);
     } else if (a->kind == 1 && a->grid == 0)
         k_grid_sample<2><<<grid, NT, 0, st>>>(*a);
