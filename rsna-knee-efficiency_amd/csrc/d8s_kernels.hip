@@ -1801,6 +1801,11 @@ DEV float ldg_f(const void* p) { return __uint_as_float(*(gu32*)p); }
 // weights are requested before the layer's tables are staged.
 // ------------------------------------------------------------------------------------------------
 static constexpr int DB_NT = 512;                          // 8 waves: 8 x 32 pixels
+
+DEV const uint8_t* db_sel(bool c, const uint8_t* a, const uint8_t* b) {
+    const uint64_t ua = (uint64_t)a, ub = (uint64_t)b, m = c ? ~0ull : 0ull;
+    return (const uint8_t*)((ua & m) | (ub & ~m));
+}
 static constexpr size_t DB_PRM = 128 * 4 + 128 * 8 + 32 * 4 + 32 * 4;
 
 static size_t dblock_lds(int H, int W, int Gmax) {
@@ -1827,6 +1832,13 @@ __global__ __launch_bounds__(DB_NT, 1) void k_dblock(D8sBlockArgs a0, D8sBlockAr
     const int h = lane >> 5, j = lane & 31;
     const int n = ps.bid;
 
+    // the layers' descriptors in LDS (L <= 64: the launch checks G0 + L - 1 <= 64), so that a layer's
+    // table and weight pointers are an LDS read away, not a global load whose pending count the
+    // conv1 loop's first wait would have to include
+    __shared__ uint64_t s_lp[64 * 7];
+    static_assert(sizeof(D8sLayerP) == 7 * sizeof(uint64_t), "descriptor layout");
+    for (int q = tid; q < min(L, 64) * 7; q += DB_NT) s_lp[q] = ((const uint64_t*)a.layers)[q];
+#define DB_LP(l_) (*(const D8sLayerP*)(s_lp + 7 * (l_)))
     // zero-padding ring of the window (the layers write only its interior)
     {
         const u32x4 pad = {SIGN4, SIGN4, SIGN4, SIGN4};
@@ -1848,13 +1860,16 @@ __global__ __launch_bounds__(DB_NT, 1) void k_dblock(D8sBlockArgs a0, D8sBlockAr
     const uint8_t* segn = (const uint8_t*)a.seg + (int64_t)n * HW * 32;
     const int64_t slot = (int64_t)N * HW * 32;
     // group g's byte at the lane's pixel: a uniform base (scalar registers) plus the lane's 32-bit offset
-#define DB_SRC(g) (((g) < G0 ? in0 + (int64_t)(g) * HW * 32 : segn + (int64_t)((g) - G0) * slot) + offl)
+// (both candidate bases computed and one selected: a branch here would make the loop's waits wait for
+// every load in flight)
+#define DB_SRC(g) (db_sel((g) < G0, in0 + (int64_t)min((g), G0 - 1) * HW * 32, \
+                          segn + (int64_t)max((g) - G0, 0) * slot) + offl)
 
-    // A layer's tables, its first conv1 weight chunk and its first 8 activation groups are requested
+    // A layer's tables, its first conv1 weight chunk and its first 4 activation groups are requested
     // during the previous layer's conv2 (layer 0: before the loop) and stored to LDS after that
     // layer's last barrier.  (Activation groups of the previous layer's own output are requested
-    // after the barrier: when G0 + l < 8.)
-    u32x4 wv[5], stg[4], ra[8];                          // conv2 weights, chunk, activations 8 ahead
+    // after the barrier: when G0 + l < 4.)
+    u32x4 wv[5], stg[4], ra[4];                          // conv2 weights, chunk, activations 4 ahead
     int32_t t_w1sum = 0, t_w2sum = 0;
     float2 t_gd = {0.f, 0.f};
     float t_sc = 0.f;
@@ -1877,11 +1892,12 @@ __global__ __launch_bounds__(DB_NT, 1) void k_dblock(D8sBlockArgs a0, D8sBlockAr
             stg[u_] = ldg_u32x4(w1_ + min(t_ + DB_NT * u_, (G_) * 256 - 1));                      \
     } while (0)
 #define DB_RA(G_)                                                                                 \
-    _Pragma("unroll") for (int s_ = 0; s_ < 8; ++s_)                                              \
+    _Pragma("unroll") for (int s_ = 0; s_ < 4; ++s_)                                              \
         ra[s_] = *(const u32x4*)DB_SRC(s_ < (G_) - 1 ? s_ : (G_) - 1)
     uint32_t offl = off;                                 // (opaque per layer: no address hoisted out
     {                                                    // of the layer loop to live in registers)
-        const D8sLayerP lp0 = a.layers[0];
+        __syncthreads();                                 // the descriptors
+        const D8sLayerP lp0 = DB_LP(0);
         DB_TABLES(lp0, G0);
         DB_RA(G0);
     }
@@ -1889,7 +1905,7 @@ __global__ __launch_bounds__(DB_NT, 1) void k_dblock(D8sBlockArgs a0, D8sBlockAr
 
     for (int l = 0; l < L; ++l) {
         asm volatile("" : "+v"(offl));
-        const D8sLayerP lp = a.layers[l];
+        const D8sLayerP lp = DB_LP(l);
         const int G = G0 + l;
         const int nk = G;
         if (!ra_ready) {                                 // groups of the layer before: now complete
@@ -1930,20 +1946,48 @@ __global__ __launch_bounds__(DB_NT, 1) void k_dblock(D8sBlockArgs a0, D8sBlockAr
             for (int v = 0; v < 16; ++v) acc[c][v] = 128 * s_w1sum[32 * c + res_row(v, h)];
         }
         // step k (group k, the (k % 8)-th of chunk k / 8 in buffer (k / 8) & 1)
+    // a step's prologue tables were read from LDS by the step before (so the prologue starts at once),
+    // its weights at its start (needed only by the MFMAs, after the prologue)
+#define DB_PQ(dst, k)                                                                             \
+    do {                                                                                          \
+        const u32x4* pn_ = (const u32x4*)(s_abh + (k) * 32 + h * 16);                             \
+        _Pragma("unroll") for (int c_ = 0; c_ < 4; ++c_) dst[c_] = pn_[c_];                       \
+    } while (0)
 #define DB_STEP(slot, k)                                                                          \
     do {                                                                                          \
         const int k_ = (k);                                                                       \
         const u32x4* wq_ = s_wc + ((k_ >> 3) & 1) * 2048 + (k_ & 7) * 256 + j + 32 * h;           \
         u32x4 rb_[4];                                                                             \
         _Pragma("unroll") for (int c_ = 0; c_ < 4; ++c_) rb_[c_] = wq_[64 * c_];                  \
-        const u32x4* pp_ = (const u32x4*)(s_abh + k_ * 32 + h * 16);                              \
-        const u32x4 bx_ = pro16(ra[slot], pp_[0], pp_[1], pp_[2], pp_[3]);                        \
-        ra[slot] = *(const u32x4*)DB_SRC(k_ + 8 < klast ? k_ + 8 : klast);                        \
+        DB_PQ(pq[((slot) + 1) & 1], min(k_ + 1, klast));                                          \
+        const u32x4* pp_ = pq[(slot) & 1];                                                        \
+        const u32x4 bx_ = pro16(ra[(slot) & 3], pp_[0], pp_[1], pp_[2], pp_[3]);                  \
+        ra[(slot) & 3] = *(const u32x4*)DB_SRC(k_ + 4 < klast ? k_ + 4 : klast);                  \
         _Pragma("unroll") for (int c_ = 0; c_ < 4; ++c_) acc[c_] = mfma_i8(rb_[c_], bx_, acc[c_]); \
     } while (0)
-        for (int ch = 0; ch < nch; ++ch) {
+        u32x4 pq[2][4];
+        DB_PQ(pq[0], 0);
+        // the whole chunks without a branch, so every wait counts exactly the loads before it (a step
+        // under a branch makes the next wait wait for every load in flight); the next chunk's weights
+        // staged unconditionally (past the last chunk: a clamped read into the idle buffer); then the
+        // last, partial chunk step by step
+        const int nfull = nk >> 3;
+        for (int ch = 0; ch < nfull; ++ch) {
             const int k0 = ch * 8;
-            if (ch + 1 < nch) DB_STAGE_LOAD(ch + 1);
+            DB_STAGE_LOAD(ch + 1);
+            DB_STEP(0, k0);
+            DB_STEP(1, k0 + 1);
+            DB_STEP(2, k0 + 2);
+            DB_STEP(3, k0 + 3);
+            DB_STEP(4, k0 + 4);
+            DB_STEP(5, k0 + 5);
+            DB_STEP(6, k0 + 6);
+            DB_STEP(7, k0 + 7);
+            DB_STAGE_STORE(ch + 1);                      // its buffer was last read in chunk ch - 1
+            __syncthreads();
+        }
+        if (nfull < nch) {
+            const int k0 = nfull * 8;
             DB_STEP(0, k0);
             if (k0 + 1 < nk) DB_STEP(1, k0 + 1);
             if (k0 + 2 < nk) DB_STEP(2, k0 + 2);
@@ -1951,13 +1995,9 @@ __global__ __launch_bounds__(DB_NT, 1) void k_dblock(D8sBlockArgs a0, D8sBlockAr
             if (k0 + 4 < nk) DB_STEP(4, k0 + 4);
             if (k0 + 5 < nk) DB_STEP(5, k0 + 5);
             if (k0 + 6 < nk) DB_STEP(6, k0 + 6);
-            if (k0 + 7 < nk) DB_STEP(7, k0 + 7);
-            if (ch + 1 < nch) {
-                DB_STAGE_STORE(ch + 1);                  // its buffer was last read in chunk ch - 1
-                __syncthreads();
-            }
         }
 #undef DB_STEP
+#undef DB_PQ
 #undef DB_STAGE_STORE
 #undef DB_STAGE_LOAD
 
@@ -1978,7 +2018,7 @@ __global__ __launch_bounds__(DB_NT, 1) void k_dblock(D8sBlockArgs a0, D8sBlockAr
 
         // the next layer's tables and chunk 0 (its first activation groups after the 3x3's MFMAs)
         if (l + 1 < L) {
-            const D8sLayerP ln = a.layers[l + 1];
+            const D8sLayerP ln = DB_LP(l + 1);
             DB_TABLES(ln, G + 1);
         }
 
@@ -2005,7 +2045,7 @@ __global__ __launch_bounds__(DB_NT, 1) void k_dblock(D8sBlockArgs a0, D8sBlockAr
                 __builtin_amdgcn_sched_barrier(0);
             }
 #undef DB_FETCH
-            ra_ready = l + 1 < L && G0 + l >= 8;         // the next layer's groups 0..7 exist already
+            ra_ready = l + 1 < L && G0 + l >= 4;         // the next layer's groups 0..3 exist already
             if (ra_ready) {
                 DB_RA(G + 1);
             }
@@ -2021,6 +2061,7 @@ __global__ __launch_bounds__(DB_NT, 1) void k_dblock(D8sBlockArgs a0, D8sBlockAr
     }
 #undef DB_RA
 #undef DB_TABLES
+#undef DB_LP
 #undef DB_SRC
 }
 
@@ -3816,7 +3857,7 @@ static int dblock_launch(const D8sBlockArgs* a, const D8sBlockArgs* b, hipStream
     REQUIRE(a->H * a->W <= DB_NT / 2, "d8s_dense_block: more than 256 pixels per image");
     REQUIRE(a->G0 + a->L - 1 <= 4 * DB_NT / 32, "d8s_dense_block: more than 64 groups");
     const size_t shm = dblock_lds(a->H, a->W, a->G0 + a->L - 1);
-    REQUIRE(shm + 36864 <= 160 * 1024, "d8s_dense_block: block too large for LDS");
+    REQUIRE(shm + 36864 + 64 * 7 * 8 <= 160 * 1024, "d8s_dense_block: block too large for LDS");
     const int np = b ? 2 : 1;
     hipLaunchKernelGGL(k_dblock, dim3((unsigned)(a->N * np)), dim3(DB_NT), shm, st, *a, b ? *b : *a, a->N);
     return launched("d8s_dense_block");
