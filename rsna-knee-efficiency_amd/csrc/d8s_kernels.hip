@@ -982,8 +982,24 @@ __global__ __launch_bounds__(256, CcShape<W_>::OCC) void k_c21(D8sConv2Args c2, 
     const __amdgpu_buffer_rsrc_t ro1 = __builtin_amdgcn_make_buffer_rsrc(c1.out, 0, (int)(M * 128), 0x00020000);
     const uint32_t lo_off = (uint32_t)(p * 32 + 16 * h);
     u32x4 ra[PF], rb[4], stg[4];
-    // the first tile's halo, activations, conv2 plane 0 and conv1 chunk 0 in flight while the tables
-    // are staged
+    // the tables first (all their loads at once, from clamped addresses: a load per loop iteration,
+    // each waited for before its store, made the start wait for every load in flight and then one L2
+    // round trip per iteration), then the first tile's halo, activations, conv2 plane 0 and conv1
+    // chunk 0, in flight while the tables are stored
+    constexpr int NAB = (D8S_C21_MAX_GROUPS * 32 + 255) / 256;
+    uint32_t tab[NAB], t_ws;
+    float2 t_gd;
+    float t_sc2;
+    int32_t t_w2;
+    {
+        const uint32_t* abh32 = (const uint32_t*)c1.abh;
+#pragma unroll
+        for (int k = 0; k < NAB; ++k) tab[k] = abh32[min(tid + 256 * k, G * 32 - 1)];
+        t_ws = (uint32_t)c1.wsum[min(tid, 127)];
+        t_gd = ((const float2*)c1.gd)[min(tid, 127)];
+        t_sc2 = c2.sc[min(tid, 31)];
+        t_w2 = c2.wsum[min(tid, 31)];
+    }
     hload(tile);
     w2load(0);
 #pragma unroll
@@ -991,15 +1007,16 @@ __global__ __launch_bounds__(256, CcShape<W_>::OCC) void k_c21(D8sConv2Args c2, 
         ra[s] = cc_act(in0, seg, in_gs, seg_gs, G0, G, Gp, s, ci, cs, ni, ns, true);
     w1load(stg, 0);
     {
-        const uint32_t* abh32 = (const uint32_t*)c1.abh;
-        for (int i = tid; i < G * 32; i += 256) s_abh[i] = abh32[i];
+#pragma unroll
+        for (int k = 0; k < NAB; ++k)
+            if (tid + 256 * k < G * 32) s_abh[tid + 256 * k] = tab[k];
         if (tid < 128) {
-            s_wsum[tid] = c1.wsum[tid];
-            s_gd[tid] = ((const float2*)c1.gd)[tid];
+            s_wsum[tid] = (int32_t)t_ws;
+            s_gd[tid] = t_gd;
         }
         if (tid < 32) {
-            s_sc2[tid] = c2.sc[tid];
-            s_ini2[tid] = 128 * c2.wsum[tid];
+            s_sc2[tid] = t_sc2;
+            s_ini2[tid] = 128 * t_w2;
         }
     }
     hstore();
