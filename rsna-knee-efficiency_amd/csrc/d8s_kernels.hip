@@ -464,21 +464,40 @@ __global__ __launch_bounds__(256, U == 2 ? 2 : 3) void k_conv1p(D8sGemmArgs a0, 
     // latencies overlap
 #pragma unroll
     for (int s0 = 0; s0 < PF; ++s0) C1P_LOAD_A(s0, s0);
+    // the tables and the weights (WM 2: chunk 0): the first NW weight and NAB table items per thread
+    // requested at once (clamped addresses), then stored; loops stage what is left (a load-and-store
+    // loop waits one L2 round trip per iteration)
     {
+        constexpr int NW = WM == 1 ? 16 : 4, NAB = 2;     // 16 (4) groups of weights, 16 of tables
         const uint32_t* abh32 = (const uint32_t*)a.abh;
-        for (int i = tid; i < G * 32; i += 256) s_abh[i] = abh32[i];
-        if (tid < 128) {
-            s_wsum[tid] = a.wsum[tid];
-            s_gd[tid] = ((const float2*)a.gd)[tid];
-        }
         const u32x4* w = (const u32x4*)a.w;
-        for (int i = tid; i < (WM == 1 ? G * 256 : 1024); i += 4 * 256) {     // WM 2: chunk 0
-            u32x4 v[4];
+        const int nw = WM == 1 ? G * 256 : min(G, 4) * 256;
+        u32x4 v[NW];
+        uint32_t vab[NAB];
 #pragma unroll
-            for (int u = 0; u < 4; ++u) v[u] = w[min(i + u * 256, G * 256 - 1)];
+        for (int k = 0; k < NW; ++k) v[k] = w[min(tid + 256 * k, G * 256 - 1)];
+#pragma unroll
+        for (int k = 0; k < NAB; ++k) vab[k] = abh32[min(tid + 256 * k, G * 32 - 1)];
+        const int32_t t_ws = a.wsum[min(tid, 127)];
+        const float2 t_gd = ((const float2*)a.gd)[min(tid, 127)];
+#pragma unroll
+        for (int k = 0; k < NW; ++k)
+            if (tid + 256 * k < nw) s_w[wperm(tid + 256 * k)] = v[k];
+#pragma unroll
+        for (int k = 0; k < NAB; ++k)
+            if (tid + 256 * k < G * 32) s_abh[tid + 256 * k] = vab[k];
+        if (tid < 128) {
+            s_wsum[tid] = t_ws;
+            s_gd[tid] = t_gd;
+        }
+        for (int i = tid + 256 * NAB; i < G * 32; i += 256) s_abh[i] = abh32[i];
+        for (int i = tid + 256 * NW; i < nw; i += 4 * 256) {
+            u32x4 x[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) x[u] = w[min(i + u * 256, G * 256 - 1)];
 #pragma unroll
             for (int u = 0; u < 4; ++u)
-                if (i + u * 256 < G * 256) s_w[wperm(i + u * 256)] = v[u];
+                if (i + u * 256 < nw) s_w[wperm(i + u * 256)] = x[u];
         }
     }
     __syncthreads();
@@ -1230,29 +1249,45 @@ __global__ __launch_bounds__(64 * NW, 1) void k_dense(D8sDenseArgs a, int tiles_
     int tile = blockIdx.x;
     if (tile >= total) return;
 
+    // the weights and tables: the first items of each per thread requested at once (clamped
+    // addresses), then stored; loops stage what is left (a load-and-store loop waits one L2 round
+    // trip per iteration)
     {
-        constexpr int NCH = (2304 + NT - 1) / NT;
-        u32x4 wv[NCH];
+        constexpr int NCH = (2304 + NT - 1) / NT, NW1 = WL ? 8 : 1, NAB = 2;
+        u32x4 wv[NCH], v1[NW1];
+        uint32_t vab[NAB];
         const u32x4* w2 = (const u32x4*)a.w2;
+        const u32x4* w1 = (const u32x4*)a.w1;
+        const uint32_t* abh32 = (const uint32_t*)a.abh;
+        const int ti = min(tid, 127), ts = min(max(tid - 128, 0), 31);
+        const int32_t t_w1sum = a.w1sum[ti], t_w2sum = a.w2sum[ts];
+        const float2 t_gd = ((const float2*)a.gd)[ti];
+        const float t_sc = a.sc[ts];
 #pragma unroll
         for (int k = 0; k < NCH; ++k) wv[k] = w2[min(tid + NT * k, 2303)];
 #pragma unroll
+        for (int k = 0; k < NAB; ++k) vab[k] = abh32[min(tid + NT * k, G * 32 - 1)];
+#pragma unroll
+        for (int k = 0; WL && k < NW1; ++k) v1[k] = w1[min(tid + NT * k, G * 256 - 1)];
+#pragma unroll
         for (int k = 0; k < NCH; ++k)
             if (tid + NT * k < 2304) s_w[swz((tid + NT * k) >> 1, tid & 1)] = wv[k];
-    }
-    if (tid < 128) {
-        s_w1sum[tid] = a.w1sum[tid];
-        s_gd[tid] = ((const float2*)a.gd)[tid];
-    } else if (tid < 160) {
-        s_sc[tid - 128] = a.sc[tid - 128];
-        s_w2sum[tid - 128] = a.w2sum[tid - 128];
-    }
-    {
-        const uint32_t* abh32 = (const uint32_t*)a.abh;
-        for (int i = tid; i < G * 32; i += NT) s_abh[i] = abh32[i];
+        if (tid < 128) {
+            s_w1sum[tid] = t_w1sum;
+            s_gd[tid] = t_gd;
+        } else if (tid < 160) {
+            s_sc[tid - 128] = t_sc;
+            s_w2sum[tid - 128] = t_w2sum;
+        }
+#pragma unroll
+        for (int k = 0; k < NAB; ++k)
+            if (tid + NT * k < G * 32) s_abh[tid + NT * k] = vab[k];
+#pragma unroll
+        for (int k = 0; WL && k < NW1; ++k)
+            if (tid + NT * k < G * 256) s_w1[wperm(tid + NT * k)] = v1[k];
+        for (int i = tid + NT * NAB; i < G * 32; i += NT) s_abh[i] = abh32[i];
         // the layer's conv1 weights (WL): every wave reads all of them for every tile
-        const u32x4* w1 = (const u32x4*)a.w1;
-        for (int i = tid; WL && i < G * 256; i += 4 * NT) {
+        for (int i = tid + NT * NW1; WL && i < G * 256; i += 4 * NT) {
             u32x4 v[4];
 #pragma unroll
             for (int u = 0; u < 4; ++u) v[u] = w1[min(i + u * NT, G * 256 - 1)];
@@ -1544,35 +1579,44 @@ void k_band(D8sDenseArgs a0, int bands, int band_rows, D8sDenseArgs a1, int spli
     const int M = (nr + RS - 1) / RS;                                     // conv2 steps
     const int64_t HW = (int64_t)H * W_;
 
+    // the layer's weights and tables: every load first (clamped addresses, all in flight together),
+    // then the stores (a load-and-store loop waits one L2 round trip per iteration)
     {
         constexpr int NCH = (2304 + NT - 1) / NT;
-        u32x4 wv[NCH];
+        constexpr int NW1 = (GM * 256 + NT - 1) / NT, NAB = (GM * 32 + NT - 1) / NT;
+        u32x4 wv[NCH], v1[NW1];
+        uint32_t vab[NAB];
         const u32x4* w2 = (const u32x4*)a.w2;
+        const u32x4* w1 = (const u32x4*)a.w1;
+        const uint32_t* abh32 = (const uint32_t*)a.abh;
+        const int ti = min(tid, 127), ts = min(max(tid - 128, 0), 31);
+        const int32_t t_w1sum = a.w1sum[ti], t_w2sum = a.w2sum[ts];
+        const float2 t_gd = ((const float2*)a.gd)[ti];
+        const float t_sc = a.sc[ts];
 #pragma unroll
         for (int k = 0; k < NCH; ++k) wv[k] = w2[min(tid + NT * k, 2303)];
 #pragma unroll
+        for (int k = 0; k < NAB; ++k) vab[k] = abh32[min(tid + NT * k, G * 32 - 1)];
+#pragma unroll
+        for (int k = 0; k < NW1; ++k) v1[k] = w1[min(tid + NT * k, G * 256 - 1)];
+#pragma unroll
         for (int k = 0; k < NCH; ++k)
             if (tid + NT * k < 2304) s_w[swz((tid + NT * k) >> 1, tid & 1)] = wv[k];
-    }
-    if (tid < 128) {                                   // the sums times 128: the accumulators' start
-        s_w1sum[tid] = 128 * a.w1sum[tid];
-        s_gd[tid] = ((const float2*)a.gd)[tid];
-    } else if (tid < 160) {
-        s_sc[tid - 128] = a.sc[tid - 128];
-        s_w2sum[tid - 128] = 128 * a.w2sum[tid - 128];
+        if (tid < 128) {                               // the sums times 128: the accumulators' start
+            s_w1sum[tid] = 128 * t_w1sum;
+            s_gd[tid] = t_gd;
+        } else if (tid < 160) {
+            s_sc[tid - 128] = t_sc;
+            s_w2sum[tid - 128] = 128 * t_w2sum;
+        }
+#pragma unroll
+        for (int k = 0; k < NAB; ++k)
+            if (tid + NT * k < G * 32) s_abh[tid + NT * k] = vab[k];
+#pragma unroll
+        for (int k = 0; k < NW1; ++k)
+            if (tid + NT * k < G * 256) s_w1[wperm(tid + NT * k)] = v1[k];
     }
     {
-        const uint32_t* abh32 = (const uint32_t*)a.abh;
-        for (int i = tid; i < G * 32; i += NT) s_abh[i] = abh32[i];
-        const u32x4* w1 = (const u32x4*)a.w1;
-        for (int i = tid; i < G * 256; i += 4 * NT) {
-            u32x4 v[4];
-#pragma unroll
-            for (int u = 0; u < 4; ++u) v[u] = w1[min(i + u * NT, G * 256 - 1)];
-#pragma unroll
-            for (int u = 0; u < 4; ++u)
-                if (i + u * NT < G * 256) s_w1[wperm(i + u * NT)] = v[u];
-        }
         // padding columns of every ring row: 0 and W + 1 .. PS - 1
         constexpr int NPAD = PS - W_;
         const u32x4 pad = {SIGN4, SIGN4, SIGN4, SIGN4};
@@ -2627,8 +2671,17 @@ __global__ __launch_bounds__(256, NT <= 5 && WB < 4 ? 2 : 1) void k_trans(D8sGem
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int h = lane >> 5, j = lane & 31;
+    // the prologue tables: the first NAB dwords per thread requested now and stored after the first
+    // groups' loads are on their way (a load-and-store loop waits one L2 round trip per iteration);
+    // NAB covers 40 groups, the widest transition input of DenseNet169 (none for the widest outputs,
+    // whose registers are full: they stage the tables here)
+    constexpr int NAB = NT >= 8 ? 0 : 5;
     const uint32_t* abh32 = (const uint32_t*)a.abh;
-    for (int i = tid; i < G * 32; i += 256) s_abh[i] = abh32[i];
+    uint32_t vab[NAB > 0 ? NAB : 1];
+#pragma unroll
+    for (int k = 0; k < NAB; ++k) vab[k] = abh32[min(tid + 256 * k, G * 32 - 1)];
+    if constexpr (NAB == 0)
+        for (int i = tid; i < G * 32; i += 256) s_abh[i] = abh32[i];
 
     // pixel counts fit 32 bits (the launcher checks N * HW)
     const uint32_t HW = (uint32_t)a.HW, W = (uint32_t)a.W;
@@ -2749,6 +2802,11 @@ __global__ __launch_bounds__(256, NT <= 5 && WB < 4 ? 2 : 1) void k_trans(D8sGem
         for (int k = 0; k < IT; ++k) ld(k, d < G ? d : G - 1, raw[d][k]);
 #pragma unroll
     for (int w = 0; w < (WB > 1 ? WB - 1 : 1); ++w) wload(w < G ? w : G - 1, aw[w]);
+#pragma unroll
+    for (int k = 0; k < NAB; ++k)
+        if (tid + 256 * k < G * 32) s_abh[tid + 256 * k] = vab[k];
+    if constexpr (NAB > 0)
+        for (int i = tid + 256 * NAB; i < G * 32; i += 256) s_abh[i] = abh32[i];
     __syncthreads();                                       // s_abh
     // D groups per step; the first step is peeled so that the loop's waits see only the steady state
     // (the preamble's load order would otherwise make them wait for every load)
