@@ -3573,12 +3573,12 @@ static bool same_gemm(const D8sGemmArgs* a, const D8sGemmArgs* b) {
 enum { C1V_P32 = 1, C1V_P64 = 2, C1V_K1 = 3, C1V_K2 = 4, C1V_K4 = 5, C1V_MAX = 5 };
 
 // The variant a launch of conv1 with `variant` runs (the choice for 0), or -1 where the shape does
-// not take it (the persistent form keeps 32-bit offsets: rows < 2^34, in0 and a slot below 4 GiB).
+// not take it (the persistent form keeps 32-bit byte offsets: in0 and a slot below 4 GiB).
 static int conv1_variant(const D8sGemmArgs* a, const D8sGemmArgs* b, int variant) {
     const int np = b ? 2 : 1;                              // problems in the launch
-    const int64_t rows = a->rows * np;
+    const int64_t rows = (int64_t)a->rows * np;
     const int64_t in0_bytes = (int64_t)a->N * a->G0 * a->HW * 32, slot_bytes = (int64_t)a->rows * 32;
-    const bool p_ok = a->rows < (1ll << 34) && in0_bytes < (1ll << 32) && slot_bytes < (1ll << 32);
+    const bool p_ok = in0_bytes < (1ll << 32) && slot_bytes < (1ll << 32);
     if (variant != 0) {
         if (variant < 1 || variant > C1V_MAX) return -1;
         return variant <= C1V_P64 && !p_ok ? -1 : variant;
@@ -3601,7 +3601,7 @@ static int conv1_launch(const D8sGemmArgs* a, const D8sGemmArgs* b, int32_t* acc
     const int v = conv1_variant(a, b, variant);
     REQUIRE(v >= 1, "d8s_conv1: variant " + std::to_string(variant) + " is not taken for this shape");
     const int np = b ? 2 : 1;                              // problems in the launch
-    const int64_t rows = a->rows * np;
+    const int64_t rows = (int64_t)a->rows * np;
     if (v == C1V_P32 || v == C1V_P64) {
         const int u = v == C1V_P64 ? 2 : 1;
         const int64_t ntiles = (rows + 32 * u - 1) / (32 * u);

@@ -209,10 +209,6 @@ DEV Geo block_geo(const PStack& st, const PArgs& a, int b) {
     }
 }
 
-DEV const uint16_t* crop_row(const PStack& st, int kk, int r) {
-    return (const uint16_t*)st.src + ((int64_t)kk * st.hr + st.y0 + r) * st.wr + st.x0;
-}
-
 constexpr int NW = NT / 64;  // waves per workgroup
 
 // Copies source rows [s0, s0 + ns) of a block, crop columns [0, w), to LDS with gfx950's
@@ -1150,7 +1146,7 @@ int prepare(const D8sPrepArgs* in, const char* what, bool resize_only, PArgs& a,
     a.inv_upr = 1.0f / (float)a.upr;
     PREQ(in->kind == 1 || img <= 1024, "img above 1024 is supported for float32 stacks (kind 1) only");
     const int rb_want = 4096 / img > 1 ? 4096 / img : 1;     // about 4096 output pixels per block
-    int64_t total_px = 0, sc_off = 0;
+    int64_t sc_off = 0;
     for (int i = 0; i < a.n; ++i) {
         const D8sPrepStack& s = in->s[i];
         PStack& p = a.s[i];
@@ -1187,7 +1183,6 @@ int prepare(const D8sPrepArgs* in, const char* what, bool resize_only, PArgs& a,
         p.r2 = s.r2;
         p.g1 = s.g1;
         p.g2 = s.g2;
-        total_px += n;
         if (in->kind == 1) {
             PREQ(s.src % 16 == 0, at + "float32 input not 16-byte aligned");
             p.mode = M_FLOAT;
