@@ -109,10 +109,12 @@ def test_conv1_ks_variants(dev, S, C, N):
     assert np.array_equal(acc, acc_x) and np.array_equal(byt, byt_x)
 
 
-@pytest.mark.parametrize("S,C,N", [(64, 320, 24), (16, 640, 24), (8, 96, 3), (100, 96, 30), (128, 224, 2)])
+@pytest.mark.parametrize("S,C,N", [(64, 320, 24), (16, 640, 24), (8, 96, 3), (100, 96, 30), (128, 224, 2),
+                                   (32, 576, 4)])
 def test_conv1_every_variant(dev, S, C, N):
     """Every conv1 kernel variant (d8s_conv1_as: the persistent form with 32- and 64-pixel tiles, one
-    pass with 1, 2 and 4 k-slices) writes the exact bottleneck."""
+    pass with 1, 2 and 4 k-slices) writes the exact bottleneck (C = 576: 18 groups of weights in LDS
+    with 64-pixel tiles, more than the first batch of setup loads holds)."""
     c = cases.gemm_case(S, C, N=N, seed=29)
     _, byt_x = checks.exact_conv1(c)
     args, _keep = checks.conv1_args(c, dev)
@@ -185,6 +187,8 @@ def test_conv2_every_variant(dev, N, H, W):
     (20, 128, 320, 96, 1),       # W = 128, 10 groups, G0 = 3
     (64, 128, 512, 64, 1),       # W = 128, 16 groups: the most the band form takes
     (16, 64, 512, 64, 1),        # W = 64 with 16 groups: conv1 weights too large for the band form
+    (16, 16, 576, 64, 2),        # 2-D tiles, 18 groups of conv1 weights in LDS (more than the first
+    (24, 20, 608, 64, 2),        # batch of setup loads holds: 16), 16 x 16 and 16 x 12 tiles
 ])
 def test_dense_layer(dev, H, W, C, c0, N):
     """d8s_dense (conv1 + conv2 fused, bottleneck in LDS): the bytes of the exact conv1 -> conv2 and of
@@ -293,11 +297,12 @@ def test_dense_block(dev, H, W, c0, L, N):
                                          (16, 128, 64, None), (12, 192, 64, None), (8, 320, 64, None),
                                          (12, 640, 128, None), (6, 96, 32, 32), (4, 224, 96, 256),
                                          (8, 1024, 128, None), (6, 416, 64, 416), (4, 256, 64, 768),
-                                         (4, 192, 64, 1024)])
+                                         (4, 192, 64, 1024), (4, 1536, 64, 512), (6, 1664, 128, 640)])
 def test_transition(dev, S, C, c0, cout):
     """The DenseNet169 geometries, then ragged pixel counts, both default activation prefetch depths (2
-    for an even group count, else 1; every variant in `test_transition_every_variant`) and tile count
-    per wave (1-6 and 8, ragged too)."""
+    for an even group count, else 1; every variant in `test_transition_every_variant`), tile count
+    per wave (1-6 and 8, ragged too) and more groups (48, 52) than the prologue tables' first batch of
+    loads holds (40)."""
     t = cases.trans_case(S, C, N=4, c0=c0, cout=cout)
     print(f"transition S={S} C={C} cout={t['cout']}", flush=True)
     got = checks.run_trans(t, dev)
