@@ -15,8 +15,10 @@ back to back, after the timed steps.
 The two seeds' passes of a step run from two streams (`--serial`: one after the other).
 `roofline`: the dominant kernel family: its launches of a configuration-5 pass recorded R times in a HIP
 graph and replayed between HIP events on the encoder's stream (algorithmic bytes of a launch / the
-average launch time); `frac_in_pass` the same family timed inside a whole pass, `in_schedule` inside a
-pass that shares the GPU with the other seed's; `roofline_runner_up`: the second family by time (the
+average launch time); `frac_in_pass` the same family's share of a whole pass (the pass's graph against
+the pass's graph without the family's launches, per launch), `in_schedule` what the family's launches
+add to the two-stream pair of passes (partly filled by the other seed's work, so no roofline fraction
+is derived from it); `roofline_runner_up`: the second family by time (the
 band layers of block 0 and the chained launches of block 2 take about as long, so either can lead),
 against HBM and the int8 MFMA peak; `step_hbm_frac`: both passes' algorithmic bytes over the timed
 step time.  `roofline_c4`: configuration 4's dominant launch (the 32 x 32 banded block)
@@ -740,56 +742,28 @@ def c4_roofline(enc, reps: int, peak_tops: float | None) -> dict:
 
 
 def family_in_pass(encs, x, reps: int, family: str, bytes_per_launch: float, concurrent: bool) -> dict:
-    """One family's launches timed inside a whole configuration-5 pass of seed 0 (launched eagerly after a
-    5 ms hold of its stream, during which the host enqueues every launch, so the pass runs as its graph
-    would), with events only around the family's launches (before the first and after the last of each
-    contiguous run: block 2's chained launches, block 0's fused layers); the summed spans / launches,
-    mean over `reps` passes after a warm one, and the algorithmic bytes per launch over it against 8 TB/s.
-    `concurrent`: seed 1's pass replays its graph on its own stream starting with it (the two passes
-    then share the GPU phase by phase, the most the two-stream schedule can overlap them)."""
+    """One family's share of a whole configuration-5 pass of seed 0 as the timed steps run it, a HIP graph
+    replay: the pass against the same pass without the family's launches (`Dense8SEncoder.pass_share`,
+    medians over `reps` replays of each), the difference / launches, and the algorithmic bytes per launch
+    over it against 8 TB/s.  `concurrent`: seed 1's pass replays its graph on its own stream from the
+    same start (the two then share the GPU as in the two-stream step); the difference is then what the
+    family adds to the pair's time, which the other pass's work partly fills, so it is reported per
+    launch without a bandwidth or roofline fraction."""
     enc = encs[0]
-    prog = enc.program
-    idx = [i for i, s in enumerate(prog) if s.family == family]
-    if not idx or idx[0] == 0:
+    if not any(s.family == family for s in enc.program):
         return {}
-    runs = []                                         # [step before the run, last step of the run, index]
-    for i in idx:
-        if runs and runs[-1][2] == i - 1:
-            runs[-1][1], runs[-1][2] = prog[i], i
-        else:
-            runs.append([prog[i - 1], prog[i], i])
-    marks = {id(a): ("a", k) for k, (a, _, _) in enumerate(runs)}
-    marks.update({id(b): ("b", k) for k, (_, b, _) in enumerate(runs)})
-    spans = []
-    for r in range(reps + 1):
-        ev: dict = {}
-
-        def after(step, ev=ev):
-            m = marks.get(id(step))
-            if m is not None:
-                e = torch.cuda.Event(enable_timing=True)
-                e.record(enc.stream)
-                ev[m] = e
-        torch.cuda.synchronize()
-        with torch.cuda.stream(enc.stream):
-            torch.cuda._sleep(12_000_000)
-            gate = torch.cuda.Event()
-            gate.record(enc.stream)
-        if concurrent:
-            encs[1].stream.wait_event(gate)
-            with torch.cuda.stream(encs[1].stream):
-                encs[1](x, flip="tta")
-        with torch.cuda.stream(enc.stream):
-            enc.launch(x, flip="tta", after=after)
-        torch.cuda.synchronize()
-        if r:
-            spans.append(sum(ev[("a", k)].elapsed_time(ev[("b", k)]) for k in range(len(runs))) / len(idx))
-    ms = float(np.mean(spans))
+    sh = enc.pass_share(x, family, reps=reps, flip="tta", beside=encs[1] if concurrent else None)
+    ms = sh["share_ms"] / sh["launches"]
+    if concurrent:
+        return {"family": family, "launches": sh["launches"], "share_ms_per_launch": round(ms, 5),
+                "pair_ms": round(sh["pass_ms"], 4), "pair_without_ms": round(sh["without_ms"], 4),
+                "timed": "seed 0's pass and seed 1's on two streams from the same start, with and without "
+                         "seed 0's launches of the family (HIP graphs)"}
     gbs = bytes_per_launch / (ms * 1e-3) / 1e9
-    return {"family": family, "launches": len(idx), "avg_launch_ms": round(ms, 5), "gbs": round(gbs, 1),
-            "frac": round(gbs / HBM_PEAK_GBS, 4),
-            "timed": ("inside seed 0's pass with seed 1's pass on another stream from the same start "
-                      "(the two share the GPU)" if concurrent else "inside seed 0's pass, alone")}
+    return {"family": family, "launches": sh["launches"], "avg_launch_ms": round(ms, 5), "gbs": round(gbs, 1),
+            "frac": round(gbs / HBM_PEAK_GBS, 4), "pass_ms": round(sh["pass_ms"], 4),
+            "without_ms": round(sh["without_ms"], 4),
+            "timed": "seed 0's pass alone, with and without the family's launches (HIP graphs)"}
 
 
 def bench_c4(dev: torch.device, passes: int, reps: int) -> dict:
@@ -1323,8 +1297,8 @@ def main() -> None:
     fam_tops = {k: round(ops[k] / (fam[k] * 1e-3) / 1e12, 1) for k in ops if fam.get(k)}
     log(f"pass of {nb}: {pass_ms:.3f} ms; families ms {json.dumps({k: round(v, 3) for k, v in fam.items()})}")
     log(f"families GB/s {fam_gbs}; int8 TOP/s {fam_tops}")
-    # the dominant family inside a whole pass, alone and beside the other seed's pass (the isolated
-    # figure above replays its launches back to back)
+    # the dominant family's share of a whole pass's graph, alone and beside the other seed's pass (the
+    # isolated figure above replays its launches back to back)
     in_pass = family_in_pass(encs, studies[0], args.prof_reps, dom, dom_bytes / launches, False)
     in_sched = family_in_pass(encs, studies[0], args.prof_reps, dom, dom_bytes / launches, True)
     log(f"{dom} launches inside a pass: {in_pass}; beside the other seed's pass: {in_sched}")

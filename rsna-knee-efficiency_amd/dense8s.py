@@ -1506,6 +1506,59 @@ class Dense8SEncoder(_PassRunner):
             by_family.setdefault(step.family, []).append(step)
         return {fam: round(self._graph_ms(steps, reps, x_ptr, mode), 4) for fam, steps in by_family.items()}
 
+    def pass_share(self, x: torch.Tensor, family: str, reps: int = 5, flip=False, beside=None) -> dict:
+        """GPU milliseconds a kernel family adds to a whole pass as the graphs run it: the pass in one HIP
+        graph against the same pass without the family's launches in another, each replayed `reps`
+        times between events after a warm replay, medians ("share_ms" = "pass_ms" - "without_ms").  The
+        pass without them computes nothing useful; every later pass rewrites what it read.  `beside`:
+        another runner whose own pass (`beside(x, flip)`) starts with each replay on its stream, so the
+        two share the GPU as in `encode_concurrent`; the times are then the pair's, from the caller's
+        stream."""
+        if not any(s.family == family for s in self.program):
+            raise ValueError(f"pass_share: no {family!r} launch in this runner's pass")
+        if beside is not None and concurrent_order([self, beside], _cu_count(self.dev))[1]:
+            raise ValueError("pass_share: the two runners' banded blocks do not fit the CUs together")
+        x_ptr, mode = self._warm(x, flip)
+        st = self.stream.cuda_stream
+        f_ptr = self.out.data_ptr()
+        graphs = {}
+        with self._launching():
+            for key, steps in (("pass_ms", self.program),
+                               ("without_ms", [s for s in self.program if s.family != family])):
+                gr = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(gr, stream=self.stream, capture_error_mode="thread_local"):
+                    for step in steps:
+                        self._launch(step, st, x_ptr, f_ptr, mode)
+                graphs[key] = gr
+        self.stream.synchronize()
+        caller = torch.cuda.current_stream(self.dev)
+        times: dict[str, list] = {k: [] for k in graphs}
+        for r in range(reps + 1):
+            for key, gr in graphs.items():
+                if beside is None:
+                    a = _record(self.stream)
+                    with torch.cuda.stream(self.stream):
+                        gr.replay()
+                    b = _record(self.stream)
+                else:
+                    a = _record(caller)
+                    self.stream.wait_stream(caller)
+                    beside.stream.wait_stream(caller)
+                    with torch.cuda.stream(beside.stream):
+                        beside(x, flip=flip)
+                    with torch.cuda.stream(self.stream):
+                        gr.replay()
+                    caller.wait_stream(self.stream)
+                    caller.wait_stream(beside.stream)
+                    b = _record(caller)
+                torch.cuda.synchronize(self.dev)
+                if r:
+                    times[key].append(a.elapsed_time(b))
+        out = {k: sorted(v)[len(v) // 2] for k, v in times.items()}
+        out["share_ms"] = out["pass_ms"] - out["without_ms"]
+        out["launches"] = sum(s.family == family for s in self.program)
+        return out
+
     def time_layers(self, reps: int = 20, families=None) -> dict:
         """ms of every launch of the pass but the stem and the final features (or only those of the
         kernel families named in `families`), on the current store (`Step.label`: "c1 b{b}l{l}",

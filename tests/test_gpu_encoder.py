@@ -223,6 +223,31 @@ def test_tune_kinds_and_recorded_kinds(dev, study512):
     assert torch.equal(r2(x).clone(), want)
 
 
+def test_pass_share(dev, study512):
+    """`pass_share` (a family's share of a whole pass: the pass's graph against the pass's graph without
+    the family's launches, alone and beside a second runner's pass) times both graphs, and a pass after
+    it (the incomplete pass ran on the same buffers) gives the same features as before."""
+    enc, x = study512["enc"], study512["xd"]
+    want = enc(x).clone()
+    other = dense8s.Dense8SEncoder(study512["pack"], dev.index or 0, 24)
+    fams = [f for f in ("chain", "block", "dense") if any(s.family == f for s in enc.program)]
+    assert fams
+    for fam in fams:
+        for beside in (None, other):
+            sh = enc.pass_share(x, fam, reps=2, beside=beside)
+            print(fam, beside is not None, sh, flush=True)
+            assert sh["launches"] == sum(s.family == fam for s in enc.program)
+            assert sh["pass_ms"] > 0 and sh["without_ms"] > 0
+            assert sh["share_ms"] == sh["pass_ms"] - sh["without_ms"]
+            if beside is None and fam == fams[0]:
+                assert sh["share_ms"] > 0
+    with pytest.raises(ValueError):
+        enc.pass_share(x, "no-such-family")
+    assert torch.equal(enc(x).clone(), want)
+    assert torch.equal(other(x).clone(), want)
+    assert enc.sync_errors() == 0 and other.sync_errors() == 0
+
+
 def test_kernel_variant_tuners(dev, study512):
     """`tune_bm` / `tune_c2` / `tune_trans` (the reference's per-layer tuners) time every kernel variant
     each conv1, conv2 and transition launch takes; applied, the runner uses the fastest, with the same
