@@ -1485,6 +1485,7 @@ class Dense8SEncoder(_PassRunner):
                 g.replay()
                 marks.append(_record(self.stream))
             self.stream.synchronize()
+        self._mark_written()
         times = sorted(a.elapsed_time(b) for a, b in zip(marks, marks[1:]))
         return times[1] / reps
 
@@ -1494,6 +1495,7 @@ class Dense8SEncoder(_PassRunner):
         x_ptr = self._pass_input(x, mode)
         with self._launching():
             self._launch_pass(x_ptr, 0, mode)
+        self._mark_written()
         return x_ptr, mode
 
     def time_families(self, x: torch.Tensor, reps: int = 5, flip=False) -> dict:
@@ -1510,7 +1512,8 @@ class Dense8SEncoder(_PassRunner):
         """GPU milliseconds a kernel family adds to a whole pass as the graphs run it: the pass in one HIP
         graph against the same pass without the family's launches in another, each replayed `reps`
         times between events after a warm replay, medians ("share_ms" = "pass_ms" - "without_ms").  The
-        pass without them computes nothing useful; every later pass rewrites what it read.  `beside`:
+        pass without them computes nothing useful (it overwrites the outputs of earlier calls, as a call
+        does); every later pass rewrites what it read.  `beside`:
         another runner whose own pass (`beside(x, flip)`) starts with each replay on its stream, so the
         two share the GPU as in `encode_concurrent`; the times are then the pair's, from the caller's
         stream."""
@@ -1554,6 +1557,7 @@ class Dense8SEncoder(_PassRunner):
                 torch.cuda.synchronize(self.dev)
                 if r:
                     times[key].append(a.elapsed_time(b))
+        self._mark_written()
         out = {k: sorted(v)[len(v) // 2] for k, v in times.items()}
         out["share_ms"] = out["pass_ms"] - out["without_ms"]
         out["launches"] = sum(s.family == family for s in self.program)
