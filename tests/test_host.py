@@ -183,6 +183,19 @@ def test_concurrent_order_keeps_banded_runners_within_the_cus():
     assert dense8s.concurrent_order([]) == []
 
 
+def test_pass_share_checks_before_any_launch():
+    """`Dense8SEncoder.pass_share` refuses a family the pass does not launch, and a runner beside it
+    whose banded blocks do not fit the CUs together with its own (their bounded waits could run out),
+    before it launches anything."""
+    import types
+    me = types.SimpleNamespace(program=[dense8s.Step("block", 2, -1, (), "d8s_dense_block_parts")],
+                               max_bands=200, dev=0)
+    with pytest.raises(ValueError, match="no 'chain' launch"):
+        dense8s.Dense8SEncoder.pass_share(me, None, "chain")
+    with pytest.raises(ValueError, match="do not fit the CUs"):
+        dense8s.Dense8SEncoder.pass_share(me, None, "block", beside=types.SimpleNamespace(max_bands=100))
+
+
 def test_graph_book_finds_the_smallest_covering_capture():
     """A batch replays the graphs captured for its size, else the first passes of the smallest capture
     that covers it (per flip mode), else none."""
