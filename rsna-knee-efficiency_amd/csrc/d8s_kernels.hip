@@ -3367,33 +3367,59 @@ __global__ __launch_bounds__(512, 1) void k_stem_rows(D8sStemArgs a0, int bands,
     const int ns = (a.flip == 2 && n >= half) ? n - half : n;          // source image
     const bool mirror = a.flip == 1 || (a.flip == 2 && n >= half);
 
-    // ring zeros (the column padding is never written again), weights, bias, inv, LUT
+    // The set-up's loads first, all in flight together (clamped addresses): the weights ([64][168]
+    // fp16 + zero K 168..175: rows of 21 16-byte chunks and a zero one), bias, inv, the LUT, and rows
+    // 4 py0 - 5 .. 4 py0 + 5 (the first pooled row's window and the conv row above it); then the LDS
+    // stores (a load-and-store loop waits one memory round trip per iteration), the ring zeros first
+    // (the column padding is never written again).  The first batches cover 512 threads; narrower
+    // workgroups stage the rest in the loops after them.
+    constexpr int NWB = (64 * 22 + 511) / 512, NLB = (3 * 256 + 511) / 512;
+    constexpr int KI = 9;                                               // 33 W/4 units over >= W threads
+    u32x4 wv[NWB];
+    uint16_t lv[NLB];
+#pragma unroll
+    for (int k = 0; k < NWB; ++k) {
+        const int q = min(tid + k * nt, 64 * 22 - 1), o = q / 22, rk = q - o * 22;
+        wv[k] = ((const u32x4*)a.w16)[o * 21 + min(rk, 20)];
+    }
+#pragma unroll
+    for (int k = 0; k < NLB; ++k) lv[k] = U8 ? a.lut[min(tid + k * nt, 3 * 256 - 1)] : (uint16_t)0;
+    const float t_bias = a.bias[min(tid, 63)], t_inv = a.inv[min(tid, 63)];
+    SrUnit u[KI];
+#pragma unroll
+    for (int k = 0; k < KI; ++k) {
+        const int q = tid + k * nt, rb = q / W4, D = q - rb * W4, c = rb / 11;
+        u[k] = sr_fetch<U8>(a.x, a.H, a.W, sr_e0(ns, c, a.H, a.W, D, mirror), 4 * py0 - 5 + (rb - 11 * c),
+                            q < 33 * W4);
+    }
     for (int k = tid; k < 3 * SR_CH / 4; k += nt) ((u32x4*)s_ring)[k] = u32x4{0u, 0u, 0u, 0u};
     if (tid < 16) s_halo[2 * SR_NWV * 64 + tid] = 0.0f;
-    for (int k = tid; k < 64 * 22; k += nt) {                          // [64][168] + zero K 168..175
+#pragma unroll
+    for (int k = 0; k < NWB; ++k) {
+        const int q = tid + k * nt, o = q / 22, rk = q - o * 22;
+        uint32_t m = rk < 21 ? ~0u : 0u;                                // chunk 21: the zero K rows
+        asm volatile("" : "+v"(m));                                     // (an AND, not a branch)
+        if (q < 64 * 22) *(u32x4*)(s_wt + o * SR_WROW + 8 * rk) = wv[k] & u32x4{m, m, m, m};
+    }
+    for (int k = tid + NWB * nt; k < 64 * 22; k += nt) {
         const int o = k / 22, rk = k - o * 22;
         u32x4 v = {0u, 0u, 0u, 0u};
         if (rk < 21) v = ((const u32x4*)a.w16)[o * 21 + rk];
         *(u32x4*)(s_wt + o * SR_WROW + 8 * rk) = v;
     }
     if (tid < 64) {
-        s_bias[tid] = a.bias[tid];
-        s_inv[tid] = a.inv[tid];
+        s_bias[tid] = t_bias;
+        s_inv[tid] = t_inv;
     }
-    if (U8)
-        for (int k = tid; k < 3 * 256; k += nt) s_lut[k] = __builtin_bit_cast(_Float16, a.lut[k]);
+    if (U8) {
+#pragma unroll
+        for (int k = 0; k < NLB; ++k)
+            if (tid + k * nt < 3 * 256) s_lut[tid + k * nt] = __builtin_bit_cast(_Float16, lv[k]);
+        for (int k = tid + NLB * nt; k < 3 * 256; k += nt) s_lut[k] = __builtin_bit_cast(_Float16, a.lut[k]);
+    }
     __syncthreads();
 
-    // rows 4 py0 - 5 .. 4 py0 + 5: the first pooled row's window and the conv row above it
     {
-        constexpr int KI = 9;                                           // 33 W/4 units over >= W threads
-        SrUnit u[KI];
-#pragma unroll
-        for (int k = 0; k < KI; ++k) {
-            const int q = tid + k * nt, rb = q / W4, D = q - rb * W4, c = rb / 11;
-            u[k] = sr_fetch<U8>(a.x, a.H, a.W, sr_e0(ns, c, a.H, a.W, D, mirror), 4 * py0 - 5 + (rb - 11 * c),
-                                q < 33 * W4);
-        }
 #pragma unroll
         for (int k = 0; k < KI; ++k) {
             const int q = tid + k * nt, rb = q / W4, D = q - rb * W4, c = rb / 11;
